@@ -1,0 +1,263 @@
+/*
+ * kvc.h — C ABI of the MI355X (gfx950) paged KV-cache library `libkvc.so`.
+ *
+ * Every entry point takes raw device pointers, element counts and element
+ * strides (never framework types), enqueues its work on `stream` (a
+ * hipStream_t; NULL is the legacy default stream), never allocates device
+ * memory and never synchronises the host.  Return value: KVC_OK (0) or a
+ * negative KVC_ERR_* code; kvc_last_error() then holds a message for the
+ * calling thread.  Caller-side ownership: the caller owns every buffer.
+ *
+ * Layouts (the engine's own, unchanged):
+ *   KV pool per layer      [num_blocks, page_size, num_kv_heads, head_dim]
+ *                          contiguous; a "slot" is block_id * page_size +
+ *                          offset, i.e. the row index of the flat
+ *                          [num_blocks * page_size, num_kv_heads * head_dim]
+ *                          view.
+ *   block_tables           int32 [batch, max_blocks_per_seq], row stride
+ *                          bt_stride, padded with -1 (entries past a row's
+ *                          context are never read).
+ *   context_lens           int32 [batch], read on the device (no host copy).
+ *   int8 per-token-head    codes int8 in the pool layout + fp32 scales
+ *     scales               [num_blocks, page_size, num_kv_heads].
+ *   int8 per-channel       codes int8 in the pool layout, scales fp32
+ *     (outlier side pool)  [num_kv_heads, head_dim], side pool bf16
+ *                          [num_blocks, page_size, num_kv_heads, n_out_max],
+ *                          out_idx2d int32 [num_kv_heads, n_out_max],
+ *                          head_n_out int32 [num_kv_heads].
+ *   whole-block slabs      a block of a multi-layer pool
+ *                          [planes, num_blocks, block_bytes] (planes =
+ *                          2 * layers for the engine's [2, L, ...] pool) is
+ *                          `planes` rows of block_bytes at plane_stride.
+ */
+#ifndef KVC_H_
+#define KVC_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* kvc_stream_t; /* hipStream_t */
+
+enum kvc_status {
+  KVC_OK = 0,
+  KVC_ERR_VALUE = -1,     /* unsupported shape / dtype / argument (ValueError) */
+  KVC_ERR_ASSERT = -2,    /* violated layout precondition (AssertionError)     */
+  KVC_ERR_RUNTIME = -3,   /* HIP runtime failure (RuntimeError)                */
+  KVC_ERR_WORKSPACE = -4, /* workspace missing or too small (ValueError)        */
+};
+
+/* KV element encodings accepted by the attention entry points. */
+enum kvc_kv_dtype {
+  KVC_KV_BF16 = 0,          /* bf16 pool                                       */
+  KVC_KV_INT8_TOKHEAD = 1,  /* int8 codes + fp32 scale per (slot, kv_head)     */
+  KVC_KV_INT8_CHAN = 2,     /* int8 codes * per-channel read scale + bf16 side */
+};
+
+/* Thread-local message for the last failing call on this thread. */
+const char* kvc_last_error(void);
+/* ABI revision of this header (bumped on any signature change). */
+int kvc_abi_version(void);
+
+/* ---------------------------------------------------------------------------
+ * KV append.
+ * ------------------------------------------------------------------------- */
+
+/* Replaces store_kvcache (nanovllm/layers/attention.py:9-30):
+ *   k_cache.view(-1, KVH*D)[slot_mapping] = key.reshape(N, KVH*D), same for V.
+ * key/value rows are addressed with their own strides (elements), so a V that
+ * is a strided view of a fused qkv projection needs no copy.  A negative slot
+ * wraps like a Python index (slot + num_slots); a slot still outside
+ * [0, num_slots) is skipped.  elem_bytes: 2 (bf16/fp16) or 4 (fp32).
+ * slot_index_bytes: 4 (int32) or 8 (int64). */
+int kvc_store_kv(const void* key, int64_t key_stride_n, int64_t key_stride_h,
+                 const void* value, int64_t value_stride_n, int64_t value_stride_h,
+                 void* k_cache, void* v_cache, int64_t num_slots,
+                 const void* slot_mapping, int slot_index_bytes,
+                 int64_t num_tokens, int64_t num_kv_heads, int64_t head_dim,
+                 int elem_bytes, kvc_stream_t stream);
+
+/* Per-token-per-head int8 quantise-on-append (the P17 layout documented in
+ * benchmarks/archive/P17-kv-int8.md:9-11, arithmetic of
+ * scripts/archive/p14_int8_kv_probe.py:37-41):
+ *   amax = max_d |x[d]| (bf16, exact) -> fp32, clamped to >= 1e-6
+ *   s    = amax / 127            (IEEE fp32 division)
+ *   code = clamp(rint_half_even(x / s), -127, 127)
+ * codes land in k_cache/v_cache [slots, KVH, D] int8 and s in
+ * k_scale/v_scale [slots, KVH] fp32.  key/value are bf16. */
+int kvc_store_int8_tokhead(const void* key, int64_t key_stride_n, int64_t key_stride_h,
+                           const void* value, int64_t value_stride_n, int64_t value_stride_h,
+                           int8_t* k_cache, int8_t* v_cache, float* k_scale, float* v_scale,
+                           int64_t num_slots, const void* slot_mapping, int slot_index_bytes,
+                           int64_t num_tokens, int64_t num_kv_heads, int64_t head_dim,
+                           kvc_stream_t stream);
+
+/* Replaces store_kvcache_int8 (nanovllm/kernels/kv_int8.py:72-93), the
+ * per-channel mode with a bf16 outlier side pool:
+ *   code = clamp(floor(x / s[h][d] + 0.5), -127, 127)   (IEEE fp32 division)
+ *   code = 0 at the head's outlier dims out_idx2d[h][:head_n_out[h]]
+ *   side[slot][h][j] = bf16(x[out_idx2d[h][j]]) for j < head_n_out[h].
+ * Unlike the reference kernel, V is read with V's own strides. */
+int kvc_store_int8_chan(const void* key, int64_t key_stride_n, int64_t key_stride_h,
+                        const void* value, int64_t value_stride_n, int64_t value_stride_h,
+                        int8_t* k_cache, int8_t* v_cache,
+                        const float* k_scale, const float* v_scale,
+                        void* side_k, void* side_v, int64_t n_out_max,
+                        const int32_t* out_idx2d, const int32_t* head_n_out,
+                        int64_t num_slots, const void* slot_mapping, int slot_index_bytes,
+                        int64_t num_tokens, int64_t num_kv_heads, int64_t head_dim,
+                        kvc_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Paged decode attention.
+ * ------------------------------------------------------------------------- */
+
+/* Bytes of split-K workspace kvc_paged_decode needs for this launch shape
+ * (0 when every sequence fits in one split).  max_blocks_per_seq is the
+ * block_tables width: the launch is sized from it, never from a host copy of
+ * the context lengths, so one captured launch serves every length. */
+size_t kvc_paged_decode_workspace_bytes(int64_t batch, int64_t num_heads, int64_t num_kv_heads,
+                                        int64_t head_dim, int64_t page_size,
+                                        int64_t max_blocks_per_seq);
+
+/* Replaces paged_decode_attention / _paged_decode_kernel
+ * (nanovllm/kernels/paged_attention.py:73-245):
+ *   out[b, h] = softmax(q[b, h] . K[b, :ctx, h // G]^T * scale) . V[b, :ctx, h // G]
+ * with G = num_heads / num_kv_heads and ctx = context_lens[b] (device).
+ * q/out bf16 [batch, num_heads, head_dim] with the given strides.  head_dim
+ * must be 128 and page_size a multiple of 32.  kv_dtype selects the pool
+ * encoding; for KVC_KV_INT8_TOKHEAD k_scale/v_scale are the per-slot scales,
+ * for KVC_KV_INT8_CHAN they are the [KVH, D] read scales (0 at outlier dims)
+ * and side_k/side_v/out_idx2d/head_n_out/n_out_max describe the side pool
+ * (side pointers may be NULL when no head has outliers).  context_lens[b] ==
+ * 0 yields 0/0 = NaN rows, as the reference kernel does. */
+int kvc_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                     const void* k_cache, const void* v_cache, int64_t num_cache_blocks,
+                     int64_t page_size, int64_t num_kv_heads, int64_t head_dim, int kv_dtype,
+                     const float* k_scale, const float* v_scale,
+                     const void* side_k, const void* side_v, const int32_t* out_idx2d,
+                     const int32_t* head_n_out, int64_t n_out_max,
+                     const int32_t* block_tables, int64_t bt_stride, int64_t max_blocks_per_seq,
+                     const int32_t* context_lens, int64_t batch, int64_t num_heads, float scale,
+                     void* out, int64_t out_stride_b, int64_t out_stride_h,
+                     void* workspace, size_t workspace_bytes, kvc_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Mixed decode + chunked-prefill attention in one launch.
+ * ------------------------------------------------------------------------- */
+
+/* Bytes of workspace kvc_varlen_attention needs.  num_q_tokens counts every
+ * query row (decode rows + prefill tokens); max_seqlen_k bounds the prefill
+ * key length; max_blocks_per_seq bounds the decode context. */
+size_t kvc_varlen_workspace_bytes(int64_t num_q_tokens, int64_t num_heads, int64_t num_kv_heads,
+                                  int64_t head_dim, int64_t num_decode_rows, int64_t max_seqlen_k,
+                                  int64_t page_size, int64_t max_blocks_per_seq);
+
+/* Number of prefill workgroups kvc_varlen_attention launches for these chunks
+ * (cu_q_host/cu_k_host: HOST copies of cu_seqlens_q/k, num_prefill + 1
+ * entries each — the engine keeps them as cu_seqlens_q_list/k_list). */
+int64_t kvc_varlen_prefill_units(const int32_t* cu_q_host, const int32_t* cu_k_host,
+                                 int64_t num_prefill, int64_t num_heads, int64_t num_kv_heads,
+                                 int64_t max_seqlen_k);
+
+/* Replaces the mixed / prefill branches of Attention.forward
+ * (nanovllm/layers/attention.py:146-173, _forward_decode :215-238 and the
+ * per-sequence loop _forward_prefill :179-213) with ONE attention launch plus
+ * a split-K merge pass.
+ *   rows [0, num_decode_rows): one decode token each, context
+ *     decode_context_lens[i] (device), block table row i.
+ *   rows num_decode_rows + [cu_seqlens_q[i], cu_seqlens_q[i+1]): prefill
+ *     chunk i with sk_i = cu_seqlens_k[i+1] - cu_seqlens_k[i] keys; query r
+ *     of the chunk sits at position sk_i - sq_i + r and sees keys j <= that
+ *     position (attention.py:210-212).  Keys come from the paged pool through
+ *     block table row num_decode_rows + i, or, when block_tables is NULL (no
+ *     prefix cache, attention.py:195-199), from the bf16 k_fresh/v_fresh
+ *     [tokens, KVH, D] rows cu_seqlens_k[i] .. (then num_decode_rows == 0).
+ * cu_seqlens_q/k are int32 device arrays of num_prefill + 1 entries;
+ * num_prefill_units comes from kvc_varlen_prefill_units. */
+int kvc_varlen_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h,
+                         int64_t num_q_tokens, int64_t num_heads,
+                         const void* k_cache, const void* v_cache, int64_t num_cache_blocks,
+                         int64_t page_size, int64_t num_kv_heads, int64_t head_dim, int kv_dtype,
+                         const float* k_scale, const float* v_scale,
+                         const void* side_k, const void* side_v, const int32_t* out_idx2d,
+                         const int32_t* head_n_out, int64_t n_out_max,
+                         const void* k_fresh, int64_t kf_stride_t, int64_t kf_stride_h,
+                         const void* v_fresh, int64_t vf_stride_t, int64_t vf_stride_h,
+                         const int32_t* block_tables, int64_t bt_stride, int64_t max_blocks_per_seq,
+                         int64_t num_decode_rows, const int32_t* decode_context_lens,
+                         int64_t num_prefill, const int32_t* cu_seqlens_q,
+                         const int32_t* cu_seqlens_k, int64_t num_prefill_units,
+                         int64_t max_seqlen_k, float scale, void* out, int64_t out_stride_t,
+                         int64_t out_stride_h, void* workspace, size_t workspace_bytes,
+                         kvc_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Dequantise gathered int8 rows (the torch-side read path).
+ * ------------------------------------------------------------------------- */
+
+/* Replaces dequant_gathered (nanovllm/kernels/kv_int8.py:96-107):
+ *   out[t,h,d] = bf16(fp32(kv[t,h,d]) * dscale[h,d]), then
+ *   out[t,h,out_idx2d[h,j]] = side[t,h,j] for j < head_n_out[h].
+ * kv int8 [T, KVH, D] contiguous, side bf16 [T, KVH, n_out_max] (may be NULL
+ * when no head has outliers), out bf16 [T, KVH, D]. */
+int kvc_dequant_chan(const int8_t* kv, const float* dscale, const void* side,
+                     const int32_t* out_idx2d, const int32_t* head_n_out, int64_t n_out_max,
+                     int64_t num_tokens, int64_t num_kv_heads, int64_t head_dim,
+                     void* out, kvc_stream_t stream);
+
+/* Per-token-per-head read path of scripts/archive/p14_int8_kv_probe.py:45-46:
+ *   out[t,h,d] = bf16(fp32(code[t,h,d]) * scale[t,h]). */
+int kvc_dequant_tokhead(const int8_t* kv, const float* scale, int64_t num_tokens,
+                        int64_t num_kv_heads, int64_t head_dim, void* out, kvc_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Whole-block movement (LRU eviction, host offload, compaction).
+ * ------------------------------------------------------------------------- */
+
+/* Gather: dst[i][p] = src[p][block_ids[i]] for p < planes, i < n.
+ * Replaces the index_select gathers of ModelRunner.offload_put
+ * (nanovllm/engine/model_runner.py:284-298) and extract_kv
+ * (nanovllm/pd/kv_channel.py:54-69).  block_ids: int32 device array.
+ * src plane p, block b starts at src + p*src_plane_stride + b*block_bytes;
+ * dst item i, plane p at dst + i*dst_item_stride + p*dst_plane_stride
+ * (bytes).  dst may be device memory or pinned host memory. */
+int kvc_block_gather(const void* src, int64_t planes, int64_t src_plane_stride,
+                     int64_t block_bytes, const int32_t* block_ids, int64_t n,
+                     void* dst, int64_t dst_item_stride, int64_t dst_plane_stride,
+                     kvc_stream_t stream);
+
+/* Scatter: dst[p][block_ids[i]] = src[i][p].  Replaces the index_copy_ of
+ * ModelRunner.offload_get (model_runner.py:300-305) and import_kv
+ * (pd/kv_channel.py:72-82).  src may be device or pinned host memory. */
+int kvc_block_scatter(const void* src, int64_t src_item_stride, int64_t src_plane_stride,
+                      int64_t planes, int64_t block_bytes, const int32_t* block_ids, int64_t n,
+                      void* dst, int64_t dst_plane_stride, kvc_stream_t stream);
+
+/* In-HBM copy pool[p][dst_ids[i]] = pool[p][src_ids[i]] (no reference
+ * function; the closed form of a compaction step).  The id sets must be
+ * disjoint (the caller stages overlapping lists). */
+int kvc_block_copy(void* pool, int64_t planes, int64_t plane_stride, int64_t block_bytes,
+                   const int32_t* src_ids, const int32_t* dst_ids, int64_t n,
+                   kvc_stream_t stream);
+
+/* DMA form of the offload byte moves: one strided 2-D copy per block on the
+ * copy engines, block ids read from HOST memory (the block manager's ints).
+ * d2h: host_dst + i*host_item_stride <- pool planes of block host_ids[i].
+ * h2d: pool planes of block host_ids[i] <- host_src + i*host_item_stride.
+ * Each item is `planes` rows of block_bytes (host side packed). */
+int kvc_block_d2h(const void* pool, int64_t planes, int64_t plane_stride, int64_t block_bytes,
+                  const int64_t* host_ids, int64_t n, void* host_dst, int64_t host_item_stride,
+                  kvc_stream_t stream);
+int kvc_block_h2d(const void* host_src, int64_t host_item_stride, int64_t planes,
+                  int64_t block_bytes, const int64_t* host_ids, int64_t n, void* pool,
+                  int64_t plane_stride, kvc_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KVC_H_ */

@@ -1,0 +1,309 @@
+"""CPU restatement of the reference's paged-KV algorithms (test infrastructure).
+
+bf16 tensors travel as uint16 bit patterns (numpy has no bfloat16); helpers
+convert with round-to-nearest-even, the rounding torch's .to(bfloat16) uses.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+# ---------------------------------------------------------------------------
+# bf16 <-> fp32 bit helpers
+# ---------------------------------------------------------------------------
+
+
+def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(x: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even fp32 -> bf16 bits (NaN stays NaN)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+def torch_bf16_bits(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def bits_to_torch_bf16(bits: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(bits, dtype=np.uint16).view(np.int16)).view(
+        torch.bfloat16)
+
+
+# ---------------------------------------------------------------------------
+# P1 — append through slot_mapping
+# ---------------------------------------------------------------------------
+
+
+def store_kvcache(key: np.ndarray, value: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
+                  slot_mapping: np.ndarray) -> None:
+    """nanovllm/layers/attention.py:9-30: flat_k[slot_mapping] = key.reshape(N, KVH*D).
+
+    Arrays are raw element bits of any width ([N, KVH, D] and
+    [blocks, page, KVH, D]); negative slots index from the end, as the
+    reference's integer index_put does."""
+    n = key.shape[0]
+    row = key.shape[1] * key.shape[2]
+    flat_k = k_cache.reshape(-1, row)
+    flat_v = v_cache.reshape(-1, row)
+    slots = np.asarray(slot_mapping, dtype=np.int64)
+    flat_k[slots] = key.reshape(n, row)
+    flat_v[slots] = value.reshape(n, row)
+
+
+# ---------------------------------------------------------------------------
+# P3 — int8 quantise / dequantise
+# ---------------------------------------------------------------------------
+
+
+def quant_tokhead(x_bits: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Per-token-per-head symmetric int8 (scripts/archive/p14_int8_kv_probe.py:37-41):
+    amax = |x|.amax(-1) (bf16, exact) -> fp32 -> clamp_min(1e-6); s = amax / 127;
+    code = round_half_even(x / s).clamp(-127, 127).  x_bits [..., D] bf16 bits.
+    Returns (codes int8 [..., D], scales fp32 [...])."""
+    x = bf16_to_f32(x_bits)
+    amax = np.abs(x).max(axis=-1)
+    amax = np.maximum(amax, np.float32(1e-6)).astype(np.float32)
+    s = (amax / np.float32(127.0)).astype(np.float32)
+    q = np.rint((x / s[..., None]).astype(np.float32))
+    q = np.clip(q, -127, 127)
+    return q.astype(np.int8), s
+
+
+def store_int8_tokhead(key_bits, value_bits, k_codes, v_codes, k_scale, v_scale, slot_mapping):
+    """Per-token-head append into the P17 layout (benchmarks/archive/P17-kv-int8.md:9-11):
+    codes [blocks, page, KVH, D] int8, scales [blocks, page, KVH] fp32."""
+    kq, ks = quant_tokhead(key_bits)
+    vq, vs = quant_tokhead(value_bits)
+    kvh, d = key_bits.shape[1], key_bits.shape[2]
+    slots = np.asarray(slot_mapping, dtype=np.int64)
+    k_codes.reshape(-1, kvh, d)[slots] = kq
+    v_codes.reshape(-1, kvh, d)[slots] = vq
+    k_scale.reshape(-1, kvh)[slots] = ks
+    v_scale.reshape(-1, kvh)[slots] = vs
+
+
+def quant_chan(x_bits: np.ndarray, scale: np.ndarray) -> np.ndarray:
+    """Per-channel int8 (nanovllm/kernels/kv_int8.py:53-60, tests/p17_kv_int8.py:47-48):
+    code = clamp(floor(x / s + 0.5), -127, 127), all in fp32."""
+    x = bf16_to_f32(x_bits)
+    q = np.floor((x / scale).astype(np.float32) + np.float32(0.5))
+    return np.clip(q, -127, 127).astype(np.int8)
+
+
+def store_int8_chan(key_bits, value_bits, k_codes, v_codes, k_scale, v_scale, side_k, side_v,
+                    out_idx2d, head_n_out, slot_mapping):
+    """tests/p17_kv_int8.py:39-61 (the bitwise spec of kv_int8.py:29-69):
+    per-channel codes, outlier dims zeroed, exact bf16 outlier values in the
+    compacted per-head side row.  side_* are bf16 bits [blocks, page, KVH, NOUT]."""
+    n, kvh, d = key_bits.shape
+    kq = quant_chan(key_bits, k_scale)
+    vq = quant_chan(value_bits, v_scale)
+    slots = np.asarray(slot_mapping, dtype=np.int64)
+    nout = side_k.shape[-1] if side_k is not None else 0
+    for h in range(kvh):
+        n_h = int(head_n_out[h]) if head_n_out is not None else 0
+        if n_h:
+            dims = np.asarray(out_idx2d[h, :n_h], dtype=np.int64)
+            kq[:, h, dims] = 0
+            vq[:, h, dims] = 0
+            side_k.reshape(-1, kvh, nout)[slots, h, :n_h] = key_bits[:, h, dims]
+            side_v.reshape(-1, kvh, nout)[slots, h, :n_h] = value_bits[:, h, dims]
+    k_codes.reshape(-1, kvh, d)[slots] = kq
+    v_codes.reshape(-1, kvh, d)[slots] = vq
+
+
+def dequant_chan(codes: np.ndarray, dscale: np.ndarray, side_bits, out_idx2d, head_n_out):
+    """nanovllm/kernels/kv_int8.py:96-107: bf16(fp32(code) * dscale), then the
+    head's outlier dims take the side values.  Returns bf16 bits [T, KVH, D]."""
+    out = f32_to_bf16(codes.astype(np.float32) * dscale.astype(np.float32))
+    if side_bits is not None and head_n_out is not None:
+        for h in range(codes.shape[1]):
+            n_h = int(head_n_out[h])
+            for j in range(n_h):
+                out[:, h, int(out_idx2d[h, j])] = side_bits[:, h, j]
+    return out
+
+
+def dequant_tokhead(codes: np.ndarray, scale: np.ndarray) -> np.ndarray:
+    """scripts/archive/p14_int8_kv_probe.py:45-46: bf16(fp32(code) * scale)."""
+    return f32_to_bf16(codes.astype(np.float32) * scale.astype(np.float32)[..., None])
+
+
+# ---------------------------------------------------------------------------
+# P2 — attention references (fp32)
+# ---------------------------------------------------------------------------
+
+
+def _gather_rows(cache: np.ndarray, block_row: np.ndarray, length: int) -> np.ndarray:
+    page = cache.shape[1]
+    nblk = (length + page - 1) // page
+    blocks = np.asarray(block_row[:nblk], dtype=np.int64)
+    return cache[blocks].reshape(-1, *cache.shape[2:])[:length]
+
+
+def kv_float(cache, fmt: str, scale=None, side=None, out_idx2d=None, head_n_out=None):
+    """Pool -> fp32 values as the reference's read path sees them
+    (paged_attention.py:138-145 and :169-172: int8 * scale kept in fp32; the
+    side pool supplies exact outlier values)."""
+    if fmt == "bf16":
+        return bf16_to_f32(cache)
+    if fmt == "int8_tokhead":
+        return cache.astype(np.float32) * scale.astype(np.float32)[..., None]
+    if fmt == "int8_chan":
+        x = cache.astype(np.float32) * scale.astype(np.float32)
+        if side is not None and head_n_out is not None:
+            sf = bf16_to_f32(side)
+            for h in range(cache.shape[-2]):
+                for j in range(int(head_n_out[h])):
+                    x[..., h, int(out_idx2d[h, j])] = sf[..., h, j]
+        return x
+    raise ValueError(fmt)
+
+
+def attend_rows(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float,
+                allowed: np.ndarray | None = None) -> np.ndarray:
+    """softmax(q k^T * scale) v per head in fp32.  q [Sq, H, D]; k, v [Sk, KVH, D]
+    fp32; allowed [Sq, Sk] bool or None.  GQA: q head h reads kv head h // G."""
+    sq, nh, d = q.shape
+    kvh = k.shape[1]
+    g = nh // kvh
+    out = np.empty((sq, nh, d), dtype=np.float32)
+    for h in range(nh):
+        kh = k[:, h // g]
+        vh = v[:, h // g]
+        logits = (q[:, h] @ kh.T).astype(np.float32) * np.float32(scale)
+        if allowed is not None:
+            logits = np.where(allowed, logits, -np.inf)
+        m = logits.max(axis=1, keepdims=True)
+        p = np.exp(logits - m)
+        out[:, h] = (p @ vh) / p.sum(axis=1, keepdims=True)
+    return out
+
+
+def paged_decode_ref(q_bits, k_f32, v_f32, block_tables, context_lens, scale) -> np.ndarray:
+    """Per-(sequence, head) fp32 decode reference (tests/archive/p5_paged_attention.py:9-27;
+    semantics of paged_attention.py:92-190).  q_bits [B, H, D] bf16 bits;
+    k_f32/v_f32 [blocks, page, KVH, D] fp32 (kv_float).  Returns fp32 [B, H, D];
+    a zero-length context gives NaN rows, like the reference kernel's 0/0."""
+    q = bf16_to_f32(q_bits)
+    b, nh, d = q.shape
+    out = np.empty((b, nh, d), dtype=np.float32)
+    for i in range(b):
+        n = int(context_lens[i])
+        if n == 0:
+            out[i] = np.nan
+            continue
+        k = _gather_rows(k_f32, block_tables[i], n)
+        v = _gather_rows(v_f32, block_tables[i], n)
+        out[i] = attend_rows(q[i][None], k, v, scale)[0]
+    return out
+
+
+def prefill_ref(q_bits, k_f32, v_f32, block_tables, cu_q, cu_k, scale, row_offset=0,
+                fresh_k=None, fresh_v=None) -> np.ndarray:
+    """nanovllm/layers/attention.py:179-213: per chunk i, queries at positions
+    sk - sq .. sk - 1 attend keys j <= position (prefix mask :210-212); without
+    block tables (fresh_k/fresh_v given) the keys are the chunk's own rows and
+    the mask is causal (:195-199).  q_bits [T, H, D]; block_tables rows start at
+    row_offset.  Returns fp32 [cu_q[-1], H, D]."""
+    q = bf16_to_f32(q_bits)
+    total = cu_q[-1]
+    out = np.full((total, q.shape[1], q.shape[2]), np.nan, dtype=np.float32)
+    for i in range(len(cu_q) - 1):
+        sq, sk = cu_q[i + 1] - cu_q[i], cu_k[i + 1] - cu_k[i]
+        if sq == 0 or sk == 0:
+            continue
+        if fresh_k is not None:
+            k = fresh_k[cu_k[i]:cu_k[i + 1]]
+            v = fresh_v[cu_k[i]:cu_k[i + 1]]
+        else:
+            k = _gather_rows(k_f32, block_tables[row_offset + i], sk)
+            v = _gather_rows(v_f32, block_tables[row_offset + i], sk)
+        pos = np.arange(sk - sq, sk)[:, None]
+        allowed = np.arange(sk)[None, :] <= pos
+        out[cu_q[i]:cu_q[i + 1]] = attend_rows(q[cu_q[i]:cu_q[i + 1]], k, v, scale, allowed)
+    return out
+
+
+def mixed_ref(q_bits, k_f32, v_f32, block_tables, num_decode_rows, decode_context_lens, cu_q, cu_k,
+              scale) -> np.ndarray:
+    """Mixed batch (attention.py:146-166): decode rows through the decode
+    reference, then prefill rows with block table rows num_decode_rows + i."""
+    n = num_decode_rows
+    dec = paged_decode_ref(q_bits[:n], k_f32, v_f32, block_tables[:n], decode_context_lens, scale)
+    pre = prefill_ref(q_bits[n:], k_f32, v_f32, block_tables, cu_q, cu_k, scale, row_offset=n)
+    return np.concatenate([dec, pre], axis=0)
+
+
+def gather_sdpa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                       block_tables: torch.Tensor, context_lens: torch.Tensor, scale: float,
+                       max_context_len: int) -> torch.Tensor:
+    """The reference's torch decode path (nanovllm/layers/attention.py:239-279) on
+    CPU tensors: gather the padded block tables, zero invalid rows, expand GQA
+    heads, masked SDPA.  This is the CPU baseline bench.py times."""
+    bs, nh = q.shape[0], q.shape[1]
+    page = k_cache.size(1)
+    max_blocks = block_tables.size(1)
+    blocks = block_tables.clamp(min=0).long()
+    full = max_blocks * page
+    kv_len = max_context_len or full
+    k = k_cache[blocks].view(bs, full, *k_cache.shape[-2:])[:, :kv_len]
+    v = v_cache[blocks].view(bs, full, *v_cache.shape[-2:])[:, :kv_len]
+    valid = torch.arange(kv_len).unsqueeze(0) < context_lens.unsqueeze(1)
+    kvh = k.size(2)
+    idx = torch.arange(kvh).repeat_interleave(nh // kvh)
+    qh = q.transpose(0, 1).unsqueeze(2)
+    k = k.index_select(2, idx).permute(2, 0, 1, 3)
+    v = v.index_select(2, idx).permute(2, 0, 1, 3)
+    kv_valid = valid.unsqueeze(0).unsqueeze(-1)
+    k = torch.where(kv_valid, k, torch.zeros((), dtype=k.dtype))
+    v = torch.where(kv_valid, v, torch.zeros((), dtype=v.dtype))
+    mask = valid.unsqueeze(0).unsqueeze(2)
+    o = torch.nn.functional.scaled_dot_product_attention(qh, k, v, attn_mask=mask, scale=scale)
+    return o.squeeze(2).permute(1, 0, 2)
+
+
+# ---------------------------------------------------------------------------
+# P4 — whole-block movement
+# ---------------------------------------------------------------------------
+
+
+def block_gather(pool: np.ndarray, ids) -> np.ndarray:
+    """[planes, blocks, ...] -> [n, planes, ...]: kv_cache.index_select(2, idx)
+    of ModelRunner.offload_put (nanovllm/engine/model_runner.py:284-298) and
+    the per-pool index_select + permute of extract_kv (nanovllm/pd/kv_channel.py:54-69)."""
+    ids = np.asarray(ids, dtype=np.int64)
+    return np.ascontiguousarray(np.moveaxis(pool[:, ids], 1, 0))
+
+
+def block_scatter(pool: np.ndarray, ids, items: np.ndarray) -> None:
+    """pool[:, ids] = items moved back to [planes, n, ...]: index_copy_ of
+    offload_get (model_runner.py:300-305) and import_kv (kv_channel.py:72-82)."""
+    ids = np.asarray(ids, dtype=np.int64)
+    pool[:, ids] = np.moveaxis(items, 0, 1)
+
+
+def block_copy(pool: np.ndarray, src_ids, dst_ids) -> None:
+    """Compaction pool[:, dst] = pool[:, src] with the right-hand side read
+    first (no reference function; the closed form of the copy)."""
+    src = np.asarray(src_ids, dtype=np.int64)
+    dst = np.asarray(dst_ids, dtype=np.int64)
+    pool[:, dst] = pool[:, src].copy()
+
+
+def decode_kv_bytes(context_lens, kvh: int, d: int, elem_bytes: int) -> int:
+    """Algorithmic KV bytes one decode launch must read: every context token's
+    K and V row for every kv head."""
+    return int(np.sum(np.asarray(context_lens, dtype=np.int64))) * 2 * kvh * d * elem_bytes
+
+
+def log2e() -> float:
+    return 1.0 / math.log(2.0)

@@ -1,0 +1,1335 @@
+// Paged attention for gfx950: split-K paged decode and the single-launch
+// mixed decode + chunked-prefill ("varlen") kernel, plus their split-K merge.
+//
+// Work unit: one wavefront owns a "column block" of 16 attention columns.  A
+// column is one (query row, q head) pair; the heads of a column block all
+// read the same kv head, so the block is a real GQA contraction and runs on
+// MFMA (v_mfma_f32_16x16x32_bf16).  Per 32-key tile a wave computes
+//   S^T[key, col] = K[key, :] . Q[col, :]^T            (2 x 4 MFMAs)
+// and, after the online softmax,
+//   O^T[d, col]  += V^T[d, key] . P^T[key, col]        (8 MFMAs)
+// Writing both products transposed puts one column per lane (col = lane % 16)
+// in every accumulator, so the running max / sum and the rescale of O are
+// lane-local; the max and sum reductions over keys are two xor-shuffles.
+// The key order inside the PV contraction is chosen so that the P^T operand
+// is exactly the register set the S^T MFMA produced (no data movement), and
+// V rows are read as whole 16-byte vectors and transposed in registers with
+// v_perm_b32.
+//
+// Decode units read K/V straight from HBM into registers (each byte is used by
+// exactly one wave, so LDS staging would only add traffic) with the next tile
+// in flight while the current one is computed.  Prefill units stage each K/V
+// tile in LDS once and four waves (different query columns) consume it.
+#include <cmath>
+#include <cstdlib>
+
+#include "kvc_internal.h"
+
+namespace kvc {
+namespace {
+
+constexpr int kD = 128;
+constexpr int kTile = 32;
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kSideMax = 8;
+constexpr int kPreNCB = 2;  // column blocks per wave in prefill units
+
+enum Enc : int { kBF16 = KVC_KV_BF16, kI8Tok = KVC_KV_INT8_TOKHEAD, kI8Chan = KVC_KV_INT8_CHAN };
+
+struct AttnParams {
+  // queries / outputs (element strides)
+  const uint16_t* q;
+  int64_t q_st, q_sh;
+  uint16_t* out;
+  int64_t o_st, o_sh;
+  int num_heads, kvh, group, hs, nslices, tpb;
+  float scale_log2;
+  // paged pool
+  const char* k_cache;
+  const char* v_cache;
+  int page;
+  int64_t tok_bytes;  // bytes between consecutive slots
+  const float* k_scale;
+  const float* v_scale;
+  const uint16_t* side_k;
+  const uint16_t* side_v;
+  const int32_t* out_idx;
+  const int32_t* head_n_out;
+  int n_out_max;
+  const int32_t* block_tables;
+  int64_t bt_stride;
+  // decode rows
+  int n_dec;
+  const int32_t* ctx_lens;
+  int chunk_tokens;
+  int dec_max_chunks;
+  int dec_units;
+  // prefill chunks
+  int n_pre;
+  const int32_t* cu_q;
+  const int32_t* cu_k;
+  int split_tokens;
+  int pre_units;
+  const uint16_t* kf;
+  int64_t kf_st, kf_sh;
+  const uint16_t* vf;
+  int64_t vf_st, vf_sh;
+  // split-K partials: [rows, heads, max_splits, D] fp32 and [rows, heads, max_splits]
+  float* part_o;
+  float* part_lse;
+  int max_splits;
+};
+
+struct LaneId {
+  int lane, lm, lg;
+};
+
+__device__ __forceinline__ LaneId lane_id() {
+  const int lane = threadIdx.x & 63;
+  return {lane, lane & 15, lane >> 4};
+}
+
+// Key (within a tile) carried by k-slot i of lane group lg: slots 0-3 are the
+// S^T rows of the first 16-key half, slots 4-7 those of the second half.
+__device__ __forceinline__ int key_of_slot(int lg, int i) {
+  return i < 4 ? 4 * lg + i : 12 + 4 * lg + i;
+}
+
+// ---------------------------------------------------------------------------
+// Per-tile operand registers.
+// bf16: k[h][c] = key h*16+lm, dims 32c+8lg..+8;  v[i] = key slot i, dims 8lm..+8
+// int8: k[h][w] = key h*16+lm, dims 32lg+16w..+16; v[i] = key slot i, dims 8lm..+8
+// ---------------------------------------------------------------------------
+template <int kEnc>
+struct Tile;
+
+template <>
+struct Tile<kBF16> {
+  u32x4_t k[2][4];
+  u32x4_t v[8];
+};
+
+template <>
+struct Tile<kI8Tok> {
+  u32x4_t k[2][2];
+  u32x2_t v[8];
+  float ks[8];
+  float vs[8];
+};
+
+template <>
+struct Tile<kI8Chan> {
+  u32x4_t k[2][2];
+  u32x2_t v[8];
+};
+
+template <int NCB>
+struct ColState {
+  f32x4_t o[NCB][8];  // O^T: [col block][d chunk jj], row r -> d = 32lg + 8r + jj
+  float m[NCB];       // running max (log2 domain), identical on the 4 lanes of a column
+  float l[NCB];       // lane-partial softmax sum
+  float vb[NCB];      // lane-partial sum of the bf16 P operand (int8 bias correction)
+  float sd[NCB][kSideMax];  // lane-partial side-pool PV (per-channel int8 only)
+};
+
+template <int NCB>
+__device__ __forceinline__ void init_state(ColState<NCB>& st) {
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) {
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) st.o[cb][jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    st.m[cb] = -INFINITY;
+    st.l[cb] = 0.f;
+    st.vb[cb] = 0.f;
+#pragma unroll
+    for (int j = 0; j < kSideMax; ++j) st.sd[cb][j] = 0.f;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Tile loads from a paged pool in HBM (decode units).  `base` points at the
+// tile's first key, head g, dim 0; `tok` is the slot stride in bytes.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void load_tile_global(Tile<kBF16>& t, const char* kb, const char* vb,
+                                                 int64_t tok, const LaneId& L) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const char* row = kb + int64_t(h * 16 + L.lm) * tok + L.lg * 16;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) t.k[h][c] = *reinterpret_cast<const u32x4_t*>(row + c * 64);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    t.v[i] = *reinterpret_cast<const u32x4_t*>(vb + int64_t(key_of_slot(L.lg, i)) * tok + L.lm * 16);
+}
+
+template <int kEnc>
+__device__ __forceinline__ void load_tile_global_i8(Tile<kEnc>& t, const char* kb, const char* vb,
+                                                    int64_t tok, const LaneId& L) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const char* row = kb + int64_t(h * 16 + L.lm) * tok + L.lg * 32;
+    t.k[h][0] = *reinterpret_cast<const u32x4_t*>(row);
+    t.k[h][1] = *reinterpret_cast<const u32x4_t*>(row + 16);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    t.v[i] = *reinterpret_cast<const u32x2_t*>(vb + int64_t(key_of_slot(L.lg, i)) * tok + L.lm * 8);
+}
+
+// Scales of the lane's 8 key slots (per-token-head int8).  `sbase` points at
+// the scale of the tile's first key for head g; consecutive keys are kvh apart.
+__device__ __forceinline__ void load_scales(Tile<kI8Tok>& t, const float* ksb, const float* vsb,
+                                            int kvh, const LaneId& L) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int64_t o = int64_t(key_of_slot(L.lg, i)) * kvh;
+    t.ks[i] = ksb[o];
+    t.vs[i] = vsb[o];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Operand formation.
+// ---------------------------------------------------------------------------
+// 8 int8 codes -> 8 bf16 of (code + 128), exact (0..255 fit bf16's mantissa).
+__device__ __forceinline__ u32x4_t i8x8_biased_bf16(uint32_t w0, uint32_t w1) {
+  w0 ^= 0x80808080u;
+  w1 ^= 0x80808080u;
+  const float f0 = float(w0 & 0xffu), f1 = float((w0 >> 8) & 0xffu);
+  const float f2 = float((w0 >> 16) & 0xffu), f3 = float(w0 >> 24);
+  const float f4 = float(w1 & 0xffu), f5 = float((w1 >> 8) & 0xffu);
+  const float f6 = float((w1 >> 16) & 0xffu), f7 = float(w1 >> 24);
+  return u32x4_t{perm(__float_as_uint(f1), __float_as_uint(f0), kPermHiHi),
+                 perm(__float_as_uint(f3), __float_as_uint(f2), kPermHiHi),
+                 perm(__float_as_uint(f5), __float_as_uint(f4), kPermHiHi),
+                 perm(__float_as_uint(f7), __float_as_uint(f6), kPermHiHi)};
+}
+
+// K operand for MFMA (key half h, d chunk c).
+__device__ __forceinline__ u32x4_t k_operand(const Tile<kBF16>& t, int h, int c) {
+  return t.k[h][c];
+}
+template <int kEnc>
+__device__ __forceinline__ u32x4_t k_operand_i8(const Tile<kEnc>& t, int h, int c) {
+  const u32x4_t w = t.k[h][c >> 1];
+  return (c & 1) ? i8x8_biased_bf16(w[2], w[3]) : i8x8_biased_bf16(w[0], w[1]);
+}
+
+// V^T operands: va[jj] holds, for MFMA row m = lm (d = 8lm + jj), the 8 keys
+// of the lane's k-slots.  Keys >= valid_end are zeroed (bf16: a poisoned tail
+// must not reach 0 * NaN inside the MFMA).
+__device__ __forceinline__ void v_operands(const Tile<kBF16>& t, u32x4_t (&va)[8], int key0,
+                                           int valid_end, const LaneId& L) {
+  u32x4_t v[8];
+  const bool tail = key0 + kTile > valid_end;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    v[i] = t.v[i];
+    if (tail && key0 + key_of_slot(L.lg, i) >= valid_end) v[i] = u32x4_t{0u, 0u, 0u, 0u};
+  }
+#pragma unroll
+  for (int jj = 0; jj < 8; ++jj) {
+    const uint32_t sel = (jj & 1) ? kPermHiHi : kPermLoLo;
+    const int dw = jj >> 1;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) va[jj][w] = perm(v[2 * w + 1][dw], v[2 * w][dw], sel);
+  }
+}
+
+template <int kEnc>
+__device__ __forceinline__ void v_operands_i8(const Tile<kEnc>& t, u32x4_t (&va)[8]) {
+  uint32_t w[8][2];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    w[i][0] = t.v[i][0] ^ 0x80808080u;
+    w[i][1] = t.v[i][1] ^ 0x80808080u;
+  }
+#pragma unroll
+  for (int jj = 0; jj < 8; ++jj) {
+    const int dw = jj >> 2, sh = (jj & 3) * 8;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const float a = float((w[2 * s][dw] >> sh) & 0xffu);
+      const float b = float((w[2 * s + 1][dw] >> sh) & 0xffu);
+      va[jj][s] = perm(__float_as_uint(b), __float_as_uint(a), kPermHiHi);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Query side of a column block.
+// ---------------------------------------------------------------------------
+struct ColInfo {
+  int64_t row;  // query row (output row)
+  int head;     // q head
+  bool valid;
+  int klim;     // largest key index the column may attend (inclusive)
+};
+
+template <int kEnc, int NCB>
+struct QOps {
+  u32x4_t op[NCB][4];
+  // Per-channel int8 folds the read scale into the query, q' = q * s; q' is
+  // carried as a bf16 pair hi + lo (about 16 mantissa bits) because a single
+  // bf16 rounding of a large-scale channel moves logits visibly.
+  u32x4_t lo[NCB][4];
+  float qsum[NCB];           // int8: sum over d of the query operand(s)
+  float qout[NCB][kSideMax]; // per-channel int8: query at the head's outlier dims
+};
+
+template <int kEnc, int NCB>
+__device__ __forceinline__ void build_q(QOps<kEnc, NCB>& Q, const AttnParams& p,
+                                        const ColInfo (&ci)[NCB], int g, const LaneId& L) {
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) {
+    const uint16_t* qrow = p.q + ci[cb].row * p.q_st + int64_t(ci[cb].head) * p.q_sh;
+    float part = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      // bf16 pool: dims 32c + 8lg; int8 pools: dims 32lg + 8c.
+      const int d0 = (kEnc == kBF16) ? (32 * c + 8 * L.lg) : (32 * L.lg + 8 * c);
+      u32x4_t w = u32x4_t{0u, 0u, 0u, 0u};
+      if (ci[cb].valid) w = *reinterpret_cast<const u32x4_t*>(qrow + d0);
+      if constexpr (kEnc == kI8Chan) {
+        // q'[d] = q[d] * s[g][d] in fp32, split as hi = bf16(q'), lo = bf16(q' - hi).
+        const float* ds = p.k_scale + g * kD + d0;
+        u32x4_t wl;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float a = bf16_bits_to_f32(w[e] & 0xffffu) * ds[2 * e];
+          const float b = bf16_bits_to_f32(w[e] >> 16) * ds[2 * e + 1];
+          const uint32_t ah = f32_to_bf16_bits(a), bh = f32_to_bf16_bits(b);
+          w[e] = ah | (bh << 16);
+          wl[e] = pack_bf16x2(a - bf16_bits_to_f32(ah), b - bf16_bits_to_f32(bh));
+          part += bf16_bits_to_f32(wl[e] & 0xffffu) + bf16_bits_to_f32(wl[e] >> 16);
+        }
+        Q.lo[cb][c] = wl;
+      }
+      if constexpr (kEnc != kBF16) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) part += bf16_bits_to_f32(w[e] & 0xffffu) + bf16_bits_to_f32(w[e] >> 16);
+      }
+      Q.op[cb][c] = w;
+    }
+    if constexpr (kEnc != kBF16) {
+      part += shfl_xor(part, 16);
+      part += shfl_xor(part, 32);
+      Q.qsum[cb] = part;
+    }
+    if constexpr (kEnc == kI8Chan) {
+      const int n_out = p.head_n_out != nullptr ? p.head_n_out[g] : 0;
+#pragma unroll
+      for (int j = 0; j < kSideMax; ++j) {
+        float v = 0.f;
+        if (ci[cb].valid && j < n_out) v = bf16_bits_to_f32(qrow[p.out_idx[g * p.n_out_max + j]]);
+        Q.qout[cb][j] = v;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// One 32-key tile against NCB column blocks.
+//   key0       absolute index of the tile's first key
+//   valid_end  keys >= valid_end do not exist (masked and zeroed)
+//   slot0      pool slot of the tile's first key (side pool rows; -1 if none)
+// ---------------------------------------------------------------------------
+template <int kEnc, int NCB>
+__device__ __forceinline__ void attend_tile(ColState<NCB>& st, const Tile<kEnc>& t,
+                                            const QOps<kEnc, NCB>& Q, const ColInfo (&ci)[NCB],
+                                            int key0, int valid_end, int64_t slot0,
+                                            const AttnParams& p, int g, const LaneId& L) {
+  u32x4_t ka[2][4];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if constexpr (kEnc == kBF16) {
+        ka[h][c] = k_operand(t, h, c);
+      } else {
+        ka[h][c] = k_operand_i8(t, h, c);
+      }
+    }
+  }
+  u32x4_t va[8];
+  if constexpr (kEnc == kBF16) {
+    v_operands(t, va, key0, valid_end, L);
+  } else {
+    v_operands_i8(t, va);
+  }
+  bool kvalid[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) kvalid[i] = key0 + key_of_slot(L.lg, i) < valid_end;
+
+  // Side-pool rows of the lane's keys (per-channel int8 with outlier dims).
+  int n_out = 0;
+  if constexpr (kEnc == kI8Chan) {
+    if (p.head_n_out != nullptr) n_out = p.head_n_out[g];
+  }
+
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) {
+    f32x4_t s0 = f32x4_t{0.f, 0.f, 0.f, 0.f}, s1 = s0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      s0 = mfma_bf16(ka[0][c], Q.op[cb][c], s0);
+      s1 = mfma_bf16(ka[1][c], Q.op[cb][c], s1);
+      if constexpr (kEnc == kI8Chan) {
+        s0 = mfma_bf16(ka[0][c], Q.lo[cb][c], s0);
+        s1 = mfma_bf16(ka[1][c], Q.lo[cb][c], s1);
+      }
+    }
+    float x[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+    if constexpr (kEnc != kBF16) {
+      const float bias = 128.f * Q.qsum[cb];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x[i] -= bias;
+    }
+    if constexpr (kEnc == kI8Tok) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x[i] *= t.ks[i];
+    }
+    if constexpr (kEnc == kI8Chan) {
+      if (n_out > 0) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const uint16_t* srow =
+              p.side_k + ((slot0 + key_of_slot(L.lg, i)) * p.kvh + g) * p.n_out_max;
+          float acc = 0.f;
+#pragma unroll
+          for (int j = 0; j < kSideMax; ++j)
+            if (j < n_out) acc += Q.qout[cb][j] * bf16_bits_to_f32(srow[j]);
+          x[i] += acc;
+        }
+      }
+    }
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const bool ok = kvalid[i] && (key0 + key_of_slot(L.lg, i) <= ci[cb].klim);
+      x[i] = ok ? x[i] * p.scale_log2 : -INFINITY;
+      tmax = fmaxf(tmax, x[i]);
+    }
+    tmax = fmaxf(tmax, shfl_xor(tmax, 16));
+    tmax = fmaxf(tmax, shfl_xor(tmax, 32));
+    const float m_new = fmaxf(st.m[cb], tmax);
+    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(st.m[cb] - m_use);
+    st.m[cb] = m_new;
+    float pr[8], psum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      pr[i] = __builtin_amdgcn_exp2f(x[i] - m_use);
+      psum += pr[i];
+    }
+    st.l[cb] = st.l[cb] * alpha + psum;
+    // P^T operand (k-slot order == the S^T register order).
+    float pv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if constexpr (kEnc == kI8Tok) {
+        pv[i] = kvalid[i] ? pr[i] * t.vs[i] : 0.f;
+      } else {
+        pv[i] = pr[i];
+      }
+    }
+    u32x4_t pb;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) pb[w] = pack_bf16x2(pv[2 * w], pv[2 * w + 1]);
+    if constexpr (kEnc != kBF16) {
+      float vsum = 0.f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) vsum += bf16_bits_to_f32(pb[w] & 0xffffu) + bf16_bits_to_f32(pb[w] >> 16);
+      st.vb[cb] = st.vb[cb] * alpha + vsum;
+    }
+    if constexpr (kEnc == kI8Chan) {
+      if (n_out > 0) {
+#pragma unroll
+        for (int j = 0; j < kSideMax; ++j) st.sd[cb][j] *= alpha;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          if (!kvalid[i]) continue;
+          const uint16_t* srow =
+              p.side_v + ((slot0 + key_of_slot(L.lg, i)) * p.kvh + g) * p.n_out_max;
+#pragma unroll
+          for (int j = 0; j < kSideMax; ++j)
+            if (j < n_out) st.sd[cb][j] += pr[i] * bf16_bits_to_f32(srow[j]);
+        }
+      }
+    }
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      f32x4_t o = st.o[cb][jj];
+      o[0] *= alpha;
+      o[1] *= alpha;
+      o[2] *= alpha;
+      o[3] *= alpha;
+      st.o[cb][jj] = mfma_bf16(va[jj], pb, o);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Epilogue helpers.  A wave dumps one column block (unnormalised O, final
+// max and sum) into LDS: obuf[col][d] fp32, ml[col] = (m, l).
+// ---------------------------------------------------------------------------
+struct WaveOut {
+  float o[16][kD];
+  float m[16];
+  float l[16];
+};
+
+template <int kEnc, int NCB>
+__device__ __forceinline__ void dump_block(WaveOut& wo, const ColState<NCB>& st, int cb,
+                                           const AttnParams& p, int g, const LaneId& L) {
+  float l = st.l[cb];
+  l += shfl_xor(l, 16);
+  l += shfl_xor(l, 32);
+  float bias = 0.f;
+  if constexpr (kEnc != kBF16) {
+    float vb = st.vb[cb];
+    vb += shfl_xor(vb, 16);
+    vb += shfl_xor(vb, 32);
+    bias = 128.f * vb;
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int d0 = 32 * L.lg + 8 * r;
+    float v[8];
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) v[jj] = st.o[cb][jj][r] - bias;
+    if constexpr (kEnc == kI8Chan) {
+      const float* vs = p.v_scale + g * kD + d0;
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) v[jj] *= vs[jj];
+    }
+    float4* dst = reinterpret_cast<float4*>(&wo.o[L.lm][d0]);
+    dst[0] = make_float4(v[0], v[1], v[2], v[3]);
+    dst[1] = make_float4(v[4], v[5], v[6], v[7]);
+  }
+  if (L.lg == 0) {
+    wo.m[L.lm] = st.m[cb];
+    wo.l[L.lm] = l;
+  }
+  if constexpr (kEnc == kI8Chan) {
+    const int n_out = p.head_n_out != nullptr ? p.head_n_out[g] : 0;
+    float sd[kSideMax];
+#pragma unroll
+    for (int j = 0; j < kSideMax; ++j) {
+      float s = st.sd[cb][j];
+      s += shfl_xor(s, 16);
+      s += shfl_xor(s, 32);
+      sd[j] = s;
+    }
+    // The main path left exactly 0 at the outlier dims (read scale 0 there);
+    // the exact side contribution takes their place.
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+    if (L.lg == 0) {
+#pragma unroll
+      for (int j = 0; j < kSideMax; ++j)
+        if (j < n_out) wo.o[L.lm][p.out_idx[g * p.n_out_max + j]] = sd[j];
+    }
+  }
+}
+
+__device__ __forceinline__ void store_final(const AttnParams& p, int64_t row, int head, int d0,
+                                            const float (&v)[8], float inv_l) {
+  uint16_t* dst = p.out + row * p.o_st + int64_t(head) * p.o_sh + d0;
+  *reinterpret_cast<u32x4_t*>(dst) =
+      u32x4_t{pack_bf16x2(v[0] * inv_l, v[1] * inv_l), pack_bf16x2(v[2] * inv_l, v[3] * inv_l),
+              pack_bf16x2(v[4] * inv_l, v[5] * inv_l), pack_bf16x2(v[6] * inv_l, v[7] * inv_l)};
+}
+
+__device__ __forceinline__ void store_partial(const AttnParams& p, int64_t row, int head, int split,
+                                              int d0, const float (&v)[8], float m, float l) {
+  const int64_t base = (row * p.num_heads + head) * p.max_splits + split;
+  const float inv_l = l > 0.f ? 1.f / l : 0.f;
+  float4* dst = reinterpret_cast<float4*>(p.part_o + base * kD + d0);
+  dst[0] = make_float4(v[0] * inv_l, v[1] * inv_l, v[2] * inv_l, v[3] * inv_l);
+  dst[1] = make_float4(v[4] * inv_l, v[5] * inv_l, v[6] * inv_l, v[7] * inv_l);
+  if (d0 == 0) p.part_lse[base] = l > 0.f ? m + __log2f(l) : -INFINITY;
+}
+
+constexpr int kDecodeSmem = kWaves * int(sizeof(WaveOut));
+constexpr int kPitchBF16 = kD * 2 + 16;
+constexpr int kPitchI8 = kD + 16;
+constexpr int kTileBytesBF16 = kTile * kPitchBF16;
+// Two buffers of (K tile, V tile, K scales, V scales).
+constexpr int kPrefillStage = 2 * kTileBytesBF16 + 2 * kTile * 4;
+constexpr int kPrefillSmem = 2 * kPrefillStage;
+constexpr int kSmemBytes = kDecodeSmem > kPrefillSmem ? kDecodeSmem : kPrefillSmem;
+
+// ---------------------------------------------------------------------------
+// Decode unit: (row b, kv head g / head slice s, key chunk).  The four waves
+// split the chunk's tiles and merge through LDS.
+// ---------------------------------------------------------------------------
+template <int kEnc>
+__device__ void decode_unit(const AttnParams& p, char* smem, int b, int kvs, int chunk) {
+  const LaneId L = lane_id();
+  const int wave = threadIdx.x >> 6;
+  const int g = kvs / p.nslices;
+  const int s = kvs - g * p.nslices;
+  const int hs = min(p.hs, p.group - s * p.hs);
+  const int ctx = p.ctx_lens[b];
+  const int nch = ctx > 0 ? (ctx + p.chunk_tokens - 1) / p.chunk_tokens : 1;
+  if (chunk >= nch) return;  // uniform over the workgroup
+  const int c0 = chunk * p.chunk_tokens;
+  const int c1 = min(c0 + p.chunk_tokens, ctx);
+  const int ntiles = c1 > c0 ? (c1 - c0 + kTile - 1) / kTile : 0;
+  const int t_begin = (wave * ntiles) / kWaves;
+  const int t_end = ((wave + 1) * ntiles) / kWaves;
+
+  ColInfo ci[1];
+  ci[0].row = b;
+  ci[0].head = g * p.group + s * p.hs + L.lm;
+  ci[0].valid = L.lm < hs;
+  ci[0].klim = ctx - 1;
+  QOps<kEnc, 1> Q;
+  build_q<kEnc, 1>(Q, p, ci, g, L);
+  ColState<1> st;
+  init_state(st);
+
+  const int32_t* bt = p.block_tables + int64_t(b) * p.bt_stride;
+  const int64_t head_off = int64_t(g) * ((kEnc == kBF16) ? kD * 2 : kD);
+  auto tile_slot0 = [&](int tix) -> int64_t {
+    const int key0 = c0 + tix * kTile;
+    const int blk = uniform(bt[key0 / p.page]);
+    return int64_t(blk) * p.page + (key0 % p.page);
+  };
+  auto load = [&](Tile<kEnc>& t, int64_t slot0) {
+    const char* kb = p.k_cache + slot0 * p.tok_bytes + head_off;
+    const char* vb = p.v_cache + slot0 * p.tok_bytes + head_off;
+    if constexpr (kEnc == kBF16) {
+      load_tile_global(t, kb, vb, p.tok_bytes, L);
+    } else {
+      load_tile_global_i8<kEnc>(t, kb, vb, p.tok_bytes, L);
+    }
+    if constexpr (kEnc == kI8Tok) {
+      load_scales(t, p.k_scale + slot0 * p.kvh + g, p.v_scale + slot0 * p.kvh + g, p.kvh, L);
+    }
+  };
+
+  if (t_begin < t_end) {
+    Tile<kEnc> ta, tb;
+    int64_t sa = tile_slot0(t_begin), sb = 0;
+    load(ta, sa);
+    for (int tix = t_begin; tix < t_end; tix += 2) {
+      const bool has_b = tix + 1 < t_end;
+      if (has_b) {
+        sb = tile_slot0(tix + 1);
+        load(tb, sb);
+      }
+      attend_tile<kEnc, 1>(st, ta, Q, ci, c0 + tix * kTile, ctx, sa, p, g, L);
+      if (!has_b) break;
+      if (tix + 2 < t_end) {
+        sa = tile_slot0(tix + 2);
+        load(ta, sa);
+      }
+      attend_tile<kEnc, 1>(st, tb, Q, ci, c0 + (tix + 1) * kTile, ctx, sb, p, g, L);
+    }
+  }
+
+  WaveOut* wo = reinterpret_cast<WaveOut*>(smem);
+  dump_block<kEnc, 1>(wo[wave], st, 0, p, g, L);
+  __syncthreads();
+  // Merge the four waves: thread -> (column, 8 dims).
+  const int col = threadIdx.x >> 4;
+  const int d0 = (threadIdx.x & 15) * 8;
+  if (col < hs) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) m = fmaxf(m, wo[w].m[col]);
+    const float m_use = (m == -INFINITY) ? 0.f : m;
+    float l = 0.f, v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float e = __builtin_amdgcn_exp2f(wo[w].m[col] - m_use);
+      l += e * wo[w].l[col];
+      const float4 a = *reinterpret_cast<const float4*>(&wo[w].o[col][d0]);
+      const float4 c = *reinterpret_cast<const float4*>(&wo[w].o[col][d0 + 4]);
+      v[0] += e * a.x; v[1] += e * a.y; v[2] += e * a.z; v[3] += e * a.w;
+      v[4] += e * c.x; v[5] += e * c.y; v[6] += e * c.z; v[7] += e * c.w;
+    }
+    const int head = g * p.group + s * p.hs + col;
+    if (nch == 1) {
+      store_final(p, b, head, d0, v, 1.f / l);
+    } else {
+      store_partial(p, b, head, chunk, d0, v, m, l);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Prefill unit: (chunk i, query tile, kv head g / slice s, key split).  The
+// workgroup covers 4 waves x kPreNCB column blocks; K/V tiles go through LDS.
+// ---------------------------------------------------------------------------
+template <int kEnc, bool kFresh>
+__device__ void prefill_unit(const AttnParams& p, char* smem, int i, int qt, int kvs, int split) {
+  const LaneId L = lane_id();
+  const int wave = threadIdx.x >> 6;
+  const int g = kvs / p.nslices;
+  const int s = kvs - g * p.nslices;
+  const int hs = min(p.hs, p.group - s * p.hs);
+  const int cq0 = p.cu_q[i];
+  const int sq = p.cu_q[i + 1] - cq0;
+  const int ck0 = p.cu_k[i];
+  const int sk = p.cu_k[i + 1] - ck0;
+  const int prefix = sk - sq;
+  const int qtile_tokens = kWaves * kPreNCB * p.tpb;
+  const int q0 = qt * qtile_tokens;
+  const int nsplit = max(1, (sk + p.split_tokens - 1) / p.split_tokens);
+
+  ColInfo ci[kPreNCB];
+#pragma unroll
+  for (int cb = 0; cb < kPreNCB; ++cb) {
+    const int tq = q0 + (wave * kPreNCB + cb) * p.tpb + L.lm / p.hs;
+    const int hh = L.lm % p.hs;
+    const bool ok = (L.lm < p.tpb * p.hs) && hh < hs && tq < sq;
+    ci[cb].row = int64_t(p.n_dec) + cq0 + (ok ? tq : 0);
+    ci[cb].head = g * p.group + s * p.hs + hh;
+    ci[cb].valid = ok;
+    ci[cb].klim = ok ? prefix + tq : -1;
+  }
+  QOps<kEnc, kPreNCB> Q;
+  build_q<kEnc, kPreNCB>(Q, p, ci, g, L);
+  ColState<kPreNCB> st;
+  init_state(st);
+
+  // Key range of this split, cut at the last key any column of the tile sees.
+  const int last_q = min(q0 + qtile_tokens, sq) - 1;
+  const int k_begin = split * p.split_tokens;
+  const int k_end = min(min(k_begin + p.split_tokens, sk), prefix + last_q + 1);
+  const int ntiles = k_end > k_begin ? (k_end - k_begin + kTile - 1) / kTile : 0;
+
+  const int32_t* bt = kFresh ? nullptr : p.block_tables + int64_t(p.n_dec + i) * p.bt_stride;
+  constexpr int kPitch = (kEnc == kBF16) ? kPitchBF16 : kPitchI8;
+  constexpr int kRowBytes = (kEnc == kBF16) ? kD * 2 : kD;
+  constexpr int kVecPerRow = kRowBytes / 16;
+  constexpr int kVecPerTile = kTile * kVecPerRow;  // per tensor
+  constexpr int kLoadsPerThread = (2 * kVecPerTile + kThreads - 1) / kThreads;
+  const int64_t head_off = int64_t(g) * kRowBytes;
+
+  auto stage_ptr = [&](int buf) { return smem + buf * kPrefillStage; };
+  auto tile_slot0 = [&](int tix) -> int64_t {
+    const int key0 = k_begin + tix * kTile;
+    if constexpr (kFresh) {
+      return int64_t(ck0) + key0;
+    } else {
+      const int blk = uniform(bt[key0 / p.page]);
+      return int64_t(blk) * p.page + (key0 % p.page);
+    }
+  };
+  // Cooperative global -> register fetch of one tile (16 B per element).
+  u32x4_t pre[kLoadsPerThread];
+  float pre_s = 0.f;
+  auto fetch = [&](int64_t slot0, int key0) {
+#pragma unroll
+    for (int e = 0; e < kLoadsPerThread; ++e) {
+      const int idx = e * kThreads + threadIdx.x;
+      pre[e] = u32x4_t{0u, 0u, 0u, 0u};
+      if (idx < 2 * kVecPerTile) {
+        const int tensor = idx / kVecPerTile;
+        const int rem = idx - tensor * kVecPerTile;
+        const int key = rem / kVecPerRow;
+        const int vec = rem - key * kVecPerRow;
+        if (key0 + key < sk) {
+          if constexpr (kFresh) {
+            const uint16_t* src = tensor == 0 ? p.kf + (slot0 + key) * p.kf_st + int64_t(g) * p.kf_sh
+                                              : p.vf + (slot0 + key) * p.vf_st + int64_t(g) * p.vf_sh;
+            pre[e] = reinterpret_cast<const u32x4_t*>(src)[vec];
+          } else {
+            const char* src = (tensor == 0 ? p.k_cache : p.v_cache) + (slot0 + key) * p.tok_bytes +
+                              head_off;
+            pre[e] = reinterpret_cast<const u32x4_t*>(src)[vec];
+          }
+        }
+      }
+    }
+    if constexpr (kEnc == kI8Tok) {
+      if (threadIdx.x < 2 * kTile) {
+        const int key = threadIdx.x & (kTile - 1);
+        const float* sp = (threadIdx.x < kTile) ? p.k_scale : p.v_scale;
+        pre_s = (key0 + key < sk) ? sp[(slot0 + key) * p.kvh + g] : 0.f;
+      }
+    }
+  };
+  auto commit = [&](int buf) {
+    char* st_base = stage_ptr(buf);
+#pragma unroll
+    for (int e = 0; e < kLoadsPerThread; ++e) {
+      const int idx = e * kThreads + threadIdx.x;
+      if (idx < 2 * kVecPerTile) {
+        const int tensor = idx / kVecPerTile;
+        const int rem = idx - tensor * kVecPerTile;
+        const int key = rem / kVecPerRow;
+        const int vec = rem - key * kVecPerRow;
+        char* dst = st_base + tensor * kTileBytesBF16 + key * kPitch + vec * 16;
+        *reinterpret_cast<u32x4_t*>(dst) = pre[e];
+      }
+    }
+    if constexpr (kEnc == kI8Tok) {
+      if (threadIdx.x < 2 * kTile)
+        reinterpret_cast<float*>(st_base + 2 * kTileBytesBF16)[threadIdx.x] = pre_s;
+    }
+  };
+  // LDS -> operand registers, same lane mapping as the HBM loads.
+  auto read_tile = [&](Tile<kEnc>& t, int buf) {
+    const char* kb = stage_ptr(buf);
+    const char* vb = kb + kTileBytesBF16;
+    if constexpr (kEnc == kBF16) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const char* row = kb + (h * 16 + L.lm) * kPitch + L.lg * 16;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) t.k[h][c] = *reinterpret_cast<const u32x4_t*>(row + c * 64);
+      }
+#pragma unroll
+      for (int ii = 0; ii < 8; ++ii)
+        t.v[ii] = *reinterpret_cast<const u32x4_t*>(vb + key_of_slot(L.lg, ii) * kPitch + L.lm * 16);
+    } else {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const char* row = kb + (h * 16 + L.lm) * kPitch + L.lg * 32;
+        t.k[h][0] = *reinterpret_cast<const u32x4_t*>(row);
+        t.k[h][1] = *reinterpret_cast<const u32x4_t*>(row + 16);
+      }
+#pragma unroll
+      for (int ii = 0; ii < 8; ++ii)
+        t.v[ii] = *reinterpret_cast<const u32x2_t*>(vb + key_of_slot(L.lg, ii) * kPitch + L.lm * 8);
+      if constexpr (kEnc == kI8Tok) {
+        const float* sc = reinterpret_cast<const float*>(kb + 2 * kTileBytesBF16);
+#pragma unroll
+        for (int ii = 0; ii < 8; ++ii) {
+          t.ks[ii] = sc[key_of_slot(L.lg, ii)];
+          t.vs[ii] = sc[kTile + key_of_slot(L.lg, ii)];
+        }
+      }
+    }
+  };
+
+  if (ntiles > 0) {
+    int64_t slot_cur = tile_slot0(0);
+    fetch(slot_cur, k_begin);
+    commit(0);
+    __syncthreads();
+    for (int tix = 0; tix < ntiles; ++tix) {
+      const int buf = tix & 1;
+      const bool has_next = tix + 1 < ntiles;
+      int64_t slot_next = 0;
+      if (has_next) {
+        slot_next = tile_slot0(tix + 1);
+        fetch(slot_next, k_begin + (tix + 1) * kTile);
+      }
+      Tile<kEnc> t;
+      read_tile(t, buf);
+      attend_tile<kEnc, kPreNCB>(st, t, Q, ci, k_begin + tix * kTile, sk, kFresh ? -1 : slot_cur,
+                                 p, g, L);
+      if (has_next) commit(buf ^ 1);
+      __syncthreads();
+      slot_cur = slot_next;
+    }
+  }
+
+  // Epilogue: each wave finalises its own columns (no cross-wave merge).
+  WaveOut* wo = reinterpret_cast<WaveOut*>(smem);
+#pragma unroll
+  for (int cb = 0; cb < kPreNCB; ++cb) {
+    dump_block<kEnc, kPreNCB>(wo[wave], st, cb, p, g, L);
+    __syncthreads();
+    // Lane -> (column lm, 32 dims of group lg) of this wave's block.
+    const int col = L.lm;
+    const int tq = q0 + (wave * kPreNCB + cb) * p.tpb + col / p.hs;
+    const int hh = col % p.hs;
+    if (col < p.tpb * p.hs && hh < hs && tq < sq) {
+      const int64_t row = int64_t(p.n_dec) + cq0 + tq;
+      const int head = g * p.group + s * p.hs + hh;
+      const float m = wo[wave].m[col];
+      const float l = wo[wave].l[col];
+#pragma unroll
+      for (int part = 0; part < 4; ++part) {
+        const int d0 = 32 * L.lg + 8 * part;
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = wo[wave].o[col][d0 + e];
+        if (nsplit == 1) {
+          store_final(p, row, head, d0, v, 1.f / l);
+        } else {
+          store_partial(p, row, head, split, d0, v, m, l);
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Kernels.
+// ---------------------------------------------------------------------------
+template <int kEnc>
+__global__ void __launch_bounds__(kThreads) paged_decode_kernel(AttnParams p) {
+  __shared__ __align__(16) char smem[kDecodeSmem];
+  const int units_per_row = p.kvh * p.nslices * p.dec_max_chunks;
+  const int u = blockIdx.x;
+  const int b = u / units_per_row;
+  const int rem = u - b * units_per_row;
+  const int chunk = rem / (p.kvh * p.nslices);
+  const int kvs = rem - chunk * (p.kvh * p.nslices);
+  decode_unit<kEnc>(p, smem, b, kvs, chunk);
+}
+
+// Locate prefill unit u: chunk i, query tile, kv slice, split (query tile
+// fastest so that units sharing K/V are adjacent).
+__device__ __forceinline__ bool find_prefill_unit(const AttnParams& p, int u, int& i, int& qt,
+                                                  int& kvs, int& split) {
+  const int qtile_tokens = kWaves * kPreNCB * p.tpb;
+  const int kvslices = p.kvh * p.nslices;
+  for (i = 0; i < p.n_pre; ++i) {
+    const int sq = p.cu_q[i + 1] - p.cu_q[i];
+    const int sk = p.cu_k[i + 1] - p.cu_k[i];
+    if (sq <= 0 || sk <= 0) continue;
+    const int ntq = (sq + qtile_tokens - 1) / qtile_tokens;
+    const int ns = max(1, (sk + p.split_tokens - 1) / p.split_tokens);
+    const int units = ntq * kvslices * ns;
+    if (u < units) {
+      qt = u % ntq;
+      const int r = u / ntq;
+      kvs = r % kvslices;
+      split = r / kvslices;
+      return true;
+    }
+    u -= units;
+  }
+  return false;
+}
+
+template <int kEnc, bool kFresh>
+__global__ void __launch_bounds__(kThreads) varlen_kernel(AttnParams p) {
+  __shared__ __align__(16) char smem[kSmemBytes];
+  const int u = blockIdx.x;
+  if (u < p.dec_units) {
+    if constexpr (!kFresh) {
+      const int units_per_row = p.kvh * p.nslices * p.dec_max_chunks;
+      const int b = u / units_per_row;
+      const int rem = u - b * units_per_row;
+      const int chunk = rem / (p.kvh * p.nslices);
+      const int kvs = rem - chunk * (p.kvh * p.nslices);
+      decode_unit<kEnc>(p, smem, b, kvs, chunk);
+    }
+    return;
+  }
+  int i, qt, kvs, split;
+  if (!find_prefill_unit(p, u - p.dec_units, i, qt, kvs, split)) return;
+  prefill_unit<kEnc, kFresh>(p, smem, i, qt, kvs, split);
+}
+
+// Split-K merge: one workgroup per query row, thread -> (head, 4 dims).
+__global__ void __launch_bounds__(kThreads) merge_kernel(AttnParams p, int num_rows) {
+  const int64_t row = blockIdx.x;
+  if (row >= num_rows) return;
+  int nsplit;
+  if (row < p.n_dec) {
+    const int ctx = p.ctx_lens[row];
+    nsplit = ctx > 0 ? (ctx + p.chunk_tokens - 1) / p.chunk_tokens : 1;
+  } else {
+    // Prefill row -> its chunk (cu_q is prefill-relative).
+    const int r = int(row - p.n_dec);
+    int i = 0;
+    while (i + 1 < p.n_pre && p.cu_q[i + 1] <= r) ++i;
+    const int sk = p.cu_k[i + 1] - p.cu_k[i];
+    nsplit = max(1, (sk + p.split_tokens - 1) / p.split_tokens);
+  }
+  if (nsplit <= 1) return;
+  const int per_head = kD / 4;
+  for (int e = threadIdx.x; e < p.num_heads * per_head; e += kThreads) {
+    const int head = e / per_head;
+    const int d0 = (e - head * per_head) * 4;
+    const int64_t base = (row * p.num_heads + head) * p.max_splits;
+    float m = -INFINITY;
+    for (int sp = 0; sp < nsplit; ++sp) m = fmaxf(m, p.part_lse[base + sp]);
+    const float m_use = (m == -INFINITY) ? 0.f : m;
+    float l = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int sp = 0; sp < nsplit; ++sp) {
+      const float w = __builtin_amdgcn_exp2f(p.part_lse[base + sp] - m_use);
+      l += w;
+      const float4 o = *reinterpret_cast<const float4*>(p.part_o + (base + sp) * kD + d0);
+      acc.x += w * o.x;
+      acc.y += w * o.y;
+      acc.z += w * o.z;
+      acc.w += w * o.w;
+    }
+    const float inv = 1.f / l;
+    uint16_t* dst = p.out + row * p.o_st + int64_t(head) * p.o_sh + d0;
+    *reinterpret_cast<u32x2_t*>(dst) =
+        u32x2_t{pack_bf16x2(acc.x * inv, acc.y * inv), pack_bf16x2(acc.z * inv, acc.w * inv)};
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host-side launch planning.
+// ---------------------------------------------------------------------------
+int env_int(const char* name, int fallback) {
+  const char* v = getenv(name);
+  if (v == nullptr || *v == '\0') return fallback;
+  return atoi(v);
+}
+
+// Keys per decode chunk: the largest power of two in [128, 4096] that still
+// gives at least ~4 workgroups per CU (1024) for this batch; KVC_DECODE_CHUNK
+// overrides it (multiple of 128).
+int plan_decode_chunk(int64_t rows, int64_t kvslices, int64_t max_ctx) {
+  const int forced = env_int("KVC_DECODE_CHUNK", 0);
+  if (forced > 0) return forced;
+  int ch = 4096;
+  while (ch > 128 && rows * kvslices * ((max_ctx + ch - 1) / ch) < 1024) ch >>= 1;
+  return ch;
+}
+
+// Keys per prefill split: a quarter of the longest key range, at least 512.
+int plan_prefill_split(int64_t max_seqlen_k) {
+  const int forced = env_int("KVC_PREFILL_SPLIT", 0);
+  if (forced > 0) return forced;
+  int64_t ks = (max_seqlen_k + 3) / 4;
+  ks = ((ks + kTile - 1) / kTile) * kTile;
+  return int(ks < 512 ? 512 : ks);
+}
+
+struct HeadPlan {
+  int group, hs, nslices, tpb;
+};
+
+HeadPlan plan_heads(int64_t num_heads, int64_t kvh) {
+  HeadPlan h;
+  h.group = int(num_heads / kvh);
+  h.hs = h.group < 16 ? h.group : 16;
+  h.nslices = (h.group + h.hs - 1) / h.hs;
+  h.tpb = 16 / h.hs;
+  return h;
+}
+
+size_t partial_bytes(int64_t rows, int64_t heads, int64_t splits) {
+  if (splits <= 1) return 0;
+  return size_t(rows) * size_t(heads) * size_t(splits) * (kD + 1) * sizeof(float) + 256;
+}
+
+void set_partials(AttnParams& p, void* ws, int64_t rows) {
+  if (p.max_splits <= 1 || ws == nullptr) {
+    p.part_o = nullptr;
+    p.part_lse = nullptr;
+    return;
+  }
+  p.part_o = static_cast<float*>(ws);
+  p.part_lse = p.part_o + size_t(rows) * p.num_heads * p.max_splits * kD;
+}
+
+int check_kv_args(int kv_dtype, const float* k_scale, const float* v_scale, const void* side_k,
+                  const void* side_v, const int32_t* out_idx2d, const int32_t* head_n_out,
+                  int64_t n_out_max, const char* what) {
+  KVC_REQUIRE(kv_dtype == KVC_KV_BF16 || kv_dtype == KVC_KV_INT8_TOKHEAD ||
+                  kv_dtype == KVC_KV_INT8_CHAN,
+              KVC_ERR_VALUE, "%s: unknown kv_dtype %d", what, kv_dtype);
+  if (kv_dtype != KVC_KV_BF16) {
+    KVC_REQUIRE(k_scale != nullptr && v_scale != nullptr, KVC_ERR_VALUE,
+                "%s: int8 KV needs k_scale and v_scale", what);
+  }
+  if (kv_dtype == KVC_KV_INT8_CHAN && head_n_out != nullptr) {
+    KVC_REQUIRE(side_k != nullptr && side_v != nullptr && out_idx2d != nullptr, KVC_ERR_VALUE,
+                "%s: outlier dims need side pools and out_idx2d", what);
+    KVC_REQUIRE(n_out_max >= 1 && n_out_max <= kSideMax, KVC_ERR_VALUE,
+                "%s: n_out_max must be in [1, %d] (got %lld)", what, kSideMax,
+                (long long)n_out_max);
+  }
+  return KVC_OK;
+}
+
+void fill_kv(AttnParams& p, const void* k_cache, const void* v_cache, int64_t page, int64_t kvh,
+             int kv_dtype, const float* k_scale, const float* v_scale, const void* side_k,
+             const void* side_v, const int32_t* out_idx2d, const int32_t* head_n_out,
+             int64_t n_out_max) {
+  p.k_cache = static_cast<const char*>(k_cache);
+  p.v_cache = static_cast<const char*>(v_cache);
+  p.page = int(page);
+  p.kvh = int(kvh);
+  p.tok_bytes = kvh * kD * (kv_dtype == KVC_KV_BF16 ? 2 : 1);
+  p.k_scale = k_scale;
+  p.v_scale = v_scale;
+  const bool side = kv_dtype == KVC_KV_INT8_CHAN && head_n_out != nullptr;
+  p.side_k = side ? static_cast<const uint16_t*>(side_k) : nullptr;
+  p.side_v = side ? static_cast<const uint16_t*>(side_v) : nullptr;
+  p.out_idx = side ? out_idx2d : nullptr;
+  p.head_n_out = side ? head_n_out : nullptr;
+  p.n_out_max = side ? int(n_out_max) : 0;
+}
+
+template <int kEnc>
+void launch_decode_enc(const AttnParams& p, int grid, hipStream_t st) {
+  paged_decode_kernel<kEnc><<<grid, kThreads, 0, st>>>(p);
+}
+
+template <int kEnc>
+void launch_varlen_enc(const AttnParams& p, int grid, bool fresh, hipStream_t st) {
+  if (fresh) {
+    if constexpr (kEnc == kBF16) varlen_kernel<kBF16, true><<<grid, kThreads, 0, st>>>(p);
+  } else {
+    varlen_kernel<kEnc, false><<<grid, kThreads, 0, st>>>(p);
+  }
+}
+
+}  // namespace
+}  // namespace kvc
+
+using namespace kvc;
+
+extern "C" size_t kvc_paged_decode_workspace_bytes(int64_t batch, int64_t num_heads,
+                                                   int64_t num_kv_heads, int64_t head_dim,
+                                                   int64_t page_size,
+                                                   int64_t max_blocks_per_seq) {
+  if (batch <= 0 || num_kv_heads <= 0 || head_dim != kD) return 0;
+  const HeadPlan hp = plan_heads(num_heads, num_kv_heads);
+  const int64_t max_ctx = max_blocks_per_seq * page_size;
+  const int ch = plan_decode_chunk(batch, num_kv_heads * hp.nslices, max_ctx);
+  const int64_t splits = max_ctx > 0 ? (max_ctx + ch - 1) / ch : 1;
+  return partial_bytes(batch, num_heads, splits);
+}
+
+extern "C" int kvc_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                const void* k_cache, const void* v_cache,
+                                int64_t num_cache_blocks, int64_t page_size, int64_t num_kv_heads,
+                                int64_t head_dim, int kv_dtype, const float* k_scale,
+                                const float* v_scale, const void* side_k, const void* side_v,
+                                const int32_t* out_idx2d, const int32_t* head_n_out,
+                                int64_t n_out_max, const int32_t* block_tables, int64_t bt_stride,
+                                int64_t max_blocks_per_seq, const int32_t* context_lens,
+                                int64_t batch, int64_t num_heads, float scale, void* out,
+                                int64_t out_stride_b, int64_t out_stride_h, void* workspace,
+                                size_t workspace_bytes, kvc_stream_t stream) {
+  clear_error();
+  KVC_REQUIRE(head_dim == kD, KVC_ERR_VALUE, "paged_decode: head_dim must be 128 (got %lld)",
+              (long long)head_dim);
+  KVC_REQUIRE(page_size > 0 && page_size % kTile == 0, KVC_ERR_VALUE,
+              "paged_decode: page_size must be a positive multiple of 32 (got %lld)",
+              (long long)page_size);
+  KVC_REQUIRE(num_kv_heads > 0 && num_heads > 0 && num_heads % num_kv_heads == 0, KVC_ERR_VALUE,
+              "paged_decode: num_heads (%lld) must be a multiple of num_kv_heads (%lld)",
+              (long long)num_heads, (long long)num_kv_heads);
+  KVC_REQUIRE(num_cache_blocks >= 0, KVC_ERR_VALUE, "paged_decode: bad num_cache_blocks");
+  int rc = check_kv_args(kv_dtype, k_scale, v_scale, side_k, side_v, out_idx2d, head_n_out,
+                         n_out_max, "paged_decode");
+  if (rc != KVC_OK) return rc;
+  KVC_REQUIRE((q_stride_b % 8) == 0 && (q_stride_h % 8) == 0 && (out_stride_b % 8) == 0 &&
+                  (out_stride_h % 8) == 0 && (reinterpret_cast<uintptr_t>(q) % 16) == 0 &&
+                  (reinterpret_cast<uintptr_t>(out) % 16) == 0,
+              KVC_ERR_ASSERT, "paged_decode: q/out rows must be 16-byte aligned");
+  if (batch == 0) return KVC_OK;
+  KVC_REQUIRE(max_blocks_per_seq > 0, KVC_ERR_VALUE, "paged_decode: empty block_tables");
+
+  const HeadPlan hp = plan_heads(num_heads, num_kv_heads);
+  AttnParams p{};
+  p.q = static_cast<const uint16_t*>(q);
+  p.q_st = q_stride_b;
+  p.q_sh = q_stride_h;
+  p.out = static_cast<uint16_t*>(out);
+  p.o_st = out_stride_b;
+  p.o_sh = out_stride_h;
+  p.num_heads = int(num_heads);
+  p.group = hp.group;
+  p.hs = hp.hs;
+  p.nslices = hp.nslices;
+  p.tpb = hp.tpb;
+  p.scale_log2 = scale * kLog2e;
+  fill_kv(p, k_cache, v_cache, page_size, num_kv_heads, kv_dtype, k_scale, v_scale, side_k, side_v,
+          out_idx2d, head_n_out, n_out_max);
+  p.block_tables = block_tables;
+  p.bt_stride = bt_stride;
+  p.n_dec = int(batch);
+  p.ctx_lens = context_lens;
+  const int64_t max_ctx = max_blocks_per_seq * page_size;
+  p.chunk_tokens = plan_decode_chunk(batch, num_kv_heads * hp.nslices, max_ctx);
+  KVC_REQUIRE(p.chunk_tokens % kTile == 0, KVC_ERR_VALUE,
+              "paged_decode: decode chunk must be a multiple of 32");
+  p.dec_max_chunks = int((max_ctx + p.chunk_tokens - 1) / p.chunk_tokens);
+  p.max_splits = p.dec_max_chunks;
+  const size_t need = partial_bytes(batch, num_heads, p.max_splits);
+  KVC_REQUIRE(need == 0 || (workspace != nullptr && workspace_bytes >= need), KVC_ERR_WORKSPACE,
+              "paged_decode: workspace of %zu bytes needed (got %zu)", need, workspace_bytes);
+  set_partials(p, workspace, batch);
+  const int64_t units = batch * num_kv_heads * hp.nslices * p.dec_max_chunks;
+  KVC_REQUIRE(units < (int64_t(1) << 31), KVC_ERR_VALUE, "paged_decode: launch too large");
+  p.dec_units = int(units);
+  hipStream_t st = as_stream(stream);
+  switch (kv_dtype) {
+    case KVC_KV_BF16: launch_decode_enc<kBF16>(p, int(units), st); break;
+    case KVC_KV_INT8_TOKHEAD: launch_decode_enc<kI8Tok>(p, int(units), st); break;
+    default: launch_decode_enc<kI8Chan>(p, int(units), st); break;
+  }
+  rc = check_launch("paged_decode");
+  if (rc != KVC_OK) return rc;
+  if (p.max_splits > 1) {
+    merge_kernel<<<unsigned(batch), kThreads, 0, st>>>(p, int(batch));
+    rc = check_launch("paged_decode merge");
+  }
+  return rc;
+}
+
+extern "C" size_t kvc_varlen_workspace_bytes(int64_t num_q_tokens, int64_t num_heads,
+                                             int64_t num_kv_heads, int64_t head_dim,
+                                             int64_t num_decode_rows, int64_t max_seqlen_k,
+                                             int64_t page_size, int64_t max_blocks_per_seq) {
+  if (num_q_tokens <= 0 || num_kv_heads <= 0 || head_dim != kD) return 0;
+  const HeadPlan hp = plan_heads(num_heads, num_kv_heads);
+  int64_t splits = 1;
+  if (num_decode_rows > 0) {
+    const int64_t max_ctx = max_blocks_per_seq * page_size;
+    const int ch = plan_decode_chunk(num_decode_rows, num_kv_heads * hp.nslices, max_ctx);
+    splits = max_ctx > 0 ? (max_ctx + ch - 1) / ch : 1;
+  }
+  if (max_seqlen_k > 0) {
+    const int ks = plan_prefill_split(max_seqlen_k);
+    const int64_t ps = (max_seqlen_k + ks - 1) / ks;
+    splits = ps > splits ? ps : splits;
+  }
+  return partial_bytes(num_q_tokens, num_heads, splits);
+}
+
+extern "C" int kvc_varlen_attention(
+    const void* q, int64_t q_stride_t, int64_t q_stride_h, int64_t num_q_tokens,
+    int64_t num_heads, const void* k_cache, const void* v_cache, int64_t num_cache_blocks,
+    int64_t page_size, int64_t num_kv_heads, int64_t head_dim, int kv_dtype,
+    const float* k_scale, const float* v_scale, const void* side_k, const void* side_v,
+    const int32_t* out_idx2d, const int32_t* head_n_out, int64_t n_out_max, const void* k_fresh,
+    int64_t kf_stride_t, int64_t kf_stride_h, const void* v_fresh, int64_t vf_stride_t,
+    int64_t vf_stride_h, const int32_t* block_tables, int64_t bt_stride,
+    int64_t max_blocks_per_seq, int64_t num_decode_rows, const int32_t* decode_context_lens,
+    int64_t num_prefill, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+    int64_t num_prefill_units, int64_t max_seqlen_k, float scale, void* out,
+    int64_t out_stride_t, int64_t out_stride_h, void* workspace, size_t workspace_bytes,
+    kvc_stream_t stream) {
+  clear_error();
+  KVC_REQUIRE(head_dim == kD, KVC_ERR_VALUE, "varlen_attention: head_dim must be 128 (got %lld)",
+              (long long)head_dim);
+  KVC_REQUIRE(num_kv_heads > 0 && num_heads > 0 && num_heads % num_kv_heads == 0, KVC_ERR_VALUE,
+              "varlen_attention: num_heads must be a multiple of num_kv_heads");
+  const bool fresh = block_tables == nullptr;
+  if (!fresh) {
+    KVC_REQUIRE(page_size > 0 && page_size % kTile == 0, KVC_ERR_VALUE,
+                "varlen_attention: page_size must be a positive multiple of 32");
+    KVC_REQUIRE(max_blocks_per_seq > 0, KVC_ERR_VALUE, "varlen_attention: empty block_tables");
+  } else {
+    KVC_REQUIRE(num_decode_rows == 0, KVC_ERR_VALUE,
+                "varlen_attention: decode rows need block_tables");
+    KVC_REQUIRE(k_fresh != nullptr && v_fresh != nullptr, KVC_ERR_VALUE,
+                "varlen_attention: without block_tables keys come from k_fresh/v_fresh");
+    KVC_REQUIRE((kf_stride_t % 8) == 0 && (kf_stride_h % 8) == 0 && (vf_stride_t % 8) == 0 &&
+                    (vf_stride_h % 8) == 0 && (reinterpret_cast<uintptr_t>(k_fresh) % 16) == 0 &&
+                    (reinterpret_cast<uintptr_t>(v_fresh) % 16) == 0,
+                KVC_ERR_ASSERT, "varlen_attention: k/v rows must be 16-byte aligned");
+  }
+  int rc = check_kv_args(fresh ? KVC_KV_BF16 : kv_dtype, k_scale, v_scale, side_k, side_v,
+                         out_idx2d, head_n_out, n_out_max, "varlen_attention");
+  if (rc != KVC_OK) return rc;
+  KVC_REQUIRE((q_stride_t % 8) == 0 && (q_stride_h % 8) == 0 && (out_stride_t % 8) == 0 &&
+                  (out_stride_h % 8) == 0 && (reinterpret_cast<uintptr_t>(q) % 16) == 0 &&
+                  (reinterpret_cast<uintptr_t>(out) % 16) == 0,
+              KVC_ERR_ASSERT, "varlen_attention: q/out rows must be 16-byte aligned");
+  KVC_REQUIRE(num_prefill == 0 || (cu_seqlens_q != nullptr && cu_seqlens_k != nullptr),
+              KVC_ERR_VALUE, "varlen_attention: prefill chunks need cu_seqlens_q/k");
+  (void)num_cache_blocks;
+  if (num_q_tokens == 0) return KVC_OK;
+
+  const HeadPlan hp = plan_heads(num_heads, num_kv_heads);
+  AttnParams p{};
+  p.q = static_cast<const uint16_t*>(q);
+  p.q_st = q_stride_t;
+  p.q_sh = q_stride_h;
+  p.out = static_cast<uint16_t*>(out);
+  p.o_st = out_stride_t;
+  p.o_sh = out_stride_h;
+  p.num_heads = int(num_heads);
+  p.group = hp.group;
+  p.hs = hp.hs;
+  p.nslices = hp.nslices;
+  p.tpb = hp.tpb;
+  p.scale_log2 = scale * kLog2e;
+  fill_kv(p, k_cache, v_cache, page_size, num_kv_heads, fresh ? KVC_KV_BF16 : kv_dtype, k_scale,
+          v_scale, side_k, side_v, out_idx2d, head_n_out, n_out_max);
+  p.block_tables = block_tables;
+  p.bt_stride = bt_stride;
+  p.n_dec = int(num_decode_rows);
+  p.ctx_lens = decode_context_lens;
+  int64_t max_splits = 1;
+  p.chunk_tokens = kTile;
+  p.dec_max_chunks = 0;
+  if (num_decode_rows > 0) {
+    KVC_REQUIRE(decode_context_lens != nullptr, KVC_ERR_VALUE,
+                "varlen_attention: decode rows need decode_context_lens");
+    const int64_t max_ctx = max_blocks_per_seq * page_size;
+    p.chunk_tokens = plan_decode_chunk(num_decode_rows, num_kv_heads * hp.nslices, max_ctx);
+    p.dec_max_chunks = int((max_ctx + p.chunk_tokens - 1) / p.chunk_tokens);
+    max_splits = p.dec_max_chunks;
+  }
+  p.n_pre = int(num_prefill);
+  p.cu_q = cu_seqlens_q;
+  p.cu_k = cu_seqlens_k;
+  p.split_tokens = plan_prefill_split(max_seqlen_k);
+  if (max_seqlen_k > 0) {
+    const int64_t ps = (max_seqlen_k + p.split_tokens - 1) / p.split_tokens;
+    max_splits = ps > max_splits ? ps : max_splits;
+  }
+  p.kf = static_cast<const uint16_t*>(k_fresh);
+  p.kf_st = kf_stride_t;
+  p.kf_sh = kf_stride_h;
+  p.vf = static_cast<const uint16_t*>(v_fresh);
+  p.vf_st = vf_stride_t;
+  p.vf_sh = vf_stride_h;
+  p.max_splits = int(max_splits);
+  const size_t need = partial_bytes(num_q_tokens, num_heads, max_splits);
+  KVC_REQUIRE(need == 0 || (workspace != nullptr && workspace_bytes >= need), KVC_ERR_WORKSPACE,
+              "varlen_attention: workspace of %zu bytes needed (got %zu)", need,
+              workspace_bytes);
+  set_partials(p, workspace, num_q_tokens);
+  const int64_t dec_units = num_decode_rows * num_kv_heads * hp.nslices * p.dec_max_chunks;
+  KVC_REQUIRE(dec_units + num_prefill_units < (int64_t(1) << 31) && num_prefill_units >= 0,
+              KVC_ERR_VALUE, "varlen_attention: launch too large");
+  p.dec_units = int(dec_units);
+  p.pre_units = int(num_prefill_units);
+  const int grid = int(dec_units + num_prefill_units);
+  hipStream_t st = as_stream(stream);
+  if (grid > 0) {
+    switch (fresh ? KVC_KV_BF16 : kv_dtype) {
+      case KVC_KV_BF16: launch_varlen_enc<kBF16>(p, grid, fresh, st); break;
+      case KVC_KV_INT8_TOKHEAD: launch_varlen_enc<kI8Tok>(p, grid, false, st); break;
+      default: launch_varlen_enc<kI8Chan>(p, grid, false, st); break;
+    }
+    rc = check_launch("varlen_attention");
+    if (rc != KVC_OK) return rc;
+  }
+  if (p.max_splits > 1) {
+    merge_kernel<<<unsigned(num_q_tokens), kThreads, 0, st>>>(p, int(num_q_tokens));
+    rc = check_launch("varlen_attention merge");
+  }
+  return rc;
+}
+
+// Number of prefill workgroups for the given chunk lengths (host arrays of
+// num_prefill + 1 cumulative offsets), matching the kernel's unit order.
+extern "C" int64_t kvc_varlen_prefill_units(const int32_t* cu_q_host, const int32_t* cu_k_host,
+                                            int64_t num_prefill, int64_t num_heads,
+                                            int64_t num_kv_heads, int64_t max_seqlen_k) {
+  if (num_prefill <= 0 || num_kv_heads <= 0) return 0;
+  const HeadPlan hp = plan_heads(num_heads, num_kv_heads);
+  const int ks = plan_prefill_split(max_seqlen_k);
+  const int qtile_tokens = kWaves * kPreNCB * hp.tpb;
+  int64_t units = 0;
+  for (int64_t i = 0; i < num_prefill; ++i) {
+    const int64_t sq = cu_q_host[i + 1] - cu_q_host[i];
+    const int64_t sk = cu_k_host[i + 1] - cu_k_host[i];
+    if (sq <= 0 || sk <= 0) continue;
+    const int64_t ntq = (sq + qtile_tokens - 1) / qtile_tokens;
+    const int64_t ns = (sk + ks - 1) / ks;
+    units += ntq * num_kv_heads * hp.nslices * (ns < 1 ? 1 : ns);
+  }
+  return units;
+}

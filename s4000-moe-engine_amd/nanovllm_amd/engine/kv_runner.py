@@ -1,0 +1,240 @@
+"""KV pool allocation and whole-block byte movement (the runner's KV slices).
+
+Mirrors the parts of nanovllm/engine/model_runner.py that own the KV pool:
+  allocate_kv_cache   :400-508   pool [2, L, blocks + 1, page, KVH, D] (the
+                                  extra block is the graph-padding scratch
+                                  block), per-layer views handed to every
+                                  module with k_cache/v_cache
+  offload_put/get/release :284-308  byte moves behind the BlockManager's
+                                  executor protocol call(name, *args)
+and adds the batched forms a swap/compaction step needs (one launch or one
+DMA submission for a whole id list).
+
+Differences from the reference, all on the byte path:
+  * no device-wide synchronize() before a snapshot (model_runner.py:294):
+    every move is ordered on the current stream after the kernels that wrote
+    the block, and before any later kernel that overwrites it;
+  * the block is copied straight from the pool into the pinned slot by the
+    copy engines (one strided 2-D copy per block), without the index_select
+    staging tensor.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from .. import _native as nat
+
+
+class BlockMover:
+    """Whole-block moves on a pool shaped [P0, P1, blocks, ...] (block axis 2),
+    i.e. the engine's [2, L, blocks, page, KVH, D] KV pool or its int8 scale /
+    side-pool companions.  A block is P0*P1 planes of block_bytes."""
+
+    def __init__(self, pool: torch.Tensor):
+        if pool.dim() < 3:
+            raise ValueError("pool must be [P0, P1, blocks, ...]")
+        if not pool.is_contiguous():
+            raise AssertionError("the KV pool must be contiguous")
+        nat.require_device(pool)
+        self.pool = pool
+        self.planes = pool.size(0) * pool.size(1)
+        self.num_blocks = pool.size(2)
+        self.item_shape = tuple(pool.shape[:2]) + tuple(pool.shape[3:])
+        self.block_bytes = pool[0, 0, 0].numel() * pool.element_size()
+        self.plane_stride = self.num_blocks * self.block_bytes
+        self.item_bytes = self.planes * self.block_bytes
+
+    # -- helpers ---------------------------------------------------------
+    def _dev_ids(self, ids) -> torch.Tensor:
+        if isinstance(ids, torch.Tensor):
+            t = ids.to(device=self.pool.device, dtype=torch.int32)
+        else:
+            t = torch.as_tensor(list(ids), dtype=torch.int32).to(self.pool.device, non_blocking=True)
+        return t.contiguous()
+
+    def _host_ids(self, ids) -> np.ndarray:
+        if isinstance(ids, torch.Tensor):
+            ids = ids.tolist()
+        arr = np.ascontiguousarray(np.asarray(list(ids), dtype=np.int64))
+        if arr.size and (arr.min() < 0 or arr.max() >= self.num_blocks):
+            raise IndexError(f"block id out of range [0, {self.num_blocks})")
+        return arr
+
+    def _check_items(self, t: torch.Tensor, n: int) -> None:
+        if tuple(t.shape) != (n,) + self.item_shape or t.dtype != self.pool.dtype:
+            raise ValueError(f"expected [{n}, {self.item_shape}] {self.pool.dtype}, got "
+                             f"{tuple(t.shape)} {t.dtype}")
+        if not t.is_contiguous():
+            raise AssertionError("staging buffer must be contiguous")
+
+    def _stream(self) -> int:
+        return nat.stream_of(self.pool)
+
+    # -- kernels ---------------------------------------------------------
+    def gather(self, ids, out: torch.Tensor | None = None) -> torch.Tensor:
+        """out[i] = pool[:, :, ids[i]] (out on the device or pinned host)."""
+        n = len(ids)
+        if out is None:
+            out = torch.empty((n,) + self.item_shape, dtype=self.pool.dtype,
+                              device=self.pool.device)
+        self._check_items(out, n)
+        if n == 0:
+            return out
+        dev_ids = self._dev_ids(ids)
+        nat.call("kvc_block_gather", self.pool.data_ptr(), self.planes, self.plane_stride,
+                 self.block_bytes, dev_ids.data_ptr(), n, out.data_ptr(), self.item_bytes,
+                 self.block_bytes, self._stream())
+        return out
+
+    def scatter(self, items: torch.Tensor, ids) -> None:
+        """pool[:, :, ids[i]] = items[i] (items on the device or pinned host)."""
+        n = len(ids)
+        self._check_items(items, n)
+        if n == 0:
+            return
+        dev_ids = self._dev_ids(ids)
+        nat.call("kvc_block_scatter", items.data_ptr(), self.item_bytes, self.block_bytes,
+                 self.planes, self.block_bytes, dev_ids.data_ptr(), n, self.pool.data_ptr(),
+                 self.plane_stride, self._stream())
+
+    def copy(self, src_ids, dst_ids) -> None:
+        """pool[:, :, dst] = pool[:, :, src] as one simultaneous copy; id lists
+        that overlap go through a device staging buffer."""
+        src = [int(x) for x in (src_ids.tolist() if isinstance(src_ids, torch.Tensor) else src_ids)]
+        dst = [int(x) for x in (dst_ids.tolist() if isinstance(dst_ids, torch.Tensor) else dst_ids)]
+        if len(src) != len(dst):
+            raise ValueError("src_ids and dst_ids differ in length")
+        if not src:
+            return
+        if len(set(dst)) != len(dst):
+            raise ValueError("duplicate destination block")
+        if set(src) & set(dst):
+            staged = self.gather(src)
+            self.scatter(staged, dst)
+            return
+        s, d = self._dev_ids(src), self._dev_ids(dst)
+        nat.call("kvc_block_copy", self.pool.data_ptr(), self.planes, self.plane_stride,
+                 self.block_bytes, s.data_ptr(), d.data_ptr(), len(src), self._stream())
+
+    # -- copy engines ----------------------------------------------------
+    def d2h(self, ids, host: torch.Tensor) -> None:
+        """host[i] = pool[:, :, ids[i]] by DMA (host must be pinned)."""
+        ids_np = self._host_ids(ids)
+        self._check_items(host, len(ids_np))
+        if not host.is_pinned():
+            raise ValueError("the host staging buffer must be pinned")
+        if len(ids_np) == 0:
+            return
+        nat.call("kvc_block_d2h", self.pool.data_ptr(), self.planes, self.plane_stride,
+                 self.block_bytes, ids_np.ctypes.data, len(ids_np), host.data_ptr(),
+                 self.item_bytes, self._stream())
+
+    def h2d(self, host: torch.Tensor, ids) -> None:
+        """pool[:, :, ids[i]] = host[i] by DMA (host must be pinned)."""
+        ids_np = self._host_ids(ids)
+        self._check_items(host, len(ids_np))
+        if not host.is_pinned():
+            raise ValueError("the host staging buffer must be pinned")
+        if len(ids_np) == 0:
+            return
+        nat.call("kvc_block_h2d", host.data_ptr(), self.item_bytes, self.planes,
+                 self.block_bytes, ids_np.ctypes.data, len(ids_np), self.pool.data_ptr(),
+                 self.plane_stride, self._stream())
+
+
+class KVCacheRunner:
+    """The runner's KV duties for one rank: the pool, its per-layer views, and
+    the offload executor protocol the BlockManager drives through call()."""
+
+    def __init__(self, num_layers: int, num_blocks: int, block_size: int, num_kv_heads: int,
+                 head_dim: int, dtype=torch.bfloat16, device="cuda", kv_int8: str | None = None,
+                 kv_offload_host_blocks: int = 0, n_out_max: int = 8):
+        self.block_size = block_size
+        self.num_layers = num_layers
+        self.num_kvcache_blocks = num_blocks
+        self.kv_int8 = kv_int8
+        # one extra block the BlockManager never sees (graph-padding scratch)
+        shape = (2, num_layers, num_blocks + 1, block_size, num_kv_heads, head_dim)
+        self.kv_cache = torch.empty(shape, dtype=torch.int8 if kv_int8 else dtype, device=device)
+        self.kv_scales = self.kv_dscales = self.kv_side = None
+        self.kv_out_idx2d = self.kv_head_n_out = None
+        if kv_int8 == "tokhead":
+            self.kv_scales = torch.ones(shape[:5], dtype=torch.float32, device=device)
+        elif kv_int8 == "chan":
+            self.kv_scales = torch.ones(2, num_layers, num_kv_heads, head_dim,
+                                        dtype=torch.float32, device=device)
+            self.kv_dscales = torch.ones_like(self.kv_scales)
+            self.kv_side = torch.zeros(2, num_layers, num_blocks + 1, block_size, num_kv_heads,
+                                       n_out_max, dtype=torch.bfloat16, device=device)
+            self.kv_out_idx2d = torch.zeros(num_layers, num_kv_heads, n_out_max,
+                                            dtype=torch.int32, device=device)
+            self.kv_head_n_out = torch.zeros(num_layers, num_kv_heads, dtype=torch.int32,
+                                             device=device)
+        elif kv_int8 is not None:
+            raise ValueError(f"kv_int8 must be None, 'tokhead' or 'chan' (got {kv_int8!r})")
+        self.scratch_block_id = num_blocks
+        self.scratch_slot = num_blocks * block_size
+        self.mover = BlockMover(self.kv_cache)
+        self.kv_offload_host_blocks = kv_offload_host_blocks
+        self.kv_offloader = None
+
+    def bind(self, modules) -> int:
+        """Hand per-layer views to every module that has k_cache/v_cache
+        (model_runner.py:494-508); returns the number of layers bound."""
+        layer = 0
+        for m in modules:
+            if not (hasattr(m, "k_cache") and hasattr(m, "v_cache")):
+                continue
+            m.k_cache = self.kv_cache[0, layer]
+            m.v_cache = self.kv_cache[1, layer]
+            if self.kv_int8 == "tokhead":
+                m.k_scale = self.kv_scales[0, layer]
+                m.v_scale = self.kv_scales[1, layer]
+            elif self.kv_int8 == "chan":
+                m.k_scale = self.kv_scales[0, layer]
+                m.v_scale = self.kv_scales[1, layer]
+                m.k_dscale = self.kv_dscales[0, layer]
+                m.v_dscale = self.kv_dscales[1, layer]
+                m.side_k = self.kv_side[0, layer]
+                m.side_v = self.kv_side[1, layer]
+                m.out_idx2d = self.kv_out_idx2d[layer]
+                m.head_n_out = self.kv_head_n_out[layer]
+            m.kv_cache_is_int8 = self.kv_int8 is not None
+            layer += 1
+        return layer
+
+    # -- executor protocol (BlockManager -> runner) ------------------------
+    def call(self, method: str, *args):
+        return getattr(self, method)(*args)
+
+    def _ensure_offloader(self):
+        from .kv_offload import HostBlockPool
+        if self.kv_offloader is None:
+            self.kv_offloader = HostBlockPool(self.kv_offload_host_blocks,
+                                              tuple(self.kv_cache[:, :, 0].shape),
+                                              dtype=self.kv_cache.dtype)
+        return self.kv_offloader
+
+    def offload_put(self, block_id: int) -> int:
+        pool = self._ensure_offloader()
+        if not pool.has_room():
+            return pool.note_full()
+        return pool.put_from_pool(self.mover, block_id)
+
+    def offload_get(self, slot: int, block_id: int) -> None:
+        self._ensure_offloader().get_into_pool(self.mover, slot, block_id)
+
+    def offload_release(self, slot: int) -> None:
+        self._ensure_offloader().release(slot)
+
+    # -- batched forms ---------------------------------------------------
+    def offload_put_many(self, block_ids) -> list[int]:
+        pool = self._ensure_offloader()
+        return pool.put_many_from_pool(self.mover, block_ids)
+
+    def offload_get_many(self, slots, block_ids) -> None:
+        self._ensure_offloader().get_many_into_pool(self.mover, slots, block_ids)
+
+    def compact(self, src_ids, dst_ids) -> None:
+        self.mover.copy(src_ids, dst_ids)

@@ -1,0 +1,101 @@
+"""Paged GQA decode attention on MI355X (libkvc `kvc_paged_decode`).
+
+Drop-in for nanovllm/kernels/paged_attention.py:193-245: same signature, same
+output allocation (torch.empty_like(q)), same ValueError conditions, and the
+same graph-capture contract (the loop bound is the device-side context_lens;
+max_context_len is accepted and ignored, paged_attention.py:212-214).
+
+Differences that only widen what is accepted:
+  * page sizes that are multiples of 32 (the reference insists on 256);
+  * int8 pools in either encoding: per-channel read scales [KVH, D] with the
+    bf16 outlier side pool (the engine's current layout), or per-token-head
+    scales [blocks, page, KVH] (k_scale.dim() == 3);
+  * the side pool is used without the reference's host sync on
+    int(head_n_out.max()) (paged_attention.py:218): the kernel reads
+    head_n_out on the device.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _native as nat
+
+
+def set_paged_config(value: str | None) -> None:
+    """Accepted for API compatibility (paged_attention.py:50); the HIP kernel
+    plans its own split-K launch from the batch shape."""
+    del value
+
+
+def _kv_encoding(k_cache: torch.Tensor, k_scale: torch.Tensor | None) -> int:
+    if k_cache.dtype == torch.int8:
+        if k_scale is None:
+            raise ValueError("an int8 KV pool needs k_scale/v_scale")
+        return nat.KVC_KV_INT8_TOKHEAD if k_scale.dim() == 3 else nat.KVC_KV_INT8_CHAN
+    if k_cache.dtype != torch.bfloat16:
+        raise ValueError(f"KV pool dtype {k_cache.dtype} is not supported (bf16 or int8)")
+    if k_scale is not None:
+        raise ValueError("k_scale given for a bf16 KV pool")
+    return nat.KVC_KV_BF16
+
+
+def paged_decode_attention(
+    q, k_cache, v_cache, block_tables, context_lens, scale, max_context_len,
+    k_scale=None, v_scale=None, side_k=None, side_v=None,
+    out_idx2d=None, head_n_out=None,
+):
+    if q.ndim != 3 or k_cache.ndim != 4 or v_cache.shape != k_cache.shape:
+        raise ValueError("expected q=[batch,heads,dim], kv=[pages,page,kv_heads,dim]")
+    batch, num_heads, head_dim = q.shape
+    page_size = k_cache.size(1)
+    num_kv_heads = k_cache.size(2)
+    if head_dim != 128 or page_size % 32 or num_heads % num_kv_heads:
+        raise ValueError(
+            "paged decode requires head_dim=128, page_size a multiple of 32 and "
+            "GQA-divisible heads")
+    if q.dtype != torch.bfloat16:
+        raise ValueError(f"q must be bf16 (got {q.dtype})")
+    nat.require_device(q, k_cache, v_cache, block_tables, context_lens)
+    enc = _kv_encoding(k_cache, k_scale)
+    if q.stride(2) != 1:
+        q = q.contiguous()
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise AssertionError("KV pools must be contiguous [pages, page, kv_heads, dim]")
+    if block_tables.dtype != torch.int32:
+        block_tables = block_tables.to(torch.int32)
+    if block_tables.stride(1) != 1:
+        block_tables = block_tables.contiguous()
+    if context_lens.dtype != torch.int32 or not context_lens.is_contiguous():
+        context_lens = context_lens.to(torch.int32).contiguous()
+    del max_context_len
+    output = torch.empty_like(q)
+    if output.stride(2) != 1:
+        output = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    if batch == 0:
+        return output
+    has_side = enc == nat.KVC_KV_INT8_CHAN and side_k is not None and head_n_out is not None
+    if enc == nat.KVC_KV_INT8_TOKHEAD:
+        k_scale = k_scale.contiguous()
+        v_scale = v_scale.contiguous()
+    elif enc == nat.KVC_KV_INT8_CHAN:
+        k_scale = k_scale.to(torch.float32).contiguous()
+        v_scale = v_scale.to(torch.float32).contiguous()
+    max_blocks = block_tables.size(1)
+    ws_bytes = nat.query("kvc_paged_decode_workspace_bytes", batch, num_heads, num_kv_heads,
+                         head_dim, page_size, max_blocks)
+    ws = nat.workspace(ws_bytes, q.device)
+    nat.call(
+        "kvc_paged_decode",
+        q.data_ptr(), q.stride(0), q.stride(1),
+        k_cache.data_ptr(), v_cache.data_ptr(), k_cache.size(0), page_size, num_kv_heads,
+        head_dim, enc,
+        nat.ptr(k_scale), nat.ptr(v_scale),
+        nat.ptr(side_k) if has_side else None, nat.ptr(side_v) if has_side else None,
+        nat.ptr(out_idx2d) if has_side else None, nat.ptr(head_n_out) if has_side else None,
+        side_k.size(-1) if has_side else 0,
+        block_tables.data_ptr(), block_tables.stride(0), max_blocks,
+        context_lens.data_ptr(), batch, num_heads, float(scale),
+        output.data_ptr(), output.stride(0), output.stride(1),
+        nat.ptr(ws), ws_bytes, nat.stream_of(q),
+    )
+    return output

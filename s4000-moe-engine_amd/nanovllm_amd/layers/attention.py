@@ -1,0 +1,142 @@
+"""Attention layer of the paged KV path, backed by libkvc.
+
+store_kvcache and Attention keep the signatures, attributes and tensor layouts
+of nanovllm/layers/attention.py:9-279, so the model (Qwen3Attention) and the
+runner (which assigns k_cache/v_cache and the int8 tensors per layer) do not
+change.  What changes is underneath:
+
+* append is one HIP launch for K and V (V read through its own strides, so the
+  strided V view of a fused qkv projection is not copied first);
+* decode is the split-K paged kernel regardless of `attention_backend` (the
+  reference's "sdpa" decode gathers and expands the whole padded table,
+  attention.py:239-279; both backends compute the same function);
+* prefill and mixed batches are ONE varlen launch instead of a Python loop
+  over sequences plus torch.cat (attention.py:146-166, :179-213).
+"""
+from __future__ import annotations
+
+from contextlib import nullcontext
+
+import torch
+from torch import nn
+
+from .. import _native as nat
+from ..kernels.kv_int8 import store_kvcache_int8
+from ..kernels.paged_attention import paged_decode_attention
+from ..kernels.varlen import varlen_attention
+from ..utils.context import get_context
+
+
+def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
+                  v_cache: torch.Tensor, slot_mapping: torch.Tensor):
+    """k_cache.view(-1, KVH*D)[slot_mapping] = key.reshape(N, KVH*D); same for V.
+
+    Same preconditions as attention.py:12-15.  A negative slot indexes from
+    the end like the reference's integer index_put; no host synchronisation,
+    so the call is graph-capturable."""
+    N, num_heads, head_dim = key.shape
+    D = num_heads * head_dim
+    assert key.stride(-1) == 1 and value.stride(-1) == 1
+    assert key.stride(1) == head_dim and value.stride(1) == head_dim
+    assert k_cache.stride(1) == D and v_cache.stride(1) == D
+    assert slot_mapping.numel() == N
+    assert key.dtype == value.dtype == k_cache.dtype == v_cache.dtype
+    assert k_cache.is_contiguous() and v_cache.is_contiguous()
+    nat.require_device(key, value, k_cache, v_cache, slot_mapping)
+    if slot_mapping.dtype == torch.int64:
+        sb = 8
+    else:
+        slot_mapping = slot_mapping.to(torch.int32)
+        sb = 4
+    slot_mapping = slot_mapping.contiguous()
+    num_slots = k_cache.numel() // D
+    nat.call("kvc_store_kv",
+             key.data_ptr(), key.stride(0), key.stride(1),
+             value.data_ptr(), value.stride(0), value.stride(1),
+             k_cache.data_ptr(), v_cache.data_ptr(), num_slots,
+             slot_mapping.data_ptr(), sb, N, num_heads, head_dim, key.element_size(),
+             nat.stream_of(key))
+
+
+class Attention(nn.Module):
+    """Attention(num_heads, head_dim, scale, num_kv_heads) with the runner-set
+    attributes of attention.py:108-123."""
+
+    def __init__(self, num_heads, head_dim, scale, num_kv_heads):
+        super().__init__()
+        self.num_heads = num_heads
+        self.head_dim = head_dim
+        self.scale = scale
+        self.num_kv_heads = num_kv_heads
+        self.block_size = None
+        self.k_cache = self.v_cache = torch.tensor([])
+        self.k_scale = self.v_scale = None      # int8 store scales
+        self.k_dscale = self.v_dscale = None    # int8 per-channel read scales
+        self.side_k = self.side_v = None        # bf16 outlier side pools
+        self.out_idx2d = None
+        self.head_n_out = None
+        self.kv_cache_is_int8 = False
+        self.attention_backend = "triton_paged"
+        self.profiler = None
+        self.layer_id = -1
+
+    def _profile(self, name):
+        if self.profiler is None:
+            return nullcontext()
+        return self.profiler.range(name, layer=self.layer_id)
+
+    def _int8_tokhead(self) -> bool:
+        return self.kv_cache_is_int8 and self.k_scale is not None and self.k_scale.dim() == 3
+
+    def _read_scales(self):
+        """Scales the read path needs: per-slot scales (per-token-head) or the
+        per-channel read scales (0 at outlier dims)."""
+        if not self.kv_cache_is_int8:
+            return None, None
+        if self._int8_tokhead():
+            return self.k_scale, self.v_scale
+        return self.k_dscale, self.v_dscale
+
+    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor):
+        context = get_context()
+        k_cache, v_cache = self.k_cache, self.v_cache
+        if k_cache.numel() and v_cache.numel():
+            if self.block_size is None:
+                self.block_size = k_cache.size(1)
+            with self._profile("attention.kv_store"):
+                if self.kv_cache_is_int8:
+                    store_kvcache_int8(k, v, k_cache, v_cache, self.k_scale, self.v_scale,
+                                       self.side_k, self.side_v, self.out_idx2d,
+                                       self.head_n_out, context.slot_mapping)
+                else:
+                    store_kvcache(k, v, k_cache, v_cache, context.slot_mapping)
+        rk, rv = self._read_scales()
+        side = self.kv_cache_is_int8 and not self._int8_tokhead()
+        if context.is_mixed or context.is_prefill:
+            q3 = q.view(-1, self.num_heads, self.head_dim)
+            with self._profile("attention.mixed" if context.is_mixed else "attention.prefill"):
+                return varlen_attention(
+                    q3, k_cache, v_cache, scale=self.scale,
+                    block_tables=context.block_tables,
+                    num_decode_rows=context.num_decode_rows if context.is_mixed else 0,
+                    decode_context_lens=context.decode_context_lens if context.is_mixed else None,
+                    cu_seqlens_q=context.cu_seqlens_q, cu_seqlens_k=context.cu_seqlens_k,
+                    cu_seqlens_q_list=context.cu_seqlens_q_list,
+                    cu_seqlens_k_list=context.cu_seqlens_k_list,
+                    k=k.view(-1, self.num_kv_heads, self.head_dim),
+                    v=v.view(-1, self.num_kv_heads, self.head_dim),
+                    k_scale=rk, v_scale=rv,
+                    side_k=self.side_k if side else None,
+                    side_v=self.side_v if side else None,
+                    out_idx2d=self.out_idx2d if side else None,
+                    head_n_out=self.head_n_out if side else None,
+                )
+        with self._profile("attention.paged_decode"):
+            return paged_decode_attention(
+                q, k_cache, v_cache, context.block_tables, context.context_lens, self.scale,
+                context.max_context_len, k_scale=rk, v_scale=rv,
+                side_k=self.side_k if side else None,
+                side_v=self.side_v if side else None,
+                out_idx2d=self.out_idx2d if side else None,
+                head_n_out=self.head_n_out if side else None,
+            )

@@ -1,0 +1,66 @@
+"""Per-step batch metadata read by the attention layer.
+
+Same fields, order and setters as nanovllm/utils/context.py:5-50, so an engine
+that builds a Context for its own attention builds one for this attention too.
+All cu_seqlens fields are prefill-only in a mixed batch; decode rows carry
+their own context lengths (nanovllm/utils/context.py:21-28).
+"""
+from dataclasses import dataclass
+
+import torch
+
+
+@dataclass(slots=True)
+class Context:
+    is_prefill: bool = False
+    cu_seqlens_q: torch.Tensor | None = None
+    cu_seqlens_k: torch.Tensor | None = None
+    cu_seqlens_q_list: list | None = None
+    cu_seqlens_k_list: list | None = None
+    max_seqlen_q: int = 0
+    max_seqlen_k: int = 0
+    slot_mapping: torch.Tensor | None = None
+    context_lens: torch.Tensor | None = None
+    block_tables: torch.Tensor | None = None
+    max_context_len: int = 0
+    is_mixed: bool = False
+    num_decode_rows: int = 0
+    decode_context_lens: torch.Tensor | None = None
+    decode_max_context_len: int = 0
+
+
+_CURRENT = Context()
+
+
+def get_context() -> Context:
+    return _CURRENT
+
+
+def set_context(is_prefill, cu_seqlens_q=None, cu_seqlens_k=None, max_seqlen_q=0, max_seqlen_k=0,
+                slot_mapping=None, context_lens=None, block_tables=None, max_context_len=0,
+                cu_seqlens_q_list=None, cu_seqlens_k_list=None,
+                is_mixed=False, num_decode_rows=0,
+                decode_context_lens=None, decode_max_context_len=0):
+    global _CURRENT
+    _CURRENT = Context(
+        is_prefill=is_prefill,
+        cu_seqlens_q=cu_seqlens_q,
+        cu_seqlens_k=cu_seqlens_k,
+        cu_seqlens_q_list=cu_seqlens_q_list,
+        cu_seqlens_k_list=cu_seqlens_k_list,
+        max_seqlen_q=max_seqlen_q,
+        max_seqlen_k=max_seqlen_k,
+        slot_mapping=slot_mapping,
+        context_lens=context_lens,
+        block_tables=block_tables,
+        max_context_len=max_context_len,
+        is_mixed=is_mixed,
+        num_decode_rows=num_decode_rows,
+        decode_context_lens=decode_context_lens,
+        decode_max_context_len=decode_max_context_len,
+    )
+
+
+def reset_context():
+    global _CURRENT
+    _CURRENT = Context()

@@ -1,0 +1,58 @@
+"""CPU checks of the C ABI: the library loads and exports every symbol the
+header declares, with matching ctypes signatures, and no device call is made."""
+import pathlib
+import re
+
+from nanovllm_amd import _native
+
+REPO = pathlib.Path(__file__).resolve().parents[1]
+
+
+def _declared_symbols():
+    text = (REPO / "include" / "kvc.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(kvc_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_expected_entry_points():
+    names = _declared_symbols()
+    for required in ("kvc_store_kv", "kvc_store_int8_tokhead", "kvc_store_int8_chan",
+                     "kvc_paged_decode", "kvc_varlen_attention", "kvc_block_gather",
+                     "kvc_block_scatter", "kvc_block_copy", "kvc_block_d2h", "kvc_block_h2d"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _native.load()
+    for name in _declared_symbols():
+        assert hasattr(lib, name), f"{name} declared in kvc.h but not exported"
+
+
+def test_binding_covers_the_header_exactly():
+    assert sorted(_native.SIGNATURES) == _declared_symbols()
+
+
+def test_abi_version_and_error_string():
+    lib = _native.load()
+    assert lib.kvc_abi_version() == 1
+    assert isinstance(lib.kvc_last_error(), bytes)
+
+
+def test_workspace_queries_are_host_only():
+    # Pure host arithmetic: 64 x 4096 decode at 32q/4kv needs split-K scratch,
+    # a single short context needs none.
+    big = _native.query("kvc_paged_decode_workspace_bytes", 64, 32, 4, 128, 256, 16)
+    assert big > 0
+    small = _native.query("kvc_paged_decode_workspace_bytes", 64, 32, 4, 128, 256, 1)
+    assert small == 0 or small < big
+
+
+def test_bad_arguments_map_to_python_exceptions():
+    import pytest
+    # head_dim 64 is rejected before any device work (ValueError).
+    with pytest.raises(ValueError):
+        _native.call("kvc_paged_decode", None, 0, 0, None, None, 0, 256, 4, 64, 0, None, None,
+                     None, None, None, None, 0, None, 0, 1, None, 1, 32, 1.0, None, 0, 0, None,
+                     0, None)
+    with pytest.raises(ValueError):
+        _native.call("kvc_block_gather", None, 1, 16, 15, None, 1, None, 16, 16, None)

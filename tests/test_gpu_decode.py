@@ -1,0 +1,151 @@
+"""Paged decode parity — HIP kvc_paged_decode vs the fp32 oracle.
+
+Tolerance: max-abs 2e-2 and mean-abs 2e-3 against fp32 (bf16 outputs).
+Cases follow the reference's kernel tests: NaN-poisoned page tails
+(tests/archive/p5_paged_attention.py:40-63), the page-boundary length matrix
+with scrambled pages (:66-95), plus GQA groupings, split-K lengths, empty
+contexts and the full 32q/4kv batch-64 decode shape.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_attention_close, bits, gathered_pool
+from nanovllm_amd.kernels.paged_attention import paged_decode_attention
+from nanovllm_amd.layers.attention import store_kvcache
+from nanovllm_amd.workloads import decode_workload, uniform_lengths
+from oracle import kv_oracle as ko
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _check(q, k_cache, v_cache, block_tables, lens, scale, label):
+    print(f"[decode] {label}: B={q.shape[0]} H={q.shape[1]} KVH={k_cache.shape[2]} "
+          f"max_ctx={int(lens.max()) if lens.numel() else 0}", flush=True)
+    out = paged_decode_attention(q, k_cache, v_cache, block_tables, lens, scale,
+                                 int(lens.max()) if lens.numel() else 0)
+    torch.cuda.synchronize()
+    kc, bt = gathered_pool(k_cache, block_tables)
+    vc, _ = gathered_pool(v_cache, block_tables)
+    ref = ko.paged_decode_ref(bits(q), ko.bf16_to_f32(bits(kc)), ko.bf16_to_f32(bits(vc)), bt,
+                              lens.cpu().numpy(), scale)
+    return assert_attention_close(out, ref, label)
+
+
+def test_small_poison_tail():
+    torch.manual_seed(20261026)
+    page = 256
+    lengths = torch.tensor([127, 256, 385, 512], dtype=torch.int32, device=DEV)
+    block_tables = torch.tensor([[7, 0], [3, 0], [6, 1], [4, 2]], dtype=torch.int32, device=DEV)
+    k_cache = torch.randn(8, page, 2, 128, dtype=torch.bfloat16, device=DEV)
+    v_cache = torch.randn_like(k_cache)
+    q = torch.randn(4, 16, 128, dtype=torch.bfloat16, device=DEV)
+    for row, length in enumerate(lengths.cpu().tolist()):
+        tail = length % page
+        if tail:
+            page_id = int(block_tables[row, length // page])
+            k_cache[page_id, tail:] = float("nan")
+            v_cache[page_id, tail:] = float("nan")
+    out_max, _ = _check(q, k_cache, v_cache, block_tables, lengths, 128 ** -0.5, "poison-tail")
+    assert out_max <= 2e-2
+
+
+def test_page_boundary_matrix():
+    torch.manual_seed(20261027)
+    lengths_cpu = [255, 256, 257, 511, 512, 513, 2047, 2048, 2049]
+    page = 256
+    per_row = [math.ceil(n / page) for n in lengths_cpu]
+    bt = torch.zeros(len(lengths_cpu), max(per_row), dtype=torch.int32)
+    nxt = 0
+    for row, cnt in enumerate(per_row):
+        pages = list(range(nxt, nxt + cnt))
+        pages[::2] = list(reversed(pages[::2]))
+        bt[row, :cnt] = torch.tensor(pages, dtype=torch.int32)
+        nxt += cnt
+    k_cache = torch.randn(nxt, page, 2, 128, dtype=torch.bfloat16, device=DEV)
+    v_cache = torch.randn_like(k_cache)
+    q = torch.randn(len(lengths_cpu), 16, 128, dtype=torch.bfloat16, device=DEV)
+    for row, n in enumerate(lengths_cpu):
+        tail = n % page
+        if tail:
+            pid = int(bt[row, n // page])
+            k_cache[pid, tail:] = float("nan")
+            v_cache[pid, tail:] = float("nan")
+    lens = torch.tensor(lengths_cpu, dtype=torch.int32, device=DEV)
+    _check(q, k_cache, v_cache, bt.to(DEV), lens, 128 ** -0.5, "page-boundary")
+
+
+@pytest.mark.parametrize("heads,kv_heads", [(16, 8), (32, 4), (32, 32), (32, 2), (64, 2), (12, 4)])
+def test_gqa_groupings(heads, kv_heads):
+    lens = uniform_lengths(6, 1, 1500, seed=heads * 100 + kv_heads)
+    wl = decode_workload(6, heads, kv_heads, 48, lens, seed=7, device=DEV)
+    _check(wl.q, wl.k_cache, wl.v_cache, wl.block_tables, wl.context_lens, wl.scale,
+           f"gqa-{heads}/{kv_heads}")
+
+
+def test_qwen3_06b_shape_after_append():
+    # 0.6B-shaped layer: 16 q / 8 kv heads, 64 blocks, batch 8, ctx U[128, 1024];
+    # one appended token per sequence, then decode with scale 1/sqrt(128).
+    lens = uniform_lengths(8, 128, 1024, seed=101)
+    wl = decode_workload(8, 16, 8, 64, lens, seed=102, device=DEV)
+    store_kvcache(wl.new_k, wl.new_v, wl.k_cache, wl.v_cache, wl.slot_mapping)
+    _check(wl.q, wl.k_cache, wl.v_cache, wl.block_tables, wl.context_lens, wl.scale, "0.6B-step")
+
+
+def test_long_context_split_k():
+    lens = [32768, 20000, 4097, 1]
+    wl = decode_workload(4, 32, 4, 256, lens, seed=9, device=DEV)
+    _check(wl.q, wl.k_cache, wl.v_cache, wl.block_tables, wl.context_lens, wl.scale, "long-split-k")
+
+
+def test_zero_length_context_gives_nan_row():
+    lens = [0, 300]
+    wl = decode_workload(2, 32, 4, 8, [1, 300], seed=3, device=DEV)
+    wl.context_lens = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    _check(wl.q, wl.k_cache, wl.v_cache, wl.block_tables, wl.context_lens, wl.scale, "zero-ctx")
+
+
+def test_full_30b_decode_shape_batch64():
+    # 32 q / 4 kv heads, batch 64, ctx U[512, 4096], non-contiguous tables over
+    # an 8192-block pool, one appended token per sequence.
+    lens = uniform_lengths(64, 512, 4096, seed=2)
+    wl = decode_workload(64, 32, 4, 8192, lens, seed=3, device=DEV, pool_device_fill=True)
+    store_kvcache(wl.new_k, wl.new_v, wl.k_cache, wl.v_cache, wl.slot_mapping)
+    _check(wl.q, wl.k_cache, wl.v_cache, wl.block_tables, wl.context_lens, wl.scale, "30B-b64")
+
+
+def test_strided_q_and_graph_width_tables():
+    # q as a strided view and block tables wider than any context (a captured
+    # graph's padded table): entries past the context are never read.
+    lens = uniform_lengths(5, 100, 900, seed=77)
+    wl = decode_workload(5, 32, 4, 40, lens, seed=78, device=DEV)
+    wide = torch.full((5, 17), 10**6, dtype=torch.int32, device=DEV)
+    wide[:, :wl.block_tables.size(1)] = wl.block_tables
+    wide = torch.where(wide == -1, torch.full_like(wide, 10**6), wide)
+    big = torch.randn(5, 48, 128, dtype=torch.bfloat16, device=DEV)
+    big[:, 8:40] = wl.q
+    q = big[:, 8:40]
+    assert not q.is_contiguous()
+    out = paged_decode_attention(q, wl.k_cache, wl.v_cache, wide, wl.context_lens, wl.scale, 0)
+    ref = paged_decode_attention(wl.q, wl.k_cache, wl.v_cache, wl.block_tables, wl.context_lens,
+                                 wl.scale, 0)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref) or float((out.float() - ref.float()).abs().max()) <= 2e-2
+
+
+def test_shape_errors_match_reference():
+    q = torch.zeros(2, 16, 64, dtype=torch.bfloat16, device=DEV)
+    kc = torch.zeros(4, 256, 2, 64, dtype=torch.bfloat16, device=DEV)
+    bt = torch.zeros(2, 1, dtype=torch.int32, device=DEV)
+    lens = torch.ones(2, dtype=torch.int32, device=DEV)
+    with pytest.raises(ValueError):
+        paged_decode_attention(q, kc, kc, bt, lens, 1.0, 1)
+    with pytest.raises(ValueError):
+        paged_decode_attention(q[:, :, None], kc, kc, bt, lens, 1.0, 1)
+    q2 = torch.zeros(2, 15, 128, dtype=torch.bfloat16, device=DEV)
+    kc2 = torch.zeros(4, 256, 2, 128, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError):
+        paged_decode_attention(q2, kc2, kc2, bt, lens, 1.0, 1)

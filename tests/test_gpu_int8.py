@@ -1,0 +1,264 @@
+"""int8 KV parity: codes and scales bit-exact, int8 decode within tolerance.
+
+Per-token-head (round half to even, fp32 scale = max(amax, 1e-6) / 127) and
+the engine's per-channel encoding with a bf16 outlier side pool
+(tests/p17_kv_int8.py:64-136 geometry: N=512, KVH=8, D=128, seed 7).
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_attention_close, bits, gathered_pool
+from nanovllm_amd.kernels.kv_int8 import (dequant_gathered, dequant_tokhead, store_kvcache_int8,
+                                          store_kvcache_int8_tokhead)
+from nanovllm_amd.kernels.paged_attention import paged_decode_attention
+from nanovllm_amd.workloads import build_block_tables, decode_workload, outlier_keys, uniform_lengths
+from oracle import kv_oracle as ko
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _tokhead_store(key, value, blocks, label, slots=None):
+    N, KVH, D = key.shape
+    print(f"[int8-tokhead] {label}: N={N} KVH={KVH}", flush=True)
+    kc = torch.zeros(blocks, 256, KVH, D, dtype=torch.int8, device=DEV)
+    vc = torch.zeros_like(kc)
+    ks = torch.zeros(blocks, 256, KVH, dtype=torch.float32, device=DEV)
+    vs = torch.zeros_like(ks)
+    if slots is None:
+        slots = torch.randperm(blocks * 256, generator=torch.Generator().manual_seed(N))[:N]
+    slots = slots.to(torch.int32).to(DEV)
+    store_kvcache_int8_tokhead(key, value, kc, vc, ks, vs, slots)
+    torch.cuda.synchronize()
+    rkc, rvc = np.zeros(kc.shape, np.int8), np.zeros(vc.shape, np.int8)
+    rks, rvs = np.zeros(ks.shape, np.float32), np.zeros(vs.shape, np.float32)
+    ko.store_int8_tokhead(bits(key), bits(value), rkc, rvc, rks, rvs, slots.cpu().numpy())
+    assert np.array_equal(kc.cpu().numpy(), rkc), f"{label}: K codes differ"
+    assert np.array_equal(vc.cpu().numpy(), rvc), f"{label}: V codes differ"
+    assert np.array_equal(ks.cpu().numpy().view(np.uint32), rks.view(np.uint32)), f"{label}: K scales"
+    assert np.array_equal(vs.cpu().numpy().view(np.uint32), rvs.view(np.uint32)), f"{label}: V scales"
+    return kc, vc, ks, vs, slots
+
+
+def test_tokhead_store_outlier_keys_bitwise():
+    # K ~ N(0,1) with 1% outliers x20, V ~ N(0,1) (the int8 KV workload).
+    key = outlier_keys((1024, 4, 128), seed=1).to(DEV)
+    value = torch.randn(1024, 4, 128, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16).to(DEV)
+    _tokhead_store(key, value, 8, "outliers")
+
+
+def test_tokhead_store_half_way_ties_and_clamps():
+    # amax 127 -> s = 1 exactly: x = k + 0.5 are exact ties (half to even);
+    # an all-zero row and a tiny row exercise the 1e-6 clamp.
+    D = 128
+    ties = torch.tensor([0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5, -126.5], dtype=torch.float32)
+    row = torch.zeros(D)
+    row[:8] = ties
+    row[8] = 127.0
+    rows = torch.stack([row, torch.zeros(D), torch.full((D,), 3e-7), -row])
+    key = rows.view(4, 1, D).to(torch.bfloat16).to(DEV)
+    kc, _, ks, _, slots = _tokhead_store(key, key.clone(), 1, "ties", slots=torch.arange(4))
+    codes = kc.view(-1, 1, D)[:4, 0, :9].cpu().tolist()
+    assert codes[0] == [0, 2, 2, 0, -2, -2, 126, -126, 127]
+
+
+def test_tokhead_dequant_bitwise():
+    key = outlier_keys((256, 4, 128), seed=5).to(DEV)
+    kc, _, ks, _, slots = _tokhead_store(key, key.clone(), 2, "dequant")
+    codes = kc.view(-1, 4, 128)[slots.long()]
+    scales = ks.view(-1, 4)[slots.long()]
+    out = dequant_tokhead(codes, scales)
+    torch.cuda.synchronize()
+    ref = ko.dequant_tokhead(codes.cpu().numpy(), scales.cpu().numpy())
+    assert np.array_equal(bits(out), ref)
+
+
+def _p17_unit_inputs():
+    N, KVH, D, N_OUT_MAX = 512, 8, 128, 4
+    g = torch.Generator(device="cpu").manual_seed(7)
+    key = (torch.randn(N, KVH, D, generator=g) * 0.7).to(torch.bfloat16)
+    value = (torch.randn(N, KVH, D, generator=g) * 0.7).to(torch.bfloat16)
+    key[:8] *= 8.0
+    key[:, 0, :4] *= 60.0
+    key[:, 1, 10] *= 120.0
+    value[:, 2, :4] *= 60.0
+    kf, vf = key.float(), value.float()
+    amax_k, amax_v = kf.abs().amax(0), vf.abs().amax(0)
+    typ_k = kf.abs().mean(0).clamp_min(1e-6)
+    typ_v = vf.abs().mean(0).clamp_min(1e-6)
+    s_k = (amax_k / 127.0).clamp_min(1e-6)
+    s_v = (amax_v / 127.0).clamp_min(1e-6)
+    ratio = torch.maximum(amax_k / typ_k, amax_v / typ_v)
+    out_idx2d = torch.zeros(KVH, N_OUT_MAX, dtype=torch.int32)
+    head_n_out = torch.zeros(KVH, dtype=torch.int32)
+    for h in range(KVH):
+        dims = ratio[h].nonzero().flatten()
+        dims = dims[ratio[h, dims] > 10.0][:N_OUT_MAX]
+        out_idx2d[h, :dims.numel()] = dims.to(torch.int32)
+        head_n_out[h] = dims.numel()
+    ds_k, ds_v = s_k.clone(), s_v.clone()
+    for h in range(KVH):
+        n_h = int(head_n_out[h])
+        ds_k[h, out_idx2d[h, :n_h].long()] = 0.0
+        ds_v[h, out_idx2d[h, :n_h].long()] = 0.0
+    return key, value, s_k, s_v, ds_k, ds_v, out_idx2d, head_n_out
+
+
+def test_chan_store_matches_p17_unit_bitwise():
+    key, value, s_k, s_v, _, _, out_idx2d, head_n_out = _p17_unit_inputs()
+    N, KVH, D = key.shape
+    assert int(head_n_out.sum()) > 0
+    print(f"[int8-chan] p17 unit: outliers per head {head_n_out.tolist()}", flush=True)
+    blocks, nout = 9, out_idx2d.shape[1]
+    slot = torch.arange(N, dtype=torch.int32)
+    kc = torch.zeros(blocks, 256, KVH, D, dtype=torch.int8, device=DEV)
+    vc = torch.zeros_like(kc)
+    sk = torch.zeros(blocks, 256, KVH, nout, dtype=torch.bfloat16, device=DEV)
+    sv = torch.zeros_like(sk)
+    store_kvcache_int8(key.to(DEV), value.to(DEV), kc, vc, s_k.to(DEV), s_v.to(DEV), sk, sv,
+                       out_idx2d.to(DEV), head_n_out.to(DEV), slot.to(DEV))
+    torch.cuda.synchronize()
+    rkc, rvc = np.zeros(kc.shape, np.int8), np.zeros(vc.shape, np.int8)
+    rsk, rsv = np.zeros(sk.shape, np.uint16), np.zeros(sv.shape, np.uint16)
+    ko.store_int8_chan(bits(key), bits(value), rkc, rvc, s_k.numpy(), s_v.numpy(), rsk, rsv,
+                       out_idx2d.numpy(), head_n_out.numpy(), slot.numpy())
+    for name, a, b in (("k_payload", kc.cpu().numpy(), rkc), ("v_payload", vc.cpu().numpy(), rvc),
+                       ("k_side", bits(sk), rsk), ("v_side", bits(sv), rsv)):
+        assert np.array_equal(a, b), f"{name} differs"
+
+
+def test_chan_store_strided_v():
+    # The reference kernel reads V with K's strides; this path takes V's own.
+    key, value, s_k, s_v, _, _, out_idx2d, head_n_out = _p17_unit_inputs()
+    N, KVH, D = key.shape
+    fused = torch.cat([key.view(N, -1), value.view(N, -1)], dim=1).to(DEV)
+    k_view = fused[:, :KVH * D].view(N, KVH, D)
+    v_view = fused[:, KVH * D:].view(N, KVH, D)
+    nout = out_idx2d.shape[1]
+    kc = torch.zeros(3, 256, KVH, D, dtype=torch.int8, device=DEV)
+    vc = torch.zeros_like(kc)
+    sk = torch.zeros(3, 256, KVH, nout, dtype=torch.bfloat16, device=DEV)
+    sv = torch.zeros_like(sk)
+    slot = torch.arange(N, dtype=torch.int32, device=DEV)
+    store_kvcache_int8(k_view, v_view, kc, vc, s_k.to(DEV), s_v.to(DEV), sk, sv,
+                       out_idx2d.to(DEV), head_n_out.to(DEV), slot)
+    torch.cuda.synchronize()
+    rvc = np.zeros(vc.shape, np.int8)
+    rkc = np.zeros(kc.shape, np.int8)
+    rsk, rsv = np.zeros(sk.shape, np.uint16), np.zeros(sv.shape, np.uint16)
+    ko.store_int8_chan(bits(key), bits(value), rkc, rvc, s_k.numpy(), s_v.numpy(), rsk, rsv,
+                       out_idx2d.numpy(), head_n_out.numpy(), slot.cpu().numpy())
+    assert np.array_equal(vc.cpu().numpy(), rvc)
+    assert np.array_equal(bits(sv), rsv)
+
+
+def test_chan_dequant_gathered_bitwise_and_relerr():
+    key, value, s_k, s_v, ds_k, ds_v, out_idx2d, head_n_out = _p17_unit_inputs()
+    N, KVH, D = key.shape
+    nout = out_idx2d.shape[1]
+    rkc = np.zeros((3, 256, KVH, D), np.int8)
+    rvc = np.zeros_like(rkc)
+    rsk = np.zeros((3, 256, KVH, nout), np.uint16)
+    rsv = np.zeros_like(rsk)
+    slot = np.arange(N)
+    ko.store_int8_chan(bits(key), bits(value), rkc, rvc, s_k.numpy(), s_v.numpy(), rsk, rsv,
+                       out_idx2d.numpy(), head_n_out.numpy(), slot)
+    gq = torch.from_numpy(rkc.reshape(-1, KVH, D)[:N].copy()).to(DEV)
+    gside = torch.from_numpy(rsk.reshape(-1, KVH, nout)[:N].view(np.int16).copy()).view(torch.bfloat16).to(DEV)
+    out = dequant_gathered(gq, ds_k.to(DEV), gside, out_idx2d.to(DEV), head_n_out.to(DEV))
+    torch.cuda.synchronize()
+    ref = ko.dequant_chan(gq.cpu().numpy(), ds_k.numpy(), bits(gside), out_idx2d.numpy(),
+                          head_n_out.numpy())
+    assert np.array_equal(bits(out), ref)
+    rel = float((out.float().cpu() - key.float()).abs().mean() / key.float().abs().mean())
+    assert rel < 0.03
+
+
+def _decode_int8_tokhead_case(batch, lens, blocks, seed, label):
+    wl = decode_workload(batch, 32, 4, blocks, lens, seed=seed, device=DEV, kv_dtype="int8_tokhead")
+    print(f"[int8-decode] {label}: B={batch} max_ctx={max(lens)}", flush=True)
+    out = paged_decode_attention(wl.q, wl.k_cache, wl.v_cache, wl.block_tables, wl.context_lens,
+                                 wl.scale, max(lens), k_scale=wl.k_scale, v_scale=wl.v_scale)
+    torch.cuda.synchronize()
+    kc, bt = gathered_pool(wl.k_cache, wl.block_tables)
+    vc, _ = gathered_pool(wl.v_cache, wl.block_tables)
+    ksc, _ = gathered_pool(wl.k_scale, wl.block_tables)
+    vsc, _ = gathered_pool(wl.v_scale, wl.block_tables)
+    kf = ko.kv_float(kc.numpy(), "int8_tokhead", ksc.numpy())
+    vf = ko.kv_float(vc.numpy(), "int8_tokhead", vsc.numpy())
+    ref = ko.paged_decode_ref(bits(wl.q), kf, vf, bt, np.asarray(lens), wl.scale)
+    assert_attention_close(out, ref, label)
+
+
+def test_int8_tokhead_decode_small():
+    _decode_int8_tokhead_case(6, uniform_lengths(6, 1, 3000, seed=4), 80, 5, "tokhead-small")
+
+
+def test_int8_tokhead_decode_long_context():
+    _decode_int8_tokhead_case(2, [32768, 12345], 200, 6, "tokhead-32k")
+
+
+def test_int8_tokhead_end_to_end_quantised_decode():
+    # Append real activations through the quantiser, then decode the int8 pool.
+    B, H, KVH, D, blocks = 4, 32, 4, 128, 24
+    lens = [700, 1, 1500, 256]
+    g = torch.Generator().manual_seed(8)
+    bt = build_block_tables(lens, blocks, 256, g)
+    kc = torch.zeros(blocks, 256, KVH, D, dtype=torch.int8, device=DEV)
+    vc = torch.zeros_like(kc)
+    ks = torch.zeros(blocks, 256, KVH, dtype=torch.float32, device=DEV)
+    vs = torch.zeros_like(ks)
+    slots = []
+    for i, n in enumerate(lens):
+        for t in range(n):
+            slots.append(int(bt[i, t // 256]) * 256 + t % 256)
+    N = len(slots)
+    key = outlier_keys((N, KVH, D), seed=9).to(DEV)
+    value = torch.randn(N, KVH, D, generator=g).to(torch.bfloat16).to(DEV)
+    store_kvcache_int8_tokhead(key, value, kc, vc, ks, vs,
+                               torch.tensor(slots, dtype=torch.int32, device=DEV))
+    q = torch.randn(B, H, D, generator=g).to(torch.bfloat16).to(DEV)
+    lens_t = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    out = paged_decode_attention(q, kc, vc, bt.to(DEV), lens_t, D ** -0.5, max(lens),
+                                 k_scale=ks, v_scale=vs)
+    torch.cuda.synchronize()
+    kf = ko.kv_float(kc.cpu().numpy(), "int8_tokhead", ks.cpu().numpy())
+    vf = ko.kv_float(vc.cpu().numpy(), "int8_tokhead", vs.cpu().numpy())
+    ref = ko.paged_decode_ref(bits(q), kf, vf, bt.numpy(), np.asarray(lens), D ** -0.5)
+    assert_attention_close(out, ref, "tokhead-e2e")
+
+
+def test_int8_chan_decode_with_side_pool():
+    key, value, s_k, s_v, ds_k, ds_v, out_idx2d, head_n_out = _p17_unit_inputs()
+    N, KVH, D = key.shape   # 512 tokens, 8 kv heads
+    H = 16
+    nout = out_idx2d.shape[1]
+    blocks = 4
+    lens = [512, 300]
+    bt = torch.tensor([[2, 0], [1, 3]], dtype=torch.int32)
+    slots = [int(bt[0, t // 256]) * 256 + t % 256 for t in range(512)]
+    kc = torch.zeros(blocks, 256, KVH, D, dtype=torch.int8, device=DEV)
+    vc = torch.zeros_like(kc)
+    sk = torch.zeros(blocks, 256, KVH, nout, dtype=torch.bfloat16, device=DEV)
+    sv = torch.zeros_like(sk)
+    store_kvcache_int8(key.to(DEV), value.to(DEV), kc, vc, s_k.to(DEV), s_v.to(DEV), sk, sv,
+                       out_idx2d.to(DEV), head_n_out.to(DEV),
+                       torch.tensor(slots, dtype=torch.int32, device=DEV))
+    slots2 = [int(bt[1, t // 256]) * 256 + t % 256 for t in range(300)]
+    store_kvcache_int8(key[:300].flip(0).contiguous().to(DEV), value[:300].to(DEV), kc, vc,
+                       s_k.to(DEV), s_v.to(DEV), sk, sv, out_idx2d.to(DEV), head_n_out.to(DEV),
+                       torch.tensor(slots2, dtype=torch.int32, device=DEV))
+    q = torch.randn(2, H, D, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16).to(DEV)
+    lens_t = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    print("[int8-chan-decode] side pool", flush=True)
+    out = paged_decode_attention(q, kc, vc, bt.to(DEV), lens_t, D ** -0.5, 512,
+                                 k_scale=ds_k.to(DEV), v_scale=ds_v.to(DEV), side_k=sk, side_v=sv,
+                                 out_idx2d=out_idx2d.to(DEV), head_n_out=head_n_out.to(DEV))
+    torch.cuda.synchronize()
+    kf = ko.kv_float(kc.cpu().numpy(), "int8_chan", ds_k.numpy(), bits(sk), out_idx2d.numpy(),
+                     head_n_out.numpy())
+    vf = ko.kv_float(vc.cpu().numpy(), "int8_chan", ds_v.numpy(), bits(sv), out_idx2d.numpy(),
+                     head_n_out.numpy())
+    ref = ko.paged_decode_ref(bits(q), kf, vf, bt.numpy(), np.asarray(lens), D ** -0.5)
+    assert_attention_close(out, ref, "chan-side")

@@ -1,0 +1,154 @@
+"""Mixed decode + chunked-prefill parity — one varlen launch vs the oracle.
+
+The oracle follows the reference's two sub-paths: paged decode for the decode
+rows and the per-chunk prefix-masked attention of
+nanovllm/layers/attention.py:179-213 for the prefill rows.
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_attention_close, bits, gathered_pool
+from nanovllm_amd.kernels.varlen import varlen_attention
+from nanovllm_amd.layers.attention import Attention
+from nanovllm_amd.utils.context import reset_context, set_context
+from nanovllm_amd.workloads import build_block_tables, uniform_lengths
+from oracle import kv_oracle as ko
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _mixed_case(H, KVH, dec_lens, chunks, seed, kv="bf16"):
+    """chunks: list of (prefix, chunk_len).  Returns inputs on the device."""
+    g = torch.Generator().manual_seed(seed)
+    pre_total = [p + c for p, c in chunks]
+    all_lens = list(dec_lens) + pre_total
+    blocks = sum(max(1, (n + 255) // 256) for n in all_lens) + 3
+    bt = build_block_tables(all_lens, blocks, 256, g)
+    shape = (blocks, 256, KVH, 128)
+    k_cache = torch.randn(shape, generator=g).to(torch.bfloat16)
+    v_cache = torch.randn(shape, generator=g).to(torch.bfloat16)
+    T = len(dec_lens) + sum(c for _, c in chunks)
+    q = torch.randn(T, H, 128, generator=g).to(torch.bfloat16)
+    cu_q, cu_k = [0], [0]
+    for p, c in chunks:
+        cu_q.append(cu_q[-1] + c)
+        cu_k.append(cu_k[-1] + p + c)
+    return dict(q=q.to(DEV), k_cache=k_cache.to(DEV), v_cache=v_cache.to(DEV), bt=bt.to(DEV),
+                dec_lens=torch.tensor(dec_lens, dtype=torch.int32).to(DEV), cu_q=cu_q, cu_k=cu_k,
+                n_dec=len(dec_lens))
+
+
+def _check_mixed(c, label, scale=128 ** -0.5):
+    print(f"[varlen] {label}: rows={c['q'].shape[0]} dec={c['n_dec']} chunks={len(c['cu_q']) - 1}",
+          flush=True)
+    out = varlen_attention(
+        c["q"], c["k_cache"], c["v_cache"], scale=scale, block_tables=c["bt"],
+        num_decode_rows=c["n_dec"], decode_context_lens=c["dec_lens"] if c["n_dec"] else None,
+        cu_seqlens_q=torch.tensor(c["cu_q"], dtype=torch.int32, device=DEV),
+        cu_seqlens_k=torch.tensor(c["cu_k"], dtype=torch.int32, device=DEV),
+        cu_seqlens_q_list=c["cu_q"], cu_seqlens_k_list=c["cu_k"])
+    torch.cuda.synchronize()
+    kc, bt = gathered_pool(c["k_cache"], c["bt"])
+    vc, _ = gathered_pool(c["v_cache"], c["bt"])
+    ref = ko.mixed_ref(bits(c["q"]), ko.bf16_to_f32(bits(kc)), ko.bf16_to_f32(bits(vc)), bt,
+                       c["n_dec"], c["dec_lens"].cpu().numpy(), c["cu_q"], c["cu_k"], scale)
+    return assert_attention_close(out, ref, label)
+
+
+def test_prefill_chunks_with_prefixes_small():
+    c = _mixed_case(32, 4, [], [(0, 40), (300, 17), (1000, 256)], seed=1)
+    _check_mixed(c, "prefill-only")
+
+
+def test_mixed_decode_plus_prefill_small():
+    c = _mixed_case(32, 4, [1, 255, 256, 257, 3000], [(0, 33), (512, 64), (2048, 100)], seed=2)
+    _check_mixed(c, "mixed-small")
+
+
+@pytest.mark.parametrize("heads,kv_heads", [(16, 8), (32, 32), (12, 4), (64, 2)])
+def test_mixed_gqa_groupings(heads, kv_heads):
+    c = _mixed_case(heads, kv_heads, [900, 17], [(0, 20), (700, 45)], seed=heads + kv_heads)
+    _check_mixed(c, f"mixed-gqa-{heads}/{kv_heads}")
+
+
+def test_stall_free_mixed_batch_full_shape():
+    # Four prefill chunks of 256 tokens with cached prefixes 0/512/2048/8192
+    # plus 60 decode rows with contexts U[256, 4096], 32q/4kv, page 256.
+    dec = uniform_lengths(60, 256, 4096, seed=3)
+    c = _mixed_case(32, 4, dec, [(0, 256), (512, 256), (2048, 256), (8192, 256)], seed=4)
+    _check_mixed(c, "stall-free-full")
+
+
+def test_fresh_kv_prefill_without_block_tables():
+    # No prefix cache: keys are the step's own k/v rows, causal inside each
+    # sequence (attention.py:195-199).
+    g = torch.Generator().manual_seed(5)
+    H, KVH, lens = 32, 4, [1, 77, 300]
+    T = sum(lens)
+    q = torch.randn(T, H, 128, generator=g).to(torch.bfloat16).to(DEV)
+    k = torch.randn(T, KVH, 128, generator=g).to(torch.bfloat16).to(DEV)
+    v = torch.randn(T, KVH, 128, generator=g).to(torch.bfloat16).to(DEV)
+    cu = [0]
+    for n in lens:
+        cu.append(cu[-1] + n)
+    print("[varlen] fresh-kv prefill", flush=True)
+    out = varlen_attention(q, None, None, scale=128 ** -0.5, block_tables=None, k=k, v=v,
+                           cu_seqlens_q_list=cu, cu_seqlens_k_list=cu)
+    torch.cuda.synchronize()
+    ref = ko.prefill_ref(bits(q), None, None, None, cu, cu, 128 ** -0.5,
+                         fresh_k=ko.bf16_to_f32(bits(k)), fresh_v=ko.bf16_to_f32(bits(v)))
+    assert_attention_close(out, ref, "fresh-kv")
+
+
+def test_attention_forward_mixed_matches_decode_and_prefill_paths():
+    # Attention.forward on a mixed Context: store, then one varlen launch; the
+    # result must match the oracle for both row groups.
+    H, KVH, D = 32, 4, 128
+    g = torch.Generator().manual_seed(6)
+    dec_lens = [129, 512]
+    chunks = [(0, 31), (256, 20)]
+    all_lens = dec_lens + [p + c for p, c in chunks]
+    blocks = 12
+    bt = build_block_tables(all_lens, blocks, 256, g)
+    k_cache = torch.randn(blocks, 256, KVH, D, generator=g).to(torch.bfloat16).to(DEV)
+    v_cache = torch.randn(blocks, 256, KVH, D, generator=g).to(torch.bfloat16).to(DEV)
+    # rows: each decode row's new token is its last position; prefill rows are
+    # the chunk's tokens (positions prefix .. prefix + c - 1).
+    slots = []
+    for i, n in enumerate(dec_lens):
+        slots.append(int(bt[i, (n - 1) // 256]) * 256 + (n - 1) % 256)
+    for j, (p, c) in enumerate(chunks):
+        row = len(dec_lens) + j
+        for t in range(p, p + c):
+            slots.append(int(bt[row, t // 256]) * 256 + t % 256)
+    T = len(slots)
+    q = torch.randn(T, H, D, generator=g).to(torch.bfloat16).to(DEV)
+    k = torch.randn(T, KVH, D, generator=g).to(torch.bfloat16).to(DEV)
+    v = torch.randn(T, KVH, D, generator=g).to(torch.bfloat16).to(DEV)
+    cu_q, cu_k = [0], [0]
+    for p, c in chunks:
+        cu_q.append(cu_q[-1] + c)
+        cu_k.append(cu_k[-1] + p + c)
+    attn = Attention(H, D, D ** -0.5, KVH)
+    attn.k_cache, attn.v_cache = k_cache, v_cache
+    set_context(True, torch.tensor(cu_q, dtype=torch.int32, device=DEV),
+                torch.tensor(cu_k, dtype=torch.int32, device=DEV), max(c for _, c in chunks),
+                max(cu_k[i + 1] - cu_k[i] for i in range(len(chunks))),
+                torch.tensor(slots, dtype=torch.int32, device=DEV), None, bt.to(DEV),
+                cu_seqlens_q_list=cu_q, cu_seqlens_k_list=cu_k, is_mixed=True,
+                num_decode_rows=len(dec_lens),
+                decode_context_lens=torch.tensor(dec_lens, dtype=torch.int32, device=DEV),
+                decode_max_context_len=max(dec_lens))
+    try:
+        print("[varlen] Attention.forward mixed", flush=True)
+        out = attn(q, k, v)
+        torch.cuda.synchronize()
+    finally:
+        reset_context()
+    kc, btn = gathered_pool(k_cache, bt.to(DEV))
+    vc, _ = gathered_pool(v_cache, bt.to(DEV))
+    ref = ko.mixed_ref(bits(q), ko.bf16_to_f32(bits(kc)), ko.bf16_to_f32(bits(vc)), btn,
+                       len(dec_lens), np.asarray(dec_lens), cu_q, cu_k, D ** -0.5)
+    assert_attention_close(out, ref, "forward-mixed")
