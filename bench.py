@@ -1,0 +1,374 @@
+"""Paged-KV decode benchmark on one MI355X.
+
+Default workload (the headline): Qwen3-30B-A3B full attention shape — 32 q
+heads, 4 kv heads, head_dim 128, bf16, page 256 — batch 64 at context 4096
+over an 8192-block pool with non-contiguous block tables.  One step = append
+one token per sequence through slot_mapping, then one paged decode launch.
+
+Prints ONE JSON line: decode tokens/s (value), the decode kernel's achieved
+KV-read bandwidth against the 8 TB/s HBM peak (roofline), and the engine's
+torch CPU decode path (gather + GQA expand + masked SDPA) timed on a bounded
+sample of the same workload on this host (cpu_baseline).
+
+    python bench.py [--gpus 1] [--steps 50] [--warmup 10]
+    python bench.py --workload mixed|int8|decode-dist|append|swap   (extra lines)
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+for _p in (REPO, os.path.join(REPO, "s4000-moe-engine_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "decode attn tokens/s + achieved KV-read HBM GB/s (% of peak), bs64×4k ctx"
+HBM_PEAK_GBPS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def parse_args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="decode",
+                    choices=["decode", "decode-dist", "int8", "mixed", "append", "swap", "copy"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample", type=int, default=8,
+                    help="sequences of the workload the CPU baseline runs")
+    return ap.parse_args()
+
+
+# ---------------------------------------------------------------------------
+# timing helpers
+# ---------------------------------------------------------------------------
+class EventTimer:
+    """Pairs of HIP events on torch's current stream (the stream libkvc launches
+    on); durations are read after the timed region ends."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.pairs = []
+
+    def start(self):
+        e = self.torch.cuda.Event(enable_timing=True)
+        e.record()
+        return e
+
+    def stop(self, s):
+        e = self.torch.cuda.Event(enable_timing=True)
+        e.record()
+        self.pairs.append((s, e))
+
+    def mean_ms(self):
+        return statistics.fmean(s.elapsed_time(e) for s, e in self.pairs)
+
+
+def cpu_threads():
+    return len(os.sched_getaffinity(0))
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the engine's torch decode path on the host
+# ---------------------------------------------------------------------------
+def cpu_decode_baseline(torch, wl, sample: int, reps: int = 5):
+    from oracle import kv_oracle as ko
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    b = min(sample, wl.batch)
+    bt = wl.block_tables[:b].cpu()
+    used = torch.unique(bt[bt >= 0])
+    remap = torch.full((wl.k_cache.size(0),), -1, dtype=torch.int64)
+    remap[used] = torch.arange(used.numel())
+    kc = wl.k_cache.index_select(0, used.to(wl.k_cache.device)).cpu()
+    vc = wl.v_cache.index_select(0, used.to(wl.v_cache.device)).cpu()
+    bt_small = torch.where(bt >= 0, remap[bt.clamp(min=0).long()], torch.full_like(bt, -1,
+                           dtype=torch.int64)).to(torch.int32)
+    q = wl.q[:b].cpu()
+    lens = wl.context_lens[:b].cpu()
+    max_len = int(lens.max())
+    ko.gather_sdpa_decode(q, kc, vc, bt_small, lens, wl.scale, max_len)   # warm-up
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        ko.gather_sdpa_decode(q, kc, vc, bt_small, lens, wl.scale, max_len)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    cv = statistics.pstdev(times) / statistics.fmean(times)
+    return {
+        "value": round(b / med, 1),
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"{b} of the {wl.batch} sequences (same block tables and KV bytes), "
+                   f"torch gather+expand+masked SDPA decode, median of {reps} reps "
+                   f"({med * 1e3:.1f} ms, cv {cv:.2f})"),
+    }
+
+
+# ---------------------------------------------------------------------------
+# workloads
+# ---------------------------------------------------------------------------
+def run_decode(args, torch, dist: bool, int8: bool = False):
+    from nanovllm_amd.kernels.kv_int8 import store_kvcache_int8_tokhead
+    from nanovllm_amd.kernels.paged_attention import paged_decode_attention
+    from nanovllm_amd.layers.attention import store_kvcache
+    from nanovllm_amd.workloads import decode_workload, uniform_lengths
+
+    dev = torch.device("cuda:0")
+    if int8:
+        batch, heads, kvh, blocks = 16, 32, 4, 2048 + 16
+        lens = [32768] * batch
+    else:
+        batch, heads, kvh, blocks = 64, 32, 4, 8192
+        lens = uniform_lengths(batch, 512, 4096, seed=2) if dist else [4096] * batch
+    wl = decode_workload(batch, heads, kvh, blocks, lens, seed=3, device=dev,
+                         pool_device_fill=True, kv_dtype="int8_tokhead" if int8 else "bf16")
+
+    def step(timer=None):
+        if int8:
+            store_kvcache_int8_tokhead(wl.new_k, wl.new_v, wl.k_cache, wl.v_cache, wl.k_scale,
+                                       wl.v_scale, wl.slot_mapping)
+        else:
+            store_kvcache(wl.new_k, wl.new_v, wl.k_cache, wl.v_cache, wl.slot_mapping)
+        s = timer.start() if timer else None
+        out = paged_decode_attention(wl.q, wl.k_cache, wl.v_cache, wl.block_tables,
+                                     wl.context_lens, wl.scale, max(lens),
+                                     k_scale=wl.k_scale, v_scale=wl.v_scale)
+        if timer:
+            timer.stop(s)
+        return out
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    timer = EventTimer(torch)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(timer)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kernel_ms = timer.mean_ms()
+    ms_per_step = wall / args.steps * 1e3
+
+    tok_bytes = 2 * kvh * 128 * (1 if int8 else 2) + (2 * kvh * 4 if int8 else 0)
+    kv_bytes = sum(lens) * tok_bytes
+    other = 2 * batch * heads * 128 * 2 + wl.block_tables.numel() * 4 + batch * 4
+    algo = kv_bytes + other
+    achieved = algo / (kernel_ms * 1e-3) / 1e9
+    ctx_desc = "ctx U[512,4096]" if dist else f"ctx {lens[0]}"
+    res = {
+        "metric": METRIC,
+        "value": round(batch / (ms_per_step * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8" if int8 else "bf16",
+        "data": "synthetic (seeded N(0,1) q/k/v, random non-contiguous block tables)",
+        "config": {
+            "workload": (f"paged decode step (append 1 token/seq + decode), {heads}q/{kvh}kv/128 "
+                         f"{'int8 per-token-head' if int8 else 'bf16'}, batch {batch} x "
+                         f"{ctx_desc}, page 256, {blocks}-block pool"),
+            "batch": batch,
+            "context": "U[512,4096]" if dist else lens[0],
+            "heads": heads,
+            "kv_heads": kvh,
+            "head_dim": 128,
+            "page": 256,
+            "decode_kernel_us": round(kernel_ms * 1e3, 2),
+            "kv_read_GBps": round(kv_bytes / (kernel_ms * 1e-3) / 1e9, 1),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": None,
+        },
+    }
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_decode_baseline(torch, wl, args.cpu_sample)
+    return res
+
+
+def run_mixed(args, torch):
+    from nanovllm_amd.kernels.varlen import varlen_attention
+    from nanovllm_amd.workloads import build_block_tables, uniform_lengths
+
+    dev = torch.device("cuda:0")
+    heads, kvh = 32, 4
+    dec = uniform_lengths(60, 256, 4096, seed=3)
+    chunks = [(0, 256), (512, 256), (2048, 256), (8192, 256)]
+    all_lens = dec + [p + c for p, c in chunks]
+    g = torch.Generator().manual_seed(4)
+    blocks = sum((n + 255) // 256 for n in all_lens) + 8
+    bt = build_block_tables(all_lens, blocks, 256, g).to(dev)
+    dg = torch.Generator(device=dev).manual_seed(5)
+    kc = torch.randn(blocks, 256, kvh, 128, generator=dg, device=dev, dtype=torch.bfloat16)
+    vc = torch.randn(blocks, 256, kvh, 128, generator=dg, device=dev, dtype=torch.bfloat16)
+    T = len(dec) + sum(c for _, c in chunks)
+    q = torch.randn(T, heads, 128, generator=dg, device=dev, dtype=torch.bfloat16)
+    cu_q, cu_k = [0], [0]
+    for p, c in chunks:
+        cu_q.append(cu_q[-1] + c)
+        cu_k.append(cu_k[-1] + p + c)
+    dlen = torch.tensor(dec, dtype=torch.int32, device=dev)
+    cq = torch.tensor(cu_q, dtype=torch.int32, device=dev)
+    ck = torch.tensor(cu_k, dtype=torch.int32, device=dev)
+
+    def call():
+        return varlen_attention(q, kc, vc, scale=128 ** -0.5, block_tables=bt,
+                                num_decode_rows=len(dec), decode_context_lens=dlen,
+                                cu_seqlens_q=cq, cu_seqlens_k=ck, cu_seqlens_q_list=cu_q,
+                                cu_seqlens_k_list=cu_k)
+
+    for _ in range(args.warmup):
+        call()
+    torch.cuda.synchronize()
+    timer = EventTimer(torch)
+    for _ in range(args.steps):
+        s = timer.start()
+        call()
+        timer.stop(s)
+    torch.cuda.synchronize()
+    ms = timer.mean_ms()
+    flops = 0
+    for p, c in chunks:
+        for r in range(c):
+            flops += 4 * 128 * heads * (p + r + 1)
+    kv = sum(dec) * 2 * kvh * 128 * 2
+    return {"workload": "mixed: 60 decode rows ctx U[256,4096] + 4x256-token prefill chunks "
+                        "(prefix 0/512/2048/8192), one varlen launch + merge",
+            "ms": round(ms, 4), "prefill_gflop": round(flops / 1e9, 2),
+            "prefill_TFLOPs_if_alone": round(flops / (ms * 1e-3) / 1e12, 1),
+            "decode_kv_GB": round(kv / 1e9, 3),
+            "tokens_per_s": round(T / (ms * 1e-3), 1)}
+
+
+def run_append(args, torch):
+    from nanovllm_amd.layers.attention import store_kvcache
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(1)
+    N, kvh = 16384, 4
+    k = torch.randn(N, kvh, 128, generator=g, device=dev, dtype=torch.bfloat16)
+    v = torch.randn(N, kvh, 128, generator=g, device=dev, dtype=torch.bfloat16)
+    kc = torch.empty(1024, 256, kvh, 128, device=dev, dtype=torch.bfloat16)
+    vc = torch.empty_like(kc)
+    slots = torch.randperm(1024 * 256, device=dev)[:N].to(torch.int32)
+    for _ in range(args.warmup):
+        store_kvcache(k, v, kc, vc, slots)
+    timer = EventTimer(torch)
+    for _ in range(args.steps):
+        s = timer.start()
+        store_kvcache(k, v, kc, vc, slots)
+        timer.stop(s)
+    torch.cuda.synchronize()
+    ms = timer.mean_ms()
+    byts = 2 * 2 * N * kvh * 128 * 2 + N * 4
+    return {"workload": f"append {N} tokens x 4kv x 128 bf16 (K and V)", "ms": round(ms, 4),
+            "GBps": round(byts / (ms * 1e-3) / 1e9, 1)}
+
+
+def run_swap(args, torch):
+    from nanovllm_amd.engine.kv_runner import BlockMover
+    dev = torch.device("cuda:0")
+    L, kvh, pool_blocks = 48, 4, 2048
+    pool = torch.empty(2, L, pool_blocks, 256, kvh, 128, device=dev, dtype=torch.bfloat16)
+    mover = BlockMover(pool)
+    g = torch.Generator().manual_seed(7)
+    perm = torch.randperm(pool_blocks, generator=g).tolist()
+    n_copy = 512
+    src, dst = perm[:n_copy], perm[n_copy:2 * n_copy]
+    for _ in range(2):
+        mover.copy(src, dst)
+    timer = EventTimer(torch)
+    for _ in range(max(3, args.steps // 10)):
+        s = timer.start()
+        mover.copy(src, dst)
+        timer.stop(s)
+    torch.cuda.synchronize()
+    ms = timer.mean_ms()
+    byts = 2 * n_copy * mover.item_bytes
+    n_swap = 32
+    host = torch.empty((n_swap,) + mover.item_shape, dtype=pool.dtype, pin_memory=True)
+    ids = perm[2 * n_copy:2 * n_copy + n_swap]
+    mover.d2h(ids, host)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    mover.d2h(ids, host)
+    torch.cuda.synchronize()
+    d2h = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    mover.h2d(host, ids)
+    torch.cuda.synchronize()
+    h2d = time.perf_counter() - t0
+    return {"workload": f"compaction copy of {n_copy} scattered 24 MiB blocks (48 layers, 4kv) "
+                        f"+ {n_swap}-block d2h/h2d",
+            "copy_ms": round(ms, 3), "copy_GBps": round(byts / (ms * 1e-3) / 1e9, 1),
+            "d2h_GBps": round(n_swap * mover.item_bytes / d2h / 1e9, 1),
+            "h2d_GBps": round(n_swap * mover.item_bytes / h2d / 1e9, 1)}
+
+
+def run_copy(args, torch):
+    """Calibration: a plain contiguous device copy of known size (the
+    block-copy kernel moving 512 x 256 KiB blocks = 128 MiB read + 128 MiB
+    written), to scale rocprof's FETCH_SIZE / WRITE_SIZE readings."""
+    from nanovllm_amd.engine.kv_runner import BlockMover
+    dev = torch.device("cuda:0")
+    pool = torch.zeros(1, 1, 1024, 256, 4, 128, device=dev, dtype=torch.bfloat16)
+    mover = BlockMover(pool)
+    src, dst = list(range(512)), list(range(512, 1024))
+    for _ in range(args.warmup):
+        mover.copy(src, dst)
+    timer = EventTimer(torch)
+    for _ in range(args.steps):
+        s = timer.start()
+        mover.copy(src, dst)
+        timer.stop(s)
+    torch.cuda.synchronize()
+    ms = timer.mean_ms()
+    nbytes = 512 * mover.item_bytes
+    return {"workload": "calibration copy: 512 contiguous 256 KiB blocks (128 MiB read + 128 MiB "
+                        "write) per launch", "read_bytes": nbytes, "write_bytes": nbytes,
+            "ms": round(ms, 4), "GBps": round(2 * nbytes / (ms * 1e-3) / 1e9, 1)}
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on exactly one GPU; --gpus {args.gpus} is not supported "
+              f"(the paged KV path has no cross-GPU exchange to measure)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs an MI355X (no GPU visible)", file=sys.stderr)
+        sys.exit(2)
+    torch.cuda.set_device(0)
+    if args.workload in ("decode", "decode-dist", "int8"):
+        res = run_decode(args, torch, dist=args.workload == "decode-dist",
+                         int8=args.workload == "int8")
+    elif args.workload == "mixed":
+        res = run_mixed(args, torch)
+    elif args.workload == "append":
+        res = run_append(args, torch)
+    elif args.workload == "copy":
+        res = run_copy(args, torch)
+    else:
+        res = run_swap(args, torch)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -30,7 +30,7 @@ namespace {
 
 constexpr int kD = 128;
 constexpr int kTile = 32;
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;  // two waves per SIMD
 constexpr int kThreads = 64 * kWaves;
 constexpr int kSideMax = 8;
 constexpr int kPreNCB = 2;  // column blocks per wave in prefill units
@@ -190,6 +190,59 @@ __device__ __forceinline__ void load_scales(Tile<kI8Tok>& t, const float* ksb, c
   }
 }
 
+// Buffer-resource forms of the tile loads.  A resource covers one tile's key
+// rows; a resource with num_records = 0 turns every load into a zero-returning
+// no-op with no memory traffic, which lets the prefetch ring issue its loads
+// unconditionally (no branch, exact waitcnt bookkeeping) past a wave's range.
+constexpr int kBufWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, kBufWord3);
+}
+
+struct TileOffsets {
+  int k[2];      // K row of key half h for this lane: (16h + lm) * tok + lane part
+  int v[8];      // V row of key slot i: key_of_slot(lg, i) * tok + lane part
+};
+
+template <int kEnc>
+__device__ __forceinline__ TileOffsets tile_offsets(int tok, const LaneId& L) {
+  TileOffsets o;
+  const int kpart = (kEnc == kBF16) ? L.lg * 16 : L.lg * 32;
+  const int vpart = (kEnc == kBF16) ? L.lm * 16 : L.lm * 8;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) o.k[h] = (h * 16 + L.lm) * tok + kpart;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o.v[i] = key_of_slot(L.lg, i) * tok + vpart;
+  return o;
+}
+
+__device__ __forceinline__ void load_tile_buf(Tile<kBF16>& t, __amdgpu_buffer_rsrc_t kr,
+                                              __amdgpu_buffer_rsrc_t vr, const TileOffsets& o) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      t.k[h][c] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(kr, o.k[h] + c * 64, 0, 0));
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    t.v[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(vr, o.v[i], 0, 0));
+}
+
+template <int kEnc>
+__device__ __forceinline__ void load_tile_buf_i8(Tile<kEnc>& t, __amdgpu_buffer_rsrc_t kr,
+                                                 __amdgpu_buffer_rsrc_t vr, const TileOffsets& o) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    t.k[h][0] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(kr, o.k[h], 0, 0));
+    t.k[h][1] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(kr, o.k[h] + 16, 0, 0));
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    t.v[i] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(vr, o.v[i], 0, 0));
+}
+
 // ---------------------------------------------------------------------------
 // Operand formation.
 // ---------------------------------------------------------------------------
@@ -217,45 +270,28 @@ __device__ __forceinline__ u32x4_t k_operand_i8(const Tile<kEnc>& t, int h, int 
   return (c & 1) ? i8x8_biased_bf16(w[2], w[3]) : i8x8_biased_bf16(w[0], w[1]);
 }
 
-// V^T operands: va[jj] holds, for MFMA row m = lm (d = 8lm + jj), the 8 keys
-// of the lane's k-slots.  Keys >= valid_end are zeroed (bf16: a poisoned tail
-// must not reach 0 * NaN inside the MFMA).
-__device__ __forceinline__ void v_operands(const Tile<kBF16>& t, u32x4_t (&va)[8], int key0,
-                                           int valid_end, const LaneId& L) {
-  u32x4_t v[8];
-  const bool tail = key0 + kTile > valid_end;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    v[i] = t.v[i];
-    if (tail && key0 + key_of_slot(L.lg, i) >= valid_end) v[i] = u32x4_t{0u, 0u, 0u, 0u};
-  }
-#pragma unroll
-  for (int jj = 0; jj < 8; ++jj) {
-    const uint32_t sel = (jj & 1) ? kPermHiHi : kPermLoLo;
-    const int dw = jj >> 1;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) va[jj][w] = perm(v[2 * w + 1][dw], v[2 * w][dw], sel);
-  }
+// V^T operand for PV MFMA jj: MFMA row m = lm is dim d = 8lm + jj, and the 8
+// bf16 of the operand are that dim of the lane's 8 key slots, picked out of
+// the row vectors with v_perm_b32.
+__device__ __forceinline__ u32x4_t v_operand(const u32x4_t (&v)[8], int jj) {
+  const uint32_t sel = (jj & 1) ? kPermHiHi : kPermLoLo;
+  const int dw = jj >> 1;
+  return u32x4_t{perm(v[1][dw], v[0][dw], sel), perm(v[3][dw], v[2][dw], sel),
+                 perm(v[5][dw], v[4][dw], sel), perm(v[7][dw], v[6][dw], sel)};
 }
 
-template <int kEnc>
-__device__ __forceinline__ void v_operands_i8(const Tile<kEnc>& t, u32x4_t (&va)[8]) {
-  uint32_t w[8][2];
+// int8 form: the codes of dim jj for the 8 key slots, as bf16 of (code + 128).
+// `w` holds the key rows already XOR-ed with 0x80 (code + 128 as unsigned).
+__device__ __forceinline__ u32x4_t v_operand_i8(const uint32_t (&w)[8][2], int jj) {
+  const int dw = jj >> 2, sh = (jj & 3) * 8;
+  u32x4_t r;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    w[i][0] = t.v[i][0] ^ 0x80808080u;
-    w[i][1] = t.v[i][1] ^ 0x80808080u;
+  for (int s = 0; s < 4; ++s) {
+    const float a = float((w[2 * s][dw] >> sh) & 0xffu);
+    const float b = float((w[2 * s + 1][dw] >> sh) & 0xffu);
+    r[s] = perm(__float_as_uint(b), __float_as_uint(a), kPermHiHi);
   }
-#pragma unroll
-  for (int jj = 0; jj < 8; ++jj) {
-    const int dw = jj >> 2, sh = (jj & 3) * 8;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const float a = float((w[2 * s][dw] >> sh) & 0xffu);
-      const float b = float((w[2 * s + 1][dw] >> sh) & 0xffu);
-      va[jj][s] = perm(__float_as_uint(b), __float_as_uint(a), kPermHiHi);
-    }
-  }
+  return r;
 }
 
 // ---------------------------------------------------------------------------
@@ -333,37 +369,50 @@ __device__ __forceinline__ void build_q(QOps<kEnc, NCB>& Q, const AttnParams& p,
 // ---------------------------------------------------------------------------
 // One 32-key tile against NCB column blocks.
 //   key0       absolute index of the tile's first key
-//   valid_end  keys >= valid_end do not exist (masked and zeroed)
-//   slot0      pool slot of the tile's first key (side pool rows; -1 if none)
+//   valid_end  keys >= valid_end do not exist (masked; bf16 V rows zeroed so a
+//              poisoned tail never reaches 0 * NaN inside the MFMA)
+//   slot0      pool slot of the tile's first key (side pool rows)
+// kMasked = false is the fast path for tiles whose 32 keys are all visible to
+// every valid column (all but the last tile of a decode row).
 // ---------------------------------------------------------------------------
-template <int kEnc, int NCB>
+template <int kEnc, int NCB, bool kMasked>
 __device__ __forceinline__ void attend_tile(ColState<NCB>& st, const Tile<kEnc>& t,
                                             const QOps<kEnc, NCB>& Q, const ColInfo (&ci)[NCB],
                                             int key0, int valid_end, int64_t slot0,
                                             const AttnParams& p, int g, const LaneId& L) {
-  u32x4_t ka[2][4];
+  bool kvalid[8];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
+  for (int i = 0; i < 8; ++i) kvalid[i] = !kMasked || (key0 + key_of_slot(L.lg, i) < valid_end);
+
+  // V rows as the PV operands will read them.
+  u32x4_t vrow[8];
+  uint32_t vq[8][2];
+  if constexpr (kEnc == kBF16) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
+    for (int i = 0; i < 8; ++i) {
+      vrow[i] = t.v[i];
+      if (kMasked && !kvalid[i]) vrow[i] = u32x4_t{0u, 0u, 0u, 0u};
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      vq[i][0] = t.v[i][0] ^ 0x80808080u;
+      vq[i][1] = t.v[i][1] ^ 0x80808080u;
+    }
+  }
+  // With several column blocks the V operands are formed once per tile.
+  u32x4_t va[NCB > 1 ? 8 : 1];
+  if constexpr (NCB > 1) {
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
       if constexpr (kEnc == kBF16) {
-        ka[h][c] = k_operand(t, h, c);
+        va[jj] = v_operand(vrow, jj);
       } else {
-        ka[h][c] = k_operand_i8(t, h, c);
+        va[jj] = v_operand_i8(vq, jj);
       }
     }
   }
-  u32x4_t va[8];
-  if constexpr (kEnc == kBF16) {
-    v_operands(t, va, key0, valid_end, L);
-  } else {
-    v_operands_i8(t, va);
-  }
-  bool kvalid[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) kvalid[i] = key0 + key_of_slot(L.lg, i) < valid_end;
 
-  // Side-pool rows of the lane's keys (per-channel int8 with outlier dims).
   int n_out = 0;
   if constexpr (kEnc == kI8Chan) {
     if (p.head_n_out != nullptr) n_out = p.head_n_out[g];
@@ -374,11 +423,19 @@ __device__ __forceinline__ void attend_tile(ColState<NCB>& st, const Tile<kEnc>&
     f32x4_t s0 = f32x4_t{0.f, 0.f, 0.f, 0.f}, s1 = s0;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      s0 = mfma_bf16(ka[0][c], Q.op[cb][c], s0);
-      s1 = mfma_bf16(ka[1][c], Q.op[cb][c], s1);
+      u32x4_t k0, k1;
+      if constexpr (kEnc == kBF16) {
+        k0 = k_operand(t, 0, c);
+        k1 = k_operand(t, 1, c);
+      } else {
+        k0 = k_operand_i8(t, 0, c);
+        k1 = k_operand_i8(t, 1, c);
+      }
+      s0 = mfma_bf16(k0, Q.op[cb][c], s0);
+      s1 = mfma_bf16(k1, Q.op[cb][c], s1);
       if constexpr (kEnc == kI8Chan) {
-        s0 = mfma_bf16(ka[0][c], Q.lo[cb][c], s0);
-        s1 = mfma_bf16(ka[1][c], Q.lo[cb][c], s1);
+        s0 = mfma_bf16(k0, Q.lo[cb][c], s0);
+        s1 = mfma_bf16(k1, Q.lo[cb][c], s1);
       }
     }
     float x[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
@@ -408,8 +465,12 @@ __device__ __forceinline__ void attend_tile(ColState<NCB>& st, const Tile<kEnc>&
     float tmax = -INFINITY;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const bool ok = kvalid[i] && (key0 + key_of_slot(L.lg, i) <= ci[cb].klim);
-      x[i] = ok ? x[i] * p.scale_log2 : -INFINITY;
+      if constexpr (kMasked) {
+        const bool ok = kvalid[i] && (key0 + key_of_slot(L.lg, i) <= ci[cb].klim);
+        x[i] = ok ? x[i] * p.scale_log2 : -INFINITY;
+      } else {
+        x[i] *= p.scale_log2;
+      }
       tmax = fmaxf(tmax, x[i]);
     }
     tmax = fmaxf(tmax, shfl_xor(tmax, 16));
@@ -461,13 +522,35 @@ __device__ __forceinline__ void attend_tile(ColState<NCB>& st, const Tile<kEnc>&
     }
 #pragma unroll
     for (int jj = 0; jj < 8; ++jj) {
+      u32x4_t a;
+      if constexpr (NCB > 1) {
+        a = va[jj];
+      } else if constexpr (kEnc == kBF16) {
+        a = v_operand(vrow, jj);
+      } else {
+        a = v_operand_i8(vq, jj);
+      }
       f32x4_t o = st.o[cb][jj];
       o[0] *= alpha;
       o[1] *= alpha;
       o[2] *= alpha;
       o[3] *= alpha;
-      st.o[cb][jj] = mfma_bf16(va[jj], pb, o);
+      st.o[cb][jj] = mfma_bf16(a, pb, o);
     }
+  }
+}
+
+// Full tiles take the unmasked path; a tile with a key at or past valid_end,
+// or past some valid column's limit, takes the masked one.
+template <int kEnc, int NCB>
+__device__ __forceinline__ void attend(ColState<NCB>& st, const Tile<kEnc>& t,
+                                       const QOps<kEnc, NCB>& Q, const ColInfo (&ci)[NCB],
+                                       int key0, int valid_end, int min_klim, int64_t slot0,
+                                       const AttnParams& p, int g, const LaneId& L) {
+  if (key0 + kTile <= valid_end && key0 + kTile - 1 <= min_klim) {
+    attend_tile<kEnc, NCB, false>(st, t, Q, ci, key0, valid_end, slot0, p, g, L);
+  } else {
+    attend_tile<kEnc, NCB, true>(st, t, Q, ci, key0, valid_end, slot0, p, g, L);
   }
 }
 
@@ -569,7 +652,7 @@ constexpr int kSmemBytes = kDecodeSmem > kPrefillSmem ? kDecodeSmem : kPrefillSm
 template <int kEnc>
 __device__ void decode_unit(const AttnParams& p, char* smem, int b, int kvs, int chunk) {
   const LaneId L = lane_id();
-  const int wave = threadIdx.x >> 6;
+  const int wave = uniform(int(threadIdx.x >> 6));  // wave-uniform (scalar) index
   const int g = kvs / p.nslices;
   const int s = kvs - g * p.nslices;
   const int hs = min(p.hs, p.group - s * p.hs);
@@ -594,18 +677,23 @@ __device__ void decode_unit(const AttnParams& p, char* smem, int b, int kvs, int
 
   const int32_t* bt = p.block_tables + int64_t(b) * p.bt_stride;
   const int64_t head_off = int64_t(g) * ((kEnc == kBF16) ? kD * 2 : kD);
+  const int tok = int(p.tok_bytes);
+  const int span = kTile * tok;
+  const TileOffsets off = tile_offsets<kEnc>(tok, L);
   auto tile_slot0 = [&](int tix) -> int64_t {
     const int key0 = c0 + tix * kTile;
     const int blk = uniform(bt[key0 / p.page]);
     return int64_t(blk) * p.page + (key0 % p.page);
   };
-  auto load = [&](Tile<kEnc>& t, int64_t slot0) {
+  // live == false turns the tile's loads into no-ops (num_records = 0).
+  auto load = [&](Tile<kEnc>& t, int64_t slot0, bool live) {
     const char* kb = p.k_cache + slot0 * p.tok_bytes + head_off;
     const char* vb = p.v_cache + slot0 * p.tok_bytes + head_off;
+    const int nrec = live ? span : 0;
     if constexpr (kEnc == kBF16) {
-      load_tile_global(t, kb, vb, p.tok_bytes, L);
+      load_tile_buf(t, tile_rsrc(kb, nrec), tile_rsrc(vb, nrec), off);
     } else {
-      load_tile_global_i8<kEnc>(t, kb, vb, p.tok_bytes, L);
+      load_tile_buf_i8<kEnc>(t, tile_rsrc(kb, nrec), tile_rsrc(vb, nrec), off);
     }
     if constexpr (kEnc == kI8Tok) {
       load_scales(t, p.k_scale + slot0 * p.kvh + g, p.v_scale + slot0 * p.kvh + g, p.kvh, L);
@@ -613,22 +701,29 @@ __device__ void decode_unit(const AttnParams& p, char* smem, int b, int kvs, int
   };
 
   if (t_begin < t_end) {
-    Tile<kEnc> ta, tb;
-    int64_t sa = tile_slot0(t_begin), sb = 0;
-    load(ta, sa);
-    for (int tix = t_begin; tix < t_end; tix += 2) {
-      const bool has_b = tix + 1 < t_end;
-      if (has_b) {
-        sb = tile_slot0(tix + 1);
-        load(tb, sb);
+    // Ring of kRing tile buffers: tile t is computed from buffer t % kRing
+    // while the next kRing - 1 tiles are in flight; the buffer is refilled
+    // with tile t + kRing right after.  With two waves per SIMD this keeps
+    // 32-64 KiB of KV reads in flight per SIMD.
+    constexpr int kRing = 2;
+    Tile<kEnc> ring[kRing];
+    int64_t slot[kRing];
+#pragma unroll
+    for (int r = 0; r < kRing; ++r) {
+      const int tix = t_begin + r;
+      slot[r] = tile_slot0(min(tix, t_end - 1));
+      load(ring[r], slot[r], tix < t_end);
+    }
+    for (int t0 = t_begin; t0 < t_end; t0 += kRing) {
+#pragma unroll
+      for (int r = 0; r < kRing; ++r) {
+        const int tix = t0 + r;
+        if (tix < t_end)
+          attend<kEnc, 1>(st, ring[r], Q, ci, c0 + tix * kTile, ctx, ctx - 1, slot[r], p, g, L);
+        const int nxt = tix + kRing;
+        slot[r] = tile_slot0(min(nxt, t_end - 1));
+        load(ring[r], slot[r], nxt < t_end);
       }
-      attend_tile<kEnc, 1>(st, ta, Q, ci, c0 + tix * kTile, ctx, sa, p, g, L);
-      if (!has_b) break;
-      if (tix + 2 < t_end) {
-        sa = tile_slot0(tix + 2);
-        load(ta, sa);
-      }
-      attend_tile<kEnc, 1>(st, tb, Q, ci, c0 + (tix + 1) * kTile, ctx, sb, p, g, L);
     }
   }
 
@@ -669,7 +764,7 @@ __device__ void decode_unit(const AttnParams& p, char* smem, int b, int kvs, int
 template <int kEnc, bool kFresh>
 __device__ void prefill_unit(const AttnParams& p, char* smem, int i, int qt, int kvs, int split) {
   const LaneId L = lane_id();
-  const int wave = threadIdx.x >> 6;
+  const int wave = uniform(int(threadIdx.x >> 6));  // wave-uniform (scalar) index
   const int g = kvs / p.nslices;
   const int s = kvs - g * p.nslices;
   const int hs = min(p.hs, p.group - s * p.hs);
@@ -697,6 +792,14 @@ __device__ void prefill_unit(const AttnParams& p, char* smem, int i, int qt, int
   build_q<kEnc, kPreNCB>(Q, p, ci, g, L);
   ColState<kPreNCB> st;
   init_state(st);
+  // Smallest key limit over the wave's valid columns: tiles entirely below it
+  // need no causal mask.
+  int min_klim = 0x7fffffff;
+#pragma unroll
+  for (int cb = 0; cb < kPreNCB; ++cb)
+    if (ci[cb].valid) min_klim = min(min_klim, ci[cb].klim);
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) min_klim = min(min_klim, __shfl_xor(min_klim, m, 64));
 
   // Key range of this split, cut at the last key any column of the tile sees.
   const int last_q = min(q0 + qtile_tokens, sq) - 1;
@@ -825,8 +928,8 @@ __device__ void prefill_unit(const AttnParams& p, char* smem, int i, int qt, int
       }
       Tile<kEnc> t;
       read_tile(t, buf);
-      attend_tile<kEnc, kPreNCB>(st, t, Q, ci, k_begin + tix * kTile, sk, kFresh ? -1 : slot_cur,
-                                 p, g, L);
+      attend<kEnc, kPreNCB>(st, t, Q, ci, k_begin + tix * kTile, sk, min_klim,
+                            kFresh ? -1 : slot_cur, p, g, L);
       if (has_next) commit(buf ^ 1);
       __syncthreads();
       slot_cur = slot_next;
@@ -977,15 +1080,35 @@ int env_int(const char* name, int fallback) {
   return atoi(v);
 }
 
-// Keys per decode chunk: the largest power of two in [128, 4096] that still
-// gives at least ~4 workgroups per CU (1024) for this batch; KVC_DECODE_CHUNK
-// overrides it (multiple of 128).
+// Compute units of the current device (cached per device).
+int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+// Keys per decode chunk.  A decode workgroup holds one wave per SIMD for the
+// whole chunk and keeps several tiles in flight per wave, so the plan aims at
+// about one workgroup per CU: (rows x kv slices) units are split into just
+// enough chunks to reach the CU count.  KVC_DECODE_CHUNK overrides it (a
+// multiple of 32).
 int plan_decode_chunk(int64_t rows, int64_t kvslices, int64_t max_ctx) {
   const int forced = env_int("KVC_DECODE_CHUNK", 0);
   if (forced > 0) return forced;
-  int ch = 4096;
-  while (ch > 128 && rows * kvslices * ((max_ctx + ch - 1) / ch) < 1024) ch >>= 1;
-  return ch;
+  const int64_t units = rows * kvslices;
+  const int64_t cus = device_cus();
+  int64_t nch = units >= cus ? 1 : (cus + units - 1) / units;
+  int64_t ch = (max_ctx + nch - 1) / nch;
+  ch = ((ch + 127) / 128) * 128;
+  return int(ch < 128 ? 128 : ch);
 }
 
 // Keys per prefill split: a quarter of the longest key range, at least 512.

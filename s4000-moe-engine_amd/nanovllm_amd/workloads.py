@@ -81,28 +81,34 @@ def decode_workload(batch: int, num_heads: int, num_kv_heads: int, num_blocks: i
     new_k = _randn((batch, num_kv_heads, HEAD_DIM), gen)
     new_v = _randn((batch, num_kv_heads, HEAD_DIM), gen)
     shape = (num_blocks, page, num_kv_heads, HEAD_DIM)
+    sshape = (num_blocks, page, num_kv_heads)
+    k_scale = v_scale = None
     if pool_device_fill:
         dgen = torch.Generator(device=device).manual_seed(seed + 1)
-        k_cache = torch.randn(shape, generator=dgen, device=device, dtype=torch.bfloat16)
-        v_cache = torch.randn(shape, generator=dgen, device=device, dtype=torch.bfloat16)
-        if fill_std != 1.0:
-            k_cache.mul_(fill_std)
-            v_cache.mul_(fill_std)
+        if kv_dtype == "int8_tokhead":
+            k_cache = torch.randint(-127, 128, shape, generator=dgen, device=device, dtype=torch.int8)
+            v_cache = torch.randint(-127, 128, shape, generator=dgen, device=device, dtype=torch.int8)
+            k_scale = torch.rand(sshape, generator=dgen, device=device) * 0.03 + 0.005
+            v_scale = torch.rand(sshape, generator=dgen, device=device) * 0.03 + 0.005
+        else:
+            k_cache = torch.randn(shape, generator=dgen, device=device, dtype=torch.bfloat16)
+            v_cache = torch.randn(shape, generator=dgen, device=device, dtype=torch.bfloat16)
+            if fill_std != 1.0:
+                k_cache.mul_(fill_std)
+                v_cache.mul_(fill_std)
+    elif kv_dtype == "int8_tokhead":
+        k_cache = torch.randint(-127, 128, shape, generator=gen, dtype=torch.int8).to(device)
+        v_cache = torch.randint(-127, 128, shape, generator=gen, dtype=torch.int8).to(device)
+        k_scale = (torch.rand(sshape, generator=gen) * 0.03 + 0.005).to(device)
+        v_scale = (torch.rand(sshape, generator=gen) * 0.03 + 0.005).to(device)
     else:
         k_cache = _randn(shape, gen, std=fill_std).to(device)
         v_cache = _randn(shape, gen, std=fill_std).to(device)
-    wl = DecodeWorkload(
+    return DecodeWorkload(
         q=q.to(device), k_cache=k_cache, v_cache=v_cache, block_tables=bt.to(device),
         context_lens=torch.tensor(context_lens, dtype=torch.int32).to(device),
         slot_mapping=slots.to(device), new_k=new_k.to(device), new_v=new_v.to(device),
-        scale=HEAD_DIM ** -0.5)
-    if kv_dtype == "int8_tokhead":
-        wl.k_cache = torch.randint(-127, 128, shape, generator=gen, dtype=torch.int8).to(device)
-        wl.v_cache = torch.randint(-127, 128, shape, generator=gen, dtype=torch.int8).to(device)
-        sshape = (num_blocks, page, num_kv_heads)
-        wl.k_scale = (torch.rand(sshape, generator=gen) * 0.03 + 0.005).to(device)
-        wl.v_scale = (torch.rand(sshape, generator=gen) * 0.03 + 0.005).to(device)
-    return wl
+        scale=HEAD_DIM ** -0.5, k_scale=k_scale, v_scale=v_scale)
 
 
 def uniform_lengths(batch: int, lo: int, hi: int, seed: int) -> list[int]:
