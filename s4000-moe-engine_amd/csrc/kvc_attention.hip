@@ -114,8 +114,7 @@ template <>
 struct Tile<kI8Tok> {
   u32x4_t k[2][2];
   u32x2_t v[8];
-  float ks[8];
-  float vs[8];
+  float sc;  // lane l < 32: K scale of key l; lane 32 + l: V scale of key l
 };
 
 template <>
@@ -148,46 +147,28 @@ __device__ __forceinline__ void init_state(ColState<NCB>& st) {
 }
 
 // ---------------------------------------------------------------------------
-// Tile loads from a paged pool in HBM (decode units).  `base` points at the
-// tile's first key, head g, dim 0; `tok` is the slot stride in bytes.
+// Tile loads from a paged pool in HBM (decode units).  Every load goes
+// through a buffer resource covering the tile's 32 key rows.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void load_tile_global(Tile<kBF16>& t, const char* kb, const char* vb,
-                                                 int64_t tok, const LaneId& L) {
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const char* row = kb + int64_t(h * 16 + L.lm) * tok + L.lg * 16;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) t.k[h][c] = *reinterpret_cast<const u32x4_t*>(row + c * 64);
-  }
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-    t.v[i] = *reinterpret_cast<const u32x4_t*>(vb + int64_t(key_of_slot(L.lg, i)) * tok + L.lm * 16);
-}
-
-template <int kEnc>
-__device__ __forceinline__ void load_tile_global_i8(Tile<kEnc>& t, const char* kb, const char* vb,
-                                                    int64_t tok, const LaneId& L) {
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const char* row = kb + int64_t(h * 16 + L.lm) * tok + L.lg * 32;
-    t.k[h][0] = *reinterpret_cast<const u32x4_t*>(row);
-    t.k[h][1] = *reinterpret_cast<const u32x4_t*>(row + 16);
-  }
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-    t.v[i] = *reinterpret_cast<const u32x2_t*>(vb + int64_t(key_of_slot(L.lg, i)) * tok + L.lm * 8);
-}
-
-// Scales of the lane's 8 key slots (per-token-head int8).  `sbase` points at
-// the scale of the tile's first key for head g; consecutive keys are kvh apart.
-__device__ __forceinline__ void load_scales(Tile<kI8Tok>& t, const float* ksb, const float* vsb,
-                                            int kvh, const LaneId& L) {
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int64_t o = int64_t(key_of_slot(L.lg, i)) * kvh;
-    t.ks[i] = ksb[o];
-    t.vs[i] = vsb[o];
-  }
+// Scales of a tile (per-token-head int8): lane l < 32 holds the K scale of
+// key l, lane 32 + l the V scale of key l, for kv head g.  Both loads use
+// buffer resources, so out-of-range lanes read 0 and `live` = false costs no
+// memory traffic.
+__device__ __forceinline__ float load_scales_buf(const float* ksb, const float* vsb, int kvh,
+                                                 int g, bool live, const LaneId& L) {
+  const int bytes = live ? kTile * kvh * 4 : 0;
+  const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(ksb), 0, bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(vsb), 0, bytes, 0x00020000);
+  const int key = L.lane & (kTile - 1);
+  const int off = (key * kvh + g) * 4;
+  const int big = 0x40000000;  // past num_records: reads 0
+  const float a = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                kr, L.lane < kTile ? off : big, 0, 0));
+  const float b = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                vr, L.lane < kTile ? big : off, 0, 0));
+  return a + b;
 }
 
 // Buffer-resource forms of the tile loads.  A resource covers one tile's key
@@ -195,6 +176,10 @@ __device__ __forceinline__ void load_scales(Tile<kI8Tok>& t, const float* ksb, c
 // no-op with no memory traffic, which lets the prefetch ring issue its loads
 // unconditionally (no branch, exact waitcnt bookkeeping) past a wave's range.
 constexpr int kBufWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format
+// Cache policy of the decode KV reads: non-temporal (gfx94x/gfx950 NT bit).
+// Each KV byte is read once per layer per step, so it is streamed past the
+// caches instead of evicting the block tables and queries.
+constexpr int kStreamCPol = 2;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, int bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, kBufWord3);
@@ -223,11 +208,11 @@ __device__ __forceinline__ void load_tile_buf(Tile<kBF16>& t, __amdgpu_buffer_rs
   for (int h = 0; h < 2; ++h) {
 #pragma unroll
     for (int c = 0; c < 4; ++c)
-      t.k[h][c] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(kr, o.k[h] + c * 64, 0, 0));
+      t.k[h][c] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(kr, o.k[h] + c * 64, 0, kStreamCPol));
   }
 #pragma unroll
   for (int i = 0; i < 8; ++i)
-    t.v[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(vr, o.v[i], 0, 0));
+    t.v[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(vr, o.v[i], 0, kStreamCPol));
 }
 
 template <int kEnc>
@@ -235,12 +220,12 @@ __device__ __forceinline__ void load_tile_buf_i8(Tile<kEnc>& t, __amdgpu_buffer_
                                                  __amdgpu_buffer_rsrc_t vr, const TileOffsets& o) {
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    t.k[h][0] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(kr, o.k[h], 0, 0));
-    t.k[h][1] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(kr, o.k[h] + 16, 0, 0));
+    t.k[h][0] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(kr, o.k[h], 0, kStreamCPol));
+    t.k[h][1] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(kr, o.k[h] + 16, 0, kStreamCPol));
   }
 #pragma unroll
   for (int i = 0; i < 8; ++i)
-    t.v[i] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(vr, o.v[i], 0, 0));
+    t.v[i] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(vr, o.v[i], 0, kStreamCPol));
 }
 
 // ---------------------------------------------------------------------------
@@ -446,7 +431,7 @@ __device__ __forceinline__ void attend_tile(ColState<NCB>& st, const Tile<kEnc>&
     }
     if constexpr (kEnc == kI8Tok) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) x[i] *= t.ks[i];
+      for (int i = 0; i < 8; ++i) x[i] *= __shfl(t.sc, key_of_slot(L.lg, i), 64);
     }
     if constexpr (kEnc == kI8Chan) {
       if (n_out > 0) {
@@ -491,7 +476,8 @@ __device__ __forceinline__ void attend_tile(ColState<NCB>& st, const Tile<kEnc>&
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       if constexpr (kEnc == kI8Tok) {
-        pv[i] = kvalid[i] ? pr[i] * t.vs[i] : 0.f;
+        const float vsc = __shfl(t.sc, kTile + key_of_slot(L.lg, i), 64);
+        pv[i] = kvalid[i] ? pr[i] * vsc : 0.f;
       } else {
         pv[i] = pr[i];
       }
@@ -662,8 +648,10 @@ __device__ void decode_unit(const AttnParams& p, char* smem, int b, int kvs, int
   const int c0 = chunk * p.chunk_tokens;
   const int c1 = min(c0 + p.chunk_tokens, ctx);
   const int ntiles = c1 > c0 ? (c1 - c0 + kTile - 1) / kTile : 0;
-  const int t_begin = (wave * ntiles) / kWaves;
-  const int t_end = ((wave + 1) * ntiles) / kWaves;
+  // Tiles are dealt round-robin (wave w takes w, w + 8, ...): at any moment
+  // the workgroup reads eight consecutive tiles, one contiguous stretch of
+  // the page, instead of eight separate streams.
+  const int my_tiles = ntiles > wave ? (ntiles - wave + kWaves - 1) / kWaves : 0;
 
   ColInfo ci[1];
   ci[0].row = b;
@@ -680,6 +668,8 @@ __device__ void decode_unit(const AttnParams& p, char* smem, int b, int kvs, int
   const int tok = int(p.tok_bytes);
   const int span = kTile * tok;
   const TileOffsets off = tile_offsets<kEnc>(tok, L);
+  // j-th tile of this wave -> chunk-relative tile index
+  auto tile_of = [&](int j) { return wave + j * kWaves; };
   auto tile_slot0 = [&](int tix) -> int64_t {
     const int key0 = c0 + tix * kTile;
     const int blk = uniform(bt[key0 / p.page]);
@@ -696,33 +686,34 @@ __device__ void decode_unit(const AttnParams& p, char* smem, int b, int kvs, int
       load_tile_buf_i8<kEnc>(t, tile_rsrc(kb, nrec), tile_rsrc(vb, nrec), off);
     }
     if constexpr (kEnc == kI8Tok) {
-      load_scales(t, p.k_scale + slot0 * p.kvh + g, p.v_scale + slot0 * p.kvh + g, p.kvh, L);
+      t.sc = load_scales_buf(p.k_scale + slot0 * p.kvh, p.v_scale + slot0 * p.kvh, p.kvh, g, live,
+                             L);
     }
   };
 
-  if (t_begin < t_end) {
-    // Ring of kRing tile buffers: tile t is computed from buffer t % kRing
+  if (my_tiles > 0) {
+    // Ring of kRing tile buffers: tile j is computed from buffer j % kRing
     // while the next kRing - 1 tiles are in flight; the buffer is refilled
-    // with tile t + kRing right after.  With two waves per SIMD this keeps
+    // with tile j + kRing right after.  With two waves per SIMD this keeps
     // 32-64 KiB of KV reads in flight per SIMD.
     constexpr int kRing = 2;
     Tile<kEnc> ring[kRing];
     int64_t slot[kRing];
 #pragma unroll
     for (int r = 0; r < kRing; ++r) {
-      const int tix = t_begin + r;
-      slot[r] = tile_slot0(min(tix, t_end - 1));
-      load(ring[r], slot[r], tix < t_end);
+      slot[r] = tile_slot0(tile_of(min(r, my_tiles - 1)));
+      load(ring[r], slot[r], r < my_tiles);
     }
-    for (int t0 = t_begin; t0 < t_end; t0 += kRing) {
+    for (int j0 = 0; j0 < my_tiles; j0 += kRing) {
 #pragma unroll
       for (int r = 0; r < kRing; ++r) {
-        const int tix = t0 + r;
-        if (tix < t_end)
-          attend<kEnc, 1>(st, ring[r], Q, ci, c0 + tix * kTile, ctx, ctx - 1, slot[r], p, g, L);
-        const int nxt = tix + kRing;
-        slot[r] = tile_slot0(min(nxt, t_end - 1));
-        load(ring[r], slot[r], nxt < t_end);
+        const int j = j0 + r;
+        if (j < my_tiles)
+          attend<kEnc, 1>(st, ring[r], Q, ci, c0 + tile_of(j) * kTile, ctx, ctx - 1, slot[r], p,
+                          g, L);
+        const int nxt = j + kRing;
+        slot[r] = tile_slot0(tile_of(min(nxt, my_tiles - 1)));
+        load(ring[r], slot[r], nxt < my_tiles);
       }
     }
   }
@@ -903,12 +894,8 @@ __device__ void prefill_unit(const AttnParams& p, char* smem, int i, int qt, int
       for (int ii = 0; ii < 8; ++ii)
         t.v[ii] = *reinterpret_cast<const u32x2_t*>(vb + key_of_slot(L.lg, ii) * kPitch + L.lm * 8);
       if constexpr (kEnc == kI8Tok) {
-        const float* sc = reinterpret_cast<const float*>(kb + 2 * kTileBytesBF16);
-#pragma unroll
-        for (int ii = 0; ii < 8; ++ii) {
-          t.ks[ii] = sc[key_of_slot(L.lg, ii)];
-          t.vs[ii] = sc[kTile + key_of_slot(L.lg, ii)];
-        }
+        // Same lane order as load_scales_buf: K scales then V scales.
+        t.sc = reinterpret_cast<const float*>(kb + 2 * kTileBytesBF16)[L.lane];
       }
     }
   };
