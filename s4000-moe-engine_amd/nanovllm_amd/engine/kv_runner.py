@@ -24,6 +24,7 @@ import numpy as np
 import torch
 
 from .. import _native as nat
+from ..utils.context import set_context
 
 
 class BlockMover:
@@ -238,3 +239,92 @@ class KVCacheRunner:
 
     def compact(self, src_ids, dst_ids) -> None:
         self.mover.copy(src_ids, dst_ids)
+
+    # -- batch preparation (the Context producer) ----------------------------
+    @property
+    def device(self) -> torch.device:
+        return self.kv_cache.device
+
+    def _h2d(self, values, dtype) -> torch.Tensor:
+        return torch.tensor(values, dtype=dtype, pin_memory=True).to(self.device, non_blocking=True)
+
+    def prepare_block_tables(self, seqs) -> torch.Tensor:
+        """int32 [len(seqs), max blocks] padded with -1 (model_runner.py:579-583)."""
+        width = max(len(seq.block_table) for seq in seqs)
+        rows = [seq.block_table + [-1] * (width - len(seq.block_table)) for seq in seqs]
+        return self._h2d(rows, torch.int32)
+
+    def prepare_decode(self, seqs):
+        """One token per sequence at position len - 1 (model_runner.py:676-699):
+        slot = block_table[-1] * block_size + last_block_num_tokens - 1."""
+        input_ids = [seq.last_token for seq in seqs]
+        positions = [len(seq) - 1 for seq in seqs]
+        lens = [len(seq) for seq in seqs]
+        slots = [seq.block_table[-1] * self.block_size + seq.last_block_num_tokens - 1
+                 for seq in seqs]
+        set_context(False, slot_mapping=self._h2d(slots, torch.int32),
+                    context_lens=self._h2d(lens, torch.int32),
+                    block_tables=self.prepare_block_tables(seqs), max_context_len=max(lens))
+        return self._h2d(input_ids, torch.int64), self._h2d(positions, torch.int64)
+
+    def prepare_prefill(self, seqs):
+        return self._prepare_rows(seqs, mixed=False)
+
+    def prepare_mixed(self, seqs):
+        """Decode rows first, then prefill chunks (model_runner.py:587-674);
+        ValueError when the rows are not contiguous decode-first."""
+        return self._prepare_rows(seqs, mixed=True)
+
+    def _prepare_rows(self, seqs, mixed: bool):
+        bs = self.block_size
+        n_dec = 0
+        dec_lens: list[int] = []
+        if mixed:
+            while n_dec < len(seqs) and not seqs[n_dec].is_prefill:
+                dec_lens.append(len(seqs[n_dec]))
+                n_dec += 1
+            if not all(seq.is_prefill for seq in seqs[n_dec:]):
+                raise ValueError("mixed batch rows not contiguous decode-first")
+        input_ids: list[int] = []
+        positions: list[int] = []
+        cu_q, cu_k = [0], [0]
+        max_q = max_k = 0
+        slots: list[int] = []
+        for seq in seqs:
+            start = seq.num_cached_tokens
+            end = start + seq.num_scheduled_tokens
+            if seq.is_prefill:
+                input_ids.extend(seq[start:end])
+                cu_q.append(cu_q[-1] + end - start)
+                cu_k.append(cu_k[-1] + end)
+                max_q, max_k = max(max_q, end - start), max(max_k, end)
+            else:
+                assert end - start == 1
+                input_ids.append(seq.last_token)
+                if not mixed:
+                    dec_lens.append(len(seq))
+                    cu_q.append(cu_q[-1] + 1)
+                    cu_k.append(cu_k[-1] + end)
+                    max_q, max_k = max(max_q, 1), max(max_k, end)
+            positions.extend(range(start, end))
+            if not seq.block_table:
+                continue
+            # slots of positions start .. end-1 through the block table
+            for pos in range(start, end):
+                slots.append(seq.block_table[pos // bs] * bs + pos % bs)
+        block_tables = None
+        if mixed or cu_k[-1] > cu_q[-1]:
+            block_tables = self.prepare_block_tables(seqs)
+        cu_q_t = self._h2d(cu_q, torch.int32)
+        cu_k_t = self._h2d(cu_k, torch.int32)
+        slot_t = self._h2d(slots, torch.int32)
+        if mixed:
+            set_context(True, cu_q_t, cu_k_t, max_q, max_k, slot_t, None, block_tables,
+                        cu_seqlens_q_list=cu_q, cu_seqlens_k_list=cu_k, is_mixed=True,
+                        num_decode_rows=n_dec,
+                        decode_context_lens=self._h2d(dec_lens, torch.int32),
+                        decode_max_context_len=max(dec_lens) if dec_lens else 0)
+        else:
+            set_context(True, cu_q_t, cu_k_t, max_q, max_k, slot_t, None, block_tables,
+                        cu_seqlens_q_list=cu_q, cu_seqlens_k_list=cu_k)
+        return self._h2d(input_ids, torch.int64), self._h2d(positions, torch.int64)

@@ -1,0 +1,291 @@
+"""Pins the CPU oracle (CPU only).
+
+Each oracle function is checked against something other than its own
+formula: hand-computed known answers, closed forms, Python's round() or
+torch's bf16 cast as independent rounding implementations, and float64 torch
+scaled_dot_product_attention as an independent attention routine.  The
+known answers are chosen so that plausible mistakes (half-up instead of
+half-even, amax/128, a missing clamp, a prefix mask off by one, a transposed
+GQA mapping) fail.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import kv_oracle as ko
+
+
+def bf16_bits(x):
+    return ko.torch_bf16_bits(torch.as_tensor(x, dtype=torch.float32).to(torch.bfloat16))
+
+
+# ---------------------------------------------------------------------------
+# bf16 helpers
+# ---------------------------------------------------------------------------
+def test_f32_to_bf16_matches_torch_cast():
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(20000, generator=g) * torch.exp(torch.randn(20000, generator=g) * 8)
+    x[:4] = torch.tensor([0.0, -0.0, float("inf"), float("-inf")])
+    ref = ko.torch_bf16_bits(x.to(torch.bfloat16))
+    assert np.array_equal(ko.f32_to_bf16(x.numpy()), ref)
+    # ties: 1 + 2^-8 sits half-way between two bf16 values -> even (1.0)
+    assert ko.f32_to_bf16(np.float32([1 + 2 ** -8]))[0] == 0x3F80
+    assert ko.f32_to_bf16(np.float32([1 + 3 * 2 ** -8]))[0] == 0x3F82
+
+
+# ---------------------------------------------------------------------------
+# store_kvcache
+# ---------------------------------------------------------------------------
+def test_store_closed_form_and_brute_force():
+    rng = np.random.default_rng(1)
+    N, KVH, D, blocks, page = 37, 3, 8, 5, 16
+    key = rng.integers(0, 2 ** 16, (N, KVH, D), dtype=np.uint16)
+    val = rng.integers(0, 2 ** 16, (N, KVH, D), dtype=np.uint16)
+    kc = rng.integers(0, 2 ** 16, (blocks, page, KVH, D), dtype=np.uint16)
+    vc = kc.copy()
+    slots = rng.permutation(blocks * page)[:N]
+    k0, v0 = kc.copy(), vc.copy()
+    ko.store_kvcache(key, val, kc, vc, slots)
+    flat_k, flat_v = k0.reshape(-1, KVH, D).copy(), v0.reshape(-1, KVH, D).copy()
+    for j, s in enumerate(slots):          # brute force
+        flat_k[s] = key[j]
+        flat_v[s] = val[j]
+    assert np.array_equal(kc.reshape(-1, KVH, D), flat_k)
+    assert np.array_equal(vc.reshape(-1, KVH, D), flat_v)
+    untouched = np.setdiff1d(np.arange(blocks * page), slots)
+    assert np.array_equal(kc.reshape(-1, KVH, D)[untouched], k0.reshape(-1, KVH, D)[untouched])
+
+
+def test_store_negative_slot_is_python_indexing():
+    key = np.arange(2 * 4, dtype=np.uint16).reshape(2, 1, 4)
+    kc = np.zeros((2, 4, 1, 4), dtype=np.uint16)
+    vc = kc.copy()
+    ko.store_kvcache(key, key, kc, vc, np.array([-1, 0]))
+    assert list(kc.reshape(-1, 4)[7]) == [0, 1, 2, 3]
+    assert list(kc.reshape(-1, 4)[0]) == [4, 5, 6, 7]
+
+
+# ---------------------------------------------------------------------------
+# per-token-head int8 (round half to even)
+# ---------------------------------------------------------------------------
+def test_tokhead_known_answers():
+    D = 16
+    row = np.zeros(D, np.float32)
+    row[:9] = [0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5, -126.5, 127.0]   # amax 127 -> s = 1
+    zero = np.zeros(D, np.float32)
+    tiny = np.full(D, 3e-7, np.float32)
+    x = np.stack([row, zero, tiny])[:, None, :]
+    codes, scales = ko.quant_tokhead(bf16_bits(x))
+    assert codes[0, 0, :9].tolist() == [0, 2, 2, 0, -2, -2, 126, -126, 127]
+    assert scales[0, 0] == np.float32(1.0)
+    assert scales[1, 0] == np.float32(np.float32(1e-6) / np.float32(127))   # clamp before /127
+    assert codes[1].max() == 0
+    tiny_b = float(ko.bf16_to_f32(bf16_bits(np.float32(3e-7))))
+    assert codes[2, 0, 0] == round(np.float32(tiny_b) / scales[2, 0])
+
+
+def test_tokhead_matches_python_round_half_even():
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(64, 4, 128, generator=g) * 3
+    xb = ko.torch_bf16_bits(x.to(torch.bfloat16))
+    codes, scales = ko.quant_tokhead(xb)
+    xf = ko.bf16_to_f32(xb)
+    for t in range(0, 64, 9):
+        for h in range(4):
+            amax = max(float(np.abs(xf[t, h]).max()), 1e-6)
+            s = np.float32(np.float32(amax) / np.float32(127.0))
+            assert scales[t, h] == s
+            for d in range(0, 128, 7):
+                q = np.float32(xf[t, h, d]) / s           # fp32 IEEE quotient
+                want = max(-127, min(127, round(float(q))))  # Python round: half to even
+                assert codes[t, h, d] == want
+
+
+def test_tokhead_saturates_and_dequant_roundtrip():
+    x = np.zeros((1, 1, 8), np.float32)
+    x[0, 0, 0] = 5.0
+    codes, scales = ko.quant_tokhead(bf16_bits(x))
+    assert codes[0, 0, 0] == 127 and abs(codes).max() == 127
+    deq = ko.dequant_tokhead(codes, scales)
+    assert ko.bf16_to_f32(deq)[0, 0, 0] == np.float32(5.0)
+
+
+# ---------------------------------------------------------------------------
+# per-channel int8 (floor(x / s + 0.5)) with the outlier side pool
+# ---------------------------------------------------------------------------
+def test_chan_known_answers():
+    x = np.float32([[[0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 200.0, -200.0]]])
+    s = np.ones((1, 8), np.float32)
+    assert ko.quant_chan(bf16_bits(x), s)[0, 0].tolist() == [1, 2, 3, 0, -1, -2, 127, -127]
+
+
+def test_chan_store_outliers_zeroed_and_side_exact():
+    KVH, D, NOUT = 2, 8, 3
+    x = np.float32(np.arange(KVH * D).reshape(1, KVH, D) - 5) / np.float32(4)
+    xb = bf16_bits(x)
+    scale = np.full((KVH, D), np.float32(0.25), np.float32)
+    out_idx = np.array([[6, 1, 0], [3, 0, 0]], np.int32)
+    n_out = np.array([2, 1], np.int32)
+    kc = np.full((1, 4, KVH, D), 99, np.int8)
+    vc = kc.copy()
+    sk = np.zeros((1, 4, KVH, NOUT), np.uint16)
+    sv = sk.copy()
+    ko.store_int8_chan(xb, xb, kc, vc, scale, scale, sk, sv, out_idx, n_out, np.array([2]))
+    expect = np.clip(np.floor(x / 0.25 + 0.5), -127, 127).astype(np.int8)[0]
+    expect[0, [6, 1]] = 0
+    expect[1, [3]] = 0
+    assert np.array_equal(kc[0, 2], expect) and np.array_equal(vc[0, 2], expect)
+    assert sk[0, 2, 0, :2].tolist() == [xb[0, 0, 6], xb[0, 0, 1]] and sk[0, 2, 0, 2] == 0
+    assert sk[0, 2, 1, 0] == xb[0, 1, 3]
+    assert (kc[0, [0, 1, 3]] == 99).all()
+
+
+def test_chan_dequant_against_torch():
+    g = torch.Generator().manual_seed(5)
+    codes = torch.randint(-127, 128, (10, 2, 16), generator=g, dtype=torch.int8)
+    ds = torch.rand(2, 16, generator=g)
+    side = torch.randn(10, 2, 4, generator=g).to(torch.bfloat16)
+    idx = torch.tensor([[3, 7, 0, 0], [15, 0, 0, 0]], dtype=torch.int32)
+    nout = torch.tensor([2, 1], dtype=torch.int32)
+    ref = (codes.float() * ds).to(torch.bfloat16)
+    ref[:, 0, 3] = side[:, 0, 0]
+    ref[:, 0, 7] = side[:, 0, 1]
+    ref[:, 1, 15] = side[:, 1, 0]
+    got = ko.dequant_chan(codes.numpy(), ds.numpy(), ko.torch_bf16_bits(side), idx.numpy(),
+                          nout.numpy())
+    assert np.array_equal(got, ko.torch_bf16_bits(ref))
+
+
+# ---------------------------------------------------------------------------
+# attention references
+# ---------------------------------------------------------------------------
+def _sdpa64(q, k, v, scale, mask=None):
+    """float64 torch SDPA per kv group: q [Sq, H, D], k/v [Sk, KVH, D]."""
+    H, KVH = q.shape[1], k.shape[1]
+    kk = torch.from_numpy(k).double().repeat_interleave(H // KVH, dim=1).transpose(0, 1)
+    vv = torch.from_numpy(v).double().repeat_interleave(H // KVH, dim=1).transpose(0, 1)
+    qq = torch.from_numpy(q).double().transpose(0, 1)
+    m = None if mask is None else torch.from_numpy(mask)[None]
+    o = F.scaled_dot_product_attention(qq, kk, vv, attn_mask=m, scale=scale)
+    return o.transpose(0, 1).numpy()
+
+
+def _paged_case(B, H, KVH, lens, seed, page=16, D=32):
+    rng = np.random.default_rng(seed)
+    nblk = [max(1, math.ceil(n / page)) for n in lens]
+    blocks = sum(nblk) + 2
+    perm = rng.permutation(blocks)
+    bt = -np.ones((B, max(nblk)), np.int64)
+    pos = 0
+    for i, n in enumerate(nblk):
+        bt[i, :n] = perm[pos:pos + n]
+        pos += n
+    q = bf16_bits(rng.standard_normal((B, H, D)).astype(np.float32))
+    k = ko.bf16_to_f32(bf16_bits(rng.standard_normal((blocks, page, KVH, D)).astype(np.float32)))
+    v = ko.bf16_to_f32(bf16_bits(rng.standard_normal((blocks, page, KVH, D)).astype(np.float32)))
+    return q, k, v, bt
+
+
+@pytest.mark.parametrize("H,KVH", [(8, 2), (4, 4), (6, 3)])
+def test_paged_decode_against_float64_sdpa(H, KVH):
+    lens = [1, 15, 16, 17, 40]
+    q, k, v, bt = _paged_case(len(lens), H, KVH, lens, seed=H * 10 + KVH)
+    out = ko.paged_decode_ref(q, k, v, bt, lens, 0.3)
+    for b, n in enumerate(lens):
+        nb = math.ceil(n / 16)
+        kk = k[bt[b, :nb]].reshape(-1, KVH, k.shape[-1])[:n]
+        vv = v[bt[b, :nb]].reshape(-1, KVH, v.shape[-1])[:n]
+        want = _sdpa64(ko.bf16_to_f32(q[b:b + 1]), kk, vv, 0.3)[0]
+        assert np.abs(out[b] - want).max() < 1e-5
+
+
+def test_paged_decode_closed_forms_and_poison():
+    q, k, v, bt = _paged_case(3, 4, 2, [1, 20, 20], seed=9)
+    # identical keys -> uniform softmax -> output is the mean of V
+    blk = bt[1, :2]
+    k[blk] = k[blk][0:1, 0:1]
+    # NaN tail past the context is never read
+    k[bt[2, 1], 4:] = np.nan
+    v[bt[2, 1], 4:] = np.nan
+    out = ko.paged_decode_ref(q, k, v, bt, [1, 20, 20], 0.5)
+    assert np.allclose(out[0, 0], v[bt[0, 0], 0, 0])         # one key -> its V row (GQA head 0)
+    assert np.allclose(out[0, 3], v[bt[0, 0], 0, 1])         # head 3 reads kv head 1
+    vv = v[blk].reshape(-1, 2, v.shape[-1])[:20]
+    assert np.allclose(out[1, 0], vv[:, 0].mean(0), atol=1e-6)
+    assert np.isfinite(out[2]).all()
+    assert np.isnan(ko.paged_decode_ref(q[:1], k, v, bt[:1], [0], 0.5)).all()
+
+
+def test_prefill_prefix_mask_against_sdpa():
+    rng = np.random.default_rng(4)
+    H, KVH, D = 4, 2, 32
+    chunks = [(0, 5), (7, 3), (16, 10)]          # (cached prefix, new queries)
+    lens = [p + c for p, c in chunks]
+    q_all, k, v, bt = _paged_case(len(chunks), H, KVH, lens, seed=4, D=D)
+    T = sum(c for _, c in chunks)
+    q = bf16_bits(rng.standard_normal((T, H, D)).astype(np.float32))
+    cu_q = [0]
+    cu_k = [0]
+    for p, c in chunks:
+        cu_q.append(cu_q[-1] + c)
+        cu_k.append(cu_k[-1] + p + c)
+    out = ko.prefill_ref(q, k, v, bt, cu_q, cu_k, 0.25)
+    for i, (p, c) in enumerate(chunks):
+        sk = p + c
+        nb = math.ceil(sk / 16)
+        kk = k[bt[i, :nb]].reshape(-1, KVH, D)[:sk]
+        vv = v[bt[i, :nb]].reshape(-1, KVH, D)[:sk]
+        mask = np.arange(sk)[None, :] <= (p + np.arange(c))[:, None]
+        want = _sdpa64(ko.bf16_to_f32(q[cu_q[i]:cu_q[i + 1]]), kk, vv, 0.25, mask)
+        assert np.abs(out[cu_q[i]:cu_q[i + 1]] - want).max() < 1e-5
+        if p == 0:   # no prefix: plain causal attention
+            qq = torch.from_numpy(ko.bf16_to_f32(q[cu_q[i]:cu_q[i + 1]])).double().transpose(0, 1)
+            kk2 = torch.from_numpy(kk).double().repeat_interleave(2, 1).transpose(0, 1)
+            vv2 = torch.from_numpy(vv).double().repeat_interleave(2, 1).transpose(0, 1)
+            causal = F.scaled_dot_product_attention(qq, kk2, vv2, is_causal=True, scale=0.25)
+            assert np.abs(out[cu_q[i]:cu_q[i + 1]] - causal.transpose(0, 1).numpy()).max() < 1e-5
+
+
+def test_mixed_is_decode_rows_then_prefill_rows():
+    lens_dec = [9, 30]
+    chunks = [(5, 4)]
+    q, k, v, bt = _paged_case(3, 4, 2, lens_dec + [9], seed=12)
+    rng = np.random.default_rng(1)
+    qq = bf16_bits(rng.standard_normal((2 + 4, 4, 32)).astype(np.float32))
+    out = ko.mixed_ref(qq, k, v, bt, 2, lens_dec, [0, 4], [0, 9], 0.2)
+    dec = ko.paged_decode_ref(qq[:2], k, v, bt[:2], lens_dec, 0.2)
+    pre = ko.prefill_ref(qq[2:], k, v, bt, [0, 4], [0, 9], 0.2, row_offset=2)
+    assert np.array_equal(out, np.concatenate([dec, pre]))
+
+
+def test_gather_sdpa_decode_matches_decode_reference():
+    lens = [5, 16, 33]
+    q, k, v, bt = _paged_case(3, 4, 2, lens, seed=21)
+    kt = torch.from_numpy(k)
+    vt = torch.from_numpy(v)
+    out = ko.gather_sdpa_decode(torch.from_numpy(ko.bf16_to_f32(q)), kt, vt,
+                                torch.from_numpy(bt).to(torch.int32),
+                                torch.tensor(lens), 0.4, max(lens))
+    ref = ko.paged_decode_ref(q, k, v, bt, lens, 0.4)
+    assert np.abs(out.numpy() - ref).max() < 1e-5
+
+
+# ---------------------------------------------------------------------------
+# whole-block movement
+# ---------------------------------------------------------------------------
+def test_block_gather_scatter_roundtrip_and_copy_semantics():
+    rng = np.random.default_rng(7)
+    pool = rng.integers(0, 2 ** 16, (6, 10, 32), dtype=np.uint16)
+    ids = [7, 2, 9]
+    items = ko.block_gather(pool, ids)
+    assert items.shape == (3, 6, 32)
+    assert np.array_equal(items[1], pool[:, 2])
+    dst = pool.copy()
+    ko.block_scatter(dst, [0, 1, 3], items)
+    assert np.array_equal(dst[:, 3], pool[:, 9])
+    chain = pool.copy()
+    ko.block_copy(chain, [1, 2], [2, 3])          # simultaneous: 3 gets the OLD block 2
+    assert np.array_equal(chain[:, 2], pool[:, 1]) and np.array_equal(chain[:, 3], pool[:, 2])
