@@ -40,7 +40,7 @@ def parse_args():
     ap.add_argument("--workload", default="decode",
                     choices=["decode", "decode-dist", "int8", "mixed", "append", "swap", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-sample", type=int, default=8,
+    ap.add_argument("--cpu-sample", type=int, default=64,
                     help="sequences of the workload the CPU baseline runs")
     return ap.parse_args()
 
@@ -106,7 +106,7 @@ def cpu_decode_baseline(torch, wl, sample: int, reps: int = 5):
         "unit": "tokens/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"{b} of the {wl.batch} sequences (same block tables and KV bytes), "
+        "sample": (f"{b} of the {wl.batch} sequences (same q, block tables and KV bytes), "
                    f"torch gather+expand+masked SDPA decode, median of {reps} reps "
                    f"({med * 1e3:.1f} ms, cv {cv:.2f})"),
     }

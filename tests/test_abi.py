@@ -39,13 +39,18 @@ def test_abi_version_and_error_string():
 
 
 def test_workspace_queries_are_host_only():
-    # Pure host arithmetic (no GPU here; the plan assumes 256 CUs): a batch of
-    # 4 at 32k context splits each (sequence, kv head) into several chunks and
-    # needs split-K scratch; 64 x 4 kv heads already fill the CUs with one
-    # chunk each and need none.
-    small_batch = _native.query("kvc_paged_decode_workspace_bytes", 4, 32, 4, 128, 256, 128)
-    assert small_batch > 0
-    assert _native.query("kvc_paged_decode_workspace_bytes", 64, 32, 4, 128, 256, 16) == 0
+    # Pure host arithmetic (no GPU here; the plan assumes 256 CUs).  A decode
+    # workgroup covers every kv head of its sequence, so batch 64 gives 64
+    # units and the context is split into 4 chunks of 1024 keys: the
+    # workspace holds fp32 partials, 128 dims + 1 log-sum-exp per (row, head,
+    # split), plus 256 bytes of slack.
+    q = _native.query
+    assert q("kvc_paged_decode_workspace_bytes", 64, 32, 4, 128, 256, 16) == \
+        64 * 32 * 4 * 129 * 4 + 256
+    # 256 sequences already fill the CUs with one chunk each: no workspace.
+    assert q("kvc_paged_decode_workspace_bytes", 256, 32, 4, 128, 256, 16) == 0
+    # A batch of 4 at 32k context splits into many chunks.
+    assert q("kvc_paged_decode_workspace_bytes", 4, 32, 4, 128, 256, 128) > 0
 
 
 def test_bad_arguments_map_to_python_exceptions():
@@ -57,3 +62,13 @@ def test_bad_arguments_map_to_python_exceptions():
                      0, None)
     with pytest.raises(ValueError):
         _native.call("kvc_block_gather", None, 1, 16, 15, None, 1, None, 16, 16, None)
+
+
+def test_binding_argument_counts_match_the_header():
+    text = re.sub(r"/\*.*?\*/", "", (REPO / "include" / "kvc.h").read_text(), flags=re.S)
+    for name, (_, argtypes) in _native.SIGNATURES.items():
+        m = re.search(r"\b" + name + r"\s*\(([^)]*)\)", text)
+        assert m, name
+        params = m.group(1).strip()
+        n = 0 if params in ("", "void") else params.count(",") + 1
+        assert n == len(argtypes), f"{name}: header has {n} parameters, binding {len(argtypes)}"
