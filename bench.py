@@ -49,29 +49,79 @@ def parse_args():
 # timing helpers
 # ---------------------------------------------------------------------------
 class EventTimer:
-    """Pairs of HIP events on torch's current stream (the stream libkvc launches
-    on); durations are read after the timed region ends."""
+    """Pairs of HIP events recorded on the stream libkvc launches on (torch's
+    current stream), created with hipEventDisableSystemFence so that a record
+    does not add a system-scope cache flush between the kernels it brackets
+    (torch.cuda.Event records one).  Durations are read after the timed
+    region ends.  The events come from the HIP runtime already loaded in the
+    process (the one torch and libkvc share, soname libamdhip64.so.7)."""
+
+    _DISABLE_SYSTEM_FENCE = 0x20000000
 
     def __init__(self, torch):
-        self.torch = torch
+        import ctypes
+        self.ct = ctypes
+        self.hip = ctypes.CDLL("libamdhip64.so.7")
+        self.hip.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p),
+                                                     ctypes.c_uint]
+        self.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float),
+                                                 ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.stream = torch.cuda.current_stream().cuda_stream
         self.pairs = []
 
+    def _record(self):
+        ev = self.ct.c_void_p()
+        rc = self.hip.hipEventCreateWithFlags(self.ct.byref(ev), self._DISABLE_SYSTEM_FENCE)
+        if rc != 0:
+            raise RuntimeError(f"hipEventCreateWithFlags failed ({rc})")
+        rc = self.hip.hipEventRecord(ev, self.stream)
+        if rc != 0:
+            raise RuntimeError(f"hipEventRecord failed ({rc})")
+        return ev
+
     def start(self):
-        e = self.torch.cuda.Event(enable_timing=True)
-        e.record()
-        return e
+        return self._record()
 
     def stop(self, s):
-        e = self.torch.cuda.Event(enable_timing=True)
-        e.record()
-        self.pairs.append((s, e))
+        self.pairs.append((s, self._record()))
 
     def mean_ms(self):
-        return statistics.fmean(s.elapsed_time(e) for s, e in self.pairs)
+        out = []
+        for s, e in self.pairs:
+            self.hip.hipEventSynchronize(e)
+            ms = self.ct.c_float()
+            rc = self.hip.hipEventElapsedTime(self.ct.byref(ms), s, e)
+            if rc != 0:
+                raise RuntimeError(f"hipEventElapsedTime failed ({rc})")
+            out.append(ms.value)
+            self.hip.hipEventDestroy(s)
+            self.hip.hipEventDestroy(e)
+        self.pairs = []
+        return statistics.fmean(out)
 
 
 def cpu_threads():
     return len(os.sched_getaffinity(0))
+
+
+def profiled_traffic(workload: str):
+    """HBM bytes per launch of the dominant kernel for `workload`, from the
+    committed rocprofv3 counter summaries: a line
+    `bench-traffic: <workload> <bytes>` in profiles/*.md (FETCH_SIZE and
+    WRITE_SIZE per dispatch, each scaled by what the counter reads for a copy
+    kernel of known size).  None when no summary covers the workload."""
+    import glob
+    import re
+    for path in sorted(glob.glob(os.path.join(REPO, "profiles", "*.md"))):
+        with open(path) as f:
+            for line in f:
+                m = re.match(r"\s*bench-traffic:\s*(\S+)\s+(\d+)", line)
+                if m and m.group(1) == workload:
+                    return int(m.group(2))
+    return None
 
 
 # ---------------------------------------------------------------------------
@@ -195,7 +245,7 @@ def run_decode(args, torch, dist: bool, int8: bool = False):
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": profiled_traffic(args.workload),
         },
     }
     if not args.no_cpu_baseline:
