@@ -80,6 +80,11 @@ struct AttnParams {
   float* part_o;
   float* part_lse;
   int max_splits;
+  // Stream-K decode (paged decode launches): each workgroup takes an equal
+  // share (at least sk_min_share) of the tiles of all rows; sk_nseg[r] gets
+  // the number of workgroups that row unit r (= row * groups + group) spans.
+  int sk_min_share;
+  int* sk_nseg;
 };
 
 struct LaneId {
@@ -115,7 +120,11 @@ template <>
 struct Tile<kI8Tok> {
   u32x4_t k[2][2];
   u32x2_t v[8];
-  float sc;  // lane l < 32: K scale of key l; lane 32 + l: V scale of key l
+  // Scales: lane l < 32 holds the K scale of key l in sck, lane 32 + l the V
+  // scale of key l in scv, the other field 0.  They are only added when the
+  // tile is attended: an add at load time would make the prefetch of the
+  // next tile wait for its own loads.
+  float sck, scv;
 };
 
 template <>
@@ -151,12 +160,13 @@ __device__ __forceinline__ void init_state(ColState<NCB>& st) {
 // Tile loads from a paged pool in HBM (decode units).  Every load goes
 // through a buffer resource covering the tile's 32 key rows.
 // ---------------------------------------------------------------------------
-// Scales of a tile (per-token-head int8): lane l < 32 holds the K scale of
+// Scales of a tile (per-token-head int8): lane l < 32 loads the K scale of
 // key l, lane 32 + l the V scale of key l, for kv head g.  Both loads use
 // buffer resources, so out-of-range lanes read 0 and `live` = false costs no
 // memory traffic.
-__device__ __forceinline__ float load_scales_buf(const float* ksb, const float* vsb, int kvh,
-                                                 int g, bool live, const LaneId& L) {
+__device__ __forceinline__ void load_scales_buf(const float* ksb, const float* vsb, int kvh, int g,
+                                                bool live, const LaneId& L, float& sck,
+                                                float& scv) {
   const int bytes = live ? kTile * kvh * 4 : 0;
   const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<float*>(ksb), 0, bytes, 0x00020000);
@@ -165,11 +175,10 @@ __device__ __forceinline__ float load_scales_buf(const float* ksb, const float* 
   const int key = L.lane & (kTile - 1);
   const int off = (key * kvh + g) * 4;
   const int big = 0x40000000;  // past num_records: reads 0
-  const float a = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                                kr, L.lane < kTile ? off : big, 0, 0));
-  const float b = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                                vr, L.lane < kTile ? big : off, 0, 0));
-  return a + b;
+  sck = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                      kr, L.lane < kTile ? off : big, 0, 0));
+  scv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                      vr, L.lane < kTile ? big : off, 0, 0));
 }
 
 // Buffer-resource forms of the tile loads.  A resource covers one tile's key
@@ -432,7 +441,7 @@ __device__ __forceinline__ void attend_tile(ColState<NCB>& st, const Tile<kEnc>&
     }
     if constexpr (kEnc == kI8Tok) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) x[i] *= __shfl(t.sc, key_of_slot(L.lg, i), 64);
+      for (int i = 0; i < 8; ++i) x[i] *= __shfl(t.sck + t.scv, key_of_slot(L.lg, i), 64);
     }
     if constexpr (kEnc == kI8Chan) {
       if (n_out > 0) {
@@ -477,7 +486,7 @@ __device__ __forceinline__ void attend_tile(ColState<NCB>& st, const Tile<kEnc>&
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       if constexpr (kEnc == kI8Tok) {
-        const float vsc = __shfl(t.sc, kTile + key_of_slot(L.lg, i), 64);
+        const float vsc = __shfl(t.sck + t.scv, kTile + key_of_slot(L.lg, i), 64);
         pv[i] = kvalid[i] ? pr[i] * vsc : 0.f;
       } else {
         pv[i] = pr[i];
@@ -663,18 +672,22 @@ constexpr int kPrefillSmem = 2 * kPrefillStage;
 constexpr int kSmemBytes = kDecodeSmem > kPrefillSmem ? kDecodeSmem : kPrefillSmem;
 
 // ---------------------------------------------------------------------------
-// Decode unit: (row b, group of kv slices, key chunk).  A kv slice is one kv
-// head (or a 16-head slice of a group wider than 16 q heads).  The workgroup
-// covers p.kvs_per_wg slices: wave w serves slice w % kvs_per_wg and takes
-// every streams-th tile of the chunk (streams = 8 / kvs_per_wg).  With the
-// engine's layout a token row holds every kv head contiguously
-// ([page, KVH, D]), so the waves of one workgroup read whole token rows
-// (KVH x 256 B) together instead of 256-byte slivers at a KVH x 256-byte
-// stride; the streaming read rate of the first pattern is measured ~13 %
-// higher on MI355X.  Waves of the same slice merge through LDS.
+// Decode segment: 32-key tiles [t0, t1) of row b's context for a group of kv
+// slices.  A kv slice is one kv head (or a 16-head slice of a group wider
+// than 16 q heads).  The workgroup covers p.kvs_per_wg slices: wave w serves
+// slice w % kvs_per_wg and takes every streams-th tile of the segment
+// (streams = 8 / kvs_per_wg).  With the engine's layout a token row holds
+// every kv head contiguously ([page, KVH, D]), so the waves of one workgroup
+// read whole token rows (KVH x 256 B) together instead of 256-byte slivers at
+// a KVH x 256-byte stride; the streaming read rate of the first pattern is
+// measured ~13 % higher on MI355X.  Waves of the same slice merge through
+// LDS; the result is the final output row (split < 0) or split-K partial
+// `split`.  Ends with a barrier, so LDS can be reused right after.
 // ---------------------------------------------------------------------------
 template <int kEnc>
-__device__ void decode_unit(const AttnParams& p, char* smem, int b, int kvg, int chunk) {
+__device__ void decode_segment(const AttnParams& p, char* smem, const int32_t* bt, int b, int kvg,
+                               int ctx, int t0, int t1, int split) {
+  b = uniform(b);
   const LaneId L = lane_id();
   const int wave = uniform(int(threadIdx.x >> 6));  // wave-uniform (scalar) index
   const int per = p.kvs_per_wg;
@@ -685,12 +698,15 @@ __device__ void decode_unit(const AttnParams& p, char* smem, int b, int kvg, int
   const int g = kvs / p.nslices;
   const int s = kvs - g * p.nslices;
   const int hs = min(p.hs, p.group - s * p.hs);
-  const int ctx = p.ctx_lens[b];
-  const int nch = ctx > 0 ? (ctx + p.chunk_tokens - 1) / p.chunk_tokens : 1;
-  if (chunk >= nch) return;  // uniform over the workgroup
-  const int c0 = chunk * p.chunk_tokens;
-  const int c1 = min(c0 + p.chunk_tokens, ctx);
-  const int ntiles = c1 > c0 ? (c1 - c0 + kTile - 1) / kTile : 0;
+  // The segment bounds are wave-uniform whatever path computed them; keeping
+  // them (and the key index below) scalar keeps the block-table lookups on
+  // the scalar unit, off the vector-memory counter that the tile prefetch
+  // ring waits on.
+  ctx = uniform(ctx);
+  t0 = uniform(t0);
+  t1 = uniform(t1);
+  const int ntiles = t1 > t0 ? t1 - t0 : 0;
+  const int c0 = t0 * kTile;
   // Tiles are dealt round-robin over the streams: at any moment the
   // workgroup reads `streams` consecutive tiles of every slice, one
   // contiguous stretch of the page.
@@ -706,15 +722,14 @@ __device__ void decode_unit(const AttnParams& p, char* smem, int b, int kvg, int
   ColState<1> st;
   init_state(st);
 
-  const int32_t* bt = p.block_tables + int64_t(b) * p.bt_stride;
   const int64_t head_off = int64_t(g) * ((kEnc == kBF16) ? kD * 2 : kD);
   const int tok = int(p.tok_bytes);
   const int span = kTile * tok;
   const TileOffsets off = tile_offsets<kEnc>(tok, L);
-  // j-th tile of this wave -> chunk-relative tile index
+  // j-th tile of this wave -> segment-relative tile index
   auto tile_of = [&](int j) { return stream + j * streams; };
   auto tile_slot0 = [&](int tix) -> int64_t {
-    const int key0 = c0 + tix * kTile;
+    const int key0 = uniform(c0 + tix * kTile);
     const int blk = uniform(bt[key0 / p.page]);
     return int64_t(blk) * p.page + (key0 % p.page);
   };
@@ -729,8 +744,8 @@ __device__ void decode_unit(const AttnParams& p, char* smem, int b, int kvg, int
       load_tile_buf_i8<kEnc>(t, tile_rsrc(kb, nrec), tile_rsrc(vb, nrec), off);
     }
     if constexpr (kEnc == kI8Tok) {
-      t.sc = load_scales_buf(p.k_scale + slot0 * p.kvh, p.v_scale + slot0 * p.kvh, p.kvh, g, live,
-                             L);
+      load_scales_buf(p.k_scale + slot0 * p.kvh, p.v_scale + slot0 * p.kvh, p.kvh, g, live, L,
+                      t.sck, t.scv);
     }
   };
 
@@ -788,12 +803,27 @@ __device__ void decode_unit(const AttnParams& p, char* smem, int b, int kvg, int
       v[4] += e * c.x; v[5] += e * c.y; v[6] += e * c.z; v[7] += e * c.w;
     }
     const int head = g_c * p.group + s_c * p.hs + col;
-    if (nch == 1) {
+    if (split < 0) {
       store_final(p, b, head, d0, v, 1.f / l);
     } else {
-      store_partial(p, b, head, chunk, d0, v, m, l);
+      store_partial(p, b, head, split, d0, v, m, l);
     }
   }
+  __syncthreads();
+}
+
+// Fixed-chunk decode unit (the mixed varlen launch): chunk `chunk` of row b,
+// p.chunk_tokens keys per chunk.
+template <int kEnc>
+__device__ void decode_unit(const AttnParams& p, char* smem, int b, int kvg, int chunk) {
+  const int ctx = p.ctx_lens[b];
+  const int nch = ctx > 0 ? (ctx + p.chunk_tokens - 1) / p.chunk_tokens : 1;
+  if (chunk >= nch) return;  // uniform over the workgroup
+  const int chunk_tiles = p.chunk_tokens / kTile;
+  const int ntiles = (ctx + kTile - 1) / kTile;
+  const int t0 = chunk * chunk_tiles;
+  decode_segment<kEnc>(p, smem, p.block_tables + int64_t(b) * p.bt_stride, b, kvg, ctx, t0,
+                       min(t0 + chunk_tiles, ntiles), nch == 1 ? -1 : chunk);
 }
 
 // ---------------------------------------------------------------------------
@@ -943,7 +973,8 @@ __device__ void prefill_unit(const AttnParams& p, char* smem, int i, int qt, int
         t.v[ii] = *reinterpret_cast<const u32x2_t*>(vb + key_of_slot(L.lg, ii) * kPitch + L.lm * 8);
       if constexpr (kEnc == kI8Tok) {
         // Same lane order as load_scales_buf: K scales then V scales.
-        t.sc = reinterpret_cast<const float*>(kb + 2 * kTileBytesBF16)[L.lane];
+        t.sck = reinterpret_cast<const float*>(kb + 2 * kTileBytesBF16)[L.lane];
+        t.scv = 0.f;
       }
     }
   };
@@ -1026,6 +1057,125 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(AttnParams p) {
   decode_unit<kEnc>(p, smem, b, kvg, chunk);
 }
 
+// ---------------------------------------------------------------------------
+// Stream-K paged decode.  The rows' 32-key tiles, concatenated in row-unit
+// order (row unit r = row * groups + slice group), are cut into gridDim.x
+// equal shares of S = max(sk_min_share, ceil(W / gridDim.x),
+// ceil(Tmax / (max_splits - 1))) tiles, W = total tiles, Tmax = longest row;
+// workgroup w attends the tiles [w S, (w + 1) S).  A share may span several
+// rows (one segment each) and a row may span several shares: every share
+// costs the same whatever the context lengths, and a row spans at most
+// ceil(T / S) + 1 <= max_splits workgroups.  Rows inside one share are
+// written final; the others as partials, merged by merge_kernel with
+// sk_nseg[r] splits.  Zero-length rows (no tiles) get NaN, the reference's
+// 0 / 0, from the workgroup whose share holds their start.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int ctx_tiles(int ctx) { return ctx > 0 ? (ctx + kTile - 1) / kTile : 0; }
+
+// NaN output rows for every head of slice group kvg of row b.
+__device__ void write_nan_rows(const AttnParams& p, int b, int kvg) {
+  const int per = p.kvs_per_wg;
+  for (int sl = 0; sl < per; ++sl) {
+    const int kvs = kvg * per + sl;
+    const int g = kvs / p.nslices;
+    const int s = kvs - g * p.nslices;
+    const int hs = min(p.hs, p.group - s * p.hs);
+    for (int col = 0; col < hs; ++col) {
+      uint16_t* dst = p.out + int64_t(b) * p.o_st + int64_t(g * p.group + s * p.hs + col) * p.o_sh;
+      for (int d = 0; d < kD; d += 8)
+        *reinterpret_cast<u32x4_t*>(dst + d) =
+            u32x4_t{0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u};
+    }
+  }
+}
+
+// block_tables and ctx_lens come as restrict-qualified kernel arguments:
+// the kernel's stores (split counts, outputs, partials) provably never touch
+// them, so their wave-uniform reads stay scalar loads inside the segment
+// loop.  Every wave computes the partition itself from one read of the
+// context lengths (lane l sums the tiles of a contiguous run of row units, a wave
+// scan by shuffles gives the prefix), so no workgroup barrier stands between
+// the launch and the first KV load.  Wave 0 also records each row's split
+// count (from the share holding its first tile) and writes NaN rows for
+// empty contexts.
+template <int kEnc>
+__global__ void __launch_bounds__(kThreads)
+paged_decode_sk_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
+                       const int32_t* __restrict__ ctx_lens) {
+  __shared__ __align__(16) char smem[kDecodeSmem];
+  const int groups = (p.kvh * p.nslices) / p.kvs_per_wg;
+  const int R = p.n_dec * groups;
+  const int w = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wave = uniform(int(threadIdx.x >> 6));
+  const int per_lane = (R + 63) / 64;
+  const int r0 = min(R, lane * per_lane);
+  const int r1 = min(R, r0 + per_lane);
+  int mine = 0, tmax = 0;
+  for (int r = r0; r < r1; ++r) {
+    const int t = ctx_tiles(ctx_lens[r / groups]);
+    mine += t;
+    tmax = max(tmax, t);
+  }
+  int incl = mine;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int t = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += t;
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) tmax = max(tmax, __shfl_xor(tmax, d, 64));
+  const int W = uniform(__shfl(incl, 63, 64));
+  const int Tmax = uniform(tmax);
+  const int excl = incl - mine;
+  int S = max(p.sk_min_share, (W + int(gridDim.x) - 1) / int(gridDim.x));
+  if (p.max_splits > 1) S = max(S, (Tmax + p.max_splits - 2) / (p.max_splits - 1));
+  const int start = w * S;
+  const int end = min(W, start + S);
+  // The row unit holding tile `start` opens this share.
+  int found_r = R, found_p = 0;
+  {
+    int P = excl;
+    for (int r = r0; r < r1; ++r) {
+      const int t = ctx_tiles(ctx_lens[r / groups]);
+      if (P <= start && start < P + t) {
+        found_r = r;
+        found_p = P;
+      }
+      if (wave == 0) {
+        if (t == 0) {
+          const int owner = W > 0 ? min(P, W - 1) / S : 0;
+          if (owner == w) {
+            write_nan_rows(p, r / groups, r % groups);
+            p.sk_nseg[r] = 0;
+          }
+        } else if (P / S == w) {
+          p.sk_nseg[r] = (P + t - 1) / S - P / S + 1;
+        }
+      }
+      P += t;
+    }
+  }
+  const unsigned long long hit = __ballot(found_r < R);
+  const int src = hit ? __ffsll(hit) - 1 : 0;
+  int r = uniform(__shfl(found_r, src, 64));
+  int P = uniform(__shfl(found_p, src, 64));
+  while (r < R && P < end) {
+    const int b = r / groups;
+    const int ctx = uniform(ctx_lens[b]);
+    const int t = ctx_tiles(ctx);
+    if (t > 0) {
+      const int t0 = max(start, P) - P;
+      const int t1 = min(end, P + t) - P;
+      const int nseg = (P + t - 1) / S - P / S + 1;
+      decode_segment<kEnc>(p, smem, block_tables + int64_t(b) * p.bt_stride, b, r - b * groups,
+                           ctx, t0, t1, nseg == 1 ? -1 : w - P / S);
+    }
+    P += t;
+    ++r;
+  }
+}
+
 // Locate prefill unit u: chunk i, query tile, kv slice, split (query tile
 // fastest so that units sharing K/V are adjacent).
 __device__ __forceinline__ bool find_prefill_unit(const AttnParams& p, int u, int& i, int& qt,
@@ -1076,8 +1226,16 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(AttnParams p, int 
   const int64_t t = int64_t(blockIdx.x) * kMergeThreads + threadIdx.x;
   const int64_t row = t / cells_per_row;
   if (row >= num_rows) return;
+  const int cell = int(t - row * cells_per_row);
+  const int head = cell / (kD / 4);
   int nsplit;
-  if (row < p.n_dec) {
+  if (p.sk_nseg != nullptr) {
+    // Stream-K: the head's slice group -> its row unit's split count.
+    const int g = head / p.group;
+    const int kvs = g * p.nslices + (head - g * p.group) / p.hs;
+    const int groups = (p.kvh * p.nslices) / p.kvs_per_wg;
+    nsplit = p.sk_nseg[row * groups + kvs / p.kvs_per_wg];
+  } else if (row < p.n_dec) {
     const int ctx = p.ctx_lens[row];
     nsplit = ctx > 0 ? (ctx + p.chunk_tokens - 1) / p.chunk_tokens : 1;
   } else {
@@ -1089,8 +1247,6 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(AttnParams p, int 
     nsplit = max(1, (sk + p.split_tokens - 1) / p.split_tokens);
   }
   if (nsplit <= 1) return;
-  const int cell = int(t - row * cells_per_row);
-  const int head = cell / (kD / 4);
   merge_cell(p, row, head, (cell - head * (kD / 4)) * 4, nsplit);
 }
 
@@ -1146,6 +1302,38 @@ int plan_decode_chunk(int64_t rows, int64_t groups, int64_t max_ctx) {
   int64_t ch = (max_ctx + nch - 1) / nch;
   ch = ((ch + 127) / 128) * 128;
   return int(ch < 128 ? 128 : ch);
+}
+
+// Stream-K plan of a paged decode launch: one workgroup per CU, shares of
+// at least kSkMinShare tiles, at most max_splits workgroups per row (bounded
+// so the partials stay within kSkMaxPartialBytes).  KVC_DECODE_STREAMK=0
+// selects the fixed-chunk partition instead.
+constexpr int kSkMinShare = 8;
+constexpr int64_t kSkMaxPartialBytes = int64_t(256) << 20;
+
+struct SkPlan {
+  bool on;
+  int grid;
+  int max_splits;
+};
+
+SkPlan plan_stream_k(int64_t rows, int64_t heads, int64_t max_ctx) {
+  SkPlan sp{env_int("KVC_DECODE_STREAMK", 1) != 0, int(device_cus()), 2};
+  const int64_t max_tiles = (max_ctx + kTile - 1) / kTile;
+  int64_t ms = (max_tiles + kSkMinShare - 1) / kSkMinShare + 1;
+  const int64_t per_split = rows * heads * (kD + 1) * int64_t(sizeof(float));
+  const int64_t cap = per_split > 0 ? kSkMaxPartialBytes / per_split : 64;
+  ms = ms > 64 ? 64 : ms;
+  ms = ms > cap ? cap : ms;
+  sp.max_splits = int(ms < 2 ? 2 : ms);
+  return sp;
+}
+
+// Workspace of a stream-K launch: the partials, then one int32 split count
+// per row unit (256-byte aligned).
+size_t sk_workspace_bytes(int64_t rows, int64_t heads, int64_t groups, int max_splits) {
+  const size_t part = size_t(rows) * size_t(heads) * size_t(max_splits) * (kD + 1) * sizeof(float);
+  return (part + 255) / 256 * 256 + size_t(rows) * size_t(groups) * sizeof(int) + 256;
 }
 
 // Keys per prefill split: a quarter of the longest key range, at least 512.
@@ -1254,6 +1442,8 @@ extern "C" size_t kvc_paged_decode_workspace_bytes(int64_t batch, int64_t num_he
   if (batch <= 0 || num_kv_heads <= 0 || head_dim != kD) return 0;
   const HeadPlan hp = plan_heads(num_heads, num_kv_heads);
   const int64_t max_ctx = max_blocks_per_seq * page_size;
+  const SkPlan sp = plan_stream_k(batch, num_heads, max_ctx);
+  if (sp.on) return sk_workspace_bytes(batch, num_heads, hp.groups, sp.max_splits);
   const int ch = plan_decode_chunk(batch, hp.groups, max_ctx);
   const int64_t splits = max_ctx > 0 ? (max_ctx + ch - 1) / ch : 1;
   return partial_bytes(batch, num_heads, splits);
@@ -1313,6 +1503,35 @@ extern "C" int kvc_paged_decode(const void* q, int64_t q_stride_b, int64_t q_str
   p.ctx_lens = context_lens;
   const int64_t max_ctx = max_blocks_per_seq * page_size;
   p.kvs_per_wg = hp.kvs_per_wg;
+  hipStream_t st = as_stream(stream);
+  const SkPlan sp = plan_stream_k(batch, num_heads, max_ctx);
+  if (sp.on) {
+    p.max_splits = sp.max_splits;
+    p.sk_min_share = kSkMinShare;
+    const size_t need = sk_workspace_bytes(batch, num_heads, hp.groups, sp.max_splits);
+    KVC_REQUIRE(workspace != nullptr && workspace_bytes >= need, KVC_ERR_WORKSPACE,
+                "paged_decode: workspace of %zu bytes needed (got %zu)", need, workspace_bytes);
+    set_partials(p, workspace, batch);
+    const size_t part = size_t(batch) * size_t(num_heads) * size_t(p.max_splits) * (kD + 1) *
+                        sizeof(float);
+    p.sk_nseg = reinterpret_cast<int*>(static_cast<char*>(workspace) + (part + 255) / 256 * 256);
+    p.chunk_tokens = kTile;
+    switch (kv_dtype) {
+      case KVC_KV_BF16:
+        paged_decode_sk_kernel<kBF16><<<sp.grid, kThreads, 0, st>>>(p, block_tables, context_lens);
+        break;
+      case KVC_KV_INT8_TOKHEAD:
+        paged_decode_sk_kernel<kI8Tok><<<sp.grid, kThreads, 0, st>>>(p, block_tables, context_lens);
+        break;
+      default:
+        paged_decode_sk_kernel<kI8Chan><<<sp.grid, kThreads, 0, st>>>(p, block_tables, context_lens);
+        break;
+    }
+    rc = check_launch("paged_decode");
+    if (rc != KVC_OK) return rc;
+    launch_merge(p, batch, st);
+    return check_launch("paged_decode merge");
+  }
   p.chunk_tokens = plan_decode_chunk(batch, hp.groups, max_ctx);
   KVC_REQUIRE(p.chunk_tokens % kTile == 0, KVC_ERR_VALUE,
               "paged_decode: decode chunk must be a multiple of 32");
@@ -1325,7 +1544,6 @@ extern "C" int kvc_paged_decode(const void* q, int64_t q_stride_b, int64_t q_str
   const int64_t units = batch * hp.groups * p.dec_max_chunks;
   KVC_REQUIRE(units < (int64_t(1) << 31), KVC_ERR_VALUE, "paged_decode: launch too large");
   p.dec_units = int(units);
-  hipStream_t st = as_stream(stream);
   switch (kv_dtype) {
     case KVC_KV_BF16: launch_decode_enc<kBF16>(p, int(units), st); break;
     case KVC_KV_INT8_TOKHEAD: launch_decode_enc<kI8Tok>(p, int(units), st); break;

@@ -39,18 +39,24 @@ def test_abi_version_and_error_string():
 
 
 def test_workspace_queries_are_host_only():
-    # Pure host arithmetic (no GPU here; the plan assumes 256 CUs).  A decode
-    # workgroup covers every kv head of its sequence, so batch 64 gives 64
-    # units and the context is split into 4 chunks of 1024 keys: the
-    # workspace holds fp32 partials, 128 dims + 1 log-sum-exp per (row, head,
-    # split), plus 256 bytes of slack.
+    # Pure host arithmetic (no GPU here; the plan assumes 256 CUs).  Paged
+    # decode is stream-K: every workgroup takes an equal share (>= 8 tiles of
+    # 32 keys) of all rows' tiles, so a row of up to 4096 keys (128 tiles) is
+    # split at most 128 / 8 + 1 = 17 ways.  The workspace holds fp32 partials
+    # (128 dims + 1 log-sum-exp per row, head and split), 256-byte aligned,
+    # then one int32 split count per (row, kv-head group), plus 256 bytes.
     q = _native.query
+    part = 64 * 32 * 17 * 129 * 4
     assert q("kvc_paged_decode_workspace_bytes", 64, 32, 4, 128, 256, 16) == \
-        64 * 32 * 4 * 129 * 4 + 256
-    # 256 sequences already fill the CUs with one chunk each: no workspace.
-    assert q("kvc_paged_decode_workspace_bytes", 256, 32, 4, 128, 256, 16) == 0
-    # A batch of 4 at 32k context splits into many chunks.
-    assert q("kvc_paged_decode_workspace_bytes", 4, 32, 4, 128, 256, 128) > 0
+        (part + 255) // 256 * 256 + 64 * 4 + 256
+    # Splits are capped at 64 however long the rows are.
+    part = 4 * 32 * 64 * 129 * 4
+    assert q("kvc_paged_decode_workspace_bytes", 4, 32, 4, 128, 256, 1024) == \
+        (part + 255) // 256 * 256 + 4 * 4 + 256
+    # 32 kv heads form 4 groups of 8 kv heads per workgroup: 4 counts per row.
+    part = 8 * 32 * 17 * 129 * 4
+    assert q("kvc_paged_decode_workspace_bytes", 8, 32, 32, 128, 256, 16) == \
+        (part + 255) // 256 * 256 + 8 * 4 * 4 + 256
 
 
 def test_bad_arguments_map_to_python_exceptions():
