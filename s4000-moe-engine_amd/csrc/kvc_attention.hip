@@ -34,6 +34,7 @@ constexpr int kWaves = 8;  // two waves per SIMD
 constexpr int kThreads = 64 * kWaves;
 constexpr int kSideMax = 8;
 constexpr int kPreNCB = 2;  // column blocks per wave in prefill units
+constexpr float kRescaleLog2 = 8.f;  // lazy-rescale threshold (log2 units)
 
 enum Enc : int { kBF16 = KVC_KV_BF16, kI8Tok = KVC_KV_INT8_TOKHEAD, kI8Chan = KVC_KV_INT8_CHAN };
 
@@ -468,12 +469,28 @@ __device__ __forceinline__ void attend_tile(ColState<NCB>& st, const Tile<kEnc>&
       }
       tmax = fmaxf(tmax, x[i]);
     }
-    tmax = fmaxf(tmax, shfl_xor(tmax, 16));
-    tmax = fmaxf(tmax, shfl_xor(tmax, 32));
-    const float m_new = fmaxf(st.m[cb], tmax);
-    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(st.m[cb] - m_use);
-    st.m[cb] = m_new;
+    tmax = rows4_max(tmax);
+    // Lazy rescale: the accumulators stay relative to a reference max that
+    // only moves when some column's max exceeds it by more than kRescaleLog2
+    // (then probabilities stay <= 2^kRescaleLog2, exact in the fp32
+    // accumulators and within bf16 range); the final normalisation divides by
+    // the sum taken against the same reference, so the result is the same
+    // softmax.  Rescales become rare after the first tiles.
+    float alpha = 1.f;
+    if (__builtin_expect(__ballot(tmax > st.m[cb] + kRescaleLog2) != 0, 0)) {
+      const float m_new = fmaxf(st.m[cb], tmax);
+      const float m_ref = (m_new == -INFINITY) ? 0.f : m_new;
+      alpha = __builtin_amdgcn_exp2f(st.m[cb] - m_ref);
+      st.m[cb] = m_new;
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        st.o[cb][jj][0] *= alpha;
+        st.o[cb][jj][1] *= alpha;
+        st.o[cb][jj][2] *= alpha;
+        st.o[cb][jj][3] *= alpha;
+      }
+    }
+    const float m_use = (st.m[cb] == -INFINITY) ? 0.f : st.m[cb];
     float pr[8], psum = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -494,7 +511,7 @@ __device__ __forceinline__ void attend_tile(ColState<NCB>& st, const Tile<kEnc>&
     }
     u32x4_t pb;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) pb[w] = pack_bf16x2(pv[2 * w], pv[2 * w + 1]);
+    for (int w = 0; w < 4; ++w) pb[w] = pack_bf16x2_fast(pv[2 * w], pv[2 * w + 1]);
     if constexpr (kEnc != kBF16) {
       float vsum = 0.f;
 #pragma unroll
@@ -526,12 +543,7 @@ __device__ __forceinline__ void attend_tile(ColState<NCB>& st, const Tile<kEnc>&
       } else {
         a = v_operand_i8(vq, jj);
       }
-      f32x4_t o = st.o[cb][jj];
-      o[0] *= alpha;
-      o[1] *= alpha;
-      o[2] *= alpha;
-      o[3] *= alpha;
-      st.o[cb][jj] = mfma_bf16(a, pb, o);
+      st.o[cb][jj] = mfma_bf16(a, pb, st.o[cb][jj]);
     }
   }
 }
@@ -894,14 +906,15 @@ __device__ void prefill_unit(const AttnParams& p, char* smem, int i, int qt, int
       return int64_t(blk) * p.page + (key0 % p.page);
     }
   };
-  // Cooperative global -> register fetch of one tile (16 B per element).
-  u32x4_t pre[kLoadsPerThread];
-  float pre_s = 0.f;
-  auto fetch = [&](int64_t slot0, int key0) {
+  // Cooperative global -> register fetch of one tile (16 B per element) into
+  // register set `set`; two sets keep two tiles in flight.
+  u32x4_t pre[2][kLoadsPerThread];
+  float pre_s[2] = {0.f, 0.f};
+  auto fetch = [&](int set, int64_t slot0, int key0) {
 #pragma unroll
     for (int e = 0; e < kLoadsPerThread; ++e) {
       const int idx = e * kThreads + threadIdx.x;
-      pre[e] = u32x4_t{0u, 0u, 0u, 0u};
+      pre[set][e] = u32x4_t{0u, 0u, 0u, 0u};
       if (idx < 2 * kVecPerTile) {
         const int tensor = idx / kVecPerTile;
         const int rem = idx - tensor * kVecPerTile;
@@ -911,11 +924,11 @@ __device__ void prefill_unit(const AttnParams& p, char* smem, int i, int qt, int
           if constexpr (kFresh) {
             const uint16_t* src = tensor == 0 ? p.kf + (slot0 + key) * p.kf_st + int64_t(g) * p.kf_sh
                                               : p.vf + (slot0 + key) * p.vf_st + int64_t(g) * p.vf_sh;
-            pre[e] = reinterpret_cast<const u32x4_t*>(src)[vec];
+            pre[set][e] = reinterpret_cast<const u32x4_t*>(src)[vec];
           } else {
             const char* src = (tensor == 0 ? p.k_cache : p.v_cache) + (slot0 + key) * p.tok_bytes +
                               head_off;
-            pre[e] = reinterpret_cast<const u32x4_t*>(src)[vec];
+            pre[set][e] = reinterpret_cast<const u32x4_t*>(src)[vec];
           }
         }
       }
@@ -924,11 +937,11 @@ __device__ void prefill_unit(const AttnParams& p, char* smem, int i, int qt, int
       if (threadIdx.x < 2 * kTile) {
         const int key = threadIdx.x & (kTile - 1);
         const float* sp = (threadIdx.x < kTile) ? p.k_scale : p.v_scale;
-        pre_s = (key0 + key < sk) ? sp[(slot0 + key) * p.kvh + g] : 0.f;
+        pre_s[set] = (key0 + key < sk) ? sp[(slot0 + key) * p.kvh + g] : 0.f;
       }
     }
   };
-  auto commit = [&](int buf) {
+  auto commit = [&](int set, int buf) {
     char* st_base = stage_ptr(buf);
 #pragma unroll
     for (int e = 0; e < kLoadsPerThread; ++e) {
@@ -939,12 +952,12 @@ __device__ void prefill_unit(const AttnParams& p, char* smem, int i, int qt, int
         const int key = rem / kVecPerRow;
         const int vec = rem - key * kVecPerRow;
         char* dst = st_base + tensor * kTileBytesBF16 + key * kPitch + vec * 16;
-        *reinterpret_cast<u32x4_t*>(dst) = pre[e];
+        *reinterpret_cast<u32x4_t*>(dst) = pre[set][e];
       }
     }
     if constexpr (kEnc == kI8Tok) {
       if (threadIdx.x < 2 * kTile)
-        reinterpret_cast<float*>(st_base + 2 * kTileBytesBF16)[threadIdx.x] = pre_s;
+        reinterpret_cast<float*>(st_base + 2 * kTileBytesBF16)[threadIdx.x] = pre_s[set];
     }
   };
   // LDS -> operand registers, same lane mapping as the HBM loads.
@@ -980,25 +993,40 @@ __device__ void prefill_unit(const AttnParams& p, char* smem, int i, int qt, int
   };
 
   if (ntiles > 0) {
-    int64_t slot_cur = tile_slot0(0);
-    fetch(slot_cur, k_begin);
-    commit(0);
+    // Tile j sits in register set j & 1 while in flight, then in LDS stage
+    // j & 1.  Iteration j issues tile j + 2's loads, attends tile j from LDS
+    // and commits tile j + 1 (loaded during iteration j - 1): two tiles of
+    // compute cover each tile's global latency.
+    int64_t slots[3];
+    slots[0] = tile_slot0(0);
+    fetch(0, slots[0], k_begin);
+    commit(0, 0);
+    slots[1] = 0;
+    if (ntiles > 1) {
+      slots[1] = tile_slot0(1);
+      fetch(1, slots[1], k_begin + kTile);
+    }
     __syncthreads();
-    for (int tix = 0; tix < ntiles; ++tix) {
-      const int buf = tix & 1;
-      const bool has_next = tix + 1 < ntiles;
-      int64_t slot_next = 0;
-      if (has_next) {
-        slot_next = tile_slot0(tix + 1);
-        fetch(slot_next, k_begin + (tix + 1) * kTile);
+    for (int j0 = 0; j0 < ntiles; j0 += 2) {
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int tix = j0 + r;
+        if (tix < ntiles) {
+          slots[2] = 0;
+          if (tix + 2 < ntiles) {
+            slots[2] = tile_slot0(tix + 2);
+            fetch(r, slots[2], k_begin + (tix + 2) * kTile);
+          }
+          Tile<kEnc> t;
+          read_tile(t, r);
+          attend<kEnc, kPreNCB>(st, t, Q, ci, k_begin + tix * kTile, sk, min_klim,
+                                kFresh ? -1 : slots[0], p, g, L);
+          if (tix + 1 < ntiles) commit(1 - r, 1 - r);
+          __syncthreads();
+          slots[0] = slots[1];
+          slots[1] = slots[2];
+        }
       }
-      Tile<kEnc> t;
-      read_tile(t, buf);
-      attend<kEnc, kPreNCB>(st, t, Q, ci, k_begin + tix * kTile, sk, min_klim,
-                            kFresh ? -1 : slot_cur, p, g, L);
-      if (has_next) commit(buf ^ 1);
-      __syncthreads();
-      slot_cur = slot_next;
     }
   }
 
@@ -1201,20 +1229,22 @@ __device__ __forceinline__ bool find_prefill_unit(const AttnParams& p, int u, in
   return false;
 }
 
+// Grid order: the prefill units first, then the decode units, so that the
+// long prefill units do not start after the memory-bound decode units.
 template <int kEnc, bool kFresh>
 __global__ void __launch_bounds__(kThreads) varlen_kernel(AttnParams p) {
   __shared__ __align__(16) char smem[kSmemBytes];
   const int u = blockIdx.x;
-  if (u < p.dec_units) {
+  if (u >= p.pre_units) {
     if constexpr (!kFresh) {
       int b, kvg, chunk;
-      decode_unit_of(p, u, b, kvg, chunk);
+      decode_unit_of(p, u - p.pre_units, b, kvg, chunk);
       decode_unit<kEnc>(p, smem, b, kvg, chunk);
     }
     return;
   }
   int i, qt, kvs, split;
-  if (!find_prefill_unit(p, u - p.dec_units, i, qt, kvs, split)) return;
+  if (!find_prefill_unit(p, u, i, qt, kvs, split)) return;
   prefill_unit<kEnc, kFresh>(p, smem, i, qt, kvs, split);
 }
 
@@ -1336,11 +1366,12 @@ size_t sk_workspace_bytes(int64_t rows, int64_t heads, int64_t groups, int max_s
   return (part + 255) / 256 * 256 + size_t(rows) * size_t(groups) * sizeof(int) + 256;
 }
 
-// Keys per prefill split: a quarter of the longest key range, at least 512.
+// Keys per prefill split: an eighth of the longest key range, at least 512
+// (the long chunk of a mixed batch then fills the CUs with its splits).
 int plan_prefill_split(int64_t max_seqlen_k) {
   const int forced = env_int("KVC_PREFILL_SPLIT", 0);
   if (forced > 0) return forced;
-  int64_t ks = (max_seqlen_k + 3) / 4;
+  int64_t ks = (max_seqlen_k + 7) / 8;
   ks = ((ks + kTile - 1) / kTile) * kTile;
   return int(ks < 512 ? 512 : ks);
 }

@@ -65,6 +65,35 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
 }
 
+// The same round-to-nearest-even conversion in one instruction
+// (v_cvt_pk_bf16_f32); a NaN keeps its NaN-ness but not necessarily its
+// payload, so bit-exact byte paths use pack_bf16x2 instead.
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
+__device__ __forceinline__ uint32_t pack_bf16x2_fast(float lo, float hi) {
+  const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// max / sum over the lanes l, l ^ 16, l ^ 32, l ^ 48 (the four 16-lane rows),
+// with the row-swap permutes instead of LDS-routed shuffles.
+__device__ __forceinline__ float rows4_max(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ __forceinline__ float rows4_sum(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // v_perm_b32 byte selectors: (lo half of a, lo half of b) and (hi of a, hi of b)
 // for perm(b, a, sel) where a supplies bytes 0-3 and b bytes 4-7.
 constexpr uint32_t kPermLoLo = 0x05040100u;
