@@ -144,6 +144,47 @@ class BlockMover:
                  self.plane_stride, self._stream())
 
 
+    # -- overlapped offload step ------------------------------------------
+    def _side_streams(self):
+        if getattr(self, "_sides", None) is None:
+            dev = self.pool.device
+            # default priority (equal to the current stream's)
+            self._sides = (torch.cuda.Stream(device=dev), torch.cuda.Stream(device=dev))
+        return self._sides
+
+    def swap(self, out_ids, host_out: torch.Tensor, in_ids, host_in: torch.Tensor,
+             compact_src=None, compact_dst=None) -> None:
+        """One offload step with its byte moves overlapped: host_out[i] =
+        pool[:, :, out_ids[i]] (device -> host) and pool[:, :, in_ids[j]] =
+        host_in[j] (host -> device) run concurrently on two copy-engine streams
+        (the link is full duplex), and the optional compaction copy
+        pool[:, :, compact_dst] = pool[:, :, compact_src] runs on the current
+        stream beside them.  The four id sets must be pairwise disjoint (the
+        moves are unordered with respect to each other); all of them are
+        ordered after the work already on the current stream, and the current
+        stream waits for them before anything it runs next."""
+        outs = [int(x) for x in (out_ids.tolist() if isinstance(out_ids, torch.Tensor) else out_ids)]
+        ins = [int(x) for x in (in_ids.tolist() if isinstance(in_ids, torch.Tensor) else in_ids)]
+        cs = [] if compact_src is None else [int(x) for x in compact_src]
+        cd = [] if compact_dst is None else [int(x) for x in compact_dst]
+        sets = [set(outs), set(ins), set(cs), set(cd)]
+        total = sum(len(x) for x in sets)
+        if total != len(set().union(*sets)) or len(outs) != len(sets[0]) or len(ins) != len(sets[1]):
+            raise ValueError("swap: the out, in and compaction id sets must be disjoint")
+        cur = torch.cuda.current_stream(self.pool.device)
+        s_out, s_in = self._side_streams()
+        s_out.wait_stream(cur)
+        s_in.wait_stream(cur)
+        with torch.cuda.stream(s_out):
+            self.d2h(outs, host_out)
+        with torch.cuda.stream(s_in):
+            self.h2d(host_in, ins)
+        if cs:
+            self.copy(cs, cd)
+        cur.wait_stream(s_out)
+        cur.wait_stream(s_in)
+
+
 class KVCacheRunner:
     """The runner's KV duties for one rank: the pool, its per-layer views, and
     the offload executor protocol the BlockManager drives through call()."""

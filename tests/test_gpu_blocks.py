@@ -85,3 +85,29 @@ def test_dma_offload_roundtrip():
     mover.h2d(host, new_ids)
     torch.cuda.synchronize()
     assert np.array_equal(_np(pool).reshape(expect.shape), expect)
+
+
+def test_overlapped_swap_step_matches_sequential_moves():
+    # One offload step with its moves on two copy-engine streams plus the
+    # compaction on the current stream: the result equals the closed forms
+    # (victims land in the host buffer, revived blocks come from the other host
+    # buffer, compaction copies src -> dst); overlapping id sets are rejected.
+    pool = _pool(L=2, blocks=24, seed=5)
+    before = _np(pool).reshape(2 * pool.size(1), pool.size(2), -1).copy()
+    mover = BlockMover(pool)
+    out_ids, in_ids, src, dst = [3, 17, 8], [0, 21, 12], [5, 6, 22, 1], [9, 10, 2, 23]
+    shape = (3,) + tuple(pool[:, :, 0].shape)
+    host_out = torch.empty(shape, dtype=pool.dtype, pin_memory=True)
+    g = torch.Generator().manual_seed(6)
+    host_in = torch.randn(shape, generator=g).to(torch.bfloat16).pin_memory()
+    print("[blocks] overlapped swap", flush=True)
+    mover.swap(out_ids, host_out, in_ids, host_in, src, dst)
+    torch.cuda.synchronize()
+    assert np.array_equal(_np(host_out).reshape(3, *before.shape[:1], -1),
+                          ko.block_gather(before, out_ids))
+    expect = before.copy()
+    ko.block_scatter(expect, in_ids, _np(host_in).reshape(3, before.shape[0], -1))
+    ko.block_copy(expect, src, dst)
+    assert np.array_equal(_np(pool).reshape(expect.shape), expect)
+    with pytest.raises(ValueError):
+        mover.swap([1], host_out[:1], [1], host_in[:1])
