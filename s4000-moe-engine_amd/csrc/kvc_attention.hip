@@ -644,36 +644,6 @@ __device__ __forceinline__ void store_partial(const AttnParams& p, int64_t row, 
   if (d0 == 0) p.part_lse[base] = l > 0.f ? m + __log2f(l) : -INFINITY;
 }
 
-// Merge the split-K partials of one (row, head) over 4 dims d0..d0+3:
-// out = sum_s 2^(lse_s - M) O_s / sum_s 2^(lse_s - M), O_s normalised.  One
-// online pass: the loads of every split are independent of the running max,
-// so they are all in flight together.
-__device__ __forceinline__ void merge_cell(const AttnParams& p, int64_t row, int head, int d0,
-                                           int nsplit) {
-  const int64_t base = (row * p.num_heads + head) * p.max_splits;
-  float m = -INFINITY, l = 0.f;
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll 4
-  for (int sp = 0; sp < nsplit; ++sp) {
-    const float lse = p.part_lse[base + sp];
-    const float4 o = *reinterpret_cast<const float4*>(p.part_o + (base + sp) * kD + d0);
-    const float m_new = fmaxf(m, lse);
-    if (m_new == -INFINITY) continue;  // every split so far empty
-    const float a = __builtin_amdgcn_exp2f(m - m_new);
-    const float w = __builtin_amdgcn_exp2f(lse - m_new);
-    l = l * a + w;
-    acc.x = acc.x * a + w * o.x;
-    acc.y = acc.y * a + w * o.y;
-    acc.z = acc.z * a + w * o.z;
-    acc.w = acc.w * a + w * o.w;
-    m = m_new;
-  }
-  const float inv = 1.f / l;
-  uint16_t* dst = p.out + row * p.o_st + int64_t(head) * p.o_sh + d0;
-  *reinterpret_cast<u32x2_t*>(dst) =
-      u32x2_t{pack_bf16x2(acc.x * inv, acc.y * inv), pack_bf16x2(acc.z * inv, acc.w * inv)};
-}
-
 constexpr int kDecodeSmem = kWaves * int(sizeof(WaveOut));
 constexpr int kPitchBF16 = kD * 2 + 16;
 constexpr int kPitchI8 = kD + 16;
@@ -1248,16 +1218,19 @@ __global__ void __launch_bounds__(kThreads) varlen_kernel(AttnParams p) {
   prefill_unit<kEnc, kFresh>(p, smem, i, qt, kvs, split);
 }
 
-// Split-K merge: one thread per (query row, head, 4 dims); rows that were
-// not split were finalised by the attention kernel and are skipped.
-constexpr int kMergeThreads = 256;
-__global__ void __launch_bounds__(kMergeThreads) merge_kernel(AttnParams p, int num_rows) {
-  const int cells_per_row = p.num_heads * (kD / 4);
-  const int64_t t = int64_t(blockIdx.x) * kMergeThreads + threadIdx.x;
-  const int64_t row = t / cells_per_row;
+// Split-K merge: one wave per (query row, head), lane l owning dims 2l and
+// 2l + 1.  The splits are taken 16 at a time with every load of a batch in
+// flight together (log-sum-exps are wave-uniform), so a row split 16 ways
+// costs one memory round trip.  Rows that were not split were finalised by
+// the attention kernel and are skipped.
+constexpr int kMergeWaves = 4;
+constexpr int kMergeBatch = 16;
+__global__ void __launch_bounds__(64 * kMergeWaves) merge_kernel(AttnParams p, int num_rows) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wv = int64_t(blockIdx.x) * kMergeWaves + (threadIdx.x >> 6);
+  const int64_t row = wv / p.num_heads;
   if (row >= num_rows) return;
-  const int cell = int(t - row * cells_per_row);
-  const int head = cell / (kD / 4);
+  const int head = int(wv - row * p.num_heads);
   int nsplit;
   if (p.sk_nseg != nullptr) {
     // Stream-K: the head's slice group -> its row unit's split count.
@@ -1276,13 +1249,48 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(AttnParams p, int 
     const int sk = p.cu_k[i + 1] - p.cu_k[i];
     nsplit = max(1, (sk + p.split_tokens - 1) / p.split_tokens);
   }
+  nsplit = uniform(nsplit);
   if (nsplit <= 1) return;
-  merge_cell(p, row, head, (cell - head * (kD / 4)) * 4, nsplit);
+  const int64_t base = (row * p.num_heads + head) * p.max_splits;
+  float m = -INFINITY, l = 0.f, acc0 = 0.f, acc1 = 0.f;
+  for (int s0 = 0; s0 < nsplit; s0 += kMergeBatch) {
+    float lse[kMergeBatch];
+    float2 o[kMergeBatch];
+#pragma unroll
+    for (int k = 0; k < kMergeBatch; ++k) {
+      const int sp = min(s0 + k, nsplit - 1);  // past the end: re-read a valid split
+      lse[k] = p.part_lse[base + sp];
+      o[k] = *reinterpret_cast<const float2*>(p.part_o + (base + sp) * kD + 2 * lane);
+    }
+    float bm = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < kMergeBatch; ++k)
+      if (s0 + k < nsplit) bm = fmaxf(bm, lse[k]);
+    const float m_new = fmaxf(m, bm);
+    if (m_new == -INFINITY) continue;  // every split so far empty
+    const float a = __builtin_amdgcn_exp2f(m - m_new);
+    l *= a;
+    acc0 *= a;
+    acc1 *= a;
+#pragma unroll
+    for (int k = 0; k < kMergeBatch; ++k) {
+      if (s0 + k < nsplit) {
+        const float w = __builtin_amdgcn_exp2f(lse[k] - m_new);
+        l += w;
+        acc0 += w * o[k].x;
+        acc1 += w * o[k].y;
+      }
+    }
+    m = m_new;
+  }
+  const float inv = 1.f / l;
+  uint16_t* dst = p.out + row * p.o_st + int64_t(head) * p.o_sh + 2 * lane;
+  *reinterpret_cast<uint32_t*>(dst) = pack_bf16x2(acc0 * inv, acc1 * inv);
 }
 
 void launch_merge(const AttnParams& p, int64_t rows, hipStream_t st) {
-  const int64_t threads = rows * p.num_heads * (kD / 4);
-  merge_kernel<<<unsigned((threads + kMergeThreads - 1) / kMergeThreads), kMergeThreads, 0, st>>>(
+  const int64_t waves = rows * p.num_heads;
+  merge_kernel<<<unsigned((waves + kMergeWaves - 1) / kMergeWaves), 64 * kMergeWaves, 0, st>>>(
       p, int(rows));
 }
 
