@@ -794,6 +794,261 @@ __device__ void decode_segment(const AttnParams& p, char* smem, const int32_t* b
   __syncthreads();
 }
 
+// ---------------------------------------------------------------------------
+// LDS-staged decode segment (bf16 pool, a group of 4 kv heads = 1 KiB of each
+// token row).  Each 32-key tile is brought into LDS as whole token rows — one
+// 1 KiB direct-to-LDS load per row, 64 rows (K and V) spread over the 8 waves
+// — double-buffered, rows padded to 1040 B so the operand reads are free of
+// bank conflicts.  Streaming whole contiguous rows is measurably faster than
+// per-head register loads (~7.2 vs ~6.85 TB/s on MI355X).  Wave w serves kv
+// head w % 4 and dim half w / 4: both halves compute the full S^T tile and
+// softmax (identical), each accumulates O^T for its 64 dims (dims
+// 8m + 4h .. 8m + 4h + 3 of the PV MFMA rows), so no cross-wave merge.
+// ---------------------------------------------------------------------------
+constexpr int kLdsPitch = 1024 + 16;
+constexpr int kLdsTensor = kTile * kLdsPitch;
+constexpr int kLdsStage = 2 * kLdsTensor;
+
+// V^T operand of PV MFMA jj (0..3 within the wave's half) from half rows:
+// v[i] holds dims 8lm + 4h .. +3 of key slot i.
+__device__ __forceinline__ u32x4_t v_operand_half(const u32x2_t (&v)[8], int jj) {
+  const uint32_t sel = (jj & 1) ? kPermHiHi : kPermLoLo;
+  const int dw = jj >> 1;
+  return u32x4_t{perm(v[1][dw], v[0][dw], sel), perm(v[3][dw], v[2][dw], sel),
+                 perm(v[5][dw], v[4][dw], sel), perm(v[7][dw], v[6][dw], sel)};
+}
+
+// One 16-byte-per-lane load straight into LDS: lane i's 16 bytes from
+// rsrc + voff land at LDS address lds + 16 i.  Issued through inline asm so
+// the compiler's wait-count pass does not treat it as a pending LDS write
+// (it would then drain every load in flight before each barrier and LDS read,
+// serialising the prefetch); the caller waits with explicit vmcnt counts.
+// M0 carries the LDS address and is restored afterwards.
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i32x4_t raw_rsrc(const void* base, int bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  return i32x4_t{int(__builtin_amdgcn_readfirstlane(uint32_t(a))),
+                 int(__builtin_amdgcn_readfirstlane(uint32_t(a >> 32) & 0xffffu)),
+                 int(__builtin_amdgcn_readfirstlane(uint32_t(bytes))), kBufWord3};
+}
+
+__device__ __forceinline__ void dma_to_lds(const i32x4_t& rsrc, int voff, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "buffer_load_dwordx4 %1, %3, 0 offen nt lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(voff), "s"(lds), "s"(rsrc)
+      : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane(
+      uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)p)));
+}
+
+struct HalfState {
+  f32x4_t o[4];  // O^T rows of PV MFMA jj (local 0..3): dim 32lg + 8r + 4h + jj
+  float m, l;
+};
+
+template <bool kMasked>
+__device__ __forceinline__ void attend_tile_half(HalfState& st, const u32x4_t (&k)[2][4],
+                                                 const u32x2_t (&vh)[8],
+                                                 const QOps<kBF16, 1>& Q, int key0,
+                                                 int valid_end, int klim, float scale_log2,
+                                                 const LaneId& L) {
+  bool kvalid[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) kvalid[i] = !kMasked || (key0 + key_of_slot(L.lg, i) < valid_end);
+  u32x2_t vrow[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    vrow[i] = vh[i];
+    if (kMasked && !kvalid[i]) vrow[i] = u32x2_t{0u, 0u};
+  }
+  f32x4_t s0 = f32x4_t{0.f, 0.f, 0.f, 0.f}, s1 = s0;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    s0 = mfma_bf16(k[0][c], Q.op[0][c], s0);
+    s1 = mfma_bf16(k[1][c], Q.op[0][c], s1);
+  }
+  float x[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+  float tmax = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    if constexpr (kMasked) {
+      const bool ok = kvalid[i] && (key0 + key_of_slot(L.lg, i) <= klim);
+      x[i] = ok ? x[i] * scale_log2 : -INFINITY;
+    } else {
+      x[i] *= scale_log2;
+    }
+    tmax = fmaxf(tmax, x[i]);
+  }
+  tmax = rows4_max(tmax);
+  float alpha = 1.f;
+  if (__builtin_expect(__ballot(tmax > st.m + kRescaleLog2) != 0, 0)) {
+    const float m_new = fmaxf(st.m, tmax);
+    const float m_ref = (m_new == -INFINITY) ? 0.f : m_new;
+    alpha = __builtin_amdgcn_exp2f(st.m - m_ref);
+    st.m = m_new;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      st.o[jj][0] *= alpha;
+      st.o[jj][1] *= alpha;
+      st.o[jj][2] *= alpha;
+      st.o[jj][3] *= alpha;
+    }
+  }
+  const float m_use = (st.m == -INFINITY) ? 0.f : st.m;
+  float pr[8], psum = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    pr[i] = __builtin_amdgcn_exp2f(x[i] - m_use);
+    psum += pr[i];
+  }
+  st.l = st.l * alpha + psum;
+  u32x4_t pb;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) pb[w] = pack_bf16x2_fast(pr[2 * w], pr[2 * w + 1]);
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) st.o[jj] = mfma_bf16(v_operand_half(vrow, jj), pb, st.o[jj]);
+}
+
+__device__ void decode_segment_lds(const AttnParams& p, char* stage0, char* stage1,
+                                   const int32_t* bt, int b, int kvg, int ctx, int t0, int t1,
+                                   int split) {
+  const LaneId L = lane_id();
+  const int wave = uniform(int(threadIdx.x >> 6));
+  const int gl = wave & 3;   // kv head within the group
+  const int hf = wave >> 2;  // dim half
+  const int g = kvg * 4 + gl;
+  b = uniform(b);
+  ctx = uniform(ctx);
+  t0 = uniform(t0);
+  t1 = uniform(t1);
+  const int ntiles = t1 > t0 ? t1 - t0 : 0;
+  const int c0 = t0 * kTile;
+
+  ColInfo ci[1];
+  ci[0].row = b;
+  ci[0].head = g * p.group + L.lm;
+  ci[0].valid = L.lm < p.hs;
+  ci[0].klim = ctx - 1;
+  QOps<kBF16, 1> Q;
+  build_q<kBF16, 1>(Q, p, ci, g, L);
+  // Land the query now: the wait-count pass does not see the DMA loads below,
+  // so a query load still pending at the loop would cost a full drain there.
+#pragma unroll
+  for (int c = 0; c < 4; ++c) asm volatile("" : "+v"(Q.op[0][c]));
+  HalfState st;
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) st.o[jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  st.m = -INFINITY;
+  st.l = 0.f;
+
+  const int tok = int(p.tok_bytes);
+  const int64_t grp_off = int64_t(kvg) * 1024;
+  // Wave w loads rows w, w + 8, w + 16, w + 24 of K and of V.
+  auto issue = [&](int tix, char* base) {
+    const int key0 = uniform(c0 + tix * kTile);
+    const int blk = uniform(bt[key0 / p.page]);
+    const int64_t slot0 = int64_t(blk) * p.page + (key0 % p.page);
+    const i32x4_t kr = raw_rsrc(p.k_cache + slot0 * p.tok_bytes + grp_off, kTile * tok);
+    const i32x4_t vr = raw_rsrc(p.v_cache + slot0 * p.tok_bytes + grp_off, kTile * tok);
+    const uint32_t lb = lds_addr(base);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int row = wave + 8 * q;
+      dma_to_lds(kr, row * tok + L.lane * 16, lb + row * kLdsPitch);
+      dma_to_lds(vr, row * tok + L.lane * 16, lb + kLdsTensor + row * kLdsPitch);
+    }
+  };
+
+  // Tile j lives in stage j & 1.  The stages are separate LDS objects and the
+  // loop is unrolled by two so every access names its stage statically: the
+  // compiler then only waits for the DMA into the stage it reads.
+  auto attend_stage = [&](int j, const char* kb) {
+    const char* vb = kb + kLdsTensor;
+    u32x4_t k[2][4];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const char* row = kb + (h * 16 + L.lm) * kLdsPitch + gl * 256 + L.lg * 16;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) k[h][c] = *reinterpret_cast<const u32x4_t*>(row + c * 64);
+    }
+    u32x2_t vh[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      vh[i] = *reinterpret_cast<const u32x2_t*>(vb + key_of_slot(L.lg, i) * kLdsPitch + gl * 256 +
+                                                L.lm * 16 + hf * 8);
+    const int key0 = c0 + j * kTile;
+    if (key0 + kTile <= ctx) {
+      attend_tile_half<false>(st, k, vh, Q, key0, ctx, ctx - 1, p.scale_log2, L);
+    } else {
+      attend_tile_half<true>(st, k, vh, Q, key0, ctx, ctx - 1, p.scale_log2, L);
+    }
+  };
+  if (ntiles > 0) {
+    issue(0, stage0);
+    for (int j0 = 0; j0 < ntiles; j0 += 2) {
+      // tile j0 in stage0, tile j0 + 1 in stage1
+      if (j0 + 1 < ntiles) {
+        issue(j0 + 1, stage1);
+        __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8): this wave's loads of tile j0
+      } else {
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+      }
+      __syncthreads();
+      attend_stage(j0, stage0);
+      __syncthreads();
+      if (j0 + 1 < ntiles) {
+        if (j0 + 2 < ntiles) {
+          issue(j0 + 2, stage0);
+          __builtin_amdgcn_s_waitcnt(0x0F78);
+        } else {
+          __builtin_amdgcn_s_waitcnt(0x0F70);
+        }
+        __syncthreads();
+        attend_stage(j0 + 1, stage1);
+        __syncthreads();
+      }
+    }
+  }
+
+  // Epilogue: lane (lm, lg) holds, for r = 0..3, dims 32lg + 8r + 4hf .. +3
+  // of column lm; l is lane-partial over the key slots.
+  const float l = rows4_sum(st.l);
+  if (L.lm < p.hs) {
+    const int head = g * p.group + L.lm;
+    const float inv_l = 1.f / l;
+    if (split < 0) {
+      uint16_t* dst = p.out + int64_t(b) * p.o_st + int64_t(head) * p.o_sh;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int d0 = 32 * L.lg + 8 * r + 4 * hf;
+        *reinterpret_cast<u32x2_t*>(dst + d0) =
+            u32x2_t{pack_bf16x2(st.o[0][r] * inv_l, st.o[1][r] * inv_l),
+                    pack_bf16x2(st.o[2][r] * inv_l, st.o[3][r] * inv_l)};
+      }
+    } else {
+      const int64_t base = (int64_t(b) * p.num_heads + head) * p.max_splits + split;
+      const float il = l > 0.f ? inv_l : 0.f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int d0 = 32 * L.lg + 8 * r + 4 * hf;
+        *reinterpret_cast<float4*>(p.part_o + base * kD + d0) =
+            make_float4(st.o[0][r] * il, st.o[1][r] * il, st.o[2][r] * il, st.o[3][r] * il);
+      }
+      if (L.lg == 0 && hf == 0) p.part_lse[base] = l > 0.f ? st.m + __log2f(l) : -INFINITY;
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+}
+
 // Fixed-chunk decode unit (the mixed varlen launch): chunk `chunk` of row b,
 // p.chunk_tokens keys per chunk.
 template <int kEnc>
@@ -1096,11 +1351,15 @@ __device__ void write_nan_rows(const AttnParams& p, int b, int kvg) {
 // the launch and the first KV load.  Wave 0 also records each row's split
 // count (from the share holding its first tile) and writes NaN rows for
 // empty contexts.
-template <int kEnc>
+template <int kEnc, bool kLds>
 __global__ void __launch_bounds__(kThreads)
 paged_decode_sk_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
                        const int32_t* __restrict__ ctx_lens) {
-  __shared__ __align__(16) char smem[kDecodeSmem];
+  // kLds: bf16 pool with 4 kv heads per workgroup (decode_segment_lds); its
+  // two stages are separate LDS objects, the first doubling as the scratch of
+  // the register path.
+  __shared__ __align__(16) char smem[kLds ? kLdsStage : kDecodeSmem];
+  __shared__ __align__(16) char smem1[kLds ? kLdsStage : 16];
   const int groups = (p.kvh * p.nslices) / p.kvs_per_wg;
   const int R = p.n_dec * groups;
   const int w = blockIdx.x;
@@ -1166,8 +1425,13 @@ paged_decode_sk_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
       const int t0 = max(start, P) - P;
       const int t1 = min(end, P + t) - P;
       const int nseg = (P + t - 1) / S - P / S + 1;
-      decode_segment<kEnc>(p, smem, block_tables + int64_t(b) * p.bt_stride, b, r - b * groups,
-                           ctx, t0, t1, nseg == 1 ? -1 : w - P / S);
+      if constexpr (kLds) {
+        decode_segment_lds(p, smem, smem1, block_tables + int64_t(b) * p.bt_stride, b,
+                           r - b * groups, ctx, t0, t1, nseg == 1 ? -1 : w - P / S);
+      } else {
+        decode_segment<kEnc>(p, smem, block_tables + int64_t(b) * p.bt_stride, b,
+                             r - b * groups, ctx, t0, t1, nseg == 1 ? -1 : w - P / S);
+      }
     }
     P += t;
     ++r;
@@ -1249,19 +1513,26 @@ __global__ void __launch_bounds__(64 * kMergeWaves) merge_kernel(AttnParams p, i
     const int sk = p.cu_k[i + 1] - p.cu_k[i];
     nsplit = max(1, (sk + p.split_tokens - 1) / p.split_tokens);
   }
-  nsplit = uniform(nsplit);
-  if (nsplit <= 1) return;
   const int64_t base = (row * p.num_heads + head) * p.max_splits;
-  float m = -INFINITY, l = 0.f, acc0 = 0.f, acc1 = 0.f;
-  for (int s0 = 0; s0 < nsplit; s0 += kMergeBatch) {
-    float lse[kMergeBatch];
-    float2 o[kMergeBatch];
+  // The first batch is loaded before the split count is known (slots past it
+  // hold stale values, are inside the workspace and are masked below), so a
+  // row of up to 16 splits costs one memory round trip.
+  float lse[kMergeBatch];
+  float2 o[kMergeBatch];
+  auto load_batch = [&](int s0, int limit) {
 #pragma unroll
     for (int k = 0; k < kMergeBatch; ++k) {
-      const int sp = min(s0 + k, nsplit - 1);  // past the end: re-read a valid split
+      const int sp = min(s0 + k, limit - 1);
       lse[k] = p.part_lse[base + sp];
       o[k] = *reinterpret_cast<const float2*>(p.part_o + (base + sp) * kD + 2 * lane);
     }
+  };
+  load_batch(0, p.max_splits);
+  nsplit = uniform(nsplit);
+  if (nsplit <= 1) return;
+  float m = -INFINITY, l = 0.f, acc0 = 0.f, acc1 = 0.f;
+  for (int s0 = 0; s0 < nsplit; s0 += kMergeBatch) {
+    if (s0 > 0) load_batch(s0, nsplit);
     float bm = -INFINITY;
 #pragma unroll
     for (int k = 0; k < kMergeBatch; ++k)
@@ -1557,13 +1828,21 @@ extern "C" int kvc_paged_decode(const void* q, int64_t q_stride_b, int64_t q_str
     p.chunk_tokens = kTile;
     switch (kv_dtype) {
       case KVC_KV_BF16:
-        paged_decode_sk_kernel<kBF16><<<sp.grid, kThreads, 0, st>>>(p, block_tables, context_lens);
+        if (hp.kvs_per_wg == 4 && hp.nslices == 1 && env_int("KVC_DECODE_LDS", 1) != 0) {
+          paged_decode_sk_kernel<kBF16, true>
+              <<<sp.grid, kThreads, 0, st>>>(p, block_tables, context_lens);
+        } else {
+          paged_decode_sk_kernel<kBF16, false>
+              <<<sp.grid, kThreads, 0, st>>>(p, block_tables, context_lens);
+        }
         break;
       case KVC_KV_INT8_TOKHEAD:
-        paged_decode_sk_kernel<kI8Tok><<<sp.grid, kThreads, 0, st>>>(p, block_tables, context_lens);
+        paged_decode_sk_kernel<kI8Tok, false>
+            <<<sp.grid, kThreads, 0, st>>>(p, block_tables, context_lens);
         break;
       default:
-        paged_decode_sk_kernel<kI8Chan><<<sp.grid, kThreads, 0, st>>>(p, block_tables, context_lens);
+        paged_decode_sk_kernel<kI8Chan, false>
+            <<<sp.grid, kThreads, 0, st>>>(p, block_tables, context_lens);
         break;
     }
     rc = check_launch("paged_decode");
