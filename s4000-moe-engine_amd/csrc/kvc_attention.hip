@@ -808,6 +808,10 @@ __device__ void decode_segment(const AttnParams& p, char* smem, const int32_t* b
 constexpr int kLdsPitch = 1024 + 16;
 constexpr int kLdsTensor = kTile * kLdsPitch;
 constexpr int kLdsStage = 2 * kLdsTensor;
+// Query block of the LDS path: [4 kv heads][16 columns][256 B], the 16-byte
+// chunks of row (h, c) stored at chunk index ^ c so that 16 columns reading
+// the same dims hit 16 different bank groups.
+constexpr int kLdsQ = 4 * 16 * 256;
 
 // V^T operand of PV MFMA jj (0..3 within the wave's half) from half rows:
 // v[i] holds dims 8lm + 4h .. +3 of key slot i.
@@ -917,7 +921,7 @@ __device__ __forceinline__ void attend_tile_half(HalfState& st, const u32x4_t (&
   for (int jj = 0; jj < 4; ++jj) st.o[jj] = mfma_bf16(v_operand_half(vrow, jj), pb, st.o[jj]);
 }
 
-__device__ void decode_segment_lds(const AttnParams& p, char* stage0, char* stage1,
+__device__ void decode_segment_lds(const AttnParams& p, char* stage0, char* stage1, char* qlds,
                                    const int32_t* bt, int b, int kvg, int ctx, int t0, int t1,
                                    int split) {
   const LaneId L = lane_id();
@@ -932,17 +936,7 @@ __device__ void decode_segment_lds(const AttnParams& p, char* stage0, char* stag
   const int ntiles = t1 > t0 ? t1 - t0 : 0;
   const int c0 = t0 * kTile;
 
-  ColInfo ci[1];
-  ci[0].row = b;
-  ci[0].head = g * p.group + L.lm;
-  ci[0].valid = L.lm < p.hs;
-  ci[0].klim = ctx - 1;
   QOps<kBF16, 1> Q;
-  build_q<kBF16, 1>(Q, p, ci, g, L);
-  // Land the query now: the wait-count pass does not see the DMA loads below,
-  // so a query load still pending at the loop would cost a full drain there.
-#pragma unroll
-  for (int c = 0; c < 4; ++c) asm volatile("" : "+v"(Q.op[0][c]));
   HalfState st;
 #pragma unroll
   for (int jj = 0; jj < 4; ++jj) st.o[jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -967,23 +961,26 @@ __device__ void decode_segment_lds(const AttnParams& p, char* stage0, char* stag
     }
   };
 
-  // Tile j lives in stage j & 1.  The stages are separate LDS objects and the
-  // loop is unrolled by two so every access names its stage statically: the
-  // compiler then only waits for the DMA into the stage it reads.
-  auto attend_stage = [&](int j, const char* kb) {
+  // Tile j lives in stage j & 1.  A stage is read into registers as soon as
+  // its tile has landed and is refilled with tile j + 2 before tile j is
+  // computed, so two tiles stay in flight under the arithmetic.  The loop is
+  // unrolled by two so every access names its stage statically.
+  u32x4_t k[2][4];
+  u32x2_t vh[8];
+  auto read_stage = [&](const char* kb) {
     const char* vb = kb + kLdsTensor;
-    u32x4_t k[2][4];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const char* row = kb + (h * 16 + L.lm) * kLdsPitch + gl * 256 + L.lg * 16;
 #pragma unroll
       for (int c = 0; c < 4; ++c) k[h][c] = *reinterpret_cast<const u32x4_t*>(row + c * 64);
     }
-    u32x2_t vh[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i)
       vh[i] = *reinterpret_cast<const u32x2_t*>(vb + key_of_slot(L.lg, i) * kLdsPitch + gl * 256 +
                                                 L.lm * 16 + hf * 8);
+  };
+  auto compute = [&](int j) {
     const int key0 = c0 + j * kTile;
     if (key0 + kTile <= ctx) {
       attend_tile_half<false>(st, k, vh, Q, key0, ctx, ctx - 1, p.scale_log2, L);
@@ -991,30 +988,55 @@ __device__ void decode_segment_lds(const AttnParams& p, char* stage0, char* stag
       attend_tile_half<true>(st, k, vh, Q, key0, ctx, ctx - 1, p.scale_log2, L);
     }
   };
+  // One step: tile j is in `stage`; tile j + 1 (if any) is already in flight.
+  auto step = [&](int j, char* stage) {
+    if (j + 1 < ntiles) {
+      __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8): this wave's loads of tile j
+    } else {
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    }
+    __syncthreads();
+    read_stage(stage);
+    __builtin_amdgcn_s_waitcnt(0xC07F);    // lgkmcnt(0): the stage is in registers
+    __syncthreads();
+    if (j + 2 < ntiles) issue(j + 2, stage);
+    compute(j);
+  };
+  // The query rides the same DMA ahead of the first two tiles: wave w brings
+  // columns 8 (w >> 2) .. + 7 of kv head w & 3 (columns past the head count
+  // repeat the last head; their results are never stored).
+  auto issue_q = [&]() {
+    const i32x4_t qr =
+        raw_rsrc(p.q + int64_t(b) * p.q_st, int(int64_t(p.num_heads) * p.q_sh * 2));
+    const uint32_t lb = lds_addr(qlds);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int col = 8 * hf + 4 * s + (L.lane >> 4);
+      const int head = g * p.group + min(col, p.hs - 1);
+      const int chunk = (L.lane & 15) ^ col;
+      dma_to_lds(qr, int(int64_t(head) * p.q_sh * 2) + chunk * 16,
+                 lb + (gl * 16 + 8 * hf + 4 * s) * 256);
+    }
+  };
   if (ntiles > 0) {
+    issue_q();
     issue(0, stage0);
+    if (ntiles > 1) {
+      issue(1, stage1);
+      __builtin_amdgcn_s_waitcnt(0x4F70);  // vmcnt(16): this wave's query loads
+    } else {
+      __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8)
+    }
+    __syncthreads();
+    {
+      const char* row = qlds + (gl * 16 + L.lm) * 256;
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        Q.op[0][c] = *reinterpret_cast<const u32x4_t*>(row + (((4 * c + L.lg) ^ L.lm) * 16));
+    }
     for (int j0 = 0; j0 < ntiles; j0 += 2) {
-      // tile j0 in stage0, tile j0 + 1 in stage1
-      if (j0 + 1 < ntiles) {
-        issue(j0 + 1, stage1);
-        __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8): this wave's loads of tile j0
-      } else {
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-      }
-      __syncthreads();
-      attend_stage(j0, stage0);
-      __syncthreads();
-      if (j0 + 1 < ntiles) {
-        if (j0 + 2 < ntiles) {
-          issue(j0 + 2, stage0);
-          __builtin_amdgcn_s_waitcnt(0x0F78);
-        } else {
-          __builtin_amdgcn_s_waitcnt(0x0F70);
-        }
-        __syncthreads();
-        attend_stage(j0 + 1, stage1);
-        __syncthreads();
-      }
+      step(j0, stage0);
+      if (j0 + 1 < ntiles) step(j0 + 1, stage1);
     }
   }
 
@@ -1360,6 +1382,7 @@ paged_decode_sk_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
   // the register path.
   __shared__ __align__(16) char smem[kLds ? kLdsStage : kDecodeSmem];
   __shared__ __align__(16) char smem1[kLds ? kLdsStage : 16];
+  __shared__ __align__(16) char smem2[kLds ? kLdsQ : 16];
   const int groups = (p.kvh * p.nslices) / p.kvs_per_wg;
   const int R = p.n_dec * groups;
   const int w = blockIdx.x;
@@ -1368,9 +1391,21 @@ paged_decode_sk_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
   const int per_lane = (R + 63) / 64;
   const int r0 = min(R, lane * per_lane);
   const int r1 = min(R, r0 + per_lane);
+  // The first kCached context lengths of the lane's run stay in registers for
+  // the second pass (one round trip to memory for batches up to 256 x groups).
+  constexpr int kCached = 4;
+  int cl[kCached];
+#pragma unroll
+  for (int i = 0; i < kCached; ++i) cl[i] = r0 + i < r1 ? ctx_lens[(r0 + i) / groups] : 0;
+  auto ctx_of = [&](int r) {
+    int c = 0;
+#pragma unroll
+    for (int i = 0; i < kCached; ++i) c = (r == r0 + i) ? cl[i] : c;
+    return r - r0 < kCached ? c : ctx_lens[r / groups];
+  };
   int mine = 0, tmax = 0;
   for (int r = r0; r < r1; ++r) {
-    const int t = ctx_tiles(ctx_lens[r / groups]);
+    const int t = ctx_tiles(ctx_of(r));
     mine += t;
     tmax = max(tmax, t);
   }
@@ -1390,14 +1425,16 @@ paged_decode_sk_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
   const int start = w * S;
   const int end = min(W, start + S);
   // The row unit holding tile `start` opens this share.
-  int found_r = R, found_p = 0;
+  int found_r = R, found_p = 0, found_c = 0;
   {
     int P = excl;
     for (int r = r0; r < r1; ++r) {
-      const int t = ctx_tiles(ctx_lens[r / groups]);
+      const int c = ctx_of(r);
+      const int t = ctx_tiles(c);
       if (P <= start && start < P + t) {
         found_r = r;
         found_p = P;
+        found_c = c;
       }
       if (wave == 0) {
         if (t == 0) {
@@ -1417,16 +1454,16 @@ paged_decode_sk_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
   const int src = hit ? __ffsll(hit) - 1 : 0;
   int r = uniform(__shfl(found_r, src, 64));
   int P = uniform(__shfl(found_p, src, 64));
+  int ctx = uniform(__shfl(found_c, src, 64));
   while (r < R && P < end) {
     const int b = r / groups;
-    const int ctx = uniform(ctx_lens[b]);
     const int t = ctx_tiles(ctx);
     if (t > 0) {
       const int t0 = max(start, P) - P;
       const int t1 = min(end, P + t) - P;
       const int nseg = (P + t - 1) / S - P / S + 1;
       if constexpr (kLds) {
-        decode_segment_lds(p, smem, smem1, block_tables + int64_t(b) * p.bt_stride, b,
+        decode_segment_lds(p, smem, smem1, smem2, block_tables + int64_t(b) * p.bt_stride, b,
                            r - b * groups, ctx, t0, t1, nseg == 1 ? -1 : w - P / S);
       } else {
         decode_segment<kEnc>(p, smem, block_tables + int64_t(b) * p.bt_stride, b,
@@ -1435,6 +1472,7 @@ paged_decode_sk_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
     }
     P += t;
     ++r;
+    if (r < R && P < end) ctx = uniform(ctx_lens[r / groups]);
   }
 }
 
