@@ -81,6 +81,7 @@ struct AttnParams {
   float* part_o;
   float* part_lse;
   int max_splits;
+  int merge_first;  // splits the merge loads before it reads a row's split count
   // Stream-K decode (paged decode launches): each workgroup takes an equal
   // share (at least sk_min_share) of the tiles of all rows; sk_nseg[r] gets
   // the number of workgroups that row unit r (= row * groups + group) spans.
@@ -1552,45 +1553,52 @@ __global__ void __launch_bounds__(64 * kMergeWaves) merge_kernel(AttnParams p, i
     nsplit = max(1, (sk + p.split_tokens - 1) / p.split_tokens);
   }
   const int64_t base = (row * p.num_heads + head) * p.max_splits;
-  // The first batch is loaded before the split count is known (slots past it
-  // hold stale values, are inside the workspace and are masked below), so a
-  // row of up to 16 splits costs one memory round trip.
+  // The first p.merge_first slots are loaded before the split count is known
+  // (slots past it hold stale values, are inside the workspace and are masked
+  // below), so a row with that many splits costs one memory round trip.
   float lse[kMergeBatch];
   float2 o[kMergeBatch];
-  auto load_batch = [&](int s0, int limit) {
+  auto load_batch = [&](int s0, int cnt) {
 #pragma unroll
     for (int k = 0; k < kMergeBatch; ++k) {
-      const int sp = min(s0 + k, limit - 1);
-      lse[k] = p.part_lse[base + sp];
-      o[k] = *reinterpret_cast<const float2*>(p.part_o + (base + sp) * kD + 2 * lane);
+      if (k < cnt) {
+        lse[k] = p.part_lse[base + s0 + k];
+        o[k] = *reinterpret_cast<const float2*>(p.part_o + (base + s0 + k) * kD + 2 * lane);
+      }
     }
   };
-  load_batch(0, p.max_splits);
+  const int first = min(p.merge_first, p.max_splits);
+  load_batch(0, first);
   nsplit = uniform(nsplit);
   if (nsplit <= 1) return;
   float m = -INFINITY, l = 0.f, acc0 = 0.f, acc1 = 0.f;
-  for (int s0 = 0; s0 < nsplit; s0 += kMergeBatch) {
-    if (s0 > 0) load_batch(s0, nsplit);
+  int s0 = 0, cnt = min(first, nsplit);
+  while (true) {
     float bm = -INFINITY;
 #pragma unroll
     for (int k = 0; k < kMergeBatch; ++k)
-      if (s0 + k < nsplit) bm = fmaxf(bm, lse[k]);
+      if (k < cnt) bm = fmaxf(bm, lse[k]);
     const float m_new = fmaxf(m, bm);
-    if (m_new == -INFINITY) continue;  // every split so far empty
-    const float a = __builtin_amdgcn_exp2f(m - m_new);
-    l *= a;
-    acc0 *= a;
-    acc1 *= a;
+    if (m_new != -INFINITY) {  // else every split so far is empty
+      const float a = __builtin_amdgcn_exp2f(m - m_new);
+      l *= a;
+      acc0 *= a;
+      acc1 *= a;
 #pragma unroll
-    for (int k = 0; k < kMergeBatch; ++k) {
-      if (s0 + k < nsplit) {
-        const float w = __builtin_amdgcn_exp2f(lse[k] - m_new);
-        l += w;
-        acc0 += w * o[k].x;
-        acc1 += w * o[k].y;
+      for (int k = 0; k < kMergeBatch; ++k) {
+        if (k < cnt) {
+          const float w = __builtin_amdgcn_exp2f(lse[k] - m_new);
+          l += w;
+          acc0 += w * o[k].x;
+          acc1 += w * o[k].y;
+        }
       }
+      m = m_new;
     }
-    m = m_new;
+    s0 += cnt;
+    if (s0 >= nsplit) break;
+    cnt = min(kMergeBatch, nsplit - s0);
+    load_batch(s0, cnt);
   }
   const float inv = 1.f / l;
   uint16_t* dst = p.out + row * p.o_st + int64_t(head) * p.o_sh + 2 * lane;
@@ -1830,6 +1838,7 @@ extern "C" int kvc_paged_decode(const void* q, int64_t q_stride_b, int64_t q_str
 
   const HeadPlan hp = plan_heads(num_heads, num_kv_heads);
   AttnParams p{};
+  p.merge_first = kMergeBatch;
   p.q = static_cast<const uint16_t*>(q);
   p.q_st = q_stride_b;
   p.q_sh = q_stride_h;
@@ -1856,6 +1865,10 @@ extern "C" int kvc_paged_decode(const void* q, int64_t q_stride_b, int64_t q_str
   if (sp.on) {
     p.max_splits = sp.max_splits;
     p.sk_min_share = kSkMinShare;
+    // Equal rows split into grid / units shares (+1 where a share boundary
+    // falls inside a row); longer rows of a ragged batch load the rest later.
+    const int64_t units = batch * hp.groups;
+    p.merge_first = int(std::min<int64_t>(kMergeBatch, (sp.grid + units - 1) / units + 1));
     const size_t need = sk_workspace_bytes(batch, num_heads, hp.groups, sp.max_splits);
     KVC_REQUIRE(workspace != nullptr && workspace_bytes >= need, KVC_ERR_WORKSPACE,
                 "paged_decode: workspace of %zu bytes needed (got %zu)", need, workspace_bytes);
@@ -1981,6 +1994,7 @@ extern "C" int kvc_varlen_attention(
 
   const HeadPlan hp = plan_heads(num_heads, num_kv_heads);
   AttnParams p{};
+  p.merge_first = kMergeBatch;
   p.q = static_cast<const uint16_t*>(q);
   p.q_st = q_stride_t;
   p.q_sh = q_stride_h;
