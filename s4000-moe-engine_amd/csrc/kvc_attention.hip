@@ -630,9 +630,9 @@ __device__ __forceinline__ void dump_block(WaveOut& wo, const ColState<NCB>& st,
 __device__ __forceinline__ void store_final(const AttnParams& p, int64_t row, int head, int d0,
                                             const float (&v)[8], float inv_l) {
   uint16_t* dst = p.out + row * p.o_st + int64_t(head) * p.o_sh + d0;
-  *reinterpret_cast<u32x4_t*>(dst) =
-      u32x4_t{pack_bf16x2(v[0] * inv_l, v[1] * inv_l), pack_bf16x2(v[2] * inv_l, v[3] * inv_l),
-              pack_bf16x2(v[4] * inv_l, v[5] * inv_l), pack_bf16x2(v[6] * inv_l, v[7] * inv_l)};
+  *reinterpret_cast<u32x4_t*>(dst) = u32x4_t{
+      pack_bf16x2_fast(v[0] * inv_l, v[1] * inv_l), pack_bf16x2_fast(v[2] * inv_l, v[3] * inv_l),
+      pack_bf16x2_fast(v[4] * inv_l, v[5] * inv_l), pack_bf16x2_fast(v[6] * inv_l, v[7] * inv_l)};
 }
 
 __device__ __forceinline__ void store_partial(const AttnParams& p, int64_t row, int head, int split,
@@ -1053,8 +1053,8 @@ __device__ void decode_segment_lds(const AttnParams& p, char* stage0, char* stag
       for (int r = 0; r < 4; ++r) {
         const int d0 = 32 * L.lg + 8 * r + 4 * hf;
         *reinterpret_cast<u32x2_t*>(dst + d0) =
-            u32x2_t{pack_bf16x2(st.o[0][r] * inv_l, st.o[1][r] * inv_l),
-                    pack_bf16x2(st.o[2][r] * inv_l, st.o[3][r] * inv_l)};
+            u32x2_t{pack_bf16x2_fast(st.o[0][r] * inv_l, st.o[1][r] * inv_l),
+                    pack_bf16x2_fast(st.o[2][r] * inv_l, st.o[3][r] * inv_l)};
       }
     } else {
       const int64_t base = (int64_t(b) * p.num_heads + head) * p.max_splits + split;
@@ -1087,11 +1087,15 @@ __device__ void decode_unit(const AttnParams& p, char* smem, int b, int kvg, int
 }
 
 // ---------------------------------------------------------------------------
-// Prefill unit: (chunk i, query tile, kv head g / slice s, key split).  The
-// workgroup covers 4 waves x kPreNCB column blocks; K/V tiles go through LDS.
+// Prefill segment: key tiles [t0, t1) of item (chunk i, query tile qt, kv
+// slice kvs); the tiles stop at the last key any query of the tile sees.  The
+// workgroup covers kWaves waves x kPreNCB column blocks; K/V tiles go through
+// LDS.  split < 0: the segment is the whole item and writes final rows;
+// otherwise it writes split-K partials at slot `split`.
 // ---------------------------------------------------------------------------
 template <int kEnc, bool kFresh>
-__device__ void prefill_unit(const AttnParams& p, char* smem, int i, int qt, int kvs, int split) {
+__device__ void prefill_segment(const AttnParams& p, char* smem, int i, int qt, int kvs, int t0,
+                                int t1, int split) {
   const LaneId L = lane_id();
   const int wave = uniform(int(threadIdx.x >> 6));  // wave-uniform (scalar) index
   const int g = kvs / p.nslices;
@@ -1104,7 +1108,6 @@ __device__ void prefill_unit(const AttnParams& p, char* smem, int i, int qt, int
   const int prefix = sk - sq;
   const int qtile_tokens = kWaves * kPreNCB * p.tpb;
   const int q0 = qt * qtile_tokens;
-  const int nsplit = max(1, (sk + p.split_tokens - 1) / p.split_tokens);
 
   ColInfo ci[kPreNCB];
 #pragma unroll
@@ -1130,10 +1133,10 @@ __device__ void prefill_unit(const AttnParams& p, char* smem, int i, int qt, int
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) min_klim = min(min_klim, __shfl_xor(min_klim, m, 64));
 
-  // Key range of this split, cut at the last key any column of the tile sees.
+  // Key range of the segment, cut at the last key any column of the tile sees.
   const int last_q = min(q0 + qtile_tokens, sq) - 1;
-  const int k_begin = split * p.split_tokens;
-  const int k_end = min(min(k_begin + p.split_tokens, sk), prefix + last_q + 1);
+  const int k_begin = uniform(t0 * kTile);
+  const int k_end = uniform(min(t1 * kTile, min(sk, prefix + last_q + 1)));
   const int ntiles = k_end > k_begin ? (k_end - k_begin + kTile - 1) / kTile : 0;
 
   const int32_t* bt = kFresh ? nullptr : p.block_tables + int64_t(p.n_dec + i) * p.bt_stride;
@@ -1279,30 +1282,84 @@ __device__ void prefill_unit(const AttnParams& p, char* smem, int i, int qt, int
   }
 
   // Epilogue: each wave finalises its own columns (no cross-wave merge).
-  WaveOut* wo = reinterpret_cast<WaveOut*>(smem);
+  if constexpr (kEnc == kI8Chan) {
+    // The outlier dims come from the side pool: the block goes through LDS so
+    // that their exact values can replace the main path's zeros.
+    WaveOut* wo = reinterpret_cast<WaveOut*>(smem);
 #pragma unroll
-  for (int cb = 0; cb < kPreNCB; ++cb) {
-    dump_block<kEnc, kPreNCB>(wo[wave], st, cb, p, g, L);
-    __syncthreads();
-    // Lane -> (column lm, 32 dims of group lg) of this wave's block.
-    const int col = L.lm;
-    const int tq = q0 + (wave * kPreNCB + cb) * p.tpb + col / p.hs;
-    const int hh = col % p.hs;
-    if (col < p.tpb * p.hs && hh < hs && tq < sq) {
-      const int64_t row = int64_t(p.n_dec) + cq0 + tq;
-      const int head = g * p.group + s * p.hs + hh;
-      const float m = wo[wave].m[col];
-      const float l = wo[wave].l[col];
+    for (int cb = 0; cb < kPreNCB; ++cb) {
+      dump_block<kEnc, kPreNCB>(wo[wave], st, cb, p, g, L);
+      __syncthreads();
+      // Lane -> (column lm, 32 dims of group lg) of this wave's block.
+      const int col = L.lm;
+      const int tq = q0 + (wave * kPreNCB + cb) * p.tpb + col / p.hs;
+      const int hh = col % p.hs;
+      if (col < p.tpb * p.hs && hh < hs && tq < sq) {
+        const int64_t row = int64_t(p.n_dec) + cq0 + tq;
+        const int head = g * p.group + s * p.hs + hh;
+        const float m = wo[wave].m[col];
+        const float l = wo[wave].l[col];
 #pragma unroll
-      for (int part = 0; part < 4; ++part) {
-        const int d0 = 32 * L.lg + 8 * part;
-        float v[8];
+        for (int part = 0; part < 4; ++part) {
+          const int d0 = 32 * L.lg + 8 * part;
+          float v[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = wo[wave].o[col][d0 + e];
-        if (nsplit == 1) {
-          store_final(p, row, head, d0, v, 1.f / l);
+          for (int e = 0; e < 8; ++e) v[e] = wo[wave].o[col][d0 + e];
+          if (split < 0) {
+            store_final(p, row, head, d0, v, 1.f / l);
+          } else {
+            store_partial(p, row, head, split, d0, v, m, l);
+          }
+        }
+      }
+      __syncthreads();
+    }
+  } else {
+    // Lane (lm, lg) holds dims 32 lg + 8 r + jj (r < 4, jj < 8) of column
+    // lm: four runs of 8 contiguous dims, stored straight from registers.
+#pragma unroll
+    for (int cb = 0; cb < kPreNCB; ++cb) {
+      float l = st.l[cb];
+      l += shfl_xor(l, 16);
+      l += shfl_xor(l, 32);
+      float bias = 0.f;
+      if constexpr (kEnc != kBF16) {
+        float vb = st.vb[cb];
+        vb += shfl_xor(vb, 16);
+        vb += shfl_xor(vb, 32);
+        bias = 128.f * vb;
+      }
+      const int col = L.lm;
+      const int tq = q0 + (wave * kPreNCB + cb) * p.tpb + col / p.hs;
+      const int hh = col % p.hs;
+      if (col < p.tpb * p.hs && hh < hs && tq < sq) {
+        const int64_t row = int64_t(p.n_dec) + cq0 + tq;
+        const int head = g * p.group + s * p.hs + hh;
+        if (split < 0) {
+          const float inv = 1.f / l;
+          uint16_t* dst = p.out + row * p.o_st + int64_t(head) * p.o_sh + 32 * L.lg;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float v[8];
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) v[jj] = (st.o[cb][jj][r] - bias) * inv;
+            *reinterpret_cast<u32x4_t*>(dst + 8 * r) =
+                u32x4_t{pack_bf16x2_fast(v[0], v[1]), pack_bf16x2_fast(v[2], v[3]),
+                        pack_bf16x2_fast(v[4], v[5]), pack_bf16x2_fast(v[6], v[7])};
+          }
         } else {
-          store_partial(p, row, head, split, d0, v, m, l);
+          const int64_t base = (row * p.num_heads + head) * p.max_splits + split;
+          const float il = l > 0.f ? 1.f / l : 0.f;
+          float* dst = p.part_o + base * kD + 32 * L.lg;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float v[8];
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) v[jj] = (st.o[cb][jj][r] - bias) * il;
+            reinterpret_cast<float4*>(dst + 8 * r)[0] = make_float4(v[0], v[1], v[2], v[3]);
+            reinterpret_cast<float4*>(dst + 8 * r)[1] = make_float4(v[4], v[5], v[6], v[7]);
+          }
+          if (L.lg == 0) p.part_lse[base] = l > 0.f ? st.m[cb] + __log2f(l) : -INFINITY;
         }
       }
     }
@@ -1347,6 +1404,13 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(AttnParams p) {
 // 0 / 0, from the workgroup whose share holds their start.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int ctx_tiles(int ctx) { return ctx > 0 ? (ctx + kTile - 1) / kTile : 0; }
+
+// Split count of every kv slice of slice group kvg of row b (sk_nseg is
+// [rows, kv slices]).
+__device__ __forceinline__ void set_nseg(const AttnParams& p, int b, int kvg, int nseg) {
+  const int per = p.kvs_per_wg;
+  for (int j = 0; j < per; ++j) p.sk_nseg[int64_t(b) * (p.kvh * p.nslices) + kvg * per + j] = nseg;
+}
 
 // NaN output rows for every head of slice group kvg of row b.
 __device__ void write_nan_rows(const AttnParams& p, int b, int kvg) {
@@ -1442,10 +1506,10 @@ paged_decode_sk_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
           const int owner = W > 0 ? min(P, W - 1) / S : 0;
           if (owner == w) {
             write_nan_rows(p, r / groups, r % groups);
-            p.sk_nseg[r] = 0;
+            set_nseg(p, r / groups, r % groups, 0);
           }
         } else if (P / S == w) {
-          p.sk_nseg[r] = (P + t - 1) / S - P / S + 1;
+          set_nseg(p, r / groups, r % groups, (P + t - 1) / S - P / S + 1);
         }
       }
       P += t;
@@ -1474,6 +1538,271 @@ paged_decode_sk_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
     P += t;
     ++r;
     if (r < R && P < end) ctx = uniform(ctx_lens[r / groups]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Stream-K mixed launch.  The work list is every prefill item (chunk i, kv
+// slice, query tile; query tile fastest) followed by every decode row unit
+// (row, slice group), each a run of 32-key tiles: a prefill item's tiles stop
+// at the last key its queries see, a decode unit has ceil(ctx / 32).  The
+// concatenated tiles are cut into equal shares exactly as in the paged decode
+// launch, so one long prefill chunk, many short ones and the decode rows all
+// spread over every CU; a prefill tile (32 keys x one query tile of every
+// head of the slice) and a decode tile (32 keys x every head of the group)
+// count the same.  Items that span several shares write partials; sk_nseg
+// [row, kv slice] gets every row's split count from the workgroup holding the
+// item's first tile.
+// ---------------------------------------------------------------------------
+struct ChunkGeo {
+  int sq, sk, prefix, ntq;
+};
+
+__device__ __forceinline__ ChunkGeo chunk_geo(const int32_t* cu_q, const int32_t* cu_k, int i,
+                                              int qtile) {
+  ChunkGeo c;
+  c.sq = cu_q[i + 1] - cu_q[i];
+  c.sk = cu_k[i + 1] - cu_k[i];
+  c.prefix = c.sk - c.sq;
+  c.ntq = (c.sq > 0 && c.sk > 0) ? (c.sq + qtile - 1) / qtile : 0;
+  return c;
+}
+
+// Key tiles of query tile qt: its last query sees keys [0, prefix + last + 1).
+__device__ __forceinline__ int qtile_tiles(const ChunkGeo& c, int qtile, int qt) {
+  const int keys = qt + 1 < c.ntq ? c.prefix + (qt + 1) * qtile : c.sk;
+  return (keys + kTile - 1) / kTile;
+}
+
+// Key tiles of query tiles [0, q), q <= ntq.  Every tile but the last sees
+// prefix + 16 tpb u keys (u = 1, 2, ...; a query tile is 16 tpb tokens), so
+// its tile count is floor(tpb u / 2) + floor((prefix + 31 + 16 (tpb u mod 2))
+// / 32): a quadratic in u plus one of two constants, by the parity of tpb u.
+static_assert(kWaves * kPreNCB == 16, "query tiles are 16 tpb tokens");
+__device__ __forceinline__ int64_t qtile_cum(const ChunkGeo& c, int tpb, int q) {
+  if (q <= 0) return 0;
+  const int64_t n = min(q, c.ntq - 1);
+  const int64_t B = int64_t(c.prefix) + kTile - 1;
+  const int64_t c0 = B >> 5, c1 = (B + 16) >> 5;
+  const int64_t nodd = (tpb & 1) ? (n + 1) >> 1 : 0;
+  int64_t s = ((int64_t(tpb) * n * (n + 1) >> 1) - nodd) / 2 + nodd * c1 + (n - nodd) * c0;
+  if (q == c.ntq) s += (c.sk + kTile - 1) / kTile;
+  return s;
+}
+
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+  return v;
+}
+
+__device__ __forceinline__ int wave_max(int v) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v = max(v, __shfl_xor(v, d, 64));
+  return v;
+}
+
+template <int kEnc, bool kFresh, bool kLds>
+__global__ void __launch_bounds__(kThreads)
+mixed_sk_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k,
+                const int32_t* __restrict__ ctx_lens) {
+  static_assert(kSmemBytes >= kLdsStage, "the first LDS stage doubles as the scratch");
+  __shared__ __align__(16) char smem[kSmemBytes];
+  __shared__ __align__(16) char smem1[kLds ? kLdsStage : 16];
+  __shared__ __align__(16) char smem2[kLds ? kLdsQ : 16];
+  const int kvs_total = p.kvh * p.nslices;
+  const int qtile = kWaves * kPreNCB * p.tpb;
+  const int w = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wave = uniform(int(threadIdx.x >> 6));
+
+  // Prefill tiles, 64 chunks per pass: lane l takes chunk c0 + l.
+  auto chunk_tiles = [&](int i, int& tmax) {
+    tmax = 0;
+    if (i >= p.n_pre) return 0;
+    const ChunkGeo c = chunk_geo(cu_q, cu_k, i, qtile);
+    if (c.ntq == 0) return 0;
+    tmax = (c.sk + kTile - 1) / kTile;
+    return kvs_total * int(qtile_cum(c, p.tpb, c.ntq));
+  };
+  int Wpre = 0, Tmax = 0;
+  for (int c0 = 0; c0 < p.n_pre; c0 += 64) {
+    int tm;
+    const int t = chunk_tiles(c0 + lane, tm);
+    Wpre += wave_sum(t);
+    Tmax = max(Tmax, wave_max(tm));
+  }
+  Wpre = uniform(Wpre);
+
+  // Decode row units, as in the paged decode launch.
+  const int groups = kvs_total / p.kvs_per_wg;
+  const int R = p.n_dec * groups;
+  const int per_lane = (R + 63) / 64;
+  const int r0 = min(R, lane * per_lane);
+  const int r1 = min(R, r0 + per_lane);
+  constexpr int kCached = 4;
+  int cl[kCached];
+#pragma unroll
+  for (int i = 0; i < kCached; ++i) cl[i] = r0 + i < r1 ? ctx_lens[(r0 + i) / groups] : 0;
+  auto ctx_of = [&](int r) {
+    int c = 0;
+#pragma unroll
+    for (int i = 0; i < kCached; ++i) c = (r == r0 + i) ? cl[i] : c;
+    return r - r0 < kCached ? c : ctx_lens[r / groups];
+  };
+  int mine = 0, tmax = 0;
+  for (int r = r0; r < r1; ++r) {
+    const int t = ctx_tiles(ctx_of(r));
+    mine += t;
+    tmax = max(tmax, t);
+  }
+  int incl = mine;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int t = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += t;
+  }
+  const int Wdec = uniform(__shfl(incl, 63, 64));
+  Tmax = uniform(max(Tmax, wave_max(tmax)));
+  const int W = Wpre + Wdec;
+  int S = max(p.sk_min_share, (W + int(gridDim.x) - 1) / int(gridDim.x));
+  if (p.max_splits > 1) S = max(S, (Tmax + p.max_splits - 2) / (p.max_splits - 1));
+  const int start = w * S;
+  const int end = min(W, start + S);
+
+  // Decode rows: split counts and NaN rows of empty contexts (wave 0), and
+  // the row unit holding `start` if it falls in the decode part.
+  int found_r = R, found_p = 0, found_c = 0;
+  {
+    int P = Wpre + incl - mine;
+    for (int r = r0; r < r1; ++r) {
+      const int c = ctx_of(r);
+      const int t = ctx_tiles(c);
+      if (P <= start && start < P + t) {
+        found_r = r;
+        found_p = P;
+        found_c = c;
+      }
+      if (wave == 0) {
+        if (t == 0) {
+          const int owner = W > 0 ? min(P, W - 1) / S : 0;
+          if (owner == w) {
+            write_nan_rows(p, r / groups, r % groups);
+            set_nseg(p, r / groups, r % groups, 0);
+          }
+        } else if (P / S == w) {
+          set_nseg(p, r / groups, r % groups, (P + t - 1) / S - P / S + 1);
+        }
+      }
+      P += t;
+    }
+  }
+  if (start >= end) return;
+
+  // Walk state: prefill item (i, kvs, qt) or decode row unit r; P = the
+  // item's first tile.
+  bool pre = start < Wpre;
+  int i = 0, kvs = 0, qt = 0, r = R, P = 0, ctx = 0;
+  ChunkGeo geo{0, 0, 0, 0};
+  if (pre) {
+    int base = 0;
+    for (int c0 = 0; c0 < p.n_pre; c0 += 64) {
+      int tm;
+      const int t = chunk_tiles(c0 + lane, tm);
+      int inc = t;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const int u = __shfl_up(inc, d, 64);
+        if (lane >= d) inc += u;
+      }
+      const int total = uniform(__shfl(inc, 63, 64));
+      if (start < base + total) {
+        const unsigned long long hit = __ballot(t > 0 && base + inc - t <= start && start < base + inc);
+        const int src = __ffsll(hit) - 1;
+        i = uniform(c0 + src);
+        P = uniform(base + __shfl(inc - t, src, 64));
+        break;
+      }
+      base += total;
+    }
+    geo = chunk_geo(cu_q, cu_k, i, qtile);
+    const int per_kvs = int(qtile_cum(geo, p.tpb, geo.ntq));
+    int off = start - P;
+    kvs = off / per_kvs;
+    off -= kvs * per_kvs;
+    int lo = 0, hi = geo.ntq - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (qtile_cum(geo, p.tpb, mid) <= off) lo = mid; else hi = mid - 1;
+    }
+    qt = uniform(lo);
+    kvs = uniform(kvs);
+    P = uniform(P + kvs * per_kvs + int(qtile_cum(geo, p.tpb, qt)));
+  } else {
+    const unsigned long long hit = __ballot(found_r < R);
+    const int src = hit ? __ffsll(hit) - 1 : 0;
+    r = uniform(__shfl(found_r, src, 64));
+    P = uniform(__shfl(found_p, src, 64));
+    ctx = uniform(__shfl(found_c, src, 64));
+  }
+
+  while (P < end) {
+    if (pre) {
+      const int T = qtile_tiles(geo, qtile, qt);
+      const int t0 = max(start, P) - P;
+      const int t1 = min(end, P + T) - P;
+      const int nseg = (P + T - 1) / S - P / S + 1;
+      if (P >= start) {
+        // This share holds the item's first tile: record the rows' split count.
+        const int q0 = qt * qtile;
+        const int nq = min(qtile, geo.sq - q0);
+        if (int(threadIdx.x) < nq) {
+          const int64_t row = int64_t(p.n_dec) + cu_q[i] + q0 + threadIdx.x;
+          p.sk_nseg[row * kvs_total + kvs] = nseg;
+        }
+      }
+      prefill_segment<kEnc, kFresh>(p, smem, i, qt, kvs, t0, t1, nseg == 1 ? -1 : w - P / S);
+      P += T;
+      if (++qt == geo.ntq) {
+        qt = 0;
+        if (++kvs == kvs_total) {
+          kvs = 0;
+          do {
+            ++i;
+            if (i < p.n_pre) geo = chunk_geo(cu_q, cu_k, i, qtile);
+          } while (i < p.n_pre && geo.ntq == 0);
+          if (i >= p.n_pre) {
+            pre = false;
+            r = 0;
+            ctx = R > 0 ? uniform(ctx_lens[0]) : 0;
+          }
+        }
+      }
+    } else {
+      if constexpr (!kFresh) {
+        if (r >= R) break;
+        const int b = r / groups;
+        const int t = ctx_tiles(ctx);
+        if (t > 0) {
+          const int t0 = max(start, P) - P;
+          const int t1 = min(end, P + t) - P;
+          const int nseg = (P + t - 1) / S - P / S + 1;
+          const int split = nseg == 1 ? -1 : w - P / S;
+          if constexpr (kLds) {
+            decode_segment_lds(p, smem, smem1, smem2, p.block_tables + int64_t(b) * p.bt_stride,
+                               b, r - b * groups, ctx, t0, t1, split);
+          } else {
+            decode_segment<kEnc>(p, smem, p.block_tables + int64_t(b) * p.bt_stride, b,
+                                 r - b * groups, ctx, t0, t1, split);
+          }
+        }
+        P += t;
+        ++r;
+        if (r < R && P < end) ctx = uniform(ctx_lens[r / groups]);
+      } else {
+        break;
+      }
+    }
   }
 }
 
@@ -1518,7 +1847,11 @@ __global__ void __launch_bounds__(kThreads) varlen_kernel(AttnParams p) {
   }
   int i, qt, kvs, split;
   if (!find_prefill_unit(p, u, i, qt, kvs, split)) return;
-  prefill_unit<kEnc, kFresh>(p, smem, i, qt, kvs, split);
+  const int sk = p.cu_k[i + 1] - p.cu_k[i];
+  const int nsplit = max(1, (sk + p.split_tokens - 1) / p.split_tokens);
+  const int per = p.split_tokens / kTile;
+  prefill_segment<kEnc, kFresh>(p, smem, i, qt, kvs, split * per, (split + 1) * per,
+                                nsplit == 1 ? -1 : split);
 }
 
 // Split-K merge: one wave per (query row, head), lane l owning dims 2l and
@@ -1536,19 +1869,23 @@ __global__ void __launch_bounds__(64 * kMergeWaves) merge_kernel(AttnParams p, i
   const int head = int(wv - row * p.num_heads);
   int nsplit;
   if (p.sk_nseg != nullptr) {
-    // Stream-K: the head's slice group -> its row unit's split count.
+    // Stream-K: the split count of the head's kv slice in this row.
     const int g = head / p.group;
     const int kvs = g * p.nslices + (head - g * p.group) / p.hs;
-    const int groups = (p.kvh * p.nslices) / p.kvs_per_wg;
-    nsplit = p.sk_nseg[row * groups + kvs / p.kvs_per_wg];
+    nsplit = p.sk_nseg[row * (p.kvh * p.nslices) + kvs];
   } else if (row < p.n_dec) {
     const int ctx = p.ctx_lens[row];
     nsplit = ctx > 0 ? (ctx + p.chunk_tokens - 1) / p.chunk_tokens : 1;
   } else {
-    // Prefill row -> its chunk (cu_q is prefill-relative).
+    // Prefill row -> its chunk (cu_q is prefill-relative and nondecreasing):
+    // i = #{j in 1 .. n_pre - 1 : cu_q[j] <= r}, counted 64 entries per load.
     const int r = int(row - p.n_dec);
     int i = 0;
-    while (i + 1 < p.n_pre && p.cu_q[i + 1] <= r) ++i;
+    for (int j0 = 1; j0 < p.n_pre; j0 += 64) {
+      const int j = j0 + lane;
+      i += __popcll(__ballot(j < p.n_pre && p.cu_q[j] <= r));
+    }
+    i = uniform(i);
     const int sk = p.cu_k[i + 1] - p.cu_k[i];
     nsplit = max(1, (sk + p.split_tokens - 1) / p.split_tokens);
   }
@@ -1602,7 +1939,7 @@ __global__ void __launch_bounds__(64 * kMergeWaves) merge_kernel(AttnParams p, i
   }
   const float inv = 1.f / l;
   uint16_t* dst = p.out + row * p.o_st + int64_t(head) * p.o_sh + 2 * lane;
-  *reinterpret_cast<uint32_t*>(dst) = pack_bf16x2(acc0 * inv, acc1 * inv);
+  *reinterpret_cast<uint32_t*>(dst) = pack_bf16x2_fast(acc0 * inv, acc1 * inv);
 }
 
 void launch_merge(const AttnParams& p, int64_t rows, hipStream_t st) {
@@ -1685,17 +2022,21 @@ SkPlan plan_stream_k(int64_t rows, int64_t heads, int64_t max_ctx) {
 }
 
 // Workspace of a stream-K launch: the partials, then one int32 split count
-// per row unit (256-byte aligned).
-size_t sk_workspace_bytes(int64_t rows, int64_t heads, int64_t groups, int max_splits) {
+// per (row, kv slice) (256-byte aligned).
+size_t sk_partial_part(int64_t rows, int64_t heads, int max_splits) {
   const size_t part = size_t(rows) * size_t(heads) * size_t(max_splits) * (kD + 1) * sizeof(float);
-  return (part + 255) / 256 * 256 + size_t(rows) * size_t(groups) * sizeof(int) + 256;
+  return (part + 255) / 256 * 256;
+}
+size_t sk_workspace_bytes(int64_t rows, int64_t heads, int64_t kv_slices, int max_splits) {
+  return sk_partial_part(rows, heads, max_splits) + size_t(rows) * size_t(kv_slices) * sizeof(int) +
+         256;
 }
 
 // Keys per prefill split: an eighth of the longest key range, at least 512
 // (the long chunk of a mixed batch then fills the CUs with its splits).
 int plan_prefill_split(int64_t max_seqlen_k) {
   const int forced = env_int("KVC_PREFILL_SPLIT", 0);
-  if (forced > 0) return forced;
+  if (forced > 0) return (forced + kTile - 1) / kTile * kTile;
   int64_t ks = (max_seqlen_k + 7) / 8;
   ks = ((ks + kTile - 1) / kTile) * kTile;
   return int(ks < 512 ? 512 : ks);
@@ -1778,6 +2119,41 @@ void launch_decode_enc(const AttnParams& p, int grid, hipStream_t st) {
 }
 
 template <int kEnc>
+void launch_mixed_enc(const AttnParams& p, int grid, bool fresh, bool lds, hipStream_t st) {
+  if (fresh) {
+    if constexpr (kEnc == kBF16)
+      mixed_sk_kernel<kBF16, true, false><<<grid, kThreads, 0, st>>>(p, p.cu_q, p.cu_k, p.ctx_lens);
+  } else if (lds) {
+    if constexpr (kEnc == kBF16)
+      mixed_sk_kernel<kBF16, false, true><<<grid, kThreads, 0, st>>>(p, p.cu_q, p.cu_k, p.ctx_lens);
+  } else {
+    mixed_sk_kernel<kEnc, false, false><<<grid, kThreads, 0, st>>>(p, p.cu_q, p.cu_k, p.ctx_lens);
+  }
+}
+
+// Stream-K plan of a mixed launch: the split cap of the paged decode plan
+// over the longest item (decode context or prefill key range).
+// Shares can be one tile, so an item of T tiles may span T + 1 workgroups;
+// the cap is 64 splits and the partials' byte bound.
+SkPlan plan_mixed(int64_t num_q_tokens, int64_t num_heads, int64_t num_decode_rows,
+                  int64_t max_ctx, int64_t max_seqlen_k) {
+  const int64_t longest = std::max<int64_t>(num_decode_rows > 0 ? max_ctx : 0, max_seqlen_k);
+  SkPlan sp{true, int(device_cus()), 2};
+  int64_t ms = (longest + kTile - 1) / kTile + 1;
+  const int64_t per_split = num_q_tokens * num_heads * (kD + 1) * int64_t(sizeof(float));
+  const int64_t cap = per_split > 0 ? kSkMaxPartialBytes / per_split : 64;
+  ms = std::min<int64_t>(std::min<int64_t>(ms, 64), cap);
+  sp.max_splits = int(ms < 2 ? 2 : ms);
+  return sp;
+}
+
+// The stream-K mixed partition is opt-in (KVC_MIXED_STREAMK=1): a prefill
+// segment carries a query load and a partial write, and shares that chain
+// several short items pay them in sequence, so one workgroup per unit is
+// still the faster default.
+bool mixed_stream_k() { return env_int("KVC_MIXED_STREAMK", 0) != 0; }
+
+template <int kEnc>
 void launch_varlen_enc(const AttnParams& p, int grid, bool fresh, hipStream_t st) {
   if (fresh) {
     if constexpr (kEnc == kBF16) varlen_kernel<kBF16, true><<<grid, kThreads, 0, st>>>(p);
@@ -1799,7 +2175,7 @@ extern "C" size_t kvc_paged_decode_workspace_bytes(int64_t batch, int64_t num_he
   const HeadPlan hp = plan_heads(num_heads, num_kv_heads);
   const int64_t max_ctx = max_blocks_per_seq * page_size;
   const SkPlan sp = plan_stream_k(batch, num_heads, max_ctx);
-  if (sp.on) return sk_workspace_bytes(batch, num_heads, hp.groups, sp.max_splits);
+  if (sp.on) return sk_workspace_bytes(batch, num_heads, num_kv_heads * hp.nslices, sp.max_splits);
   const int ch = plan_decode_chunk(batch, hp.groups, max_ctx);
   const int64_t splits = max_ctx > 0 ? (max_ctx + ch - 1) / ch : 1;
   return partial_bytes(batch, num_heads, splits);
@@ -1838,7 +2214,7 @@ extern "C" int kvc_paged_decode(const void* q, int64_t q_stride_b, int64_t q_str
 
   const HeadPlan hp = plan_heads(num_heads, num_kv_heads);
   AttnParams p{};
-  p.merge_first = kMergeBatch;
+  p.merge_first = 0;  // most rows of these launches are not split
   p.q = static_cast<const uint16_t*>(q);
   p.q_st = q_stride_b;
   p.q_sh = q_stride_h;
@@ -1869,13 +2245,12 @@ extern "C" int kvc_paged_decode(const void* q, int64_t q_stride_b, int64_t q_str
     // falls inside a row); longer rows of a ragged batch load the rest later.
     const int64_t units = batch * hp.groups;
     p.merge_first = int(std::min<int64_t>(kMergeBatch, (sp.grid + units - 1) / units + 1));
-    const size_t need = sk_workspace_bytes(batch, num_heads, hp.groups, sp.max_splits);
+    const size_t need = sk_workspace_bytes(batch, num_heads, num_kv_heads * hp.nslices, sp.max_splits);
     KVC_REQUIRE(workspace != nullptr && workspace_bytes >= need, KVC_ERR_WORKSPACE,
                 "paged_decode: workspace of %zu bytes needed (got %zu)", need, workspace_bytes);
     set_partials(p, workspace, batch);
-    const size_t part = size_t(batch) * size_t(num_heads) * size_t(p.max_splits) * (kD + 1) *
-                        sizeof(float);
-    p.sk_nseg = reinterpret_cast<int*>(static_cast<char*>(workspace) + (part + 255) / 256 * 256);
+    p.sk_nseg = reinterpret_cast<int*>(static_cast<char*>(workspace) +
+                                       sk_partial_part(batch, num_heads, p.max_splits));
     p.chunk_tokens = kTile;
     switch (kv_dtype) {
       case KVC_KV_BF16:
@@ -1933,6 +2308,11 @@ extern "C" size_t kvc_varlen_workspace_bytes(int64_t num_q_tokens, int64_t num_h
                                              int64_t page_size, int64_t max_blocks_per_seq) {
   if (num_q_tokens <= 0 || num_kv_heads <= 0 || head_dim != kD) return 0;
   const HeadPlan hp = plan_heads(num_heads, num_kv_heads);
+  if (mixed_stream_k()) {
+    const SkPlan sp = plan_mixed(num_q_tokens, num_heads, num_decode_rows,
+                                 max_blocks_per_seq * page_size, max_seqlen_k);
+    return sk_workspace_bytes(num_q_tokens, num_heads, num_kv_heads * hp.nslices, sp.max_splits);
+  }
   int64_t splits = 1;
   if (num_decode_rows > 0) {
     const int64_t max_ctx = max_blocks_per_seq * page_size;
@@ -1994,7 +2374,7 @@ extern "C" int kvc_varlen_attention(
 
   const HeadPlan hp = plan_heads(num_heads, num_kv_heads);
   AttnParams p{};
-  p.merge_first = kMergeBatch;
+  p.merge_first = 0;  // most rows of these launches are not split
   p.q = static_cast<const uint16_t*>(q);
   p.q_st = q_stride_t;
   p.q_sh = q_stride_h;
@@ -2039,6 +2419,45 @@ extern "C" int kvc_varlen_attention(
   p.vf = static_cast<const uint16_t*>(v_fresh);
   p.vf_st = vf_stride_t;
   p.vf_sh = vf_stride_h;
+  if (mixed_stream_k()) {
+    // One workgroup per CU over the concatenated tiles of every prefill item
+    // and decode row unit (mixed_sk_kernel), then the merge over every row.
+    const int64_t kv_slices = num_kv_heads * hp.nslices;
+    const int64_t max_ctx = max_blocks_per_seq * page_size;
+    const int64_t qtile = int64_t(kWaves) * kPreNCB * hp.tpb;
+    const int64_t pre_bound =
+        kv_slices * (num_q_tokens / qtile + num_prefill + 1) * ((max_seqlen_k + kTile - 1) / kTile);
+    const int64_t dec_bound = num_decode_rows * kv_slices * ((max_ctx + kTile - 1) / kTile);
+    KVC_REQUIRE(pre_bound + dec_bound < (int64_t(1) << 30), KVC_ERR_VALUE,
+                "varlen_attention: launch too large");
+    const SkPlan sp = plan_mixed(num_q_tokens, num_heads, num_decode_rows, max_ctx, max_seqlen_k);
+    p.chunk_tokens = kTile;
+    p.max_splits = sp.max_splits;
+    // Shares as small as one tile: a prefill segment costs a query load and
+    // an epilogue, so short items are better spread than queued.
+    p.sk_min_share = 1;
+    p.merge_first = 0;
+    const size_t need = sk_workspace_bytes(num_q_tokens, num_heads, kv_slices, sp.max_splits);
+    KVC_REQUIRE(workspace != nullptr && workspace_bytes >= need, KVC_ERR_WORKSPACE,
+                "varlen_attention: workspace of %zu bytes needed (got %zu)", need,
+                workspace_bytes);
+    set_partials(p, workspace, num_q_tokens);
+    p.sk_nseg = reinterpret_cast<int*>(static_cast<char*>(workspace) +
+                                       sk_partial_part(num_q_tokens, num_heads, p.max_splits));
+    hipStream_t st = as_stream(stream);
+    const int enc = fresh ? KVC_KV_BF16 : kv_dtype;
+    const bool lds = !fresh && enc == KVC_KV_BF16 && hp.kvs_per_wg == 4 && hp.nslices == 1 &&
+                     env_int("KVC_DECODE_LDS", 1) != 0;
+    switch (enc) {
+      case KVC_KV_BF16: launch_mixed_enc<kBF16>(p, sp.grid, fresh, lds, st); break;
+      case KVC_KV_INT8_TOKHEAD: launch_mixed_enc<kI8Tok>(p, sp.grid, false, false, st); break;
+      default: launch_mixed_enc<kI8Chan>(p, sp.grid, false, false, st); break;
+    }
+    rc = check_launch("varlen_attention");
+    if (rc != KVC_OK) return rc;
+    launch_merge(p, num_q_tokens, st);
+    return check_launch("varlen_attention merge");
+  }
   p.max_splits = int(max_splits);
   const size_t need = partial_bytes(num_q_tokens, num_heads, max_splits);
   KVC_REQUIRE(need == 0 || (workspace != nullptr && workspace_bytes >= need), KVC_ERR_WORKSPACE,

@@ -44,19 +44,19 @@ def test_workspace_queries_are_host_only():
     # 32 keys) of all rows' tiles, so a row of up to 4096 keys (128 tiles) is
     # split at most 128 / 8 + 1 = 17 ways.  The workspace holds fp32 partials
     # (128 dims + 1 log-sum-exp per row, head and split), 256-byte aligned,
-    # then one int32 split count per (row, kv-head group), plus 256 bytes.
+    # then one int32 split count per (row, kv slice), plus 256 bytes.
     q = _native.query
     part = 64 * 32 * 17 * 129 * 4
     assert q("kvc_paged_decode_workspace_bytes", 64, 32, 4, 128, 256, 16) == \
-        (part + 255) // 256 * 256 + 64 * 4 + 256
+        (part + 255) // 256 * 256 + 64 * 4 * 4 + 256
     # Splits are capped at 64 however long the rows are.
     part = 4 * 32 * 64 * 129 * 4
     assert q("kvc_paged_decode_workspace_bytes", 4, 32, 4, 128, 256, 1024) == \
-        (part + 255) // 256 * 256 + 4 * 4 + 256
-    # 32 kv heads form 4 groups of 8 kv heads per workgroup: 4 counts per row.
+        (part + 255) // 256 * 256 + 4 * 4 * 4 + 256
+    # 32 kv heads: 32 counts per row.
     part = 8 * 32 * 17 * 129 * 4
     assert q("kvc_paged_decode_workspace_bytes", 8, 32, 32, 128, 256, 16) == \
-        (part + 255) // 256 * 256 + 8 * 4 * 4 + 256
+        (part + 255) // 256 * 256 + 8 * 32 * 4 + 256
 
 
 def test_bad_arguments_map_to_python_exceptions():

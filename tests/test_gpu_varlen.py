@@ -19,6 +19,14 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
+@pytest.fixture(params=["units", "stream-k"])
+def partition(request, monkeypatch):
+    """Both launch partitions of the mixed kernel: one workgroup per prefill
+    unit (the default) and the stream-K cut of all items' tiles."""
+    monkeypatch.setenv("KVC_MIXED_STREAMK", "1" if request.param == "stream-k" else "0")
+    return request.param
+
+
 def _mixed_case(H, KVH, dec_lens, chunks, seed, kv="bf16"):
     """chunks: list of (prefix, chunk_len).  Returns inputs on the device."""
     g = torch.Generator().manual_seed(seed)
@@ -57,23 +65,23 @@ def _check_mixed(c, label, scale=128 ** -0.5):
     return assert_attention_close(out, ref, label)
 
 
-def test_prefill_chunks_with_prefixes_small():
+def test_prefill_chunks_with_prefixes_small(partition):
     c = _mixed_case(32, 4, [], [(0, 40), (300, 17), (1000, 256)], seed=1)
     _check_mixed(c, "prefill-only")
 
 
-def test_mixed_decode_plus_prefill_small():
+def test_mixed_decode_plus_prefill_small(partition):
     c = _mixed_case(32, 4, [1, 255, 256, 257, 3000], [(0, 33), (512, 64), (2048, 100)], seed=2)
     _check_mixed(c, "mixed-small")
 
 
 @pytest.mark.parametrize("heads,kv_heads", [(16, 8), (32, 32), (12, 4), (64, 2)])
-def test_mixed_gqa_groupings(heads, kv_heads):
+def test_mixed_gqa_groupings(heads, kv_heads, partition):
     c = _mixed_case(heads, kv_heads, [900, 17], [(0, 20), (700, 45)], seed=heads + kv_heads)
     _check_mixed(c, f"mixed-gqa-{heads}/{kv_heads}")
 
 
-def test_stall_free_mixed_batch_full_shape():
+def test_stall_free_mixed_batch_full_shape(partition):
     # Four prefill chunks of 256 tokens with cached prefixes 0/512/2048/8192
     # plus 60 decode rows with contexts U[256, 4096], 32q/4kv, page 256.
     dec = uniform_lengths(60, 256, 4096, seed=3)
@@ -81,7 +89,26 @@ def test_stall_free_mixed_batch_full_shape():
     _check_mixed(c, "stall-free-full")
 
 
-def test_fresh_kv_prefill_without_block_tables():
+def test_many_chunks_empty_chunks_and_empty_context(partition):
+    # 70 prefill chunks (more than one 64-chunk pass of the stream-K scan),
+    # every ninth of them empty (prefix only), plus decode rows with an empty
+    # context (NaN row) between non-empty ones.
+    rng = np.random.default_rng(11)
+    chunks = [(int(rng.integers(0, 300)), 0 if i % 9 == 4 else int(rng.integers(1, 24)))
+              for i in range(70)]
+    c = _mixed_case(32, 4, [40, 0, 700], chunks, seed=11)
+    _check_mixed(c, "many-chunks")
+
+
+def test_long_chunk_many_query_tiles(partition):
+    # 64 q / 2 kv heads: 16-head slices and 16-token query tiles, so a
+    # 1100-token chunk spans 69 query tiles (the item search crosses a
+    # 64-tile pass).
+    c = _mixed_case(64, 2, [300], [(100, 1100), (0, 5)], seed=12)
+    _check_mixed(c, "long-chunk")
+
+
+def test_fresh_kv_prefill_without_block_tables(partition):
     # No prefix cache: keys are the step's own k/v rows, causal inside each
     # sequence (attention.py:195-199).
     g = torch.Generator().manual_seed(5)
