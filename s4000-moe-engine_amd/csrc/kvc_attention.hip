@@ -1072,6 +1072,401 @@ __device__ void decode_segment_lds(const AttnParams& p, char* stage0, char* stag
   __syncthreads();
 }
 
+// The query against int8 key codes, as two int8 terms per dim: q ~= scale
+// (hi + lo / 254) with |hi|, |lo| <= 127, so q . k = scale (hi . k + lo . k /
+// 254) comes out of integer MFMAs with the codes used as stored (the error is
+// at most max|q| / 64516 per dim, below bf16's own rounding of q).  Lane
+// (lm, lg) holds dims 64 c + 16 lg .. +16 of column lm.
+typedef int i32x4v_t __attribute__((ext_vector_type(4)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+struct QueryI8 {
+  i32x4v_t hi[2], lo[2];
+  float scale;
+};
+
+__device__ __forceinline__ i32x4v_t mfma_i8(const u32x4_t& a, const i32x4v_t& b,
+                                            const i32x4v_t& c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4v_t, a), b, c, 0, 0, 0);
+}
+
+// 16x16 output, 16-deep bf16 product: lane (lm, lg) supplies row / column lm
+// and k = 4 lg .. +3 of each operand.
+__device__ __forceinline__ f32x4_t mfma_bf16_k16(const u32x2_t& a, const u32x2_t& b,
+                                                 const f32x4_t& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_t, a),
+                                                   __builtin_bit_cast(s16x4_t, b), c, 0, 0, 0);
+}
+
+// q[32] = dims 64 c + 16 lg + e (c = 0, 1; e < 16) of the lane's column.
+__device__ __forceinline__ QueryI8 quantise_query(const float (&q)[32]) {
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(q[i]));
+  amax = rows4_max(amax);
+  QueryI8 Q;
+  Q.scale = amax * (1.f / 127.f);
+  const float inv = amax > 0.f ? 127.f / amax : 0.f;
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      uint32_t hw = 0u, lw = 0u;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float t = q[16 * c + 4 * w + e] * inv;
+        const float h = __builtin_rintf(t);
+        const float l = __builtin_rintf((t - h) * 254.f);
+        hw |= (uint32_t(int(h)) & 0xffu) << (8 * e);
+        lw |= (uint32_t(int(l)) & 0xffu) << (8 * e);
+      }
+      Q.hi[c][w] = int(hw);
+      Q.lo[c][w] = int(lw);
+    }
+  }
+  return Q;
+}
+
+// One wave's half of an int8 tile: keys 16 kh + 4 lg + i (i < 4) of the
+// lane's S^T column, every dim of the output (o[jj][i] = dim 32 lg + 8 i + jj).
+struct KeyHalfState {
+  f32x4_t o[8];
+  float m, l;
+  float vb;  // lane-partial sum of the bf16 P operand (the +128 bias of V)
+};
+
+template <bool kMasked>
+__device__ __forceinline__ void attend_key_half_i8(KeyHalfState& st, const u32x4_t (&kc)[2],
+                                                   const u32x2_t (&vr)[4], const float (&ksc)[4],
+                                                   const float (&vsc)[4], const QueryI8& Q,
+                                                   int key0, int valid_end, int klim,
+                                                   float scale_log2, const LaneId& L) {
+  bool kvalid[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) kvalid[i] = !kMasked || (key0 + 4 * L.lg + i < valid_end);
+  i32x4v_t h = {0, 0, 0, 0}, lo = h;
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    h = mfma_i8(kc[c], Q.hi[c], h);
+    lo = mfma_i8(kc[c], Q.lo[c], lo);
+  }
+  const float qs = Q.scale * scale_log2;
+  float x[4];
+  float tmax = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float v = (float(h[i]) + float(lo[i]) * (1.f / 254.f)) * (qs * ksc[i]);
+    if constexpr (kMasked) {
+      const bool ok = kvalid[i] && (key0 + 4 * L.lg + i <= klim);
+      x[i] = ok ? v : -INFINITY;
+    } else {
+      x[i] = v;
+    }
+    tmax = fmaxf(tmax, x[i]);
+  }
+  tmax = rows4_max(tmax);
+  float alpha = 1.f;
+  if (__builtin_expect(__ballot(tmax > st.m + kRescaleLog2) != 0, 0)) {
+    const float m_new = fmaxf(st.m, tmax);
+    const float m_ref = (m_new == -INFINITY) ? 0.f : m_new;
+    alpha = __builtin_amdgcn_exp2f(st.m - m_ref);
+    st.m = m_new;
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      st.o[jj][0] *= alpha;
+      st.o[jj][1] *= alpha;
+      st.o[jj][2] *= alpha;
+      st.o[jj][3] *= alpha;
+    }
+  }
+  const float m_use = (st.m == -INFINITY) ? 0.f : st.m;
+  float pv[4], psum = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float pr = __builtin_amdgcn_exp2f(x[i] - m_use);
+    psum += pr;
+    pv[i] = kvalid[i] ? pr * vsc[i] : 0.f;
+  }
+  st.l = st.l * alpha + psum;
+  const u32x2_t pb = {pack_bf16x2_fast(pv[0], pv[1]), pack_bf16x2_fast(pv[2], pv[3])};
+  st.vb = st.vb * alpha + (bf16_bits_to_f32(pb[0] & 0xffffu) + bf16_bits_to_f32(pb[0] >> 16) +
+                           bf16_bits_to_f32(pb[1] & 0xffffu) + bf16_bits_to_f32(pb[1] >> 16));
+  // V^T operand of dims 8 lm + jj: byte jj of the lane's 4 key rows, as
+  // bf16 of (code + 128).
+  u32x2_t vq[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) vq[i] = vr[i] ^ 0x80808080u;
+#pragma unroll
+  for (int jj = 0; jj < 8; ++jj) {
+    const int dw = jj >> 2, sh = (jj & 3) * 8;
+    const float a0 = float((vq[0][dw] >> sh) & 0xffu), a1 = float((vq[1][dw] >> sh) & 0xffu);
+    const float a2 = float((vq[2][dw] >> sh) & 0xffu), a3 = float((vq[3][dw] >> sh) & 0xffu);
+    const u32x2_t va = {perm(__float_as_uint(a1), __float_as_uint(a0), kPermHiHi),
+                        perm(__float_as_uint(a3), __float_as_uint(a2), kPermHiHi)};
+    st.o[jj] = mfma_bf16_k16(va, pb, st.o[jj]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// LDS-staged decode segment, per-token-head int8 pool, a group of 4 kv heads
+// (512 B of each token row).  A ring of four stages holds 32-key tiles: K
+// codes [32][512] and V codes [32][512], unpadded, the 16-byte chunk c of row
+// r stored at chunk c ^ (r & 15) so that the rows a read touches fall on
+// different banks; then the tile's K and V scales (16 B per token: the
+// group's 4 heads).  Every wave issues exactly five 1 KiB DMA loads per tile
+// (two of K, two of V, and the K scales on wave 0, the V scales on wave 1, a
+// zero-length load into a dummy block on the others), so one vmcnt count
+// covers every wave.  A stage is read into registers as soon as its tile
+// lands and refilled four tiles ahead, so up to four tiles are in flight
+// under the arithmetic.  Wave w serves kv head w & 3 and keys 16 (w >> 2) ..
+// +15 of every tile; the two key halves of a head merge through LDS at the
+// end.
+// ---------------------------------------------------------------------------
+constexpr int kI8Rows = kTile * 512;
+constexpr int kI8Stage = 2 * kI8Rows + 2 * 1024;
+constexpr int kI8Ring = 4;
+constexpr int kLdsI8 = kI8Ring * kI8Stage + 1024;  // + the dummy block
+constexpr int kI8LoadsPerTile = 5;
+constexpr int kI8MergePitch = kD + 4;  // floats per (head, column) row of the merge block
+static_assert(4 * 16 * kI8MergePitch * 4 + 4 * 16 * 8 <= kI8Stage, "merge block fits a stage");
+
+constexpr int vmcnt_imm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
+
+// Wait until at most `tiles` tiles' loads of this wave are outstanding (the
+// immediate is static, so the count is switched over).
+__device__ __forceinline__ void wait_tiles_left(int tiles) {
+  switch (tiles) {
+    case 0: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
+    case 1: __builtin_amdgcn_s_waitcnt(vmcnt_imm(kI8LoadsPerTile)); break;
+    case 2: __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kI8LoadsPerTile)); break;
+    case 3: __builtin_amdgcn_s_waitcnt(vmcnt_imm(3 * kI8LoadsPerTile)); break;
+    default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(4 * kI8LoadsPerTile)); break;
+  }
+}
+
+__device__ void decode_segment_lds_i8(const AttnParams& p, char* ring, char* qlds,
+                                      const int32_t* bt, int b, int kvg, int ctx, int t0, int t1,
+                                      int split) {
+  const LaneId L = lane_id();
+  const int wave = uniform(int(threadIdx.x >> 6));
+  const int gl = wave & 3;   // kv head within the group
+  const int kh = wave >> 2;  // key half of every tile
+  const int g = kvg * 4 + gl;
+  b = uniform(b);
+  ctx = uniform(ctx);
+  t0 = uniform(t0);
+  t1 = uniform(t1);
+  const int ntiles = t1 > t0 ? t1 - t0 : 0;
+  const int c0 = t0 * kTile;
+
+  QueryI8 Q;
+  KeyHalfState st;
+#pragma unroll
+  for (int jj = 0; jj < 8; ++jj) st.o[jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  st.m = -INFINITY;
+  st.l = 0.f;
+  st.vb = 0.f;
+
+  const int tok = int(p.tok_bytes);
+  const int64_t grp_off = int64_t(kvg) * 512;
+  const int sc_tok = p.kvh * 4;  // bytes of scales per token
+  const uint32_t dummy = lds_addr(ring + kI8Ring * kI8Stage);
+  auto stage_of = [&](int j) { return ring + (j & (kI8Ring - 1)) * kI8Stage; };
+  // Wave w brings rows 2n, 2n + 1 (n = w, w + 8) of K and of V, then one
+  // scale block or the dummy load.
+  auto issue = [&](int tix) {
+    char* base = stage_of(tix);
+    const int key0 = uniform(c0 + tix * kTile);
+    const int blk = uniform(bt[key0 / p.page]);
+    const int64_t slot0 = int64_t(blk) * p.page + (key0 % p.page);
+    const i32x4_t kr = raw_rsrc(p.k_cache + slot0 * p.tok_bytes + grp_off, kTile * tok);
+    const i32x4_t vr = raw_rsrc(p.v_cache + slot0 * p.tok_bytes + grp_off, kTile * tok);
+    const uint32_t lb = lds_addr(base);
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const int n = wave + 8 * m;
+      const int row = 2 * n + (L.lane >> 5);
+      const int chunk = (L.lane & 31) ^ (row & 15);
+      const int voff = row * tok + chunk * 16;
+      dma_to_lds(kr, voff, lb + n * 1024);
+      dma_to_lds(vr, voff, lb + kI8Rows + n * 1024);
+    }
+    if (wave < 2) {
+      const float* sp = (wave == 0 ? p.k_scale : p.v_scale) + slot0 * p.kvh;
+      const i32x4_t sr = raw_rsrc(sp, kTile * sc_tok);
+      const int soff = L.lane < kTile ? L.lane * sc_tok + kvg * 16 : 0x40000000;
+      dma_to_lds(sr, soff, lb + 2 * kI8Rows + wave * 1024);
+    } else {
+      dma_to_lds(raw_rsrc(p.k_scale, 0), 0, dummy);
+    }
+  };
+  // The query rides the same DMA ahead of the first tiles: wave w brings
+  // columns 8 (w >> 2) .. + 7 of kv head w & 3 (columns past the head count
+  // repeat the last head; their results are never stored), 16-byte chunk c
+  // of column col at chunk c ^ col.
+  auto issue_q = [&]() {
+    const i32x4_t qr =
+        raw_rsrc(p.q + int64_t(b) * p.q_st, int(int64_t(p.num_heads) * p.q_sh * 2));
+    const uint32_t lb = lds_addr(qlds);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int col = 8 * kh + 4 * s + (L.lane >> 4);
+      const int head = g * p.group + min(col, p.hs - 1);
+      const int chunk = (L.lane & 15) ^ col;
+      dma_to_lds(qr, int(int64_t(head) * p.q_sh * 2) + chunk * 16,
+                 lb + (gl * 16 + 8 * kh + 4 * s) * 256);
+    }
+  };
+
+  // One tile's operands of this wave, read from its stage.
+  struct Regs {
+    u32x4_t kc[2];
+    u32x2_t vr[4];
+    float ksc[4], vsc[4];
+  };
+  auto read_stage = [&](const char* base, Regs& r) {
+    const int krow = 16 * kh + L.lm;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int chunk = (8 * gl + 4 * c + L.lg) ^ (krow & 15);
+      r.kc[c] = *reinterpret_cast<const u32x4_t*>(base + krow * 512 + chunk * 16);
+    }
+    const char* vb = base + kI8Rows;
+    const char* sb = base + 2 * kI8Rows;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = 16 * kh + 4 * L.lg + i;
+      const int chunk = (8 * gl + (L.lm >> 1)) ^ (row & 15);
+      r.vr[i] = *reinterpret_cast<const u32x2_t*>(vb + row * 512 + chunk * 16 + 8 * (L.lm & 1));
+      r.ksc[i] = *reinterpret_cast<const float*>(sb + row * 16 + gl * 4);
+      r.vsc[i] = *reinterpret_cast<const float*>(sb + 1024 + row * 16 + gl * 4);
+    }
+  };
+  auto compute = [&](int j, const Regs& r) {
+    const int key0 = c0 + j * kTile;
+    const int hkey0 = key0 + 16 * kh;
+    if (key0 + kTile <= ctx) {
+      attend_key_half_i8<false>(st, r.kc, r.vr, r.ksc, r.vsc, Q, hkey0, ctx, ctx - 1,
+                                p.scale_log2, L);
+    } else {
+      attend_key_half_i8<true>(st, r.kc, r.vr, r.ksc, r.vsc, Q, hkey0, ctx, ctx - 1,
+                               p.scale_log2, L);
+    }
+  };
+  // Step j: tile j is in registers `cur`; once tile j + 1 has landed (one
+  // barrier, which also retires every wave's reads of stage j), stage j is
+  // refilled with tile j + 4, tile j + 1 is read into `nxt`, and tile j is
+  // computed while those reads are in flight.
+  auto step = [&](int j, const Regs& cur, Regs& nxt) {
+    if (j + 1 < ntiles) wait_tiles_left(min(ntiles - 2 - j, kI8Ring - 2));
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): `cur` has arrived
+    __syncthreads();
+    if (j + kI8Ring < ntiles) issue(j + kI8Ring);
+    if (j + 1 < ntiles) read_stage(stage_of(j + 1), nxt);
+    compute(j, cur);
+  };
+
+  if (ntiles > 0) {
+    issue_q();
+    const int first = min(ntiles, kI8Ring);
+    for (int j = 0; j < first; ++j) issue(j);
+    wait_tiles_left(first);  // the query loads, issued first, have landed
+    __syncthreads();
+    {
+      const char* row = qlds + (gl * 16 + L.lm) * 256;
+      float qf[32];
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const u32x4_t w =
+              *reinterpret_cast<const u32x4_t*>(row + (((8 * c + 2 * L.lg + e) ^ L.lm) * 16));
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            qf[16 * c + 8 * e + 2 * k] = bf16_bits_to_f32(w[k] & 0xffffu);
+            qf[16 * c + 8 * e + 2 * k + 1] = bf16_bits_to_f32(w[k] >> 16);
+          }
+        }
+      }
+      Q = quantise_query(qf);
+    }
+    Regs ra, rb;
+    // Tile 0 lands (tiles 1 .. min(3, ntiles - 1) may still be in flight).
+    wait_tiles_left(min(ntiles - 1, kI8Ring - 1));
+    __syncthreads();
+    read_stage(stage_of(0), ra);
+    for (int j = 0; j < ntiles; j += 2) {
+      step(j, ra, rb);
+      if (j + 1 < ntiles) step(j + 1, rb, ra);
+    }
+  }
+
+  // Epilogue: each wave's o has the +128 V bias removed, then the key-half-1
+  // waves hand (o, m, l) to the key-half-0 waves through the first stage,
+  // which write the merged rows.  Lane (lm, lg) holds dims 32 lg + 8 i + jj.
+  const float l = rows4_sum(st.l);
+  const float bias = 128.f * rows4_sum(st.vb);
+  float* mo = reinterpret_cast<float*>(ring);
+  float* mml = mo + 4 * 16 * kI8MergePitch;
+  float* orow = mo + (gl * 16 + L.lm) * kI8MergePitch + 32 * L.lg;
+  __syncthreads();
+  if (kh == 1) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      reinterpret_cast<float4*>(orow + 8 * i)[0] =
+          make_float4(st.o[0][i] - bias, st.o[1][i] - bias, st.o[2][i] - bias, st.o[3][i] - bias);
+      reinterpret_cast<float4*>(orow + 8 * i)[1] =
+          make_float4(st.o[4][i] - bias, st.o[5][i] - bias, st.o[6][i] - bias, st.o[7][i] - bias);
+    }
+    if (L.lg == 0) {
+      mml[(gl * 16 + L.lm) * 2] = st.m;
+      mml[(gl * 16 + L.lm) * 2 + 1] = l;
+    }
+  }
+  __syncthreads();
+  if (kh == 0 && L.lm < p.hs) {
+    const float m1 = mml[(gl * 16 + L.lm) * 2], l1 = mml[(gl * 16 + L.lm) * 2 + 1];
+    const float mm = fmaxf(st.m, m1);
+    const float mref = mm == -INFINITY ? 0.f : mm;
+    const float a0 = __builtin_amdgcn_exp2f(st.m - mref), a1 = __builtin_amdgcn_exp2f(m1 - mref);
+    const float lt = a0 * l + a1 * l1;
+    const int head = g * p.group + L.lm;
+    float v[4][8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float4 u0 = reinterpret_cast<const float4*>(orow + 8 * i)[0];
+      const float4 u1 = reinterpret_cast<const float4*>(orow + 8 * i)[1];
+      const float o1[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) v[i][jj] = a0 * (st.o[jj][i] - bias) + a1 * o1[jj];
+    }
+    if (split < 0) {
+      const float inv = 1.f / lt;
+      uint16_t* dst = p.out + int64_t(b) * p.o_st + int64_t(head) * p.o_sh + 32 * L.lg;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<u32x4_t*>(dst + 8 * i) =
+            u32x4_t{pack_bf16x2_fast(v[i][0] * inv, v[i][1] * inv),
+                    pack_bf16x2_fast(v[i][2] * inv, v[i][3] * inv),
+                    pack_bf16x2_fast(v[i][4] * inv, v[i][5] * inv),
+                    pack_bf16x2_fast(v[i][6] * inv, v[i][7] * inv)};
+    } else {
+      const int64_t base = (int64_t(b) * p.num_heads + head) * p.max_splits + split;
+      const float il = lt > 0.f ? 1.f / lt : 0.f;
+      float* dst = p.part_o + base * kD + 32 * L.lg;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        reinterpret_cast<float4*>(dst + 8 * i)[0] =
+            make_float4(v[i][0] * il, v[i][1] * il, v[i][2] * il, v[i][3] * il);
+        reinterpret_cast<float4*>(dst + 8 * i)[1] =
+            make_float4(v[i][4] * il, v[i][5] * il, v[i][6] * il, v[i][7] * il);
+      }
+      if (L.lg == 0) p.part_lse[base] = lt > 0.f ? mref + __log2f(lt) : -INFINITY;
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+}
+
 // Fixed-chunk decode unit (the mixed varlen launch): chunk `chunk` of row b,
 // p.chunk_tokens keys per chunk.
 template <int kEnc>
@@ -1442,11 +1837,14 @@ template <int kEnc, bool kLds>
 __global__ void __launch_bounds__(kThreads)
 paged_decode_sk_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
                        const int32_t* __restrict__ ctx_lens) {
-  // kLds: bf16 pool with 4 kv heads per workgroup (decode_segment_lds); its
-  // two stages are separate LDS objects, the first doubling as the scratch of
-  // the register path.
-  __shared__ __align__(16) char smem[kLds ? kLdsStage : kDecodeSmem];
-  __shared__ __align__(16) char smem1[kLds ? kLdsStage : 16];
+  // kLds: 4 kv heads per workgroup staged through LDS, bf16
+  // (decode_segment_lds: two stages) or per-token-head int8
+  // (decode_segment_lds_i8: a four-stage ring); smem2 holds the query.
+  constexpr bool kBfLds = kLds && kEnc == kBF16;
+  constexpr bool kI8Lds = kLds && kEnc == kI8Tok;
+  static_assert(!kLds || kBfLds || kI8Lds, "no LDS-staged form for this encoding");
+  __shared__ __align__(16) char smem[kBfLds ? kLdsStage : (kI8Lds ? kLdsI8 : kDecodeSmem)];
+  __shared__ __align__(16) char smem1[kBfLds ? kLdsStage : 16];
   __shared__ __align__(16) char smem2[kLds ? kLdsQ : 16];
   const int groups = (p.kvh * p.nslices) / p.kvs_per_wg;
   const int R = p.n_dec * groups;
@@ -1527,9 +1925,12 @@ paged_decode_sk_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
       const int t0 = max(start, P) - P;
       const int t1 = min(end, P + t) - P;
       const int nseg = (P + t - 1) / S - P / S + 1;
-      if constexpr (kLds) {
+      if constexpr (kBfLds) {
         decode_segment_lds(p, smem, smem1, smem2, block_tables + int64_t(b) * p.bt_stride, b,
                            r - b * groups, ctx, t0, t1, nseg == 1 ? -1 : w - P / S);
+      } else if constexpr (kI8Lds) {
+        decode_segment_lds_i8(p, smem, smem2, block_tables + int64_t(b) * p.bt_stride, b,
+                              r - b * groups, ctx, t0, t1, nseg == 1 ? -1 : w - P / S);
       } else {
         decode_segment<kEnc>(p, smem, block_tables + int64_t(b) * p.bt_stride, b,
                              r - b * groups, ctx, t0, t1, nseg == 1 ? -1 : w - P / S);
@@ -2263,8 +2664,13 @@ extern "C" int kvc_paged_decode(const void* q, int64_t q_stride_b, int64_t q_str
         }
         break;
       case KVC_KV_INT8_TOKHEAD:
-        paged_decode_sk_kernel<kI8Tok, false>
-            <<<sp.grid, kThreads, 0, st>>>(p, block_tables, context_lens);
+        if (hp.kvs_per_wg == 4 && hp.nslices == 1 && env_int("KVC_DECODE_LDS", 1) != 0) {
+          paged_decode_sk_kernel<kI8Tok, true>
+              <<<sp.grid, kThreads, 0, st>>>(p, block_tables, context_lens);
+        } else {
+          paged_decode_sk_kernel<kI8Tok, false>
+              <<<sp.grid, kThreads, 0, st>>>(p, block_tables, context_lens);
+        }
         break;
       default:
         paged_decode_sk_kernel<kI8Chan, false>
