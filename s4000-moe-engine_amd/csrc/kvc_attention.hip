@@ -1469,15 +1469,18 @@ __device__ void decode_segment_lds_i8(const AttnParams& p, char* ring, char* qld
 
 // Fixed-chunk decode unit (the mixed varlen launch): chunk `chunk` of row b,
 // p.chunk_tokens keys per chunk.
+// bt_base is the launch's block-table argument (declared __restrict__ by the
+// kernel, so its reads stay scalar loads).
 template <int kEnc>
-__device__ void decode_unit(const AttnParams& p, char* smem, int b, int kvg, int chunk) {
+__device__ void decode_unit(const AttnParams& p, char* smem, const int32_t* bt_base, int b,
+                            int kvg, int chunk) {
   const int ctx = p.ctx_lens[b];
   const int nch = ctx > 0 ? (ctx + p.chunk_tokens - 1) / p.chunk_tokens : 1;
   if (chunk >= nch) return;  // uniform over the workgroup
   const int chunk_tiles = p.chunk_tokens / kTile;
   const int ntiles = (ctx + kTile - 1) / kTile;
   const int t0 = chunk * chunk_tiles;
-  decode_segment<kEnc>(p, smem, p.block_tables + int64_t(b) * p.bt_stride, b, kvg, ctx, t0,
+  decode_segment<kEnc>(p, smem, bt_base + int64_t(b) * p.bt_stride, b, kvg, ctx, t0,
                        min(t0 + chunk_tiles, ntiles), nch == 1 ? -1 : chunk);
 }
 
@@ -1489,8 +1492,8 @@ __device__ void decode_unit(const AttnParams& p, char* smem, int b, int kvg, int
 // otherwise it writes split-K partials at slot `split`.
 // ---------------------------------------------------------------------------
 template <int kEnc, bool kFresh>
-__device__ void prefill_segment(const AttnParams& p, char* smem, int i, int qt, int kvs, int t0,
-                                int t1, int split) {
+__device__ void prefill_segment(const AttnParams& p, char* smem, const int32_t* bt_base, int i,
+                                int qt, int kvs, int t0, int t1, int split) {
   const LaneId L = lane_id();
   const int wave = uniform(int(threadIdx.x >> 6));  // wave-uniform (scalar) index
   const int g = kvs / p.nslices;
@@ -1534,7 +1537,7 @@ __device__ void prefill_segment(const AttnParams& p, char* smem, int i, int qt, 
   const int k_end = uniform(min(t1 * kTile, min(sk, prefix + last_q + 1)));
   const int ntiles = k_end > k_begin ? (k_end - k_begin + kTile - 1) / kTile : 0;
 
-  const int32_t* bt = kFresh ? nullptr : p.block_tables + int64_t(p.n_dec + i) * p.bt_stride;
+  const int32_t* bt = kFresh ? nullptr : bt_base + int64_t(p.n_dec + i) * p.bt_stride;
   constexpr int kPitch = (kEnc == kBF16) ? kPitchBF16 : kPitchI8;
   constexpr int kRowBytes = (kEnc == kBF16) ? kD * 2 : kD;
   constexpr int kVecPerRow = kRowBytes / 16;
@@ -1782,7 +1785,7 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(AttnParams p) {
   __shared__ __align__(16) char smem[kDecodeSmem];
   int b, kvg, chunk;
   decode_unit_of(p, blockIdx.x, b, kvg, chunk);
-  decode_unit<kEnc>(p, smem, b, kvg, chunk);
+  decode_unit<kEnc>(p, smem, p.block_tables, b, kvg, chunk);
 }
 
 // ---------------------------------------------------------------------------
@@ -2006,7 +2009,7 @@ __device__ __forceinline__ int wave_max(int v) {
 template <int kEnc, bool kFresh, bool kLds>
 __global__ void __launch_bounds__(kThreads)
 mixed_sk_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k,
-                const int32_t* __restrict__ ctx_lens) {
+                const int32_t* __restrict__ ctx_lens, const int32_t* __restrict__ block_tables) {
   static_assert(kSmemBytes >= kLdsStage, "the first LDS stage doubles as the scratch");
   __shared__ __align__(16) char smem[kSmemBytes];
   __shared__ __align__(16) char smem1[kLds ? kLdsStage : 16];
@@ -2162,7 +2165,8 @@ mixed_sk_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t* _
           p.sk_nseg[row * kvs_total + kvs] = nseg;
         }
       }
-      prefill_segment<kEnc, kFresh>(p, smem, i, qt, kvs, t0, t1, nseg == 1 ? -1 : w - P / S);
+      prefill_segment<kEnc, kFresh>(p, smem, block_tables, i, qt, kvs, t0, t1,
+                                    nseg == 1 ? -1 : w - P / S);
       P += T;
       if (++qt == geo.ntq) {
         qt = 0;
@@ -2190,10 +2194,10 @@ mixed_sk_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t* _
           const int nseg = (P + t - 1) / S - P / S + 1;
           const int split = nseg == 1 ? -1 : w - P / S;
           if constexpr (kLds) {
-            decode_segment_lds(p, smem, smem1, smem2, p.block_tables + int64_t(b) * p.bt_stride,
+            decode_segment_lds(p, smem, smem1, smem2, block_tables + int64_t(b) * p.bt_stride,
                                b, r - b * groups, ctx, t0, t1, split);
           } else {
-            decode_segment<kEnc>(p, smem, p.block_tables + int64_t(b) * p.bt_stride, b,
+            decode_segment<kEnc>(p, smem, block_tables + int64_t(b) * p.bt_stride, b,
                                  r - b * groups, ctx, t0, t1, split);
           }
         }
@@ -2235,14 +2239,15 @@ __device__ __forceinline__ bool find_prefill_unit(const AttnParams& p, int u, in
 // Grid order: the prefill units first, then the decode units, so that the
 // long prefill units do not start after the memory-bound decode units.
 template <int kEnc, bool kFresh>
-__global__ void __launch_bounds__(kThreads) varlen_kernel(AttnParams p) {
+__global__ void __launch_bounds__(kThreads)
+varlen_kernel(AttnParams p, const int32_t* __restrict__ block_tables) {
   __shared__ __align__(16) char smem[kSmemBytes];
   const int u = blockIdx.x;
   if (u >= p.pre_units) {
     if constexpr (!kFresh) {
       int b, kvg, chunk;
       decode_unit_of(p, u - p.pre_units, b, kvg, chunk);
-      decode_unit<kEnc>(p, smem, b, kvg, chunk);
+      decode_unit<kEnc>(p, smem, block_tables, b, kvg, chunk);
     }
     return;
   }
@@ -2251,8 +2256,8 @@ __global__ void __launch_bounds__(kThreads) varlen_kernel(AttnParams p) {
   const int sk = p.cu_k[i + 1] - p.cu_k[i];
   const int nsplit = max(1, (sk + p.split_tokens - 1) / p.split_tokens);
   const int per = p.split_tokens / kTile;
-  prefill_segment<kEnc, kFresh>(p, smem, i, qt, kvs, split * per, (split + 1) * per,
-                                nsplit == 1 ? -1 : split);
+  prefill_segment<kEnc, kFresh>(p, smem, block_tables, i, qt, kvs, split * per,
+                                (split + 1) * per, nsplit == 1 ? -1 : split);
 }
 
 // Split-K merge: one wave per (query row, head), lane l owning dims 2l and
@@ -2523,12 +2528,15 @@ template <int kEnc>
 void launch_mixed_enc(const AttnParams& p, int grid, bool fresh, bool lds, hipStream_t st) {
   if (fresh) {
     if constexpr (kEnc == kBF16)
-      mixed_sk_kernel<kBF16, true, false><<<grid, kThreads, 0, st>>>(p, p.cu_q, p.cu_k, p.ctx_lens);
+      mixed_sk_kernel<kBF16, true, false><<<grid, kThreads, 0, st>>>(p, p.cu_q, p.cu_k, p.ctx_lens,
+                                                                 p.block_tables);
   } else if (lds) {
     if constexpr (kEnc == kBF16)
-      mixed_sk_kernel<kBF16, false, true><<<grid, kThreads, 0, st>>>(p, p.cu_q, p.cu_k, p.ctx_lens);
+      mixed_sk_kernel<kBF16, false, true><<<grid, kThreads, 0, st>>>(p, p.cu_q, p.cu_k, p.ctx_lens,
+                                                                 p.block_tables);
   } else {
-    mixed_sk_kernel<kEnc, false, false><<<grid, kThreads, 0, st>>>(p, p.cu_q, p.cu_k, p.ctx_lens);
+    mixed_sk_kernel<kEnc, false, false><<<grid, kThreads, 0, st>>>(p, p.cu_q, p.cu_k, p.ctx_lens,
+                                                                 p.block_tables);
   }
 }
 
@@ -2557,9 +2565,10 @@ bool mixed_stream_k() { return env_int("KVC_MIXED_STREAMK", 0) != 0; }
 template <int kEnc>
 void launch_varlen_enc(const AttnParams& p, int grid, bool fresh, hipStream_t st) {
   if (fresh) {
-    if constexpr (kEnc == kBF16) varlen_kernel<kBF16, true><<<grid, kThreads, 0, st>>>(p);
+    if constexpr (kEnc == kBF16)
+      varlen_kernel<kBF16, true><<<grid, kThreads, 0, st>>>(p, p.block_tables);
   } else {
-    varlen_kernel<kEnc, false><<<grid, kThreads, 0, st>>>(p);
+    varlen_kernel<kEnc, false><<<grid, kThreads, 0, st>>>(p, p.block_tables);
   }
 }
 
