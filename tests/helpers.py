@@ -52,3 +52,38 @@ def kv_float_from_torch(cache: torch.Tensor) -> np.ndarray:
     if cache.dtype == torch.bfloat16:
         return ko.bf16_to_f32(bits(cache))
     raise TypeError(cache.dtype)
+
+
+def p17_unit_inputs():
+    """The per-channel int8 unit case of tests/p17_kv_int8.py:64-136 (N=512,
+    KVH=8, D=128, seed 7, 4 outlier dims per head at most): key, value, the
+    write scales s_k/s_v, the read scales ds_k/ds_v (0 at outlier dims),
+    out_idx2d and head_n_out."""
+    N, KVH, D, N_OUT_MAX = 512, 8, 128, 4
+    g = torch.Generator(device="cpu").manual_seed(7)
+    key = (torch.randn(N, KVH, D, generator=g) * 0.7).to(torch.bfloat16)
+    value = (torch.randn(N, KVH, D, generator=g) * 0.7).to(torch.bfloat16)
+    key[:8] *= 8.0
+    key[:, 0, :4] *= 60.0
+    key[:, 1, 10] *= 120.0
+    value[:, 2, :4] *= 60.0
+    kf, vf = key.float(), value.float()
+    amax_k, amax_v = kf.abs().amax(0), vf.abs().amax(0)
+    typ_k = kf.abs().mean(0).clamp_min(1e-6)
+    typ_v = vf.abs().mean(0).clamp_min(1e-6)
+    s_k = (amax_k / 127.0).clamp_min(1e-6)
+    s_v = (amax_v / 127.0).clamp_min(1e-6)
+    ratio = torch.maximum(amax_k / typ_k, amax_v / typ_v)
+    out_idx2d = torch.zeros(KVH, N_OUT_MAX, dtype=torch.int32)
+    head_n_out = torch.zeros(KVH, dtype=torch.int32)
+    for h in range(KVH):
+        dims = ratio[h].nonzero().flatten()
+        dims = dims[ratio[h, dims] > 10.0][:N_OUT_MAX]
+        out_idx2d[h, :dims.numel()] = dims.to(torch.int32)
+        head_n_out[h] = dims.numel()
+    ds_k, ds_v = s_k.clone(), s_v.clone()
+    for h in range(KVH):
+        n_h = int(head_n_out[h])
+        ds_k[h, out_idx2d[h, :n_h].long()] = 0.0
+        ds_v[h, out_idx2d[h, :n_h].long()] = 0.0
+    return key, value, s_k, s_v, ds_k, ds_v, out_idx2d, head_n_out

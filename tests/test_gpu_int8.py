@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import assert_attention_close, bits, gathered_pool
+from helpers import assert_attention_close, bits, gathered_pool, p17_unit_inputs
 from nanovllm_amd.kernels.kv_int8 import (dequant_gathered, dequant_tokhead, store_kvcache_int8,
                                           store_kvcache_int8_tokhead)
 from nanovllm_amd.kernels.paged_attention import paged_decode_attention
@@ -74,39 +74,8 @@ def test_tokhead_dequant_bitwise():
     assert np.array_equal(bits(out), ref)
 
 
-def _p17_unit_inputs():
-    N, KVH, D, N_OUT_MAX = 512, 8, 128, 4
-    g = torch.Generator(device="cpu").manual_seed(7)
-    key = (torch.randn(N, KVH, D, generator=g) * 0.7).to(torch.bfloat16)
-    value = (torch.randn(N, KVH, D, generator=g) * 0.7).to(torch.bfloat16)
-    key[:8] *= 8.0
-    key[:, 0, :4] *= 60.0
-    key[:, 1, 10] *= 120.0
-    value[:, 2, :4] *= 60.0
-    kf, vf = key.float(), value.float()
-    amax_k, amax_v = kf.abs().amax(0), vf.abs().amax(0)
-    typ_k = kf.abs().mean(0).clamp_min(1e-6)
-    typ_v = vf.abs().mean(0).clamp_min(1e-6)
-    s_k = (amax_k / 127.0).clamp_min(1e-6)
-    s_v = (amax_v / 127.0).clamp_min(1e-6)
-    ratio = torch.maximum(amax_k / typ_k, amax_v / typ_v)
-    out_idx2d = torch.zeros(KVH, N_OUT_MAX, dtype=torch.int32)
-    head_n_out = torch.zeros(KVH, dtype=torch.int32)
-    for h in range(KVH):
-        dims = ratio[h].nonzero().flatten()
-        dims = dims[ratio[h, dims] > 10.0][:N_OUT_MAX]
-        out_idx2d[h, :dims.numel()] = dims.to(torch.int32)
-        head_n_out[h] = dims.numel()
-    ds_k, ds_v = s_k.clone(), s_v.clone()
-    for h in range(KVH):
-        n_h = int(head_n_out[h])
-        ds_k[h, out_idx2d[h, :n_h].long()] = 0.0
-        ds_v[h, out_idx2d[h, :n_h].long()] = 0.0
-    return key, value, s_k, s_v, ds_k, ds_v, out_idx2d, head_n_out
-
-
 def test_chan_store_matches_p17_unit_bitwise():
-    key, value, s_k, s_v, _, _, out_idx2d, head_n_out = _p17_unit_inputs()
+    key, value, s_k, s_v, _, _, out_idx2d, head_n_out = p17_unit_inputs()
     N, KVH, D = key.shape
     assert int(head_n_out.sum()) > 0
     print(f"[int8-chan] p17 unit: outliers per head {head_n_out.tolist()}", flush=True)
@@ -130,7 +99,7 @@ def test_chan_store_matches_p17_unit_bitwise():
 
 def test_chan_store_strided_v():
     # The reference kernel reads V with K's strides; this path takes V's own.
-    key, value, s_k, s_v, _, _, out_idx2d, head_n_out = _p17_unit_inputs()
+    key, value, s_k, s_v, _, _, out_idx2d, head_n_out = p17_unit_inputs()
     N, KVH, D = key.shape
     fused = torch.cat([key.view(N, -1), value.view(N, -1)], dim=1).to(DEV)
     k_view = fused[:, :KVH * D].view(N, KVH, D)
@@ -154,7 +123,7 @@ def test_chan_store_strided_v():
 
 
 def test_chan_dequant_gathered_bitwise_and_relerr():
-    key, value, s_k, s_v, ds_k, ds_v, out_idx2d, head_n_out = _p17_unit_inputs()
+    key, value, s_k, s_v, ds_k, ds_v, out_idx2d, head_n_out = p17_unit_inputs()
     N, KVH, D = key.shape
     nout = out_idx2d.shape[1]
     rkc = np.zeros((3, 256, KVH, D), np.int8)
@@ -230,7 +199,7 @@ def test_int8_tokhead_end_to_end_quantised_decode():
 
 
 def test_int8_chan_decode_with_side_pool():
-    key, value, s_k, s_v, ds_k, ds_v, out_idx2d, head_n_out = _p17_unit_inputs()
+    key, value, s_k, s_v, ds_k, ds_v, out_idx2d, head_n_out = p17_unit_inputs()
     N, KVH, D = key.shape   # 512 tokens, 8 kv heads
     H = 16
     nout = out_idx2d.shape[1]

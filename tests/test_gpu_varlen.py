@@ -8,7 +8,8 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import assert_attention_close, bits, gathered_pool
+from helpers import assert_attention_close, bits, gathered_pool, p17_unit_inputs
+from nanovllm_amd.kernels.kv_int8 import store_kvcache_int8
 from nanovllm_amd.kernels.varlen import varlen_attention
 from nanovllm_amd.layers.attention import Attention
 from nanovllm_amd.utils.context import reset_context, set_context
@@ -127,6 +128,84 @@ def test_fresh_kv_prefill_without_block_tables(partition):
     ref = ko.prefill_ref(bits(q), None, None, None, cu, cu, 128 ** -0.5,
                          fresh_k=ko.bf16_to_f32(bits(k)), fresh_v=ko.bf16_to_f32(bits(v)))
     assert_attention_close(out, ref, "fresh-kv")
+
+
+def test_mixed_int8_tokhead_pool(partition):
+    # Decode rows and prefix-cached prefill chunks over a per-token-head int8
+    # pool (codes + fp32 scale per slot and kv head): the oracle reads the
+    # pool as codes x scale in fp32 (paged_attention.py:138-145).
+    H, KVH, D = 32, 4, 128
+    dec_lens = [900, 1, 2500]
+    chunks = [(0, 40), (700, 90), (3000, 33)]
+    g = torch.Generator().manual_seed(21)
+    all_lens = dec_lens + [p + c for p, c in chunks]
+    blocks = sum(max(1, (n + 255) // 256) for n in all_lens) + 2
+    bt = build_block_tables(all_lens, blocks, 256, g)
+    kc = torch.randint(-127, 128, (blocks, 256, KVH, D), generator=g, dtype=torch.int8)
+    vc = torch.randint(-127, 128, (blocks, 256, KVH, D), generator=g, dtype=torch.int8)
+    ks = torch.rand(blocks, 256, KVH, generator=g) * 0.03 + 0.005
+    vs = torch.rand(blocks, 256, KVH, generator=g) * 0.03 + 0.005
+    T = len(dec_lens) + sum(c for _, c in chunks)
+    q = torch.randn(T, H, D, generator=g).to(torch.bfloat16)
+    cu_q, cu_k = [0], [0]
+    for p, c in chunks:
+        cu_q.append(cu_q[-1] + c)
+        cu_k.append(cu_k[-1] + p + c)
+    print(f"[varlen] int8 tokhead mixed: rows={T} ({partition})", flush=True)
+    out = varlen_attention(
+        q.to(DEV), kc.to(DEV), vc.to(DEV), scale=D ** -0.5, block_tables=bt.to(DEV),
+        num_decode_rows=len(dec_lens),
+        decode_context_lens=torch.tensor(dec_lens, dtype=torch.int32, device=DEV),
+        cu_seqlens_q=torch.tensor(cu_q, dtype=torch.int32, device=DEV),
+        cu_seqlens_k=torch.tensor(cu_k, dtype=torch.int32, device=DEV),
+        cu_seqlens_q_list=cu_q, cu_seqlens_k_list=cu_k, k_scale=ks.to(DEV), v_scale=vs.to(DEV))
+    torch.cuda.synchronize()
+    kf = ko.kv_float(kc.numpy(), "int8_tokhead", ks.numpy())
+    vf = ko.kv_float(vc.numpy(), "int8_tokhead", vs.numpy())
+    ref = ko.mixed_ref(bits(q), kf, vf, bt.numpy(), len(dec_lens), np.asarray(dec_lens), cu_q,
+                       cu_k, D ** -0.5)
+    assert_attention_close(out, ref, "mixed-int8-tokhead")
+
+
+def test_mixed_int8_channel_pool_with_side(partition):
+    # The engine's per-channel int8 pool with the bf16 outlier side pool
+    # (tests/p17_kv_int8.py:64-136 geometry, 16 q / 8 kv heads): one decode
+    # row over 512 stored tokens plus a 100-token chunk after a 200-token
+    # prefix; the outlier dims come from the side pool exactly.
+    key, value, s_k, s_v, ds_k, ds_v, out_idx2d, head_n_out = p17_unit_inputs()
+    KVH, D, H = key.shape[1], key.shape[2], 16
+    nout = out_idx2d.shape[1]
+    blocks = 4
+    bt = torch.tensor([[2, 0], [1, 3]], dtype=torch.int32)
+    kc = torch.zeros(blocks, 256, KVH, D, dtype=torch.int8, device=DEV)
+    vc = torch.zeros_like(kc)
+    sk = torch.zeros(blocks, 256, KVH, nout, dtype=torch.bfloat16, device=DEV)
+    sv = torch.zeros_like(sk)
+    oi, hn = out_idx2d.to(DEV), head_n_out.to(DEV)
+    slots_a = [int(bt[0, t // 256]) * 256 + t % 256 for t in range(512)]
+    store_kvcache_int8(key.to(DEV), value.to(DEV), kc, vc, s_k.to(DEV), s_v.to(DEV), sk, sv, oi,
+                       hn, torch.tensor(slots_a, dtype=torch.int32, device=DEV))
+    slots_b = [int(bt[1, t // 256]) * 256 + t % 256 for t in range(300)]
+    store_kvcache_int8(key[:300].flip(0).contiguous().to(DEV), value[:300].to(DEV), kc, vc,
+                       s_k.to(DEV), s_v.to(DEV), sk, sv, oi, hn,
+                       torch.tensor(slots_b, dtype=torch.int32, device=DEV))
+    q = torch.randn(101, H, D, generator=torch.Generator().manual_seed(22)).to(torch.bfloat16)
+    cu_q, cu_k = [0, 100], [0, 300]
+    print(f"[varlen] int8 channel mixed + side pool ({partition})", flush=True)
+    out = varlen_attention(
+        q.to(DEV), kc, vc, scale=D ** -0.5, block_tables=bt.to(DEV), num_decode_rows=1,
+        decode_context_lens=torch.tensor([512], dtype=torch.int32, device=DEV),
+        cu_seqlens_q=torch.tensor(cu_q, dtype=torch.int32, device=DEV),
+        cu_seqlens_k=torch.tensor(cu_k, dtype=torch.int32, device=DEV),
+        cu_seqlens_q_list=cu_q, cu_seqlens_k_list=cu_k, k_scale=ds_k.to(DEV),
+        v_scale=ds_v.to(DEV), side_k=sk, side_v=sv, out_idx2d=oi, head_n_out=hn)
+    torch.cuda.synchronize()
+    kf = ko.kv_float(kc.cpu().numpy(), "int8_chan", ds_k.numpy(), bits(sk), out_idx2d.numpy(),
+                     head_n_out.numpy())
+    vf = ko.kv_float(vc.cpu().numpy(), "int8_chan", ds_v.numpy(), bits(sv), out_idx2d.numpy(),
+                     head_n_out.numpy())
+    ref = ko.mixed_ref(bits(q), kf, vf, bt.numpy(), 1, np.asarray([512]), cu_q, cu_k, D ** -0.5)
+    assert_attention_close(out, ref, "mixed-int8-chan-side")
 
 
 def test_attention_forward_mixed_matches_decode_and_prefill_paths():
