@@ -82,6 +82,7 @@ struct AttnParams {
   float* part_lse;
   int max_splits;
   int merge_first;  // splits the merge loads before it reads a row's split count
+  float xcd_skew;   // stream-K decode: even workgroups take (1 + skew) shares, odd (1 - skew)
   // Stream-K decode (paged decode launches): each workgroup takes an equal
   // share (at least sk_min_share) of the tiles of all rows; sk_nseg[r] gets
   // the number of workgroups that row unit r (= row * groups + group) spans.
@@ -1887,9 +1888,21 @@ paged_decode_sk_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
   const int Tmax = uniform(tmax);
   const int excl = incl - mine;
   int S = max(p.sk_min_share, (W + int(gridDim.x) - 1) / int(gridDim.x));
-  if (p.max_splits > 1) S = max(S, (Tmax + p.max_splits - 2) / (p.max_splits - 1));
-  const int start = w * S;
-  const int end = min(W, start + S);
+  const int need = p.max_splits > 1 ? (Tmax + p.max_splits - 2) / (p.max_splits - 1) : 1;
+  S = max(S, need);
+  // XCD-aware shares: workgroup v runs on XCD v mod 8, and the odd XCDs
+  // stream measurably slower, so even shares take S + d tiles and odd ones
+  // S - d (d <= S / 4, and S - d still meets the split bound).
+  int d = int(p.xcd_skew * float(S) + 0.5f);
+  d = max(0, min(d, min(S / 4, S - max(need, 1))));
+  auto share_start = [&](int v) { return v * S + ((v & 1) ? d : 0); };
+  auto share_of = [&](int x) {
+    int v = x / S;
+    if ((v & 1) && x - v * S < d) --v;
+    return v;
+  };
+  const int start = share_start(w);
+  const int end = min(W, share_start(w + 1));
   // The row unit holding tile `start` opens this share.
   int found_r = R, found_p = 0, found_c = 0;
   {
@@ -1904,13 +1917,13 @@ paged_decode_sk_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
       }
       if (wave == 0) {
         if (t == 0) {
-          const int owner = W > 0 ? min(P, W - 1) / S : 0;
+          const int owner = W > 0 ? share_of(min(P, W - 1)) : 0;
           if (owner == w) {
             write_nan_rows(p, r / groups, r % groups);
             set_nseg(p, r / groups, r % groups, 0);
           }
-        } else if (P / S == w) {
-          set_nseg(p, r / groups, r % groups, (P + t - 1) / S - P / S + 1);
+        } else if (share_of(P) == w) {
+          set_nseg(p, r / groups, r % groups, share_of(P + t - 1) - share_of(P) + 1);
         }
       }
       P += t;
@@ -1927,16 +1940,18 @@ paged_decode_sk_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
     if (t > 0) {
       const int t0 = max(start, P) - P;
       const int t1 = min(end, P + t) - P;
-      const int nseg = (P + t - 1) / S - P / S + 1;
+      const int first_share = share_of(P);
+      const int nseg = share_of(P + t - 1) - first_share + 1;
+      const int split = nseg == 1 ? -1 : w - first_share;
       if constexpr (kBfLds) {
         decode_segment_lds(p, smem, smem1, smem2, block_tables + int64_t(b) * p.bt_stride, b,
-                           r - b * groups, ctx, t0, t1, nseg == 1 ? -1 : w - P / S);
+                           r - b * groups, ctx, t0, t1, split);
       } else if constexpr (kI8Lds) {
         decode_segment_lds_i8(p, smem, smem2, block_tables + int64_t(b) * p.bt_stride, b,
-                              r - b * groups, ctx, t0, t1, nseg == 1 ? -1 : w - P / S);
+                              r - b * groups, ctx, t0, t1, split);
       } else {
         decode_segment<kEnc>(p, smem, block_tables + int64_t(b) * p.bt_stride, b,
-                             r - b * groups, ctx, t0, t1, nseg == 1 ? -1 : w - P / S);
+                             r - b * groups, ctx, t0, t1, split);
       }
     }
     P += t;
@@ -2363,6 +2378,18 @@ int env_int(const char* name, int fallback) {
   return atoi(v);
 }
 
+float env_float(const char* name, float fallback) {
+  const char* v = getenv(name);
+  if (v == nullptr || *v == '\0') return fallback;
+  return float(atof(v));
+}
+
+// Share skew of the stream-K decode between even and odd workgroups (XCDs):
+// on MI355X the odd XCDs stream the same share ~8 % slower (per-workgroup
+// timestamps, stable across runs and when the shares are rotated by one
+// workgroup), so they take 4 % less of a bf16 decode.
+constexpr float kXcdSkew = 0.04f;
+
 // Compute units of the current device (cached per device).
 int device_cus() {
   static int cached[64] = {0};
@@ -2651,6 +2678,11 @@ extern "C" int kvc_paged_decode(const void* q, int64_t q_stride_b, int64_t q_str
   if (sp.on) {
     p.max_splits = sp.max_splits;
     p.sk_min_share = kSkMinShare;
+    // bf16 pools are HBM-bound and profit; the int8 segments are bound by their
+    // arithmetic, which the XCDs share evenly.
+    p.xcd_skew = kv_dtype == KVC_KV_BF16
+                     ? std::min(0.25f, std::max(0.f, env_float("KVC_XCD_SKEW", kXcdSkew)))
+                     : 0.f;
     // Equal rows split into grid / units shares (+1 where a share boundary
     // falls inside a row); longer rows of a ragged batch load the rest later.
     const int64_t units = batch * hp.groups;
