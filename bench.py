@@ -151,6 +151,8 @@ def cpu_decode_baseline(torch, wl, sample: int, reps: int = 5):
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
     cv = statistics.pstdev(times) / statistics.fmean(times)
+    import resource
+    rss_gb = resource.getrusage(resource.RUSAGE_SELF).ru_maxrss / 1e6   # KiB -> GB
     return {
         "value": round(b / med, 1),
         "unit": "tokens/s",
@@ -158,7 +160,7 @@ def cpu_decode_baseline(torch, wl, sample: int, reps: int = 5):
         "kind": "port",
         "sample": (f"{b} of the {wl.batch} sequences (same q, block tables and KV bytes), "
                    f"torch gather+expand+masked SDPA decode, median of {reps} reps "
-                   f"({med * 1e3:.1f} ms, cv {cv:.2f})"),
+                   f"({med * 1e3:.1f} ms, cv {cv:.2f}); process peak RSS {rss_gb:.1f} GB"),
     }
 
 
