@@ -2589,6 +2589,17 @@ SkPlan plan_mixed(int64_t num_q_tokens, int64_t num_heads, int64_t num_decode_ro
 // still the faster default.
 bool mixed_stream_k() { return env_int("KVC_MIXED_STREAMK", 0) != 0; }
 
+// A varlen call with decode rows over a paged pool runs them as a paged decode
+// launch (stream-K, LDS-staged) and the prefill rows as a second launch on the
+// same stream: one combined launch costs the sum of its two halves anyway
+// (the compute-bound prefill units occupy every CU before the decode units
+// start), and the decode rows run faster in the decode kernel.
+// KVC_MIXED_SPLIT=0 keeps the single launch.
+bool split_mixed(int64_t num_decode_rows, int64_t page_size) {
+  return num_decode_rows > 0 && page_size > 0 && !mixed_stream_k() &&
+         env_int("KVC_MIXED_SPLIT", 1) != 0;
+}
+
 template <int kEnc>
 void launch_varlen_enc(const AttnParams& p, int grid, bool fresh, hipStream_t st) {
   if (fresh) {
@@ -2755,6 +2766,15 @@ extern "C" size_t kvc_varlen_workspace_bytes(int64_t num_q_tokens, int64_t num_h
                                              int64_t page_size, int64_t max_blocks_per_seq) {
   if (num_q_tokens <= 0 || num_kv_heads <= 0 || head_dim != kD) return 0;
   const HeadPlan hp = plan_heads(num_heads, num_kv_heads);
+  if (split_mixed(num_decode_rows, page_size)) {
+    // Decode rows through the paged decode launch, then the prefill rows.
+    const size_t dec = kvc_paged_decode_workspace_bytes(num_decode_rows, num_heads, num_kv_heads,
+                                                        head_dim, page_size, max_blocks_per_seq);
+    const size_t pre = kvc_varlen_workspace_bytes(num_q_tokens - num_decode_rows, num_heads,
+                                                  num_kv_heads, head_dim, 0, max_seqlen_k,
+                                                  page_size, max_blocks_per_seq);
+    return (dec + 255) / 256 * 256 + pre;
+  }
   if (mixed_stream_k()) {
     const SkPlan sp = plan_mixed(num_q_tokens, num_heads, num_decode_rows,
                                  max_blocks_per_seq * page_size, max_seqlen_k);
@@ -2818,6 +2838,41 @@ extern "C" int kvc_varlen_attention(
               KVC_ERR_VALUE, "varlen_attention: prefill chunks need cu_seqlens_q/k");
   (void)num_cache_blocks;
   if (num_q_tokens == 0) return KVC_OK;
+
+  if (!fresh && split_mixed(num_decode_rows, page_size)) {
+    KVC_REQUIRE(decode_context_lens != nullptr, KVC_ERR_VALUE,
+                "varlen_attention: decode rows need decode_context_lens");
+    KVC_REQUIRE(num_q_tokens >= num_decode_rows, KVC_ERR_VALUE,
+                "varlen_attention: fewer query rows than decode rows");
+    const size_t dec_ws = kvc_paged_decode_workspace_bytes(num_decode_rows, num_heads,
+                                                           num_kv_heads, head_dim, page_size,
+                                                           max_blocks_per_seq);
+    const size_t dec_span = (dec_ws + 255) / 256 * 256;
+    const size_t pre_ws = kvc_varlen_workspace_bytes(num_q_tokens - num_decode_rows, num_heads,
+                                                     num_kv_heads, head_dim, 0, max_seqlen_k,
+                                                     page_size, max_blocks_per_seq);
+    KVC_REQUIRE((dec_span + pre_ws == 0) ||
+                    (workspace != nullptr && workspace_bytes >= dec_span + pre_ws),
+                KVC_ERR_WORKSPACE, "varlen_attention: workspace of %zu bytes needed (got %zu)",
+                dec_span + pre_ws, workspace_bytes);
+    char* ws = static_cast<char*>(workspace);
+    rc = kvc_paged_decode(q, q_stride_t, q_stride_h, k_cache, v_cache, num_cache_blocks,
+                          page_size, num_kv_heads, head_dim, kv_dtype, k_scale, v_scale, side_k,
+                          side_v, out_idx2d, head_n_out, n_out_max, block_tables, bt_stride,
+                          max_blocks_per_seq, decode_context_lens, num_decode_rows, num_heads,
+                          scale, out, out_stride_t, out_stride_h, dec_ws ? ws : nullptr, dec_ws,
+                          stream);
+    if (rc != KVC_OK || num_q_tokens == num_decode_rows) return rc;
+    const int64_t nd = num_decode_rows;
+    return kvc_varlen_attention(
+        static_cast<const uint16_t*>(q) + nd * q_stride_t, q_stride_t, q_stride_h,
+        num_q_tokens - nd, num_heads, k_cache, v_cache, num_cache_blocks, page_size,
+        num_kv_heads, head_dim, kv_dtype, k_scale, v_scale, side_k, side_v, out_idx2d,
+        head_n_out, n_out_max, nullptr, 0, 0, nullptr, 0, 0, block_tables + nd * bt_stride,
+        bt_stride, max_blocks_per_seq, 0, nullptr, num_prefill, cu_seqlens_q, cu_seqlens_k,
+        num_prefill_units, max_seqlen_k, scale, static_cast<uint16_t*>(out) + nd * out_stride_t,
+        out_stride_t, out_stride_h, pre_ws ? ws + dec_span : nullptr, pre_ws, stream);
+  }
 
   const HeadPlan hp = plan_heads(num_heads, num_kv_heads);
   AttnParams p{};
