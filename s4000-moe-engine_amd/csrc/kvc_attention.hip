@@ -416,26 +416,38 @@ __device__ __forceinline__ void attend_tile(ColState<NCB>& st, const Tile<kEnc>&
     if (p.head_n_out != nullptr) n_out = p.head_n_out[g];
   }
 
+  // S^T of every column block first: the K operands die before the softmax,
+  // and a later block's MFMAs can run under an earlier block's softmax.
+  f32x4_t sacc[NCB][2];
 #pragma unroll
   for (int cb = 0; cb < NCB; ++cb) {
-    f32x4_t s0 = f32x4_t{0.f, 0.f, 0.f, 0.f}, s1 = s0;
+    sacc[cb][0] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    sacc[cb][1] = sacc[cb][0];
+  }
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      u32x4_t k0, k1;
-      if constexpr (kEnc == kBF16) {
-        k0 = k_operand(t, 0, c);
-        k1 = k_operand(t, 1, c);
-      } else {
-        k0 = k_operand_i8(t, 0, c);
-        k1 = k_operand_i8(t, 1, c);
-      }
-      s0 = mfma_bf16(k0, Q.op[cb][c], s0);
-      s1 = mfma_bf16(k1, Q.op[cb][c], s1);
+  for (int c = 0; c < 4; ++c) {
+    u32x4_t k0, k1;
+    if constexpr (kEnc == kBF16) {
+      k0 = k_operand(t, 0, c);
+      k1 = k_operand(t, 1, c);
+    } else {
+      k0 = k_operand_i8(t, 0, c);
+      k1 = k_operand_i8(t, 1, c);
+    }
+#pragma unroll
+    for (int cb = 0; cb < NCB; ++cb) {
+      sacc[cb][0] = mfma_bf16(k0, Q.op[cb][c], sacc[cb][0]);
+      sacc[cb][1] = mfma_bf16(k1, Q.op[cb][c], sacc[cb][1]);
       if constexpr (kEnc == kI8Chan) {
-        s0 = mfma_bf16(k0, Q.lo[cb][c], s0);
-        s1 = mfma_bf16(k1, Q.lo[cb][c], s1);
+        sacc[cb][0] = mfma_bf16(k0, Q.lo[cb][c], sacc[cb][0]);
+        sacc[cb][1] = mfma_bf16(k1, Q.lo[cb][c], sacc[cb][1]);
       }
     }
+  }
+
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) {
+    const f32x4_t s0 = sacc[cb][0], s1 = sacc[cb][1];
     float x[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
     if constexpr (kEnc != kBF16) {
       const float bias = 128.f * Q.qsum[cb];
@@ -844,6 +856,20 @@ __device__ __forceinline__ void dma_to_lds(const i32x4_t& rsrc, int voff, uint32
       "s_mov_b32 %0, m0\n\t"
       "s_mov_b32 m0, %2\n\t"
       "buffer_load_dwordx4 %1, %3, 0 offen nt lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(voff), "s"(lds), "s"(rsrc)
+      : "memory");
+}
+
+// The same load with the default cache policy, for data that other
+// workgroups read again soon (prefill keys and queries).
+__device__ __forceinline__ void dma_to_lds_cached(const i32x4_t& rsrc, int voff, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "buffer_load_dwordx4 %1, %3, 0 offen lds\n\t"
       "s_mov_b32 m0, %0"
       : "=&s"(saved)
       : "v"(voff), "s"(lds), "s"(rsrc)
@@ -1486,6 +1512,56 @@ __device__ void decode_unit(const AttnParams& p, char* smem, const int32_t* bt_b
 }
 
 // ---------------------------------------------------------------------------
+// Prefill epilogue of column block cb (bf16 and per-token-head int8 keys):
+// lane (lm, lg) holds dims 32 lg + 8 r + jj (r < 4, jj < 8) of column lm,
+// four runs of 8 contiguous dims stored straight from registers, either as
+// the final bf16 row (split < 0) or as split-K partial `split`.  `ok` is the
+// lane's column validity; every lane must call (the sum is a wave reduction).
+// ---------------------------------------------------------------------------
+template <int kEnc, int NCB>
+__device__ __forceinline__ void store_prefill_block(const AttnParams& p, const ColState<NCB>& st,
+                                                    int cb, int64_t row, int head, bool ok,
+                                                    int split, const LaneId& L) {
+  float l = st.l[cb];
+  l += shfl_xor(l, 16);
+  l += shfl_xor(l, 32);
+  float bias = 0.f;
+  if constexpr (kEnc != kBF16) {
+    float vb = st.vb[cb];
+    vb += shfl_xor(vb, 16);
+    vb += shfl_xor(vb, 32);
+    bias = 128.f * vb;
+  }
+  if (!ok) return;
+  if (split < 0) {
+    const float inv = 1.f / l;
+    uint16_t* dst = p.out + row * p.o_st + int64_t(head) * p.o_sh + 32 * L.lg;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v[8];
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) v[jj] = (st.o[cb][jj][r] - bias) * inv;
+      *reinterpret_cast<u32x4_t*>(dst + 8 * r) =
+          u32x4_t{pack_bf16x2_fast(v[0], v[1]), pack_bf16x2_fast(v[2], v[3]),
+                  pack_bf16x2_fast(v[4], v[5]), pack_bf16x2_fast(v[6], v[7])};
+    }
+  } else {
+    const int64_t base = (row * p.num_heads + head) * p.max_splits + split;
+    const float il = l > 0.f ? 1.f / l : 0.f;
+    float* dst = p.part_o + base * kD + 32 * L.lg;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v[8];
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) v[jj] = (st.o[cb][jj][r] - bias) * il;
+      reinterpret_cast<float4*>(dst + 8 * r)[0] = make_float4(v[0], v[1], v[2], v[3]);
+      reinterpret_cast<float4*>(dst + 8 * r)[1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
+    if (L.lg == 0) p.part_lse[base] = l > 0.f ? st.m[cb] + __log2f(l) : -INFINITY;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Prefill segment: key tiles [t0, t1) of item (chunk i, query tile qt, kv
 // slice kvs); the tiles stop at the last key any query of the tile sees.  The
 // workgroup covers kWaves waves x kPreNCB column blocks; K/V tiles go through
@@ -1714,53 +1790,14 @@ __device__ void prefill_segment(const AttnParams& p, char* smem, const int32_t* 
       __syncthreads();
     }
   } else {
-    // Lane (lm, lg) holds dims 32 lg + 8 r + jj (r < 4, jj < 8) of column
-    // lm: four runs of 8 contiguous dims, stored straight from registers.
 #pragma unroll
     for (int cb = 0; cb < kPreNCB; ++cb) {
-      float l = st.l[cb];
-      l += shfl_xor(l, 16);
-      l += shfl_xor(l, 32);
-      float bias = 0.f;
-      if constexpr (kEnc != kBF16) {
-        float vb = st.vb[cb];
-        vb += shfl_xor(vb, 16);
-        vb += shfl_xor(vb, 32);
-        bias = 128.f * vb;
-      }
       const int col = L.lm;
       const int tq = q0 + (wave * kPreNCB + cb) * p.tpb + col / p.hs;
       const int hh = col % p.hs;
-      if (col < p.tpb * p.hs && hh < hs && tq < sq) {
-        const int64_t row = int64_t(p.n_dec) + cq0 + tq;
-        const int head = g * p.group + s * p.hs + hh;
-        if (split < 0) {
-          const float inv = 1.f / l;
-          uint16_t* dst = p.out + row * p.o_st + int64_t(head) * p.o_sh + 32 * L.lg;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            float v[8];
-#pragma unroll
-            for (int jj = 0; jj < 8; ++jj) v[jj] = (st.o[cb][jj][r] - bias) * inv;
-            *reinterpret_cast<u32x4_t*>(dst + 8 * r) =
-                u32x4_t{pack_bf16x2_fast(v[0], v[1]), pack_bf16x2_fast(v[2], v[3]),
-                        pack_bf16x2_fast(v[4], v[5]), pack_bf16x2_fast(v[6], v[7])};
-          }
-        } else {
-          const int64_t base = (row * p.num_heads + head) * p.max_splits + split;
-          const float il = l > 0.f ? 1.f / l : 0.f;
-          float* dst = p.part_o + base * kD + 32 * L.lg;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            float v[8];
-#pragma unroll
-            for (int jj = 0; jj < 8; ++jj) v[jj] = (st.o[cb][jj][r] - bias) * il;
-            reinterpret_cast<float4*>(dst + 8 * r)[0] = make_float4(v[0], v[1], v[2], v[3]);
-            reinterpret_cast<float4*>(dst + 8 * r)[1] = make_float4(v[4], v[5], v[6], v[7]);
-          }
-          if (L.lg == 0) p.part_lse[base] = l > 0.f ? st.m[cb] + __log2f(l) : -INFINITY;
-        }
-      }
+      store_prefill_block<kEnc, kPreNCB>(p, st, cb, int64_t(p.n_dec) + cq0 + tq,
+                                         g * p.group + s * p.hs + hh,
+                                         col < p.tpb * p.hs && hh < hs && tq < sq, split, L);
     }
     __syncthreads();
   }
@@ -2275,6 +2312,659 @@ varlen_kernel(AttnParams p, const int32_t* __restrict__ block_tables) {
                                 (split + 1) * per, nsplit == 1 ? -1 : split);
 }
 
+// ---------------------------------------------------------------------------
+// Stream-K prefill launch over bf16 keys (a paged bf16 pool, or the step's
+// fresh k/v when there is no prefix cache).  Items are (chunk i, kv slice,
+// query tile), query tile fastest; each is a run of 32-key tiles that stops
+// at the last key its queries see.  The concatenated tiles are cut into one
+// equal share per workgroup, so chunks of any length mix spread evenly over
+// the CUs.  A workgroup streams its share through a three-stage LDS ring
+// with no break at item boundaries: tile j + 2 is in flight (direct-to-LDS
+// loads) while tile j is attended, whichever item either belongs to, and the
+// query block of the next item rides the same DMA while the current item
+// runs, so an item boundary costs its epilogue and not a pipeline refill.
+// Items spanning several shares write split-K partials; the share holding an
+// item's first tile records the split count of its rows for the merge.
+//
+// LDS rows are 256 bytes padded to 272 (17 chunks of 16 bytes): 16 rows read
+// at one column offset touch 16 different bank groups, and every operand
+// read is a per-lane base plus an immediate.  A 64-lane direct-to-LDS load
+// fills 64 consecutive chunks, so lane l of load k fetches whichever chunk
+// belongs at slot 64 k + l (pad slots and rows past the tile read 0).
+// ---------------------------------------------------------------------------
+constexpr int kPfRowSlots = 17;
+constexpr int kPfPitch = kPfRowSlots * 16;                          // 272
+constexpr int kPfLoadsPerTensor = (kTile * kPfRowSlots + 63) / 64;  // 9
+constexpr int kPfTensor = kPfLoadsPerTensor * 1024;
+constexpr int kPfStage = 2 * kPfTensor;  // K then V
+#ifndef KVC_PF_STAGES
+#define KVC_PF_STAGES 4
+#endif
+constexpr int kPfStages = KVC_PF_STAGES;  // tile j + kPfStages - 1 loads while tile j is attended
+constexpr int kPfTileLoads = (2 * kPfLoadsPerTensor + kWaves - 1) / kWaves;  // per wave: 3
+constexpr int kPfCols = kWaves * kPreNCB * 16;                     // query columns per item
+constexpr int kPfQLoads = (kPfCols * kPfRowSlots + 63) / 64;       // 68
+constexpr int kPfQLoadsPerWave = (kPfQLoads + kWaves - 1) / kWaves;  // 9
+constexpr int kPfQOff = kPfStages * kPfStage;
+constexpr int kPfDummyOff = kPfQOff + kPfQLoads * 1024;
+constexpr int kPfSmem = kPfDummyOff + 1024;
+constexpr int kPfMinShare = 4;
+#ifndef KVC_PF_NT
+#define KVC_PF_NT 0
+#endif
+// Prefill keys are read by every query tile of their chunk: keep them cached.
+constexpr bool kPfNonTemporal = KVC_PF_NT != 0;
+constexpr int kOob = 0x40000000;  // a buffer offset past every resource: reads 0, no traffic
+static_assert(kPfTileLoads == 3 && kPfQLoadsPerWave == 9, "wait counts below assume these");
+static_assert(kPfStages >= 3 && 3 * (kPfStages - 1) + 9 * (kPfStages - 2) <= 45, "pf_wait_vm range");
+static_assert(kPfSmem <= 160 * 1024, "one workgroup per CU");
+
+// Each item also carries kPfItemCost virtual tiles in the partition: a
+// segment costs its query load, its epilogue and a pipeline bubble (about
+// two tiles' time), so shares that chain many short items get fewer tiles.
+constexpr int kPfItemCost = 2;
+
+struct PfItem {
+  int i, kvs, qt;  // chunk, kv slice, query tile
+  int g, s;        // kv head and slice within its group: kvs = g * nslices + s
+  int P;           // weighted position of the item's span (kPfItemCost + T long)
+  int T;           // tiles of the item
+  int cq0, ck0;    // chunk's first query row / key row (prefill-relative)
+  ChunkGeo geo;
+};
+
+__device__ __forceinline__ void pf_load_chunk(PfItem& it, const int32_t* cu_q, const int32_t* cu_k,
+                                              int qtile) {
+  it.geo = chunk_geo(cu_q, cu_k, it.i, qtile);
+  it.cq0 = cu_q[it.i];
+  it.ck0 = cu_k[it.i];
+}
+
+// The item after `it` (T = 0 past the last one).
+__device__ __forceinline__ void pf_next_item(PfItem& it, const int32_t* cu_q, const int32_t* cu_k,
+                                             int n_pre, int kvs_total, int nslices, int qtile) {
+  it.P += kPfItemCost + it.T;
+  if (++it.qt == it.geo.ntq) {
+    it.qt = 0;
+    ++it.kvs;
+    if (++it.s == nslices) {
+      it.s = 0;
+      ++it.g;
+    }
+    if (it.kvs == kvs_total) {
+      it.kvs = it.g = it.s = 0;
+      do {
+        ++it.i;
+        if (it.i < n_pre) pf_load_chunk(it, cu_q, cu_k, qtile);
+      } while (it.i < n_pre && it.geo.ntq == 0);
+    }
+  }
+  it.T = it.i < n_pre ? qtile_tiles(it.geo, qtile, it.qt) : 0;
+}
+
+// Wait until at most n of this wave's vector memory operations are pending
+// (n = the loads issued after the ones waited for).
+// n is a multiple of 3 (tile loads and query loads come in threes and nines)
+// below 3 (kPfStages - 1) + 9 (kPfStages - 2) <= 45.
+__device__ __forceinline__ void pf_wait_vm(int n) {
+  switch (n / 3) {
+    case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+    case 1: __builtin_amdgcn_s_waitcnt(0x0F73); break;
+    case 2: __builtin_amdgcn_s_waitcnt(0x0F76); break;
+    case 3: __builtin_amdgcn_s_waitcnt(0x0F79); break;
+    case 4: __builtin_amdgcn_s_waitcnt(0x0F7C); break;
+    case 5: __builtin_amdgcn_s_waitcnt(0x0F7F); break;
+    case 6: __builtin_amdgcn_s_waitcnt(0x4F72); break;  // 18
+    case 7: __builtin_amdgcn_s_waitcnt(0x4F75); break;  // 21
+    case 8: __builtin_amdgcn_s_waitcnt(0x4F78); break;  // 24
+    case 9: __builtin_amdgcn_s_waitcnt(0x4F7B); break;  // 27
+    case 10: __builtin_amdgcn_s_waitcnt(0x4F7E); break;  // 30
+    case 11: __builtin_amdgcn_s_waitcnt(0x8F71); break;  // 33
+    case 12: __builtin_amdgcn_s_waitcnt(0x8F74); break;  // 36
+    case 13: __builtin_amdgcn_s_waitcnt(0x8F77); break;  // 39
+    case 14: __builtin_amdgcn_s_waitcnt(0x8F7A); break;  // 42
+    default: __builtin_amdgcn_s_waitcnt(0x8F7D); break;  // 45
+  }
+}
+
+// Workgroup barrier over LDS only: this wave's LDS accesses are complete and
+// every wave has arrived.  (__syncthreads would also wait for the epilogue's
+// global stores, and with them for every direct-to-LDS load in flight.)
+__device__ __forceinline__ void pf_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// One 32-key tile of the stream-K prefill against the wave's kPreNCB column
+// blocks (bf16 keys).  Differences from attend_tile, each removing VALU work:
+//  * V^T operands come straight from LDS through transposing reads
+//    (ds_read_b64_tr_b16: lane j of a 16-lane group receives element j % 4 of
+//    the 8-byte rows addressed by lanes j / 4 + 4 k, k = 0..3), so PV MFMA jj
+//    row m is dim 16 jj + m and the O^T accumulators hold, in lane (lm, lg),
+//    dims 16 jj + 4 lg + r (r < 4) of column lm;
+//  * the scale folds into the exponent (one fma per logit; the max is taken
+//    on raw logits, the scale being positive);
+//  * the column sums of P come from one more MFMA against an all-ones
+//    operand (every row of the result is the sum, of the same bf16 P that
+//    weights V), not from lane adds and a final reduction.
+constexpr int kPfVRowSlots = 18;              // V rows padded to 288 B: tr reads conflict-free
+constexpr int kPfPitchV = kPfVRowSlots * 16;  // 288
+constexpr uint32_t kOnesBf16x2 = 0x3F803F80u;
+
+struct PfState {
+  f32x4_t o[kPreNCB][8];  // O^T of PV MFMA jj (dims 16 jj + 4 lg + r)
+  f32x4_t l[kPreNCB];     // column sums of P (all four rows equal)
+  float m[kPreNCB];       // reference max (log2 domain), identical on the column's lanes
+};
+
+__device__ __forceinline__ void pf_init(PfState& st) {
+#pragma unroll
+  for (int cb = 0; cb < kPreNCB; ++cb) {
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) st.o[cb][jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    st.l[cb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    st.m[cb] = -INFINITY;
+  }
+}
+
+typedef short s16x4v_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x2_t lds_read_tr16(const char* p) {
+  const s16x4v_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4v_t*)(
+          (__attribute__((address_space(3))) char*)(p)));
+  return __builtin_bit_cast(u32x2_t, r);
+}
+
+// k: K operands as in Tile<kBF16>; va[jj]: V^T operand of PV MFMA jj;
+// klim[cb]: the lane's column key limit (-1 for an invalid column).
+template <bool kMasked>
+__device__ __forceinline__ void pf_attend(PfState& st, const u32x4_t (&k)[2][4],
+                                          const u32x4_t (&va)[8],
+                                          const QOps<kBF16, kPreNCB>& Q,
+                                          const int (&klim)[kPreNCB], int key0, int valid_end,
+                                          float scale_log2, const LaneId& L) {
+  f32x4_t sacc[kPreNCB][2];
+#pragma unroll
+  for (int cb = 0; cb < kPreNCB; ++cb) {
+    sacc[cb][0] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    sacc[cb][1] = sacc[cb][0];
+  }
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+#pragma unroll
+    for (int cb = 0; cb < kPreNCB; ++cb) {
+      sacc[cb][0] = mfma_bf16(k[0][c], Q.op[cb][c], sacc[cb][0]);
+      sacc[cb][1] = mfma_bf16(k[1][c], Q.op[cb][c], sacc[cb][1]);
+    }
+  }
+  const u32x4_t ones = u32x4_t{kOnesBf16x2, kOnesBf16x2, kOnesBf16x2, kOnesBf16x2};
+#pragma unroll
+  for (int cb = 0; cb < kPreNCB; ++cb) {
+    float x[8] = {sacc[cb][0][0], sacc[cb][0][1], sacc[cb][0][2], sacc[cb][0][3],
+                  sacc[cb][1][0], sacc[cb][1][1], sacc[cb][1][2], sacc[cb][1][3]};
+    if constexpr (kMasked) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int key = key0 + key_of_slot(L.lg, i);
+        x[i] = (key < valid_end && key <= klim[cb]) ? x[i] : -INFINITY;
+      }
+    }
+    float tmax = fmaxf(fmaxf(x[0], x[1]), x[2]);
+    tmax = fmaxf(fmaxf(tmax, x[3]), x[4]);
+    tmax = fmaxf(fmaxf(tmax, x[5]), x[6]);
+    tmax = fmaxf(tmax, x[7]);
+    tmax = rows4_max(tmax) * scale_log2;
+    if (__builtin_expect(__ballot(tmax > st.m[cb] + kRescaleLog2) != 0, 0)) {
+      const float m_new = fmaxf(st.m[cb], tmax);
+      const float m_ref = (m_new == -INFINITY) ? 0.f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(st.m[cb] - m_ref);
+      st.m[cb] = m_new;
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) st.o[cb][jj][r] *= alpha;
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) st.l[cb][r] *= alpha;
+    }
+    const float neg_m = (st.m[cb] == -INFINITY) ? 0.f : -st.m[cb];
+    float pr[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) pr[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[i], scale_log2, neg_m));
+    u32x4_t pb;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) pb[w] = pack_bf16x2_fast(pr[2 * w], pr[2 * w + 1]);
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) st.o[cb][jj] = mfma_bf16(va[jj], pb, st.o[cb][jj]);
+    st.l[cb] = mfma_bf16(ones, pb, st.l[cb]);
+  }
+}
+
+// Weighted tiles of query tiles [0, q) of chunk c.
+__device__ __forceinline__ int pf_qcum(const ChunkGeo& c, int tpb, int q) {
+  return int(qtile_cum(c, tpb, q)) + kPfItemCost * q;
+}
+
+template <bool kFresh>
+__global__ void __launch_bounds__(kThreads)
+prefill_sk_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k,
+                  const int32_t* __restrict__ block_tables) {
+  __shared__ __align__(16) char lds[kPfSmem];
+  auto pf_dma = [](const i32x4_t& r, int voff, uint32_t dst) {
+    if constexpr (kPfNonTemporal) {
+      dma_to_lds(r, voff, dst);
+    } else {
+      dma_to_lds_cached(r, voff, dst);
+    }
+  };
+  const LaneId L = lane_id();
+  const int wave = uniform(int(threadIdx.x >> 6));
+  const int kvs_total = p.kvh * p.nslices;
+  const int qtile = kWaves * kPreNCB * p.tpb;
+  // Consecutive shares run on one XCD (workgroup v is placed on XCD v mod 8),
+  // so the query tiles of an item that read the same keys at the same time
+  // share that XCD's L2.
+  const int G = int(gridDim.x);
+  const int v = int(blockIdx.x);
+  const int w = (G % 8 == 0) ? (v % 8) * (G / 8) + v / 8 : v;
+
+  // Weighted total W and the longest item; shares of S.  Lane l holds chunk
+  // c0 + l of the first 64 (one memory round trip for the usual batch of at
+  // most 64 chunks); its counts stay in registers for the search.
+  int W = 0, Tmax = 0;
+  int t_first = 0;
+  int cq_first = 0, ck_first = 0;
+  ChunkGeo g_first{0, 0, 0, 0};
+  for (int c0 = 0; c0 < p.n_pre; c0 += 64) {
+    const int ci = c0 + L.lane;
+    int t = 0, tm = 0;
+    if (ci < p.n_pre) {
+      const ChunkGeo c = chunk_geo(cu_q, cu_k, ci, qtile);
+      if (c.ntq > 0) {
+        tm = (c.sk + kTile - 1) / kTile;
+        t = kvs_total * pf_qcum(c, p.tpb, c.ntq);
+      }
+      if (c0 == 0) {
+        g_first = c;
+        cq_first = cu_q[ci];
+        ck_first = cu_k[ci];
+      }
+    }
+    if (c0 == 0) t_first = t;
+    W += wave_sum(t);
+    Tmax = max(Tmax, wave_max(tm));
+  }
+  W = uniform(W);
+  Tmax = uniform(Tmax);
+  int S = max(p.sk_min_share, (W + G - 1) / G);
+  if (p.max_splits > 1) S = max(S, (Tmax + kPfItemCost + p.max_splits - 2) / (p.max_splits - 1));
+  S = uniform(S);
+  if (int64_t(w) * S >= W) return;
+  const int start = w * S;
+  const int end = min(W, start + S);
+
+  // The item whose weighted span holds `start`: its chunk by a 64-wide scan
+  // (the first 64 chunks from registers), its kv slice by division, its query
+  // tile by bisection of the closed-form counts.
+  PfItem it;
+  {
+    int base = 0, ci = -1, P = 0;
+    for (int c0 = 0; c0 < p.n_pre && ci < 0; c0 += 64) {
+      int t = t_first;
+      if (c0 > 0) {
+        t = 0;
+        if (c0 + L.lane < p.n_pre) {
+          const ChunkGeo c = chunk_geo(cu_q, cu_k, c0 + L.lane, qtile);
+          if (c.ntq > 0) t = kvs_total * pf_qcum(c, p.tpb, c.ntq);
+        }
+      }
+      int inc = t;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const int u = __shfl_up(inc, d, 64);
+        if (L.lane >= d) inc += u;
+      }
+      const int total = uniform(__shfl(inc, 63, 64));
+      if (start < base + total) {
+        const unsigned long long hit =
+            __ballot(t > 0 && base + inc - t <= start && start < base + inc);
+        const int src = __ffsll(hit) - 1;
+        ci = uniform(c0 + src);
+        P = uniform(base + __shfl(inc - t, src, 64));
+        if (c0 == 0) {
+          it.geo.sq = uniform(__shfl(g_first.sq, src, 64));
+          it.geo.sk = uniform(__shfl(g_first.sk, src, 64));
+          it.geo.prefix = it.geo.sk - it.geo.sq;
+          it.geo.ntq = uniform(__shfl(g_first.ntq, src, 64));
+          it.cq0 = uniform(__shfl(cq_first, src, 64));
+          it.ck0 = uniform(__shfl(ck_first, src, 64));
+        }
+      }
+      base += total;
+    }
+    it.i = ci;
+    if (ci >= 64) pf_load_chunk(it, cu_q, cu_k, qtile);
+    const int per_kvs = pf_qcum(it.geo, p.tpb, it.geo.ntq);
+    int off = start - P;
+    it.kvs = uniform(off / per_kvs);
+    off -= it.kvs * per_kvs;
+    int lo = 0, hi = it.geo.ntq - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (pf_qcum(it.geo, p.tpb, mid) <= off) lo = mid; else hi = mid - 1;
+    }
+    it.qt = uniform(lo);
+    it.g = uniform(it.kvs / p.nslices);
+    it.s = it.kvs - it.g * p.nslices;
+    it.P = uniform(P + it.kvs * per_kvs + pf_qcum(it.geo, p.tpb, it.qt));
+    it.T = qtile_tiles(it.geo, qtile, it.qt);
+  }
+  // Real tile t of item x sits at weighted position x.P + kPfItemCost + t;
+  // the share owns the real tiles whose positions fall in [start, end).
+  int ct = max(0, start - it.P - kPfItemCost);  // consumer's tile in `it`
+
+  // Tile loads: wave w issues loads w, w + 8, w + 16 of the 18 per tile (9 of
+  // K, 9 of V; the six past 18 are zero loads into a dummy block, so every
+  // wave waits with the same counts).  Lane slots are fixed; the offsets
+  // change with the item's kv head.
+  const uint32_t lds0 = lds_addr(lds);
+  int boff[kPfTileLoads];  // lane offset of load jj inside a tile, before the kv head's
+#pragma unroll
+  for (int jj = 0; jj < kPfTileLoads; ++jj) {
+    const int k = wave + kWaves * jj;
+    const int sl = (k % kPfLoadsPerTensor) * 64 + L.lane;
+    const int slots = k < kPfLoadsPerTensor ? kPfRowSlots : kPfVRowSlots;  // K 272 B, V 288 B rows
+    const int row = sl / slots;
+    const int ch = sl - row * slots;
+    int rs;
+    if constexpr (kFresh) {
+      rs = int((k >= kPfLoadsPerTensor ? p.vf_st : p.kf_st) * 2);
+    } else {
+      rs = int(p.tok_bytes);
+    }
+    const bool ok = k < 2 * kPfLoadsPerTensor && row < kTile && ch < 16;
+    boff[jj] = ok ? row * rs + ch * 16 : kOob;
+  }
+
+  // Producer cursor: real tile pt of item pi.  Paged keys: the block-table
+  // entry of the tile's page (pblk) is kept in pblk_val, the next page's
+  // entry is loaded a page ahead (reads stay inside the item's keys).  The
+  // table is read through the __restrict__ kernel argument itself, so these
+  // are scalar loads; a vector load's wait would drain the ring.
+  PfItem pi = it;
+  int pt = ct;
+  int pblk = 0, poff = 0, pblk_val = 0, pnext_val = 0, plast = 0;
+  int64_t pbt = 0;  // element offset of the producer item's table row
+  auto table_setup = [&]() {
+    if constexpr (!kFresh) {
+      pbt = int64_t(p.n_dec + pi.i) * p.bt_stride;
+      const int key0 = pt * kTile;
+      pblk = uniform(key0 / p.page);
+      poff = uniform(key0 - pblk * p.page);
+      plast = uniform((pi.geo.sk - 1) / p.page);  // last page holding keys of the chunk
+      pblk_val = block_tables[pbt + pblk];
+      pnext_val = block_tables[pbt + min(pblk + 1, plast)];
+    }
+  };
+  table_setup();
+  auto produce = [&](int stage) {
+    const int nvalid = min(kTile, pi.geo.sk - pt * kTile);
+    int hk, hv;  // byte offset of kv head g inside a K / V row
+    const char* kb;
+    const char* vb;
+    int kbytes, vbytes;
+    if constexpr (kFresh) {
+      hk = int(pi.g * p.kf_sh * 2);
+      hv = int(pi.g * p.vf_sh * 2);
+      const int64_t r0 = int64_t(pi.ck0) + pt * kTile;
+      kb = reinterpret_cast<const char*>(p.kf + r0 * p.kf_st);
+      vb = reinterpret_cast<const char*>(p.vf + r0 * p.vf_st);
+      kbytes = int(nvalid * p.kf_st * 2);
+      vbytes = int(nvalid * p.vf_st * 2);
+    } else {
+      hk = hv = pi.g * kD * 2;
+      const int64_t slot0 = int64_t(pblk_val) * p.page + poff;
+      kb = p.k_cache + slot0 * p.tok_bytes;
+      vb = p.v_cache + slot0 * p.tok_bytes;
+      kbytes = vbytes = nvalid * int(p.tok_bytes);
+    }
+    const i32x4_t rk = raw_rsrc(kb, kbytes);
+    const i32x4_t rv = raw_rsrc(vb, vbytes);
+    const uint32_t sb = lds0 + stage * kPfStage;
+#pragma unroll
+    for (int jj = 0; jj < kPfTileLoads; ++jj) {
+      const int k = wave + kWaves * jj;
+      if (k < kPfLoadsPerTensor) {
+        pf_dma(rk, boff[jj] + hk, sb + k * 1024);
+      } else if (k < 2 * kPfLoadsPerTensor) {
+        pf_dma(rv, boff[jj] + hv, sb + kPfTensor + (k - kPfLoadsPerTensor) * 1024);
+      } else {
+        pf_dma(rk, kOob, lds0 + kPfDummyOff);
+      }
+    }
+    // Advance to the next real tile.
+    if (++pt == pi.T) {
+      pf_next_item(pi, cu_q, cu_k, p.n_pre, kvs_total, p.nslices, qtile);
+      pt = 0;
+      if (pi.P + kPfItemCost < end) table_setup();
+    } else if constexpr (!kFresh) {
+      poff += kTile;
+      if (poff == p.page) {
+        poff = 0;
+        ++pblk;
+        pblk_val = pnext_val;
+        pnext_val = block_tables[pbt + min(pblk + 1, plast)];
+      }
+    }
+  };
+  auto prod_live = [&]() { return pi.P + kPfItemCost + pt < end; };
+
+  // Query block of item x: column c (16-column block c / 16, lane c % 16) at
+  // slots 17 c .. 17 c + 15; columns past the chunk or the slice read 0.
+  const float inv_hs = 1.f / float(p.hs);
+  auto issue_q = [&](const PfItem& x) {
+    const int hs = min(p.hs, p.group - x.s * p.hs);
+    const int q0 = x.qt * qtile;
+    const uint16_t* qb = p.q + (int64_t(p.n_dec) + x.cq0) * p.q_st;
+    const i32x4_t rq = raw_rsrc(qb, int(int64_t(x.geo.sq) * p.q_st * 2));
+#pragma unroll
+    for (int jj = 0; jj < kPfQLoadsPerWave; ++jj) {
+      const int k = wave + kWaves * jj;
+      const int sl = k * 64 + L.lane;
+      const int col = sl / kPfRowSlots;
+      const int ch = sl - col * kPfRowSlots;
+      const int lm = col & 15;
+      const int tdiv = int((float(lm) + 0.5f) * inv_hs);  // lm / hs (lm < 16)
+      const int hh = lm - tdiv * p.hs;
+      const int tq = q0 + (col >> 4) * p.tpb + tdiv;
+      const bool ok = k < kPfQLoads && ch < 16 && lm < p.tpb * p.hs && hh < hs && tq < x.geo.sq;
+      const int off =
+          ok ? int((int64_t(tq) * p.q_st + int64_t(x.g * p.group + x.s * p.hs + hh) * p.q_sh) *
+                   2) +
+                   ch * 16
+             : kOob;
+      pf_dma(rq, off, k < kPfQLoads ? lds0 + kPfQOff + k * 1024 : lds0 + kPfDummyOff);
+    }
+  };
+
+  // Prologue: the first item's query, then the first kPfStages - 1 tiles.
+  // `issued` counts this wave's loads; mk[k] = its value right after the
+  // loads of the k-th tile ahead, q_mark right after the latest query loads,
+  // so the wait for a tile (and for its segment's query) is issued - mark.
+  int issued = 0;
+  issue_q(it);
+  issued += kPfQLoadsPerWave;
+  int q_mark = issued;
+  int q_issued_for = it.P;  // item (by its span start) whose query was loaded last
+  int mk[kPfStages - 1];
+#pragma unroll
+  for (int k = 0; k < kPfStages - 1; ++k) {
+    if (prod_live()) {
+      produce(k);
+      issued += kPfTileLoads;
+    }
+    mk[k] = issued;
+  }
+
+  int stage = 0;
+  bool first = true;
+  PfState st;
+  QOps<kBF16, kPreNCB> Q;
+  int klim[kPreNCB];
+  int min_klim = 0, split = -1;
+
+  while (it.P + kPfItemCost + ct < end) {
+    const bool seg_start = first || ct == 0;
+    const bool seg_end = ct + 1 == it.T || it.P + kPfItemCost + ct + 1 >= end;
+    first = false;
+    // (a) This wave's loads of the tile (and of its segment's query) have
+    // landed ...
+    int need = mk[0];
+    if (seg_start && q_issued_for == it.P) need = max(need, q_mark);
+    if (issued - need == kPfTileLoads * (kPfStages - 2)) {
+      pf_wait_vm(kPfTileLoads * (kPfStages - 2));  // steady state: an immediate
+    } else {
+      pf_wait_vm(issued - need);
+    }
+    // ... and every wave's: the stage is complete, and every wave is done
+    // with the stage refilled below and with the query block.
+    pf_barrier();
+    if (seg_start) {
+      if (q_issued_for != it.P) {
+        // The previous segment was one tile long: load this one's query now.
+        issue_q(it);
+        issued += kPfQLoadsPerWave;
+        q_mark = issued;
+        q_issued_for = it.P;
+        pf_wait_vm(0);
+        pf_barrier();
+      }
+      const int hs = min(p.hs, p.group - it.s * p.hs);
+      const int q0 = it.qt * qtile;
+      const int prefix = it.geo.sk - it.geo.sq;
+      const char* qrow = lds + kPfQOff + (32 * wave + L.lm) * kPfPitch + L.lg * 16;
+#pragma unroll
+      for (int cb = 0; cb < kPreNCB; ++cb) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          Q.op[cb][c] = *reinterpret_cast<const u32x4_t*>(qrow + cb * 16 * kPfPitch + c * 64);
+        const int tq = q0 + (wave * kPreNCB + cb) * p.tpb + L.lm / p.hs;
+        const int hh = L.lm % p.hs;
+        const bool ok = (L.lm < p.tpb * p.hs) && hh < hs && tq < it.geo.sq;
+        klim[cb] = ok ? prefix + tq : -1;
+      }
+      min_klim = 0x7fffffff;
+#pragma unroll
+      for (int cb = 0; cb < kPreNCB; ++cb)
+        if (klim[cb] >= 0) min_klim = min(min_klim, klim[cb]);
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1) min_klim = min(min_klim, __shfl_xor(min_klim, m, 64));
+      pf_init(st);
+      // Split bookkeeping: the item's real tiles span shares [f, l].
+      const int f = (it.P + kPfItemCost) / S;
+      const int nseg = (it.P + kPfItemCost + it.T - 1) / S - f + 1;
+      split = nseg == 1 ? -1 : w - f;
+      if (f == w && int(threadIdx.x) < min(qtile, it.geo.sq - q0) && p.sk_nseg != nullptr)
+        p.sk_nseg[(int64_t(p.n_dec) + it.cq0 + q0 + threadIdx.x) * kvs_total + it.kvs] = nseg;
+    }
+    // (b) The tile from LDS into registers: K rows as the S^T operands, V^T
+    // operands through transposing reads (lane (lm, lg) addresses key
+    // key_of_slot(lg, lm / 4) (+ 16 for the second half) at dims
+    // 16 jj + 4 (lm % 4)).  Issued before the next loads so that their
+    // latency hides under the DMA issue.
+    u32x4_t kop[2][4];
+    u32x4_t va[8];
+    {
+      const char* kb = lds + stage * kPfStage + L.lm * kPfPitch + L.lg * 16;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          kop[h][c] = *reinterpret_cast<const u32x4_t*>(kb + h * 16 * kPfPitch + c * 64);
+      }
+      const char* vb = lds + stage * kPfStage + kPfTensor +
+                       (4 * L.lg + (L.lm >> 2)) * kPfPitchV + (L.lm & 3) * 8;
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        const u32x2_t lo = lds_read_tr16(vb + jj * 32);
+        const u32x2_t hi = lds_read_tr16(vb + 16 * kPfPitchV + jj * 32);
+        va[jj] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
+      }
+    }
+    // (c) The next item's query once this segment's has been read (the
+    // barrier above), then the tile kPfStages - 1 ahead into the stage the
+    // previous iteration read.
+    {
+      const int nP = it.P + kPfItemCost + it.T;  // span start of the next item
+      if (!seg_start && nP + kPfItemCost < end && q_issued_for != nP) {
+        PfItem nx = it;
+        pf_next_item(nx, cu_q, cu_k, p.n_pre, kvs_total, p.nslices, qtile);
+        issue_q(nx);
+        issued += kPfQLoadsPerWave;
+        q_mark = issued;
+        q_issued_for = nP;
+      }
+    }
+    if (prod_live()) {
+      produce(stage == 0 ? kPfStages - 1 : stage - 1);
+      issued += kPfTileLoads;
+    }
+#pragma unroll
+    for (int k = 0; k + 1 < kPfStages - 1; ++k) mk[k] = mk[k + 1];
+    mk[kPfStages - 2] = issued;
+    // (d) Attend: the unmasked form when every key exists and every valid
+    // column sees all 32.
+    const int key0 = ct * kTile;
+    if (key0 + kTile <= it.geo.sk && key0 + kTile - 1 <= min_klim) {
+      pf_attend<false>(st, kop, va, Q, klim, key0, it.geo.sk, p.scale_log2, L);
+    } else {
+      pf_attend<true>(st, kop, va, Q, klim, key0, it.geo.sk, p.scale_log2, L);
+    }
+    // (e) Segment end: store (lane (lm, lg) holds dims 16 jj + 4 lg .. + 3 of
+    // column lm for every jj), then move to the next item.
+    if (seg_end) {
+      const int q0 = it.qt * qtile;
+      const int hs = min(p.hs, p.group - it.s * p.hs);
+#pragma unroll
+      for (int cb = 0; cb < kPreNCB; ++cb) {
+        const int tq = q0 + (wave * kPreNCB + cb) * p.tpb + L.lm / p.hs;
+        const int hh = L.lm % p.hs;
+        if ((L.lm < p.tpb * p.hs) && hh < hs && tq < it.geo.sq) {
+          const int64_t row = int64_t(p.n_dec) + it.cq0 + tq;
+          const int head = it.g * p.group + it.s * p.hs + hh;
+          const float l = st.l[cb][0];
+          if (split < 0) {
+            const float inv = 1.f / l;
+            uint16_t* dst = p.out + row * p.o_st + int64_t(head) * p.o_sh + 4 * L.lg;
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) {
+              *reinterpret_cast<u32x2_t*>(dst + 16 * jj) =
+                  u32x2_t{pack_bf16x2_fast(st.o[cb][jj][0] * inv, st.o[cb][jj][1] * inv),
+                          pack_bf16x2_fast(st.o[cb][jj][2] * inv, st.o[cb][jj][3] * inv)};
+            }
+          } else {
+            const int64_t base = (row * p.num_heads + head) * p.max_splits + split;
+            const float il = l > 0.f ? 1.f / l : 0.f;
+            float* dst = p.part_o + base * kD + 4 * L.lg;
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj)
+              *reinterpret_cast<float4*>(dst + 16 * jj) =
+                  make_float4(st.o[cb][jj][0] * il, st.o[cb][jj][1] * il, st.o[cb][jj][2] * il,
+                              st.o[cb][jj][3] * il);
+            if (L.lg == 0) p.part_lse[base] = l > 0.f ? st.m[cb] + __log2f(l) : -INFINITY;
+          }
+        }
+      }
+    }
+    if (++ct == it.T) {
+      if (it.P + kPfItemCost + it.T >= end) break;
+      pf_next_item(it, cu_q, cu_k, p.n_pre, kvs_total, p.nslices, qtile);
+      ct = 0;
+    }
+    stage = stage == kPfStages - 1 ? 0 : stage + 1;
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+}
+
 // Split-K merge: one wave per (query row, head), lane l owning dims 2l and
 // 2l + 1.  The splits are taken 16 at a time with every load of a batch in
 // flight together (log-sum-exps are wave-uniform), so a row split 16 ways
@@ -2600,6 +3290,35 @@ bool split_mixed(int64_t num_decode_rows, int64_t page_size) {
          env_int("KVC_MIXED_SPLIT", 1) != 0;
 }
 
+// Prefill-only launches over bf16 keys run as one stream-K launch
+// (prefill_sk_kernel) unless KVC_PREFILL_SK=0 selects one workgroup per
+// prefill unit.  The workspace query cannot see the key encoding or the
+// query strides, so it sizes for both; the launch also needs every chunk's
+// query rows below 2 GiB (one buffer resource).
+bool prefill_stream_k(int64_t num_decode_rows) {
+  return num_decode_rows == 0 && !mixed_stream_k() && env_int("KVC_PREFILL_SK", 1) != 0;
+}
+
+// Split cap of a stream-K prefill launch: an item of T tiles spans at most
+// ceil(T / S) + 1 shares; the cap is 64 and the partials' byte bound.
+SkPlan plan_prefill_sk(int64_t num_q_tokens, int64_t num_heads, int64_t max_seqlen_k) {
+  SkPlan sp{true, int(device_cus()), 2};
+  int64_t ms = (max_seqlen_k + kTile - 1) / kTile / kPfMinShare + 2;
+  const int64_t per_split = num_q_tokens * num_heads * (kD + 1) * int64_t(sizeof(float));
+  const int64_t cap = per_split > 0 ? kSkMaxPartialBytes / per_split : 64;
+  ms = std::min<int64_t>(std::min<int64_t>(ms, 64), cap);
+  sp.max_splits = int(ms < 2 ? 2 : ms);
+  return sp;
+}
+
+void launch_prefill_sk(const AttnParams& p, int grid, bool fresh, hipStream_t st) {
+  if (fresh) {
+    prefill_sk_kernel<true><<<grid, kThreads, 0, st>>>(p, p.cu_q, p.cu_k, p.block_tables);
+  } else {
+    prefill_sk_kernel<false><<<grid, kThreads, 0, st>>>(p, p.cu_q, p.cu_k, p.block_tables);
+  }
+}
+
 template <int kEnc>
 void launch_varlen_enc(const AttnParams& p, int grid, bool fresh, hipStream_t st) {
   if (fresh) {
@@ -2791,7 +3510,14 @@ extern "C" size_t kvc_varlen_workspace_bytes(int64_t num_q_tokens, int64_t num_h
     const int64_t ps = (max_seqlen_k + ks - 1) / ks;
     splits = ps > splits ? ps : splits;
   }
-  return partial_bytes(num_q_tokens, num_heads, splits);
+  const size_t units = partial_bytes(num_q_tokens, num_heads, splits);
+  if (prefill_stream_k(num_decode_rows)) {
+    const SkPlan sp = plan_prefill_sk(num_q_tokens, num_heads, max_seqlen_k);
+    const size_t sk =
+        sk_workspace_bytes(num_q_tokens, num_heads, num_kv_heads * hp.nslices, sp.max_splits);
+    return sk > units ? sk : units;
+  }
+  return units;
 }
 
 extern "C" int kvc_varlen_attention(
@@ -2959,6 +3685,36 @@ extern "C" int kvc_varlen_attention(
     if (rc != KVC_OK) return rc;
     launch_merge(p, num_q_tokens, st);
     return check_launch("varlen_attention merge");
+  }
+  if (prefill_stream_k(num_decode_rows) && (fresh || kv_dtype == KVC_KV_BF16) &&
+      num_q_tokens * q_stride_t * 2 < (int64_t(1) << 31)) {
+    // Prefill rows only, bf16 keys: one workgroup per CU over the
+    // concatenated tiles of every item (prefill_sk_kernel), then the merge.
+    const int64_t kv_slices = num_kv_heads * hp.nslices;
+    const int64_t qtile = int64_t(kWaves) * kPreNCB * hp.tpb;
+    const int64_t bound =
+        kv_slices * (num_q_tokens / qtile + num_prefill + 1) * ((max_seqlen_k + kTile - 1) / kTile);
+    KVC_REQUIRE(bound < (int64_t(1) << 30), KVC_ERR_VALUE, "varlen_attention: launch too large");
+    const SkPlan sp = plan_prefill_sk(num_q_tokens, num_heads, max_seqlen_k);
+    p.max_splits = sp.max_splits;
+    p.sk_min_share = kPfMinShare;
+    p.merge_first = 0;
+    const size_t need = sk_workspace_bytes(num_q_tokens, num_heads, kv_slices, sp.max_splits);
+    KVC_REQUIRE(workspace != nullptr && workspace_bytes >= need, KVC_ERR_WORKSPACE,
+                "varlen_attention: workspace of %zu bytes needed (got %zu)", need,
+                workspace_bytes);
+    set_partials(p, workspace, num_q_tokens);
+    p.sk_nseg = reinterpret_cast<int*>(static_cast<char*>(workspace) +
+                                       sk_partial_part(num_q_tokens, num_heads, p.max_splits));
+    hipStream_t st = as_stream(stream);
+    if (num_prefill > 0) {
+      launch_prefill_sk(p, sp.grid, fresh, st);
+      rc = check_launch("varlen_attention");
+      if (rc != KVC_OK) return rc;
+      launch_merge(p, num_q_tokens, st);
+      rc = check_launch("varlen_attention merge");
+    }
+    return rc;
   }
   p.max_splits = int(max_splits);
   const size_t need = partial_bytes(num_q_tokens, num_heads, max_splits);

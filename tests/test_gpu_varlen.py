@@ -20,11 +20,14 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-@pytest.fixture(params=["units", "stream-k"])
+@pytest.fixture(params=["prefill-sk", "units", "stream-k"])
 def partition(request, monkeypatch):
-    """Both launch partitions of the mixed kernel: one workgroup per prefill
-    unit (the default) and the stream-K cut of all items' tiles."""
+    """Every launch partition: prefill rows over bf16 keys as one stream-K
+    prefill launch (the default), one workgroup per prefill unit
+    (KVC_PREFILL_SK=0), and the single stream-K launch of decode and prefill
+    items together (KVC_MIXED_STREAMK=1)."""
     monkeypatch.setenv("KVC_MIXED_STREAMK", "1" if request.param == "stream-k" else "0")
+    monkeypatch.setenv("KVC_PREFILL_SK", "0" if request.param == "units" else "1")
     return request.param
 
 
