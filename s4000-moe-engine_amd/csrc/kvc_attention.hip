@@ -3059,6 +3059,97 @@ void launch_merge(const AttnParams& p, int64_t rows, hipStream_t st) {
       p, int(rows));
 }
 
+// Split-K merge of a stream-K prefill launch: one wave per (query row, kv
+// slice).  The wave reads the slice's split count once; lane l then owns
+// head l / 8 of the slice (eight heads per pass) and dims 16 (l % 8) .. +15,
+// so a whole slice's partials are in flight together and a row costs two
+// memory round trips (the count, then the partials) whatever its head count.
+constexpr int kSliceBatch = 8;  // splits per load batch
+__global__ void __launch_bounds__(64 * kMergeWaves)
+merge_slices_kernel(AttnParams p, int num_rows, const float* __restrict__ part_o,
+                    const float* __restrict__ part_lse, const int* __restrict__ nseg_arr) {
+  const int lane = threadIdx.x & 63;
+  const int e = lane >> 3;   // head within the pass
+  const int sub = lane & 7;  // 16-dim chunk
+  const int kvs_total = p.kvh * p.nslices;
+  const int64_t wv = int64_t(blockIdx.x) * kMergeWaves + (threadIdx.x >> 6);
+  const int64_t row = wv / kvs_total;
+  if (row >= num_rows) return;
+  const int kvs = int(wv - row * kvs_total);
+  const int nsplit = uniform(nseg_arr[row * kvs_total + kvs]);
+  if (nsplit <= 1) return;
+  const int g = kvs / p.nslices;
+  const int s = kvs - g * p.nslices;
+  const int h0 = g * p.group + s * p.hs;
+  const int hs = min(p.hs, p.group - s * p.hs);
+  for (int hb = 0; hb < hs; hb += 8) {
+    const int hh = min(hb + e, hs - 1);  // lanes past the slice repeat its last head
+    const int64_t base = (row * p.num_heads + h0 + hh) * p.max_splits;
+    float m = -INFINITY, l = 0.f;
+    float acc[16];
+#pragma unroll
+    for (int d = 0; d < 16; ++d) acc[d] = 0.f;
+    for (int s0 = 0; s0 < nsplit; s0 += kSliceBatch) {
+      const int cnt = min(kSliceBatch, nsplit - s0);
+      float lse[kSliceBatch];
+      float4 o[kSliceBatch][4];
+#pragma unroll
+      for (int k = 0; k < kSliceBatch; ++k) {
+        if (k < cnt) {
+          lse[k] = part_lse[base + s0 + k];
+          const float4* src = reinterpret_cast<const float4*>(part_o + (base + s0 + k) * kD) + 4 * sub;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) o[k][q] = src[q];
+        }
+      }
+      float bm = -INFINITY;
+#pragma unroll
+      for (int k = 0; k < kSliceBatch; ++k)
+        if (k < cnt) bm = fmaxf(bm, lse[k]);
+      const float m_new = fmaxf(m, bm);
+      if (m_new != -INFINITY) {  // else every split so far is empty
+        const float a = __builtin_amdgcn_exp2f(m - m_new);
+        l *= a;
+#pragma unroll
+        for (int d = 0; d < 16; ++d) acc[d] *= a;
+#pragma unroll
+        for (int k = 0; k < kSliceBatch; ++k) {
+          if (k < cnt) {
+            const float wgt = __builtin_amdgcn_exp2f(lse[k] - m_new);
+            l += wgt;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              acc[4 * q + 0] += wgt * o[k][q].x;
+              acc[4 * q + 1] += wgt * o[k][q].y;
+              acc[4 * q + 2] += wgt * o[k][q].z;
+              acc[4 * q + 3] += wgt * o[k][q].w;
+            }
+          }
+        }
+        m = m_new;
+      }
+    }
+    if (hb + e < hs) {
+      const float inv = 1.f / l;
+      uint16_t* dst = p.out + row * p.o_st + int64_t(h0 + hb + e) * p.o_sh + 16 * sub;
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        *reinterpret_cast<u32x4_t*>(dst + 8 * q) =
+            u32x4_t{pack_bf16x2_fast(acc[8 * q + 0] * inv, acc[8 * q + 1] * inv),
+                    pack_bf16x2_fast(acc[8 * q + 2] * inv, acc[8 * q + 3] * inv),
+                    pack_bf16x2_fast(acc[8 * q + 4] * inv, acc[8 * q + 5] * inv),
+                    pack_bf16x2_fast(acc[8 * q + 6] * inv, acc[8 * q + 7] * inv)};
+      }
+    }
+  }
+}
+
+void launch_merge_slices(const AttnParams& p, int64_t rows, hipStream_t st) {
+  const int64_t waves = rows * p.kvh * p.nslices;
+  merge_slices_kernel<<<unsigned((waves + kMergeWaves - 1) / kMergeWaves), 64 * kMergeWaves, 0,
+                        st>>>(p, int(rows), p.part_o, p.part_lse, p.sk_nseg);
+}
+
 // ---------------------------------------------------------------------------
 // Host-side launch planning.
 // ---------------------------------------------------------------------------
@@ -3711,7 +3802,7 @@ extern "C" int kvc_varlen_attention(
       launch_prefill_sk(p, sp.grid, fresh, st);
       rc = check_launch("varlen_attention");
       if (rc != KVC_OK) return rc;
-      launch_merge(p, num_q_tokens, st);
+      launch_merge_slices(p, num_q_tokens, st);
       rc = check_launch("varlen_attention merge");
     }
     return rc;
