@@ -286,25 +286,43 @@ def run_mixed(args, torch):
                                 cu_seqlens_q=cq, cu_seqlens_k=ck, cu_seqlens_q_list=cu_q,
                                 cu_seqlens_k_list=cu_k)
 
-    for _ in range(args.warmup):
-        call()
-    torch.cuda.synchronize()
-    timer = EventTimer(torch)
-    for _ in range(args.steps):
-        s = timer.start()
-        call()
-        timer.stop(s)
-    torch.cuda.synchronize()
-    ms = timer.mean_ms()
+    # The same prefill rows alone (their block-table rows and queries), to
+    # price the prefill launch against the MFMA roofline.
+    nd = len(dec)
+    q_pre, bt_pre = q[nd:], bt[nd:]
+
+    def call_prefill():
+        return varlen_attention(q_pre, kc, vc, scale=128 ** -0.5, block_tables=bt_pre,
+                                cu_seqlens_q=cq, cu_seqlens_k=ck, cu_seqlens_q_list=cu_q,
+                                cu_seqlens_k_list=cu_k)
+
+    def timed(fn):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        timer = EventTimer(torch)
+        for _ in range(args.steps):
+            s = timer.start()
+            fn()
+            timer.stop(s)
+        torch.cuda.synchronize()
+        return timer.mean_ms()
+
+    ms = timed(call)
+    ms_pre = timed(call_prefill)
     flops = 0
     for p, c in chunks:
         for r in range(c):
             flops += 4 * 128 * heads * (p + r + 1)
     kv = sum(dec) * 2 * kvh * 128 * 2
+    pre_tflops = flops / (ms_pre * 1e-3) / 1e12
     return {"workload": "mixed: 60 decode rows ctx U[256,4096] + 4x256-token prefill chunks "
-                        "(prefix 0/512/2048/8192), one varlen launch + merge",
+                        "(prefix 0/512/2048/8192): paged decode launch + stream-K prefill "
+                        "launch + their merges",
             "ms": round(ms, 4), "prefill_gflop": round(flops / 1e9, 2),
-            "prefill_TFLOPs_if_alone": round(flops / (ms * 1e-3) / 1e12, 1),
+            "prefill_only_ms": round(ms_pre, 4),
+            "prefill_TFLOPs": round(pre_tflops, 1),
+            "prefill_mfma_frac": round(pre_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
             "decode_kv_GB": round(kv / 1e9, 3),
             "tokens_per_s": round(T / (ms * 1e-3), 1)}
 
