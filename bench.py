@@ -38,7 +38,8 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "decode-dist", "int8", "mixed", "append", "swap", "copy"])
+                    choices=["decode", "decode-dist", "int8", "mixed", "append", "swap", "copy",
+                             "rope"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample", type=int, default=64,
                     help="sequences of the workload the CPU baseline runs")
@@ -351,6 +352,55 @@ def run_append(args, torch):
             "GBps": round(byts / (ms * 1e-3) / 1e9, 1)}
 
 
+def run_rope(args, torch):
+    """q/k RMSNorm + rotary embedding + KV append in one launch at the
+    Qwen3-30B-A3B attention shape (32 q / 4 kv heads x 128, page 256): a
+    decode step (64 tokens) and a 16384-token prefill batch.  HBM bytes per
+    token: the fused qkv row read (40 x 256 B) + q out (32 x 256 B) + K and V
+    rows appended (2 x 4 x 256 B) + the token's fp32 cos/sin row (512 B) +
+    its position and slot (16 B)."""
+    from nanovllm_amd.layers.rotary import build_cos_sin_cache, qk_norm_rope_store
+    dev = torch.device("cuda:0")
+    H, KVH = 32, 4
+    per_token = (H + 2 * KVH) * 256 + H * 256 + 2 * KVH * 256 + 512 + 16
+    cache = build_cos_sin_cache(128, 40960, 1000000.0, dev)
+    qw = torch.ones(128, dtype=torch.bfloat16, device=dev)
+    kw = torch.ones(128, dtype=torch.bfloat16, device=dev)
+    out = {"workload": "q/k RMSNorm + RoPE + KV append, 32q/4kv/128 bf16, one launch"}
+    for N in (64, 16384):
+        g = torch.Generator(device=dev).manual_seed(N)
+        qkv = torch.randn(N, (H + 2 * KVH) * 128, generator=g, device=dev, dtype=torch.bfloat16)
+        q = qkv[:, :H * 128].view(N, H, 128)
+        k = qkv[:, H * 128:(H + KVH) * 128].view(N, KVH, 128)
+        v = qkv[:, (H + KVH) * 128:].view(N, KVH, 128)
+        pos = torch.randint(0, 40960, (N,), generator=g, device=dev)
+        blocks = max(64, (N + 255) // 256 * 2)
+        kc = torch.empty(blocks, 256, KVH, 128, device=dev, dtype=torch.bfloat16)
+        vc = torch.empty_like(kc)
+        slots = torch.randperm(blocks * 256, generator=g, device=dev)[:N]
+        q_out = torch.empty(N, H, 128, device=dev, dtype=torch.bfloat16)
+
+        def call():
+            qk_norm_rope_store(q, k, v, pos, cache, qw, kw, 1e-6, kc, vc, slots,
+                               return_k=False, q_out=q_out)
+
+        for _ in range(args.warmup):
+            call()
+        torch.cuda.synchronize()
+        timer = EventTimer(torch)
+        for _ in range(args.steps):
+            s = timer.start()
+            call()
+            timer.stop(s)
+        torch.cuda.synchronize()
+        ms = timer.mean_ms()
+        out[f"tokens_{N}"] = {"us": round(ms * 1e3, 2),
+                              "GBps": round(N * per_token / (ms * 1e-3) / 1e9, 1),
+                              "tokens_per_s": round(N / (ms * 1e-3), 1)}
+    out["bytes_per_token"] = per_token
+    return out
+
+
 def run_swap(args, torch):
     """Block eviction / offload step at the config-5 shape: a pool of 8192
     blocks of [2 (K, V), 48 layers, 256, 4 kv heads, 128] bf16 (24 MiB each,
@@ -460,6 +510,8 @@ def main():
         res = run_append(args, torch)
     elif args.workload == "copy":
         res = run_copy(args, torch)
+    elif args.workload == "rope":
+        res = run_rope(args, torch)
     else:
         res = run_swap(args, torch)
     print(json.dumps(res), flush=True)

@@ -256,6 +256,40 @@ int kvc_block_h2d(const void* host_src, int64_t host_item_stride, int64_t planes
                   int64_t block_bytes, const int64_t* host_ids, int64_t n, void* pool,
                   int64_t plane_stride, kvc_stream_t stream);
 
+/* ---------------------------------------------------------------------------
+ * The step that feeds the path: q/k RMSNorm + rotary embedding + KV append.
+ * ------------------------------------------------------------------------- */
+
+/* Replaces, in one launch, Qwen3Attention.forward's sequence between the qkv
+ * projection and attention (nanovllm/models/qwen3.py:77-86):
+ *   q = q_norm(q); k = k_norm(k)                 (nanovllm/layers/layernorm.py:18-26)
+ *   q, k = rotary_emb(positions, q, k)           (nanovllm/layers/rotary_embedding.py:7-15,
+ *                                                 :38-49, neox halves)
+ *   store_kvcache(k, v, k_cache, v_cache, slots) (nanovllm/layers/attention.py:9-30)
+ * q/k/v are bf16 [num_tokens, heads, 128] with their own element strides
+ * (views of the fused qkv projection need no copy).  Per (token, head):
+ *   xf = float(x); r = 1 / sqrt(sum(xf^2) / 128 + eps)   (IEEE sqrt and divide)
+ *   y = bf16(bf16(xf * r) * w)                            (skipped when w is NULL)
+ *   out = bf16(y1 * c - y2 * s | y2 * c + y1 * s)         (c, s = cos_sin_cache[pos])
+ * cos_sin_cache is fp32 [max_position, 128] (cos in 0..63, sin in 64..127),
+ * as RotaryEmbedding builds it.  q_out receives the rotated q; k_out (may be
+ * NULL) the rotated k.  With k_cache/v_cache non-NULL, the rotated k and the
+ * unchanged v are appended at slot_mapping like kvc_store_kv (negative slots
+ * wrap, slots outside [0, num_slots) are skipped).  A negative position wraps
+ * like a Python index; one still outside the cache yields NaN rows (torch
+ * raises IndexError).  position/slot index bytes: 4 or 8. */
+int kvc_qk_norm_rope_store(const void* q, int64_t q_stride_t, int64_t q_stride_h,
+                           const void* k, int64_t k_stride_t, int64_t k_stride_h,
+                           const void* v, int64_t v_stride_t, int64_t v_stride_h,
+                           int64_t num_tokens, int64_t num_heads, int64_t num_kv_heads,
+                           int64_t head_dim, const void* positions, int position_index_bytes,
+                           const void* q_norm_weight, const void* k_norm_weight, float eps,
+                           const float* cos_sin_cache, int64_t max_position, void* q_out,
+                           int64_t q_out_stride_t, int64_t q_out_stride_h, void* k_out,
+                           int64_t k_out_stride_t, int64_t k_out_stride_h, void* k_cache,
+                           void* v_cache, int64_t num_slots, const void* slot_mapping,
+                           int slot_index_bytes, kvc_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -307,3 +307,47 @@ def decode_kv_bytes(context_lens, kvh: int, d: int, elem_bytes: int) -> int:
 
 def log2e() -> float:
     return 1.0 / math.log(2.0)
+
+
+# ---------------------------------------------------------------------------
+# The step in front of the path: q/k RMSNorm + rotary embedding.  CPU torch in
+# the engine's own op order (its arithmetic is torch's), bf16 in and out.
+# ---------------------------------------------------------------------------
+
+
+def cos_sin_cache_ref(head_size: int, max_position: int, base: float) -> torch.Tensor:
+    """nanovllm/layers/rotary_embedding.py:30-35: fp32 [max_position, D],
+    cos(t * inv_freq) then sin(t * inv_freq)."""
+    inv_freq = 1.0 / (base ** (torch.arange(0, head_size, 2, dtype=torch.float) / head_size))
+    t = torch.arange(max_position, dtype=torch.float)
+    freqs = torch.einsum("i,j -> ij", t, inv_freq)
+    return torch.cat((freqs.cos(), freqs.sin()), dim=-1)
+
+
+def rms_norm_ref(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """nanovllm/layers/layernorm.py:18-26 (rms_forward), bf16 x and weight."""
+    xf = x.float()
+    var = xf.pow(2).mean(dim=-1, keepdim=True)
+    return (xf * torch.rsqrt(var + eps)).to(x.dtype).mul_(weight)
+
+
+def apply_rotary_ref(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """nanovllm/layers/rotary_embedding.py:7-15 (neox halves, fp32 arithmetic)."""
+    x1, x2 = torch.chunk(x.float(), 2, dim=-1)
+    y1 = x1 * cos - x2 * sin
+    y2 = x2 * cos + x1 * sin
+    return torch.cat((y1, y2), dim=-1).to(x.dtype)
+
+
+def qk_norm_rope_ref(q: torch.Tensor, k: torch.Tensor, positions: torch.Tensor,
+                     cos_sin_cache: torch.Tensor, q_w: torch.Tensor | None,
+                     k_w: torch.Tensor | None, eps: float):
+    """nanovllm/models/qwen3.py:80-85 on CPU tensors: q/k [N, heads, D] bf16
+    -> (rotated q, rotated k).  Norms are skipped when the weight is None."""
+    if q_w is not None:
+        q = rms_norm_ref(q, q_w, eps)
+    if k_w is not None:
+        k = rms_norm_ref(k, k_w, eps)
+    cos_sin = cos_sin_cache[positions.long()].unsqueeze(1)
+    cos, sin = cos_sin.chunk(2, dim=-1)
+    return apply_rotary_ref(q, cos, sin), apply_rotary_ref(k, cos, sin)

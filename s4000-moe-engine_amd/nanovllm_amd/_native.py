@@ -62,6 +62,10 @@ SIGNATURES = {
     "kvc_block_copy": (_INT, [_P, _I64, _I64, _I64, _P, _P, _I64, _P]),
     "kvc_block_d2h": (_INT, [_P, _I64, _I64, _I64, _P, _I64, _P, _I64, _P]),
     "kvc_block_h2d": (_INT, [_P, _I64, _I64, _I64, _P, _I64, _P, _I64, _P]),
+    "kvc_qk_norm_rope_store": (_INT, [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,
+                                      _I64, _I64, _I64, _I64, _P, _INT, _P, _P, _F32,
+                                      _P, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _P,
+                                      _I64, _P, _INT, _P]),
 }
 
 _lock = threading.Lock()

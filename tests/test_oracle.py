@@ -289,3 +289,61 @@ def test_block_gather_scatter_roundtrip_and_copy_semantics():
     chain = pool.copy()
     ko.block_copy(chain, [1, 2], [2, 3])          # simultaneous: 3 gets the OLD block 2
     assert np.array_equal(chain[:, 2], pool[:, 1]) and np.array_equal(chain[:, 3], pool[:, 2])
+
+
+# ---------------------------------------------------------------------------
+# q/k RMSNorm + rotary embedding (the step in front of the path)
+# ---------------------------------------------------------------------------
+def test_cos_sin_cache_matches_closed_form():
+    cache = ko.cos_sin_cache_ref(128, 64, 10000.0)
+    assert cache.shape == (64, 128) and cache.dtype == torch.float32
+    t = np.arange(64)[:, None]
+    inv = 10000.0 ** (-np.arange(0, 128, 2) / 128.0)
+    np.testing.assert_allclose(cache[:, :64].numpy(), np.cos(t * inv), atol=2e-5)
+    np.testing.assert_allclose(cache[:, 64:].numpy(), np.sin(t * inv), atol=2e-5)
+
+
+def test_rotary_at_position_zero_is_the_identity():
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(5, 4, 128, generator=g).to(torch.bfloat16)
+    cache = ko.cos_sin_cache_ref(128, 16, 10000.0)
+    q, k = ko.qk_norm_rope_ref(x, x[:, :2], torch.zeros(5, dtype=torch.long), cache, None, None,
+                               1e-6)
+    assert torch.equal(q, x) and torch.equal(k, x[:, :2])
+
+
+def test_rotary_is_multiplication_by_the_phase():
+    # (x1 + i x2) * exp(i p theta_j), theta_j = base^(-2j/D), in float64: a
+    # swapped sign or half fails by O(1).
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(7, 3, 128, generator=g).to(torch.bfloat16)
+    pos = torch.tensor([1, 5, 17, 100, 511, 1000, 2047])
+    cache = ko.cos_sin_cache_ref(128, 2048, 10000.0)
+    q, _ = ko.qk_norm_rope_ref(x, x[:, :1], pos, cache, None, None, 1e-6)
+    xf = x.double().numpy()
+    theta = 10000.0 ** (-np.arange(0, 128, 2) / 128.0)
+    ph = pos.double().numpy()[:, None, None] * theta[None, None, :]
+    z = (xf[..., :64] + 1j * xf[..., 64:]) * np.exp(1j * ph)
+    want = np.concatenate([z.real, z.imag], axis=-1)
+    got = q.double().numpy()
+    assert np.abs(got - want).max() <= 2.0 ** -7 * np.abs(want).max() + 2e-3
+    # The rotation keeps each (x1_j, x2_j) pair's length.
+    n_in = xf[..., :64] ** 2 + xf[..., 64:] ** 2
+    n_out = got[..., :64] ** 2 + got[..., 64:] ** 2
+    assert np.abs(n_out - n_in).max() <= 2.0 ** -6 * n_in.max()
+
+
+def test_rms_norm_closed_forms():
+    # A constant row c normalises to c / sqrt(c^2 + eps) = 1 (after the bf16
+    # rounding), so the output is the weight itself.
+    w = torch.tensor(np.linspace(-2, 2, 128), dtype=torch.float32).to(torch.bfloat16)
+    for c in (0.75, -3.0, 40.0):
+        x = torch.full((1, 1, 128), c).to(torch.bfloat16)
+        y = ko.rms_norm_ref(x, w, 1e-6)
+        assert torch.equal(y[0, 0], w * math.copysign(1.0, c))
+    # A random row comes out with unit RMS (unit weight), to bf16 precision.
+    g = torch.Generator().manual_seed(5)
+    x = (torch.randn(64, 128, generator=g) * 7).to(torch.bfloat16)
+    y = ko.rms_norm_ref(x, torch.ones(128, dtype=torch.bfloat16), 1e-6).double()
+    rms = y.pow(2).mean(-1).sqrt()
+    assert torch.all((rms - 1).abs() < 2.0 ** -7)
