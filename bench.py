@@ -39,7 +39,7 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="decode",
                     choices=["decode", "decode-dist", "int8", "mixed", "append", "swap", "copy",
-                             "rope"])
+                             "rope", "decode-graph"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample", type=int, default=64,
                     help="sequences of the workload the CPU baseline runs")
@@ -401,6 +401,66 @@ def run_rope(args, torch):
     return out
 
 
+def run_decode_graph(args, torch):
+    """A 48-layer decode step's KV work (per layer: append one token per
+    sequence, then paged decode) run eagerly and as a replayed HIP graph of
+    the batch's bucket, with the padded rows aimed at the scratch block.  Two
+    sizes: batch 64 x context 4096 (the headline shape, GPU-bound) and
+    batch 8 x context 512 (launch-bound).  Shape 32 q / 4 kv heads x 128 bf16,
+    page 256."""
+    from nanovllm_amd.engine.graph_runner import DecodeGraphRunner
+    from nanovllm_amd.kernels.paged_attention import paged_decode_attention
+    from nanovllm_amd.layers.attention import store_kvcache
+    from nanovllm_amd.workloads import build_block_tables, slots_for_last_token
+    dev = torch.device("cuda:0")
+    L, H, KVH = 48, 32, 4
+    out = {"workload": "48-layer decode step KV work (append + paged decode per layer), "
+                       "eager vs HIP-graph replay"}
+    for bs, ctx in ((64, 4096), (8, 512)):
+        nb = bs * ((ctx + 255) // 256)
+        g = torch.Generator(device=dev).manual_seed(bs)
+        kcs = [torch.randn(nb + 1, 256, KVH, 128, generator=g, device=dev, dtype=torch.bfloat16)
+               for _ in range(L)]
+        vcs = [torch.randn(nb + 1, 256, KVH, 128, generator=g, device=dev, dtype=torch.bfloat16)
+               for _ in range(L)]
+        lens = [ctx] * bs
+        bt = build_block_tables(lens, nb, 256, torch.Generator().manual_seed(bs))
+        slots = slots_for_last_token(bt, lens, 256).to(dev)
+        bt = bt.to(dev)
+        cl = torch.tensor(lens, dtype=torch.int32, device=dev)
+        q = torch.randn(L, bs, H, 128, generator=g, device=dev, dtype=torch.bfloat16)
+        k = torch.randn(L, bs, KVH, 128, generator=g, device=dev, dtype=torch.bfloat16)
+        v = torch.randn(L, bs, KVH, 128, generator=g, device=dev, dtype=torch.bfloat16)
+
+        def eager():
+            for layer in range(L):
+                store_kvcache(k[layer], v[layer], kcs[layer], vcs[layer], slots)
+                paged_decode_attention(q[layer], kcs[layer], vcs[layer], bt, cl, 128 ** -0.5, ctx)
+
+        runner = DecodeGraphRunner(kcs, vcs, H, max_bs=bs, max_blocks_per_seq=bt.size(1),
+                                   scale=128 ** -0.5, buckets=[bs])
+        runner.capture()
+
+        def graph():
+            runner.run(q, k, v, slots, cl, bt)
+
+        res = {}
+        for name, fn in (("eager", eager), ("graph", graph)):
+            for _ in range(max(2, args.warmup // 2)):
+                fn()
+            torch.cuda.synchronize()
+            steps = max(5, args.steps // 5)
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                fn()
+            torch.cuda.synchronize()
+            res[f"{name}_ms_per_step"] = round((time.perf_counter() - t0) * 1e3 / steps, 3)
+        out[f"bs{bs}_ctx{ctx}"] = res
+        del kcs, vcs, runner
+        torch.cuda.empty_cache()
+    return out
+
+
 def run_swap(args, torch):
     """Block eviction / offload step at the config-5 shape: a pool of 8192
     blocks of [2 (K, V), 48 layers, 256, 4 kv heads, 128] bf16 (24 MiB each,
@@ -512,6 +572,8 @@ def main():
         res = run_copy(args, torch)
     elif args.workload == "rope":
         res = run_rope(args, torch)
+    elif args.workload == "decode-graph":
+        res = run_decode_graph(args, torch)
     else:
         res = run_swap(args, torch)
     print(json.dumps(res), flush=True)

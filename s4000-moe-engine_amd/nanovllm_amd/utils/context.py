@@ -64,3 +64,20 @@ def set_context(is_prefill, cu_seqlens_q=None, cu_seqlens_k=None, max_seqlen_q=0
 def reset_context():
     global _CURRENT
     _CURRENT = Context()
+
+
+def last_row_indices(context: Context, device=None) -> torch.Tensor | None:
+    """Rows the LM head samples (nanovllm/layers/embed_head.py:56-71): in a
+    mixed batch every decode row [0, n) then each prefill chunk's last row
+    (cu_seqlens_q is prefill-relative, so + n); in a prefill batch each
+    chunk's last row; None for a decode batch (every row).  Built on the
+    device from the context's tensors, with no host read, so it can run
+    inside a captured graph."""
+    if context.is_mixed:
+        n = context.num_decode_rows
+        cu = context.cu_seqlens_q
+        dec = torch.arange(n, device=cu.device if device is None else device, dtype=torch.long)
+        return torch.cat([dec, cu[1:].long() - 1 + n])
+    if context.is_prefill:
+        return context.cu_seqlens_q[1:].long() - 1
+    return None
