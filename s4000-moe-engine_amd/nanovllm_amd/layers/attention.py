@@ -25,6 +25,7 @@ from ..kernels.kv_int8 import store_kvcache_int8
 from ..kernels.paged_attention import paged_decode_attention
 from ..kernels.varlen import varlen_attention
 from ..utils.context import get_context
+from .rotary import qk_norm_rope_store
 
 
 def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
@@ -97,12 +98,40 @@ class Attention(nn.Module):
             return self.k_scale, self.v_scale
         return self.k_dscale, self.v_dscale
 
-    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor):
+    def forward_fused(self, positions: torch.Tensor, q: torch.Tensor, k: torch.Tensor,
+                      v: torch.Tensor, cos_sin_cache: torch.Tensor,
+                      q_norm_weight: torch.Tensor | None, k_norm_weight: torch.Tensor | None,
+                      eps: float):
+        """Qwen3Attention.forward's q_norm, k_norm and rotary_emb
+        (nanovllm/models/qwen3.py:82-85) fused with this layer's append
+        (one launch on a bf16 pool), then attention.  q [N, H*D] or
+        [N, H, D]; k, v [N, KVH*D] or [N, KVH, D] (views of the qkv
+        projection are fine)."""
+        context = get_context()
+        N = positions.numel()
+        q3 = q.view(N, self.num_heads, self.head_dim)
+        k3 = k.view(N, self.num_kv_heads, self.head_dim)
+        v3 = v.view(N, self.num_kv_heads, self.head_dim)
+        k_cache, v_cache = self.k_cache, self.v_cache
+        bf16_pool = bool(k_cache.numel() and v_cache.numel()) and not self.kv_cache_is_int8
+        need_k = not bf16_pool or context.block_tables is None
+        with self._profile("attention.qk_norm_rope_store"):
+            q_rot, k_rot = qk_norm_rope_store(
+                q3, k3, v3, positions, cos_sin_cache, q_norm_weight, k_norm_weight, eps,
+                k_cache if bf16_pool else None, v_cache if bf16_pool else None,
+                context.slot_mapping if bf16_pool else None, return_k=need_k)
+        if k_rot is None:
+            k_rot = k3  # not read: the rows are in the pool
+        return self.forward(q_rot, k_rot, v3, kv_stored=bf16_pool)
+
+    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kv_stored: bool = False):
+        """attention.py:130-177.  kv_stored: the step's k/v rows are already
+        in the pool (appended by forward_fused), so the store is skipped."""
         context = get_context()
         k_cache, v_cache = self.k_cache, self.v_cache
-        if k_cache.numel() and v_cache.numel():
-            if self.block_size is None:
-                self.block_size = k_cache.size(1)
+        if k_cache.numel() and self.block_size is None:
+            self.block_size = k_cache.size(1)
+        if k_cache.numel() and v_cache.numel() and not kv_stored:
             with self._profile("attention.kv_store"):
                 if self.kv_cache_is_int8:
                     store_kvcache_int8(k, v, k_cache, v_cache, self.k_scale, self.v_scale,

@@ -125,3 +125,65 @@ def test_empty_batch_and_no_cache():
     with pytest.raises(ValueError):
         qk_norm_rope_store(q[:, :, :64], k, None, torch.empty(0, dtype=torch.int64, device=DEV),
                            cache)
+
+
+@pytest.mark.parametrize("mode", ["decode", "prefill"])
+def test_attention_forward_fused_equals_prologue_then_forward(mode):
+    """Attention.forward_fused (norm + rope + append in one launch, then
+    attention without a second store) == the prologue without the append
+    followed by the layer's ordinary forward (which appends), bit for bit."""
+    from nanovllm_amd.layers.attention import Attention
+    from nanovllm_amd.utils.context import reset_context, set_context
+    from nanovllm_amd.workloads import build_block_tables
+    H, KVH = 32, 4
+    g = torch.Generator().manual_seed(21)
+    if mode == "decode":
+        lens = [1, 300, 2000]
+        N = len(lens)
+    else:
+        lens = [700]          # one chunk of 64 tokens after a 636-token prefix
+        N = 64
+    bt = build_block_tables(lens, 16, 256, g)
+    qkv = torch.randn(N, (H + 2 * KVH) * 128, generator=g).to(torch.bfloat16).to(DEV)
+    q = qkv[:, :H * 128]
+    k = qkv[:, H * 128:(H + KVH) * 128]
+    v = qkv[:, (H + KVH) * 128:]
+    if mode == "decode":
+        pos = torch.tensor([n - 1 for n in lens])
+        slots = torch.tensor([int(bt[i, (n - 1) // 256]) * 256 + (n - 1) % 256
+                              for i, n in enumerate(lens)], dtype=torch.int32)
+    else:
+        pos = torch.arange(lens[0] - N, lens[0])
+        slots = torch.tensor([int(bt[0, p // 256]) * 256 + p % 256 for p in pos.tolist()],
+                             dtype=torch.int32)
+    qw = (1 + 0.1 * torch.randn(128, generator=g)).to(torch.bfloat16).to(DEV)
+    kw = (1 + 0.1 * torch.randn(128, generator=g)).to(torch.bfloat16).to(DEV)
+    cache = build_cos_sin_cache(128, 4096, 1000000.0, DEV)
+    pool_k = torch.randn(17, 256, KVH, 128, generator=g).to(torch.bfloat16).to(DEV)
+    pool_v = torch.randn(17, 256, KVH, 128, generator=g).to(torch.bfloat16).to(DEV)
+    outs, pools = [], []
+    for fused in (True, False):
+        layer = Attention(H, 128, 128 ** -0.5, KVH)
+        layer.k_cache, layer.v_cache = pool_k.clone(), pool_v.clone()
+        if mode == "decode":
+            set_context(False, slot_mapping=slots.to(DEV),
+                        context_lens=torch.tensor(lens, dtype=torch.int32).to(DEV),
+                        block_tables=bt.to(DEV), max_context_len=max(lens))
+        else:
+            cq = torch.tensor([0, N], dtype=torch.int32)
+            ck = torch.tensor([0, lens[0]], dtype=torch.int32)
+            set_context(True, cq.to(DEV), ck.to(DEV), N, lens[0], slots.to(DEV), None, bt.to(DEV),
+                        cu_seqlens_q_list=cq.tolist(), cu_seqlens_k_list=ck.tolist())
+        if fused:
+            o = layer.forward_fused(pos.to(DEV), q, k, v, cache, qw, kw, 1e-6)
+        else:
+            qr, kr = qk_norm_rope_store(q.view(N, H, 128), k.view(N, KVH, 128), None, pos.to(DEV),
+                                        cache, qw, kw, 1e-6)
+            o = layer.forward(qr, kr, v.view(N, KVH, 128))
+        torch.cuda.synchronize()
+        reset_context()
+        outs.append(o.cpu())
+        pools.append((layer.k_cache.cpu(), layer.v_cache.cpu()))
+    assert np.array_equal(bits(outs[0]), bits(outs[1]))
+    assert np.array_equal(bits(pools[0][0]), bits(pools[1][0]))
+    assert np.array_equal(bits(pools[0][1]), bits(pools[1][1]))
