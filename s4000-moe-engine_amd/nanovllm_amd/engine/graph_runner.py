@@ -85,11 +85,12 @@ class DecodeGraphRunner:
 
     def _step(self, bs: int) -> None:
         sm, cl, bt = self.slot_mapping[:bs], self.context_lens[:bs], self.block_tables[:bs]
+        max_len = bt.size(1) * self.page  # an upper bound: no host read of context_lens
         for layer in range(self.num_layers):
             kc, vc = self.k_caches[layer], self.v_caches[layer]
             store_kvcache(self.k[layer, :bs], self.v[layer, :bs], kc, vc, sm)
             self.out[layer, :bs] = paged_decode_attention(
-                self.q[layer, :bs], kc, vc, bt, cl, self.scale, self.page)
+                self.q[layer, :bs], kc, vc, bt, cl, self.scale, max_len)
 
     def capture(self) -> None:
         """Capture every bucket, small first (model_runner.py:1169-1175): a

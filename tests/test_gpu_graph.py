@@ -57,7 +57,7 @@ def _eager_padded(kcs, vcs, q, k, v, slots, lens, tables, bucket, runner):
     for layer in range(L):
         store_kvcache(kp[layer], vp[layer], kcs[layer], vcs[layer], sb)
         outs.append(paged_decode_attention(qp[layer], kcs[layer], vcs[layer], tb, lb,
-                                           128 ** -0.5, PAGE))
+                                           128 ** -0.5, MAXB * PAGE))
     return torch.stack(outs)[:, :bs]
 
 
