@@ -11,7 +11,8 @@ torch CPU decode path (gather + GQA expand + masked SDPA) timed on a bounded
 sample of the same workload on this host (cpu_baseline).
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 10]
-    python bench.py --workload mixed|int8|decode-dist|append|swap   (extra lines)
+    python bench.py --workload mixed|int8|decode-dist|append|swap|copy|rope|
+                     decode-graph|offload-overlap|pd-wire      (extra lines)
 """
 from __future__ import annotations
 
@@ -39,7 +40,7 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="decode",
                     choices=["decode", "decode-dist", "int8", "mixed", "append", "swap", "copy",
-                             "rope", "decode-graph"])
+                             "rope", "decode-graph", "offload-overlap", "pd-wire"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample", type=int, default=64,
                     help="sequences of the workload the CPU baseline runs")
@@ -461,6 +462,205 @@ def run_decode_graph(args, torch):
     return out
 
 
+def run_offload_overlap(args, torch):
+    """A 48-layer decode step (batch 64 x context 4096: per layer append one
+    token per sequence, then paged decode, through bound Attention layers)
+    that also offloads E = 8 blocks of 24 MiB to pinned host slots and
+    revives the 8 offloaded one step earlier (the BlockManager's evict /
+    revive traffic): blocking moves on the compute stream vs the
+    AsyncOffloader (copy streams, per-layer-group fences), against the same
+    step without offload traffic."""
+    from nanovllm_amd.engine.kv_runner import KVCacheRunner
+    from nanovllm_amd.layers.attention import Attention
+    from nanovllm_amd.utils.context import reset_context, set_context
+    from nanovllm_amd.workloads import build_block_tables, slots_for_last_token
+    dev = torch.device("cuda:0")
+    L, H, KVH, BS, CTX, E = 48, 32, 4, 64, 4096, 8
+    nb = BS * CTX // 256
+    lens = [CTX] * BS
+    bt = build_block_tables(lens, nb, 256, torch.Generator().manual_seed(1))
+    slots = slots_for_last_token(bt, lens, 256).to(dev)
+    bt = bt.to(dev)
+    cl = torch.tensor(lens, dtype=torch.int32, device=dev)
+    g = torch.Generator(device=dev).manual_seed(2)
+    q = torch.randn(L, BS, H, 128, generator=g, device=dev, dtype=torch.bfloat16)
+    k = torch.randn(L, BS, KVH, 128, generator=g, device=dev, dtype=torch.bfloat16)
+    v = torch.randn(L, BS, KVH, 128, generator=g, device=dev, dtype=torch.bfloat16)
+    put_ids = list(range(nb, nb + E))
+    get_ids = list(range(nb + E, nb + 2 * E))
+    block_mib = 2 * L * 256 * KVH * 128 * 2 / 2 ** 20
+    out = {"workload": (f"48-layer decode step (bs {BS} x {CTX}) + offload of {E} and revival "
+                        f"of {E} blocks of {block_mib:.0f} MiB per step"),
+           "block_MiB": block_mib}
+    modes = (("no_offload", 0, None), ("blocking", 0, None), ("copies_only_blocking", 0, None),
+             ("async_dma_g4", 4, "dma"), ("async_kernel_g1", 1, "kernel"),
+             ("async_kernel_g8", 8, "kernel"))
+    for mode, groups, engine in modes:
+        r = KVCacheRunner(L, nb + 2 * E, 256, KVH, 128, kv_offload_host_blocks=3 * E,
+                          async_offload_groups=groups, async_copy_engine=engine or "kernel",
+                          device=dev)
+        r.kv_cache.normal_(generator=g)
+        mods = [Attention(H, 128, 128 ** -0.5, KVH) for _ in range(L)]
+        r.bind(mods)
+
+        fifo = []   # slots filled one step earlier: this step's revivals
+
+        def step():
+            revive, fresh = [], []
+            if mode != "no_offload":
+                fresh = r.offload_put_many(put_ids)
+                if fifo:
+                    revive = fifo.pop(0)
+                    r.offload_get_many(revive, get_ids)
+            if mode != "copies_only_blocking":
+                set_context(False, slot_mapping=slots, context_lens=cl, block_tables=bt,
+                            max_context_len=CTX)
+                for i, m in enumerate(mods):
+                    m.forward(q[i], k[i], v[i])
+                reset_context()
+            r.fence()
+            for s_ in revive:
+                r.offload_release(s_)
+            if fresh:
+                fifo.append(fresh)
+
+        for _ in range(3):
+            step()
+        torch.cuda.synchronize()
+        n = max(5, args.steps // 5)
+        t0 = time.perf_counter()
+        for _ in range(n):
+            step()
+        torch.cuda.synchronize()
+        out[f"{mode}_ms_per_step"] = round((time.perf_counter() - t0) * 1e3 / n, 3)
+        del r, mods
+        torch.cuda.empty_cache()
+    extra = out["blocking_ms_per_step"] - out["no_offload_ms_per_step"]
+    out["offload_cost_blocking_ms"] = round(extra, 3)
+    for gname, _, engine in modes:
+        if engine is None:
+            continue
+        out[f"offload_cost_{gname}_ms"] = round(
+            out[f"{gname}_ms_per_step"] - out["no_offload_ms_per_step"], 3)
+    return out
+
+
+def run_pd_wire(args, torch):
+    """PD KV transfer of one request's 16 blocks (48 layers x 256 tokens x 4 kv
+    heads x 128 bf16: 12 MiB per side per block, 384 MiB per frame) from one
+    pool to another through a socketpair, sender in a thread:
+    * channel: TcpKVChannel (gather kernels into pinned staging, sent and
+      received without host copies, chunked so the link and the GPU overlap);
+    * torch_ops: the same frame moved with the engine's own composition
+      (index_select + permute + pinned copy_ + tobytes + sendall; recv +
+      frombuffer + copy + index_copy_, nanovllm/pd/kv_channel.py:54-178).
+    Plus extract_kv / import_kv alone (device <-> pinned, the PCIe legs)."""
+    import socket
+    import struct
+    import threading
+
+    from nanovllm_amd.pd.kv_channel import (KVBlockBuffer, TcpKVChannel, extract_kv,
+                                            import_kv)
+    dev = torch.device("cuda:0")
+    L, KVH, NB, N = 48, 4, 40, 16
+    g = torch.Generator(device=dev).manual_seed(4)
+    src = torch.randn(2, L, NB, 256, KVH, 128, generator=g, device=dev, dtype=torch.bfloat16)
+    dst = torch.zeros_like(src)
+    t_src = list(range(0, 2 * N, 2))
+    t_dst = list(range(NB - 1, NB - 1 - N, -1))
+    frame_bytes = 2 * N * L * 256 * KVH * 128 * 2
+    reps = max(3, args.steps // 10)
+
+    def torch_ops_send(sock, buf):
+        idx = torch.tensor(t_src, device=dev, dtype=torch.long)
+        buf.k[:N].copy_(src[0].index_select(1, idx).permute(1, 0, 2, 3, 4))
+        buf.v[:N].copy_(src[1].index_select(1, idx).permute(1, 0, 2, 3, 4))
+        torch.cuda.synchronize()
+        kb = buf.k[:N].contiguous().view(torch.int16).numpy().tobytes()
+        vb = buf.v[:N].contiguous().view(torch.int16).numpy().tobytes()
+        sock.sendall(struct.pack("<III", N, len(kb), len(vb)))
+        sock.sendall(kb)
+        sock.sendall(vb)
+
+    def torch_ops_recv(sock, buf):
+        def exact(n):
+            parts = []
+            while n:
+                c = sock.recv(min(n, 1 << 22))
+                parts.append(c)
+                n -= len(c)
+            return b"".join(parts)
+        n, kl, vl = struct.unpack("<III", exact(12))
+        kd, vd = exact(kl), exact(vl)
+        shape = (n,) + tuple(buf.k.shape[1:])
+        buf.k[:n] = torch.frombuffer(bytearray(kd), dtype=torch.int16).view(torch.bfloat16).reshape(shape)
+        buf.v[:n] = torch.frombuffer(bytearray(vd), dtype=torch.int16).view(torch.bfloat16).reshape(shape)
+        idx = torch.tensor(t_dst, device=dev, dtype=torch.long)
+        dst[0].index_copy_(1, idx, buf.k[:n].to(dev).permute(1, 0, 2, 3, 4).contiguous())
+        dst[1].index_copy_(1, idx, buf.v[:n].to(dev).permute(1, 0, 2, 3, 4).contiguous())
+        torch.cuda.synchronize()
+
+    def timed(send, recv):
+        a, b = socket.socketpair()
+        for sk in (a, b):
+            sk.setsockopt(socket.SOL_SOCKET, socket.SO_SNDBUF, 4 << 20)
+            sk.setsockopt(socket.SOL_SOCKET, socket.SO_RCVBUF, 4 << 20)
+        times = []
+        try:
+            for _ in range(reps + 1):
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                th = threading.Thread(target=send, args=(a,))
+                th.start()
+                recv(b)
+                th.join()
+                times.append(time.perf_counter() - t0)
+        finally:
+            a.close()
+            b.close()
+        return statistics.median(times[1:])
+
+    out = {"workload": f"PD transfer of {N} blocks (48 layers, 24 MiB each) over a socketpair",
+           "frame_MiB": frame_bytes / 2 ** 20}
+    tx_buf = KVBlockBuffer.from_pool(src, N)
+    rx_buf = KVBlockBuffer.from_pool(dst, N)
+    t = timed(lambda sk: torch_ops_send(sk, tx_buf), lambda sk: torch_ops_recv(sk, rx_buf))
+    out["torch_ops_ms"] = round(t * 1e3, 2)
+    out["torch_ops_GBps"] = round(frame_bytes / t / 1e9, 2)
+    torch_ops_dst = dst.clone()
+    dst.zero_()
+    for chunk in (2, 4):
+        holder = {}
+
+        def send(sk, chunk=chunk):
+            if "tx" not in holder or holder["tx"].sock is not sk:
+                holder["tx"] = TcpKVChannel(sk, src, N, chunk_blocks=chunk)
+            holder["tx"].send_blocks(t_src)
+
+        def recv(sk, chunk=chunk):
+            if "rx" not in holder or holder["rx"].sock is not sk:
+                holder["rx"] = TcpKVChannel(sk, dst, N, chunk_blocks=chunk)
+            holder["rx"].recv_blocks(t_dst)
+        t = timed(send, recv)
+        out[f"channel_chunk{chunk}_ms"] = round(t * 1e3, 2)
+        out[f"channel_chunk{chunk}_GBps"] = round(frame_bytes / t / 1e9, 2)
+    out["channel_equals_torch_ops"] = bool(torch.equal(dst.view(torch.int16),
+                                                       torch_ops_dst.view(torch.int16)))
+    buf = KVBlockBuffer.from_pool(src, N)
+    for name, fn in (("extract", lambda: extract_kv(src, t_src, buf)),
+                     ("import", lambda: import_kv(dst, t_dst, buf))):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+        t = (time.perf_counter() - t0) / reps
+        out[f"{name}_ms"] = round(t * 1e3, 2)
+        out[f"{name}_GBps"] = round(frame_bytes / t / 1e9, 2)
+    return out
+
+
 def run_swap(args, torch):
     """Block eviction / offload step at the config-5 shape: a pool of 8192
     blocks of [2 (K, V), 48 layers, 256, 4 kv heads, 128] bf16 (24 MiB each,
@@ -574,6 +774,10 @@ def main():
         res = run_rope(args, torch)
     elif args.workload == "decode-graph":
         res = run_decode_graph(args, torch)
+    elif args.workload == "offload-overlap":
+        res = run_offload_overlap(args, torch)
+    elif args.workload == "pd-wire":
+        res = run_pd_wire(args, torch)
     else:
         res = run_swap(args, torch)
     print(json.dumps(res), flush=True)

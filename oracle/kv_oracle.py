@@ -351,3 +351,43 @@ def qk_norm_rope_ref(q: torch.Tensor, k: torch.Tensor, positions: torch.Tensor,
     cos_sin = cos_sin_cache[positions.long()].unsqueeze(1)
     cos, sin = cos_sin.chunk(2, dim=-1)
     return apply_rotary_ref(q, cos, sin), apply_rotary_ref(k, cos, sin)
+
+
+# ---------------------------------------------------------------------------
+# PD wire format (nanovllm/pd/kv_channel.py:110-220)
+# ---------------------------------------------------------------------------
+
+
+def kv_frame_ref(kv_pool: np.ndarray, block_table) -> bytes:
+    """The frame TcpKVChannel.send_blocks (kv_channel.py:137-154) writes for
+    `block_table` of a pool [2, L, blocks, page, kvh, d] (any element type,
+    little endian): header (n, k_bytes, v_bytes) as three u32 LE, then for
+    each side every named block's [L, page, kvh, d] slab in table order —
+    extract_kv's buf.k[:n] / buf.v[:n] (kv_channel.py:54-69) taken as bytes
+    (_tensor_to_bytes, :110-112)."""
+    ids = [int(b) for b in block_table]
+    sides = []
+    for side in (0, 1):
+        slabs = [np.ascontiguousarray(kv_pool[side, :, b]).tobytes() for b in ids]
+        sides.append(b"".join(slabs))
+    n, k, v = len(ids), sides[0], sides[1]
+    header = (n.to_bytes(4, "little") + len(k).to_bytes(4, "little")
+              + len(v).to_bytes(4, "little"))
+    return header + k + v
+
+
+def split_frames_ref(stream: bytes) -> tuple[list, bytes]:
+    """Cut a byte stream into complete frames (n, k_bytes, v_bytes), the
+    reassembly rule of KVFrameAssembler (kv_channel.py:181-220); returns the
+    frames and the unconsumed tail."""
+    frames, pos = [], 0
+    while len(stream) - pos >= 12:
+        n = int.from_bytes(stream[pos:pos + 4], "little")
+        kl = int.from_bytes(stream[pos + 4:pos + 8], "little")
+        vl = int.from_bytes(stream[pos + 8:pos + 12], "little")
+        if len(stream) - pos - 12 < kl + vl:
+            break
+        body = pos + 12
+        frames.append((n, stream[body:body + kl], stream[body + kl:body + kl + vl]))
+        pos = body + kl + vl
+    return frames, stream[pos:]

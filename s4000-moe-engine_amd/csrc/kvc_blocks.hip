@@ -2,10 +2,17 @@
 //
 // A block of the engine's pool [2, L, blocks, page, KVH, D] is `planes`
 // (= 2L) rows of block_bytes, one per (K|V, layer), plane_stride apart.
-// Kernels copy 16-byte vectors, four in flight per thread, one workgroup per
-// 16 KiB piece of one (item, plane) row; the block id is resolved once per
-// workgroup.  The DMA entry points issue one strided 2-D copy per block on the
-// copy engines instead (PCIe-bound moves need no shader time).
+// Kernels copy 16-byte vectors, four in flight per thread, one 16 KiB piece
+// of one (item, plane) row per workgroup iteration; the block id is resolved
+// once per piece.  An in-HBM move launches a workgroup per piece.  A move to
+// or from pinned host memory is PCIe-bound: a few workgroups saturate the
+// link, so it launches at most KVC_HOST_MOVE_WGS (default 64) workgroups that
+// stride over the pieces, and leaves the other CUs to whatever kernels run
+// beside it.  The DMA entry points issue one strided 2-D copy per block on
+// the copy engines instead.
+#include <algorithm>
+#include <cstdlib>
+
 #include "kvc_internal.h"
 
 namespace kvc {
@@ -29,45 +36,58 @@ struct MoveArgs {
   int64_t dst_plane, dst_item;
 };
 
-__global__ void __launch_bounds__(kThreads) move_blocks_kernel(MoveArgs a) {
-  const int64_t w = blockIdx.x;
-  const int64_t row = w / a.pieces;
-  const int64_t piece = w - row * a.pieces;
-  const int64_t item = row / a.planes;
-  const int64_t plane = row - item * a.planes;
-  const int64_t s_sel = a.src_ids ? int64_t(a.src_ids[item]) : item;
-  const int64_t d_sel = a.dst_ids ? int64_t(a.dst_ids[item]) : item;
-  const char* s = a.src + plane * a.src_plane + s_sel * a.src_item + piece * kPiece;
-  char* d = a.dst + plane * a.dst_plane + d_sel * a.dst_item + piece * kPiece;
-  const int64_t limit = a.block_bytes - piece * kPiece;
-  u32x4_t v[kUnroll];
+__global__ void __launch_bounds__(kThreads) move_blocks_kernel(MoveArgs a, int64_t total) {
+  for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
+    const int64_t row = w / a.pieces;
+    const int64_t piece = w - row * a.pieces;
+    const int64_t item = row / a.planes;
+    const int64_t plane = row - item * a.planes;
+    const int64_t s_sel = a.src_ids ? int64_t(a.src_ids[item]) : item;
+    const int64_t d_sel = a.dst_ids ? int64_t(a.dst_ids[item]) : item;
+    const char* s = a.src + plane * a.src_plane + s_sel * a.src_item + piece * kPiece;
+    char* d = a.dst + plane * a.dst_plane + d_sel * a.dst_item + piece * kPiece;
+    const int64_t limit = a.block_bytes - piece * kPiece;
+    u32x4_t v[kUnroll];
 #pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
-    const int64_t off = (int64_t(u) * kThreads + threadIdx.x) * 16;
-    if (off < limit) v[u] = *reinterpret_cast<const u32x4_t*>(s + off);
-  }
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t off = (int64_t(u) * kThreads + threadIdx.x) * 16;
+      if (off < limit) v[u] = *reinterpret_cast<const u32x4_t*>(s + off);
+    }
 #pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
-    const int64_t off = (int64_t(u) * kThreads + threadIdx.x) * 16;
-    if (off < limit) *reinterpret_cast<u32x4_t*>(d + off) = v[u];
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t off = (int64_t(u) * kThreads + threadIdx.x) * 16;
+      if (off < limit) *reinterpret_cast<u32x4_t*>(d + off) = v[u];
+    }
   }
 }
 
-int launch_move(const MoveArgs& a, int64_t n, hipStream_t st, const char* what) {
+int64_t host_move_workgroups() {
+  static const int64_t wgs = [] {
+    const char* e = std::getenv("KVC_HOST_MOVE_WGS");
+    const long v = e ? std::strtol(e, nullptr, 10) : 0;
+    return int64_t(v > 0 ? v : 64);
+  }();
+  return wgs;
+}
+
+int launch_move(const MoveArgs& a, int64_t n, hipStream_t st, const char* what,
+                bool host_side = false) {
   if (n == 0 || a.planes == 0 || a.block_bytes == 0) return KVC_OK;
-  const int64_t grid = n * a.planes * a.pieces;
+  const int64_t total = n * a.planes * a.pieces;
+  const int64_t grid = host_side ? std::min(total, host_move_workgroups()) : total;
   KVC_REQUIRE(grid < (int64_t(1) << 31), KVC_ERR_VALUE, "%s: %lld workgroups exceed one launch",
               what, (long long)grid);
-  move_blocks_kernel<<<unsigned(grid), kThreads, 0, st>>>(a);
+  move_blocks_kernel<<<unsigned(grid), kThreads, 0, st>>>(a, total);
   return check_launch(what);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // Address a kernel may dereference for `p`: device memory as is, pinned host
-// memory through its device mapping.  Pageable (unregistered) host memory is
-// rejected rather than handed to a kernel.
-int device_view(const void* p, const void** out, const char* what) {
+// memory through its device mapping (*is_host set).  Pageable (unregistered)
+// host memory is rejected rather than handed to a kernel.
+int device_view(const void* p, const void** out, const char* what, bool* is_host) {
+  *is_host = false;
   hipPointerAttribute_t attr;
   hipError_t e = hipPointerGetAttributes(&attr, p);
   if (e != hipSuccess) {
@@ -84,6 +104,7 @@ int device_view(const void* p, const void** out, const char* what) {
                 "%s: pinned buffer %p has no device mapping", what, p);
     *out = static_cast<const char*>(attr.devicePointer) +
            (static_cast<const char*>(p) - static_cast<const char*>(attr.hostPointer));
+    *is_host = true;
     return KVC_OK;
   }
   *out = p;
@@ -119,7 +140,8 @@ extern "C" int kvc_block_gather(const void* src, int64_t planes, int64_t src_pla
   if (rc != KVC_OK) return rc;
   if (n == 0) return KVC_OK;
   const void* dview = nullptr;
-  rc = device_view(dst, &dview, "block_gather");
+  bool host_side = false;
+  rc = device_view(dst, &dview, "block_gather", &host_side);
   if (rc != KVC_OK) return rc;
   MoveArgs a{};
   a.src = static_cast<const char*>(src);
@@ -133,7 +155,7 @@ extern "C" int kvc_block_gather(const void* src, int64_t planes, int64_t src_pla
   a.dst_ids = nullptr;
   a.dst_plane = dst_plane_stride;
   a.dst_item = dst_item_stride;
-  return launch_move(a, n, as_stream(stream), "block_gather");
+  return launch_move(a, n, as_stream(stream), "block_gather", host_side);
 }
 
 extern "C" int kvc_block_scatter(const void* src, int64_t src_item_stride,
@@ -147,7 +169,8 @@ extern "C" int kvc_block_scatter(const void* src, int64_t src_item_stride,
   if (rc != KVC_OK) return rc;
   if (n == 0) return KVC_OK;
   const void* sview = nullptr;
-  rc = device_view(src, &sview, "block_scatter");
+  bool host_side = false;
+  rc = device_view(src, &sview, "block_scatter", &host_side);
   if (rc != KVC_OK) return rc;
   MoveArgs a{};
   a.src = static_cast<const char*>(sview);
@@ -161,7 +184,7 @@ extern "C" int kvc_block_scatter(const void* src, int64_t src_item_stride,
   a.dst_ids = block_ids;
   a.dst_plane = dst_plane_stride;
   a.dst_item = block_bytes;
-  return launch_move(a, n, as_stream(stream), "block_scatter");
+  return launch_move(a, n, as_stream(stream), "block_scatter", host_side);
 }
 
 extern "C" int kvc_block_copy(void* pool, int64_t planes, int64_t plane_stride,

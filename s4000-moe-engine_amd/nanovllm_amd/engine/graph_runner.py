@@ -9,7 +9,9 @@ Follows the engine's decode graph protocol (nanovllm/engine/model_runner.py:
   context_lens = 1, block-table rows = the scratch block id.  They write and
   read only that block, never a live one;
 * graph inputs are static buffers refreshed before each replay; the padding
-  fills and copies run eagerly, outside the graph.
+  fills and copies run eagerly, outside the graph.  Padded q/k/v rows are
+  zeros, so the padded rows' appends (all to the one scratch slot) store the
+  same bytes whichever lands last.
 
 What is captured is the path's part of a decode step, per layer:
 store_kvcache(k, v, k_cache, v_cache, slot_mapping) then
@@ -118,6 +120,12 @@ class DecodeGraphRunner:
         self.q[:, :bs] = q
         self.k[:, :bs] = k
         self.v[:, :bs] = v
+        # Padded rows all append to the one scratch slot; zeroing them makes
+        # every such write the same bytes, so the scratch block's contents do
+        # not depend on which row lands last.
+        self.q[:, bs:b].zero_()
+        self.k[:, bs:b].zero_()
+        self.v[:, bs:b].zero_()
         pad_decode_inputs(slot_mapping, context_lens, block_tables, self.slot_mapping[:b],
                           self.context_lens[:b], self.block_tables[:b], self.scratch_slot,
                           self.scratch_block_id)

@@ -83,6 +83,29 @@ class HostBlockPool:
         self._free.append(slot)
         self.releases += 1
 
+    # -- slot reservation for callers that move the bytes themselves ---------
+    def reserve(self, keys) -> list[int]:
+        """A slot for each key, in order (-1 once the pool is full), counted
+        as puts; the caller fills the slots."""
+        slots = []
+        for key in keys:
+            slot = self._take_slot()
+            if slot != -1:
+                self._in_use[slot] = key
+                self.puts += 1
+            slots.append(slot)
+        return slots
+
+    def check_in_use(self, slots) -> None:
+        for s in slots:
+            if s not in self._in_use:
+                raise KeyError(f"slot {s} is not in use")
+
+    @property
+    def buffer(self) -> torch.Tensor | None:
+        """The pinned slots [num_slots, *block_shape] (None when disabled)."""
+        return self._buf
+
     # -- pool-direct moves (copy engines) ------------------------------------
     def _check_mover(self, mover) -> None:
         if mover.item_shape != self.block_shape or mover.pool.dtype != self.dtype:

@@ -191,7 +191,8 @@ class KVCacheRunner:
 
     def __init__(self, num_layers: int, num_blocks: int, block_size: int, num_kv_heads: int,
                  head_dim: int, dtype=torch.bfloat16, device="cuda", kv_int8: str | None = None,
-                 kv_offload_host_blocks: int = 0, n_out_max: int = 8):
+                 kv_offload_host_blocks: int = 0, n_out_max: int = 8,
+                 async_offload_groups: int = 0, async_copy_engine: str = "kernel"):
         self.block_size = block_size
         self.num_layers = num_layers
         self.num_kvcache_blocks = num_blocks
@@ -220,6 +221,13 @@ class KVCacheRunner:
         self.mover = BlockMover(self.kv_cache)
         self.kv_offload_host_blocks = kv_offload_host_blocks
         self.kv_offloader = None
+        # async_offload_groups > 0: offload moves run on copy streams
+        # (AsyncOffloader, 8 groups recommended), fenced per layer group by the
+        # bound attention layers.
+        self.async_offload = async_offload_groups > 0
+        self.async_offload_groups = async_offload_groups
+        self.async_copy_engine = async_copy_engine
+        self.kv_async = None
 
     def bind(self, modules) -> int:
         """Hand per-layer views to every module that has k_cache/v_cache
@@ -243,6 +251,8 @@ class KVCacheRunner:
                 m.out_idx2d = self.kv_out_idx2d[layer]
                 m.head_n_out = self.kv_head_n_out[layer]
             m.kv_cache_is_int8 = self.kv_int8 is not None
+            m.kv_layer = layer
+            m.kv_fence = self._fence_layer if self.async_offload else None
             layer += 1
         return layer
 
@@ -256,16 +266,35 @@ class KVCacheRunner:
             self.kv_offloader = HostBlockPool(self.kv_offload_host_blocks,
                                               tuple(self.kv_cache[:, :, 0].shape),
                                               dtype=self.kv_cache.dtype)
+            if self.async_offload and self.kv_offloader.buffer is not None:
+                from .offload_pipeline import AsyncOffloader
+                self.kv_async = AsyncOffloader(self.kv_cache, self.kv_offloader,
+                                               self.async_offload_groups, self.async_copy_engine)
         return self.kv_offloader
+
+    def _fence_layer(self, layer: int) -> None:
+        if self.kv_async is not None:
+            self.kv_async.fence_layer(layer)
+
+    def fence(self) -> None:
+        """Order the compute stream after every offload copy issued so far
+        (needed before pool writes outside the attention layers)."""
+        if self.kv_async is not None:
+            self.kv_async.fence()
 
     def offload_put(self, block_id: int) -> int:
         pool = self._ensure_offloader()
         if not pool.has_room():
             return pool.note_full()
+        if self.kv_async is not None:
+            return self.kv_async.put(block_id)
         return pool.put_from_pool(self.mover, block_id)
 
     def offload_get(self, slot: int, block_id: int) -> None:
-        self._ensure_offloader().get_into_pool(self.mover, slot, block_id)
+        pool = self._ensure_offloader()
+        if self.kv_async is not None:
+            return self.kv_async.get(slot, block_id)
+        pool.get_into_pool(self.mover, slot, block_id)
 
     def offload_release(self, slot: int) -> None:
         self._ensure_offloader().release(slot)
@@ -273,12 +302,18 @@ class KVCacheRunner:
     # -- batched forms ---------------------------------------------------
     def offload_put_many(self, block_ids) -> list[int]:
         pool = self._ensure_offloader()
+        if self.kv_async is not None:
+            return self.kv_async.put_many(block_ids)
         return pool.put_many_from_pool(self.mover, block_ids)
 
     def offload_get_many(self, slots, block_ids) -> None:
-        self._ensure_offloader().get_many_into_pool(self.mover, slots, block_ids)
+        pool = self._ensure_offloader()
+        if self.kv_async is not None:
+            return self.kv_async.get_many(slots, block_ids)
+        pool.get_many_into_pool(self.mover, slots, block_ids)
 
     def compact(self, src_ids, dst_ids) -> None:
+        self.fence()
         self.mover.copy(src_ids, dst_ids)
 
     # -- batch preparation (the Context producer) ----------------------------

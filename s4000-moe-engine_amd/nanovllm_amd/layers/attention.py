@@ -80,6 +80,10 @@ class Attention(nn.Module):
         self.attention_backend = "triton_paged"
         self.profiler = None
         self.layer_id = -1
+        # Set by a runner whose block moves run asynchronously: called with
+        # kv_layer before this layer first touches its pool planes in a step.
+        self.kv_fence = None
+        self.kv_layer = -1
 
     def _profile(self, name):
         if self.profiler is None:
@@ -108,6 +112,8 @@ class Attention(nn.Module):
         [N, H, D]; k, v [N, KVH*D] or [N, KVH, D] (views of the qkv
         projection are fine)."""
         context = get_context()
+        if self.kv_fence is not None:
+            self.kv_fence(self.kv_layer)
         N = positions.numel()
         q3 = q.view(N, self.num_heads, self.head_dim)
         k3 = k.view(N, self.num_kv_heads, self.head_dim)
@@ -128,6 +134,8 @@ class Attention(nn.Module):
         """attention.py:130-177.  kv_stored: the step's k/v rows are already
         in the pool (appended by forward_fused), so the store is skipped."""
         context = get_context()
+        if self.kv_fence is not None and not kv_stored:
+            self.kv_fence(self.kv_layer)
         k_cache, v_cache = self.k_cache, self.v_cache
         if k_cache.numel() and self.block_size is None:
             self.block_size = k_cache.size(1)

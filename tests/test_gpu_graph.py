@@ -49,10 +49,10 @@ def _eager_padded(kcs, vcs, q, k, v, slots, lens, tables, bucket, runner):
     lb = torch.empty(bucket, dtype=torch.int32, device=DEV)
     tb = torch.empty(bucket, MAXB, dtype=torch.int32, device=DEV)
     pad_decode_inputs(slots, lens, tables, sb, lb, tb, runner.scratch_slot, runner.scratch_block_id)
-    qp = runner.q[:, :bucket].clone()
-    kp = runner.k[:, :bucket].clone()
-    vp = runner.v[:, :bucket].clone()
-    qp[:, :bs], kp[:, :bs], vp[:, :bs] = q, k, v
+    qp = torch.zeros_like(runner.q[:, :bucket])
+    kp = torch.zeros_like(runner.k[:, :bucket])
+    vp = torch.zeros_like(runner.v[:, :bucket])
+    qp[:, :bs], kp[:, :bs], vp[:, :bs] = q, k, v  # padded rows are zeros
     outs = []
     for layer in range(L):
         store_kvcache(kp[layer], vp[layer], kcs[layer], vcs[layer], sb)
