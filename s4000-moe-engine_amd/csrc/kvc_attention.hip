@@ -2482,39 +2482,50 @@ __device__ __forceinline__ void pf_attend(PfState& st, const u32x4_t (&k)[2][4],
                                           const QOps<kBF16, kPreNCB>& Q,
                                           const int (&klim)[kPreNCB], int key0, int valid_end,
                                           float scale_log2, const LaneId& L) {
+  static_assert(kPreNCB == 2, "the schedule below pairs two column blocks");
+  // S^T of column block 0, then of block 1 (block 0's max runs under block
+  // 1's MFMAs).
   f32x4_t sacc[kPreNCB][2];
 #pragma unroll
   for (int cb = 0; cb < kPreNCB; ++cb) {
     sacc[cb][0] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     sacc[cb][1] = sacc[cb][0];
-  }
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-#pragma unroll
-    for (int cb = 0; cb < kPreNCB; ++cb) {
+    for (int c = 0; c < 4; ++c) {
       sacc[cb][0] = mfma_bf16(k[0][c], Q.op[cb][c], sacc[cb][0]);
       sacc[cb][1] = mfma_bf16(k[1][c], Q.op[cb][c], sacc[cb][1]);
     }
   }
-  const u32x4_t ones = u32x4_t{kOnesBf16x2, kOnesBf16x2, kOnesBf16x2, kOnesBf16x2};
+  float x[kPreNCB][8];
+  float tmax[kPreNCB];
 #pragma unroll
   for (int cb = 0; cb < kPreNCB; ++cb) {
-    float x[8] = {sacc[cb][0][0], sacc[cb][0][1], sacc[cb][0][2], sacc[cb][0][3],
-                  sacc[cb][1][0], sacc[cb][1][1], sacc[cb][1][2], sacc[cb][1][3]};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[cb][i] = sacc[cb][0][i];
+      x[cb][4 + i] = sacc[cb][1][i];
+    }
     if constexpr (kMasked) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int key = key0 + key_of_slot(L.lg, i);
-        x[i] = (key < valid_end && key <= klim[cb]) ? x[i] : -INFINITY;
+        x[cb][i] = (key < valid_end && key <= klim[cb]) ? x[cb][i] : -INFINITY;
       }
     }
-    float tmax = fmaxf(fmaxf(x[0], x[1]), x[2]);
-    tmax = fmaxf(fmaxf(tmax, x[3]), x[4]);
-    tmax = fmaxf(fmaxf(tmax, x[5]), x[6]);
-    tmax = fmaxf(tmax, x[7]);
-    tmax = rows4_max(tmax) * scale_log2;
-    if (__builtin_expect(__ballot(tmax > st.m[cb] + kRescaleLog2) != 0, 0)) {
-      const float m_new = fmaxf(st.m[cb], tmax);
+    float t = fmaxf(fmaxf(x[cb][0], x[cb][1]), x[cb][2]);
+    t = fmaxf(fmaxf(t, x[cb][3]), x[cb][4]);
+    t = fmaxf(fmaxf(t, x[cb][5]), x[cb][6]);
+    t = fmaxf(t, x[cb][7]);
+    tmax[cb] = rows4_max(t) * scale_log2;
+  }
+  // One rare branch for both blocks: rescale whichever moved its max by more
+  // than the threshold.
+  if (__builtin_expect(__ballot(tmax[0] > st.m[0] + kRescaleLog2 ||
+                                tmax[1] > st.m[1] + kRescaleLog2) != 0, 0)) {
+#pragma unroll
+    for (int cb = 0; cb < kPreNCB; ++cb) {
+      if (__ballot(tmax[cb] > st.m[cb] + kRescaleLog2) == 0) continue;
+      const float m_new = fmaxf(st.m[cb], tmax[cb]);
       const float m_ref = (m_new == -INFINITY) ? 0.f : m_new;
       const float alpha = __builtin_amdgcn_exp2f(st.m[cb] - m_ref);
       st.m[cb] = m_new;
@@ -2526,16 +2537,24 @@ __device__ __forceinline__ void pf_attend(PfState& st, const u32x4_t (&k)[2][4],
 #pragma unroll
       for (int r = 0; r < 4; ++r) st.l[cb][r] *= alpha;
     }
+  }
+  const u32x4_t ones = u32x4_t{kOnesBf16x2, kOnesBf16x2, kOnesBf16x2, kOnesBf16x2};
+  u32x4_t pb[kPreNCB];
+#pragma unroll
+  for (int cb = 0; cb < kPreNCB; ++cb) {
     const float neg_m = (st.m[cb] == -INFINITY) ? 0.f : -st.m[cb];
     float pr[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) pr[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[i], scale_log2, neg_m));
-    u32x4_t pb;
+    for (int i = 0; i < 8; ++i)
+      pr[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[cb][i], scale_log2, neg_m));
 #pragma unroll
-    for (int w = 0; w < 4; ++w) pb[w] = pack_bf16x2_fast(pr[2 * w], pr[2 * w + 1]);
+    for (int w = 0; w < 4; ++w) pb[cb][w] = pack_bf16x2_fast(pr[2 * w], pr[2 * w + 1]);
+  }
 #pragma unroll
-    for (int jj = 0; jj < 8; ++jj) st.o[cb][jj] = mfma_bf16(va[jj], pb, st.o[cb][jj]);
-    st.l[cb] = mfma_bf16(ones, pb, st.l[cb]);
+  for (int cb = 0; cb < kPreNCB; ++cb) {
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) st.o[cb][jj] = mfma_bf16(va[jj], pb[cb], st.o[cb][jj]);
+    st.l[cb] = mfma_bf16(ones, pb[cb], st.l[cb]);
   }
 }
 
