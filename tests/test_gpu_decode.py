@@ -149,3 +149,12 @@ def test_shape_errors_match_reference():
     kc2 = torch.zeros(4, 256, 2, 128, dtype=torch.bfloat16, device=DEV)
     with pytest.raises(ValueError):
         paged_decode_attention(q2, kc2, kc2, bt, lens, 1.0, 1)
+
+
+@pytest.mark.parametrize("page", [32, 64, 128])
+def test_pages_smaller_than_256(page):
+    lens = [1, page - 1, page, page + 1, 5 * page + 3, 4000]
+    blocks = sum((n + page - 1) // page for n in lens) + 4
+    wl = decode_workload(len(lens), 32, 4, blocks, lens, seed=page, device=DEV, page=page)
+    _check(wl.q, wl.k_cache, wl.v_cache, wl.block_tables, wl.context_lens, wl.scale,
+           f"page-{page}")

@@ -31,14 +31,14 @@ def partition(request, monkeypatch):
     return request.param
 
 
-def _mixed_case(H, KVH, dec_lens, chunks, seed, kv="bf16"):
+def _mixed_case(H, KVH, dec_lens, chunks, seed, kv="bf16", page=256):
     """chunks: list of (prefix, chunk_len).  Returns inputs on the device."""
     g = torch.Generator().manual_seed(seed)
     pre_total = [p + c for p, c in chunks]
     all_lens = list(dec_lens) + pre_total
-    blocks = sum(max(1, (n + 255) // 256) for n in all_lens) + 3
-    bt = build_block_tables(all_lens, blocks, 256, g)
-    shape = (blocks, 256, KVH, 128)
+    blocks = sum(max(1, (n + page - 1) // page) for n in all_lens) + 3
+    bt = build_block_tables(all_lens, blocks, page, g)
+    shape = (blocks, page, KVH, 128)
     k_cache = torch.randn(shape, generator=g).to(torch.bfloat16)
     v_cache = torch.randn(shape, generator=g).to(torch.bfloat16)
     T = len(dec_lens) + sum(c for _, c in chunks)
@@ -261,3 +261,12 @@ def test_attention_forward_mixed_matches_decode_and_prefill_paths():
     ref = ko.mixed_ref(bits(q), ko.bf16_to_f32(bits(kc)), ko.bf16_to_f32(bits(vc)), btn,
                        len(dec_lens), np.asarray(dec_lens), cu_q, cu_k, D ** -0.5)
     assert_attention_close(out, ref, "forward-mixed")
+
+
+@pytest.mark.parametrize("page", [32, 64, 128])
+def test_pages_smaller_than_256(page, partition):
+    # The reference insists on 256-token pages; the kernels take any multiple
+    # of 32 (a 32-key tile never straddles a page).
+    c = _mixed_case(32, 4, [1, page - 1, page, page + 1, 700],
+                    [(0, 40), (page + 3, 33), (5 * page, 64)], seed=page, page=page)
+    _check_mixed(c, f"page-{page}")
