@@ -50,6 +50,12 @@ from .kv_offload import HostBlockPool
 
 
 class AsyncOffloader:
+    """Offload executor over one KV pool [2, L, blocks, page, KVH, D] and a
+    HostBlockPool of matching slots: put/put_many/get/get_many/release with
+    the HostBlockPool's accounting (-1 past its room, KeyError on a slot not
+    in use), returning before the bytes move; fence_layer/fence order the
+    compute stream after them, wait_host the host.  layer_groups: how many
+    contiguous layer ranges get an event of their own (8 measured best)."""
 
     def __init__(self, kv_cache: torch.Tensor, host_pool: HostBlockPool, layer_groups: int = 8,
                  copy_engine: str = "kernel"):
@@ -79,6 +85,7 @@ class AsyncOffloader:
         self._pending: list[list[torch.cuda.Event]] = [[] for _ in self.groups]
         self._slot_put_done: dict[int, torch.cuda.Event] = {}
         self._gets_done: torch.cuda.Event | None = None
+        # the compute stream is whatever stream is current at each call
         self._cur = lambda: torch.cuda.current_stream(kv_cache.device)
 
     # -- byte moves --------------------------------------------------------
