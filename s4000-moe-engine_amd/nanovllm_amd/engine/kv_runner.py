@@ -193,6 +193,12 @@ class KVCacheRunner:
                  head_dim: int, dtype=torch.bfloat16, device="cuda", kv_int8: str | None = None,
                  kv_offload_host_blocks: int = 0, n_out_max: int = 8,
                  async_offload_groups: int = 0, async_copy_engine: str = "kernel"):
+        if kv_offload_host_blocks:
+            # nanovllm/config.py:75-78: a block's int8 codes would travel
+            # without their scales and side pool
+            assert kv_int8 is None, (
+                "KV offload requires the bf16 KV cache (int8 carries side-channel scales)")
+            assert kv_offload_host_blocks >= 0
         self.block_size = block_size
         self.num_layers = num_layers
         self.num_kvcache_blocks = num_blocks

@@ -79,3 +79,12 @@ def test_block_tables_are_disjoint_permutations():
     used = bt[bt >= 0].tolist()
     assert len(used) == len(set(used)) == 2 + 1 + 3
     assert (bt[1, 1:] == -1).all()
+
+
+def test_runner_refuses_offload_with_an_int8_pool():
+    # nanovllm/config.py:75-78: offload moves kv_cache blocks only, so an int8
+    # pool's scales / side pool would not follow; refused before any allocation.
+    from nanovllm_amd.engine.kv_runner import KVCacheRunner
+    for mode in ("tokhead", "chan"):
+        with pytest.raises(AssertionError, match="bf16"):
+            KVCacheRunner(2, 4, 256, 4, 128, kv_int8=mode, kv_offload_host_blocks=2)
