@@ -148,3 +148,32 @@ def test_local_channel_round_trip():
     expect[:, :, [0, 2, 3]] = before[:, :, [8, 1, 5]]
     assert np.array_equal(_u16(pool), expect)
     assert chan.bytes_moved == 2 * buf.nbytes
+
+
+def test_int8_pool_frame_and_round_trip():
+    # An int8 code pool travels the same way (the reference's int16 byte view
+    # of the staging rows, kv_channel.py:110-112, is just its bytes).
+    g = torch.Generator().manual_seed(51)
+    src = torch.randint(-127, 128, (2, L, 9, PAGE, KVH, 128), generator=g,
+                        dtype=torch.int8).to(DEV)
+    dst = torch.zeros_like(src)
+    table, target = [8, 3, 0], [1, 2, 7]
+    want = ko.kv_frame_ref(src.cpu().numpy(), table)
+    a, b = socket.socketpair()
+    tx = TcpKVChannel(a, src, max_blocks=4, chunk_blocks=2)
+    rx = TcpKVChannel(b, dst, max_blocks=4, chunk_blocks=2)
+    print("[wire] int8 pool", flush=True)
+    th, err = _send_in_thread(lambda: tx.send_blocks(table))
+    try:
+        got = _read_all(b, len(want))
+        th.join(60)
+        assert got == want
+        th, err2 = _send_in_thread(lambda: a.sendall(got))
+        rx.recv_blocks(target)
+        th.join(60)
+    finally:
+        a.close(), b.close()
+    assert not err and not err2
+    expect = torch.zeros_like(src).cpu()
+    expect[:, :, target] = src.cpu()[:, :, table]
+    assert torch.equal(dst.cpu(), expect)
