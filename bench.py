@@ -171,8 +171,7 @@ def cpu_decode_baseline(torch, wl, sample: int, reps: int = 5):
 # ---------------------------------------------------------------------------
 def run_decode(args, torch, dist: bool, int8: bool = False):
     from nanovllm_amd.kernels.kv_int8 import store_kvcache_int8_tokhead
-    from nanovllm_amd.kernels.paged_attention import paged_decode_attention
-    from nanovllm_amd.layers.attention import store_kvcache
+    from nanovllm_amd.kernels.paged_attention import paged_decode_append, paged_decode_attention
     from nanovllm_amd.workloads import decode_workload, uniform_lengths
 
     dev = torch.device("cuda:0")
@@ -189,31 +188,45 @@ def run_decode(args, torch, dist: bool, int8: bool = False):
         if int8:
             store_kvcache_int8_tokhead(wl.new_k, wl.new_v, wl.k_cache, wl.v_cache, wl.k_scale,
                                        wl.v_scale, wl.slot_mapping)
+            s = timer.start() if timer else None
+            out = paged_decode_attention(wl.q, wl.k_cache, wl.v_cache, wl.block_tables,
+                                         wl.context_lens, wl.scale, max(lens),
+                                         k_scale=wl.k_scale, v_scale=wl.v_scale)
         else:
-            store_kvcache(wl.new_k, wl.new_v, wl.k_cache, wl.v_cache, wl.slot_mapping)
-        s = timer.start() if timer else None
-        out = paged_decode_attention(wl.q, wl.k_cache, wl.v_cache, wl.block_tables,
-                                     wl.context_lens, wl.scale, max(lens),
-                                     k_scale=wl.k_scale, v_scale=wl.v_scale)
+            # the engine's decode step (store_kvcache + paged decode) in one call:
+            # the append rides in the decode launch
+            s = timer.start() if timer else None
+            out = paged_decode_append(wl.q, wl.new_k, wl.new_v, wl.k_cache, wl.v_cache,
+                                      wl.slot_mapping, wl.block_tables, wl.context_lens,
+                                      wl.scale)
         if timer:
             timer.stop(s)
         return out
 
     for _ in range(args.warmup):
         step()
+    # Throughput: exactly K steps, nothing else in the stream (the per-call
+    # events below add command-processor work between the steps).
     torch.cuda.synchronize()
-    timer = EventTimer(torch)
     t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall / args.steps * 1e3
+    # Roofline: the decode call's own duration, from HIP events around it on
+    # its stream, in a second pass of K steps.
+    timer = EventTimer(torch)
     for _ in range(args.steps):
         step(timer)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
     kernel_ms = timer.mean_ms()
-    ms_per_step = wall / args.steps * 1e3
 
     tok_bytes = 2 * kvh * 128 * (1 if int8 else 2) + (2 * kvh * 4 if int8 else 0)
     kv_bytes = sum(lens) * tok_bytes
     other = 2 * batch * heads * 128 * 2 + wl.block_tables.numel() * 4 + batch * 4
+    if not int8:
+        other += 2 * 2 * batch * kvh * 128 * 2 + batch * 4  # the append: new rows in and out, slots
     algo = kv_bytes + other
     achieved = algo / (kernel_ms * 1e-3) / 1e9
     ctx_desc = "ctx U[512,4096]" if dist else f"ctx {lens[0]}"

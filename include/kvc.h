@@ -145,6 +145,33 @@ int kvc_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                      void* out, int64_t out_stride_b, int64_t out_stride_h,
                      void* workspace, size_t workspace_bytes, kvc_stream_t stream);
 
+/* The decode step's KV work on a bf16 pool: kvc_store_kv of one new token
+ * per row (key/value [batch, num_kv_heads, head_dim] with their own element
+ * strides, at slot_mapping[b], with kvc_store_kv's slot rules) followed by
+ * kvc_paged_decode over context_lens (which count the new token).  Replaces
+ * store_kvcache + paged_decode_attention of the engine's decode step
+ * (nanovllm/layers/attention.py:9-30, :239-245;
+ * nanovllm/kernels/paged_attention.py:193-245).  Where the decode launch
+ * stages 4 kv heads per workgroup and the rows are 16-byte aligned, the
+ * store rides in the decode launch itself: the workgroup holding a row's
+ * last tile stores the row and uses it straight from the inputs.  That form
+ * requires what the engine's decode slots satisfy (model_runner.py:685):
+ * slot_mapping[b] is the slot of position context_lens[b] - 1 in row b's
+ * block table, and no other row of the call reads that slot.  Otherwise,
+ * or for other layouts, the store runs as its own launch first.  Results
+ * and pool contents equal the two calls' bit for bit. */
+int kvc_paged_decode_append(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                            const void* key, int64_t key_stride_n, int64_t key_stride_h,
+                            const void* value, int64_t value_stride_n, int64_t value_stride_h,
+                            const void* slot_mapping, int slot_index_bytes, void* k_cache,
+                            void* v_cache, int64_t num_cache_blocks, int64_t page_size,
+                            int64_t num_kv_heads, int64_t head_dim,
+                            const int32_t* block_tables, int64_t bt_stride,
+                            int64_t max_blocks_per_seq, const int32_t* context_lens,
+                            int64_t batch, int64_t num_heads, float scale, void* out,
+                            int64_t out_stride_b, int64_t out_stride_h, void* workspace,
+                            size_t workspace_bytes, kvc_stream_t stream);
+
 /* ---------------------------------------------------------------------------
  * Mixed decode + chunked-prefill attention in one launch.
  * ------------------------------------------------------------------------- */

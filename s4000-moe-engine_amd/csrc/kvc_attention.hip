@@ -88,6 +88,16 @@ struct AttnParams {
   // the number of workgroups that row unit r (= row * groups + group) spans.
   int sk_min_share;
   int* sk_nseg;
+  // Paged decode with the step's append fused (app_k null: no append): row b
+  // of app_k / app_v (element strides) goes to pool slot app_slots[b]
+  // (int32 or int64, wrapped like a Python index, skipped when outside
+  // [0, app_num_slots)).
+  const uint16_t* app_k;
+  const uint16_t* app_v;
+  int64_t app_k_st, app_k_sh, app_v_st, app_v_sh;
+  const void* app_slots;
+  int app_slot_bytes;
+  int64_t app_num_slots;
 };
 
 struct LaneId {
@@ -949,6 +959,31 @@ __device__ __forceinline__ void attend_tile_half(HalfState& st, const u32x4_t (&
   for (int jj = 0; jj < 4; ++jj) st.o[jj] = mfma_bf16(v_operand_half(vrow, jj), pb, st.o[jj]);
 }
 
+// The fused append's 16 bytes of lane `lane` of row b's new K and V, for kv
+// heads 4 kvg .. 4 kvg + 3: head 4 kvg + lane / 16, dims 8 (lane % 16) .. +7,
+// i.e. the bytes the lane's DMA slot covers in a token row of the pool.
+__device__ __forceinline__ void append_load(const AttnParams& p, int b, int kvg, int lane,
+                                            u32x4_t& kn, u32x4_t& vn) {
+  const int head = kvg * 4 + (lane >> 4);
+  const int d = (lane & 15) * 8;
+  kn = *reinterpret_cast<const u32x4_t*>(p.app_k + int64_t(b) * p.app_k_st +
+                                         int64_t(head) * p.app_k_sh + d);
+  vn = *reinterpret_cast<const u32x4_t*>(p.app_v + int64_t(b) * p.app_v_st +
+                                         int64_t(head) * p.app_v_sh + d);
+}
+
+// Stores them at row b's slot (store_kvcache's rules for the slot).
+__device__ __forceinline__ void append_store(const AttnParams& p, int b, int kvg, int lane,
+                                             const u32x4_t& kn, const u32x4_t& vn) {
+  const int64_t raw = p.app_slot_bytes == 8 ? load_index<8>(p.app_slots, b)
+                                            : load_index<4>(p.app_slots, b);
+  const int64_t slot = wrap_slot(raw, p.app_num_slots);
+  if (slot < 0 || slot >= p.app_num_slots) return;
+  const int64_t off = slot * p.tok_bytes + int64_t(kvg) * 1024 + lane * 16;
+  *reinterpret_cast<u32x4_t*>(const_cast<char*>(p.k_cache) + off) = kn;
+  *reinterpret_cast<u32x4_t*>(const_cast<char*>(p.v_cache) + off) = vn;
+}
+
 __device__ void decode_segment_lds(const AttnParams& p, char* stage0, char* stage1, char* qlds,
                                    const int32_t* bt, int b, int kvg, int ctx, int t0, int t1,
                                    int split) {
@@ -963,6 +998,14 @@ __device__ void decode_segment_lds(const AttnParams& p, char* stage0, char* stag
   t1 = uniform(t1);
   const int ntiles = t1 > t0 ? t1 - t0 : 0;
   const int c0 = t0 * kTile;
+  // Fused append: the segment holding the row's last tile stores the new
+  // token's K/V rows, and the wave whose DMA brings that token's row into
+  // the last tile's stage overwrites it there with the same bytes (so the
+  // tile never depends on when the pool store lands).
+  const bool app = p.app_k != nullptr && ntiles > 0 && t1 == (ctx + kTile - 1) / kTile;
+  const int app_row = (ctx - 1) & (kTile - 1);
+  const bool app_wave = app && wave == (app_row & 7);
+  u32x4_t app_kn, app_vn;
 
   QOps<kBF16, 1> Q;
   HalfState st;
@@ -1023,6 +1066,12 @@ __device__ void decode_segment_lds(const AttnParams& p, char* stage0, char* stag
     } else {
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     }
+    if (app_wave && j == ntiles - 1) {
+      // this wave's DMA of the row has landed (vmcnt(0) above); the pool
+      // store waits for the epilogue, where this segment drains its stores
+      *reinterpret_cast<u32x4_t*>(stage + app_row * kLdsPitch + L.lane * 16) = app_kn;
+      *reinterpret_cast<u32x4_t*>(stage + kLdsTensor + app_row * kLdsPitch + L.lane * 16) = app_vn;
+    }
     __syncthreads();
     read_stage(stage);
     __builtin_amdgcn_s_waitcnt(0xC07F);    // lgkmcnt(0): the stage is in registers
@@ -1049,8 +1098,11 @@ __device__ void decode_segment_lds(const AttnParams& p, char* stage0, char* stag
   if (ntiles > 0) {
     issue_q();
     issue(0, stage0);
+    if (ntiles > 1) issue(1, stage1);
+    // Issued after the segment's first DMAs: every wait below still covers
+    // what it covered, as the youngest outstanding loads are the same.
+    if (app_wave) append_load(p, b, kvg, L.lane, app_kn, app_vn);
     if (ntiles > 1) {
-      issue(1, stage1);
       __builtin_amdgcn_s_waitcnt(0x4F70);  // vmcnt(16): this wave's query loads
     } else {
       __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8)
@@ -1068,6 +1120,7 @@ __device__ void decode_segment_lds(const AttnParams& p, char* stage0, char* stag
     }
   }
 
+  if (app_wave) append_store(p, b, kvg, L.lane, app_kn, app_vn);
   // Epilogue: lane (lm, lg) holds, for r = 0..3, dims 32lg + 8r + 4hf .. +3
   // of column lm; l is lane-partial over the key slots.
   const float l = rows4_sum(st.l);
@@ -1958,6 +2011,16 @@ paged_decode_sk_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
           if (owner == w) {
             write_nan_rows(p, r / groups, r % groups);
             set_nseg(p, r / groups, r % groups, 0);
+            if constexpr (kBfLds) {
+              if (p.app_k != nullptr) {
+                // one lane holds this row unit here: it stores all 64 chunks
+                for (int c = 0; c < 64; ++c) {
+                  u32x4_t kn, vn;
+                  append_load(p, r / groups, r % groups, c, kn, vn);
+                  append_store(p, r / groups, r % groups, c, kn, vn);
+                }
+              }
+            }
           }
         } else if (share_of(P) == w) {
           set_nseg(p, r / groups, r % groups, share_of(P + t - 1) - share_of(P) + 1);
@@ -3458,17 +3521,26 @@ extern "C" size_t kvc_paged_decode_workspace_bytes(int64_t batch, int64_t num_he
   return partial_bytes(batch, num_heads, splits);
 }
 
-extern "C" int kvc_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
-                                const void* k_cache, const void* v_cache,
-                                int64_t num_cache_blocks, int64_t page_size, int64_t num_kv_heads,
-                                int64_t head_dim, int kv_dtype, const float* k_scale,
-                                const float* v_scale, const void* side_k, const void* side_v,
-                                const int32_t* out_idx2d, const int32_t* head_n_out,
-                                int64_t n_out_max, const int32_t* block_tables, int64_t bt_stride,
-                                int64_t max_blocks_per_seq, const int32_t* context_lens,
-                                int64_t batch, int64_t num_heads, float scale, void* out,
-                                int64_t out_stride_b, int64_t out_stride_h, void* workspace,
-                                size_t workspace_bytes, kvc_stream_t stream) {
+namespace {
+// The step's append to fuse into a paged decode launch (key null: none).
+struct DecodeAppend {
+  const void* key;
+  int64_t key_stride_n, key_stride_h;
+  const void* value;
+  int64_t value_stride_n, value_stride_h;
+  const void* slot_mapping;
+  int slot_index_bytes;
+};
+
+int paged_decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_cache,
+                      const void* v_cache, int64_t num_cache_blocks, int64_t page_size,
+                      int64_t num_kv_heads, int64_t head_dim, int kv_dtype, const float* k_scale,
+                      const float* v_scale, const void* side_k, const void* side_v,
+                      const int32_t* out_idx2d, const int32_t* head_n_out, int64_t n_out_max,
+                      const int32_t* block_tables, int64_t bt_stride, int64_t max_blocks_per_seq,
+                      const int32_t* context_lens, int64_t batch, int64_t num_heads, float scale,
+                      void* out, int64_t out_stride_b, int64_t out_stride_h, void* workspace,
+                      size_t workspace_bytes, const DecodeAppend& app, kvc_stream_t stream) {
   clear_error();
   KVC_REQUIRE(head_dim == kD, KVC_ERR_VALUE, "paged_decode: head_dim must be 128 (got %lld)",
               (long long)head_dim);
@@ -3534,9 +3606,37 @@ extern "C" int kvc_paged_decode(const void* q, int64_t q_stride_b, int64_t q_str
     p.sk_nseg = reinterpret_cast<int*>(static_cast<char*>(workspace) +
                                        sk_partial_part(batch, num_heads, p.max_splits));
     p.chunk_tokens = kTile;
+    const bool lds_bf16 = kv_dtype == KVC_KV_BF16 && hp.kvs_per_wg == 4 && hp.nslices == 1 &&
+                          env_int("KVC_DECODE_LDS", 1) != 0;
+    if (app.key != nullptr) {
+      // The LDS bf16 segments take the append in (16-byte rows of 4 kv heads);
+      // any other form gets the store launch first.
+      const bool fuse = lds_bf16 && (reinterpret_cast<uintptr_t>(app.key) % 16) == 0 &&
+                        (reinterpret_cast<uintptr_t>(app.value) % 16) == 0 &&
+                        app.key_stride_n % 8 == 0 && app.key_stride_h % 8 == 0 &&
+                        app.value_stride_n % 8 == 0 && app.value_stride_h % 8 == 0;
+      if (fuse) {
+        p.app_k = static_cast<const uint16_t*>(app.key);
+        p.app_v = static_cast<const uint16_t*>(app.value);
+        p.app_k_st = app.key_stride_n;
+        p.app_k_sh = app.key_stride_h;
+        p.app_v_st = app.value_stride_n;
+        p.app_v_sh = app.value_stride_h;
+        p.app_slots = app.slot_mapping;
+        p.app_slot_bytes = app.slot_index_bytes;
+        p.app_num_slots = num_cache_blocks * page_size;
+      } else {
+        rc = kvc_store_kv(app.key, app.key_stride_n, app.key_stride_h, app.value,
+                          app.value_stride_n, app.value_stride_h, const_cast<void*>(k_cache),
+                          const_cast<void*>(v_cache), num_cache_blocks * page_size,
+                          app.slot_mapping, app.slot_index_bytes, batch, num_kv_heads, head_dim,
+                          2, stream);
+        if (rc != KVC_OK) return rc;
+      }
+    }
     switch (kv_dtype) {
       case KVC_KV_BF16:
-        if (hp.kvs_per_wg == 4 && hp.nslices == 1 && env_int("KVC_DECODE_LDS", 1) != 0) {
+        if (lds_bf16) {
           paged_decode_sk_kernel<kBF16, true>
               <<<sp.grid, kThreads, 0, st>>>(p, block_tables, context_lens);
         } else {
@@ -3563,6 +3663,13 @@ extern "C" int kvc_paged_decode(const void* q, int64_t q_stride_b, int64_t q_str
     launch_merge(p, batch, st);
     return check_launch("paged_decode merge");
   }
+  if (app.key != nullptr) {
+    rc = kvc_store_kv(app.key, app.key_stride_n, app.key_stride_h, app.value,
+                      app.value_stride_n, app.value_stride_h, const_cast<void*>(k_cache),
+                      const_cast<void*>(v_cache), num_cache_blocks * page_size, app.slot_mapping,
+                      app.slot_index_bytes, batch, num_kv_heads, head_dim, 2, stream);
+    if (rc != KVC_OK) return rc;
+  }
   p.chunk_tokens = plan_decode_chunk(batch, hp.groups, max_ctx);
   KVC_REQUIRE(p.chunk_tokens % kTile == 0, KVC_ERR_VALUE,
               "paged_decode: decode chunk must be a multiple of 32");
@@ -3587,6 +3694,49 @@ extern "C" int kvc_paged_decode(const void* q, int64_t q_stride_b, int64_t q_str
     rc = check_launch("paged_decode merge");
   }
   return rc;
+}
+}  // namespace
+
+extern "C" int kvc_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                const void* k_cache, const void* v_cache,
+                                int64_t num_cache_blocks, int64_t page_size, int64_t num_kv_heads,
+                                int64_t head_dim, int kv_dtype, const float* k_scale,
+                                const float* v_scale, const void* side_k, const void* side_v,
+                                const int32_t* out_idx2d, const int32_t* head_n_out,
+                                int64_t n_out_max, const int32_t* block_tables, int64_t bt_stride,
+                                int64_t max_blocks_per_seq, const int32_t* context_lens,
+                                int64_t batch, int64_t num_heads, float scale, void* out,
+                                int64_t out_stride_b, int64_t out_stride_h, void* workspace,
+                                size_t workspace_bytes, kvc_stream_t stream) {
+  return paged_decode_impl(q, q_stride_b, q_stride_h, k_cache, v_cache, num_cache_blocks,
+                           page_size, num_kv_heads, head_dim, kv_dtype, k_scale, v_scale, side_k,
+                           side_v, out_idx2d, head_n_out, n_out_max, block_tables, bt_stride,
+                           max_blocks_per_seq, context_lens, batch, num_heads, scale, out,
+                           out_stride_b, out_stride_h, workspace, workspace_bytes,
+                           DecodeAppend{}, stream);
+}
+
+extern "C" int kvc_paged_decode_append(
+    const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* key, int64_t key_stride_n,
+    int64_t key_stride_h, const void* value, int64_t value_stride_n, int64_t value_stride_h,
+    const void* slot_mapping, int slot_index_bytes, void* k_cache, void* v_cache,
+    int64_t num_cache_blocks, int64_t page_size, int64_t num_kv_heads, int64_t head_dim,
+    const int32_t* block_tables, int64_t bt_stride, int64_t max_blocks_per_seq,
+    const int32_t* context_lens, int64_t batch, int64_t num_heads, float scale, void* out,
+    int64_t out_stride_b, int64_t out_stride_h, void* workspace, size_t workspace_bytes,
+    kvc_stream_t stream) {
+  clear_error();
+  KVC_REQUIRE(key != nullptr && value != nullptr && slot_mapping != nullptr, KVC_ERR_VALUE,
+              "paged_decode_append: key, value and slot_mapping are required");
+  KVC_REQUIRE(slot_index_bytes == 4 || slot_index_bytes == 8, KVC_ERR_VALUE,
+              "paged_decode_append: slot_mapping must be int32 or int64");
+  const DecodeAppend app{key, key_stride_n, key_stride_h, value, value_stride_n, value_stride_h,
+                         slot_mapping, slot_index_bytes};
+  return paged_decode_impl(q, q_stride_b, q_stride_h, k_cache, v_cache, num_cache_blocks,
+                           page_size, num_kv_heads, head_dim, KVC_KV_BF16, nullptr, nullptr,
+                           nullptr, nullptr, nullptr, nullptr, 0, block_tables, bt_stride,
+                           max_blocks_per_seq, context_lens, batch, num_heads, scale, out,
+                           out_stride_b, out_stride_h, workspace, workspace_bytes, app, stream);
 }
 
 extern "C" size_t kvc_varlen_workspace_bytes(int64_t num_q_tokens, int64_t num_heads,

@@ -49,6 +49,9 @@ SIGNATURES = {
     "kvc_paged_decode": (_INT, [_P, _I64, _I64, _P, _P, _I64, _I64, _I64, _I64, _INT,
                                 _P, _P, _P, _P, _P, _P, _I64, _P, _I64, _I64, _P, _I64,
                                 _I64, _F32, _P, _I64, _I64, _P, _SZ, _P]),
+    "kvc_paged_decode_append": (_INT, [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _INT,
+                                       _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _I64, _P,
+                                       _I64, _I64, _F32, _P, _I64, _I64, _P, _SZ, _P]),
     "kvc_varlen_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64]),
     "kvc_varlen_prefill_units": (_I64, [_P, _P, _I64, _I64, _I64, _I64]),
     "kvc_varlen_attention": (_INT, [_P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _I64,

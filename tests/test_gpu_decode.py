@@ -158,3 +158,42 @@ def test_pages_smaller_than_256(page):
     wl = decode_workload(len(lens), 32, 4, blocks, lens, seed=page, device=DEV, page=page)
     _check(wl.q, wl.k_cache, wl.v_cache, wl.block_tables, wl.context_lens, wl.scale,
            f"page-{page}")
+
+
+@pytest.mark.parametrize("case", ["b64x4096", "ragged-with-empty", "int64-negative-slots",
+                                  "unaligned-key-fallback", "two-kv-heads-fallback"])
+def test_decode_append_equals_store_then_decode(case):
+    """paged_decode_append (the store inside the decode launch where the
+    layout allows) against store_kvcache then paged_decode_attention: the
+    same output bits and the same pool bytes."""
+    from nanovllm_amd.kernels.paged_attention import paged_decode_append
+    heads, kvh = (16, 2) if case == "two-kv-heads-fallback" else (32, 4)
+    if case == "b64x4096":
+        lens, nb = [4096] * 64, 1100
+    elif case == "ragged-with-empty":
+        lens, nb = [1, 0, 33, 4096, 257, 0, 9000, 31], 80
+    else:
+        lens, nb = uniform_lengths(20, 1, 5000, seed=61), 600
+    wl = decode_workload(len(lens), heads, kvh, nb, [max(1, n) for n in lens], seed=len(lens),
+                         device=DEV, pool_device_fill=True)
+    wl.context_lens = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    slots = wl.slot_mapping.clone()
+    num_slots = wl.k_cache.size(0) * wl.k_cache.size(1)
+    if case == "int64-negative-slots":
+        slots = slots.long()
+        slots[::3] -= num_slots            # wraps back to the same slot
+    key, value = wl.new_k, wl.new_v
+    if case == "unaligned-key-fallback":
+        big = torch.randn(len(lens), kvh * 128 + 4, dtype=torch.bfloat16, device=DEV)
+        big[:, 4:] = key.reshape(len(lens), -1)
+        key = big[:, 4:].view(len(lens), kvh, 128)   # 8-byte aligned rows
+    print(f"[decode] append fused {case}: B={len(lens)}", flush=True)
+    kc0, vc0 = wl.k_cache.clone(), wl.v_cache.clone()
+    store_kvcache(key, value, kc0, vc0, slots)
+    ref = paged_decode_attention(wl.q, kc0, vc0, wl.block_tables, wl.context_lens, wl.scale, 0)
+    kc1, vc1 = wl.k_cache.clone(), wl.v_cache.clone()
+    out = paged_decode_append(wl.q, key, value, kc1, vc1, slots, wl.block_tables,
+                              wl.context_lens, wl.scale)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(out), bits(ref)), "outputs differ from store + decode"
+    assert np.array_equal(bits(kc1), bits(kc0)) and np.array_equal(bits(vc1), bits(vc0))
