@@ -417,14 +417,14 @@ def run_rope(args, torch):
 
 def run_decode_graph(args, torch):
     """A 48-layer decode step's KV work (per layer: append one token per
-    sequence, then paged decode) run eagerly and as a replayed HIP graph of
+    sequence and paged decode, one paged_decode_append call) run eagerly and
+    as a replayed HIP graph of
     the batch's bucket, with the padded rows aimed at the scratch block.  Two
     sizes: batch 64 x context 4096 (the headline shape, GPU-bound) and
     batch 8 x context 512 (launch-bound).  Shape 32 q / 4 kv heads x 128 bf16,
     page 256."""
     from nanovllm_amd.engine.graph_runner import DecodeGraphRunner
-    from nanovllm_amd.kernels.paged_attention import paged_decode_attention
-    from nanovllm_amd.layers.attention import store_kvcache
+    from nanovllm_amd.kernels.paged_attention import paged_decode_append
     from nanovllm_amd.workloads import build_block_tables, slots_for_last_token
     dev = torch.device("cuda:0")
     L, H, KVH = 48, 32, 4
@@ -448,8 +448,8 @@ def run_decode_graph(args, torch):
 
         def eager():
             for layer in range(L):
-                store_kvcache(k[layer], v[layer], kcs[layer], vcs[layer], slots)
-                paged_decode_attention(q[layer], kcs[layer], vcs[layer], bt, cl, 128 ** -0.5, ctx)
+                paged_decode_append(q[layer], k[layer], v[layer], kcs[layer], vcs[layer], slots,
+                                    bt, cl, 128 ** -0.5)
 
         runner = DecodeGraphRunner(kcs, vcs, H, max_bs=bs, max_blocks_per_seq=bt.size(1),
                                    scale=128 ** -0.5, buckets=[bs])

@@ -14,18 +14,18 @@ Follows the engine's decode graph protocol (nanovllm/engine/model_runner.py:
   same bytes whichever lands last.
 
 What is captured is the path's part of a decode step, per layer:
-store_kvcache(k, v, k_cache, v_cache, slot_mapping) then
-paged_decode_attention(q, ...).  Neither records a host synchronisation or a
-memset: loop bounds come from the device context_lens, and the split-K
-workspace is taken from torch's caching allocator (the graph's private pool
-during capture).
+store_kvcache(k, v, k_cache, v_cache, slot_mapping) then the paged decode,
+as one paged_decode_append call (the append rides in the decode launch; a
+padded row's slot is position 0 of its scratch-block table row, as the fused
+append requires).  Nothing records a host synchronisation or a memset: loop
+bounds come from the device context_lens, and the split-K workspace is taken
+from torch's caching allocator (the graph's private pool during capture).
 """
 from __future__ import annotations
 
 import torch
 
-from ..kernels.paged_attention import paged_decode_attention
-from ..layers.attention import store_kvcache
+from ..kernels.paged_attention import paged_decode_append
 
 
 def default_buckets(max_bs: int) -> list[int]:
@@ -87,12 +87,11 @@ class DecodeGraphRunner:
 
     def _step(self, bs: int) -> None:
         sm, cl, bt = self.slot_mapping[:bs], self.context_lens[:bs], self.block_tables[:bs]
-        max_len = bt.size(1) * self.page  # an upper bound: no host read of context_lens
         for layer in range(self.num_layers):
             kc, vc = self.k_caches[layer], self.v_caches[layer]
-            store_kvcache(self.k[layer, :bs], self.v[layer, :bs], kc, vc, sm)
-            self.out[layer, :bs] = paged_decode_attention(
-                self.q[layer, :bs], kc, vc, bt, cl, self.scale, max_len)
+            self.out[layer, :bs] = paged_decode_append(
+                self.q[layer, :bs], self.k[layer, :bs], self.v[layer, :bs], kc, vc, sm, bt, cl,
+                self.scale)
 
     def capture(self) -> None:
         """Capture every bucket, small first (model_runner.py:1169-1175): a
