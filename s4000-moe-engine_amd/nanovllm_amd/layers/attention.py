@@ -9,7 +9,9 @@ change.  What changes is underneath:
   strided V view of a fused qkv projection is not copied first);
 * decode is the split-K paged kernel regardless of `attention_backend` (the
   reference's "sdpa" decode gathers and expands the whole padded table,
-  attention.py:239-279; both backends compute the same function);
+  attention.py:239-279; both backends compute the same function); on a bf16
+  pool the step's append rides in the decode launch (paged_decode_append),
+  with the same results and pool bytes as store + decode;
 * prefill and mixed batches are ONE varlen launch instead of a Python loop
   over sequences plus torch.cat (attention.py:146-166, :179-213).
 """
