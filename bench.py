@@ -42,8 +42,9 @@ def parse_args():
                     choices=["decode", "decode-dist", "int8", "mixed", "append", "swap", "copy",
                              "rope", "decode-graph", "offload-overlap", "pd-wire"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-sample", type=int, default=64,
-                    help="sequences of the workload the CPU baseline runs")
+    ap.add_argument("--cpu-sample", type=int, default=0,
+                    help="sequences of the workload the CPU baseline runs (default: 64 of "
+                         "the bf16 decode batch, 2 of the 32k-context int8 batch)")
     return ap.parse_args()
 
 
@@ -129,7 +130,39 @@ def profiled_traffic(workload: str):
 # ---------------------------------------------------------------------------
 # CPU baseline: the engine's torch decode path on the host
 # ---------------------------------------------------------------------------
-def cpu_decode_baseline(torch, wl, sample: int, reps: int = 5):
+def _median_cv(times):
+    med = statistics.median(times)
+    return med, statistics.pstdev(times) / statistics.fmean(times)
+
+
+def _peak_rss_gb():
+    import resource
+    return resource.getrusage(resource.RUSAGE_SELF).ru_maxrss / 1e6   # KiB -> GB
+
+
+def _timed_reps(fn, reps):
+    fn()   # warm-up
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return _median_cv(times)
+
+
+def _host_blocks(torch, cache, bt, used):
+    """The blocks `used` of a device pool on the host, renumbered 0.."""
+    return cache.index_select(0, used.to(cache.device)).cpu()
+
+
+def cpu_decode_baseline(torch, wl, sample: int, tok_bytes: int, reps: int = 5,
+                        int8: bool = False):
+    """The engine's torch CPU decode step on a bounded sample of the
+    workload's sequences: bf16, append (index_put, attention.py:9-30) + the
+    gather + expand + masked SDPA decode (attention.py:239-279); int8
+    per-token-head, the p14 quantise-on-append (p14_int8_kv_probe.py:37-41)
+    + gather + dequantise (:45-46) + the same SDPA.  Reported as tokens/s and
+    as effective GB/s over the sample's algorithmic KV bytes."""
     from oracle import kv_oracle as ko
     threads = cpu_threads()
     torch.set_num_threads(threads)
@@ -138,32 +171,122 @@ def cpu_decode_baseline(torch, wl, sample: int, reps: int = 5):
     used = torch.unique(bt[bt >= 0])
     remap = torch.full((wl.k_cache.size(0),), -1, dtype=torch.int64)
     remap[used] = torch.arange(used.numel())
-    kc = wl.k_cache.index_select(0, used.to(wl.k_cache.device)).cpu()
-    vc = wl.v_cache.index_select(0, used.to(wl.v_cache.device)).cpu()
+    kc = _host_blocks(torch, wl.k_cache, bt, used)
+    vc = _host_blocks(torch, wl.v_cache, bt, used)
     bt_small = torch.where(bt >= 0, remap[bt.clamp(min=0).long()], torch.full_like(bt, -1,
                            dtype=torch.int64)).to(torch.int32)
     q = wl.q[:b].cpu()
     lens = wl.context_lens[:b].cpu()
     max_len = int(lens.max())
-    ko.gather_sdpa_decode(q, kc, vc, bt_small, lens, wl.scale, max_len)   # warm-up
-    times = []
-    for _ in range(reps):
-        t0 = time.perf_counter()
-        ko.gather_sdpa_decode(q, kc, vc, bt_small, lens, wl.scale, max_len)
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
-    cv = statistics.pstdev(times) / statistics.fmean(times)
-    import resource
-    rss_gb = resource.getrusage(resource.RUSAGE_SELF).ru_maxrss / 1e6   # KiB -> GB
+    page = kc.size(1)
+    last = lens.long() - 1
+    slots = (bt_small.long().gather(1, (last // page).unsqueeze(1)).squeeze(1) * page
+             + last % page)
+    nk, nv = wl.new_k[:b].cpu(), wl.new_v[:b].cpu()
+    if int8:
+        ks = _host_blocks(torch, wl.k_scale, bt, used)
+        vs = _host_blocks(torch, wl.v_scale, bt, used)
+        row = kc.size(2) * kc.size(3)
+
+        def step():
+            for x, codes, sc in ((nk, kc, ks), (nv, vc, vs)):
+                c, s_ = ko.quant_tokhead_torch(x)
+                codes.view(-1, row)[slots] = c.reshape(b, row)
+                sc.view(-1, sc.size(-1))[slots] = s_.squeeze(-1)
+            ko.gather_sdpa_decode_int8_tokhead(q, kc, vc, ks, vs, bt_small, lens, wl.scale,
+                                               max_len)
+        what = ("p14 int8 quantise-on-append + gather + dequantise + expand + masked SDPA "
+                "decode")
+    else:
+        row = kc.size(2) * kc.size(3)
+
+        def step():
+            kc.view(-1, row)[slots] = nk.reshape(b, row)
+            vc.view(-1, row)[slots] = nv.reshape(b, row)
+            ko.gather_sdpa_decode(q, kc, vc, bt_small, lens, wl.scale, max_len)
+        what = "torch append (index_put) + gather + expand + masked SDPA decode"
+    med, cv = _timed_reps(step, reps)
+    kv_bytes = int(lens.sum()) * tok_bytes
     return {
         "value": round(b / med, 1),
         "unit": "tokens/s",
+        "GBps_effective": round(kv_bytes / med / 1e9, 3),
         "cores": threads,
         "kind": "port",
         "sample": (f"{b} of the {wl.batch} sequences (same q, block tables and KV bytes), "
-                   f"torch gather+expand+masked SDPA decode, median of {reps} reps "
-                   f"({med * 1e3:.1f} ms, cv {cv:.2f}); process peak RSS {rss_gb:.1f} GB"),
+                   f"{what}, median of {reps} reps ({med * 1e3:.1f} ms, cv {cv:.2f}); "
+                   f"process peak RSS {_peak_rss_gb():.1f} GB"),
     }
+
+
+def cpu_mixed_baseline(torch, q, kc, vc, bt, dec, dlen, cu_q, cu_k, flops, reps=3):
+    """The engine's torch mixed batch on the host (attention.py:146-166):
+    gather + SDPA decode of the decode rows, the per-sequence prefill loop
+    with the prefix mask (:179-213), torch.cat.  The whole workload (it is
+    bounded: about a second per call on 16 cores)."""
+    from oracle import kv_oracle as ko
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    bt_h = bt.cpu()
+    used = torch.unique(bt_h[bt_h >= 0])
+    remap = torch.full((kc.size(0),), -1, dtype=torch.int64)
+    remap[used] = torch.arange(used.numel())
+    kch = kc.index_select(0, used.to(kc.device)).cpu()
+    vch = vc.index_select(0, used.to(vc.device)).cpu()
+    bt_small = torch.where(bt_h >= 0, remap[bt_h.clamp(min=0).long()],
+                           torch.full_like(bt_h, -1, dtype=torch.int64)).to(torch.int32)
+    qh = q.cpu()
+    dl = dlen.cpu()
+    nd = len(dec)
+
+    def call():
+        ko.mixed_torch(qh, kch, vch, bt_small, nd, dl, int(dl.max()), cu_q, cu_k, 128 ** -0.5)
+    med, cv = _timed_reps(call, reps)
+    T = q.size(0)
+    return {"value": round(T / med, 1), "unit": "tokens/s",
+            "prefill_TFLOPs": round(flops / med / 1e12, 3),
+            "decode_kv_GBps_effective": round(sum(dec) * 2048 / med / 1e9, 3),
+            "cores": threads, "kind": "port",
+            "sample": (f"the whole mixed call ({nd} decode rows + {len(cu_q) - 1} prefill "
+                       f"chunks), torch gather + SDPA decode rows, per-sequence prefix-masked "
+                       f"SDPA prefill loop, cat; median of {reps} reps ({med * 1e3:.1f} ms, "
+                       f"cv {cv:.2f}); process peak RSS {_peak_rss_gb():.1f} GB")}
+
+
+def cpu_swap_baseline(torch, L, kvh, reps=3):
+    """The engine's torch block moves on the host (model_runner.py:284-305
+    offload_put / offload_get, and the compaction as index_select +
+    index_copy_) on a host pool scaled to host memory: 96 blocks of
+    [2, L, 256, kvh, 128] bf16 (24 MiB each at 48 layers x 4 kv heads),
+    8 puts into pinned-size host slots, 8 gets back, a 32-block compaction
+    (the config's 128 / 128 / 1024 scaled by 1/16 and 1/32)."""
+    from oracle import kv_oracle as ko
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    nb, n_swap, n_copy = 96, 8, 32
+    g = torch.Generator().manual_seed(7)
+    pool = torch.empty(2, L, nb, 256, kvh, 128, dtype=torch.bfloat16)
+    pool.view(torch.int16).random_(generator=g)
+    perm = torch.randperm(nb, generator=g).tolist()
+    out_ids, in_ids = perm[:n_swap], perm[n_swap:2 * n_swap]
+    src, dst = perm[2 * n_swap:2 * n_swap + n_copy], perm[2 * n_swap + n_copy:2 * n_swap + 2 * n_copy]
+    slots = torch.empty(n_swap, 2, L, 256, kvh, 128, dtype=torch.bfloat16)
+
+    def step():
+        for i, b in enumerate(out_ids):
+            ko.offload_put_torch(pool, b, slots[i])
+        for i, b in enumerate(in_ids):
+            ko.offload_get_torch(pool, slots[i], b)
+        ko.compact_torch(pool, src, dst)
+    med, cv = _timed_reps(step, reps)
+    item = 2 * L * 256 * kvh * 128 * 2
+    moved = 2 * n_swap * item + 2 * n_copy * item
+    return {"value": round(moved / med / 1e9, 3), "unit": "GB/s (moved bytes: put + get + "
+            "2 x compaction)", "cores": threads, "kind": "port",
+            "sample": (f"host pool of {nb} x {item / 2 ** 20:.0f} MiB blocks: {n_swap} "
+                       f"offload_put (index_select + slot copy), {n_swap} offload_get "
+                       f"(index_copy_), {n_copy}-block compaction; median of {reps} reps "
+                       f"({med * 1e3:.1f} ms, cv {cv:.2f})")}
 
 
 # ---------------------------------------------------------------------------
@@ -172,17 +295,21 @@ def cpu_decode_baseline(torch, wl, sample: int, reps: int = 5):
 def run_decode(args, torch, dist: bool, int8: bool = False):
     from nanovllm_amd.kernels.kv_int8 import store_kvcache_int8_tokhead
     from nanovllm_amd.kernels.paged_attention import paged_decode_append, paged_decode_attention
-    from nanovllm_amd.workloads import decode_workload, uniform_lengths
+    from nanovllm_amd.workloads import (decode_workload, int8_tokhead_decode_workload,
+                                        uniform_lengths)
 
     dev = torch.device("cuda:0")
     if int8:
+        # K ~ N(0,1) with 1 % of entries x20, V ~ N(0,1), every context token
+        # appended through the per-token-head quantiser before the timed steps
         batch, heads, kvh, blocks = 16, 32, 4, 2048 + 16
         lens = [32768] * batch
+        wl = int8_tokhead_decode_workload(batch, heads, kvh, blocks, lens, seed=3, device=dev)
     else:
         batch, heads, kvh, blocks = 64, 32, 4, 8192
         lens = uniform_lengths(batch, 512, 4096, seed=2) if dist else [4096] * batch
-    wl = decode_workload(batch, heads, kvh, blocks, lens, seed=3, device=dev,
-                         pool_device_fill=True, kv_dtype="int8_tokhead" if int8 else "bf16")
+        wl = decode_workload(batch, heads, kvh, blocks, lens, seed=3, device=dev,
+                             pool_device_fill=True)
 
     def step(timer=None):
         if int8:
@@ -242,7 +369,9 @@ def run_decode(args, torch, dist: bool, int8: bool = False):
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8" if int8 else "bf16",
-        "data": "synthetic (seeded N(0,1) q/k/v, random non-contiguous block tables)",
+        "data": ("synthetic (seeded N(0,1) q/v, K N(0,1) with 1% x20 outliers quantised "
+                 "through the append, random non-contiguous block tables)" if int8 else
+                 "synthetic (seeded N(0,1) q/k/v, random non-contiguous block tables)"),
         "config": {
             "workload": (f"paged decode step (append 1 token/seq + decode), {heads}q/{kvh}kv/128 "
                          f"{'int8 per-token-head' if int8 else 'bf16'}, batch {batch} x "
@@ -253,7 +382,9 @@ def run_decode(args, torch, dist: bool, int8: bool = False):
             "kv_heads": kvh,
             "head_dim": 128,
             "page": 256,
-            "decode_kernel_us": round(kernel_ms * 1e3, 2),
+            # HIP events around the decode call: the decode kernel + its split
+            # merge (the kernel alone is in the committed kernel trace)
+            "decode_call_us": round(kernel_ms * 1e3, 2),
             "kv_read_GBps": round(kv_bytes / (kernel_ms * 1e-3) / 1e9, 1),
         },
         "roofline": {
@@ -263,10 +394,13 @@ def run_decode(args, torch, dist: bool, int8: bool = False):
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": profiled_traffic(args.workload),
+            "traffic_source": "rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE of the same workload, "
+                              "committed under profiles/ (not measured in this run)",
         },
     }
     if not args.no_cpu_baseline:
-        res["cpu_baseline"] = cpu_decode_baseline(torch, wl, args.cpu_sample)
+        sample = args.cpu_sample if args.cpu_sample else (2 if int8 else 64)
+        res["cpu_baseline"] = cpu_decode_baseline(torch, wl, sample, tok_bytes, int8=int8)
     return res
 
 
@@ -331,7 +465,7 @@ def run_mixed(args, torch):
             flops += 4 * 128 * heads * (p + r + 1)
     kv = sum(dec) * 2 * kvh * 128 * 2
     pre_tflops = flops / (ms_pre * 1e-3) / 1e12
-    return {"workload": "mixed: 60 decode rows ctx U[256,4096] + 4x256-token prefill chunks "
+    res = {"workload": "mixed: 60 decode rows ctx U[256,4096] + 4x256-token prefill chunks "
                         "(prefix 0/512/2048/8192): paged decode launch + stream-K prefill "
                         "launch + their merges",
             "ms": round(ms, 4), "prefill_gflop": round(flops / 1e9, 2),
@@ -340,6 +474,10 @@ def run_mixed(args, torch):
             "prefill_mfma_frac": round(pre_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
             "decode_kv_GB": round(kv / 1e9, 3),
             "tokens_per_s": round(T / (ms * 1e-3), 1)}
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_mixed_baseline(torch, q, kc, vc, bt, dec, dlen, cu_q, cu_k,
+                                                 flops)
+    return res
 
 
 def run_append(args, torch):
@@ -726,7 +864,7 @@ def run_swap(args, torch):
         mover.swap(victims, host_out, revived, host_in, src, dst)
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) / steps
-    return {"workload": (f"offload/compaction step: pool {pool_blocks} x 24 MiB blocks "
+    res = {"workload": (f"offload/compaction step: pool {pool_blocks} x 24 MiB blocks "
                          f"([2, {L}, 256, {kvh}, 128] bf16), {active} active; {n_swap} blocks "
                          f"d2h + {n_swap} h2d (pinned, copy engines) + compaction copy of "
                          f"{n_copy} scattered blocks"),
@@ -736,7 +874,12 @@ def run_swap(args, torch):
             "h2d_ms": round(h2d, 3), "h2d_GBps": round(n_swap * item / (h2d * 1e-3) / 1e9, 1),
             "copy_ms": round(cp, 3),
             "copy_GBps_read_plus_write": round(2 * n_copy * item / (cp * 1e-3) / 1e9, 1),
-            "copy_frac_of_8TBps": round(2 * n_copy * item / (cp * 1e-3) / 8e12, 4)}
+            "copy_frac_of_8TBps": round(2 * n_copy * item / (cp * 1e-3) / 8e12, 4),
+            "step_GBps_moved": round((2 * n_swap + 2 * n_copy) * item / wall / 1e9, 1)}
+    if not args.no_cpu_baseline:
+        del host_out, host_in
+        res["cpu_baseline"] = cpu_swap_baseline(torch, L, kvh)
+    return res
 
 
 def run_copy(args, torch):

@@ -243,20 +243,12 @@ def mixed_ref(q_bits, k_f32, v_f32, block_tables, num_decode_rows, decode_contex
     return np.concatenate([dec, pre], axis=0)
 
 
-def gather_sdpa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
-                       block_tables: torch.Tensor, context_lens: torch.Tensor, scale: float,
-                       max_context_len: int) -> torch.Tensor:
-    """The reference's torch decode path (nanovllm/layers/attention.py:239-279) on
-    CPU tensors: gather the padded block tables, zero invalid rows, expand GQA
-    heads, masked SDPA.  This is the CPU baseline bench.py times."""
-    bs, nh = q.shape[0], q.shape[1]
-    page = k_cache.size(1)
-    max_blocks = block_tables.size(1)
-    blocks = block_tables.clamp(min=0).long()
-    full = max_blocks * page
-    kv_len = max_context_len or full
-    k = k_cache[blocks].view(bs, full, *k_cache.shape[-2:])[:, :kv_len]
-    v = v_cache[blocks].view(bs, full, *v_cache.shape[-2:])[:, :kv_len]
+def _masked_sdpa_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                        context_lens: torch.Tensor, scale: float) -> torch.Tensor:
+    """attention.py:264-279 on gathered rows k, v [B, kv_len, KVH, D]: zero the
+    rows past each context, expand the GQA heads, masked SDPA."""
+    nh = q.shape[1]
+    kv_len = k.size(1)
     valid = torch.arange(kv_len).unsqueeze(0) < context_lens.unsqueeze(1)
     kvh = k.size(2)
     idx = torch.arange(kvh).repeat_interleave(nh // kvh)
@@ -269,6 +261,113 @@ def gather_sdpa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Te
     mask = valid.unsqueeze(0).unsqueeze(2)
     o = torch.nn.functional.scaled_dot_product_attention(qh, k, v, attn_mask=mask, scale=scale)
     return o.squeeze(2).permute(1, 0, 2)
+
+
+def gather_sdpa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                       block_tables: torch.Tensor, context_lens: torch.Tensor, scale: float,
+                       max_context_len: int) -> torch.Tensor:
+    """The reference's torch decode path (nanovllm/layers/attention.py:239-279) on
+    CPU tensors: gather the padded block tables, zero invalid rows, expand GQA
+    heads, masked SDPA.  This is the CPU baseline bench.py times."""
+    bs = q.shape[0]
+    page = k_cache.size(1)
+    blocks = block_tables.clamp(min=0).long()
+    full = block_tables.size(1) * page
+    kv_len = max_context_len or full
+    k = k_cache[blocks].view(bs, full, *k_cache.shape[-2:])[:, :kv_len]
+    v = v_cache[blocks].view(bs, full, *v_cache.shape[-2:])[:, :kv_len]
+    return _masked_sdpa_decode(q, k, v, context_lens, scale)
+
+
+def _expand_heads(kv: torch.Tensor, num_heads: int, dim: int) -> torch.Tensor:
+    """GQA expansion by index_select (nanovllm/layers/attention.py:54-61)."""
+    kvh = kv.size(dim)
+    if kvh == num_heads:
+        return kv
+    return kv.index_select(dim, torch.arange(kvh).repeat_interleave(num_heads // kvh))
+
+
+def prefill_loop_torch(q: torch.Tensor, k_fresh: torch.Tensor, v_fresh: torch.Tensor,
+                       k_cache: torch.Tensor, v_cache: torch.Tensor, cu_q: list, cu_k: list,
+                       block_tables: torch.Tensor | None, scale: float) -> torch.Tensor:
+    """The reference's per-sequence prefill (nanovllm/layers/attention.py:179-213)
+    on CPU tensors: for chunk i, without block tables causal SDPA over the
+    chunk's own expanded k/v (:195-199); with them, gather sk cached tokens
+    (_gather_kv :33-51 without the int8 branch), expand the kv heads and run
+    SDPA under allowed[r, j] = j <= (sk - sq) + r (:200-212); outputs are
+    concatenated in chunk order.  q [T, H, D]."""
+    nh = q.size(1)
+    page = k_cache.size(1)
+    outs = []
+    for i in range(len(cu_q) - 1):
+        sq, sk = cu_q[i + 1] - cu_q[i], cu_k[i + 1] - cu_k[i]
+        if sq == 0 or sk == 0:
+            continue
+        qi = q[cu_q[i]:cu_q[i + 1]].transpose(0, 1).contiguous()
+        if block_tables is None:
+            ki = _expand_heads(k_fresh[cu_k[i]:cu_k[i + 1]], nh, 1).transpose(0, 1).contiguous()
+            vi = _expand_heads(v_fresh[cu_k[i]:cu_k[i + 1]], nh, 1).transpose(0, 1).contiguous()
+            o = torch.nn.functional.scaled_dot_product_attention(
+                qi.unsqueeze(0), ki.unsqueeze(0), vi.unsqueeze(0), scale=scale, is_causal=True)
+        else:
+            nblk = (sk + page - 1) // page
+            blocks = block_tables[i][:nblk].long()
+            kg = k_cache[blocks].view(-1, *k_cache.shape[-2:])[:sk]
+            vg = v_cache[blocks].view(-1, *v_cache.shape[-2:])[:sk]
+            ki = _expand_heads(kg, nh, 1).transpose(0, 1).contiguous()
+            vi = _expand_heads(vg, nh, 1).transpose(0, 1).contiguous()
+            pos = torch.arange(sk - sq, sk)
+            allowed = torch.arange(sk) <= pos.unsqueeze(1)
+            o = torch.nn.functional.scaled_dot_product_attention(
+                qi.unsqueeze(0), ki.unsqueeze(0), vi.unsqueeze(0),
+                attn_mask=allowed.unsqueeze(0), scale=scale)
+        outs.append(o.squeeze(0))
+    return torch.cat(outs, dim=1).transpose(0, 1)
+
+
+def mixed_torch(q, k_cache, v_cache, block_tables, num_decode_rows, decode_context_lens,
+                decode_max_context_len, cu_q, cu_k, scale) -> torch.Tensor:
+    """The reference's mixed batch (attention.py:146-166) on CPU tensors: decode
+    rows through the gather + SDPA decode, prefill rows through the
+    per-sequence loop with block table rows num_decode_rows + i, then cat."""
+    n = num_decode_rows
+    out_dec = gather_sdpa_decode(q[:n], k_cache, v_cache, block_tables[:n], decode_context_lens,
+                                 scale, decode_max_context_len)
+    out_pre = prefill_loop_torch(q[n:], None, None, k_cache, v_cache, cu_q, cu_k,
+                                 block_tables[n:], scale)
+    return torch.cat([out_dec, out_pre], dim=0)
+
+
+def quant_tokhead_torch(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """scripts/archive/p14_int8_kv_probe.py:37-41 as torch ops: amax over D
+    (bf16) -> fp32 -> clamp_min(1e-6); s = amax / 127; codes =
+    round(x / s) (half to even) clamped to +-127.  Returns (codes int8,
+    scales fp32 [..., 1])."""
+    amax = x.abs().amax(dim=-1, keepdim=True).float().clamp_min_(1e-6)
+    s = amax / 127.0
+    return (x.float() / s).round().clamp_(-127, 127).to(torch.int8), s
+
+
+def gather_sdpa_decode_int8_tokhead(q, k_codes, v_codes, k_scale, v_scale, block_tables,
+                                    context_lens, scale, max_context_len) -> torch.Tensor:
+    """The torch decode path over a per-token-head int8 pool: gather the padded
+    block tables' codes and scales (attention.py:251-254), dequantise with the
+    p14 read path bf16(fp32(code) * scale) (p14_int8_kv_probe.py:45-46), then
+    the masked SDPA of attention.py:264-279.  codes [blocks, page, KVH, D]
+    int8, scales [blocks, page, KVH] fp32."""
+    bs = q.size(0)
+    page = k_codes.size(1)
+    full = block_tables.size(1) * page
+    kv_len = max_context_len or full
+    blocks = block_tables.clamp(min=0).long()
+
+    def deq(codes, sc):
+        c = codes[blocks].view(bs, full, *codes.shape[-2:])[:, :kv_len]
+        f = sc[blocks].view(bs, full, sc.size(-1))[:, :kv_len]
+        return (c.float() * f.unsqueeze(-1)).to(torch.bfloat16)
+
+    return _masked_sdpa_decode(q, deq(k_codes, k_scale), deq(v_codes, v_scale), context_lens,
+                               scale)
 
 
 # ---------------------------------------------------------------------------
@@ -297,6 +396,29 @@ def block_copy(pool: np.ndarray, src_ids, dst_ids) -> None:
     src = np.asarray(src_ids, dtype=np.int64)
     dst = np.asarray(dst_ids, dtype=np.int64)
     pool[:, dst] = pool[:, src].copy()
+
+
+def offload_put_torch(kv_cache: torch.Tensor, block_id: int, slot_buf: torch.Tensor) -> None:
+    """ModelRunner.offload_put's byte move (nanovllm/engine/model_runner.py:284-298,
+    HostBlockPool.put kv_offload.py:72-88): index_select one block of the
+    [2, L, blocks, page, KVH, D] pool along dim 2, copy it into the slot."""
+    idx = torch.tensor([block_id], dtype=torch.long)
+    slot_buf.copy_(kv_cache.index_select(2, idx).squeeze(2))
+
+
+def offload_get_torch(kv_cache: torch.Tensor, slot_buf: torch.Tensor, block_id: int) -> None:
+    """ModelRunner.offload_get's byte move (model_runner.py:300-305):
+    index_copy_ of the slot back into block block_id along dim 2."""
+    idx = torch.tensor([block_id], dtype=torch.long)
+    kv_cache.index_copy_(2, idx, slot_buf.unsqueeze(2))
+
+
+def compact_torch(kv_cache: torch.Tensor, src_ids, dst_ids) -> None:
+    """The compaction copy pool[:, :, dst] = pool[:, :, src] in the engine's
+    torch idiom (index_select, then index_copy_ along the block axis)."""
+    src = torch.as_tensor(list(src_ids), dtype=torch.long)
+    dst = torch.as_tensor(list(dst_ids), dtype=torch.long)
+    kv_cache.index_copy_(2, dst, kv_cache.index_select(2, src))
 
 
 def decode_kv_bytes(context_lens, kvh: int, d: int, elem_bytes: int) -> int:

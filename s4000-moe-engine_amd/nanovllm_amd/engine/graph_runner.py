@@ -113,8 +113,14 @@ class DecodeGraphRunner:
                 return b
         raise ValueError(f"batch {bs} exceeds the largest bucket {max(self.buckets)}")
 
-    def run(self, q, k, v, slot_mapping, context_lens, block_tables) -> torch.Tensor:
+    def run(self, q, k, v, slot_mapping, context_lens, block_tables,
+            fence=None) -> torch.Tensor:
+        """One replay.  fence: called before the replay, on the current
+        stream (e.g. KVCacheRunner.fence when block moves run asynchronously:
+        a replayed graph holds no per-layer waits of its own)."""
         bs = q.size(1)
+        if fence is not None:
+            fence()
         b = self.bucket_of(bs)
         self.q[:, :bs] = q
         self.k[:, :bs] = k

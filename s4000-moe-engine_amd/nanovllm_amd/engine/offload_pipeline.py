@@ -15,9 +15,12 @@ section 1, "async + event double buffering").  Here:
 * a copy stream first waits for the work already enqueued on the compute
   stream, so a put reads the block's final contents and a get does not
   overwrite a block that earlier kernels still read;
-* across the two directions: a get waits for the put that filled its slot,
-  and a put waits for the gets issued before it (one of them may still read
-  the slot the put reuses);
+* across the two directions: a get waits for the put that filled its slot
+  and for the last put that read any of its destination blocks (the block
+  manager evicts block B with a put and revives another prefix into the same
+  B at once, so the scatter must not overwrite B while the gather still
+  copies it); a put waits for the gets issued before it (one of them may
+  still read the slot the put reuses, or still write the block it reads);
 * every layer group's copies end in an event.  The compute stream waits for
   a group's events only when it reaches that group: fence_layer(l), called by
   the attention layer before it appends to or reads layer l's planes.  The
@@ -84,6 +87,10 @@ class AsyncOffloader:
         self.get_stream = torch.cuda.Stream(device=kv_cache.device)
         self._pending: list[list[torch.cuda.Event]] = [[] for _ in self.groups]
         self._slot_put_done: dict[int, torch.cuda.Event] = {}
+        # last put event per source block, until a get into that block has
+        # been ordered after it (the get stream is in order: later gets need
+        # no wait of their own)
+        self._block_put_done: dict[int, torch.cuda.Event] = {}
         self._gets_done: torch.cuda.Event | None = None
         # the compute stream is whatever stream is current at each call
         self._cur = lambda: torch.cuda.current_stream(kv_cache.device)
@@ -129,10 +136,11 @@ class AsyncOffloader:
             if self._gets_done is not None:
                 stream.wait_event(self._gets_done)
         else:
-            for s in set(slots):
-                ev = self._slot_put_done.get(s)
-                if ev is not None:
-                    stream.wait_event(ev)
+            waits = {self._slot_put_done.get(s) for s in set(slots)}
+            waits |= {self._block_put_done.pop(b, None) for b in set(block_ids)}
+            waits.discard(None)
+            for ev in waits:
+                stream.wait_event(ev)
         ev = None
         for gi, (l0, l1) in enumerate(self.groups):
             for side in (0, 1):
@@ -158,6 +166,8 @@ class AsyncOffloader:
         if to_host:
             for s in slots:
                 self._slot_put_done[s] = ev
+            for b in block_ids:
+                self._block_put_done[b] = ev
         else:
             self._gets_done = ev
 
@@ -199,9 +209,20 @@ class AsyncOffloader:
     # -- ordering ------------------------------------------------------------
     def fence_layer(self, layer: int) -> None:
         """Make the compute stream wait for the copies of `layer`'s group
-        (device-side wait; the host does not block)."""
+        (device-side wait; the host does not block).
+
+        The wait is enqueued from Python, so it exists only in eager
+        execution: a graph captured over the attention layers would replay
+        without it.  Under capture, with copies still pending, this raises
+        RuntimeError; a caller that replays graphs calls fence() on the
+        compute stream before each replay, outside the graph."""
         pending = self._pending[self.group_of_layer[layer]]
         if pending:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError(
+                    "async KV offload copies are pending while a graph is being captured: "
+                    "the per-layer fence would not be replayed; call fence() before the "
+                    "capture and before every replay")
             cur = self._cur()
             for ev in pending:
                 cur.wait_event(ev)
@@ -217,6 +238,8 @@ class AsyncOffloader:
         self.get_stream.synchronize()
         for p in self._pending:
             p.clear()  # finished: later compute needs no wait for them
+        self._block_put_done.clear()
+        self._slot_put_done.clear()
 
     def in_flight(self) -> bool:
         return any(not ev.query() for p in self._pending for ev in p)

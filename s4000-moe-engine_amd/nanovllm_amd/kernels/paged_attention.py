@@ -16,9 +16,17 @@ Differences that only widen what is accepted:
 """
 from __future__ import annotations
 
+import os
+
+import numpy as np
 import torch
 
 from .. import _native as nat
+
+# KVC_CHECK_APPEND=1: paged_decode_append checks on the host that the decode
+# slots satisfy the fused append's contract before it launches (reads the
+# metadata back, so it synchronises; for debugging, never under capture).
+_CHECK_APPEND = os.environ.get("KVC_CHECK_APPEND", "0") == "1"
 
 
 def set_paged_config(value: str | None) -> None:
@@ -101,6 +109,43 @@ def paged_decode_attention(
     return output
 
 
+def check_append_contract(slot_mapping, block_tables, context_lens, page_size: int,
+                          num_slots: int) -> None:
+    """The decode-slot contract the fused append relies on, checked on the
+    host (AssertionError naming the first offending row):
+    * every row b with context_lens[b] > 0 appends at the slot of its own
+      last position, block_tables[b][(ctx-1) // page] * page + (ctx-1) % page
+      (nanovllm/engine/model_runner.py:685), after the same negative-slot
+      wrap the store applies;
+    * no row reads another row's new slot at a position before its own last
+      one (a row whose last position is that slot replaces it with its own
+      token, as the padded scratch rows of a graph replay do)."""
+    sm = slot_mapping.detach().to("cpu", torch.int64).numpy()
+    bt = block_tables.detach().to("cpu", torch.int64).numpy()
+    cl = context_lens.detach().to("cpu", torch.int64).numpy()
+    sm = np.where(sm < 0, sm + num_slots, sm)
+    live = np.nonzero(cl > 0)[0]
+    for b in live:
+        last = int(cl[b]) - 1
+        blk = int(bt[b, last // page_size])
+        want = blk * page_size + last % page_size
+        assert int(sm[b]) == want, (
+            f"paged_decode_append: row {b} appends at slot {int(sm[b])}, but its last position "
+            f"{last} is slot {want} (block {blk}); use store_kvcache + paged_decode_attention")
+    for b in live:
+        blk, off = divmod(int(sm[b]), page_size)
+        for c in live:
+            if c == b:
+                continue
+            nblk = (int(cl[c]) + page_size - 1) // page_size
+            hits = np.nonzero(bt[c, :nblk] == blk)[0]
+            pos = hits * page_size + off
+            early = pos[pos < int(cl[c]) - 1]
+            assert early.size == 0, (
+                f"paged_decode_append: row {c} reads row {b}'s new slot {int(sm[b])} at "
+                f"position {int(early[0])} before its own last one")
+
+
 def paged_decode_append(q, key, value, k_cache, v_cache, slot_mapping, block_tables,
                         context_lens, scale):
     """The decode step's KV work on a bf16 pool in one call:
@@ -147,6 +192,9 @@ def paged_decode_append(q, key, value, k_cache, v_cache, slot_mapping, block_tab
         output = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     if batch == 0:
         return output
+    if _CHECK_APPEND:
+        check_append_contract(slot_mapping, block_tables, context_lens, page_size,
+                              k_cache.size(0) * page_size)
     max_blocks = block_tables.size(1)
     ws_bytes = nat.query("kvc_paged_decode_workspace_bytes", batch, num_heads, num_kv_heads,
                          head_dim, page_size, max_blocks)

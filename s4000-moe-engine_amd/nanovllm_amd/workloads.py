@@ -124,3 +124,65 @@ def outlier_keys(shape, seed: int, frac: float = 0.01, mult: float = 20.0) -> to
     mask = torch.rand(shape, generator=gen) < frac
     x = torch.where(mask, x * mult, x)
     return x.to(torch.bfloat16)
+
+
+@dataclass
+class Int8DecodeWorkload(DecodeWorkload):
+    raw_k: torch.Tensor | None = None     # [history tokens, KVH, D] bf16 appended before the step
+    raw_v: torch.Tensor | None = None
+    history_slots: torch.Tensor | None = None   # [history tokens] int32, their slots
+
+
+def int8_tokhead_decode_workload(batch: int, num_heads: int, num_kv_heads: int,
+                                 num_blocks: int, context_lens: list[int], seed: int,
+                                 device, page: int = PAGE, outlier_frac: float = 0.01,
+                                 outlier_mult: float = 20.0, keep_raw: bool = False
+                                 ) -> Int8DecodeWorkload:
+    """The per-token-head int8 decode workload: K ~ N(0,1) with a fraction
+    `outlier_frac` of entries scaled by `outlier_mult`, V ~ N(0,1), drawn in
+    bf16 on the device with a seeded generator and appended through the
+    quantiser (kvc_store_int8_tokhead), so the pool holds the codes and
+    scales the append produces.  Positions 0 .. len-2 of every sequence are
+    the history; position len-1 is the step's own append (new_k / new_v,
+    slot_mapping), left to the caller.  keep_raw keeps the history's bf16
+    rows and slots for checking."""
+    from .kernels.kv_int8 import store_kvcache_int8_tokhead
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    bt = build_block_tables(context_lens, num_blocks, page, gen)
+    slots = slots_for_last_token(bt, context_lens, page)
+    q = _randn((batch, num_heads, HEAD_DIM), gen).to(device)
+    dgen = torch.Generator(device=device).manual_seed(seed + 1)
+
+    def draw(n, outliers):
+        x = torch.randn((n, num_kv_heads, HEAD_DIM), generator=dgen, device=device)
+        if outliers:
+            hit = torch.rand(x.shape, generator=dgen, device=device) < outlier_frac
+            x = torch.where(hit, x * outlier_mult, x)
+        return x.to(torch.bfloat16)
+
+    shape = (num_blocks, page, num_kv_heads, HEAD_DIM)
+    k_cache = torch.zeros(shape, dtype=torch.int8, device=device)
+    v_cache = torch.zeros(shape, dtype=torch.int8, device=device)
+    k_scale = torch.ones(shape[:3], dtype=torch.float32, device=device)
+    v_scale = torch.ones(shape[:3], dtype=torch.float32, device=device)
+    # history slots, sequence by sequence
+    hist = []
+    bt_dev = bt.to(device)
+    for i, n in enumerate(context_lens):
+        if n > 1:
+            pos = torch.arange(n - 1, device=device)
+            hist.append((bt_dev[i, pos // page].long() * page + pos % page).to(torch.int32))
+    hslots = torch.cat(hist) if hist else torch.zeros(0, dtype=torch.int32, device=device)
+    raw_k = draw(hslots.numel(), True)
+    raw_v = draw(hslots.numel(), False)
+    if hslots.numel():
+        store_kvcache_int8_tokhead(raw_k, raw_v, k_cache, v_cache, k_scale, v_scale, hslots)
+    new_k = draw(batch, True)
+    new_v = draw(batch, False)
+    if not keep_raw:
+        raw_k = raw_v = hslots = None
+    return Int8DecodeWorkload(
+        q=q, k_cache=k_cache, v_cache=v_cache, block_tables=bt_dev,
+        context_lens=torch.tensor(context_lens, dtype=torch.int32).to(device),
+        slot_mapping=slots.to(device), new_k=new_k, new_v=new_v, scale=HEAD_DIM ** -0.5,
+        k_scale=k_scale, v_scale=v_scale, raw_k=raw_k, raw_v=raw_v, history_slots=hslots)

@@ -15,6 +15,22 @@ def bits(t: torch.Tensor) -> np.ndarray:
     return ko.torch_bf16_bits(t)
 
 
+def half_ulp_bf16(x: np.ndarray) -> np.ndarray:
+    """Half a bf16 ulp at |x|: 2^(floor(log2|x|) - 8) (8 significant bits),
+    the most that rounding a value of that binade to bf16 can move it."""
+    ax = np.abs(np.asarray(x, dtype=np.float64))
+    e = np.floor(np.log2(np.where(ax > 0, ax, 1.0)))
+    return np.where(ax > 0, np.exp2(e - 8.0), 0.0)
+
+
+def attention_bound(ref: np.ndarray, max_abs: float = MAX_ABS) -> np.ndarray:
+    """Per-element max-abs bound: the bare max_abs, plus half a bf16 ulp of
+    the reference only where that half ulp itself exceeds max_abs (|ref| >= 8
+    for 2e-2: the output is bf16, and its rounding alone can cost that much)."""
+    h = half_ulp_bf16(ref)
+    return max_abs + np.where(h > max_abs, h, 0.0)
+
+
 def assert_attention_close(out: torch.Tensor, ref: np.ndarray, label: str,
                            max_abs: float = MAX_ABS, mean_abs: float = MEAN_ABS) -> tuple[float, float]:
     got = out.detach().float().cpu().numpy()
@@ -23,15 +39,17 @@ def assert_attention_close(out: torch.Tensor, ref: np.ndarray, label: str,
     assert np.array_equal(np.isnan(got), nan_ref), f"{label}: NaN pattern differs"
     finite = ~nan_ref
     if not finite.any():
+        print(f"[tol] {label}: every row NaN (as the reference)", flush=True)
         return 0.0, 0.0
     err = np.abs(got[finite] - ref[finite])
-    # The output is bf16: rounding it alone costs up to half a bf16 ulp
-    # (2^-9 relative), which exceeds an absolute 2e-2 once |out| > 10 (the int8
-    # outlier-channel cases).  The max-abs bound therefore carries that term.
-    bound = max_abs + np.abs(ref[finite]) * 2.0 ** -8
+    bound = attention_bound(ref[finite], max_abs)
     worst = float((err - bound).max())
     mx, mn = float(err.max()), float(err.mean())
-    assert worst <= 0.0, f"{label}: max_abs {mx:.3e} exceeds {max_abs} + 2^-8|ref|"
+    widened = int((bound > max_abs).sum())
+    print(f"[tol] {label}: max_abs {mx:.3e} mean_abs {mn:.3e} "
+          f"({widened} of {err.size} elements have |ref| >= 8)", flush=True)
+    assert worst <= 0.0, (f"{label}: max_abs {mx:.3e} exceeds {max_abs} "
+                          f"(+ half a bf16 ulp where that exceeds {max_abs})")
     assert mn <= mean_abs, f"{label}: mean_abs {mn:.3e} > {mean_abs}"
     return mx, mn
 

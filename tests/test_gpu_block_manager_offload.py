@@ -55,3 +55,62 @@ def test_evict_to_host_and_revive_bitwise(groups):
     bm.deallocate(rerun)
     bm.clear_prefix_cache()
     assert runner.kv_offloader.metrics()["kv_offload_slots_in_use"] == 0
+
+
+@pytest.mark.parametrize("groups,engine", [(0, "kernel"), (2, "kernel"), (8, "kernel"),
+                                           (3, "dma")])
+def test_revive_into_the_block_its_own_eviction_frees(groups, engine):
+    """A revive whose fresh block is the LRU victim of the same allocation:
+    _revive_from_host -> _allocate_block evicts hashed block B
+    (offload_put(B)) and then brings the host copy back into B
+    (offload_get(slot, B)).  The put must read B before the get overwrites
+    it: the new slot holds B's old bytes, B holds the revived bytes."""
+    print(f"[bm-offload] revive into the evicted block groups={groups} engine={engine}",
+          flush=True)
+    runner = KVCacheRunner(L, NB, PAGE, KVH, 128, kv_offload_host_blocks=2,
+                           async_offload_groups=groups, async_copy_engine=engine)
+    g = torch.Generator(device="cuda").manual_seed(11)
+    runner.kv_cache.normal_(generator=g)
+    bm = BlockManager(NB, PAGE)
+    bm.set_offload_executor(runner)
+    tok_x = list(range(1000, 1000 + PAGE + 1))
+    donor = Sequence(tok_x)
+    bm.allocate(donor, 0)
+    bm.hash_blocks(donor, len(donor))
+    x_bytes = _u16(runner.kv_cache[:, :, donor.block_table[0]])
+    bm.deallocate(donor)
+    # Y takes every block (X's block goes to host slot 0), writes its KV and
+    # hashes every block: afterwards each free block is a cached LRU block.
+    y = Sequence(list(range(7000, 7000 + NB * PAGE)))
+    bm.allocate(y, 0)
+    assert bm.metrics()["kv_offload_puts_total"] == 1
+    runner.fence()
+    runner.kv_cache.normal_(generator=g)
+    bm.hash_blocks(y, len(y))
+    # deallocated last block first: the LRU order is Y's table reversed
+    victim, second = y.block_table[-1], y.block_table[-2]
+    y_bytes = _u16(runner.kv_cache[:, :, victim])
+    y2_bytes = _u16(runner.kv_cache[:, :, second])
+    bm.deallocate(y)
+    rerun = Sequence(tok_x)
+    cached = bm.can_allocate(rerun)
+    assert cached == 1
+    # block 0: put(victim) -> slot 1, get(slot 0 -> victim), release slot 0;
+    # block 1: put(second) -> slot 0 again, which the get above still reads
+    bm.allocate(rerun, cached)
+    m = bm.metrics()
+    assert m["kv_offload_revives_total"] == 1 and m["kv_offload_puts_total"] == 3
+    assert rerun.block_table == [victim, second]
+    runner.fence()
+    if runner.kv_async is not None:
+        runner.kv_async.wait_host()
+    torch.cuda.synchronize()
+    host = runner.kv_offloader.buffer
+    assert np.array_equal(_u16(host[1]), y_bytes), \
+        "the evicted block's host copy is not its old bytes"
+    assert np.array_equal(_u16(host[0]), y2_bytes), "the reused slot's copy is not block 1's"
+    assert np.array_equal(_u16(runner.kv_cache[:, :, victim]), x_bytes), \
+        "the revived block is not the host copy"
+    bm.deallocate(rerun)
+    bm.clear_prefix_cache()
+    assert runner.kv_offloader.metrics()["kv_offload_slots_in_use"] == 0

@@ -347,3 +347,88 @@ def test_rms_norm_closed_forms():
     y = ko.rms_norm_ref(x, torch.ones(128, dtype=torch.bfloat16), 1e-6).double()
     rms = y.pow(2).mean(-1).sqrt()
     assert torch.all((rms - 1).abs() < 2.0 ** -7)
+
+
+# ---------------------------------------------------------------------------
+# torch restatements timed as the CPU baselines
+# ---------------------------------------------------------------------------
+def _small_pool(seed, blocks=24, page=32, kvh=2):
+    g = torch.Generator().manual_seed(seed)
+    kc = torch.randn(blocks, page, kvh, 128, generator=g).to(torch.bfloat16)
+    vc = torch.randn(blocks, page, kvh, 128, generator=g).to(torch.bfloat16)
+    return g, kc, vc
+
+
+def test_prefill_loop_torch_matches_prefill_reference():
+    g, kc, vc = _small_pool(31)
+    cu_q, cu_k = [0, 5, 5, 37], [0, 40, 41, 100]          # prefixes 35, (empty), 27
+    bt = torch.randperm(24, generator=g)[:12].view(3, 4).to(torch.int32)
+    q = torch.randn(37, 8, 128, generator=g).to(torch.bfloat16)
+    got = ko.prefill_loop_torch(q, None, None, kc, vc, cu_q, cu_k, bt, 0.09)
+    ref = ko.prefill_ref(ko.torch_bf16_bits(q), ko.bf16_to_f32(ko.torch_bf16_bits(kc)),
+                         ko.bf16_to_f32(ko.torch_bf16_bits(vc)), bt.numpy(), cu_q, cu_k, 0.09)
+    assert got.shape == (37, 8, 128)
+    assert np.abs(got.float().numpy() - ref).max() < 2e-2
+    # without block tables: causal over the chunk's own rows
+    kf = torch.randn(37, 2, 128, generator=g).to(torch.bfloat16)
+    vf = torch.randn(37, 2, 128, generator=g).to(torch.bfloat16)
+    got = ko.prefill_loop_torch(q, kf, vf, kc, vc, [0, 5, 37], [0, 5, 37], None, 0.09)
+    ref = ko.prefill_ref(ko.torch_bf16_bits(q), None, None, None, [0, 5, 37], [0, 5, 37], 0.09,
+                         fresh_k=ko.bf16_to_f32(ko.torch_bf16_bits(kf)),
+                         fresh_v=ko.bf16_to_f32(ko.torch_bf16_bits(vf)))
+    assert np.abs(got.float().numpy() - ref).max() < 2e-2
+
+
+def test_mixed_torch_matches_mixed_reference():
+    g, kc, vc = _small_pool(32)
+    bt = torch.randperm(24, generator=g)[:15].view(5, 3).to(torch.int32)
+    dlen = torch.tensor([1, 70, 96], dtype=torch.int32)
+    cu_q, cu_k = [0, 4, 10], [0, 30, 90]
+    q = torch.randn(13, 8, 128, generator=g).to(torch.bfloat16)
+    got = ko.mixed_torch(q, kc, vc, bt, 3, dlen, 96, cu_q, cu_k, 0.09)
+    ref = ko.mixed_ref(ko.torch_bf16_bits(q), ko.bf16_to_f32(ko.torch_bf16_bits(kc)),
+                       ko.bf16_to_f32(ko.torch_bf16_bits(vc)), bt.numpy(), 3, dlen.numpy(),
+                       cu_q, cu_k, 0.09)
+    assert np.abs(got.float().numpy() - ref).max() < 2e-2
+
+
+def test_quant_tokhead_torch_equals_numpy_restatement():
+    g = torch.Generator().manual_seed(33)
+    x = (torch.randn(300, 4, 128, generator=g) * torch.where(
+        torch.rand(300, 4, 128, generator=g) < 0.01, 20.0, 1.0)).to(torch.bfloat16)
+    x[0, 0] = 0.0                                          # the 1e-6 clamp
+    codes, s = ko.quant_tokhead_torch(x)
+    want_c, want_s = ko.quant_tokhead(ko.torch_bf16_bits(x))
+    assert np.array_equal(codes.numpy(), want_c)
+    assert np.array_equal(s.squeeze(-1).numpy().view(np.uint32), want_s.view(np.uint32))
+
+
+def test_int8_tokhead_decode_is_the_bf16_decode_of_the_dequantised_pool():
+    g, kc, vc = _small_pool(34)
+    kq, ks = ko.quant_tokhead_torch(kc)
+    vq, vs = ko.quant_tokhead_torch(vc)
+    bt = torch.randperm(24, generator=g)[:12].view(3, 4).to(torch.int32)
+    lens = torch.tensor([1, 77, 128], dtype=torch.int32)
+    q = torch.randn(3, 8, 128, generator=g).to(torch.bfloat16)
+    got = ko.gather_sdpa_decode_int8_tokhead(q, kq, vq, ks.squeeze(-1), vs.squeeze(-1), bt, lens,
+                                             0.09, 128)
+    kd = ko.bits_to_torch_bf16(ko.dequant_tokhead(kq.numpy(), ks.squeeze(-1).numpy()))
+    vd = ko.bits_to_torch_bf16(ko.dequant_tokhead(vq.numpy(), vs.squeeze(-1).numpy()))
+    want = ko.gather_sdpa_decode(q, kd, vd, bt, lens, 0.09, 128)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+def test_block_moves_torch_match_closed_forms():
+    g = torch.Generator().manual_seed(35)
+    pool = torch.randint(-2**15, 2**15, (2, 3, 10, 4, 2, 8), generator=g, dtype=torch.int16)
+    orig = pool.clone()
+    slot = torch.empty_like(pool[:, :, 0])
+    ko.offload_put_torch(pool, 7, slot)
+    assert torch.equal(slot, orig[:, :, 7])
+    ko.offload_get_torch(pool, slot, 2)
+    assert torch.equal(pool[:, :, 2], orig[:, :, 7])
+    ko.compact_torch(pool, [0, 1, 9], [4, 5, 6])
+    want = orig.numpy().reshape(6, 10, -1).copy()
+    ko.block_scatter(want, [2], ko.block_gather(orig.numpy().reshape(6, 10, -1), [7]))
+    ko.block_copy(want, [0, 1, 9], [4, 5, 6])
+    assert np.array_equal(pool.numpy().reshape(6, 10, -1), want)

@@ -38,3 +38,66 @@ def test_async_offloader_validates_before_the_device():
         AsyncOffloader(pool[:, :, :, :, :, :64], host)   # not contiguous
     with pytest.raises(RuntimeError, match="device"):
         AsyncOffloader(pool, host)
+
+
+def _decode_meta(lens, page=32, width=4, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    ids = torch.randperm(len(lens) * width, generator=g).view(len(lens), width).to(torch.int32)
+    last = torch.tensor(lens) - 1
+    slots = (ids.long().gather(1, (last // page).unsqueeze(1)).squeeze(1) * page + last % page)
+    return slots.to(torch.int32), ids, torch.tensor(lens, dtype=torch.int32)
+
+
+def test_append_contract_accepts_engine_decode_slots():
+    from nanovllm_amd.kernels.paged_attention import check_append_contract
+    sm, bt, cl = _decode_meta([1, 32, 33, 100, 128])
+    check_append_contract(sm, bt, cl, 32, 20 * 32)
+    # int64 slots given as negative (Python-index) forms are the same slots
+    check_append_contract(sm.long() - 20 * 32, bt, cl, 32, 20 * 32)
+    # empty rows append nothing and are not checked
+    cl0 = cl.clone()
+    cl0[1] = 0
+    check_append_contract(sm, bt, cl0, 32, 20 * 32)
+
+
+def test_append_contract_rejects_a_slot_off_the_last_position():
+    from nanovllm_amd.kernels.paged_attention import check_append_contract
+    sm, bt, cl = _decode_meta([40, 64, 90])
+    sm[1] += 1
+    with pytest.raises(AssertionError, match="row 1"):
+        check_append_contract(sm, bt, cl, 32, 20 * 32)
+
+
+def test_append_contract_rejects_a_slot_another_row_reads():
+    from nanovllm_amd.kernels.paged_attention import check_append_contract
+    sm, bt, cl = _decode_meta([40, 64, 90])
+    bt[2, 0] = bt[0, 1]                 # row 2 reads row 0's last block at position 7
+    with pytest.raises(AssertionError, match="row 2 reads row 0"):
+        check_append_contract(sm, bt, cl, 32, 20 * 32)
+
+
+def test_append_contract_allows_padded_rows_sharing_the_scratch_slot():
+    from nanovllm_amd.kernels.paged_attention import check_append_contract
+    sm, bt, cl = _decode_meta([40, 64])
+    scratch = 19
+    pad = torch.full((3, 4), scratch, dtype=torch.int32)
+    bt = torch.cat([bt, pad])
+    sm = torch.cat([sm, torch.full((3,), scratch * 32, dtype=torch.int32)])
+    cl = torch.cat([cl, torch.ones(3, dtype=torch.int32)])
+    check_append_contract(sm, bt, cl, 32, 20 * 32)
+
+
+def test_attention_bound_is_the_bare_bound_below_eight():
+    import numpy as np
+    from helpers import MAX_ABS, attention_bound, half_ulp_bf16
+    x = np.array([0.0, 1.0, 1.99, 4.0, 7.99, 8.0, 15.9, 16.0, -100.0])
+    assert np.array_equal(half_ulp_bf16(x),
+                          [0, 2**-8, 2**-8, 2**-6, 2**-6, 2**-5, 2**-5, 2**-4, 2**-2])
+    b = attention_bound(x)
+    assert np.all(b[:5] == MAX_ABS)
+    assert np.allclose(b[5:], MAX_ABS + half_ulp_bf16(x[5:]))
+    # half an ulp bounds torch's bf16 rounding of every fp32 value of a binade
+    g = torch.Generator().manual_seed(1)
+    v = torch.randn(100000, generator=g) * 50
+    err = (v.to(torch.bfloat16).float() - v).abs().numpy()
+    assert np.all(err <= half_ulp_bf16(v.numpy()))
