@@ -172,6 +172,35 @@ int kvc_paged_decode_append(const void* q, int64_t q_stride_b, int64_t q_stride_
                             int64_t out_stride_b, int64_t out_stride_h, void* workspace,
                             size_t workspace_bytes, kvc_stream_t stream);
 
+/* Bytes of device scratch kvc_paged_decode_append_static holds on each GPU
+ * it runs on: 64 MiB.  At 32 q / 4 kv heads and pages of 256 that covers
+ * batch 32 at any table width, batch 64 with tables of up to 62 pages
+ * (15872 tokens), batch 128 up to 30 pages, batch 256 up to 14 pages. */
+#define KVC_STATIC_SCRATCH_BYTES (64u << 20)
+
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under graph capture that must not allocate, tight serving
+ * loops, harnesses that forbid hipMalloc).  kvc_paged_decode_append with the
+ * split-K workspace taken from a file-scope device array of
+ * KVC_STATIC_SCRATCH_BYTES per GPU (held until the process ends) instead of
+ * a caller buffer; same kernels, results and pool contents.  Allocates
+ * nothing (no hipMalloc, no library allocation); the caller passes inputs
+ * and outputs.  A launch shape whose workspace
+ * (kvc_paged_decode_workspace_bytes) exceeds the scratch returns
+ * KVC_ERR_WORKSPACE before any device work.  Every call on one GPU shares
+ * that GPU's scratch, which keeps the last call's contents: calls that
+ * overlap on one GPU (on different streams or from different threads) race
+ * and must be ordered by the caller, e.g. on one stream.  The scratch is
+ * that of the device `stream` belongs to. */
+int kvc_paged_decode_append_static(
+    const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* key, int64_t key_stride_n,
+    int64_t key_stride_h, const void* value, int64_t value_stride_n, int64_t value_stride_h,
+    const void* slot_mapping, int slot_index_bytes, void* k_cache, void* v_cache,
+    int64_t num_cache_blocks, int64_t page_size, int64_t num_kv_heads, int64_t head_dim,
+    const int32_t* block_tables, int64_t bt_stride, int64_t max_blocks_per_seq,
+    const int32_t* context_lens, int64_t batch, int64_t num_heads, float scale, void* out,
+    int64_t out_stride_b, int64_t out_stride_h, kvc_stream_t stream);
+
 /* ---------------------------------------------------------------------------
  * Mixed decode + chunked-prefill attention in one launch.
  * ------------------------------------------------------------------------- */

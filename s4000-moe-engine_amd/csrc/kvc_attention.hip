@@ -20,8 +20,10 @@
 // exactly one wave, so LDS staging would only add traffic) with the next tile
 // in flight while the current one is computed.  Prefill units stage each K/V
 // tile in LDS once and four waves (different query columns) consume it.
+#include <atomic>
 #include <cmath>
 #include <cstdlib>
+#include <mutex>
 
 #include "kvc_internal.h"
 
@@ -3737,6 +3739,114 @@ extern "C" int kvc_paged_decode_append(
                            nullptr, nullptr, nullptr, nullptr, 0, block_tables, bt_stride,
                            max_blocks_per_seq, context_lens, batch, num_heads, scale, out,
                            out_stride_b, out_stride_h, workspace, workspace_bytes, app, stream);
+}
+
+// ---------------------------------------------------------------------------
+// The decode step without a caller workspace: the split-K partials and split
+// counts live in `scratch`, one array per GPU (each device that loads the
+// library's code object holds its own copy, until the process ends).  Host
+// code never uses the array's name as an address: the first call on a device
+// resolves that device's copy with hipGetSymbolAddress (the device current
+// while it does so) and every later call on it passes the cached pointer.
+// The array needs no clearing: each launch writes every split count and
+// partial its merge reads.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[KVC_STATIC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxScratchDevices];
+std::mutex g_scratch_mu;
+
+// The device `stream` runs on (the current device for the NULL stream).
+int stream_device(hipStream_t stream, int* dev) {
+  hipError_t e = hipGetDevice(dev);
+  KVC_REQUIRE(e == hipSuccess, KVC_ERR_RUNTIME, "paged_decode_append_static: hipGetDevice: %s",
+              hipGetErrorString(e));
+  if (stream != nullptr) {
+    e = hipStreamGetDevice(stream, dev);
+    KVC_REQUIRE(e == hipSuccess, KVC_ERR_RUNTIME,
+                "paged_decode_append_static: hipStreamGetDevice: %s", hipGetErrorString(e));
+  }
+  KVC_REQUIRE(*dev >= 0 && *dev < kMaxScratchDevices, KVC_ERR_RUNTIME,
+              "paged_decode_append_static: device %d out of range", *dev);
+  return KVC_OK;
+}
+
+// Address of device `dev`'s scratch array, resolved once per device.
+int scratch_for_device(int dev, void** ptr) {
+  void* cached = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (cached != nullptr) {
+    *ptr = cached;
+    return KVC_OK;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  cached = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+  if (cached == nullptr) {
+    int prev = 0;
+    hipError_t e = hipGetDevice(&prev);
+    KVC_REQUIRE(e == hipSuccess, KVC_ERR_RUNTIME, "paged_decode_append_static: hipGetDevice: %s",
+                hipGetErrorString(e));
+    if (prev != dev) {
+      e = hipSetDevice(dev);
+      KVC_REQUIRE(e == hipSuccess, KVC_ERR_RUNTIME,
+                  "paged_decode_append_static: hipSetDevice(%d): %s", dev, hipGetErrorString(e));
+    }
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    const hipError_t restore = prev != dev ? hipSetDevice(prev) : hipSuccess;
+    KVC_REQUIRE(e == hipSuccess && p != nullptr, KVC_ERR_RUNTIME,
+                "paged_decode_append_static: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                hipGetErrorString(e));
+    KVC_REQUIRE(restore == hipSuccess, KVC_ERR_RUNTIME,
+                "paged_decode_append_static: hipSetDevice(%d): %s", prev,
+                hipGetErrorString(restore));
+    g_scratch_ptr[dev].store(p, std::memory_order_release);
+    cached = p;
+  }
+  *ptr = cached;
+  return KVC_OK;
+}
+}  // namespace
+
+extern "C" int kvc_paged_decode_append_static(
+    const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* key, int64_t key_stride_n,
+    int64_t key_stride_h, const void* value, int64_t value_stride_n, int64_t value_stride_h,
+    const void* slot_mapping, int slot_index_bytes, void* k_cache, void* v_cache,
+    int64_t num_cache_blocks, int64_t page_size, int64_t num_kv_heads, int64_t head_dim,
+    const int32_t* block_tables, int64_t bt_stride, int64_t max_blocks_per_seq,
+    const int32_t* context_lens, int64_t batch, int64_t num_heads, float scale, void* out,
+    int64_t out_stride_b, int64_t out_stride_h, kvc_stream_t stream) {
+  clear_error();
+  const size_t need = kvc_paged_decode_workspace_bytes(batch, num_heads, num_kv_heads, head_dim,
+                                                       page_size, max_blocks_per_seq);
+  KVC_REQUIRE(need <= size_t(KVC_STATIC_SCRATCH_BYTES), KVC_ERR_WORKSPACE,
+              "paged_decode_append_static: this launch needs %zu bytes of split-K scratch; the "
+              "static scratch holds %zu (batch %lld, %lld heads, %lld-block tables): use "
+              "kvc_paged_decode_append with a workspace",
+              need, size_t(KVC_STATIC_SCRATCH_BYTES), (long long)batch, (long long)num_heads,
+              (long long)max_blocks_per_seq);
+  if (batch == 0) {
+    return kvc_paged_decode_append(q, q_stride_b, q_stride_h, key, key_stride_n, key_stride_h,
+                                   value, value_stride_n, value_stride_h, slot_mapping,
+                                   slot_index_bytes, k_cache, v_cache, num_cache_blocks,
+                                   page_size, num_kv_heads, head_dim, block_tables, bt_stride,
+                                   max_blocks_per_seq, context_lens, batch, num_heads, scale, out,
+                                   out_stride_b, out_stride_h, nullptr, 0, stream);
+  }
+  int dev = 0;
+  int rc = stream_device(as_stream(stream), &dev);
+  if (rc != KVC_OK) return rc;
+  void* ws = nullptr;
+  rc = scratch_for_device(dev, &ws);
+  if (rc != KVC_OK) return rc;
+  return kvc_paged_decode_append(q, q_stride_b, q_stride_h, key, key_stride_n, key_stride_h,
+                                 value, value_stride_n, value_stride_h, slot_mapping,
+                                 slot_index_bytes, k_cache, v_cache, num_cache_blocks, page_size,
+                                 num_kv_heads, head_dim, block_tables, bt_stride,
+                                 max_blocks_per_seq, context_lens, batch, num_heads, scale, out,
+                                 out_stride_b, out_stride_h, ws, size_t(KVC_STATIC_SCRATCH_BYTES),
+                                 stream);
 }
 
 extern "C" size_t kvc_varlen_workspace_bytes(int64_t num_q_tokens, int64_t num_heads,

@@ -21,6 +21,8 @@ LIB_PATH = pathlib.Path(os.environ.get("KVC_LIBRARY", PKG_ROOT / "lib" / "libkvc
 KVC_KV_BF16 = 0
 KVC_KV_INT8_TOKHEAD = 1
 KVC_KV_INT8_CHAN = 2
+# include/kvc.h KVC_STATIC_SCRATCH_BYTES
+STATIC_SCRATCH_BYTES = 64 << 20
 
 _ERRORS = {
     -1: ValueError,
@@ -52,6 +54,10 @@ SIGNATURES = {
     "kvc_paged_decode_append": (_INT, [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _INT,
                                        _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _I64, _P,
                                        _I64, _I64, _F32, _P, _I64, _I64, _P, _SZ, _P]),
+    "kvc_paged_decode_append_static": (_INT, [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,
+                                              _P, _INT, _P, _P, _I64, _I64, _I64, _I64, _P,
+                                              _I64, _I64, _P, _I64, _I64, _F32, _P, _I64, _I64,
+                                              _P]),
     "kvc_varlen_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64]),
     "kvc_varlen_prefill_units": (_I64, [_P, _P, _I64, _I64, _I64, _I64]),
     "kvc_varlen_attention": (_INT, [_P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _I64,

@@ -212,3 +212,53 @@ def paged_decode_append(q, key, value, k_cache, v_cache, slot_mapping, block_tab
         nat.ptr(ws), ws_bytes, nat.stream_of(q),
     )
     return output
+
+
+def paged_decode_append_static(q, key, value, k_cache, v_cache, slot_mapping, block_tables,
+                               context_lens, scale, out):
+    """paged_decode_append for callers that cannot allocate device memory:
+    the split-K workspace is the library's per-GPU static scratch
+    (kvc_paged_decode_append_static) and the output goes to the caller's
+    `out` [batch, heads, 128] bf16.  Nothing is converted or copied, so every
+    argument must already be in the launch's form (int32 tables and lengths,
+    int32 or int64 slots, unit inner strides); ValueError when the launch
+    needs more scratch than the library holds.  Calls that overlap on one GPU
+    share that scratch and must be ordered by the caller."""
+    if q.ndim != 3 or key.ndim != 3 or value.shape != key.shape or k_cache.ndim != 4 \
+            or v_cache.shape != k_cache.shape or out.shape != q.shape:
+        raise ValueError("expected q/out=[batch,heads,dim], key/value=[batch,kv_heads,dim], "
+                         "kv=[pages,page,kv_heads,dim]")
+    batch, num_heads, head_dim = q.shape
+    page_size = k_cache.size(1)
+    num_kv_heads = k_cache.size(2)
+    if head_dim != 128 or page_size % 32 or num_heads % num_kv_heads:
+        raise ValueError(
+            "paged decode requires head_dim=128, page_size a multiple of 32 and "
+            "GQA-divisible heads")
+    if not (q.dtype == key.dtype == value.dtype == k_cache.dtype == out.dtype == torch.bfloat16):
+        raise ValueError("paged_decode_append_static takes a bf16 pool and bf16 q/k/v/out")
+    if block_tables.dtype != torch.int32 or context_lens.dtype != torch.int32:
+        raise ValueError("block_tables and context_lens must be int32 (no conversion here)")
+    if slot_mapping.dtype not in (torch.int32, torch.int64):
+        raise ValueError("slot_mapping must be int32 or int64")
+    assert key.size(0) == batch and key.size(1) == num_kv_heads and slot_mapping.numel() == batch
+    assert q.stride(2) == 1 and out.stride(2) == 1 and key.stride(-1) == 1 \
+        and value.stride(-1) == 1
+    assert block_tables.stride(1) == 1 and context_lens.is_contiguous() \
+        and slot_mapping.is_contiguous()
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise AssertionError("KV pools must be contiguous [pages, page, kv_heads, dim]")
+    nat.require_device(q, key, value, k_cache, v_cache, slot_mapping, block_tables, context_lens,
+                       out)
+    nat.call(
+        "kvc_paged_decode_append_static",
+        q.data_ptr(), q.stride(0), q.stride(1),
+        key.data_ptr(), key.stride(0), key.stride(1),
+        value.data_ptr(), value.stride(0), value.stride(1),
+        slot_mapping.data_ptr(), slot_mapping.element_size(),
+        k_cache.data_ptr(), v_cache.data_ptr(), k_cache.size(0), page_size, num_kv_heads,
+        head_dim, block_tables.data_ptr(), block_tables.stride(0), block_tables.size(1),
+        context_lens.data_ptr(), batch, num_heads, float(scale),
+        out.data_ptr(), out.stride(0), out.stride(1), nat.stream_of(q),
+    )
+    return out
