@@ -77,7 +77,10 @@ def op_tokens(op):
 
 
 def run(ops, manager_cls, sequence_cls, num_blocks=24, block_size=256, host_slots=5,
-        make_seq=None):
+        make_seq=None, log_calls=False):
+    """Execute `ops`; with log_calls every record also carries the executor
+    calls the op made, in order, with their arguments."""
+    logged = 0
     mgr = manager_cls(num_blocks, block_size)
     mgr.lru_enabled = True
     ex = SlotExecutor(host_slots)
@@ -131,5 +134,8 @@ def run(ops, manager_cls, sequence_cls, num_blocks=24, block_size=256, host_slot
         rec["free_head"] = list(mgr.free_block_ids)[:8]
         rec["host_in_use"] = sorted(ex.in_use)
         rec["exec_calls"] = len(ex.log)
+        if log_calls:
+            rec["exec_log"] = ex.log[logged:]
+            logged = len(ex.log)
         records.append(rec)
     return records

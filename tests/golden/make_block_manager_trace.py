@@ -37,15 +37,22 @@ def main():
     sq = load("nanovllm.engine.sequence", "nanovllm/engine/sequence.py")
     bm = load("nanovllm.engine.block_manager", "nanovllm/engine/block_manager.py")
     traces = []
-    for seed in (1, 2, 3):
-        ops = drv.make_ops(seed)
-        recs = drv.run(ops, bm.BlockManager, sq.Sequence,
-                       make_seq=lambda toks: sq.Sequence(toks, sp.SamplingParams(max_tokens=1)))
-        traces.append({"seed": seed, "ops": ops, "records": recs})
+    # (seed, ops, pool blocks, host slots): the first three are the original
+    # 24-block / 5-slot traces; the others squeeze the pool and the host
+    # slots (more drops and revive-into-evicted-block cases) or widen them.
+    for seed, n_ops, blocks, slots in ((1, 400, 24, 5), (2, 400, 24, 5), (3, 400, 24, 5),
+                                       (4, 600, 12, 2), (5, 600, 40, 10), (6, 800, 16, 3)):
+        ops = drv.make_ops(seed, n_ops=n_ops)
+        recs = drv.run(ops, bm.BlockManager, sq.Sequence, num_blocks=blocks, host_slots=slots,
+                       make_seq=lambda toks: sq.Sequence(toks, sp.SamplingParams(max_tokens=1)),
+                       log_calls=True)
+        traces.append({"seed": seed, "num_blocks": blocks, "host_slots": slots, "ops": ops,
+                       "records": recs})
     out = os.path.join(HERE, "block_manager_trace.json.gz")
     with gzip.open(out, "wt") as f:
-        json.dump({"source": "nanovllm/engine/block_manager.py (reference), 24 blocks x 256, "
-                             "5 host slots", "traces": traces}, f, separators=(",", ":"))
+        json.dump({"source": "nanovllm/engine/block_manager.py (reference), pages of 256; "
+                             "each record holds the op's executor calls",
+                   "traces": traces}, f, separators=(",", ":"))
     print(out, os.path.getsize(out), "bytes")
 
 

@@ -1,8 +1,10 @@
 """BlockManager against golden traces recorded from the reference
 implementation (tests/golden/make_block_manager_trace.py): seeded random
 allocate / append / preempt / free / probe / clear / LRU-toggle sequences on
-a 24-block pool with a 5-slot host offload executor.  Every op's return
-values, block tables, metrics, free-list head and host slots must match."""
+pools of 12 to 40 blocks with 2 to 10 host offload slots.  Every op's return
+values, block tables, metrics, free-list head, host slots in use and the
+executor calls it made (put / get / release, with arguments, in order) must
+match."""
 import gzip
 import json
 import os
@@ -21,9 +23,12 @@ with gzip.open(os.path.join(HERE, "golden", "block_manager_trace.json.gz"), "rt"
     TRACES = json.load(f)["traces"]
 
 
-@pytest.mark.parametrize("trace", TRACES, ids=[f"seed{t['seed']}" for t in TRACES])
+@pytest.mark.parametrize("trace", TRACES,
+                         ids=[f"seed{t['seed']}-{t['num_blocks']}blk-{t['host_slots']}slots"
+                              for t in TRACES])
 def test_replay_matches_reference_trace(trace):
-    got = drv.run(trace["ops"], BlockManager, Sequence)
+    got = drv.run(trace["ops"], BlockManager, Sequence, num_blocks=trace["num_blocks"],
+                  host_slots=trace["host_slots"], log_calls=True)
     assert len(got) == len(trace["records"])
     for i, (g, want) in enumerate(zip(got, trace["records"])):
         assert g == want, f"op {i} ({trace['ops'][i]['op']}): {g} != {want}"

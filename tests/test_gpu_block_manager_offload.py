@@ -114,3 +114,96 @@ def test_revive_into_the_block_its_own_eviction_frees(groups, engine):
     bm.deallocate(rerun)
     bm.clear_prefix_cache()
     assert runner.kv_offloader.metrics()["kv_offload_slots_in_use"] == 0
+
+
+def _trace(seed):
+    import gzip
+    import json
+    import os
+    path = os.path.join(os.path.dirname(__file__), "golden", "block_manager_trace.json.gz")
+    with gzip.open(path, "rt") as f:
+        return next(t for t in json.load(f)["traces"] if t["seed"] == seed)
+
+
+@pytest.mark.parametrize("seed", [1, 4, 6])
+@pytest.mark.parametrize("groups", [0, 4])
+def test_replay_reference_executor_logs_bitwise(seed, groups):
+    """The offload_put / offload_get / offload_release calls the reference's
+    BlockManager made on a recorded trace, replayed in order against the GPU
+    runner.  Between ops the blocks the op reused and did not revive are
+    overwritten on the compute stream (the next prefill's KV).  Every slot
+    number must be the reference executor's, and the bytes of every host slot
+    and device block must follow the calls: put copies a block to its slot,
+    get copies a slot back."""
+    tr = _trace(seed)
+    nb, slots = tr["num_blocks"], tr["host_slots"]
+    print(f"[bm-offload] replay seed={seed} blocks={nb} slots={slots} groups={groups}",
+          flush=True)
+    Lr = 2
+    runner = KVCacheRunner(Lr, nb, PAGE, KVH, 128, kv_offload_host_blocks=slots,
+                           async_offload_groups=groups)
+    planes = torch.arange(2 * Lr, device="cuda", dtype=torch.int32).view(2, Lr, 1, 1, 1)
+
+    def write(b, tag):
+        # every plane of block b: (tag * 8 + plane) in each 16-bit element
+        val = ((tag * 8 + planes) & 0x7FFF).to(torch.int16)
+        runner.kv_cache.view(torch.int16)[:, :, b] = val.expand(2, Lr, PAGE, KVH, 128)
+
+    dev_tag = {b: b + 1 for b in range(nb)}
+    runner.fence()
+    for b, t in dev_tag.items():
+        write(b, t)
+    slot_tag = {}
+    next_tag = nb + 1
+    calls = 0
+
+    def expected(tag):
+        return ((tag * 8 + torch.arange(2 * Lr, dtype=torch.int32).view(2, Lr, 1, 1, 1))
+                & 0x7FFF).to(torch.int16).expand(2, Lr, PAGE, KVH, 128)
+
+    def check():
+        runner.fence()
+        if runner.kv_async is not None:
+            runner.kv_async.wait_host()
+        torch.cuda.synchronize()
+        pool = runner.kv_cache.view(torch.int16).cpu()
+        for b, t in dev_tag.items():
+            assert torch.equal(pool[:, :, b], expected(t)), f"block {b} after {calls} calls"
+        host = runner.kv_offloader.buffer.view(torch.int16)
+        for s_, t in slot_tag.items():
+            assert torch.equal(host[s_], expected(t)), f"slot {s_} after {calls} calls"
+
+    for i, rec in enumerate(tr["records"]):
+        reused = []
+        for call in rec["exec_log"]:
+            name = call[0]
+            calls += 1
+            if name == "offload_put":
+                b = call[1]
+                got = runner.call("offload_put", b)
+                reused.append(b)
+                if got != -1:
+                    slot_tag[got] = dev_tag[b]
+            elif name == "offload_get":
+                s, b = call[1], call[2]
+                runner.call("offload_get", s, b)
+                dev_tag[b] = slot_tag[s]
+                if b in reused:
+                    reused.remove(b)
+            else:
+                s = call[1]
+                runner.call("offload_release", s)
+                del slot_tag[s]
+        # the slot numbers are the reference executor's (both hand them out LIFO)
+        assert sorted(slot_tag) == rec["host_in_use"], f"op {i}: host slots in use"
+        if reused:
+            runner.fence()
+            for b in reused:
+                assert next_tag < 4000          # tags stay distinct in 15 bits
+                dev_tag[b] = next_tag
+                write(b, next_tag)
+                next_tag += 1
+        if i % 100 == 99:
+            check()
+    check()
+    assert calls == sum(len(r["exec_log"]) for r in tr["records"]) > 0
