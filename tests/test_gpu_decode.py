@@ -22,6 +22,17 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
+@pytest.fixture(params=["stream-k-lds", "fixed-chunk", "register"])
+def decode_path(request, monkeypatch):
+    """Every decode launch form: the stream-K launch with LDS-staged segments
+    (the default), the fixed-chunk launch of one workgroup per (row, chunk)
+    (KVC_DECODE_STREAMK=0), and the stream-K launch with register segments
+    for every grouping (KVC_DECODE_LDS=0)."""
+    monkeypatch.setenv("KVC_DECODE_STREAMK", "0" if request.param == "fixed-chunk" else "1")
+    monkeypatch.setenv("KVC_DECODE_LDS", "0" if request.param == "register" else "1")
+    return request.param
+
+
 def _check(q, k_cache, v_cache, block_tables, lens, scale, label):
     print(f"[decode] {label}: B={q.shape[0]} H={q.shape[1]} KVH={k_cache.shape[2]} "
           f"max_ctx={int(lens.max()) if lens.numel() else 0}", flush=True)
@@ -35,7 +46,7 @@ def _check(q, k_cache, v_cache, block_tables, lens, scale, label):
     return assert_attention_close(out, ref, label)
 
 
-def test_small_poison_tail():
+def test_small_poison_tail(decode_path):
     torch.manual_seed(20261026)
     page = 256
     lengths = torch.tensor([127, 256, 385, 512], dtype=torch.int32, device=DEV)
@@ -53,7 +64,7 @@ def test_small_poison_tail():
     assert out_max <= 2e-2
 
 
-def test_page_boundary_matrix():
+def test_page_boundary_matrix(decode_path):
     torch.manual_seed(20261027)
     lengths_cpu = [255, 256, 257, 511, 512, 513, 2047, 2048, 2049]
     page = 256
@@ -79,7 +90,7 @@ def test_page_boundary_matrix():
 
 
 @pytest.mark.parametrize("heads,kv_heads", [(16, 8), (32, 4), (32, 32), (32, 2), (64, 2), (12, 4)])
-def test_gqa_groupings(heads, kv_heads):
+def test_gqa_groupings(heads, kv_heads, decode_path):
     lens = uniform_lengths(6, 1, 1500, seed=heads * 100 + kv_heads)
     wl = decode_workload(6, heads, kv_heads, 48, lens, seed=7, device=DEV)
     _check(wl.q, wl.k_cache, wl.v_cache, wl.block_tables, wl.context_lens, wl.scale,
@@ -95,20 +106,20 @@ def test_qwen3_06b_shape_after_append():
     _check(wl.q, wl.k_cache, wl.v_cache, wl.block_tables, wl.context_lens, wl.scale, "0.6B-step")
 
 
-def test_long_context_split_k():
+def test_long_context_split_k(decode_path):
     lens = [32768, 20000, 4097, 1]
     wl = decode_workload(4, 32, 4, 256, lens, seed=9, device=DEV)
     _check(wl.q, wl.k_cache, wl.v_cache, wl.block_tables, wl.context_lens, wl.scale, "long-split-k")
 
 
-def test_zero_length_context_gives_nan_row():
+def test_zero_length_context_gives_nan_row(decode_path):
     lens = [0, 300]
     wl = decode_workload(2, 32, 4, 8, [1, 300], seed=3, device=DEV)
     wl.context_lens = torch.tensor(lens, dtype=torch.int32, device=DEV)
     _check(wl.q, wl.k_cache, wl.v_cache, wl.block_tables, wl.context_lens, wl.scale, "zero-ctx")
 
 
-def test_full_30b_decode_shape_batch64():
+def test_full_30b_decode_shape_batch64(decode_path):
     # 32 q / 4 kv heads, batch 64, ctx U[512, 4096], non-contiguous tables over
     # an 8192-block pool, one appended token per sequence.
     lens = uniform_lengths(64, 512, 4096, seed=2)
@@ -152,7 +163,7 @@ def test_shape_errors_match_reference():
 
 
 @pytest.mark.parametrize("page", [32, 64, 128])
-def test_pages_smaller_than_256(page):
+def test_pages_smaller_than_256(page, decode_path):
     lens = [1, page - 1, page, page + 1, 5 * page + 3, 4000]
     blocks = sum((n + page - 1) // page for n in lens) + 4
     wl = decode_workload(len(lens), 32, 4, blocks, lens, seed=page, device=DEV, page=page)
@@ -162,7 +173,7 @@ def test_pages_smaller_than_256(page):
 
 @pytest.mark.parametrize("case", ["b64x4096", "ragged-with-empty", "int64-negative-slots",
                                   "unaligned-key-fallback", "two-kv-heads-fallback"])
-def test_decode_append_equals_store_then_decode(case):
+def test_decode_append_equals_store_then_decode(case, decode_path):
     """paged_decode_append (the store inside the decode launch where the
     layout allows) against store_kvcache then paged_decode_attention: the
     same output bits and the same pool bytes."""

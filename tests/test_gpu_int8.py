@@ -19,6 +19,17 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
+@pytest.fixture(params=["stream-k-lds", "fixed-chunk", "register"])
+def decode_path(request, monkeypatch):
+    """The int8 decode launch forms: stream-K with the LDS int8 segment (the
+    default for 4 kv heads per workgroup), the fixed-chunk launch
+    (KVC_DECODE_STREAMK=0) and stream-K with register segments
+    (KVC_DECODE_LDS=0)."""
+    monkeypatch.setenv("KVC_DECODE_STREAMK", "0" if request.param == "fixed-chunk" else "1")
+    monkeypatch.setenv("KVC_DECODE_LDS", "0" if request.param == "register" else "1")
+    return request.param
+
+
 def _tokhead_store(key, value, blocks, label, slots=None):
     N, KVH, D = key.shape
     print(f"[int8-tokhead] {label}: N={N} KVH={KVH}", flush=True)
@@ -160,15 +171,15 @@ def _decode_int8_tokhead_case(batch, lens, blocks, seed, label):
     assert_attention_close(out, ref, label)
 
 
-def test_int8_tokhead_decode_small():
+def test_int8_tokhead_decode_small(decode_path):
     _decode_int8_tokhead_case(6, uniform_lengths(6, 1, 3000, seed=4), 80, 5, "tokhead-small")
 
 
-def test_int8_tokhead_decode_long_context():
+def test_int8_tokhead_decode_long_context(decode_path):
     _decode_int8_tokhead_case(2, [32768, 12345], 200, 6, "tokhead-32k")
 
 
-def test_int8_tokhead_end_to_end_quantised_decode():
+def test_int8_tokhead_end_to_end_quantised_decode(decode_path):
     # Append real activations through the quantiser, then decode the int8 pool.
     B, H, KVH, D, blocks = 4, 32, 4, 128, 24
     lens = [700, 1, 1500, 256]
@@ -198,7 +209,7 @@ def test_int8_tokhead_end_to_end_quantised_decode():
     assert_attention_close(out, ref, "tokhead-e2e")
 
 
-def test_int8_chan_decode_with_side_pool():
+def test_int8_chan_decode_with_side_pool(decode_path):
     key, value, s_k, s_v, ds_k, ds_v, out_idx2d, head_n_out = p17_unit_inputs()
     N, KVH, D = key.shape   # 512 tokens, 8 kv heads
     H = 16

@@ -20,14 +20,17 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-@pytest.fixture(params=["prefill-sk", "units", "stream-k"])
+@pytest.fixture(params=["prefill-sk", "units", "stream-k", "combined"])
 def partition(request, monkeypatch):
     """Every launch partition: prefill rows over bf16 keys as one stream-K
     prefill launch (the default), one workgroup per prefill unit
-    (KVC_PREFILL_SK=0), and the single stream-K launch of decode and prefill
-    items together (KVC_MIXED_STREAMK=1)."""
+    (KVC_PREFILL_SK=0), the single stream-K launch of decode and prefill
+    items together (KVC_MIXED_STREAMK=1), and the single unit launch of
+    decode and prefill units together (KVC_MIXED_SPLIT=0; without decode
+    rows it is the default launch)."""
     monkeypatch.setenv("KVC_MIXED_STREAMK", "1" if request.param == "stream-k" else "0")
     monkeypatch.setenv("KVC_PREFILL_SK", "0" if request.param == "units" else "1")
+    monkeypatch.setenv("KVC_MIXED_SPLIT", "0" if request.param == "combined" else "1")
     return request.param
 
 
