@@ -111,6 +111,35 @@ int kvc_store_int8_chan(const void* key, int64_t key_stride_n, int64_t key_strid
                         int64_t num_tokens, int64_t num_kv_heads, int64_t head_dim,
                         kvc_stream_t stream);
 
+/* Calibration statistics of the per-channel encoding: the forward pre-hook
+ * of ModelRunner.kv_calibrate_begin (nanovllm/engine/model_runner.py:510-539)
+ * run over one observed forward's key/value rows [num_tokens, KVH, 128]
+ * (bf16, own element strides):
+ *   amax[s][h][d]    = max(amax[s][h][d], max_n |x_s[n][h][d]|)
+ *   abs_sum[s][h][d] += sum_n |x_s[n][h][d]|          (fp32)
+ * for s = 0 (key) and 1 (value); amax and abs_sum are fp32 [2, KVH, 128],
+ * zeroed by the caller before the first call.  Sums are accumulated in a
+ * fixed order (no atomics).  The caller counts the tokens. */
+int kvc_kv_calib_observe(const void* key, int64_t key_stride_n, int64_t key_stride_h,
+                         const void* value, int64_t value_stride_n, int64_t value_stride_h,
+                         int64_t num_tokens, int64_t num_kv_heads, int64_t head_dim,
+                         float* amax, float* abs_sum, kvc_stream_t stream);
+
+/* Freeze of one layer's statistics over `count` observed tokens
+ * (ModelRunner.kv_calibrate_freeze, model_runner.py:541-577):
+ *   scale  = max(amax / 127, 1e-6)                   -> k_scale / v_scale [KVH, 128]
+ *   typ    = max(abs_sum / count, 1e-6)
+ *   ratio  = max(amax_k / typ_k, amax_v / typ_v)     (K and V jointly)
+ *   outlier dims of head h: its first n_out_max dims, in index order, with
+ *   ratio > 10 -> out_idx2d[h][0 .. head_n_out[h]) (entries past head_n_out
+ *   are left as they are)
+ *   read scales k_dscale / v_dscale = scale, 0 at the outlier dims.
+ * KVC_ERR_ASSERT when count is 0 (the reference asserts). */
+int kvc_kv_calib_freeze(const float* amax, const float* abs_sum, int64_t count,
+                        int64_t num_kv_heads, int64_t head_dim, int64_t n_out_max,
+                        float* k_scale, float* v_scale, float* k_dscale, float* v_dscale,
+                        int32_t* out_idx2d, int32_t* head_n_out, kvc_stream_t stream);
+
 /* ---------------------------------------------------------------------------
  * Paged decode attention.
  * ------------------------------------------------------------------------- */

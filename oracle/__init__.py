@@ -25,6 +25,13 @@ How each function is pinned (checked in tests/test_oracle.py):
                            exact; the seeded tests/p17_kv_int8.py unit case.
   dequant_*                closed form code * scale with bf16 RNE (checked
                            against torch's bf16 cast).
+  calib_stats / calib_freeze
+                           the calibration of tests/p17_kv_int8.py:80-101
+                           (restated in tests/helpers.p17_unit_inputs) on its
+                           seeded unit case, bit for bit; known answers at
+                           the ratio threshold (10 is not an outlier, the
+                           first n_out_max dims in index order win), the
+                           1e-6 clamps, statistics split over forwards.
   paged_decode_ref         float64 torch scaled_dot_product_attention; closed
                            forms (one key -> V row; identical keys -> mean of
                            V); a NaN-poisoned tail never read; the reference

@@ -137,6 +137,41 @@ def dequant_tokhead(codes: np.ndarray, scale: np.ndarray) -> np.ndarray:
     return f32_to_bf16(codes.astype(np.float32) * scale.astype(np.float32)[..., None])
 
 
+def calib_stats(x_bits: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """The calibration hook's per-channel statistics of one forward's rows
+    (nanovllm/engine/model_runner.py:522-532): x_bits [N, KVH, D] bf16 bits ->
+    (amax of |x| over tokens, sum of |x| over tokens), fp32 [KVH, D]."""
+    a = np.abs(bf16_to_f32(x_bits))
+    return a.max(axis=0), a.sum(axis=0, dtype=np.float32)
+
+
+def calib_freeze(amax_k, amax_v, sum_k, sum_v, count: int, n_out_max: int):
+    """ModelRunner.kv_calibrate_freeze (model_runner.py:541-577) for one
+    layer: scale = max(amax / 127, 1e-6); typ = max(sum / count, 1e-6);
+    ratio = max(amax_k / typ_k, amax_v / typ_v); a head's outlier dims are
+    its first n_out_max dims (index order) with ratio > 10; read scales are
+    the scales with 0 at those dims.  All fp32.  Returns
+    (s_k, s_v, ds_k, ds_v, out_idx2d [KVH, n_out_max] int32 (0 past
+    head_n_out), head_n_out [KVH] int32)."""
+    f = np.float32
+    s_k = np.maximum((amax_k / f(127.0)).astype(f), f(1e-6))
+    s_v = np.maximum((amax_v / f(127.0)).astype(f), f(1e-6))
+    typ_k = np.maximum((sum_k / f(count)).astype(f), f(1e-6))
+    typ_v = np.maximum((sum_v / f(count)).astype(f), f(1e-6))
+    ratio = np.maximum((amax_k / typ_k).astype(f), (amax_v / typ_v).astype(f))
+    kvh = amax_k.shape[0]
+    out_idx2d = np.zeros((kvh, n_out_max), dtype=np.int32)
+    head_n_out = np.zeros(kvh, dtype=np.int32)
+    ds_k, ds_v = s_k.copy(), s_v.copy()
+    for h in range(kvh):
+        dims = np.nonzero(ratio[h] > f(10.0))[0][:n_out_max]
+        out_idx2d[h, :dims.size] = dims
+        head_n_out[h] = dims.size
+        ds_k[h, dims] = 0.0
+        ds_v[h, dims] = 0.0
+    return s_k, s_v, ds_k, ds_v, out_idx2d, head_n_out
+
+
 # ---------------------------------------------------------------------------
 # P2 — attention references (fp32)
 # ---------------------------------------------------------------------------

@@ -47,6 +47,9 @@ SIGNATURES = {
                                       _P, _INT, _I64, _I64, _I64, _P]),
     "kvc_store_int8_chan": (_INT, [_P, _I64, _I64, _P, _I64, _I64, _P, _P, _P, _P, _P, _P,
                                    _I64, _P, _P, _I64, _P, _INT, _I64, _I64, _I64, _P]),
+    "kvc_kv_calib_observe": (_INT, [_P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P, _P,
+                                    _P]),
+    "kvc_kv_calib_freeze": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P]),
     "kvc_paged_decode_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64]),
     "kvc_paged_decode": (_INT, [_P, _I64, _I64, _P, _P, _I64, _I64, _I64, _I64, _INT,
                                 _P, _P, _P, _P, _P, _P, _I64, _P, _I64, _I64, _P, _I64,

@@ -234,6 +234,7 @@ class KVCacheRunner:
         self.async_offload_groups = async_offload_groups
         self.async_copy_engine = async_copy_engine
         self.kv_async = None
+        self._calib = None     # (amax [L, 2, KVH, D], abs_sum, token counts) while calibrating
 
     def bind(self, modules) -> int:
         """Hand per-layer views to every module that has k_cache/v_cache
@@ -259,8 +260,54 @@ class KVCacheRunner:
             m.kv_cache_is_int8 = self.kv_int8 is not None
             m.kv_layer = layer
             m.kv_fence = self._fence_layer if self.async_offload else None
+            m.kv_observe = self._observe if self.kv_int8 == "chan" else None
             layer += 1
         return layer
+
+    # -- per-channel int8 calibration (model_runner.py:510-577) ---------------
+    def kv_calibrate_begin(self) -> None:
+        """Start collecting per-channel |K| / |V| statistics in every bound
+        layer's forwards (running max and running sum over all calibration
+        tokens, on the device)."""
+        if self.kv_int8 != "chan":
+            raise ValueError("calibration is for the per-channel int8 pool (kv_int8='chan')")
+        _, L, _, _, KVH, D = self.kv_cache.shape
+        amax = torch.zeros(L, 2, KVH, D, dtype=torch.float32, device=self.device)
+        self._calib = (amax, torch.zeros_like(amax), [0] * L)
+
+    def _observe(self, layer: int, k: torch.Tensor, v: torch.Tensor) -> None:
+        if self._calib is None:
+            return
+        from ..kernels.kv_int8 import kv_calib_observe
+        amax, abs_sum, counts = self._calib
+        KVH, D = self.kv_cache.shape[-2:]
+        k3, v3 = k.view(-1, KVH, D), v.view(-1, KVH, D)
+        kv_calib_observe(k3, v3, amax[layer], abs_sum[layer])
+        counts[layer] += k3.size(0)
+
+    def kv_calibrate_freeze(self) -> dict:
+        """Freeze the statistics into store scales (amax / 127), read scales
+        (0 at outlier dims), out_idx2d and head_n_out (K/V joint ratio
+        amax / mean|x| > 10, at most n_out_max dims per head), on the device;
+        returns the reference's summary (outlier dims, scale range)."""
+        from ..kernels.kv_int8 import kv_calib_freeze
+        if self._calib is None:
+            raise RuntimeError("kv_calibrate_freeze without kv_calibrate_begin")
+        amax, abs_sum, counts = self._calib
+        self._calib = None
+        for layer, n in enumerate(counts):
+            assert n > 0, "calibration saw no activations"
+            kv_calib_freeze(amax[layer], abs_sum[layer], n, self.kv_scales[0, layer],
+                            self.kv_scales[1, layer], self.kv_dscales[0, layer],
+                            self.kv_dscales[1, layer], self.kv_out_idx2d[layer],
+                            self.kv_head_n_out[layer])
+        summary = {"outlier_dims": int(self.kv_head_n_out.sum()),
+                   "scale_min": float(self.kv_scales.min()),
+                   "scale_max": float(self.kv_scales.max())}
+        print(f"[kv-int8] mixed-precision scales frozen (bf16 outlier dims: "
+              f"{summary['outlier_dims']}, scale range [{summary['scale_min']:.4g}, "
+              f"{summary['scale_max']:.4g}])", flush=True)
+        return summary
 
     # -- executor protocol (BlockManager -> runner) ------------------------
     def call(self, method: str, *args):

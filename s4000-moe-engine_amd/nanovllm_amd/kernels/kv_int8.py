@@ -128,3 +128,44 @@ def dequant_tokhead(kv_i8, scale):
     nat.call("kvc_dequant_tokhead", kv_i8.data_ptr(), scale.data_ptr(), T, KVH, D,
              out.data_ptr(), nat.stream_of(kv_i8))
     return out
+
+
+def kv_calib_observe(key, value, amax, abs_sum):
+    """Fold one forward's key/value rows [N, KVH, 128] (bf16, views fine)
+    into a layer's per-channel statistics: amax [2, KVH, 128] fp32 (running
+    max of |x|) and abs_sum (running sum of |x|), K in [0], V in [1]."""
+    if key.ndim != 3 or value.shape != key.shape:
+        raise ValueError("expected key/value [tokens, kv_heads, dim]")
+    N, KVH, D = key.shape
+    if key.dtype != torch.bfloat16 or value.dtype != torch.bfloat16:
+        raise ValueError("calibration observes bf16 key/value")
+    assert key.stride(2) == 1 and value.stride(2) == 1
+    assert amax.shape == (2, KVH, D) and abs_sum.shape == (2, KVH, D)
+    assert amax.dtype == abs_sum.dtype == torch.float32
+    assert amax.is_contiguous() and abs_sum.is_contiguous()
+    nat.require_device(key, value, amax, abs_sum)
+    nat.call("kvc_kv_calib_observe", key.data_ptr(), key.stride(0), key.stride(1),
+             value.data_ptr(), value.stride(0), value.stride(1), N, KVH, D, amax.data_ptr(),
+             abs_sum.data_ptr(), nat.stream_of(key))
+
+
+def kv_calib_freeze(amax, abs_sum, count, k_scale, v_scale, k_dscale, v_dscale, out_idx2d,
+                    head_n_out):
+    """Freeze one layer's statistics over `count` tokens into store scales,
+    read scales (0 at outlier dims) and the per-head outlier dims (ratio
+    amax / mean|x| > 10 for K or V, the first out_idx2d.size(-1) of them per
+    head), all in place, on the device."""
+    KVH, D = k_scale.shape
+    n_out_max = out_idx2d.size(-1)
+    for t in (k_scale, v_scale, k_dscale, v_dscale):
+        assert t.shape == (KVH, D) and t.dtype == torch.float32 and t.is_contiguous()
+    assert out_idx2d.shape == (KVH, n_out_max) and out_idx2d.dtype == torch.int32
+    assert head_n_out.shape == (KVH,) and head_n_out.dtype == torch.int32
+    assert out_idx2d.is_contiguous() and head_n_out.is_contiguous()
+    assert amax.shape == abs_sum.shape == (2, KVH, D)
+    nat.require_device(amax, abs_sum, k_scale, v_scale, k_dscale, v_dscale, out_idx2d,
+                       head_n_out)
+    nat.call("kvc_kv_calib_freeze", amax.data_ptr(), abs_sum.data_ptr(), int(count), KVH, D,
+             n_out_max, k_scale.data_ptr(), v_scale.data_ptr(), k_dscale.data_ptr(),
+             v_dscale.data_ptr(), out_idx2d.data_ptr(), head_n_out.data_ptr(),
+             nat.stream_of(amax))

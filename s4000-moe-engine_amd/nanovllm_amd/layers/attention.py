@@ -86,6 +86,10 @@ class Attention(nn.Module):
         # kv_layer before this layer first touches its pool planes in a step.
         self.kv_fence = None
         self.kv_layer = -1
+        # Set by a runner with a per-channel int8 pool: called with
+        # (kv_layer, k, v) on every forward; it records calibration
+        # statistics between kv_calibrate_begin and kv_calibrate_freeze.
+        self.kv_observe = None
 
     def _profile(self, name):
         if self.profiler is None:
@@ -138,6 +142,8 @@ class Attention(nn.Module):
         context = get_context()
         if self.kv_fence is not None and not kv_stored:
             self.kv_fence(self.kv_layer)
+        if self.kv_observe is not None:
+            self.kv_observe(self.kv_layer, k, v)
         k_cache, v_cache = self.k_cache, self.v_cache
         if k_cache.numel() and self.block_size is None:
             self.block_size = k_cache.size(1)

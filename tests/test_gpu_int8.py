@@ -242,3 +242,58 @@ def test_int8_chan_decode_with_side_pool(decode_path):
                      head_n_out.numpy())
     ref = ko.paged_decode_ref(bits(q), kf, vf, bt.numpy(), np.asarray(lens), D ** -0.5)
     assert_attention_close(out, ref, "chan-side")
+
+
+def test_chan_calibration_on_device_matches_p17_unit_case():
+    """KVCacheRunner.kv_calibrate_begin / the bound layer's kv_observe hook /
+    kv_calibrate_freeze (model_runner.py:510-577) on the seeded unit case of
+    tests/p17_kv_int8.py:64-101, observed as three forwards of 200, 300 and
+    12 tokens: store scales, read scales, out_idx2d and head_n_out equal the
+    unit case's calibration bit for bit; the append with the frozen scales is
+    the oracle's, and dequantisation is within 3 % (p17_kv_int8.py:126-134)."""
+    from nanovllm_amd.engine.kv_runner import KVCacheRunner
+    from nanovllm_amd.layers.attention import Attention
+    key, value, s_k, s_v, ds_k, ds_v, out_idx2d, head_n_out = p17_unit_inputs()
+    N, KVH, D = key.shape
+    n_out = out_idx2d.shape[1]
+    print(f"[int8-calib] p17 unit case N={N} KVH={KVH} n_out_max={n_out}", flush=True)
+    runner = KVCacheRunner(1, 8, 256, KVH, D, kv_int8="chan", n_out_max=n_out)
+    mod = Attention(16, D, D ** -0.5, KVH)
+    assert runner.bind([mod]) == 1 and mod.kv_observe is not None
+    mod.kv_observe(0, key.to(DEV), value.to(DEV))          # before begin: ignored
+    runner.kv_calibrate_begin()
+    kd, vd = key.to(DEV), value.to(DEV)
+    for a, b in ((0, 200), (200, 500), (500, 512)):
+        mod.kv_observe(0, kd[a:b], vd[a:b])
+    summary = runner.kv_calibrate_freeze()
+    assert summary["outlier_dims"] == int(head_n_out.sum())
+    u32 = lambda t: t.cpu().contiguous().view(torch.int32).numpy()
+    for got, want, name in ((runner.kv_scales[0, 0], s_k, "k_scale"),
+                            (runner.kv_scales[1, 0], s_v, "v_scale"),
+                            (runner.kv_dscales[0, 0], ds_k, "k_dscale"),
+                            (runner.kv_dscales[1, 0], ds_v, "v_dscale")):
+        assert np.array_equal(u32(got), u32(want)), name
+    assert torch.equal(runner.kv_head_n_out[0].cpu(), head_n_out)
+    for h in range(KVH):
+        n_h = int(head_n_out[h])
+        assert torch.equal(runner.kv_out_idx2d[0, h, :n_h].cpu(), out_idx2d[h, :n_h])
+    # append with the frozen scales through the bound views, against the oracle
+    runner.kv_cache.zero_()           # the runner's pool starts uninitialised
+    slot = torch.arange(N, dtype=torch.int32, device=DEV)
+    store_kvcache_int8(kd, vd, mod.k_cache, mod.v_cache, mod.k_scale, mod.v_scale, mod.side_k,
+                       mod.side_v, mod.out_idx2d, mod.head_n_out, slot)
+    torch.cuda.synchronize()
+    kc = np.zeros((9, 256, KVH, D), np.int8)
+    vc = np.zeros_like(kc)
+    sdk = np.zeros((9, 256, KVH, n_out), np.uint16)
+    sdv = np.zeros_like(sdk)
+    ko.store_int8_chan(bits(key), bits(value), kc, vc, s_k.numpy(), s_v.numpy(), sdk, sdv,
+                       out_idx2d.numpy(), head_n_out.numpy(), np.arange(N))
+    assert np.array_equal(mod.k_cache.cpu().numpy(), kc)
+    assert np.array_equal(mod.v_cache.cpu().numpy(), vc)
+    assert np.array_equal(bits(mod.side_k), sdk) and np.array_equal(bits(mod.side_v), sdv)
+    deq = dequant_gathered(mod.k_cache.view(-1, KVH, D)[:N], mod.k_dscale,
+                           mod.side_k.view(-1, KVH, n_out)[:N], mod.out_idx2d, mod.head_n_out)
+    rel = float((deq.float().cpu() - key.float()).abs().mean() / key.float().abs().mean())
+    print(f"[int8-calib] dequant rel err {rel:.4%}", flush=True)
+    assert rel < 0.03

@@ -432,3 +432,54 @@ def test_block_moves_torch_match_closed_forms():
     ko.block_scatter(want, [2], ko.block_gather(orig.numpy().reshape(6, 10, -1), [7]))
     ko.block_copy(want, [0, 1, 9], [4, 5, 6])
     assert np.array_equal(pool.numpy().reshape(6, 10, -1), want)
+
+
+# ---------------------------------------------------------------------------
+# per-channel int8 calibration
+# ---------------------------------------------------------------------------
+def test_calib_freeze_matches_p17_unit_calibration():
+    """tests/p17_kv_int8.py:80-101 (torch, restated in helpers) against the
+    oracle's statistics + freeze on the same seeded unit case."""
+    from helpers import p17_unit_inputs
+    key, value, s_k, s_v, ds_k, ds_v, out_idx2d, head_n_out = p17_unit_inputs()
+    ak, sk = ko.calib_stats(ko.torch_bf16_bits(key))
+    av, sv = ko.calib_stats(ko.torch_bf16_bits(value))
+    got = ko.calib_freeze(ak, av, sk, sv, key.shape[0], out_idx2d.shape[1])
+    for g, w in zip(got[:4], (s_k, s_v, ds_k, ds_v)):
+        assert np.array_equal(g.view(np.uint32), w.numpy().view(np.uint32))
+    assert np.array_equal(got[4], out_idx2d.numpy())
+    assert np.array_equal(got[5], head_n_out.numpy())
+    assert got[5].sum() > 0
+
+
+def test_calib_freeze_known_answers():
+    f = np.float32
+    kvh, d = 2, 128
+    amax_k = np.ones((kvh, d), f)
+    amax_v = np.ones((kvh, d), f)
+    sum_k = np.full((kvh, d), 4.0, f)      # typ = 4 / 4 = 1 -> ratio 1
+    sum_v = np.full((kvh, d), 4.0, f)
+    amax_k[0, 5] = 10.0                     # ratio exactly 10: not an outlier
+    amax_k[0, 9] = 10.5                     # > 10
+    amax_v[0, 2] = 40.0                     # V alone decides (joint ratio)
+    amax_k[1, :] = 50.0                     # every dim of head 1: first 3 in index order
+    amax_k[1, 0] = 0.0                      # scale clamps to 1e-6, ratio 0
+    s_k, s_v, ds_k, ds_v, idx, n = ko.calib_freeze(amax_k, amax_v, sum_k, sum_v, 4, 3)
+    assert n.tolist() == [2, 3]
+    assert idx[0].tolist() == [2, 9, 0] and idx[1].tolist() == [1, 2, 3]
+    assert s_k[1, 0] == f(1e-6) and s_k[0, 9] == f(10.5) / f(127)
+    assert ds_k[0, 2] == 0 and ds_v[0, 9] == 0 and ds_k[0, 5] == s_k[0, 5]
+    # typ clamps at 1e-6: an all-zero column has ratio 0
+    z = np.zeros((1, d), f)
+    assert ko.calib_freeze(z, z, z, z, 7, 8)[5].tolist() == [0]
+
+
+def test_calib_stats_fold_over_forwards():
+    g = torch.Generator().manual_seed(44)
+    x = (torch.randn(300, 4, 128, generator=g) * 3).to(torch.bfloat16)
+    a_all, s_all = ko.calib_stats(ko.torch_bf16_bits(x))
+    a1, s1 = ko.calib_stats(ko.torch_bf16_bits(x[:120]))
+    a2, s2 = ko.calib_stats(ko.torch_bf16_bits(x[120:]))
+    assert np.array_equal(np.maximum(a1, a2), a_all)
+    assert np.allclose(s1 + s2, s_all, rtol=1e-5)
+    assert np.array_equal(a_all, np.abs(x.float().numpy()).max(0))

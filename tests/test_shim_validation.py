@@ -101,3 +101,40 @@ def test_attention_bound_is_the_bare_bound_below_eight():
     v = torch.randn(100000, generator=g) * 50
     err = (v.to(torch.bfloat16).float() - v).abs().numpy()
     assert np.all(err <= half_ulp_bf16(v.numpy()))
+
+
+def test_bound_layer_observes_k_v_before_the_store():
+    """The calibration hook runs on every forward, before the append (the
+    reference's forward pre-hook, model_runner.py:519-535)."""
+    from nanovllm_amd.layers.attention import Attention
+    from nanovllm_amd.utils.context import reset_context, set_context
+    seen = []
+    m = Attention(4, 128, 0.1, 2)
+    m.k_cache = torch.zeros(2, 256, 2, 128, dtype=torch.int8)
+    m.v_cache = torch.zeros_like(m.k_cache)
+    m.kv_cache_is_int8 = True
+    m.k_scale = m.v_scale = torch.ones(2, 128)
+    m.kv_layer = 3
+    m.kv_observe = lambda layer, k, v: seen.append((layer, k.shape, v.shape))
+    set_context(False, slot_mapping=torch.zeros(5, dtype=torch.int32),
+                context_lens=torch.ones(5, dtype=torch.int32),
+                block_tables=torch.zeros(5, 1, dtype=torch.int32), max_context_len=1)
+    try:
+        with pytest.raises(RuntimeError, match="device"):
+            m.forward(torch.zeros(5, 4, 128, dtype=torch.bfloat16),
+                      torch.zeros(5, 2, 128, dtype=torch.bfloat16),
+                      torch.zeros(5, 2, 128, dtype=torch.bfloat16))
+    finally:
+        reset_context()
+    assert seen == [(3, (5, 2, 128), (5, 2, 128))]
+
+
+def test_calibration_needs_a_per_channel_pool():
+    from nanovllm_amd.engine.kv_runner import KVCacheRunner
+    r = KVCacheRunner.__new__(KVCacheRunner)
+    r.kv_int8 = "tokhead"
+    with pytest.raises(ValueError, match="per-channel"):
+        r.kv_calibrate_begin()
+    r._calib = None
+    with pytest.raises(RuntimeError, match="begin"):
+        r.kv_calibrate_freeze()
