@@ -2539,14 +2539,15 @@ __device__ __forceinline__ u32x2_t lds_read_tr16(const char* p) {
   return __builtin_bit_cast(u32x2_t, r);
 }
 
-// k: K operands as in Tile<kBF16>; va[jj]: V^T operand of PV MFMA jj;
-// klim[cb]: the lane's column key limit (-1 for an invalid column).
+// S^T, the online softmax and P of one tile.  k: K operands as in
+// Tile<kBF16>; klim[cb]: the lane's column key limit (-1 for an invalid
+// column); pb[cb]: P^T of column block cb (bf16), the PV operand.
 template <bool kMasked>
-__device__ __forceinline__ void pf_attend(PfState& st, const u32x4_t (&k)[2][4],
-                                          const u32x4_t (&va)[8],
-                                          const QOps<kBF16, kPreNCB>& Q,
-                                          const int (&klim)[kPreNCB], int key0, int valid_end,
-                                          float scale_log2, const LaneId& L) {
+__device__ __forceinline__ void pf_score(PfState& st, const u32x4_t (&k)[2][4],
+                                         const QOps<kBF16, kPreNCB>& Q,
+                                         const int (&klim)[kPreNCB], int key0, int valid_end,
+                                         float scale_log2, const LaneId& L,
+                                         u32x4_t (&pb)[kPreNCB]) {
   static_assert(kPreNCB == 2, "the schedule below pairs two column blocks");
   // S^T of column block 0, then of block 1 (block 0's max runs under block
   // 1's MFMAs).
@@ -2603,8 +2604,6 @@ __device__ __forceinline__ void pf_attend(PfState& st, const u32x4_t (&k)[2][4],
       for (int r = 0; r < 4; ++r) st.l[cb][r] *= alpha;
     }
   }
-  const u32x4_t ones = u32x4_t{kOnesBf16x2, kOnesBf16x2, kOnesBf16x2, kOnesBf16x2};
-  u32x4_t pb[kPreNCB];
 #pragma unroll
   for (int cb = 0; cb < kPreNCB; ++cb) {
     const float neg_m = (st.m[cb] == -INFINITY) ? 0.f : -st.m[cb];
@@ -2615,6 +2614,12 @@ __device__ __forceinline__ void pf_attend(PfState& st, const u32x4_t (&k)[2][4],
 #pragma unroll
     for (int w = 0; w < 4; ++w) pb[cb][w] = pack_bf16x2_fast(pr[2 * w], pr[2 * w + 1]);
   }
+}
+
+// O^T += V^T P^T and the column sums of P.  va[jj]: V^T operand of PV MFMA jj.
+__device__ __forceinline__ void pf_pv(PfState& st, const u32x4_t (&va)[8],
+                                      const u32x4_t (&pb)[kPreNCB]) {
+  const u32x4_t ones = u32x4_t{kOnesBf16x2, kOnesBf16x2, kOnesBf16x2, kOnesBf16x2};
 #pragma unroll
   for (int cb = 0; cb < kPreNCB; ++cb) {
 #pragma unroll
@@ -2870,23 +2875,48 @@ prefill_sk_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t*
     }
   };
 
-  // Prologue: the first item's query, then the first kPfStages - 1 tiles.
-  // `issued` counts this wave's loads; mk[k] = its value right after the
-  // loads of the k-th tile ahead, q_mark right after the latest query loads,
-  // so the wait for a tile (and for its segment's query) is issued - mark.
+  // Prologue: the first item's query, then the first kPfStages tiles (every
+  // stage).  `issued` counts this wave's loads; mk[k] = its value right after
+  // the loads of the tile k + 1 ahead of the one being attended, q_mark right
+  // after the latest query loads, so the wait for a tile (and for its
+  // segment's query) is issued - mark.
   int issued = 0;
   issue_q(it);
   issued += kPfQLoadsPerWave;
   int q_mark = issued;
   int q_issued_for = it.P;  // item (by its span start) whose query was loaded last
+  int mk0 = 0;              // after the first tile's loads
   int mk[kPfStages - 1];
 #pragma unroll
-  for (int k = 0; k < kPfStages - 1; ++k) {
+  for (int k = 0; k < kPfStages; ++k) {
     if (prod_live()) {
       produce(k);
       issued += kPfTileLoads;
     }
-    mk[k] = issued;
+    if (k == 0) {
+      mk0 = issued;
+    } else {
+      mk[k - 1] = issued;
+    }
+  }
+
+  // K operands of the tile about to be attended: read one step ahead, under
+  // the previous tile's P V MFMAs (lane (lm, lg) holds key lm (+ 16 for the
+  // second half) at dims 32 c + 8 lg .. + 7).
+  u32x4_t kop[2][4];
+  auto read_k = [&](int stg) {
+    const char* kb = lds + stg * kPfStage + L.lm * kPfPitch + L.lg * 16;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        kop[h][c] = *reinterpret_cast<const u32x4_t*>(kb + h * 16 * kPfPitch + c * 64);
+    }
+  };
+  if (it.P + kPfItemCost + ct < end) {
+    pf_wait_vm(issued - mk0);  // the first tile and the first query
+    pf_barrier();
+    read_k(0);
   }
 
   int stage = 0;
@@ -2896,22 +2926,16 @@ prefill_sk_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t*
   int klim[kPreNCB];
   int min_klim = 0, split = -1;
 
+  // Per tile: (a) V^T operands, (b) S^T and the softmax, (c) the wait for the
+  // next tile and the barrier, (d) the next query and tile loads into the
+  // stages every wave is done with, (e) the next tile's K operands, (f) P V,
+  // (g) the epilogue at a segment end.  The K reads of (e) run under the MFMAs
+  // of (f), the V reads of (a) under those of (b).
   while (it.P + kPfItemCost + ct < end) {
     const bool seg_start = first || ct == 0;
     const bool seg_end = ct + 1 == it.T || it.P + kPfItemCost + ct + 1 >= end;
+    const bool has_next = it.P + kPfItemCost + ct + 1 < end;
     first = false;
-    // (a) This wave's loads of the tile (and of its segment's query) have
-    // landed ...
-    int need = mk[0];
-    if (seg_start && q_issued_for == it.P) need = max(need, q_mark);
-    if (issued - need == kPfTileLoads * (kPfStages - 2)) {
-      pf_wait_vm(kPfTileLoads * (kPfStages - 2));  // steady state: an immediate
-    } else {
-      pf_wait_vm(issued - need);
-    }
-    // ... and every wave's: the stage is complete, and every wave is done
-    // with the stage refilled below and with the query block.
-    pf_barrier();
     if (seg_start) {
       if (q_issued_for != it.P) {
         // The previous segment was one tile long: load this one's query now.
@@ -2950,21 +2974,11 @@ prefill_sk_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t*
       if (f == w && int(threadIdx.x) < min(qtile, it.geo.sq - q0) && p.sk_nseg != nullptr)
         p.sk_nseg[(int64_t(p.n_dec) + it.cq0 + q0 + threadIdx.x) * kvs_total + it.kvs] = nseg;
     }
-    // (b) The tile from LDS into registers: K rows as the S^T operands, V^T
-    // operands through transposing reads (lane (lm, lg) addresses key
-    // key_of_slot(lg, lm / 4) (+ 16 for the second half) at dims
-    // 16 jj + 4 (lm % 4)).  Issued before the next loads so that their
-    // latency hides under the DMA issue.
-    u32x4_t kop[2][4];
+    // (a) This tile's V^T operands through transposing reads (lane (lm, lg)
+    // addresses key key_of_slot(lg, lm / 4) (+ 16 for the second half) at
+    // dims 16 jj + 4 (lm % 4)).
     u32x4_t va[8];
     {
-      const char* kb = lds + stage * kPfStage + L.lm * kPfPitch + L.lg * 16;
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-          kop[h][c] = *reinterpret_cast<const u32x4_t*>(kb + h * 16 * kPfPitch + c * 64);
-      }
       const char* vb = lds + stage * kPfStage + kPfTensor +
                        (4 * L.lg + (L.lm >> 2)) * kPfPitchV + (L.lm & 3) * 8;
 #pragma unroll
@@ -2974,12 +2988,34 @@ prefill_sk_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t*
         va[jj] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
       }
     }
-    // (c) The next item's query once this segment's has been read (the
-    // barrier above), then the tile kPfStages - 1 ahead into the stage the
-    // previous iteration read.
-    {
+    // (b) S^T and the softmax: the unmasked form when every key exists and
+    // every valid column sees all 32.
+    const int key0 = ct * kTile;
+    u32x4_t pb[kPreNCB];
+    if (key0 + kTile <= it.geo.sk && key0 + kTile - 1 <= min_klim) {
+      pf_score<false>(st, kop, Q, klim, key0, it.geo.sk, p.scale_log2, L, pb);
+    } else {
+      pf_score<true>(st, kop, Q, klim, key0, it.geo.sk, p.scale_log2, L, pb);
+    }
+    const int next_stage = stage == kPfStages - 1 ? 0 : stage + 1;
+    if (has_next) {
+      // (c) This wave's loads of the next tile (and, when the next tile starts
+      // the next segment, of its prefetched query) have landed, and every
+      // wave's: the next stage is complete, and every wave is done with this
+      // tile's K and V and with this segment's query block.
       const int nP = it.P + kPfItemCost + it.T;  // span start of the next item
-      if (!seg_start && nP + kPfItemCost < end && q_issued_for != nP) {
+      int need = mk[0];
+      if (seg_end && q_issued_for == nP) need = max(need, q_mark);
+      if (issued - need == kPfTileLoads * (kPfStages - 2)) {
+        pf_wait_vm(kPfTileLoads * (kPfStages - 2));  // steady state: an immediate
+      } else {
+        pf_wait_vm(issued - need);
+      }
+      pf_barrier();
+      // (d) The next item's query, unless the next tile starts it (no barrier
+      // would separate its loads from the reads), then the tile kPfStages
+      // ahead into this tile's stage.
+      if (!seg_end && nP + kPfItemCost < end && q_issued_for != nP) {
         PfItem nx = it;
         pf_next_item(nx, cu_q, cu_k, p.n_pre, kvs_total, p.nslices, qtile);
         issue_q(nx);
@@ -2987,23 +3023,19 @@ prefill_sk_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t*
         q_mark = issued;
         q_issued_for = nP;
       }
-    }
-    if (prod_live()) {
-      produce(stage == 0 ? kPfStages - 1 : stage - 1);
-      issued += kPfTileLoads;
-    }
+      if (prod_live()) {
+        produce(stage);
+        issued += kPfTileLoads;
+      }
 #pragma unroll
-    for (int k = 0; k + 1 < kPfStages - 1; ++k) mk[k] = mk[k + 1];
-    mk[kPfStages - 2] = issued;
-    // (d) Attend: the unmasked form when every key exists and every valid
-    // column sees all 32.
-    const int key0 = ct * kTile;
-    if (key0 + kTile <= it.geo.sk && key0 + kTile - 1 <= min_klim) {
-      pf_attend<false>(st, kop, va, Q, klim, key0, it.geo.sk, p.scale_log2, L);
-    } else {
-      pf_attend<true>(st, kop, va, Q, klim, key0, it.geo.sk, p.scale_log2, L);
+      for (int k = 0; k + 1 < kPfStages - 1; ++k) mk[k] = mk[k + 1];
+      mk[kPfStages - 2] = issued;
+      // (e) The next tile's K operands.
+      read_k(next_stage);
     }
-    // (e) Segment end: store (lane (lm, lg) holds dims 16 jj + 4 lg .. + 3 of
+    // (f) O^T += V^T P^T.
+    pf_pv(st, va, pb);
+    // (g) Segment end: store (lane (lm, lg) holds dims 16 jj + 4 lg .. + 3 of
     // column lm for every jj), then move to the next item.
     if (seg_end) {
       const int q0 = it.qt * qtile;
@@ -3044,7 +3076,7 @@ prefill_sk_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t*
       pf_next_item(it, cu_q, cu_k, p.n_pre, kvs_total, p.nslices, qtile);
       ct = 0;
     }
-    stage = stage == kPfStages - 1 ? 0 : stage + 1;
+    stage = next_stage;
   }
   __builtin_amdgcn_s_waitcnt(0);
 }
