@@ -2774,6 +2774,16 @@ prefill_sk_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t*
     boff[jj] = ok ? row * rs + ch * 16 : kOob;
   }
 
+  // LDS targets of this wave's three loads (load jj is number wave + 8 jj of
+  // the tile's 18; stage-relative, the dummy block aside).
+  static_assert(kWaves == 8 && kPfLoadsPerTensor == 9 && kPfTileLoads == 3,
+                "the load pattern below");
+  const bool w0 = wave == 0;
+  const bool w01 = wave < 2;
+  const uint32_t dst0 = uint32_t(wave) * 1024;
+  const uint32_t dst1 = w0 ? 8 * 1024 : kPfTensor + uint32_t(wave - 1) * 1024;
+  const uint32_t dst2 = kPfTensor + uint32_t(7 + wave) * 1024;  // used by waves 0 and 1
+
   // Producer cursor: real tile pt of item pi.  Paged keys: the block-table
   // entry of the tile's page (pblk) is kept in pblk_val, the next page's
   // entry is loaded a page ahead (reads stay inside the item's keys).  The
@@ -2819,17 +2829,12 @@ prefill_sk_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t*
     const i32x4_t rk = raw_rsrc(kb, kbytes);
     const i32x4_t rv = raw_rsrc(vb, vbytes);
     const uint32_t sb = lds0 + stage * kPfStage;
-#pragma unroll
-    for (int jj = 0; jj < kPfTileLoads; ++jj) {
-      const int k = wave + kWaves * jj;
-      if (k < kPfLoadsPerTensor) {
-        pf_dma(rk, boff[jj] + hk, sb + k * 1024);
-      } else if (k < 2 * kPfLoadsPerTensor) {
-        pf_dma(rv, boff[jj] + hv, sb + kPfTensor + (k - kPfLoadsPerTensor) * 1024);
-      } else {
-        pf_dma(rk, kOob, lds0 + kPfDummyOff);
-      }
-    }
+    // Selects, not branches: load 0 of every wave is a K block, load 1 is K
+    // for wave 0 and V otherwise, load 2 is V for waves 0 and 1 and a zero
+    // load (boff = kOob) into the dummy block otherwise.
+    pf_dma(rk, boff[0] + hk, sb + dst0);
+    pf_dma(w0 ? rk : rv, boff[1] + (w0 ? hk : hv), sb + dst1);
+    pf_dma(rv, boff[2] + hv, w01 ? sb + dst2 : lds0 + kPfDummyOff);
     // Advance to the next real tile.
     if (++pt == pi.T) {
       pf_next_item(pi, cu_q, cu_k, p.n_pre, kvs_total, p.nslices, qtile);
