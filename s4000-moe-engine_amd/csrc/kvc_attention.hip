@@ -16,10 +16,15 @@
 // V rows are read as whole 16-byte vectors and transposed in registers with
 // v_perm_b32.
 //
-// Decode units read K/V straight from HBM into registers (each byte is used by
-// exactly one wave, so LDS staging would only add traffic) with the next tile
-// in flight while the current one is computed.  Prefill units stage each K/V
-// tile in LDS once and four waves (different query columns) consume it.
+// Decode (the headline path): a stream-K launch whose workgroups stream 4 kv
+// heads at a time through LDS.  Direct-to-LDS buffer loads bring each 32-key
+// K/V tile into a two-stage ring (int8 per-token-head pools: a four-stage
+// ring), so eight waves keep two tiles in flight with no VGPRs held by the
+// loads; each wave then reads its head's rows from LDS.  Other head layouts
+// run register segments (K/V straight from HBM into VGPRs, the next tile in
+// flight).  Prefill: a stream-K launch over (chunk, kv slice, query tile)
+// items whose 32-key tiles stream through a four-stage LDS ring, every tile
+// consumed by eight waves of different query columns.
 #include <atomic>
 #include <cmath>
 #include <cstdlib>
@@ -2383,11 +2388,12 @@ varlen_kernel(AttnParams p, const int32_t* __restrict__ block_tables) {
 // query tile), query tile fastest; each is a run of 32-key tiles that stops
 // at the last key its queries see.  The concatenated tiles are cut into one
 // equal share per workgroup, so chunks of any length mix spread evenly over
-// the CUs.  A workgroup streams its share through a three-stage LDS ring
-// with no break at item boundaries: tile j + 2 is in flight (direct-to-LDS
-// loads) while tile j is attended, whichever item either belongs to, and the
-// query block of the next item rides the same DMA while the current item
-// runs, so an item boundary costs its epilogue and not a pipeline refill.
+// the CUs.  A workgroup streams its share through a kPfStages-deep LDS ring
+// with no break at item boundaries: tiles j + 1 .. j + 3 are in flight
+// (direct-to-LDS loads) while tile j is attended, whichever item they belong
+// to, and the query block of the next item rides the same DMA while the
+// current item runs, so an item boundary costs its epilogue and not a
+// pipeline refill.
 // Items spanning several shares write split-K partials; the share holding an
 // item's first tile records the split count of its rows for the merge.
 //
