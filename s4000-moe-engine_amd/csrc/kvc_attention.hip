@@ -2426,6 +2426,8 @@ constexpr int kPfMinShare = 4;
 // Prefill keys are read by every query tile of their chunk: keep them cached.
 constexpr bool kPfNonTemporal = KVC_PF_NT != 0;
 constexpr int kOob = 0x40000000;  // a buffer offset past every resource: reads 0, no traffic
+// s_waitcnt immediate for lgkmcnt(0) alone (vmcnt 63 and expcnt 7 do not wait).
+constexpr int kWaitLgkm0 = 0xC07F;
 static_assert(kPfTileLoads == 3 && kPfQLoadsPerWave == 9, "wait counts below assume these");
 static_assert(kPfStages >= 3 && 3 * (kPfStages - 1) + 9 * (kPfStages - 2) <= 45, "pf_wait_vm range");
 static_assert(kPfSmem <= 160 * 1024, "one workgroup per CU");
@@ -2500,10 +2502,23 @@ __device__ __forceinline__ void pf_wait_vm(int n) {
 
 // Workgroup barrier over LDS only: this wave's LDS accesses are complete and
 // every wave has arrived.  (__syncthreads would also wait for the epilogue's
-// global stores, and with them for every direct-to-LDS load in flight.)
+// global stores, and with them for every direct-to-LDS load in flight.)  The
+// wait and the barrier are builtins, so the compiler's wait-count model knows
+// the LDS queue is empty after it; the empty asm statements keep memory
+// accesses from moving across it.
 __device__ __forceinline__ void pf_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
+
+// Scalar loads (block-table entries, chunk bounds) are waited for right where
+// they are issued: while one is pending the compiler's wait-count model must
+// treat the LDS counter as out of order and waits for every LDS read before
+// the first use of any, which serialises the K and V operand reads with the
+// MFMAs.  With the queue drained here its LDS waits stay partial.
+__device__ __forceinline__ void smem_drain() { __builtin_amdgcn_s_waitcnt(kWaitLgkm0); }
 
 // One 32-key tile of the stream-K prefill against the wave's kPreNCB column
 // blocks (bf16 keys).  Differences from attend_tile, each removing VALU work:
@@ -2619,6 +2634,85 @@ __device__ __forceinline__ void pf_score(PfState& st, const u32x4_t (&k)[2][4],
       pr[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[cb][i], scale_log2, neg_m));
 #pragma unroll
     for (int w = 0; w < 4; ++w) pb[cb][w] = pack_bf16x2_fast(pr[2 * w], pr[2 * w + 1]);
+  }
+}
+
+// The fast loop's form of pf_score (unmasked tiles, reference max already
+// set by the segment's first tile): P against the current reference max
+// first, and the overflow test (a logit more than 2^kRescaleLog2 above the
+// reference, i.e. a P above 2^kRescaleLog2) on the exp2 results, which as
+// arithmetic results need no canonicalising max (MFMA results do).  The rare
+// branch recomputes S^T (the logits are not kept live across the test),
+// moves the reference and redoes P exactly as pf_score does.
+__device__ __forceinline__ void pf_score_fast(PfState& st, const u32x4_t (&k)[2][4],
+                                              const QOps<kBF16, kPreNCB>& Q, float scale_log2,
+                                              u32x4_t (&pb)[kPreNCB]) {
+  auto qk = [&](f32x4_t (&sacc)[kPreNCB][2]) {
+#pragma unroll
+    for (int cb = 0; cb < kPreNCB; ++cb) {
+      sacc[cb][0] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      sacc[cb][1] = sacc[cb][0];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        sacc[cb][0] = mfma_bf16(k[0][c], Q.op[cb][c], sacc[cb][0]);
+        sacc[cb][1] = mfma_bf16(k[1][c], Q.op[cb][c], sacc[cb][1]);
+      }
+    }
+  };
+  auto exp_all = [&](const f32x4_t (&sacc)[kPreNCB][2], float (&pr)[kPreNCB][8]) {
+#pragma unroll
+    for (int cb = 0; cb < kPreNCB; ++cb) {
+      const float neg_m = (st.m[cb] == -INFINITY) ? 0.f : -st.m[cb];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        pr[cb][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[cb][0][i], scale_log2, neg_m));
+        pr[cb][4 + i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[cb][1][i], scale_log2, neg_m));
+      }
+    }
+  };
+  float pr[kPreNCB][8];
+  {
+    f32x4_t sacc[kPreNCB][2];
+    qk(sacc);
+    exp_all(sacc, pr);
+  }
+  constexpr float kRescaleP = float(1 << int(kRescaleLog2));
+  bool over = false;
+#pragma unroll
+  for (int cb = 0; cb < kPreNCB; ++cb) {
+    const float pm = fmaxf(fmaxf(fmaxf(pr[cb][0], pr[cb][1]), fmaxf(pr[cb][2], pr[cb][3])),
+                           fmaxf(fmaxf(pr[cb][4], pr[cb][5]), fmaxf(pr[cb][6], pr[cb][7])));
+    over |= pm > kRescaleP;
+  }
+  if (__builtin_expect(__ballot(over) != 0, 0)) {
+    f32x4_t sacc[kPreNCB][2];
+    qk(sacc);
+#pragma unroll
+    for (int cb = 0; cb < kPreNCB; ++cb) {
+      float t = fmaxf(fmaxf(sacc[cb][0][0], sacc[cb][0][1]), sacc[cb][0][2]);
+      t = fmaxf(fmaxf(t, sacc[cb][0][3]), sacc[cb][1][0]);
+      t = fmaxf(fmaxf(t, sacc[cb][1][1]), sacc[cb][1][2]);
+      t = fmaxf(t, sacc[cb][1][3]);
+      const float tmax = rows4_max(t) * scale_log2;
+      if (__ballot(tmax > st.m[cb] + kRescaleLog2) == 0) continue;
+      const float m_new = fmaxf(st.m[cb], tmax);
+      const float m_ref = (m_new == -INFINITY) ? 0.f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(st.m[cb] - m_ref);
+      st.m[cb] = m_new;
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) st.o[cb][jj][r] *= alpha;
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) st.l[cb][r] *= alpha;
+    }
+    exp_all(sacc, pr);
+  }
+#pragma unroll
+  for (int cb = 0; cb < kPreNCB; ++cb) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) pb[cb][w] = pack_bf16x2_fast(pr[cb][2 * w], pr[cb][2 * w + 1]);
   }
 }
 
@@ -2855,6 +2949,7 @@ prefill_sk_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t*
         pnext_val = block_tables[pbt + min(pblk + 1, plast)];
       }
     }
+    smem_drain();
   };
   auto prod_live = [&]() { return pi.P + kPfItemCost + pt < end; };
 
@@ -3029,6 +3124,7 @@ prefill_sk_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t*
       if (!seg_end && nP + kPfItemCost < end && q_issued_for != nP) {
         PfItem nx = it;
         pf_next_item(nx, cu_q, cu_k, p.n_pre, kvs_total, p.nslices, qtile);
+        smem_drain();
         issue_q(nx);
         issued += kPfQLoadsPerWave;
         q_mark = issued;
@@ -3085,9 +3181,655 @@ prefill_sk_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t*
     if (++ct == it.T) {
       if (it.P + kPfItemCost + it.T >= end) break;
       pf_next_item(it, cu_q, cu_k, p.n_pre, kvs_total, p.nslices, qtile);
+      smem_drain();
       ct = 0;
     }
     stage = next_stage;
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+}
+
+// ---------------------------------------------------------------------------
+// Stream-K prefill over bf16 keys, lean ring (prefill_sk2_kernel).
+//
+// The same items, partition, split bookkeeping and output formats as
+// prefill_sk_kernel, with a cheaper tile loop:
+//  * each wave stages its own 32 query columns in a private LDS region by
+//    direct-to-LDS loads and reads them back after its own vmcnt wait, so a
+//    query reload needs no workgroup barrier.  The next segment's query is
+//    loaded as soon as the current one is in registers;
+//  * every vector memory operation a wave issues is counted (tile loads,
+//    query loads and the epilogue stores, which are buffer stores issued
+//    unconditionally with out-of-range offsets for the lanes that do not
+//    write): vector memory operations complete in issue order, so a wait for
+//    tile j is vmcnt(operations issued after tile j) exactly, and an epilogue
+//    never holds the next tile's wait;
+//  * the steady state waits with one immediate.
+// ---------------------------------------------------------------------------
+constexpr int kP2Stages = 4;
+constexpr int kP2QSlots = kPreNCB * 16 * kPfRowSlots;       // 32 columns x 17 slots
+constexpr int kP2QLoads = (kP2QSlots + 63) / 64;            // 9 per wave
+constexpr int kP2QRegion = kP2QLoads * 1024;
+constexpr int kP2QOff = kP2Stages * kPfStage;
+constexpr int kP2DummyOff = kP2QOff + kWaves * kP2QRegion;
+constexpr int kP2Smem = kP2DummyOff + 1024;
+constexpr int kP2StoresFinal = kPreNCB * 4;   // bf16 rows: 4 x 16 B a lane per column block
+constexpr int kP2StoresPart = kPreNCB * 9;    // fp32 partials: 8 x 16 B + the lse
+constexpr int kP2Steady = kPfTileLoads * (kP2Stages - 2);   // loads after the next tile's
+static_assert(kP2Smem <= 160 * 1024, "one workgroup per CU");
+static_assert(kPfTileLoads * (kP2Stages - 1) + kP2QLoads + kP2StoresPart + 1 <= 47,
+              "every pending count is below the clamp of vm_wait");
+
+template <int N>
+__device__ __forceinline__ void vm_wait_const() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
+template <int LO, int HI>
+__device__ __forceinline__ void vm_wait_range(int n) {
+  if constexpr (LO == HI) {
+    vm_wait_const<LO>();
+  } else {
+    constexpr int MID = (LO + HI) / 2;
+    if (n <= MID) {
+      vm_wait_range<LO, MID>(n);
+    } else {
+      vm_wait_range<MID + 1, HI>(n);
+    }
+  }
+}
+
+// Wait until at most n of this wave's vector memory operations are pending
+// (n >= 0 and wave-uniform; values above 47 wait for 47, more than needed,
+// which is safe).
+__device__ __forceinline__ void vm_wait(int n) { vm_wait_range<0, 47>(uniform(n)); }
+
+// Chunk geometry of the first 64 chunks, kept in LDS by the stream-K prefill
+// launch (sq, sk, first query row, first key row): an item change then costs
+// an LDS read instead of a chain of scalar loads.
+__device__ __forceinline__ void p2_load_chunk(PfItem& it, const int4* ctab, const int32_t* cu_q,
+                                              const int32_t* cu_k, int qtile) {
+  if (it.i < 64) {
+    const int4 e = ctab[it.i];
+    it.geo.sq = uniform(e.x);
+    it.geo.sk = uniform(e.y);
+    it.geo.prefix = it.geo.sk - it.geo.sq;
+    it.geo.ntq = (it.geo.sq > 0 && it.geo.sk > 0) ? (it.geo.sq + qtile - 1) / qtile : 0;
+    it.cq0 = uniform(e.z);
+    it.ck0 = uniform(e.w);
+  } else {
+    pf_load_chunk(it, cu_q, cu_k, qtile);
+  }
+}
+
+// Virtual tiles per item in the partition of prefill_sk2_kernel: an item
+// change (its query, its epilogue, the first step of the next segment) costs
+// about three tiles' time.
+constexpr int kP2ItemCost = 3;
+
+// Weighted tiles of query tiles [0, q) of chunk c (pf_qcum with kP2ItemCost).
+__device__ __forceinline__ int p2_qcum(const ChunkGeo& c, int tpb, int q) {
+  return int(qtile_cum(c, tpb, q)) + kP2ItemCost * q;
+}
+
+// pf_next_item with the chunk table.
+__device__ __forceinline__ void p2_next_item(PfItem& it, const int4* ctab, const int32_t* cu_q,
+                                             const int32_t* cu_k, int n_pre, int kvs_total,
+                                             int nslices, int qtile) {
+  it.P += kP2ItemCost + it.T;
+  if (++it.qt == it.geo.ntq) {
+    it.qt = 0;
+    ++it.kvs;
+    if (++it.s == nslices) {
+      it.s = 0;
+      ++it.g;
+    }
+    if (it.kvs == kvs_total) {
+      it.kvs = it.g = it.s = 0;
+      do {
+        ++it.i;
+        if (it.i < n_pre) p2_load_chunk(it, ctab, cu_q, cu_k, qtile);
+      } while (it.i < n_pre && it.geo.ntq == 0);
+    }
+  }
+  it.T = it.i < n_pre ? qtile_tiles(it.geo, qtile, it.qt) : 0;
+}
+
+template <bool kFresh>
+__global__ void __launch_bounds__(kThreads)
+prefill_sk2_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k,
+                   const int32_t* __restrict__ block_tables) {
+  __shared__ __align__(16) char lds[kP2Smem];
+  __shared__ int4 ctab[64];
+  const LaneId L = lane_id();
+  const int wave = uniform(int(threadIdx.x >> 6));
+  const int kvs_total = p.kvh * p.nslices;
+  const int qtile = kWaves * kPreNCB * p.tpb;
+  const int G = int(gridDim.x);
+  const int v = int(blockIdx.x);
+  // Consecutive shares run on one XCD (workgroup v is placed on XCD v mod 8).
+  const int w = (G % 8 == 0) ? (v % 8) * (G / 8) + v / 8 : v;
+
+  // Weighted total W and the longest item; shares of S.
+  int W = 0, Tmax = 0;
+  int t_first = 0;
+  int cq_first = 0, ck_first = 0;
+  ChunkGeo g_first{0, 0, 0, 0};
+  for (int c0 = 0; c0 < p.n_pre; c0 += 64) {
+    const int ci = c0 + L.lane;
+    int t = 0, tm = 0;
+    if (ci < p.n_pre) {
+      const ChunkGeo c = chunk_geo(cu_q, cu_k, ci, qtile);
+      if (c.ntq > 0) {
+        tm = (c.sk + kTile - 1) / kTile;
+        t = kvs_total * p2_qcum(c, p.tpb, c.ntq);
+      }
+      if (c0 == 0) {
+        g_first = c;
+        cq_first = cu_q[ci];
+        ck_first = cu_k[ci];
+        ctab[L.lane] = int4{c.sq, c.sk, cq_first, ck_first};  // every wave writes the same
+      }
+    }
+    if (c0 == 0) t_first = t;
+    W += wave_sum(t);
+    Tmax = max(Tmax, wave_max(tm));
+  }
+  W = uniform(W);
+  Tmax = uniform(Tmax);
+  int S = max(p.sk_min_share, (W + G - 1) / G);
+  if (p.max_splits > 1) S = max(S, (Tmax + kP2ItemCost + p.max_splits - 2) / (p.max_splits - 1));
+  S = uniform(S);
+  if (int64_t(w) * S >= W) return;
+  const int start = w * S;
+  const int end = min(W, start + S);
+
+  // The item whose weighted span holds `start`.
+  PfItem it;
+  {
+    int base = 0, ci = -1, P = 0;
+    for (int c0 = 0; c0 < p.n_pre && ci < 0; c0 += 64) {
+      int t = t_first;
+      if (c0 > 0) {
+        t = 0;
+        if (c0 + L.lane < p.n_pre) {
+          const ChunkGeo c = chunk_geo(cu_q, cu_k, c0 + L.lane, qtile);
+          if (c.ntq > 0) t = kvs_total * p2_qcum(c, p.tpb, c.ntq);
+        }
+      }
+      int inc = t;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const int u = __shfl_up(inc, d, 64);
+        if (L.lane >= d) inc += u;
+      }
+      const int total = uniform(__shfl(inc, 63, 64));
+      if (start < base + total) {
+        const unsigned long long hit =
+            __ballot(t > 0 && base + inc - t <= start && start < base + inc);
+        const int src = __ffsll(hit) - 1;
+        ci = uniform(c0 + src);
+        P = uniform(base + __shfl(inc - t, src, 64));
+        if (c0 == 0) {
+          it.geo.sq = uniform(__shfl(g_first.sq, src, 64));
+          it.geo.sk = uniform(__shfl(g_first.sk, src, 64));
+          it.geo.prefix = it.geo.sk - it.geo.sq;
+          it.geo.ntq = uniform(__shfl(g_first.ntq, src, 64));
+          it.cq0 = uniform(__shfl(cq_first, src, 64));
+          it.ck0 = uniform(__shfl(ck_first, src, 64));
+        }
+      }
+      base += total;
+    }
+    it.i = ci;
+    if (ci >= 64) pf_load_chunk(it, cu_q, cu_k, qtile);
+    const int per_kvs = p2_qcum(it.geo, p.tpb, it.geo.ntq);
+    int off = start - P;
+    it.kvs = uniform(off / per_kvs);
+    off -= it.kvs * per_kvs;
+    int lo = 0, hi = it.geo.ntq - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (p2_qcum(it.geo, p.tpb, mid) <= off) lo = mid; else hi = mid - 1;
+    }
+    it.qt = uniform(lo);
+    it.g = uniform(it.kvs / p.nslices);
+    it.s = it.kvs - it.g * p.nslices;
+    it.P = uniform(P + it.kvs * per_kvs + p2_qcum(it.geo, p.tpb, it.qt));
+    it.T = qtile_tiles(it.geo, qtile, it.qt);
+  }
+  int ct = max(0, start - it.P - kP2ItemCost);  // consumer's tile in `it`
+
+  // Tile loads: wave w issues loads w, w + 8, w + 16 of the 18 per tile (9 of
+  // K, 9 of V; the six past 18 are zero loads into a dummy block).
+  const uint32_t lds0 = lds_addr(lds);
+  int boff[kPfTileLoads];
+#pragma unroll
+  for (int jj = 0; jj < kPfTileLoads; ++jj) {
+    const int k = wave + kWaves * jj;
+    const int sl = (k % kPfLoadsPerTensor) * 64 + L.lane;
+    const int slots = k < kPfLoadsPerTensor ? kPfRowSlots : kPfVRowSlots;
+    const int row = sl / slots;
+    const int ch = sl - row * slots;
+    int rs;
+    if constexpr (kFresh) {
+      rs = int((k >= kPfLoadsPerTensor ? p.vf_st : p.kf_st) * 2);
+    } else {
+      rs = int(p.tok_bytes);
+    }
+    const bool ok = k < 2 * kPfLoadsPerTensor && row < kTile && ch < 16;
+    boff[jj] = ok ? row * rs + ch * 16 : kOob;
+  }
+  static_assert(kWaves == 8 && kPfLoadsPerTensor == 9 && kPfTileLoads == 3,
+                "the load pattern below");
+  const bool w0 = wave == 0;
+  const bool w01 = wave < 2;
+  const uint32_t dst0 = uint32_t(wave) * 1024;
+  const uint32_t dst1 = w0 ? 8 * 1024 : kPfTensor + uint32_t(wave - 1) * 1024;
+  const uint32_t dst2 = kPfTensor + uint32_t(7 + wave) * 1024;
+
+  // Producer cursor (as in prefill_sk_kernel).
+  PfItem pi = it;
+  int pt = ct;
+  int pblk = 0, poff = 0, pblk_val = 0, pnext_val = 0, plast = 0;
+  int64_t pbt = 0;
+  auto table_setup = [&]() {
+    if constexpr (!kFresh) {
+      pbt = int64_t(p.n_dec + pi.i) * p.bt_stride;
+      const int key0 = pt * kTile;
+      pblk = uniform(key0 / p.page);
+      poff = uniform(key0 - pblk * p.page);
+      plast = uniform((pi.geo.sk - 1) / p.page);
+      pblk_val = block_tables[pbt + pblk];
+      pnext_val = block_tables[pbt + min(pblk + 1, plast)];
+    }
+  };
+  table_setup();
+  int issued = 0;  // vector memory operations this wave has issued
+  auto produce = [&](int stage) {
+    const int nvalid = min(kTile, pi.geo.sk - pt * kTile);
+    int hk, hv;
+    const char* kb;
+    const char* vb;
+    int kbytes, vbytes;
+    if constexpr (kFresh) {
+      hk = int(pi.g * p.kf_sh * 2);
+      hv = int(pi.g * p.vf_sh * 2);
+      const int64_t r0 = int64_t(pi.ck0) + pt * kTile;
+      kb = reinterpret_cast<const char*>(p.kf + r0 * p.kf_st);
+      vb = reinterpret_cast<const char*>(p.vf + r0 * p.vf_st);
+      kbytes = int(nvalid * p.kf_st * 2);
+      vbytes = int(nvalid * p.vf_st * 2);
+    } else {
+      hk = hv = pi.g * kD * 2;
+      const int64_t slot0 = int64_t(pblk_val) * p.page + poff;
+      kb = p.k_cache + slot0 * p.tok_bytes;
+      vb = p.v_cache + slot0 * p.tok_bytes;
+      kbytes = vbytes = nvalid * int(p.tok_bytes);
+    }
+    const i32x4_t rk = raw_rsrc(kb, kbytes);
+    const i32x4_t rv = raw_rsrc(vb, vbytes);
+    const uint32_t sb = lds0 + stage * kPfStage;
+    dma_to_lds_cached(rk, boff[0] + hk, sb + dst0);
+    dma_to_lds_cached(w0 ? rk : rv, boff[1] + (w0 ? hk : hv), sb + dst1);
+    dma_to_lds_cached(rv, boff[2] + hv, w01 ? sb + dst2 : lds0 + kP2DummyOff);
+    issued += kPfTileLoads;
+    if (++pt == pi.T) {
+      p2_next_item(pi, ctab, cu_q, cu_k, p.n_pre, kvs_total, p.nslices, qtile);
+      pt = 0;
+      if (pi.P + kP2ItemCost < end) table_setup();
+    } else if constexpr (!kFresh) {
+      poff += kTile;
+      if (poff == p.page) {
+        poff = 0;
+        ++pblk;
+        pblk_val = pnext_val;
+        pnext_val = block_tables[pbt + min(pblk + 1, plast)];
+      }
+    }
+  };
+  auto prod_live = [&]() { return pi.P + kP2ItemCost + pt < end; };
+
+  // This wave's query columns of item x into its LDS region: column c
+  // (0..31: block c / 16, lane c % 16) at slots 17 c .. 17 c + 15; columns
+  // past the chunk or the slice read 0.
+  const uint32_t qreg = lds0 + kP2QOff + uint32_t(wave) * kP2QRegion;
+  const char* qreg_p = lds + kP2QOff + wave * kP2QRegion;
+  const float inv_hs = 1.f / float(p.hs);
+  auto issue_q = [&](const PfItem& x) {
+    const int hs = min(p.hs, p.group - x.s * p.hs);
+    const int q0 = x.qt * qtile + wave * kPreNCB * p.tpb;  // this wave's first query row
+    const int rows = max(0, min(kPreNCB * p.tpb, x.geo.sq - q0));
+    const uint16_t* qb = p.q + (int64_t(p.n_dec) + x.cq0 + q0) * p.q_st;
+    const i32x4_t rq = raw_rsrc(qb, int(rows * p.q_st * 2));
+    const int hbase = x.g * p.group + x.s * p.hs;
+#pragma unroll
+    for (int k = 0; k < kP2QLoads; ++k) {
+      const int sl = k * 64 + L.lane;
+      const int col = sl / kPfRowSlots;
+      const int ch = sl - col * kPfRowSlots;
+      const int lm = col & 15;
+      const int tdiv = int((float(lm) + 0.5f) * inv_hs);  // lm / hs (lm < 16)
+      const int hh = lm - tdiv * p.hs;
+      const int tq = (col >> 4) * p.tpb + tdiv;  // row past q0
+      const bool ok = col < 32 && ch < 16 && lm < p.tpb * p.hs && hh < hs && tq < rows;
+      const int off =
+          ok ? int((int64_t(tq) * p.q_st + int64_t(hbase + hh) * p.q_sh) * 2) + ch * 16 : kOob;
+      dma_to_lds_cached(rq, off, qreg + k * 1024);
+    }
+    issued += kP2QLoads;
+  };
+
+  // Prologue: this wave's first query, then the first kP2Stages - 1 tiles.
+  // tmk[k]: `issued` right after the loads of tile j + k, j being the tile
+  // the next step attends; q_mark: right after the latest query loads.
+  issue_q(it);
+  int q_mark = issued;
+  int q_for = it.P;  // item (by its span start) whose query is in the region
+  int tmk[kP2Stages - 1];
+#pragma unroll
+  for (int k = 0; k < kP2Stages - 1; ++k) {
+    if (prod_live()) produce(k);
+    tmk[k] = issued;
+  }
+
+  QOps<kBF16, kPreNCB> Q;
+  // The query of the item in the region into registers (once its loads have
+  // landed), and the query of the item after `it` into the region (once the
+  // region's reads are back).
+  auto read_q = [&]() {
+    vm_wait(issued - q_mark);
+#pragma unroll
+    for (int cb = 0; cb < kPreNCB; ++cb) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        Q.op[cb][c] = *reinterpret_cast<const u32x4_t*>(qreg_p + (cb * 16 + L.lm) * kPfPitch +
+                                                        c * 64 + L.lg * 16);
+    }
+  };
+  auto issue_next_q = [&]() {
+    const int nP = it.P + kP2ItemCost + it.T;  // span start of the item after `it`
+    if (nP + kP2ItemCost < end) {
+      __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+      PfItem nx = it;
+      p2_next_item(nx, ctab, cu_q, cu_k, p.n_pre, kvs_total, p.nslices, qtile);
+      issue_q(nx);
+      q_mark = issued;
+      q_for = nP;
+    }
+  };
+  read_q();
+  issue_next_q();
+
+  PfState st;
+  int klim[kPreNCB];
+  int min_klim = 0, split = -1, nrows = 0;
+  int stage = 0;  // stage of the tile the next step attends
+  bool first = true;
+  __amdgpu_buffer_rsrc_t ro = tile_rsrc(p.out, 0);
+  __amdgpu_buffer_rsrc_t rl = tile_rsrc(p.out, 0);
+
+  // K operands (lane (lm, lg): key lm, + 16 for the second half, dims
+  // 32 c + 8 lg .. + 7) and V^T operands (transposing reads: PV MFMA jj row m
+  // is dim 16 jj + m) of the tile in stage stg.
+  auto read_k = [&](int stg, u32x4_t (&kop)[2][4]) {
+    const char* kb = lds + stg * kPfStage + L.lm * kPfPitch + L.lg * 16;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        kop[h][c] = *reinterpret_cast<const u32x4_t*>(kb + h * 16 * kPfPitch + c * 64);
+    }
+  };
+  auto read_v = [&](int stg, u32x4_t (&va)[8]) {
+    const char* vb =
+        lds + stg * kPfStage + kPfTensor + (4 * L.lg + (L.lm >> 2)) * kPfPitchV + (L.lm & 3) * 8;
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      const u32x2_t lo = lds_read_tr16(vb + jj * 32);
+      const u32x2_t hi = lds_read_tr16(vb + 16 * kPfPitchV + jj * 32);
+      va[jj] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
+    }
+  };
+
+  // Fast producer step: a full tile inside the producer's item.  Its K/V
+  // addresses advance by one tile per step (kcur, vcur include the kv head's
+  // offset); a page boundary reloads them from the prefetched table entry.
+  const char* kcur = nullptr;
+  const char* vcur = nullptr;
+  int64_t kstep = 0, vstep = 0;
+  auto fast_setup = [&]() {
+    if constexpr (kFresh) {
+      const int64_t r0 = int64_t(pi.ck0) + pt * kTile;
+      kcur = reinterpret_cast<const char*>(p.kf + r0 * p.kf_st + pi.g * p.kf_sh);
+      vcur = reinterpret_cast<const char*>(p.vf + r0 * p.vf_st + pi.g * p.vf_sh);
+      kstep = int64_t(kTile) * p.kf_st * 2;
+      vstep = int64_t(kTile) * p.vf_st * 2;
+    } else {
+      const int64_t off = (int64_t(pblk_val) * p.page + poff) * p.tok_bytes + pi.g * kD * 2;
+      kcur = p.k_cache + off;
+      vcur = p.v_cache + off;
+      kstep = vstep = int64_t(kTile) * p.tok_bytes;
+    }
+  };
+  auto produce_fast = [&](int stg) {
+    const i32x4_t rk = raw_rsrc(kcur, int(kstep));
+    const i32x4_t rv = raw_rsrc(vcur, int(vstep));
+    const uint32_t sb = lds0 + stg * kPfStage;
+    dma_to_lds_cached(rk, boff[0], sb + dst0);
+    dma_to_lds_cached(w0 ? rk : rv, boff[1], sb + dst1);
+    dma_to_lds_cached(rv, boff[2], w01 ? sb + dst2 : lds0 + kP2DummyOff);
+    issued += kPfTileLoads;
+    ++pt;
+    kcur += kstep;
+    vcur += vstep;
+    if constexpr (!kFresh) {
+      poff += kTile;
+      if (poff == p.page) {
+        poff = 0;
+        ++pblk;
+        pblk_val = pnext_val;
+        pnext_val = block_tables[pbt + min(pblk + 1, plast)];
+        const int64_t off = int64_t(pblk_val) * p.page * p.tok_bytes + pi.g * kD * 2;
+        kcur = p.k_cache + off;
+        vcur = p.v_cache + off;
+      }
+    }
+  };
+
+  // Top of a step: the tile it attends has landed for every wave and every
+  // wave is done with the previous tile's stage, which then receives the tile
+  // kP2Stages - 1 ahead.
+  auto step_top = [&](bool fast) {
+    const int n = issued - tmk[0];
+    if (n == kP2Steady) {
+      vm_wait_const<kP2Steady>();
+    } else {
+      vm_wait(n);
+    }
+    pf_barrier();
+    const int free_stage = stage == 0 ? kP2Stages - 1 : stage - 1;
+    if (fast) {
+      produce_fast(free_stage);
+    } else if (prod_live()) {
+      produce(free_stage);
+    }
+#pragma unroll
+    for (int k = 0; k + 1 < kP2Stages - 1; ++k) tmk[k] = tmk[k + 1];
+    tmk[kP2Stages - 2] = issued;
+  };
+
+  // Fast steps available from the current state: consumer tiles ct, ct + 1,
+  // ... that are unmasked and not the last of their segment; producer steps
+  // inside its item and the share.
+  auto run_length = [&]() {
+    const int mk = uniform(min_klim);
+    const int unmasked = min(it.geo.sk >> 5, mk >= kTile - 1 ? ((mk - (kTile - 1)) >> 5) + 1 : 0);
+    const int r1 = min(min(it.T - 1, unmasked), end - 1 - (it.P + kP2ItemCost)) - ct;
+    const int r2 = min(pi.T - 1 - pt, end - (pi.P + kP2ItemCost + pt));
+    return uniform(max(0, min(r1, r2)));
+  };
+
+  while (it.P + kP2ItemCost + ct < end) {
+    if (!first && ct != 0) {
+      const int R = run_length();
+      if (R > 0) {
+        fast_setup();
+        for (int r = 0; r < R; ++r) {
+          step_top(true);
+          u32x4_t pb[kPreNCB];
+          {
+            u32x4_t kop[2][4];
+            read_k(stage, kop);
+            pf_score_fast(st, kop, Q, p.scale_log2, pb);
+          }
+          u32x4_t va[8];
+          read_v(stage, va);
+          pf_pv(st, va, pb);
+          ++ct;
+          stage = stage == kP2Stages - 1 ? 0 : stage + 1;
+        }
+      }
+    }
+    // General step.
+    const bool seg_start = first || ct == 0;
+    const bool seg_end = ct + 1 == it.T || it.P + kP2ItemCost + ct + 1 >= end;
+    first = false;
+    step_top(false);
+    const int q0 = it.qt * qtile;
+    if (seg_start) {
+      const int hs = min(p.hs, p.group - it.s * p.hs);
+      const int prefix = it.geo.sk - it.geo.sq;
+#pragma unroll
+      for (int cb = 0; cb < kPreNCB; ++cb) {
+        const int tq = q0 + (wave * kPreNCB + cb) * p.tpb + L.lm / p.hs;
+        const int hh = L.lm % p.hs;
+        const bool ok = (L.lm < p.tpb * p.hs) && hh < hs && tq < it.geo.sq;
+        klim[cb] = ok ? prefix + tq : -1;
+      }
+      // The wave's smallest key limit is lane 0's first column's (the wave's
+      // first query row); when that column does not exist, no column does.
+      {
+        const int k0 = __shfl(klim[0], 0, 64);
+        min_klim = k0 >= 0 ? k0 : 0x7fffffff;
+      }
+      pf_init(st);
+      const int f = (it.P + kP2ItemCost) / S;
+      const int nseg = (it.P + kP2ItemCost + it.T - 1) / S - f + 1;
+      split = nseg == 1 ? -1 : w - f;
+      nrows = min(qtile, it.geo.sq - q0);
+      const int64_t row0 = int64_t(p.n_dec) + it.cq0 + q0;
+      if (split < 0) {
+        ro = tile_rsrc(p.out + row0 * p.o_st, int(int64_t(nrows) * p.o_st * 2));
+      } else {
+        const int64_t per_row = int64_t(p.num_heads) * p.max_splits;
+        ro = tile_rsrc(p.part_o + row0 * per_row * kD, int(nrows * per_row * kD * 4));
+        rl = tile_rsrc(p.part_lse + row0 * per_row, int(nrows * per_row * 4));
+      }
+      if (f == w && p.sk_nseg != nullptr && 64 * wave < nrows) {
+        // Split counts of the item's rows (one per row and kv slice).
+        const __amdgpu_buffer_rsrc_t rn =
+            tile_rsrc(p.sk_nseg + row0 * kvs_total, int(nrows * kvs_total * 4));
+        const int t = int(threadIdx.x);
+        const int off = t < nrows ? (t * kvs_total + it.kvs) * 4 : kOob;
+        __builtin_amdgcn_raw_buffer_store_b32(uint32_t(nseg), rn, off, 0, 0);
+        ++issued;
+      }
+    }
+    const int key0 = ct * kTile;
+    u32x4_t pb[kPreNCB];
+    {
+      u32x4_t kop[2][4];
+      read_k(stage, kop);
+      if (key0 + kTile <= it.geo.sk && key0 + kTile - 1 <= min_klim) {
+        pf_score<false>(st, kop, Q, klim, key0, it.geo.sk, p.scale_log2, L, pb);
+      } else {
+        pf_score<true>(st, kop, Q, klim, key0, it.geo.sk, p.scale_log2, L, pb);
+      }
+    }
+    {
+      u32x4_t va[8];
+      read_v(stage, va);
+      pf_pv(st, va, pb);
+    }
+    stage = stage == kP2Stages - 1 ? 0 : stage + 1;
+    // Segment end: every lane's dims (16 jj + 4 lg .. + 3 of its column), as
+    // unconditional buffer stores (lanes of columns that do not exist store
+    // out of range).  bf16 rows: lanes lg and lg ^ 1 swap halves first
+    // (v_permlane16_swap), so each lane stores 16 contiguous bytes and each
+    // row gets 64-byte pieces.
+    const bool next_in = ct + 1 == it.T && it.P + 2 * kP2ItemCost + it.T < end;
+    if (next_in) {
+      // The next item's query into registers (the query registers are dead
+      // after this tile's S^T) and the one after into the region, ahead of the
+      // stores, so those loads do not queue behind them.
+      const PfItem cur = it;
+      p2_next_item(it, ctab, cu_q, cu_k, p.n_pre, kvs_total, p.nslices, qtile);
+      if (q_for != it.P) {  // defensive: its query is normally issued one item ahead
+        issue_q(it);
+        q_mark = issued;
+        q_for = it.P;
+      }
+      read_q();
+      issue_next_q();
+      it = cur;
+    }
+    if (seg_end) {
+      const int hs = min(p.hs, p.group - it.s * p.hs);
+      const int hbase = it.g * p.group + it.s * p.hs;
+#pragma unroll
+      for (int cb = 0; cb < kPreNCB; ++cb) {
+        const int tr = (wave * kPreNCB + cb) * p.tpb + L.lm / p.hs;  // row in the query tile
+        const int hh = L.lm % p.hs;
+        const bool ok = (L.lm < p.tpb * p.hs) && hh < hs && tr < nrows;
+        const float l = st.l[cb][0];
+        if (split < 0) {
+          const float inv = 1.f / l;
+          // Even rows of lanes (lg even) keep jj = 2t, odd rows jj = 2t + 1.
+          const int base = ok ? int((int64_t(tr) * p.o_st + int64_t(hbase + hh) * p.o_sh) * 2) +
+                                    32 * (L.lg & 1) + 16 * (L.lg >> 1)
+                              : kOob;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const uint32_t a0 = pack_bf16x2_fast(st.o[cb][2 * t][0] * inv, st.o[cb][2 * t][1] * inv);
+            const uint32_t a1 = pack_bf16x2_fast(st.o[cb][2 * t][2] * inv, st.o[cb][2 * t][3] * inv);
+            const uint32_t b0 =
+                pack_bf16x2_fast(st.o[cb][2 * t + 1][0] * inv, st.o[cb][2 * t + 1][1] * inv);
+            const uint32_t b1 =
+                pack_bf16x2_fast(st.o[cb][2 * t + 1][2] * inv, st.o[cb][2 * t + 1][3] * inv);
+            const auto x0 = __builtin_amdgcn_permlane16_swap(a0, b0, false, false);
+            const auto x1 = __builtin_amdgcn_permlane16_swap(a1, b1, false, false);
+            // Lane lg even: its own 4 dims then lane lg + 1's (jj = 2t); lane lg
+            // odd: lane lg - 1's 4 dims then its own (jj = 2t + 1).
+            const u32x4_t val = u32x4_t{x0[0], x1[0], x0[1], x1[1]};
+            __builtin_amdgcn_raw_buffer_store_b128(val, ro, base + 64 * t, 0, 0);
+          }
+        } else {
+          const int idx = (tr * p.num_heads + hbase + hh) * p.max_splits + split;
+          const float il = l > 0.f ? 1.f / l : 0.f;
+          const int base = ok ? idx * (kD * 4) + 16 * L.lg : kOob;
+#pragma unroll
+          for (int jj = 0; jj < 8; ++jj) {
+            const u32x4_t val = u32x4_t{__float_as_uint(st.o[cb][jj][0] * il),
+                                        __float_as_uint(st.o[cb][jj][1] * il),
+                                        __float_as_uint(st.o[cb][jj][2] * il),
+                                        __float_as_uint(st.o[cb][jj][3] * il)};
+            __builtin_amdgcn_raw_buffer_store_b128(val, ro, base + 64 * jj, 0, 0);
+          }
+          const float lse = l > 0.f ? st.m[cb] + __log2f(l) : -INFINITY;
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(lse), rl,
+                                                (ok && L.lg == 0) ? idx * 4 : kOob, 0, 0);
+        }
+      }
+      issued += split < 0 ? kP2StoresFinal : kP2StoresPart;
+    }
+    if (++ct == it.T) {
+      // The next item, if one of its real tiles is in this share.
+      if (it.P + 2 * kP2ItemCost + it.T >= end) break;
+      p2_next_item(it, ctab, cu_q, cu_k, p.n_pre, kvs_total, p.nslices, qtile);
+      ct = 0;
+    }
   }
   __builtin_amdgcn_s_waitcnt(0);
 }
@@ -3530,10 +4272,18 @@ SkPlan plan_prefill_sk(int64_t num_q_tokens, int64_t num_heads, int64_t max_seql
 }
 
 void launch_prefill_sk(const AttnParams& p, int grid, bool fresh, hipStream_t st) {
+  if (env_int("KVC_PF_RING", 0) != 0) {
+    if (fresh) {
+      prefill_sk_kernel<true><<<grid, kThreads, 0, st>>>(p, p.cu_q, p.cu_k, p.block_tables);
+    } else {
+      prefill_sk_kernel<false><<<grid, kThreads, 0, st>>>(p, p.cu_q, p.cu_k, p.block_tables);
+    }
+    return;
+  }
   if (fresh) {
-    prefill_sk_kernel<true><<<grid, kThreads, 0, st>>>(p, p.cu_q, p.cu_k, p.block_tables);
+    prefill_sk2_kernel<true><<<grid, kThreads, 0, st>>>(p, p.cu_q, p.cu_k, p.block_tables);
   } else {
-    prefill_sk_kernel<false><<<grid, kThreads, 0, st>>>(p, p.cu_q, p.cu_k, p.block_tables);
+    prefill_sk2_kernel<false><<<grid, kThreads, 0, st>>>(p, p.cu_q, p.cu_k, p.block_tables);
   }
 }
 
