@@ -4040,6 +4040,19 @@ float env_float(const char* name, float fallback) {
 // workgroup), so they take 4 % less of a bf16 decode.
 constexpr float kXcdSkew = 0.04f;
 
+// Workgroups of a stream-K launch: one per CU, or the CUs this thread's
+// current launch may occupy (a mixed call running its decode and prefill
+// launches side by side gives each a share of the CUs; LDS keeps their
+// workgroups on separate CUs).
+thread_local int tl_launch_cus = 0;
+struct LaunchCus {
+  int saved;
+  explicit LaunchCus(int n) : saved(tl_launch_cus) { tl_launch_cus = n; }
+  ~LaunchCus() { tl_launch_cus = saved; }
+};
+int device_cus();
+int launch_cus() { return tl_launch_cus > 0 ? tl_launch_cus : device_cus(); }
+
 // Compute units of the current device (cached per device).
 int device_cus() {
   static int cached[64] = {0};
@@ -4093,7 +4106,7 @@ struct SkPlan {
 };
 
 SkPlan plan_stream_k(int64_t rows, int64_t heads, int64_t max_ctx) {
-  SkPlan sp{env_int("KVC_DECODE_STREAMK", 1) != 0, int(device_cus()), 2};
+  SkPlan sp{env_int("KVC_DECODE_STREAMK", 1) != 0, launch_cus(), 2};
   const int64_t max_tiles = (max_ctx + kTile - 1) / kTile;
   int64_t ms = (max_tiles + kSkMinShare - 1) / kSkMinShare + 1;
   const int64_t per_split = rows * heads * (kD + 1) * int64_t(sizeof(float));
@@ -4250,6 +4263,50 @@ bool split_mixed(int64_t num_decode_rows, int64_t page_size) {
          env_int("KVC_MIXED_SPLIT", 1) != 0;
 }
 
+// A mixed call's decode launch can run beside its prefill launch: on a side
+// stream of the library's (one per device, default priority, non-blocking),
+// forked from and joined back into the caller's stream with events.  The
+// decode launch is HBM-bound and the prefill launch MFMA-bound, and each of
+// their workgroups takes a whole CU's LDS, so two launches of G_d and
+// CUs - G_d workgroups split the CUs between them.
+struct SideStream {
+  hipStream_t s = nullptr;
+  hipEvent_t fork = nullptr;
+  hipEvent_t join = nullptr;
+  std::mutex mu;
+  bool ok = false;
+};
+
+SideStream* side_stream() {
+  static SideStream streams[64];
+  static std::mutex init_mu;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> lk(init_mu);
+  SideStream& ss = streams[dev];
+  if (!ss.ok) {
+    if (ss.s == nullptr && hipStreamCreateWithFlags(&ss.s, hipStreamNonBlocking) != hipSuccess)
+      return nullptr;
+    if (ss.fork == nullptr && hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming) != hipSuccess)
+      return nullptr;
+    if (ss.join == nullptr && hipEventCreateWithFlags(&ss.join, hipEventDisableTiming) != hipSuccess)
+      return nullptr;
+    ss.ok = true;
+  }
+  return &ss;
+}
+
+// CUs given to the decode launch of a mixed call when it runs beside the
+// prefill launch (0: the two launches run one after the other).
+// KVC_MIXED_DECODE_CUS overrides (rounded down to a multiple of 8).
+int mixed_decode_cus(int64_t num_decode_rows, int64_t num_prefill_tokens) {
+  const int total = device_cus();
+  int n = env_int("KVC_MIXED_DECODE_CUS", 0);
+  if (num_decode_rows <= 0 || num_prefill_tokens <= 0) return 0;
+  n = n / 8 * 8;
+  return (n > 0 && n < total) ? n : 0;
+}
+
 // Prefill-only launches over bf16 keys run as one stream-K launch
 // (prefill_sk_kernel) unless KVC_PREFILL_SK=0 selects one workgroup per
 // prefill unit.  The workspace query cannot see the key encoding or the
@@ -4262,7 +4319,7 @@ bool prefill_stream_k(int64_t num_decode_rows) {
 // Split cap of a stream-K prefill launch: an item of T tiles spans at most
 // ceil(T / S) + 1 shares; the cap is 64 and the partials' byte bound.
 SkPlan plan_prefill_sk(int64_t num_q_tokens, int64_t num_heads, int64_t max_seqlen_k) {
-  SkPlan sp{true, int(device_cus()), 2};
+  SkPlan sp{true, launch_cus(), 2};
   int64_t ms = (max_seqlen_k + kTile - 1) / kTile / kPfMinShare + 2;
   const int64_t per_split = num_q_tokens * num_heads * (kD + 1) * int64_t(sizeof(float));
   const int64_t cap = per_split > 0 ? kSkMaxPartialBytes / per_split : 64;
@@ -4745,6 +4802,47 @@ extern "C" int kvc_varlen_attention(
                 KVC_ERR_WORKSPACE, "varlen_attention: workspace of %zu bytes needed (got %zu)",
                 dec_span + pre_ws, workspace_bytes);
     char* ws = static_cast<char*>(workspace);
+    const int64_t nd = num_decode_rows;
+    const int dec_cus = mixed_decode_cus(nd, num_q_tokens - nd);
+    SideStream* ss = dec_cus > 0 ? side_stream() : nullptr;
+    if (ss != nullptr) {
+      // Decode rows on the side stream with dec_cus workgroups, prefill rows
+      // on the caller's stream with the other CUs, joined before returning.
+      std::lock_guard<std::mutex> lk(ss->mu);
+      hipStream_t main_st = as_stream(stream);
+      KVC_REQUIRE(hipEventRecord(ss->fork, main_st) == hipSuccess &&
+                      hipStreamWaitEvent(ss->s, ss->fork, 0) == hipSuccess,
+                  KVC_ERR_RUNTIME, "varlen_attention: fork to the side stream failed");
+      int rc_d;
+      {
+        LaunchCus cus(dec_cus);
+        rc_d = kvc_paged_decode(q, q_stride_t, q_stride_h, k_cache, v_cache, num_cache_blocks,
+                                page_size, num_kv_heads, head_dim, kv_dtype, k_scale, v_scale,
+                                side_k, side_v, out_idx2d, head_n_out, n_out_max, block_tables,
+                                bt_stride, max_blocks_per_seq, decode_context_lens, nd, num_heads,
+                                scale, out, out_stride_t, out_stride_h, dec_ws ? ws : nullptr,
+                                dec_ws, reinterpret_cast<kvc_stream_t>(ss->s));
+      }
+      const bool joined = hipEventRecord(ss->join, ss->s) == hipSuccess;
+      int rc_p = KVC_OK;
+      if (rc_d == KVC_OK) {
+        LaunchCus cus(device_cus() - dec_cus);
+        rc_p = kvc_varlen_attention(
+            static_cast<const uint16_t*>(q) + nd * q_stride_t, q_stride_t, q_stride_h,
+            num_q_tokens - nd, num_heads, k_cache, v_cache, num_cache_blocks, page_size,
+            num_kv_heads, head_dim, kv_dtype, k_scale, v_scale, side_k, side_v, out_idx2d,
+            head_n_out, n_out_max, nullptr, 0, 0, nullptr, 0, 0, block_tables + nd * bt_stride,
+            bt_stride, max_blocks_per_seq, 0, nullptr, num_prefill, cu_seqlens_q, cu_seqlens_k,
+            num_prefill_units, max_seqlen_k, scale,
+            static_cast<uint16_t*>(out) + nd * out_stride_t, out_stride_t, out_stride_h,
+            pre_ws ? ws + dec_span : nullptr, pre_ws, stream);
+      }
+      const bool waited = joined && hipStreamWaitEvent(main_st, ss->join, 0) == hipSuccess;
+      if (rc_d != KVC_OK) return rc_d;
+      if (rc_p != KVC_OK) return rc_p;
+      KVC_REQUIRE(waited, KVC_ERR_RUNTIME, "varlen_attention: join of the side stream failed");
+      return KVC_OK;
+    }
     rc = kvc_paged_decode(q, q_stride_t, q_stride_h, k_cache, v_cache, num_cache_blocks,
                           page_size, num_kv_heads, head_dim, kv_dtype, k_scale, v_scale, side_k,
                           side_v, out_idx2d, head_n_out, n_out_max, block_tables, bt_stride,
@@ -4752,7 +4850,6 @@ extern "C" int kvc_varlen_attention(
                           scale, out, out_stride_t, out_stride_h, dec_ws ? ws : nullptr, dec_ws,
                           stream);
     if (rc != KVC_OK || num_q_tokens == num_decode_rows) return rc;
-    const int64_t nd = num_decode_rows;
     return kvc_varlen_attention(
         static_cast<const uint16_t*>(q) + nd * q_stride_t, q_stride_t, q_stride_h,
         num_q_tokens - nd, num_heads, k_cache, v_cache, num_cache_blocks, page_size,

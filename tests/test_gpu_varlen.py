@@ -20,17 +20,22 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-@pytest.fixture(params=["prefill-sk", "units", "stream-k", "combined"])
+@pytest.fixture(params=["prefill-sk", "prefill-ring", "side-by-side", "units", "stream-k",
+                        "combined"])
 def partition(request, monkeypatch):
     """Every launch partition: prefill rows over bf16 keys as one stream-K
-    prefill launch (the default), one workgroup per prefill unit
-    (KVC_PREFILL_SK=0), the single stream-K launch of decode and prefill
-    items together (KVC_MIXED_STREAMK=1), and the single unit launch of
-    decode and prefill units together (KVC_MIXED_SPLIT=0; without decode
-    rows it is the default launch)."""
+    prefill launch (the default), the same items through the first form of
+    that launch (KVC_PF_RING=1), the decode and prefill launches of a mixed
+    call side by side on 64 and the remaining CUs (KVC_MIXED_DECODE_CUS=64),
+    one workgroup per prefill unit (KVC_PREFILL_SK=0), the single stream-K
+    launch of decode and prefill items together (KVC_MIXED_STREAMK=1), and
+    the single unit launch of decode and prefill units together
+    (KVC_MIXED_SPLIT=0; without decode rows it is the default launch)."""
     monkeypatch.setenv("KVC_MIXED_STREAMK", "1" if request.param == "stream-k" else "0")
     monkeypatch.setenv("KVC_PREFILL_SK", "0" if request.param == "units" else "1")
     monkeypatch.setenv("KVC_MIXED_SPLIT", "0" if request.param == "combined" else "1")
+    monkeypatch.setenv("KVC_PF_RING", "1" if request.param == "prefill-ring" else "0")
+    monkeypatch.setenv("KVC_MIXED_DECODE_CUS", "64" if request.param == "side-by-side" else "0")
     return request.param
 
 
@@ -94,6 +99,26 @@ def test_stall_free_mixed_batch_full_shape(partition):
     dec = uniform_lengths(60, 256, 4096, seed=3)
     c = _mixed_case(32, 4, dec, [(0, 256), (512, 256), (2048, 256), (8192, 256)], seed=4)
     _check_mixed(c, "stall-free-full")
+
+
+def test_stall_free_mixed_batch_repeats_bit_for_bit(partition):
+    # The same call three times on the same inputs gives the same bits: the
+    # launches have no order-dependent arithmetic, so a difference means a
+    # read raced with a load or an MFMA result.
+    dec = uniform_lengths(60, 256, 4096, seed=3)
+    c = _mixed_case(32, 4, dec, [(0, 256), (512, 256), (2048, 256), (8192, 256)], seed=4)
+    outs = []
+    for _ in range(3):
+        outs.append(bits(varlen_attention(
+            c["q"], c["k_cache"], c["v_cache"], scale=128 ** -0.5, block_tables=c["bt"],
+            num_decode_rows=c["n_dec"], decode_context_lens=c["dec_lens"],
+            cu_seqlens_q=torch.tensor(c["cu_q"], dtype=torch.int32, device=DEV),
+            cu_seqlens_k=torch.tensor(c["cu_k"], dtype=torch.int32, device=DEV),
+            cu_seqlens_q_list=c["cu_q"], cu_seqlens_k_list=c["cu_k"])))
+    for i in (1, 2):
+        diff = int((outs[i] != outs[0]).sum())
+        print(f"[varlen] repeat {i} ({partition}): {diff} differing elements", flush=True)
+        assert diff == 0
 
 
 def test_many_chunks_empty_chunks_and_empty_context(partition):
