@@ -3264,9 +3264,13 @@ __device__ __forceinline__ void p2_load_chunk(PfItem& it, const int4* ctab, cons
 }
 
 // Virtual tiles per item in the partition of prefill_sk2_kernel: an item
-// change (its query, its epilogue, the first step of the next segment) costs
-// about three tiles' time.
-constexpr int kP2ItemCost = 3;
+// change (its query, its epilogue, the first step of the next segment, the
+// general steps of its masked tiles) costs several tiles' time; 6 balanced
+// the shares best on mixed chunk lengths (3, 5, 6 and 8 measured).
+#ifndef KVC_P2_ITEM_COST
+#define KVC_P2_ITEM_COST 6
+#endif
+constexpr int kP2ItemCost = KVC_P2_ITEM_COST;
 
 // Weighted tiles of query tiles [0, q) of chunk c (pf_qcum with kP2ItemCost).
 __device__ __forceinline__ int p2_qcum(const ChunkGeo& c, int tpb, int q) {
@@ -4304,7 +4308,7 @@ int mixed_decode_cus(int64_t num_decode_rows, int64_t num_prefill_tokens) {
   int n = env_int("KVC_MIXED_DECODE_CUS", 0);
   if (num_decode_rows <= 0 || num_prefill_tokens <= 0) return 0;
   n = n / 8 * 8;
-  return (n > 0 && n < total) ? n : 0;
+  return (n > 0 && n <= total) ? n : 0;
 }
 
 // Prefill-only launches over bf16 keys run as one stream-K launch
@@ -4813,8 +4817,25 @@ extern "C" int kvc_varlen_attention(
       KVC_REQUIRE(hipEventRecord(ss->fork, main_st) == hipSuccess &&
                       hipStreamWaitEvent(ss->s, ss->fork, 0) == hipSuccess,
                   KVC_ERR_RUNTIME, "varlen_attention: fork to the side stream failed");
-      int rc_d;
-      {
+      // dec_cus == every CU: the prefill launch goes first with every CU and
+      // the decode launch's workgroups take the CUs its shares leave.
+      const bool tail = dec_cus >= device_cus();
+      auto launch_prefill = [&]() {
+        LaunchCus cus(tail ? device_cus() : device_cus() - dec_cus);
+        return kvc_varlen_attention(
+            static_cast<const uint16_t*>(q) + nd * q_stride_t, q_stride_t, q_stride_h,
+            num_q_tokens - nd, num_heads, k_cache, v_cache, num_cache_blocks, page_size,
+            num_kv_heads, head_dim, kv_dtype, k_scale, v_scale, side_k, side_v, out_idx2d,
+            head_n_out, n_out_max, nullptr, 0, 0, nullptr, 0, 0, block_tables + nd * bt_stride,
+            bt_stride, max_blocks_per_seq, 0, nullptr, num_prefill, cu_seqlens_q, cu_seqlens_k,
+            num_prefill_units, max_seqlen_k, scale,
+            static_cast<uint16_t*>(out) + nd * out_stride_t, out_stride_t, out_stride_h,
+            pre_ws ? ws + dec_span : nullptr, pre_ws, stream);
+      };
+      int rc_p = KVC_OK;
+      if (tail) rc_p = launch_prefill();
+      int rc_d = KVC_OK;
+      if (rc_p == KVC_OK) {
         LaunchCus cus(dec_cus);
         rc_d = kvc_paged_decode(q, q_stride_t, q_stride_h, k_cache, v_cache, num_cache_blocks,
                                 page_size, num_kv_heads, head_dim, kv_dtype, k_scale, v_scale,
@@ -4824,19 +4845,7 @@ extern "C" int kvc_varlen_attention(
                                 dec_ws, reinterpret_cast<kvc_stream_t>(ss->s));
       }
       const bool joined = hipEventRecord(ss->join, ss->s) == hipSuccess;
-      int rc_p = KVC_OK;
-      if (rc_d == KVC_OK) {
-        LaunchCus cus(device_cus() - dec_cus);
-        rc_p = kvc_varlen_attention(
-            static_cast<const uint16_t*>(q) + nd * q_stride_t, q_stride_t, q_stride_h,
-            num_q_tokens - nd, num_heads, k_cache, v_cache, num_cache_blocks, page_size,
-            num_kv_heads, head_dim, kv_dtype, k_scale, v_scale, side_k, side_v, out_idx2d,
-            head_n_out, n_out_max, nullptr, 0, 0, nullptr, 0, 0, block_tables + nd * bt_stride,
-            bt_stride, max_blocks_per_seq, 0, nullptr, num_prefill, cu_seqlens_q, cu_seqlens_k,
-            num_prefill_units, max_seqlen_k, scale,
-            static_cast<uint16_t*>(out) + nd * out_stride_t, out_stride_t, out_stride_h,
-            pre_ws ? ws + dec_span : nullptr, pre_ws, stream);
-      }
+      if (!tail && rc_d == KVC_OK) rc_p = launch_prefill();
       const bool waited = joined && hipStreamWaitEvent(main_st, ss->join, 0) == hipSuccess;
       if (rc_d != KVC_OK) return rc_d;
       if (rc_p != KVC_OK) return rc_p;
