@@ -3937,7 +3937,7 @@ void launch_merge(const AttnParams& p, int64_t rows, hipStream_t st) {
 // head l / 8 of the slice (eight heads per pass) and dims 16 (l % 8) .. +15,
 // so a whole slice's partials are in flight together and a row costs two
 // memory round trips (the count, then the partials) whatever its head count.
-constexpr int kSliceBatch = 8;  // splits per load batch
+constexpr int kSliceBatch = 4;  // splits per load batch (124 VGPRs: every wave resident)
 __global__ void __launch_bounds__(64 * kMergeWaves)
 merge_slices_kernel(AttnParams p, int num_rows, const float* __restrict__ part_o,
                     const float* __restrict__ part_lse, const int* __restrict__ nseg_arr) {
