@@ -42,6 +42,11 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kSideMax = 8;
 constexpr int kPreNCB = 2;  // column blocks per wave in prefill units
 constexpr float kRescaleLog2 = 8.f;  // lazy-rescale threshold (log2 units)
+// Virtual tiles per row of a ragged stream-K decode (see paged_decode_sk_kernel).
+#ifndef KVC_DEC_ROW_COST
+#define KVC_DEC_ROW_COST 2
+#endif
+constexpr int kDecRowCost = KVC_DEC_ROW_COST;
 
 enum Enc : int { kBF16 = KVC_KV_BF16, kI8Tok = KVC_KV_INT8_TOKHEAD, kI8Chan = KVC_KV_INT8_CHAN };
 
@@ -1959,6 +1964,7 @@ paged_decode_sk_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
   // the second pass (one round trip to memory for batches up to 256 x groups).
   constexpr int kCached = 4;
   int cl[kCached];
+  int row_cost = 0;
 #pragma unroll
   for (int i = 0; i < kCached; ++i) cl[i] = r0 + i < r1 ? ctx_lens[(r0 + i) / groups] : 0;
   auto ctx_of = [&](int r) {
@@ -1967,11 +1973,28 @@ paged_decode_sk_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
     for (int i = 0; i < kCached; ++i) c = (r == r0 + i) ? cl[i] : c;
     return r - r0 < kCached ? c : ctx_lens[r / groups];
   };
-  int mine = 0, tmax = 0;
+  int mine = 0, tmax = 0, rows = 0;
   for (int r = r0; r < r1; ++r) {
     const int t = ctx_tiles(ctx_of(r));
     mine += t;
     tmax = max(tmax, t);
+    rows += t > 0;
+  }
+  // Rows of unequal length: each non-empty row also carries kDecRowCost
+  // virtual tiles (a share that starts a second row pays the ring's restart:
+  // its drain, query and first tiles), so such shares get fewer real tiles.
+  // Equal rows keep shares aligned to rows and carry none.
+  {
+    int rsum = rows, tm = tmax, tsum = mine;
+#pragma unroll
+    for (int dd = 32; dd >= 1; dd >>= 1) {
+      rsum += __shfl_xor(rsum, dd, 64);
+      tm = max(tm, __shfl_xor(tm, dd, 64));
+      tsum += __shfl_xor(tsum, dd, 64);
+    }
+    const int cost = uniform(tsum == tm * rsum) ? 0 : kDecRowCost;
+    row_cost = cost;
+    mine += cost * rows;
   }
   int incl = mine;
 #pragma unroll
@@ -2007,7 +2030,8 @@ paged_decode_sk_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
     for (int r = r0; r < r1; ++r) {
       const int c = ctx_of(r);
       const int t = ctx_tiles(c);
-      if (P <= start && start < P + t) {
+      const int span = t > 0 ? t + row_cost : 0;  // real tiles at [P + row_cost, P + span)
+      if (t > 0 && P <= start && start < P + span) {
         found_r = r;
         found_p = P;
         found_c = c;
@@ -2029,11 +2053,12 @@ paged_decode_sk_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
               }
             }
           }
-        } else if (share_of(P) == w) {
-          set_nseg(p, r / groups, r % groups, share_of(P + t - 1) - share_of(P) + 1);
+        } else if (share_of(P + row_cost) == w) {
+          set_nseg(p, r / groups, r % groups,
+                   share_of(P + row_cost + t - 1) - share_of(P + row_cost) + 1);
         }
       }
-      P += t;
+      P += span;
     }
   }
   const unsigned long long hit = __ballot(found_r < R);
@@ -2044,11 +2069,12 @@ paged_decode_sk_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
   while (r < R && P < end) {
     const int b = r / groups;
     const int t = ctx_tiles(ctx);
-    if (t > 0) {
-      const int t0 = max(start, P) - P;
-      const int t1 = min(end, P + t) - P;
-      const int first_share = share_of(P);
-      const int nseg = share_of(P + t - 1) - first_share + 1;
+    const int Pr = P + row_cost;  // the row's first real tile
+    if (t > 0 && Pr < end) {
+      const int t0 = max(start, Pr) - Pr;
+      const int t1 = min(end, Pr + t) - Pr;
+      const int first_share = share_of(Pr);
+      const int nseg = share_of(Pr + t - 1) - first_share + 1;
       const int split = nseg == 1 ? -1 : w - first_share;
       if constexpr (kBfLds) {
         decode_segment_lds(p, smem, smem1, smem2, block_tables + int64_t(b) * p.bt_stride, b,
@@ -2061,7 +2087,7 @@ paged_decode_sk_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
                              r - b * groups, ctx, t0, t1, split);
       }
     }
-    P += t;
+    P += t > 0 ? t + row_cost : 0;
     ++r;
     if (r < R && P < end) ctx = uniform(ctx_lens[r / groups]);
   }
