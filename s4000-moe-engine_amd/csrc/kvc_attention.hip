@@ -1220,11 +1220,62 @@ __device__ __forceinline__ QueryI8 quantise_query(const float (&q)[32]) {
 
 // One wave's half of an int8 tile: keys 16 kh + 4 lg + i (i < 4) of the
 // lane's S^T column, every dim of the output (o[jj][i] = dim 32 lg + 8 i + jj).
+// Scores are kept relative to mu (the running max m, or 0 while m is -inf):
+// x' = x - mu comes out of one FMA and feeds exp2 directly.  The rescale test
+// is lane-local (x' > thr, thr = kRescaleLog2 once m is finite, -inf
+// before), so the column max across the four lane groups is only formed on
+// the rare rescale path.
 struct KeyHalfState {
   f32x4_t o[8];
-  float m, l;
-  float vb;  // lane-partial sum of the bf16 P operand (the +128 bias of V)
+  f32x4_t vb;  // every row: the column's sum of the bf16 P operand (the +128 bias of V)
+  float m;     // running reference max of x (log2 units), -inf before any key
+  float mu;    // m, or 0 while m is -inf
+  float thr;   // rescale threshold on x'
+  float l;     // lane-partial sum of exp2(x') over the lane's keys
 };
+
+__device__ __forceinline__ void init_key_half(KeyHalfState& st) {
+#pragma unroll
+  for (int jj = 0; jj < 8; ++jj) st.o[jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  st.vb = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  st.m = -INFINITY;
+  st.mu = 0.f;
+  st.thr = -INFINITY;
+  st.l = 0.f;
+}
+
+// exp2 of the shifted scores, the P operand and the PV products of one key
+// half (the part after any rescale).
+template <bool kMasked>
+__device__ __forceinline__ void key_half_pv_i8(KeyHalfState& st, const float (&x)[4],
+                                               const bool (&kvalid)[4], const u32x2_t (&vr)[4],
+                                               const float (&vsc)[4]) {
+  float pr[4], pv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    pr[i] = __builtin_amdgcn_exp2f(x[i]);
+    pv[i] = kvalid[i] ? pr[i] * vsc[i] : 0.f;
+  }
+  st.l += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+  const u32x2_t pb = {pack_bf16x2_fast(pv[0], pv[1]), pack_bf16x2_fast(pv[2], pv[3])};
+  // Column sums of the P operand as rounded, from a ones operand: the
+  // +128 bias of V comes off exactly at the end.
+  st.vb = mfma_bf16_k16(u32x2_t{0x3f803f80u, 0x3f803f80u}, pb, st.vb);
+  // V^T operand of dims 8 lm + jj: byte jj of the lane's 4 key rows, as
+  // bf16 of (code + 128).
+  u32x2_t vq[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) vq[i] = vr[i] ^ 0x80808080u;
+#pragma unroll
+  for (int jj = 0; jj < 8; ++jj) {
+    const int dw = jj >> 2, sh = (jj & 3) * 8;
+    const float a0 = float((vq[0][dw] >> sh) & 0xffu), a1 = float((vq[1][dw] >> sh) & 0xffu);
+    const float a2 = float((vq[2][dw] >> sh) & 0xffu), a3 = float((vq[3][dw] >> sh) & 0xffu);
+    const u32x2_t va = {perm(__float_as_uint(a1), __float_as_uint(a0), kPermHiHi),
+                        perm(__float_as_uint(a3), __float_as_uint(a2), kPermHiHi)};
+    st.o[jj] = mfma_bf16_k16(va, pb, st.o[jj]);
+  }
+}
 
 template <bool kMasked>
 __device__ __forceinline__ void attend_key_half_i8(KeyHalfState& st, const u32x4_t (&kc)[2],
@@ -1241,12 +1292,14 @@ __device__ __forceinline__ void attend_key_half_i8(KeyHalfState& st, const u32x4
     h = mfma_i8(kc[c], Q.hi[c], h);
     lo = mfma_i8(kc[c], Q.lo[c], lo);
   }
-  const float qs = Q.scale * scale_log2;
+  // q . k = scale (254 hi.k + lo.k) / 254; |hi.k| <= 128 * 128 * 127 < 2^23,
+  // so 254 hi.k + lo.k is one exact 24-bit multiply-add.
+  const float qs = Q.scale * scale_log2 * (1.f / 254.f);
   float x[4];
   float tmax = -INFINITY;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const float v = (float(h[i]) + float(lo[i]) * (1.f / 254.f)) * (qs * ksc[i]);
+    const float v = fmaf(float(__mul24(h[i], 254) + lo[i]), qs * ksc[i], -st.mu);
     if constexpr (kMasked) {
       const bool ok = kvalid[i] && (key0 + 4 * L.lg + i <= klim);
       x[i] = ok ? v : -INFINITY;
@@ -1255,13 +1308,20 @@ __device__ __forceinline__ void attend_key_half_i8(KeyHalfState& st, const u32x4
     }
     tmax = fmaxf(tmax, x[i]);
   }
-  tmax = rows4_max(tmax);
-  float alpha = 1.f;
-  if (__builtin_expect(__ballot(tmax > st.m + kRescaleLog2) != 0, 0)) {
-    const float m_new = fmaxf(st.m, tmax);
-    const float m_ref = (m_new == -INFINITY) ? 0.f : m_new;
-    alpha = __builtin_amdgcn_exp2f(st.m - m_ref);
+  // The rescale path carries its own copy of the PV part, so the common
+  // path's accumulators flow straight into its MFMAs (no merge of two
+  // versions of o ahead of them).
+  if (__builtin_expect(__ballot(tmax > st.thr) != 0, 0)) {
+    const float m_new = fmaxf(st.m, rows4_max(tmax + st.mu));
+    const float mu_new = (m_new == -INFINITY) ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(st.m - mu_new);
+    const float shift = st.mu - mu_new;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] += shift;
     st.m = m_new;
+    st.mu = mu_new;
+    st.thr = (m_new == -INFINITY) ? -INFINITY : kRescaleLog2;
+    st.l *= alpha;
 #pragma unroll
     for (int jj = 0; jj < 8; ++jj) {
       st.o[jj][0] *= alpha;
@@ -1269,32 +1329,13 @@ __device__ __forceinline__ void attend_key_half_i8(KeyHalfState& st, const u32x4
       st.o[jj][2] *= alpha;
       st.o[jj][3] *= alpha;
     }
-  }
-  const float m_use = (st.m == -INFINITY) ? 0.f : st.m;
-  float pv[4], psum = 0.f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float pr = __builtin_amdgcn_exp2f(x[i] - m_use);
-    psum += pr;
-    pv[i] = kvalid[i] ? pr * vsc[i] : 0.f;
-  }
-  st.l = st.l * alpha + psum;
-  const u32x2_t pb = {pack_bf16x2_fast(pv[0], pv[1]), pack_bf16x2_fast(pv[2], pv[3])};
-  st.vb = st.vb * alpha + (bf16_bits_to_f32(pb[0] & 0xffffu) + bf16_bits_to_f32(pb[0] >> 16) +
-                           bf16_bits_to_f32(pb[1] & 0xffffu) + bf16_bits_to_f32(pb[1] >> 16));
-  // V^T operand of dims 8 lm + jj: byte jj of the lane's 4 key rows, as
-  // bf16 of (code + 128).
-  u32x2_t vq[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) vq[i] = vr[i] ^ 0x80808080u;
-#pragma unroll
-  for (int jj = 0; jj < 8; ++jj) {
-    const int dw = jj >> 2, sh = (jj & 3) * 8;
-    const float a0 = float((vq[0][dw] >> sh) & 0xffu), a1 = float((vq[1][dw] >> sh) & 0xffu);
-    const float a2 = float((vq[2][dw] >> sh) & 0xffu), a3 = float((vq[3][dw] >> sh) & 0xffu);
-    const u32x2_t va = {perm(__float_as_uint(a1), __float_as_uint(a0), kPermHiHi),
-                        perm(__float_as_uint(a3), __float_as_uint(a2), kPermHiHi)};
-    st.o[jj] = mfma_bf16_k16(va, pb, st.o[jj]);
+    st.vb[0] *= alpha;
+    st.vb[1] *= alpha;
+    st.vb[2] *= alpha;
+    st.vb[3] *= alpha;
+    key_half_pv_i8<kMasked>(st, x, kvalid, vr, vsc);
+  } else {
+    key_half_pv_i8<kMasked>(st, x, kvalid, vr, vsc);
   }
 }
 
@@ -1352,11 +1393,7 @@ __device__ void decode_segment_lds_i8(const AttnParams& p, char* ring, char* qld
 
   QueryI8 Q;
   KeyHalfState st;
-#pragma unroll
-  for (int jj = 0; jj < 8; ++jj) st.o[jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  st.m = -INFINITY;
-  st.l = 0.f;
-  st.vb = 0.f;
+  init_key_half(st);
 
   const int tok = int(p.tok_bytes);
   const int64_t grp_off = int64_t(kvg) * 512;
@@ -1496,7 +1533,7 @@ __device__ void decode_segment_lds_i8(const AttnParams& p, char* ring, char* qld
   // waves hand (o, m, l) to the key-half-0 waves through the first stage,
   // which write the merged rows.  Lane (lm, lg) holds dims 32 lg + 8 i + jj.
   const float l = rows4_sum(st.l);
-  const float bias = 128.f * rows4_sum(st.vb);
+  const float bias = 128.f * st.vb[0];
   float* mo = reinterpret_cast<float*>(ring);
   float* mml = mo + 4 * 16 * kI8MergePitch;
   float* orow = mo + (gl * 16 + L.lm) * kI8MergePitch + 32 * L.lg;
