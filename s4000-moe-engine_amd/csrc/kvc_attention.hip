@@ -903,10 +903,64 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
       uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)p)));
 }
 
+// s_waitcnt immediate for lgkmcnt(0) alone (vmcnt 63 and expcnt 7 do not wait).
+constexpr int kWaitLgkm0 = 0xC07F;
+
+// Workgroup barrier over LDS only: this wave's LDS accesses are complete and
+// every wave has arrived.  (__syncthreads would also wait for the epilogue's
+// global stores, and with them for every direct-to-LDS load in flight.)  The
+// wait and the barrier are builtins, so the compiler's wait-count model knows
+// the LDS queue is empty after it; the empty asm statements keep memory
+// accesses from moving across it.
+__device__ __forceinline__ void pf_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Scalar loads (block-table entries, chunk bounds) are waited for right where
+// they are issued: while one is pending the compiler's wait-count model must
+// treat the LDS counter as out of order and waits for every LDS read before
+// the first use of any, which serialises the K and V operand reads with the
+// MFMAs.  With the queue drained here its LDS waits stay partial.
+__device__ __forceinline__ void smem_drain() { __builtin_amdgcn_s_waitcnt(kWaitLgkm0); }
+
+// Scores are kept relative to mu (the running max m, or 0 while m is -inf):
+// x' = x - mu comes out of one FMA and feeds exp2 directly.  The rescale test
+// is lane-local (x' > thr, thr = kRescaleLog2 once m is finite, -inf before),
+// so the column max across the four lane groups is only formed on the rare
+// rescale path, which also carries its own copy of the P V part (the common
+// path's accumulators then flow straight into its MFMAs).
 struct HalfState {
   f32x4_t o[4];  // O^T rows of PV MFMA jj (local 0..3): dim 32lg + 8r + 4h + jj
-  float m, l;
+  float m;       // running reference max of x (log2 units), -inf before any key
+  float mu;      // m, or 0 while m is -inf
+  float thr;     // rescale threshold on x'
+  float l;       // lane-partial sum of exp2(x') over the lane's key slots
 };
+
+__device__ __forceinline__ void init_half(HalfState& st) {
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) st.o[jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  st.m = -INFINITY;
+  st.mu = 0.f;
+  st.thr = -INFINITY;
+  st.l = 0.f;
+}
+
+__device__ __forceinline__ void half_pv(HalfState& st, const float (&x)[8],
+                                        const u32x2_t (&vrow)[8]) {
+  float pr[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) pr[i] = __builtin_amdgcn_exp2f(x[i]);
+  st.l += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
+  u32x4_t pb;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) pb[w] = pack_bf16x2_fast(pr[2 * w], pr[2 * w + 1]);
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) st.o[jj] = mfma_bf16(v_operand_half(vrow, jj), pb, st.o[jj]);
+}
 
 template <bool kMasked>
 __device__ __forceinline__ void attend_tile_half(HalfState& st, const u32x4_t (&k)[2][4],
@@ -929,25 +983,31 @@ __device__ __forceinline__ void attend_tile_half(HalfState& st, const u32x4_t (&
     s0 = mfma_bf16(k[0][c], Q.op[0][c], s0);
     s1 = mfma_bf16(k[1][c], Q.op[0][c], s1);
   }
-  float x[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+  const float sv[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+  float x[8];
   float tmax = -INFINITY;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
+    const float v = fmaf(sv[i], scale_log2, -st.mu);
     if constexpr (kMasked) {
       const bool ok = kvalid[i] && (key0 + key_of_slot(L.lg, i) <= klim);
-      x[i] = ok ? x[i] * scale_log2 : -INFINITY;
+      x[i] = ok ? v : -INFINITY;
     } else {
-      x[i] *= scale_log2;
+      x[i] = v;
     }
     tmax = fmaxf(tmax, x[i]);
   }
-  tmax = rows4_max(tmax);
-  float alpha = 1.f;
-  if (__builtin_expect(__ballot(tmax > st.m + kRescaleLog2) != 0, 0)) {
-    const float m_new = fmaxf(st.m, tmax);
-    const float m_ref = (m_new == -INFINITY) ? 0.f : m_new;
-    alpha = __builtin_amdgcn_exp2f(st.m - m_ref);
+  if (__builtin_expect(__ballot(tmax > st.thr) != 0, 0)) {
+    const float m_new = fmaxf(st.m, rows4_max(tmax + st.mu));
+    const float mu_new = (m_new == -INFINITY) ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(st.m - mu_new);
+    const float shift = st.mu - mu_new;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] += shift;
     st.m = m_new;
+    st.mu = mu_new;
+    st.thr = (m_new == -INFINITY) ? -INFINITY : kRescaleLog2;
+    st.l *= alpha;
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
       st.o[jj][0] *= alpha;
@@ -955,20 +1015,10 @@ __device__ __forceinline__ void attend_tile_half(HalfState& st, const u32x4_t (&
       st.o[jj][2] *= alpha;
       st.o[jj][3] *= alpha;
     }
+    half_pv(st, x, vrow);
+  } else {
+    half_pv(st, x, vrow);
   }
-  const float m_use = (st.m == -INFINITY) ? 0.f : st.m;
-  float pr[8], psum = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    pr[i] = __builtin_amdgcn_exp2f(x[i] - m_use);
-    psum += pr[i];
-  }
-  st.l = st.l * alpha + psum;
-  u32x4_t pb;
-#pragma unroll
-  for (int w = 0; w < 4; ++w) pb[w] = pack_bf16x2_fast(pr[2 * w], pr[2 * w + 1]);
-#pragma unroll
-  for (int jj = 0; jj < 4; ++jj) st.o[jj] = mfma_bf16(v_operand_half(vrow, jj), pb, st.o[jj]);
 }
 
 // The fused append's 16 bytes of lane `lane` of row b's new K and V, for kv
@@ -996,18 +1046,35 @@ __device__ __forceinline__ void append_store(const AttnParams& p, int b, int kvg
   *reinterpret_cast<u32x4_t*>(const_cast<char*>(p.v_cache) + off) = vn;
 }
 
-__device__ void decode_segment_lds(const AttnParams& p, char* stage0, char* stage1, char* qlds,
-                                   const int32_t* bt, int b, int kvg, int ctx, int t0, int t1,
-                                   int split) {
+// One segment of a decode share: tiles t0 .. t1 of row b's kv group kvg,
+// written as a split partial when split >= 0.  (Block-table rows are formed
+// from the kernel argument where they are read, so the compiler keeps those
+// reads scalar.)
+struct DecSeg {
+  int b, kvg, ctx, t0, t1, split;
+};
+
+// `next(nx)` names the share's next segment (false: none); it is asked
+// after this segment's first loads are issued, so its reads overlap them.
+// Returns whether a next segment was found (its first loads are then in
+// flight: call it with `pre`).
+template <typename NextFn>
+__device__ __forceinline__ bool decode_segment_lds(const AttnParams& p, char* stage0, char* stage1,
+                                                   char* qlds,
+                                                   const int32_t* __restrict__ block_tables,
+                                                   const DecSeg& sg, bool pre, NextFn&& next,
+                                                   DecSeg& nx) {
   const LaneId L = lane_id();
   const int wave = uniform(int(threadIdx.x >> 6));
   const int gl = wave & 3;   // kv head within the group
   const int hf = wave >> 2;  // dim half
+  const int b = uniform(sg.b);
+  const int kvg = uniform(sg.kvg);
+  const int ctx = uniform(sg.ctx);
+  const int t0 = uniform(sg.t0);
+  const int t1 = uniform(sg.t1);
+  const int split = uniform(sg.split);
   const int g = kvg * 4 + gl;
-  b = uniform(b);
-  ctx = uniform(ctx);
-  t0 = uniform(t0);
-  t1 = uniform(t1);
   const int ntiles = t1 > t0 ? t1 - t0 : 0;
   const int c0 = t0 * kTile;
   // Fused append: the segment holding the row's last tile stores the new
@@ -1021,18 +1088,16 @@ __device__ void decode_segment_lds(const AttnParams& p, char* stage0, char* stag
 
   QOps<kBF16, 1> Q;
   HalfState st;
-#pragma unroll
-  for (int jj = 0; jj < 4; ++jj) st.o[jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  st.m = -INFINITY;
-  st.l = 0.f;
+  init_half(st);
+  bool has_next = false;
 
   const int tok = int(p.tok_bytes);
-  const int64_t grp_off = int64_t(kvg) * 1024;
-  // Wave w loads rows w, w + 8, w + 16, w + 24 of K and of V.
-  auto issue = [&](int tix, char* base) {
-    const int key0 = uniform(c0 + tix * kTile);
-    const int blk = uniform(bt[key0 / p.page]);
+  // Wave w loads rows w, w + 8, w + 16, w + 24 of K and of V of the tile at
+  // key0 of a segment's row (b_) and kv group (kvg_).
+  auto issue_tile = [&](int b_, int kvg_, int key0, char* base) {
+    const int blk = table_entry(block_tables, int64_t(b_) * p.bt_stride + key0 / p.page);
     const int64_t slot0 = int64_t(blk) * p.page + (key0 % p.page);
+    const int64_t grp_off = int64_t(kvg_) * 1024;
     const i32x4_t kr = raw_rsrc(p.k_cache + slot0 * p.tok_bytes + grp_off, kTile * tok);
     const i32x4_t vr = raw_rsrc(p.v_cache + slot0 * p.tok_bytes + grp_off, kTile * tok);
     const uint32_t lb = lds_addr(base);
@@ -1043,11 +1108,35 @@ __device__ void decode_segment_lds(const AttnParams& p, char* stage0, char* stag
       dma_to_lds(vr, row * tok + L.lane * 16, lb + kLdsTensor + row * kLdsPitch);
     }
   };
+  auto issue = [&](int tix, char* base) {
+    issue_tile(b, kvg, uniform(c0 + tix * kTile), base);
+  };
+  // The query rides the same DMA ahead of a segment's first two tiles: wave
+  // w brings columns 8 (w >> 2) .. + 7 of kv head w & 3 (columns past the
+  // head count repeat the last head; their results are never stored).
+  auto issue_q = [&](int b_, int kvg_) {
+    const int g_ = kvg_ * 4 + gl;
+    const i32x4_t qr =
+        raw_rsrc(p.q + int64_t(b_) * p.q_st, int(int64_t(p.num_heads) * p.q_sh * 2));
+    const uint32_t lb = lds_addr(qlds);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int col = 8 * hf + 4 * s + (L.lane >> 4);
+      const int head = g_ * p.group + min(col, p.hs - 1);
+      const int chunk = (L.lane & 15) ^ col;
+      dma_to_lds(qr, int(int64_t(head) * p.q_sh * 2) + chunk * 16,
+                 lb + (gl * 16 + 8 * hf + 4 * s) * 256);
+    }
+  };
 
   // Tile j lives in stage j & 1.  A stage is read into registers as soon as
   // its tile has landed and is refilled with tile j + 2 before tile j is
   // computed, so two tiles stay in flight under the arithmetic.  The loop is
-  // unrolled by two so every access names its stage statically.
+  // unrolled by two so every access names its stage statically.  At the
+  // last tile both stages and the query block are free: the next segment's
+  // query and first two tiles are issued there (its `pre`), so its start
+  // does not wait out a full load latency.  Barriers cover LDS only: the
+  // epilogue's global stores must not hold back the loads in flight.
   u32x4_t k[2][4];
   u32x2_t vh[8];
   auto read_stage = [&](const char* kb) {
@@ -1080,46 +1169,42 @@ __device__ void decode_segment_lds(const AttnParams& p, char* stage0, char* stag
     }
     if (app_wave && j == ntiles - 1) {
       // this wave's DMA of the row has landed (vmcnt(0) above); the pool
-      // store waits for the epilogue, where this segment drains its stores
+      // store is issued after the segment's last tile
       *reinterpret_cast<u32x4_t*>(stage + app_row * kLdsPitch + L.lane * 16) = app_kn;
       *reinterpret_cast<u32x4_t*>(stage + kLdsTensor + app_row * kLdsPitch + L.lane * 16) = app_vn;
     }
-    __syncthreads();
+    pf_barrier();
     read_stage(stage);
-    __builtin_amdgcn_s_waitcnt(0xC07F);    // lgkmcnt(0): the stage is in registers
-    __syncthreads();
+    pf_barrier();  // every wave holds the stage in registers
     if (j + 2 < ntiles) issue(j + 2, stage);
+    if (has_next && j == ntiles - 1) {
+      const int nb = uniform(nx.b);
+      const int nkvg = uniform(nx.kvg);
+      const int nc0 = uniform(nx.t0) * kTile;
+      issue_q(nb, nkvg);
+      issue_tile(nb, nkvg, nc0, stage0);
+      if (uniform(nx.t1) - uniform(nx.t0) > 1) issue_tile(nb, nkvg, nc0 + kTile, stage1);
+    }
     compute(j);
   };
-  // The query rides the same DMA ahead of the first two tiles: wave w brings
-  // columns 8 (w >> 2) .. + 7 of kv head w & 3 (columns past the head count
-  // repeat the last head; their results are never stored).
-  auto issue_q = [&]() {
-    const i32x4_t qr =
-        raw_rsrc(p.q + int64_t(b) * p.q_st, int(int64_t(p.num_heads) * p.q_sh * 2));
-    const uint32_t lb = lds_addr(qlds);
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const int col = 8 * hf + 4 * s + (L.lane >> 4);
-      const int head = g * p.group + min(col, p.hs - 1);
-      const int chunk = (L.lane & 15) ^ col;
-      dma_to_lds(qr, int(int64_t(head) * p.q_sh * 2) + chunk * 16,
-                 lb + (gl * 16 + 8 * hf + 4 * s) * 256);
-    }
-  };
   if (ntiles > 0) {
-    issue_q();
-    issue(0, stage0);
-    if (ntiles > 1) issue(1, stage1);
-    // Issued after the segment's first DMAs: every wait below still covers
-    // what it covered, as the youngest outstanding loads are the same.
+    if (!pre) {
+      issue_q(b, kvg);
+      issue(0, stage0);
+      if (ntiles > 1) issue(1, stage1);
+    }
+    has_next = next(nx);
+    // Issued after the segment's first DMAs (and, with `pre`, after the
+    // previous segment's output stores): the waits below count only the
+    // youngest loads as outstanding, so they can only wait longer, never
+    // less, than they name.
     if (app_wave) append_load(p, b, kvg, L.lane, app_kn, app_vn);
     if (ntiles > 1) {
       __builtin_amdgcn_s_waitcnt(0x4F70);  // vmcnt(16): this wave's query loads
     } else {
       __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8)
     }
-    __syncthreads();
+    pf_barrier();
     {
       const char* row = qlds + (gl * 16 + L.lm) * 256;
 #pragma unroll
@@ -1160,8 +1245,12 @@ __device__ void decode_segment_lds(const AttnParams& p, char* stage0, char* stag
       if (L.lg == 0 && hf == 0) p.part_lse[base] = l > 0.f ? st.m + __log2f(l) : -INFINITY;
     }
   }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
+  if (!has_next) {
+    // nothing in flight for a next segment: drain and realign the waves
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+  return has_next;
 }
 
 // The query against int8 key codes, as two int8 terms per dim: q ~= scale
@@ -1405,7 +1494,7 @@ __device__ void decode_segment_lds_i8(const AttnParams& p, char* ring, char* qld
   auto issue = [&](int tix) {
     char* base = stage_of(tix);
     const int key0 = uniform(c0 + tix * kTile);
-    const int blk = uniform(bt[key0 / p.page]);
+    const int blk = table_entry(bt, key0 / p.page);
     const int64_t slot0 = int64_t(blk) * p.page + (key0 % p.page);
     const i32x4_t kr = raw_rsrc(p.k_cache + slot0 * p.tok_bytes + grp_off, kTile * tok);
     const i32x4_t vr = raw_rsrc(p.v_cache + slot0 * p.tok_bytes + grp_off, kTile * tok);
@@ -1989,7 +2078,11 @@ paged_decode_sk_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
   __shared__ __align__(16) char smem[kBfLds ? kLdsStage : (kI8Lds ? kLdsI8 : kDecodeSmem)];
   __shared__ __align__(16) char smem1[kBfLds ? kLdsStage : 16];
   __shared__ __align__(16) char smem2[kLds ? kLdsQ : 16];
-  const int groups = (p.kvh * p.nslices) / p.kvs_per_wg;
+  touch_kernel_args(int(sizeof(AttnParams) + 2 * sizeof(void*)));
+  // kvs_per_wg divides 8 (a power of two)
+  const int groups = (p.kvh * p.nslices) >> __builtin_ctz(unsigned(p.kvs_per_wg));
+  const float rgroups = __builtin_amdgcn_rcpf(float(groups));
+  auto row_of = [&](int r) { return div_small(r, groups, rgroups); };
   const int R = p.n_dec * groups;
   const int w = blockIdx.x;
   const int lane = threadIdx.x & 63;
@@ -2001,14 +2094,13 @@ paged_decode_sk_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
   // the second pass (one round trip to memory for batches up to 256 x groups).
   constexpr int kCached = 4;
   int cl[kCached];
-  int row_cost = 0;
 #pragma unroll
-  for (int i = 0; i < kCached; ++i) cl[i] = r0 + i < r1 ? ctx_lens[(r0 + i) / groups] : 0;
+  for (int i = 0; i < kCached; ++i) cl[i] = r0 + i < r1 ? ctx_lens[row_of(r0 + i)] : 0;
   auto ctx_of = [&](int r) {
     int c = 0;
 #pragma unroll
     for (int i = 0; i < kCached; ++i) c = (r == r0 + i) ? cl[i] : c;
-    return r - r0 < kCached ? c : ctx_lens[r / groups];
+    return r - r0 < kCached ? c : ctx_lens[row_of(r)];
   };
   int mine = 0, tmax = 0, rows = 0;
   for (int r = r0; r < r1; ++r) {
@@ -2017,32 +2109,21 @@ paged_decode_sk_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
     tmax = max(tmax, t);
     rows += t > 0;
   }
+  // Wave prefix sums of the lanes' tiles and non-empty rows, and the
+  // longest row (DPP scans; lane 63 holds the totals).
+  const int tiles_incl = wave_scan_add(mine);
+  const int rows_incl = wave_scan_add(rows);
+  const int tsum = __builtin_amdgcn_readlane(tiles_incl, 63);
+  const int rsum = __builtin_amdgcn_readlane(rows_incl, 63);
+  const int Tmax = __builtin_amdgcn_readlane(wave_scan_max_nonneg(tmax), 63);
   // Rows of unequal length: each non-empty row also carries kDecRowCost
   // virtual tiles (a share that starts a second row pays the ring's restart:
   // its drain, query and first tiles), so such shares get fewer real tiles.
   // Equal rows keep shares aligned to rows and carry none.
-  {
-    int rsum = rows, tm = tmax, tsum = mine;
-#pragma unroll
-    for (int dd = 32; dd >= 1; dd >>= 1) {
-      rsum += __shfl_xor(rsum, dd, 64);
-      tm = max(tm, __shfl_xor(tm, dd, 64));
-      tsum += __shfl_xor(tsum, dd, 64);
-    }
-    const int cost = uniform(tsum == tm * rsum) ? 0 : kDecRowCost;
-    row_cost = cost;
-    mine += cost * rows;
-  }
-  int incl = mine;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int t = __shfl_up(incl, d, 64);
-    if (lane >= d) incl += t;
-  }
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) tmax = max(tmax, __shfl_xor(tmax, d, 64));
-  const int W = uniform(__shfl(incl, 63, 64));
-  const int Tmax = uniform(tmax);
+  const int row_cost = tsum == Tmax * rsum ? 0 : kDecRowCost;
+  mine += row_cost * rows;
+  const int incl = tiles_incl + row_cost * rows_incl;
+  const int W = tsum + row_cost * rsum;
   const int excl = incl - mine;
   int S = max(p.sk_min_share, (W + int(gridDim.x) - 1) / int(gridDim.x));
   const int need = p.max_splits > 1 ? (Tmax + p.max_splits - 2) / (p.max_splits - 1) : 1;
@@ -2053,8 +2134,9 @@ paged_decode_sk_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
   int d = int(p.xcd_skew * float(S) + 0.5f);
   d = max(0, min(d, min(S / 4, S - max(need, 1))));
   auto share_start = [&](int v) { return v * S + ((v & 1) ? d : 0); };
+  const float rS = __builtin_amdgcn_rcpf(float(S));
   auto share_of = [&](int x) {
-    int v = x / S;
+    int v = div_small(x, S, rS);
     if ((v & 1) && x - v * S < d) --v;
     return v;
   };
@@ -2077,21 +2159,23 @@ paged_decode_sk_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
         if (t == 0) {
           const int owner = W > 0 ? share_of(min(P, W - 1)) : 0;
           if (owner == w) {
-            write_nan_rows(p, r / groups, r % groups);
-            set_nseg(p, r / groups, r % groups, 0);
+            const int rb = row_of(r), rg = r - rb * groups;
+            write_nan_rows(p, rb, rg);
+            set_nseg(p, rb, rg, 0);
             if constexpr (kBfLds) {
               if (p.app_k != nullptr) {
                 // one lane holds this row unit here: it stores all 64 chunks
                 for (int c = 0; c < 64; ++c) {
                   u32x4_t kn, vn;
-                  append_load(p, r / groups, r % groups, c, kn, vn);
-                  append_store(p, r / groups, r % groups, c, kn, vn);
+                  append_load(p, rb, rg, c, kn, vn);
+                  append_store(p, rb, rg, c, kn, vn);
                 }
               }
             }
           }
         } else if (share_of(P + row_cost) == w) {
-          set_nseg(p, r / groups, r % groups,
+          const int rb = row_of(r);
+          set_nseg(p, rb, r - rb * groups,
                    share_of(P + row_cost + t - 1) - share_of(P + row_cost) + 1);
         }
       }
@@ -2099,34 +2183,54 @@ paged_decode_sk_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
     }
   }
   const unsigned long long hit = __ballot(found_r < R);
-  const int src = hit ? __ffsll(hit) - 1 : 0;
-  int r = uniform(__shfl(found_r, src, 64));
-  int P = uniform(__shfl(found_p, src, 64));
-  int ctx = uniform(__shfl(found_c, src, 64));
-  while (r < R && P < end) {
-    const int b = r / groups;
-    const int t = ctx_tiles(ctx);
-    const int Pr = P + row_cost;  // the row's first real tile
-    if (t > 0 && Pr < end) {
-      const int t0 = max(start, Pr) - Pr;
-      const int t1 = min(end, Pr + t) - Pr;
-      const int first_share = share_of(Pr);
-      const int nseg = share_of(Pr + t - 1) - first_share + 1;
-      const int split = nseg == 1 ? -1 : w - first_share;
-      if constexpr (kBfLds) {
-        decode_segment_lds(p, smem, smem1, smem2, block_tables + int64_t(b) * p.bt_stride, b,
-                           r - b * groups, ctx, t0, t1, split);
-      } else if constexpr (kI8Lds) {
-        decode_segment_lds_i8(p, smem, smem2, block_tables + int64_t(b) * p.bt_stride, b,
-                              r - b * groups, ctx, t0, t1, split);
+  const int src = uniform(hit ? __ffsll(hit) - 1 : 0);
+  int r = __builtin_amdgcn_readlane(found_r, src);
+  int P = __builtin_amdgcn_readlane(found_p, src);
+  int ctx = __builtin_amdgcn_readlane(found_c, src);
+  // The share's segments in order: each row unit with real tiles in
+  // [start, end).
+  auto next_seg = [&](DecSeg& sg) -> bool {
+    while (r < R && P < end) {
+      const int b = uniform(row_of(r));
+      const int t = ctx_tiles(ctx);
+      const int Pr = P + row_cost;  // the row's first real tile
+      bool hit = false;
+      if (t > 0 && Pr < end) {
+        const int first_share = share_of(Pr);
+        const int nseg = share_of(Pr + t - 1) - first_share + 1;
+        sg = DecSeg{b, r - b * groups, ctx, max(start, Pr) - Pr, min(end, Pr + t) - Pr,
+                    nseg == 1 ? -1 : w - first_share};
+        hit = true;
+      }
+      P += t > 0 ? t + row_cost : 0;
+      ++r;
+      if (r < R && P < end) ctx = table_entry(ctx_lens, row_of(r));
+      if (hit) return true;
+    }
+    return false;
+  };
+  if constexpr (kBfLds) {
+    // Each segment finds the next one (after issuing its own first loads)
+    // and issues that one's first loads under its own last tile.
+    DecSeg cur, nxt;
+    bool have = next_seg(cur);
+    bool pre = false;
+    while (have) {
+      have = decode_segment_lds(p, smem, smem1, smem2, block_tables, cur, pre, next_seg, nxt);
+      pre = have;
+      cur = nxt;
+    }
+  } else {
+    DecSeg sg;
+    while (next_seg(sg)) {
+      if constexpr (kI8Lds) {
+        decode_segment_lds_i8(p, smem, smem2, block_tables + int64_t(sg.b) * p.bt_stride, sg.b,
+                              sg.kvg, sg.ctx, sg.t0, sg.t1, sg.split);
       } else {
-        decode_segment<kEnc>(p, smem, block_tables + int64_t(b) * p.bt_stride, b,
-                             r - b * groups, ctx, t0, t1, split);
+        decode_segment<kEnc>(p, smem, block_tables + int64_t(sg.b) * p.bt_stride, sg.b, sg.kvg,
+                             sg.ctx, sg.t0, sg.t1, sg.split);
       }
     }
-    P += t > 0 ? t + row_cost : 0;
-    ++r;
-    if (r < R && P < end) ctx = uniform(ctx_lens[r / groups]);
   }
 }
 
@@ -2379,8 +2483,10 @@ mixed_sk_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t* _
           const int nseg = (P + t - 1) / S - P / S + 1;
           const int split = nseg == 1 ? -1 : w - P / S;
           if constexpr (kLds) {
-            decode_segment_lds(p, smem, smem1, smem2, block_tables + int64_t(b) * p.bt_stride,
-                               b, r - b * groups, ctx, t0, t1, split);
+            const DecSeg sg{b, r - b * groups, ctx, t0, t1, split};
+            DecSeg unused;
+            decode_segment_lds(p, smem, smem1, smem2, block_tables, sg, false,
+                               [](DecSeg&) { return false; }, unused);
           } else {
             decode_segment<kEnc>(p, smem, block_tables + int64_t(b) * p.bt_stride, b,
                                  r - b * groups, ctx, t0, t1, split);
@@ -2489,8 +2595,6 @@ constexpr int kPfMinShare = 4;
 // Prefill keys are read by every query tile of their chunk: keep them cached.
 constexpr bool kPfNonTemporal = KVC_PF_NT != 0;
 constexpr int kOob = 0x40000000;  // a buffer offset past every resource: reads 0, no traffic
-// s_waitcnt immediate for lgkmcnt(0) alone (vmcnt 63 and expcnt 7 do not wait).
-constexpr int kWaitLgkm0 = 0xC07F;
 static_assert(kPfTileLoads == 3 && kPfQLoadsPerWave == 9, "wait counts below assume these");
 static_assert(kPfStages >= 3 && 3 * (kPfStages - 1) + 9 * (kPfStages - 2) <= 45, "pf_wait_vm range");
 static_assert(kPfSmem <= 160 * 1024, "one workgroup per CU");
@@ -2563,25 +2667,6 @@ __device__ __forceinline__ void pf_wait_vm(int n) {
   }
 }
 
-// Workgroup barrier over LDS only: this wave's LDS accesses are complete and
-// every wave has arrived.  (__syncthreads would also wait for the epilogue's
-// global stores, and with them for every direct-to-LDS load in flight.)  The
-// wait and the barrier are builtins, so the compiler's wait-count model knows
-// the LDS queue is empty after it; the empty asm statements keep memory
-// accesses from moving across it.
-__device__ __forceinline__ void pf_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
-// Scalar loads (block-table entries, chunk bounds) are waited for right where
-// they are issued: while one is pending the compiler's wait-count model must
-// treat the LDS counter as out of order and waits for every LDS read before
-// the first use of any, which serialises the K and V operand reads with the
-// MFMAs.  With the queue drained here its LDS waits stay partial.
-__device__ __forceinline__ void smem_drain() { __builtin_amdgcn_s_waitcnt(kWaitLgkm0); }
 
 // One 32-key tile of the stream-K prefill against the wave's kPreNCB column
 // blocks (bf16 keys).  Differences from attend_tile, each removing VALU work:

@@ -118,6 +118,70 @@ __device__ __forceinline__ T uniform(T v) {
   return __builtin_amdgcn_readfirstlane(v);
 }
 
+// Entry idx of a table that nothing writes while the kernel runs (block
+// tables), read as one scalar load: the address is made wave-uniform and the
+// load goes through the constant address space, so it never becomes a vector
+// load whose wait would also drain the loads in flight.
+__device__ __forceinline__ int table_entry(const int32_t* table, int64_t idx) {
+  const uint64_t a = reinterpret_cast<uint64_t>(table + idx);
+  // (readfirstlane returns int: each half goes back through uint32_t so the
+  // low half is zero-extended, not sign-extended into the high word)
+  const uint32_t hi = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(a >> 32))));
+  const uint32_t lo = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(a))));
+  const uint64_t u = (uint64_t(hi) << 32) | uint64_t(lo);
+  return *reinterpret_cast<const __attribute__((address_space(4))) int32_t*>(u);
+}
+
+// Touch every 64-byte line of the kernel's argument block once, at entry:
+// the scalar loads issue together and are waited for once, so the
+// parameter reads spread through the kernel hit the scalar cache instead of
+// each first touch of a line being its own round trip to memory.
+__device__ __forceinline__ void touch_kernel_args(int bytes) {
+  const __attribute__((address_space(4))) char* k =
+      (const __attribute__((address_space(4))) char*)__builtin_amdgcn_kernarg_segment_ptr();
+  int acc = 0;
+#pragma unroll
+  for (int off = 0; off < 1024; off += 64)
+    if (off < bytes) acc ^= *(const __attribute__((address_space(4))) int*)(k + off);
+  asm volatile("" ::"s"(acc));
+}
+
+// floor(x / d) for 0 <= x < 2^24 with a quotient below 2^21, given rcp, 1 / d
+// to within a few ulp (v_rcp_f32): the float estimate is then within one of
+// the quotient, and one correction each way makes it exact.  (The compiler's
+// general int32 division is some thirty dependent instructions.)
+__device__ __forceinline__ int div_small(int x, int d, float rcp) {
+  int q = int(float(x) * rcp);
+  q += (q + 1) * d <= x ? 1 : 0;
+  q -= q * d > x ? 1 : 0;
+  return q;
+}
+
+// Inclusive prefix sum / running maximum over the 64 lanes of a wave (every
+// lane active), by DPP without LDS round trips: row_shr 1, 2, 4, 8 build the
+// prefix inside each 16-lane row (lanes shifted in from outside the row read
+// 0), then row_bcast:15 carries each row's last lane into the next row (rows
+// 1 and 3) and row_bcast:31 carries lane 31 into rows 2 and 3.  The maximum
+// form takes non-negative values (0 is its identity here).
+__device__ __forceinline__ int wave_scan_add(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31
+  return x;
+}
+__device__ __forceinline__ int wave_scan_max_nonneg(int x) {
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false));
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false));
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false));
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false));
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false));
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false));
+  return x;
+}
+
 __device__ __forceinline__ int64_t wrap_slot(int64_t s, int64_t num_slots) {
   return s < 0 ? s + num_slots : s;
 }
