@@ -2303,6 +2303,7 @@ mixed_sk_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t* _
   __shared__ __align__(16) char smem[kSmemBytes];
   __shared__ __align__(16) char smem1[kLds ? kLdsStage : 16];
   __shared__ __align__(16) char smem2[kLds ? kLdsQ : 16];
+  touch_kernel_args(int(sizeof(AttnParams) + 4 * sizeof(void*)));
   const int kvs_total = p.kvh * p.nslices;
   const int qtile = kWaves * kPreNCB * p.tpb;
   const int w = blockIdx.x;
@@ -2886,6 +2887,7 @@ __global__ void __launch_bounds__(kThreads)
 prefill_sk_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k,
                   const int32_t* __restrict__ block_tables) {
   __shared__ __align__(16) char lds[kPfSmem];
+  touch_kernel_args(int(sizeof(AttnParams) + 3 * sizeof(void*)));
   auto pf_dma = [](const i32x4_t& r, int voff, uint32_t dst) {
     if constexpr (kPfNonTemporal) {
       dma_to_lds(r, voff, dst);
@@ -3454,6 +3456,7 @@ prefill_sk2_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t
                    const int32_t* __restrict__ block_tables) {
   __shared__ __align__(16) char lds[kP2Smem];
   __shared__ int4 ctab[64];
+  touch_kernel_args(int(sizeof(AttnParams) + 3 * sizeof(void*)));
   const LaneId L = lane_id();
   const int wave = uniform(int(threadIdx.x >> 6));
   const int kvs_total = p.kvh * p.nslices;
@@ -3994,6 +3997,7 @@ prefill_sk2_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t
 constexpr int kMergeWaves = 4;
 constexpr int kMergeBatch = 16;
 __global__ void __launch_bounds__(64 * kMergeWaves) merge_kernel(AttnParams p, int num_rows) {
+  touch_kernel_args(int(sizeof(AttnParams) + sizeof(int)));
   const int lane = threadIdx.x & 63;
   const int64_t wv = int64_t(blockIdx.x) * kMergeWaves + (threadIdx.x >> 6);
   const int64_t row = wv / p.num_heads;
@@ -4089,6 +4093,7 @@ constexpr int kSliceBatch = 4;  // splits per load batch (124 VGPRs: every wave 
 __global__ void __launch_bounds__(64 * kMergeWaves)
 merge_slices_kernel(AttnParams p, int num_rows, const float* __restrict__ part_o,
                     const float* __restrict__ part_lse, const int* __restrict__ nseg_arr) {
+  touch_kernel_args(int(sizeof(AttnParams) + 4 * sizeof(void*)));
   const int lane = threadIdx.x & 63;
   const int e = lane >> 3;   // head within the pass
   const int sub = lane & 7;  // 16-dim chunk
