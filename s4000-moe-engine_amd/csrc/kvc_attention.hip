@@ -2065,26 +2065,23 @@ __device__ void write_nan_rows(const AttnParams& p, int b, int kvg) {
 // the launch and the first KV load.  Wave 0 also records each row's split
 // count (from the share holding its first tile) and writes NaN rows for
 // empty contexts.
+// One workgroup's share (share w of `grid`) of a stream-K decode launch.
+// kLds: 4 kv heads per workgroup staged through LDS, bf16
+// (decode_segment_lds: two stages in smem and smem1) or per-token-head int8
+// (decode_segment_lds_i8: a four-stage ring in smem); smem2 holds the query.
 template <int kEnc, bool kLds>
-__global__ void __launch_bounds__(kThreads)
-paged_decode_sk_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
-                       const int32_t* __restrict__ ctx_lens) {
-  // kLds: 4 kv heads per workgroup staged through LDS, bf16
-  // (decode_segment_lds: two stages) or per-token-head int8
-  // (decode_segment_lds_i8: a four-stage ring); smem2 holds the query.
+__device__ __forceinline__ void decode_sk_share(const AttnParams& p,
+                                                const int32_t* __restrict__ block_tables,
+                                                const int32_t* __restrict__ ctx_lens, int w,
+                                                int grid, char* smem, char* smem1, char* smem2) {
   constexpr bool kBfLds = kLds && kEnc == kBF16;
   constexpr bool kI8Lds = kLds && kEnc == kI8Tok;
   static_assert(!kLds || kBfLds || kI8Lds, "no LDS-staged form for this encoding");
-  __shared__ __align__(16) char smem[kBfLds ? kLdsStage : (kI8Lds ? kLdsI8 : kDecodeSmem)];
-  __shared__ __align__(16) char smem1[kBfLds ? kLdsStage : 16];
-  __shared__ __align__(16) char smem2[kLds ? kLdsQ : 16];
-  touch_kernel_args(int(sizeof(AttnParams) + 2 * sizeof(void*)));
   // kvs_per_wg divides 8 (a power of two)
   const int groups = (p.kvh * p.nslices) >> __builtin_ctz(unsigned(p.kvs_per_wg));
   const float rgroups = __builtin_amdgcn_rcpf(float(groups));
   auto row_of = [&](int r) { return div_small(r, groups, rgroups); };
   const int R = p.n_dec * groups;
-  const int w = blockIdx.x;
   const int lane = threadIdx.x & 63;
   const int wave = uniform(int(threadIdx.x >> 6));
   const int per_lane = (R + 63) / 64;
@@ -2125,7 +2122,7 @@ paged_decode_sk_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
   const int incl = tiles_incl + row_cost * rows_incl;
   const int W = tsum + row_cost * rsum;
   const int excl = incl - mine;
-  int S = max(p.sk_min_share, (W + int(gridDim.x) - 1) / int(gridDim.x));
+  int S = max(p.sk_min_share, (W + grid - 1) / grid);
   const int need = p.max_splits > 1 ? (Tmax + p.max_splits - 2) / (p.max_splits - 1) : 1;
   S = max(S, need);
   // XCD-aware shares: workgroup v runs on XCD v mod 8, and the odd XCDs
@@ -2232,6 +2229,20 @@ paged_decode_sk_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
       }
     }
   }
+}
+
+template <int kEnc, bool kLds>
+__global__ void __launch_bounds__(kThreads)
+paged_decode_sk_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
+                       const int32_t* __restrict__ ctx_lens) {
+  constexpr bool kBfLds = kLds && kEnc == kBF16;
+  constexpr bool kI8Lds = kLds && kEnc == kI8Tok;
+  __shared__ __align__(16) char smem[kBfLds ? kLdsStage : (kI8Lds ? kLdsI8 : kDecodeSmem)];
+  __shared__ __align__(16) char smem1[kBfLds ? kLdsStage : 16];
+  __shared__ __align__(16) char smem2[kLds ? kLdsQ : 16];
+  touch_kernel_args(int(sizeof(AttnParams) + 2 * sizeof(void*)));
+  decode_sk_share<kEnc, kLds>(p, block_tables, ctx_lens, int(blockIdx.x), int(gridDim.x), smem,
+                              smem1, smem2);
 }
 
 // ---------------------------------------------------------------------------
@@ -3450,19 +3461,20 @@ __device__ __forceinline__ void p2_next_item(PfItem& it, const int4* ctab, const
   it.T = it.i < n_pre ? qtile_tiles(it.geo, qtile, it.qt) : 0;
 }
 
+// One workgroup's share (workgroup v of G) of a stream-K prefill launch;
+// lds holds the ring, the query regions and the dummy block (kP2Smem bytes),
+// ctab the first 64 chunks' geometry.
 template <bool kFresh>
-__global__ void __launch_bounds__(kThreads)
-prefill_sk2_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k,
-                   const int32_t* __restrict__ block_tables) {
-  __shared__ __align__(16) char lds[kP2Smem];
-  __shared__ int4 ctab[64];
-  touch_kernel_args(int(sizeof(AttnParams) + 3 * sizeof(void*)));
+__device__ __forceinline__ void prefill_sk2_share(const AttnParams& p,
+                                                  const int32_t* __restrict__ cu_q,
+                                                  const int32_t* __restrict__ cu_k,
+                                                  const int32_t* __restrict__ block_tables,
+                                                  const int v, const int G, char* lds,
+                                                  int4* ctab) {
   const LaneId L = lane_id();
   const int wave = uniform(int(threadIdx.x >> 6));
   const int kvs_total = p.kvh * p.nslices;
   const int qtile = kWaves * kPreNCB * p.tpb;
-  const int G = int(gridDim.x);
-  const int v = int(blockIdx.x);
   // Consecutive shares run on one XCD (workgroup v is placed on XCD v mod 8).
   const int w = (G % 8 == 0) ? (v % 8) * (G / 8) + v / 8 : v;
 
@@ -3989,6 +4001,40 @@ prefill_sk2_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t
   __builtin_amdgcn_s_waitcnt(0);
 }
 
+template <bool kFresh>
+__global__ void __launch_bounds__(kThreads)
+prefill_sk2_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k,
+                   const int32_t* __restrict__ block_tables) {
+  __shared__ __align__(16) char lds[kP2Smem];
+  __shared__ int4 ctab[64];
+  touch_kernel_args(int(sizeof(AttnParams) + 3 * sizeof(void*)));
+  prefill_sk2_share<kFresh>(p, cu_q, cu_k, block_tables, int(blockIdx.x), int(gridDim.x), lds,
+                            ctab);
+}
+
+// A mixed call's decode rows and prefill rows in one launch over a static
+// CU split: workgroups [0, dec_wgs) run the stream-K decode over dec_wgs
+// shares (bf16 pool, LDS-staged), the others the stream-K prefill over the
+// rest.  dec_wgs is a multiple of 8, so both sides keep their XCD placement
+// (workgroup b runs on XCD b mod 8).  Each side plans, and is merged, as its
+// own launch would be.
+constexpr int kMixSplitLds = 2 * kLdsStage + kLdsQ;
+static_assert(kMixSplitLds >= kP2Smem + 64 * int(sizeof(int4)), "one LDS block serves both sides");
+__global__ void __launch_bounds__(kThreads)
+mixed_split_kernel(AttnParams pd, AttnParams pp, int dec_wgs) {
+  __shared__ __align__(16) char lds[kMixSplitLds];
+  touch_kernel_args(int(2 * sizeof(AttnParams) + sizeof(int)));
+  const int b = int(blockIdx.x);
+  if (b < dec_wgs) {
+    decode_sk_share<kBF16, true>(pd, pd.block_tables, pd.ctx_lens, b, dec_wgs, lds,
+                                 lds + kLdsStage, lds + 2 * kLdsStage);
+  } else {
+    prefill_sk2_share<false>(pp, pp.cu_q, pp.cu_k, pp.block_tables, b - dec_wgs,
+                             int(gridDim.x) - dec_wgs, lds,
+                             reinterpret_cast<int4*>(lds + kP2Smem));
+  }
+}
+
 // Split-K merge: one wave per (query row, head), lane l owning dims 2l and
 // 2l + 1.  The splits are taken 16 at a time with every load of a batch in
 // flight together (log-sum-exps are wave-uniform), so a row split 16 ways
@@ -3996,10 +4042,10 @@ prefill_sk2_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t
 // the attention kernel and are skipped.
 constexpr int kMergeWaves = 4;
 constexpr int kMergeBatch = 16;
-__global__ void __launch_bounds__(64 * kMergeWaves) merge_kernel(AttnParams p, int num_rows) {
-  touch_kernel_args(int(sizeof(AttnParams) + sizeof(int)));
+// Block `block` of the split merge of a decode launch (merge_kernel).
+__device__ __forceinline__ void merge_rows(const AttnParams& p, int num_rows, int64_t block) {
   const int lane = threadIdx.x & 63;
-  const int64_t wv = int64_t(blockIdx.x) * kMergeWaves + (threadIdx.x >> 6);
+  const int64_t wv = block * kMergeWaves + (threadIdx.x >> 6);
   const int64_t row = wv / p.num_heads;
   if (row >= num_rows) return;
   const int head = int(wv - row * p.num_heads);
@@ -4078,6 +4124,11 @@ __global__ void __launch_bounds__(64 * kMergeWaves) merge_kernel(AttnParams p, i
   *reinterpret_cast<uint32_t*>(dst) = pack_bf16x2_fast(acc0 * inv, acc1 * inv);
 }
 
+__global__ void __launch_bounds__(64 * kMergeWaves) merge_kernel(AttnParams p, int num_rows) {
+  touch_kernel_args(int(sizeof(AttnParams) + sizeof(int)));
+  merge_rows(p, num_rows, blockIdx.x);
+}
+
 void launch_merge(const AttnParams& p, int64_t rows, hipStream_t st) {
   const int64_t waves = rows * p.num_heads;
   merge_kernel<<<unsigned((waves + kMergeWaves - 1) / kMergeWaves), 64 * kMergeWaves, 0, st>>>(
@@ -4090,15 +4141,18 @@ void launch_merge(const AttnParams& p, int64_t rows, hipStream_t st) {
 // so a whole slice's partials are in flight together and a row costs two
 // memory round trips (the count, then the partials) whatever its head count.
 constexpr int kSliceBatch = 4;  // splits per load batch (124 VGPRs: every wave resident)
-__global__ void __launch_bounds__(64 * kMergeWaves)
-merge_slices_kernel(AttnParams p, int num_rows, const float* __restrict__ part_o,
-                    const float* __restrict__ part_lse, const int* __restrict__ nseg_arr) {
-  touch_kernel_args(int(sizeof(AttnParams) + 4 * sizeof(void*)));
+// Block `block` of the split merge of a stream-K prefill launch
+// (merge_slices_kernel).
+__device__ __forceinline__ void merge_slice_rows(const AttnParams& p, int num_rows,
+                                                 const float* __restrict__ part_o,
+                                                 const float* __restrict__ part_lse,
+                                                 const int* __restrict__ nseg_arr,
+                                                 int64_t block) {
   const int lane = threadIdx.x & 63;
   const int e = lane >> 3;   // head within the pass
   const int sub = lane & 7;  // 16-dim chunk
   const int kvs_total = p.kvh * p.nslices;
-  const int64_t wv = int64_t(blockIdx.x) * kMergeWaves + (threadIdx.x >> 6);
+  const int64_t wv = block * kMergeWaves + (threadIdx.x >> 6);
   const int64_t row = wv / kvs_total;
   if (row >= num_rows) return;
   const int kvs = int(wv - row * kvs_total);
@@ -4170,6 +4224,27 @@ merge_slices_kernel(AttnParams p, int num_rows, const float* __restrict__ part_o
   }
 }
 
+__global__ void __launch_bounds__(64 * kMergeWaves)
+merge_slices_kernel(AttnParams p, int num_rows, const float* __restrict__ part_o,
+                    const float* __restrict__ part_lse, const int* __restrict__ nseg_arr) {
+  touch_kernel_args(int(sizeof(AttnParams) + 4 * sizeof(void*)));
+  merge_slice_rows(p, num_rows, part_o, part_lse, nseg_arr, blockIdx.x);
+}
+
+// Both merges of a mixed call's split launch in one launch: blocks
+// [0, dec_blocks) merge the decode rows' splits, the others the prefill
+// rows' splits.
+__global__ void __launch_bounds__(64 * kMergeWaves)
+merge_mixed_kernel(AttnParams pd, AttnParams pp, int dec_rows, int dec_blocks, int pre_rows) {
+  touch_kernel_args(int(2 * sizeof(AttnParams) + 3 * sizeof(int)));
+  const int64_t b = blockIdx.x;
+  if (b < dec_blocks) {
+    merge_rows(pd, dec_rows, b);
+  } else {
+    merge_slice_rows(pp, pre_rows, pp.part_o, pp.part_lse, pp.sk_nseg, b - dec_blocks);
+  }
+}
+
 void launch_merge_slices(const AttnParams& p, int64_t rows, hipStream_t st) {
   const int64_t waves = rows * p.kvh * p.nslices;
   merge_slices_kernel<<<unsigned((waves + kMergeWaves - 1) / kMergeWaves), 64 * kMergeWaves, 0,
@@ -4206,6 +4281,26 @@ struct LaunchCus {
   int saved;
   explicit LaunchCus(int n) : saved(tl_launch_cus) { tl_launch_cus = n; }
   ~LaunchCus() { tl_launch_cus = saved; }
+};
+
+// A stream-K launch recorded instead of launched: while tl_record is set,
+// the paged decode entry point (bf16 pool, LDS-staged, no append) and the
+// prefill-only entry point (stream-K launch over cached bf16 keys) validate,
+// plan and fill their parameters as usual, store them here and return
+// without launching the kernel or its merge.  A mixed call then runs both in
+// one mixed_split_kernel launch.  An entry point that cannot take this form
+// launches as usual and leaves `taken` false.
+struct SkRecord {
+  bool taken = false;
+  AttnParams p{};
+  int grid = 0;
+  int64_t rows = 0;  // rows its merge covers
+};
+thread_local SkRecord* tl_record = nullptr;
+struct RecordInto {
+  SkRecord* saved;
+  explicit RecordInto(SkRecord* r) : saved(tl_record) { tl_record = r; }
+  ~RecordInto() { tl_record = saved; }
 };
 int device_cus();
 int launch_cus() { return tl_launch_cus > 0 ? tl_launch_cus : device_cus(); }
@@ -4420,48 +4515,32 @@ bool split_mixed(int64_t num_decode_rows, int64_t page_size) {
          env_int("KVC_MIXED_SPLIT", 1) != 0;
 }
 
-// A mixed call's decode launch can run beside its prefill launch: on a side
-// stream of the library's (one per device, default priority, non-blocking),
-// forked from and joined back into the caller's stream with events.  The
-// decode launch is HBM-bound and the prefill launch MFMA-bound, and each of
-// their workgroups takes a whole CU's LDS, so two launches of G_d and
-// CUs - G_d workgroups split the CUs between them.
-struct SideStream {
-  hipStream_t s = nullptr;
-  hipEvent_t fork = nullptr;
-  hipEvent_t join = nullptr;
-  std::mutex mu;
-  bool ok = false;
-};
-
-SideStream* side_stream() {
-  static SideStream streams[64];
-  static std::mutex init_mu;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-  std::lock_guard<std::mutex> lk(init_mu);
-  SideStream& ss = streams[dev];
-  if (!ss.ok) {
-    if (ss.s == nullptr && hipStreamCreateWithFlags(&ss.s, hipStreamNonBlocking) != hipSuccess)
-      return nullptr;
-    if (ss.fork == nullptr && hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming) != hipSuccess)
-      return nullptr;
-    if (ss.join == nullptr && hipEventCreateWithFlags(&ss.join, hipEventDisableTiming) != hipSuccess)
-      return nullptr;
-    ss.ok = true;
-  }
-  return &ss;
-}
-
-// CUs given to the decode launch of a mixed call when it runs beside the
-// prefill launch (0: the two launches run one after the other).
-// KVC_MIXED_DECODE_CUS overrides (rounded down to a multiple of 8).
-int mixed_decode_cus(int64_t num_decode_rows, int64_t num_prefill_tokens) {
-  const int total = device_cus();
-  int n = env_int("KVC_MIXED_DECODE_CUS", 0);
+// Workgroups (= CUs) the decode side of a mixed call's split launch gets
+// (mixed_split_kernel: decode rows on dec_wgs CUs, prefill rows on the rest
+// at once; 0: the decode launch, then the prefill launch).  The split form
+// needs both sides in their stream-K forms: a bf16 pool with 4 kv heads per
+// decode workgroup (LDS-staged) and the stream-K prefill.
+// KVC_MIXED_DECODE_CUS sets the count (rounded down to a multiple of 8; 0:
+// the two launches one after the other).  By default the decode side gets
+// 3/8 of the CUs: the decode rows are HBM-bound and keep most of their rate
+// on fewer CUs, the prefill is MFMA-bound and scales with its CUs (on a mix
+// of 60 decode rows of U[256,4096] and four 256-token chunks the two sides
+// then take about the same time).
+int mixed_decode_cus(int64_t num_decode_rows, int64_t num_prefill_tokens, int kv_dtype,
+                     int64_t num_heads, int64_t num_kv_heads) {
   if (num_decode_rows <= 0 || num_prefill_tokens <= 0) return 0;
+  if (kv_dtype != KVC_KV_BF16 || mixed_stream_k() || env_int("KVC_DECODE_STREAMK", 1) == 0 ||
+      env_int("KVC_DECODE_LDS", 1) == 0 || env_int("KVC_PREFILL_SK", 1) == 0 ||
+      env_int("KVC_PF_RING", 0) != 0)
+    return 0;
+  const HeadPlan hp = plan_heads(num_heads, num_kv_heads);
+  if (hp.kvs_per_wg != 4 || hp.nslices != 1) return 0;
+  const int total = device_cus();
+  if (total < 16 || total % 8 != 0) return 0;
+  int n = env_int("KVC_MIXED_DECODE_CUS", -1);
+  if (n < 0) n = total * 3 / 8;
   n = n / 8 * 8;
-  return (n > 0 && n <= total) ? n : 0;
+  return (n >= 8 && n <= total - 8) ? n : 0;
 }
 
 // Prefill-only launches over bf16 keys run as one stream-K launch
@@ -4642,6 +4721,13 @@ int paged_decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, con
                           2, stream);
         if (rc != KVC_OK) return rc;
       }
+    }
+    if (tl_record != nullptr && kv_dtype == KVC_KV_BF16 && lds_bf16 && p.app_k == nullptr) {
+      tl_record->taken = true;
+      tl_record->p = p;
+      tl_record->grid = sp.grid;
+      tl_record->rows = batch;
+      return KVC_OK;
     }
     switch (kv_dtype) {
       case KVC_KV_BF16:
@@ -4960,22 +5046,28 @@ extern "C" int kvc_varlen_attention(
                 dec_span + pre_ws, workspace_bytes);
     char* ws = static_cast<char*>(workspace);
     const int64_t nd = num_decode_rows;
-    const int dec_cus = mixed_decode_cus(nd, num_q_tokens - nd);
-    SideStream* ss = dec_cus > 0 ? side_stream() : nullptr;
-    if (ss != nullptr) {
-      // Decode rows on the side stream with dec_cus workgroups, prefill rows
-      // on the caller's stream with the other CUs, joined before returning.
-      std::lock_guard<std::mutex> lk(ss->mu);
+    const int dec_cus = mixed_decode_cus(nd, num_q_tokens - nd, kv_dtype, num_heads, num_kv_heads);
+    if (dec_cus > 0) {
+      // One launch over a static CU split (mixed_split_kernel): the decode
+      // rows planned for dec_cus workgroups, the prefill rows for the rest,
+      // each recorded by its own entry point, then both merges.
       hipStream_t main_st = as_stream(stream);
-      KVC_REQUIRE(hipEventRecord(ss->fork, main_st) == hipSuccess &&
-                      hipStreamWaitEvent(ss->s, ss->fork, 0) == hipSuccess,
-                  KVC_ERR_RUNTIME, "varlen_attention: fork to the side stream failed");
-      // dec_cus == every CU: the prefill launch goes first with every CU and
-      // the decode launch's workgroups take the CUs its shares leave.
-      const bool tail = dec_cus >= device_cus();
-      auto launch_prefill = [&]() {
-        LaunchCus cus(tail ? device_cus() : device_cus() - dec_cus);
-        return kvc_varlen_attention(
+      SkRecord rd, rp;
+      {
+        LaunchCus cus(dec_cus);
+        RecordInto rec(&rd);
+        rc = kvc_paged_decode(q, q_stride_t, q_stride_h, k_cache, v_cache, num_cache_blocks,
+                              page_size, num_kv_heads, head_dim, kv_dtype, k_scale, v_scale,
+                              side_k, side_v, out_idx2d, head_n_out, n_out_max, block_tables,
+                              bt_stride, max_blocks_per_seq, decode_context_lens, nd, num_heads,
+                              scale, out, out_stride_t, out_stride_h, dec_ws ? ws : nullptr,
+                              dec_ws, stream);
+      }
+      if (rc != KVC_OK) return rc;
+      {
+        LaunchCus cus(device_cus() - dec_cus);
+        RecordInto rec(&rp);
+        rc = kvc_varlen_attention(
             static_cast<const uint16_t*>(q) + nd * q_stride_t, q_stride_t, q_stride_h,
             num_q_tokens - nd, num_heads, k_cache, v_cache, num_cache_blocks, page_size,
             num_kv_heads, head_dim, kv_dtype, k_scale, v_scale, side_k, side_v, out_idx2d,
@@ -4984,26 +5076,33 @@ extern "C" int kvc_varlen_attention(
             num_prefill_units, max_seqlen_k, scale,
             static_cast<uint16_t*>(out) + nd * out_stride_t, out_stride_t, out_stride_h,
             pre_ws ? ws + dec_span : nullptr, pre_ws, stream);
-      };
-      int rc_p = KVC_OK;
-      if (tail) rc_p = launch_prefill();
-      int rc_d = KVC_OK;
-      if (rc_p == KVC_OK) {
-        LaunchCus cus(dec_cus);
-        rc_d = kvc_paged_decode(q, q_stride_t, q_stride_h, k_cache, v_cache, num_cache_blocks,
-                                page_size, num_kv_heads, head_dim, kv_dtype, k_scale, v_scale,
-                                side_k, side_v, out_idx2d, head_n_out, n_out_max, block_tables,
-                                bt_stride, max_blocks_per_seq, decode_context_lens, nd, num_heads,
-                                scale, out, out_stride_t, out_stride_h, dec_ws ? ws : nullptr,
-                                dec_ws, reinterpret_cast<kvc_stream_t>(ss->s));
       }
-      const bool joined = hipEventRecord(ss->join, ss->s) == hipSuccess;
-      if (!tail && rc_d == KVC_OK) rc_p = launch_prefill();
-      const bool waited = joined && hipStreamWaitEvent(main_st, ss->join, 0) == hipSuccess;
-      if (rc_d != KVC_OK) return rc_d;
-      if (rc_p != KVC_OK) return rc_p;
-      KVC_REQUIRE(waited, KVC_ERR_RUNTIME, "varlen_attention: join of the side stream failed");
-      return KVC_OK;
+      if (rc != KVC_OK) return rc;
+      if (rd.taken && rp.taken) {
+        mixed_split_kernel<<<rd.grid + rp.grid, kThreads, 0, main_st>>>(rd.p, rp.p, rd.grid);
+        rc = check_launch("varlen_attention");
+        if (rc != KVC_OK) return rc;
+      } else if (rd.taken) {
+        paged_decode_sk_kernel<kBF16, true>
+            <<<rd.grid, kThreads, 0, main_st>>>(rd.p, rd.p.block_tables, rd.p.ctx_lens);
+        rc = check_launch("varlen_attention decode");
+        if (rc != KVC_OK) return rc;
+      } else if (rp.taken) {
+        launch_prefill_sk(rp.p, rp.grid, false, main_st);
+        rc = check_launch("varlen_attention prefill");
+        if (rc != KVC_OK) return rc;
+      }
+      if (rd.taken && rp.taken) {
+        const int64_t dec_blocks = (rd.rows * rd.p.num_heads + kMergeWaves - 1) / kMergeWaves;
+        const int64_t pre_blocks =
+            (rp.rows * rp.p.kvh * rp.p.nslices + kMergeWaves - 1) / kMergeWaves;
+        merge_mixed_kernel<<<unsigned(dec_blocks + pre_blocks), 64 * kMergeWaves, 0, main_st>>>(
+            rd.p, rp.p, int(rd.rows), int(dec_blocks), int(rp.rows));
+      } else {
+        if (rd.taken) launch_merge(rd.p, rd.rows, main_st);
+        if (rp.taken) launch_merge_slices(rp.p, rp.rows, main_st);
+      }
+      return check_launch("varlen_attention merge");
     }
     rc = kvc_paged_decode(q, q_stride_t, q_stride_h, k_cache, v_cache, num_cache_blocks,
                           page_size, num_kv_heads, head_dim, kv_dtype, k_scale, v_scale, side_k,
@@ -5129,6 +5228,13 @@ extern "C" int kvc_varlen_attention(
     p.sk_nseg = reinterpret_cast<int*>(static_cast<char*>(workspace) +
                                        sk_partial_part(num_q_tokens, num_heads, p.max_splits));
     hipStream_t st = as_stream(stream);
+    if (num_prefill > 0 && tl_record != nullptr && !fresh && env_int("KVC_PF_RING", 0) == 0) {
+      tl_record->taken = true;
+      tl_record->p = p;
+      tl_record->grid = sp.grid;
+      tl_record->rows = num_q_tokens;
+      return KVC_OK;
+    }
     if (num_prefill > 0) {
       launch_prefill_sk(p, sp.grid, fresh, st);
       rc = check_launch("varlen_attention");
