@@ -24,7 +24,10 @@
 // run register segments (K/V straight from HBM into VGPRs, the next tile in
 // flight).  Prefill: a stream-K launch over (chunk, kv slice, query tile)
 // items whose 32-key tiles stream through a four-stage LDS ring, every tile
-// consumed by eight waves of different query columns.
+// consumed by eight waves of different query columns.  A mixed call over a
+// bf16 pool runs both in one launch over a static CU split (decode shares on
+// the first workgroups, prefill shares on the rest) and both merges in one
+// more launch.
 #include <atomic>
 #include <cmath>
 #include <cstdlib>
