@@ -466,8 +466,8 @@ def run_mixed(args, torch):
     kv = sum(dec) * 2 * kvh * 128 * 2
     pre_tflops = flops / (ms_pre * 1e-3) / 1e12
     res = {"workload": "mixed: 60 decode rows ctx U[256,4096] + 4x256-token prefill chunks "
-                        "(prefix 0/512/2048/8192): paged decode launch + stream-K prefill "
-                        "launch + their merges",
+                        "(prefix 0/512/2048/8192): one launch over a CU split (stream-K decode "
+                        "+ stream-K prefill) + one merge launch",
             "ms": round(ms, 4), "prefill_gflop": round(flops / 1e9, 2),
             "prefill_only_ms": round(ms_pre, 4),
             "prefill_TFLOPs": round(pre_tflops, 1),
