@@ -45,9 +45,11 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kSideMax = 8;
 constexpr int kPreNCB = 2;  // column blocks per wave in prefill units
 constexpr float kRescaleLog2 = 8.f;  // lazy-rescale threshold (log2 units)
-// Virtual tiles per row of a ragged stream-K decode (see paged_decode_sk_kernel).
+// Virtual tiles per row of a ragged stream-K decode (see decode_sk_share):
+// on 64 rows of U[512,4096], 1 / 2 / 3 / 4 measured 51.6 / 51.4 / 51.1 /
+// 51.1 us.
 #ifndef KVC_DEC_ROW_COST
-#define KVC_DEC_ROW_COST 2
+#define KVC_DEC_ROW_COST 3
 #endif
 constexpr int kDecRowCost = KVC_DEC_ROW_COST;
 
