@@ -2299,18 +2299,6 @@ __device__ __forceinline__ int64_t qtile_cum(const ChunkGeo& c, int tpb, int q) 
   return s;
 }
 
-__device__ __forceinline__ int wave_sum(int v) {
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
-  return v;
-}
-
-__device__ __forceinline__ int wave_max(int v) {
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) v = max(v, __shfl_xor(v, d, 64));
-  return v;
-}
-
 template <int kEnc, bool kFresh, bool kLds>
 __global__ void __launch_bounds__(kThreads)
 mixed_sk_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k,
@@ -2366,13 +2354,8 @@ mixed_sk_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t* _
     mine += t;
     tmax = max(tmax, t);
   }
-  int incl = mine;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int t = __shfl_up(incl, d, 64);
-    if (lane >= d) incl += t;
-  }
-  const int Wdec = uniform(__shfl(incl, 63, 64));
+  const int incl = wave_scan_add(mine);
+  const int Wdec = uniform(__builtin_amdgcn_readlane(incl, 63));
   Tmax = uniform(max(Tmax, wave_max(tmax)));
   const int W = Wpre + Wdec;
   int S = max(p.sk_min_share, (W + int(gridDim.x) - 1) / int(gridDim.x));
@@ -2419,18 +2402,13 @@ mixed_sk_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t* _
     for (int c0 = 0; c0 < p.n_pre; c0 += 64) {
       int tm;
       const int t = chunk_tiles(c0 + lane, tm);
-      int inc = t;
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const int u = __shfl_up(inc, d, 64);
-        if (lane >= d) inc += u;
-      }
-      const int total = uniform(__shfl(inc, 63, 64));
+      const int inc = wave_scan_add(t);
+      const int total = uniform(__builtin_amdgcn_readlane(inc, 63));
       if (start < base + total) {
         const unsigned long long hit = __ballot(t > 0 && base + inc - t <= start && start < base + inc);
         const int src = __ffsll(hit) - 1;
         i = uniform(c0 + src);
-        P = uniform(base + __shfl(inc - t, src, 64));
+        P = uniform(base + __builtin_amdgcn_readlane(inc - t, src));
         break;
       }
       base += total;
@@ -2451,9 +2429,9 @@ mixed_sk_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t* _
   } else {
     const unsigned long long hit = __ballot(found_r < R);
     const int src = hit ? __ffsll(hit) - 1 : 0;
-    r = uniform(__shfl(found_r, src, 64));
-    P = uniform(__shfl(found_p, src, 64));
-    ctx = uniform(__shfl(found_c, src, 64));
+    r = uniform(__builtin_amdgcn_readlane(found_r, src));
+    P = uniform(__builtin_amdgcn_readlane(found_p, src));
+    ctx = uniform(__builtin_amdgcn_readlane(found_c, src));
   }
 
   while (P < end) {
@@ -2972,26 +2950,21 @@ prefill_sk_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t*
           if (c.ntq > 0) t = kvs_total * pf_qcum(c, p.tpb, c.ntq);
         }
       }
-      int inc = t;
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const int u = __shfl_up(inc, d, 64);
-        if (L.lane >= d) inc += u;
-      }
-      const int total = uniform(__shfl(inc, 63, 64));
+      const int inc = wave_scan_add(t);
+      const int total = uniform(__builtin_amdgcn_readlane(inc, 63));
       if (start < base + total) {
         const unsigned long long hit =
             __ballot(t > 0 && base + inc - t <= start && start < base + inc);
         const int src = __ffsll(hit) - 1;
         ci = uniform(c0 + src);
-        P = uniform(base + __shfl(inc - t, src, 64));
+        P = uniform(base + __builtin_amdgcn_readlane(inc - t, src));
         if (c0 == 0) {
-          it.geo.sq = uniform(__shfl(g_first.sq, src, 64));
-          it.geo.sk = uniform(__shfl(g_first.sk, src, 64));
+          it.geo.sq = uniform(__builtin_amdgcn_readlane(g_first.sq, src));
+          it.geo.sk = uniform(__builtin_amdgcn_readlane(g_first.sk, src));
           it.geo.prefix = it.geo.sk - it.geo.sq;
-          it.geo.ntq = uniform(__shfl(g_first.ntq, src, 64));
-          it.cq0 = uniform(__shfl(cq_first, src, 64));
-          it.ck0 = uniform(__shfl(ck_first, src, 64));
+          it.geo.ntq = uniform(__builtin_amdgcn_readlane(g_first.ntq, src));
+          it.cq0 = uniform(__builtin_amdgcn_readlane(cq_first, src));
+          it.ck0 = uniform(__builtin_amdgcn_readlane(ck_first, src));
         }
       }
       base += total;
@@ -3236,8 +3209,8 @@ prefill_sk_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t*
 #pragma unroll
       for (int cb = 0; cb < kPreNCB; ++cb)
         if (klim[cb] >= 0) min_klim = min(min_klim, klim[cb]);
-#pragma unroll
-      for (int m = 32; m >= 1; m >>= 1) min_klim = min(min_klim, __shfl_xor(min_klim, m, 64));
+    #pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) min_klim = min(min_klim, __shfl_xor(min_klim, m, 64));
       pf_init(st);
       // Split bookkeeping: the item's real tiles span shares [f, l].
       const int f = (it.P + kPfItemCost) / S;
@@ -3530,26 +3503,21 @@ __device__ __forceinline__ void prefill_sk2_share(const AttnParams& p,
           if (c.ntq > 0) t = kvs_total * p2_qcum(c, p.tpb, c.ntq);
         }
       }
-      int inc = t;
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const int u = __shfl_up(inc, d, 64);
-        if (L.lane >= d) inc += u;
-      }
-      const int total = uniform(__shfl(inc, 63, 64));
+      const int inc = wave_scan_add(t);
+      const int total = uniform(__builtin_amdgcn_readlane(inc, 63));
       if (start < base + total) {
         const unsigned long long hit =
             __ballot(t > 0 && base + inc - t <= start && start < base + inc);
         const int src = __ffsll(hit) - 1;
         ci = uniform(c0 + src);
-        P = uniform(base + __shfl(inc - t, src, 64));
+        P = uniform(base + __builtin_amdgcn_readlane(inc - t, src));
         if (c0 == 0) {
-          it.geo.sq = uniform(__shfl(g_first.sq, src, 64));
-          it.geo.sk = uniform(__shfl(g_first.sk, src, 64));
+          it.geo.sq = uniform(__builtin_amdgcn_readlane(g_first.sq, src));
+          it.geo.sk = uniform(__builtin_amdgcn_readlane(g_first.sk, src));
           it.geo.prefix = it.geo.sk - it.geo.sq;
-          it.geo.ntq = uniform(__shfl(g_first.ntq, src, 64));
-          it.cq0 = uniform(__shfl(cq_first, src, 64));
-          it.ck0 = uniform(__shfl(ck_first, src, 64));
+          it.geo.ntq = uniform(__builtin_amdgcn_readlane(g_first.ntq, src));
+          it.cq0 = uniform(__builtin_amdgcn_readlane(cq_first, src));
+          it.ck0 = uniform(__builtin_amdgcn_readlane(ck_first, src));
         }
       }
       base += total;

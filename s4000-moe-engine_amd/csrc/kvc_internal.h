@@ -182,6 +182,28 @@ __device__ __forceinline__ int wave_scan_max_nonneg(int x) {
   return x;
 }
 
+// The same scan for max over any ints (lanes without a source read INT_MIN).
+__device__ __forceinline__ int wave_scan_max(int x) {
+  constexpr int kLow = -2147483647 - 1;
+  x = max(x, __builtin_amdgcn_update_dpp(kLow, x, 0x111, 0xf, 0xf, false));
+  x = max(x, __builtin_amdgcn_update_dpp(kLow, x, 0x112, 0xf, 0xf, false));
+  x = max(x, __builtin_amdgcn_update_dpp(kLow, x, 0x114, 0xf, 0xf, false));
+  x = max(x, __builtin_amdgcn_update_dpp(kLow, x, 0x118, 0xf, 0xf, false));
+  x = max(x, __builtin_amdgcn_update_dpp(kLow, x, 0x142, 0xa, 0xf, false));
+  x = max(x, __builtin_amdgcn_update_dpp(kLow, x, 0x143, 0xc, 0xf, false));
+  return x;
+}
+
+// Wave-wide sum and max (integers, so any order gives the same result) from
+// the DPP scans, read back from lane 63: no LDS round trips.
+__device__ __forceinline__ int wave_sum(int v) {
+  return __builtin_amdgcn_readlane(wave_scan_add(v), 63);
+}
+
+__device__ __forceinline__ int wave_max(int v) {
+  return __builtin_amdgcn_readlane(wave_scan_max(v), 63);
+}
+
 __device__ __forceinline__ int64_t wrap_slot(int64_t s, int64_t num_slots) {
   return s < 0 ? s + num_slots : s;
 }

@@ -7,7 +7,7 @@
 // q heads, H .. H+KVH-1 k heads, H+KVH .. H+2KVH-1 v heads.  In a q/k row
 // lane j holds dims 4 j .. 4 j + 3 and 64 + 4 j .. 64 + 4 j + 3, so the
 // rotation's pairs (i, i + 64) never leave a lane; the RMS over 128 dims is a
-// 16-lane xor reduction.
+// 16-lane butterfly of DPP moves.
 //
 // Arithmetic follows the engine's torch ops in their order, each result
 // rounded where torch rounds it:
@@ -60,6 +60,19 @@ struct RopeArgs {
 // finite value.
 __device__ __forceinline__ float round_bf16(float x) {
   return static_cast<float>(static_cast<__bf16>(x));
+}
+
+// Sum over a 16-lane row without LDS: the xor-1 and xor-2 partners through
+// quad permutes, then the other quad of each half (row_half_mirror) and the
+// other half (row_mirror).  After the quad steps every lane of a quad holds
+// the same value, so each mirror adds exactly what the xor-4 / xor-8 partner
+// of a butterfly would: the same sums, in the same order, as the butterfly.
+__device__ __forceinline__ float sum16(float x) {
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xf, 0xf, false));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xf, 0xf, false));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x141, 0xf, 0xf, false));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x140, 0xf, 0xf, false));
+  return x;
 }
 
 __device__ __forceinline__ void unpack4(const u32x2_t& w, float* x) {
@@ -155,8 +168,7 @@ __global__ void __launch_bounds__(kThreads) qk_norm_rope_store_kernel(RopeArgs a
       for (int i = 0; i < 4; ++i) ss += x1[i] * x1[i];
 #pragma unroll
       for (int i = 0; i < 4; ++i) ss += x2[i] * x2[i];
-#pragma unroll
-      for (int m = 1; m < kLanes; m <<= 1) ss += __shfl_xor(ss, m, kLanes);
+      ss = sum16(ss);
       const float var = ss / float(kD);
       const float rinv = 1.f / __fsqrt_rn(var + a.eps);
       float w1[4], w2[4];
