@@ -95,6 +95,15 @@ def test_mixed_decode_plus_prefill_small(partition):
     _check_mixed(c, "mixed-small")
 
 
+@pytest.mark.parametrize("dec,chunks", [([1], [(0, 1)]), ([5000], [(4096, 1)]),
+                                        ([3, 4096], [(0, 1), (0, 300)])])
+def test_mixed_extremes_of_the_split(dec, chunks, partition):
+    """One or two decode rows spread over the decode side's shares (most of
+    them empty) and one-token chunks (a prefill item of one query column)."""
+    c = _mixed_case(32, 4, dec, chunks, seed=len(dec) + 7 * len(chunks))
+    _check_mixed(c, f"extremes dec={dec} chunks={chunks}")
+
+
 @pytest.mark.parametrize("heads,kv_heads", [(16, 8), (32, 32), (12, 4), (64, 2)])
 def test_mixed_gqa_groupings(heads, kv_heads, partition):
     c = _mixed_case(heads, kv_heads, [900, 17], [(0, 20), (700, 45)], seed=heads + kv_heads)
