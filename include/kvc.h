@@ -116,10 +116,13 @@ int kvc_store_int8_chan(const void* key, int64_t key_stride_n, int64_t key_strid
  * run over one observed forward's key/value rows [num_tokens, KVH, 128]
  * (bf16, own element strides):
  *   amax[s][h][d]    = max(amax[s][h][d], max_n |x_s[n][h][d]|)
- *   abs_sum[s][h][d] += sum_n |x_s[n][h][d]|          (fp32)
+ *   abs_sum[s][h][d] += bf16(sum_n |x_s[n][h][d]|)    (fp32 add)
  * for s = 0 (key) and 1 (value); amax and abs_sum are fp32 [2, KVH, 128],
- * zeroed by the caller before the first call.  Sums are accumulated in a
- * fixed order (no atomics).  The caller counts the tokens. */
+ * zeroed by the caller before the first call.  As in the hook, whose
+ * `k.abs().sum(dim=0)` torch returns in bf16 (model_runner.py:529-532), each
+ * call's sum is rounded to bf16 (nearest, ties to even) before it is added;
+ * the sum is formed exactly before that rounding, so it does not depend on
+ * the order of the additions.  The caller counts the tokens. */
 int kvc_kv_calib_observe(const void* key, int64_t key_stride_n, int64_t key_stride_h,
                          const void* value, int64_t value_stride_n, int64_t value_stride_h,
                          int64_t num_tokens, int64_t num_kv_heads, int64_t head_dim,

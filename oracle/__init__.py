@@ -25,13 +25,20 @@ How each function is pinned (checked in tests/test_oracle.py):
                            exact; the seeded tests/p17_kv_int8.py unit case.
   dequant_*                closed form code * scale with bf16 RNE (checked
                            against torch's bf16 cast).
-  calib_stats / calib_freeze
-                           the calibration of tests/p17_kv_int8.py:80-101
-                           (restated in tests/helpers.p17_unit_inputs) on its
-                           seeded unit case, bit for bit; known answers at
-                           the ratio threshold (10 is not an outlier, the
-                           first n_out_max dims in index order win), the
-                           1e-6 clamps, statistics split over forwards.
+  calib_stats / calib_fold / calib_freeze
+                           the engine hook's own torch statements
+                           (model_runner.py:527-533: torch's bf16 sum per
+                           forward, fp32 fold) over forwards of different
+                           lengths, bit for bit; two dims whose outlier
+                           decision flips with the per-forward bf16 rounding;
+                           the calibration of tests/p17_kv_int8.py:80-101 on
+                           its seeded unit case; known answers at the ratio
+                           threshold (10 is not an outlier, the first
+                           n_out_max dims in index order win), the 1e-6
+                           clamps.
+  f64_to_bf16_value        torch's fp32 -> bf16 cast on fp32-exact values
+                           (ties, subnormals, overflow) and known answers a
+                           double rounding through fp32 would miss.
   paged_decode_ref         float64 torch scaled_dot_product_attention; closed
                            forms (one key -> V row; identical keys -> mean of
                            V); a NaN-poisoned tail never read; the reference

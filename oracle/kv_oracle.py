@@ -137,12 +137,53 @@ def dequant_tokhead(codes: np.ndarray, scale: np.ndarray) -> np.ndarray:
     return f32_to_bf16(codes.astype(np.float32) * scale.astype(np.float32)[..., None])
 
 
+def f64_to_bf16_value(x: np.ndarray) -> np.ndarray:
+    """Correctly rounded (ties to even) bf16 value of non-negative finite
+    float64 numbers, returned as float32.  bf16 keeps 8 significant bits and
+    fp32's exponent range: below 2^-126 its spacing is fixed at 2^-133."""
+    x = np.asarray(x, dtype=np.float64)
+    out = np.empty(x.shape, np.float32)
+    flat, res = x.ravel(), out.ravel()
+    for i, v in enumerate(flat):
+        if v == 0.0:
+            res[i] = 0.0
+            continue
+        e = max(math.frexp(v)[1] - 8, -133)       # bf16 spacing at v is 2^e
+        q, r = divmod(v, math.ldexp(1.0, e))      # exact: v and 2^e are doubles
+        half = math.ldexp(1.0, e - 1)
+        if r > half or (r == half and int(q) % 2 == 1):
+            q += 1.0
+        y = math.ldexp(q, e)
+        res[i] = np.float32(y) if y < 2.0 ** 128 else np.float32(np.inf)
+    return out
+
+
 def calib_stats(x_bits: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     """The calibration hook's per-channel statistics of one forward's rows
     (nanovllm/engine/model_runner.py:522-532): x_bits [N, KVH, D] bf16 bits ->
-    (amax of |x| over tokens, sum of |x| over tokens), fp32 [KVH, D]."""
+    (amax of |x| over tokens, sum of |x| over tokens), fp32 [KVH, D].
+
+    The hook sums a bf16 tensor (`k.abs().sum(dim=0)`), which torch returns
+    in bf16 before `.float()`: the sum here is the exact one (float64 holds
+    every partial sum of bf16 terms exactly while they span < 2^45) rounded
+    once to bf16.  The caller adds these per-forward sums in fp32, as the
+    hook's `buf["k_sum"] + ...` does."""
     a = np.abs(bf16_to_f32(x_bits))
-    return a.max(axis=0), a.sum(axis=0, dtype=np.float32)
+    return a.max(axis=0), f64_to_bf16_value(a.astype(np.float64).sum(axis=0))
+
+
+def calib_fold(forwards: list) -> tuple[np.ndarray, np.ndarray, int]:
+    """The hook over several forwards (model_runner.py:527-533): running
+    max of the per-forward amax, running fp32 sum of the per-forward
+    (bf16-rounded) sums, token count.  forwards: list of [N_i, KVH, D] bf16
+    bits."""
+    amax, total, n = None, None, 0
+    for x_bits in forwards:
+        a, s = calib_stats(x_bits)
+        amax = a if amax is None else np.maximum(amax, a)
+        total = s if total is None else (total + s).astype(np.float32)
+        n += x_bits.shape[0]
+    return amax, total, n
 
 
 def calib_freeze(amax_k, amax_v, sum_k, sum_v, count: int, n_out_max: int):

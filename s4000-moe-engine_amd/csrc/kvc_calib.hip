@@ -3,9 +3,13 @@
 // store scales, read scales and each kv head's outlier dims.
 //
 // Statistics are per (K or V, kv head, dim): the running max of |x| and the
-// running fp32 sum of |x| over every observed token, accumulated without
-// atomics (one workgroup owns a (side, head) and reduces its token lanes in a
-// fixed order), so a calibration is reproducible run to run.
+// running fp32 sum, over the observed forwards, of each forward's sum of |x|
+// rounded to bf16.  The engine's hook sums a bf16 tensor, and torch returns
+// that sum as bf16 (nanovllm/engine/model_runner.py:529-532); here the
+// forward's sum is formed exactly (fp64: every bf16 term is exact in it while
+// the terms of one forward span less than 2^45) and rounded once to bf16
+// with round-to-nearest-even, so the result does not depend on the order of
+// the additions.  No atomics: one workgroup owns a (side, head).
 #include "kvc_internal.h"
 
 namespace kvc {
@@ -16,24 +20,43 @@ constexpr int kLanes = 8;                 // token lanes per workgroup
 constexpr int kObsThreads = kD * kLanes;  // 1024
 constexpr float kRatioThreshold = 10.f;
 
+// Round a non-negative finite double to the nearest bf16 (ties to even),
+// returned as the fp32 holding that bf16 value.  In the normal range the
+// 45 low mantissa bits are rounded off in the double itself (a carry moves
+// into the exponent, and past bf16's largest value the result becomes
+// infinity on the conversion).  Below 2^-126 the sum is a multiple of 2^-133
+// (a sum of bf16 subnormals) and exact in fp32, whose bf16 rounding then is
+// the usual add-and-truncate.
+__device__ __forceinline__ float round_bf16_rne(double x) {
+  if (x < 0x1p-126) {
+    const uint32_t b = __float_as_uint(float(x));
+    return __uint_as_float((b + 0x7fffu + ((b >> 16) & 1u)) & 0xffff0000u);
+  }
+  uint64_t b = uint64_t(__double_as_longlong(x));
+  b += (uint64_t(1) << 44) - 1 + ((b >> 45) & 1);
+  b &= ~((uint64_t(1) << 45) - 1);
+  return float(__longlong_as_double(int64_t(b)));
+}
+
 // Workgroup (side, head): thread (lane, d) walks tokens lane, lane + 8, ...
-// of column d, then lane 0 folds the 8 partials in lane order.
+// of column d, then lane 0 folds the 8 partials (all sums exact in fp64).
 __global__ void __launch_bounds__(kObsThreads)
 calib_observe_kernel(const uint16_t* __restrict__ key, int64_t k_sn, int64_t k_sh,
                      const uint16_t* __restrict__ value, int64_t v_sn, int64_t v_sh,
                      int64_t num_tokens, int kvh, float* __restrict__ amax,
                      float* __restrict__ abs_sum) {
   __shared__ float s_max[kLanes][kD];
-  __shared__ float s_sum[kLanes][kD];
+  __shared__ double s_sum[kLanes][kD];
   const int side = blockIdx.x / kvh;
   const int h = blockIdx.x - side * kvh;
   const int d = threadIdx.x % kD;
   const int lane = threadIdx.x / kD;
   const uint16_t* base = side == 0 ? key + h * k_sh + d : value + h * v_sh + d;
   const int64_t sn = side == 0 ? k_sn : v_sn;
-  float mx = 0.f, sum = 0.f;
+  float mx = 0.f;
+  double sum = 0.0;
   int64_t n = lane;
-  // four tokens' loads in flight, accumulated in token order
+  // four tokens' loads in flight
   for (; n + 3 * kLanes < num_tokens; n += 4 * kLanes) {
     uint32_t b[4];
 #pragma unroll
@@ -42,13 +65,13 @@ calib_observe_kernel(const uint16_t* __restrict__ key, int64_t k_sn, int64_t k_s
     for (int u = 0; u < 4; ++u) {
       const float a = __uint_as_float((b[u] & 0x7fffu) << 16);
       mx = fmaxf(mx, a);
-      sum += a;
+      sum += double(a);
     }
   }
   for (; n < num_tokens; n += kLanes) {
     const float a = __uint_as_float((uint32_t(base[n * sn]) & 0x7fffu) << 16);
     mx = fmaxf(mx, a);
-    sum += a;
+    sum += double(a);
   }
   s_max[lane][d] = mx;
   s_sum[lane][d] = sum;
@@ -61,7 +84,7 @@ calib_observe_kernel(const uint16_t* __restrict__ key, int64_t k_sn, int64_t k_s
     }
     const int64_t i = (int64_t(side) * kvh + h) * kD + d;
     amax[i] = fmaxf(amax[i], mx);
-    abs_sum[i] += sum;
+    abs_sum[i] += round_bf16_rne(sum);
   }
 }
 

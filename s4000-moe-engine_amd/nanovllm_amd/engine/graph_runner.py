@@ -54,11 +54,19 @@ class DecodeGraphRunner:
     (the last block is the scratch block).  run(q, k, v, ...) takes
     q [L, bs, H, D], k / v [L, bs, KVH, D] and returns the attention outputs
     [L, bs, H, D] (a view into the static output buffer, valid until the
-    next run)."""
+    next run).
+
+    fence: the pool owner's ordering call, run on the current stream before
+    every capture and every replay (KVCacheRunner.fence: with asynchronous
+    offload, a put may still be reading a block that the replay appends
+    into after the block manager reallocated it, and a replayed graph holds
+    none of the eager per-layer waits).  from_kv_runner binds it; a runner
+    built without one is for pools that no asynchronous move touches."""
 
     def __init__(self, k_caches, v_caches, num_heads: int, max_bs: int, max_blocks_per_seq: int,
-                 scale: float, buckets: list[int] | None = None):
+                 scale: float, buckets: list[int] | None = None, fence=None):
         assert len(k_caches) == len(v_caches) and len(k_caches) > 0
+        self.fence = fence
         self.k_caches, self.v_caches = list(k_caches), list(v_caches)
         kc = self.k_caches[0]
         self.num_layers = len(self.k_caches)
@@ -85,6 +93,19 @@ class DecodeGraphRunner:
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
         self.pool = None
 
+    @classmethod
+    def from_kv_runner(cls, kv_runner, num_heads: int, max_bs: int, max_blocks_per_seq: int,
+                       scale: float, buckets: list[int] | None = None) -> "DecodeGraphRunner":
+        """A runner over every layer of a KVCacheRunner's bf16 pool, fenced by
+        that runner (its asynchronous offload copies, if any, are ordered
+        before each capture and replay)."""
+        if kv_runner.kv_int8 is not None:
+            raise ValueError("the captured decode step runs on a bf16 pool")
+        k_caches = [kv_runner.kv_cache[0, i] for i in range(kv_runner.num_layers)]
+        v_caches = [kv_runner.kv_cache[1, i] for i in range(kv_runner.num_layers)]
+        return cls(k_caches, v_caches, num_heads, max_bs, max_blocks_per_seq, scale, buckets,
+                   fence=kv_runner.fence)
+
     def _step(self, bs: int) -> None:
         sm, cl, bt = self.slot_mapping[:bs], self.context_lens[:bs], self.block_tables[:bs]
         for layer in range(self.num_layers):
@@ -97,6 +118,8 @@ class DecodeGraphRunner:
         """Capture every bucket, small first (model_runner.py:1169-1175): a
         warm-up run on the padded (scratch) inputs, then the capture."""
         for bs in sorted(self.buckets):
+            if self.fence is not None:
+                self.fence()
             self._step(bs)  # warm-up on the side: scratch rows only
             torch.cuda.synchronize()
             graph = torch.cuda.CUDAGraph()
@@ -113,14 +136,13 @@ class DecodeGraphRunner:
                 return b
         raise ValueError(f"batch {bs} exceeds the largest bucket {max(self.buckets)}")
 
-    def run(self, q, k, v, slot_mapping, context_lens, block_tables,
-            fence=None) -> torch.Tensor:
-        """One replay.  fence: called before the replay, on the current
-        stream (e.g. KVCacheRunner.fence when block moves run asynchronously:
-        a replayed graph holds no per-layer waits of its own)."""
+    def run(self, q, k, v, slot_mapping, context_lens, block_tables) -> torch.Tensor:
+        """One replay, after the runner's fence (asynchronous block moves
+        issued so far are ordered before the replay's pool reads and
+        appends)."""
         bs = q.size(1)
-        if fence is not None:
-            fence()
+        if self.fence is not None:
+            self.fence()
         b = self.bucket_of(bs)
         self.q[:, :bs] = q
         self.k[:, :bs] = k

@@ -23,10 +23,13 @@ import torch
 
 from .. import _native as nat
 
-# KVC_CHECK_APPEND=1: paged_decode_append checks on the host that the decode
-# slots satisfy the fused append's contract before it launches (reads the
-# metadata back, so it synchronises; for debugging, never under capture).
-_CHECK_APPEND = os.environ.get("KVC_CHECK_APPEND", "0") == "1"
+
+def _check_append_enabled() -> bool:
+    """KVC_CHECK_APPEND=1 (read at every call): paged_decode_append checks on
+    the host that the decode slots satisfy the fused append's contract before
+    it launches (reads the metadata back, so it synchronises; for debugging,
+    never under capture)."""
+    return os.environ.get("KVC_CHECK_APPEND", "0") == "1"
 
 
 def set_paged_config(value: str | None) -> None:
@@ -192,7 +195,7 @@ def paged_decode_append(q, key, value, k_cache, v_cache, slot_mapping, block_tab
         output = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     if batch == 0:
         return output
-    if _CHECK_APPEND:
+    if _check_append_enabled():
         check_append_contract(slot_mapping, block_tables, context_lens, page_size,
                               k_cache.size(0) * page_size)
     max_blocks = block_tables.size(1)

@@ -105,3 +105,70 @@ def p17_unit_inputs():
         ds_k[h, out_idx2d[h, :n_h].long()] = 0.0
         ds_v[h, out_idx2d[h, :n_h].long()] = 0.0
     return key, value, s_k, s_v, ds_k, ds_v, out_idx2d, head_n_out
+
+
+def _column(n: int, counts: dict) -> torch.Tensor:
+    """A column of n tokens holding `counts[value]` copies of each value
+    (every value exact in bf16), zeros elsewhere."""
+    vals = [v for v, c in counts.items() for _ in range(c)]
+    assert len(vals) <= n
+    return torch.tensor(vals + [0.0] * (n - len(vals)))
+
+
+# Forward lengths of the ratio-flip calibration case and, per flip dim, each
+# forward's column: one 8.0 (the amax) plus 2.0 / 1.0 / 0.75 terms.  Over the
+# 900 tokens a dim is an outlier iff its sum of |x| < 720 (ratio 8 * 900 /
+# sum > 10).
+#   dim "hook_in":  sums 239.75 + 199.75 + 279.75 = 719.25 in fp32 (outlier);
+#                   each rounds up to bf16: 240 + 200 + 280 = 720 (ratio 10: not)
+#   dim "hook_out": sums 239.25 + 200.25 + 280.5 = 720.0 in fp32 (ratio 10: not);
+#                   each rounds down: 239 + 200 + 280 = 719 (outlier)
+CALIB_FLIP_LENGTHS = (300, 250, 350)
+CALIB_FLIP_COLUMNS = {
+    "hook_in": ({8.0: 1, 1.0: 30, 0.75: 269}, {8.0: 1, 2.0: 4, 0.75: 245},
+                {8.0: 1, 2.0: 8, 0.75: 341}),
+    "hook_out": ({8.0: 1, 2.0: 5, 1.0: 3, 0.75: 291}, {8.0: 1, 2.0: 4, 1.0: 2, 0.75: 243},
+                 {8.0: 1, 2.0: 8, 1.0: 3, 0.75: 338}),
+}
+
+
+def calib_flip_forwards(kvh: int = 4, d: int = 128, seed: int = 21):
+    """Three calibration forwards (key, value bf16 [n_i, kvh, d]) with two
+    dims of head 0 whose outlier decision flips between fp32 sums and the
+    engine's bf16-rounded per-forward sums (CALIB_FLIP_COLUMNS), a 60x
+    outlier channel in head 1, and N(0, 0.7^2) elsewhere (ratio about 4.5).
+    Returns (forwards, dims) with dims = {"hook_in": 3, "hook_out": 77}."""
+    g = torch.Generator().manual_seed(seed)
+    dims = {"hook_in": 3, "hook_out": 77}
+    forwards = []
+    for i, n in enumerate(CALIB_FLIP_LENGTHS):
+        key = torch.randn(n, kvh, d, generator=g) * 0.7
+        value = torch.randn(n, kvh, d, generator=g) * 0.7
+        key[n // 2, 1, 40] = 40.0
+        for name, dim in dims.items():
+            col = _column(n, CALIB_FLIP_COLUMNS[name][i])
+            key[:, 0, dim] = col[torch.randperm(n, generator=g)]
+            value[:, 0, dim] = 0.5        # V ratio 1: K alone decides
+        forwards.append((key.to(torch.bfloat16), value.to(torch.bfloat16)))
+    return forwards, dims
+
+
+def torch_hook_stats(forwards):
+    """The engine's forward pre-hook statements (model_runner.py:527-533),
+    run in CPU torch on the observed rows: per-forward amax and bf16 sum of
+    |x|, folded with torch.maximum and fp32 adds.  Returns
+    (amax_k, amax_v, sum_k, sum_v, n) as fp32 numpy."""
+    buf = {"k": None, "v": None, "k_sum": None, "v_sum": None, "n": 0}
+    for k, v in forwards:
+        kf = k.detach().abs().amax(dim=0).float()
+        vf = v.detach().abs().amax(dim=0).float()
+        buf["k"] = kf if buf["k"] is None else torch.maximum(buf["k"], kf)
+        buf["v"] = vf if buf["v"] is None else torch.maximum(buf["v"], vf)
+        ks = k.detach().abs().sum(dim=0)
+        vs = v.detach().abs().sum(dim=0)
+        assert ks.dtype == torch.bfloat16        # the hook's sum is bf16
+        buf["k_sum"] = ks.float() if buf["k_sum"] is None else buf["k_sum"] + ks.float()
+        buf["v_sum"] = vs.float() if buf["v_sum"] is None else buf["v_sum"] + vs.float()
+        buf["n"] += k.shape[0]
+    return (buf["k"].numpy(), buf["v"].numpy(), buf["k_sum"].numpy(), buf["v_sum"].numpy(),
+            buf["n"])

@@ -108,3 +108,56 @@ def test_graph_replays_match_eager_and_touch_only_live_slots_and_scratch():
                                       np.asarray(lens_list), 128 ** -0.5)
             assert_attention_close(got[layer], ref, f"replay {rnd} layer {layer}")
         del before_k, before_v, ek, ev
+
+
+def _runner_with_pool(init, async_groups):
+    from nanovllm_amd.engine.kv_runner import KVCacheRunner
+    L_, nb = init.size(1), init.size(2) - 1
+    r = KVCacheRunner(L_, nb, PAGE, KVH, 128, kv_offload_host_blocks=4,
+                      async_offload_groups=async_groups, async_copy_engine="dma")
+    r.kv_cache.copy_(init)
+    return r
+
+
+def test_graph_replay_after_async_eviction_of_the_appended_block():
+    """An eviction put of block B on the copy streams, then a graph replay
+    whose appends land in B (the block manager reallocated it): the runner
+    built by from_kv_runner fences before the replay, so the host slot holds
+    B as it was before the append, and the pool and outputs equal the same
+    sequence with blocking offload."""
+    Lg, nb = 8, 40
+    g = torch.Generator().manual_seed(3)
+    init = torch.randn(2, Lg, nb + 1, PAGE, KVH, 128, generator=g).to(torch.bfloat16).to(DEV)
+    bs, B = 3, 17
+    lens = [PAGE + 1, 700, 2 * PAGE + 5]
+    # row 0 appends at position PAGE of its table -> the first token of block B
+    tables = torch.tensor([[5, B, -1], [9, 10, 11], [20, 21, 22]], dtype=torch.int32)
+    slots = torch.tensor([B * PAGE, 11 * PAGE + 699 - 2 * PAGE, 22 * PAGE + 4], dtype=torch.int32)
+    q = torch.randn(Lg, bs, H, 128, generator=g).to(torch.bfloat16).to(DEV)
+    k = torch.randn(Lg, bs, KVH, 128, generator=g).to(torch.bfloat16).to(DEV)
+    v = torch.randn(Lg, bs, KVH, 128, generator=g).to(torch.bfloat16).to(DEV)
+    results = {}
+    for groups in (0, 4):
+        print(f"[graph-offload] async groups {groups}: put block {B}, replay batch {bs}",
+              flush=True)
+        r = _runner_with_pool(init, groups)
+        gr = DecodeGraphRunner.from_kv_runner(r, H, max_bs=4, max_blocks_per_seq=3,
+                                              scale=128 ** -0.5, buckets=[4])
+        gr.capture()
+        torch.cuda.synchronize()
+        r.kv_cache.copy_(init)                      # capture wrote the scratch block only
+        torch.cuda.synchronize()
+        slot = r.offload_put(B)
+        out = gr.run(q, k, v, slots.to(DEV), torch.tensor(lens, dtype=torch.int32, device=DEV),
+                     tables.to(DEV)).clone()
+        if r.kv_async is not None:
+            r.kv_async.wait_host()
+        torch.cuda.synchronize()
+        host = bits(r.kv_offloader.buffer[slot])
+        results[groups] = (bits(out), bits(r.kv_cache), host)
+        assert np.array_equal(host, bits(init[:, :, B])), "host slot is not B before the append"
+    for a, b in zip(results[0], results[4]):
+        assert np.array_equal(a, b)
+    flat = r.kv_cache.view(2, Lg, -1, KVH, 128)
+    assert np.array_equal(bits(flat[0][:, slots.long().to(DEV)]), bits(k))
+    assert np.array_equal(bits(flat[1][:, slots.long().to(DEV)]), bits(v))

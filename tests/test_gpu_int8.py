@@ -297,3 +297,46 @@ def test_chan_calibration_on_device_matches_p17_unit_case():
     rel = float((deq.float().cpu() - key.float()).abs().mean() / key.float().abs().mean())
     print(f"[int8-calib] dequant rel err {rel:.4%}", flush=True)
     assert rel < 0.03
+
+
+def test_chan_calibration_follows_the_engine_hook_over_forwards():
+    """Calibration over three forwards of 300, 250 and 350 tokens whose
+    per-forward sums of |x| round to bf16 (model_runner.py:529-532): the
+    device statistics equal the oracle's fold bit for bit (amax, fp32 sum of
+    bf16-rounded forward sums), and the frozen store scales, read scales,
+    out_idx2d and head_n_out equal the oracle's freeze.  Two dims of head 0
+    are outliers under the hook's rounding and not under fp32 sums (or the
+    reverse), so a kernel that skips the rounding fails here."""
+    from helpers import calib_flip_forwards
+    from nanovllm_amd.engine.kv_runner import KVCacheRunner
+    from nanovllm_amd.layers.attention import Attention
+    forwards, dims = calib_flip_forwards()
+    KVH, D, n_out = 4, 128, 4
+    print(f"[int8-calib] flip case: forwards {[k.shape[0] for k, _ in forwards]}, "
+          f"dims {dims}", flush=True)
+    runner = KVCacheRunner(1, 4, 256, KVH, D, kv_int8="chan", n_out_max=n_out)
+    mod = Attention(32, D, D ** -0.5, KVH)
+    assert runner.bind([mod]) == 1
+    runner.kv_calibrate_begin()
+    for k, v in forwards:
+        mod.kv_observe(0, k.to(DEV), v.to(DEV))
+    amax_dev, sum_dev = runner._calib[0][0].cpu().numpy(), runner._calib[1][0].cpu().numpy()
+    a_k, s_k, n = ko.calib_fold([bits(k) for k, _ in forwards])
+    a_v, s_v, _ = ko.calib_fold([bits(v) for _, v in forwards])
+    u32 = lambda a: np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+    assert np.array_equal(u32(amax_dev[0]), u32(a_k)) and np.array_equal(u32(amax_dev[1]), u32(a_v))
+    assert np.array_equal(u32(sum_dev[0]), u32(s_k)) and np.array_equal(u32(sum_dev[1]), u32(s_v))
+    runner.kv_calibrate_freeze()
+    want = ko.calib_freeze(a_k, a_v, s_k, s_v, n, n_out)
+    for got, w, name in ((runner.kv_scales[0, 0], want[0], "k_scale"),
+                         (runner.kv_scales[1, 0], want[1], "v_scale"),
+                         (runner.kv_dscales[0, 0], want[2], "k_dscale"),
+                         (runner.kv_dscales[1, 0], want[3], "v_dscale")):
+        assert np.array_equal(u32(got.cpu().numpy()), u32(w)), name
+    n_got = runner.kv_head_n_out[0].cpu().numpy()
+    assert np.array_equal(n_got, want[5])
+    for h in range(KVH):
+        assert np.array_equal(runner.kv_out_idx2d[0, h, :n_got[h]].cpu().numpy(),
+                              want[4][h, :n_got[h]])
+    head0 = set(want[4][0, :want[5][0]].tolist())
+    assert dims["hook_out"] in head0 and dims["hook_in"] not in head0

@@ -474,12 +474,74 @@ def test_calib_freeze_known_answers():
     assert ko.calib_freeze(z, z, z, z, 7, 8)[5].tolist() == [0]
 
 
-def test_calib_stats_fold_over_forwards():
+def test_f64_to_bf16_value_single_rounding():
+    """The per-forward sum's rounding: against torch's fp32 -> bf16 cast on
+    fp32-exact inputs (ties included), and known answers that a double
+    rounding through fp32 would get wrong."""
+    g = torch.Generator().manual_seed(5)
+    x = (torch.rand(4000, generator=g) * torch.exp2(torch.randint(-140, 120, (4000,),
+                                                                     generator=g).float()))
+    x[:6] = torch.tensor([0.0, 1 + 2 ** -8, 1 + 3 * 2 ** -8, 2.0 ** -130, 3 * 2.0 ** -134,
+                          3.3895e38])
+    want = ko.bf16_to_f32(ko.torch_bf16_bits(x.to(torch.bfloat16)))
+    got = ko.f64_to_bf16_value(x.double().numpy())
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # just above a tie: the exact value rounds up; via fp32 it would tie to even
+    assert ko.f64_to_bf16_value(np.float64([1 + 2 ** -8 + 2 ** -40]))[0] == np.float32(1 + 2 ** -7)
+    assert ko.f64_to_bf16_value(np.float64([239.75, 239.25, 280.5, 281.01])).tolist() == \
+        [240.0, 239.0, 280.0, 282.0]
+    assert ko.f64_to_bf16_value(np.float64([2.0 ** 128 - 2.0 ** 119]))[0] == np.inf
+
+
+def test_calib_stats_match_the_engine_hook_in_torch():
+    """Per-forward statistics folded over forwards of different lengths equal
+    the hook's own torch statements (model_runner.py:527-533) bit for bit:
+    amax, and the bf16 sums torch returns, added in fp32."""
+    from helpers import torch_hook_stats
     g = torch.Generator().manual_seed(44)
-    x = (torch.randn(300, 4, 128, generator=g) * 3).to(torch.bfloat16)
-    a_all, s_all = ko.calib_stats(ko.torch_bf16_bits(x))
-    a1, s1 = ko.calib_stats(ko.torch_bf16_bits(x[:120]))
-    a2, s2 = ko.calib_stats(ko.torch_bf16_bits(x[120:]))
-    assert np.array_equal(np.maximum(a1, a2), a_all)
-    assert np.allclose(s1 + s2, s_all, rtol=1e-5)
-    assert np.array_equal(a_all, np.abs(x.float().numpy()).max(0))
+    forwards = []
+    for n in (300, 17, 512, 1):
+        k = (torch.randn(n, 4, 128, generator=g) * 3).to(torch.bfloat16)
+        v = (torch.randn(n, 4, 128, generator=g) * torch.exp2(
+            torch.randint(-6, 6, (n, 4, 128), generator=g).float())).to(torch.bfloat16)
+        forwards.append((k, v))
+    ak, av, sk, sv, n = torch_hook_stats(forwards)
+    ak2, sk2, n2 = ko.calib_fold([ko.torch_bf16_bits(k) for k, _ in forwards])
+    av2, sv2, _ = ko.calib_fold([ko.torch_bf16_bits(v) for _, v in forwards])
+    assert n2 == n == 830
+    for got, want in ((ak2, ak), (av2, av), (sk2, sk), (sv2, sv)):
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # the per-forward rounding is visible: fp32 sums differ from the hook's
+    exact = sum(np.abs(ko.bf16_to_f32(ko.torch_bf16_bits(k))).astype(np.float64).sum(0)
+                for k, _ in forwards)
+    assert (np.abs(exact - sk) > 0).mean() > 0.5
+
+
+def test_calib_outlier_flip_follows_the_hook():
+    """Two dims whose outlier decision depends on the bf16 rounding of each
+    forward's sum (tests/helpers.CALIB_FLIP_COLUMNS): the oracle's freeze
+    follows the hook's torch statistics, and the fp32-sum statistics would
+    decide both dims the other way."""
+    from helpers import calib_flip_forwards, torch_hook_stats
+    forwards, dims = calib_flip_forwards()
+    ak, av, sk, sv, n = torch_hook_stats(forwards)
+    assert n == 900
+    assert sk[0, dims["hook_in"]] == 720.0 and sk[0, dims["hook_out"]] == 719.0
+    a_k, s_k, _ = ko.calib_fold([ko.torch_bf16_bits(k) for k, _ in forwards])
+    a_v, s_v, _ = ko.calib_fold([ko.torch_bf16_bits(v) for _, v in forwards])
+    assert np.array_equal(s_k, sk) and np.array_equal(s_v, sv)
+    got = ko.calib_freeze(a_k, a_v, s_k, s_v, n, 4)
+    want = ko.calib_freeze(ak, av, sk, sv, n, 4)
+    for g_, w_ in zip(got, want):
+        assert np.array_equal(g_, w_)
+    idx, n_out = got[4], got[5]
+    head0 = set(idx[0, :n_out[0]].tolist())
+    assert dims["hook_out"] in head0 and dims["hook_in"] not in head0
+    assert idx[1, :n_out[1]].tolist() == [40]
+    # with plain fp32 sums of |x| (no per-forward rounding) both flip
+    f32_sum = lambda side: np.sum([np.abs(ko.bf16_to_f32(ko.torch_bf16_bits(f[side])))
+                                   .astype(np.float64).sum(0) for f in forwards],
+                                  axis=0).astype(np.float32)
+    alt = ko.calib_freeze(a_k, a_v, f32_sum(0), f32_sum(1), n, 4)
+    head0_alt = set(alt[4][0, :alt[5][0]].tolist())
+    assert dims["hook_in"] in head0_alt and dims["hook_out"] not in head0_alt
