@@ -155,6 +155,20 @@ size_t kvc_paged_decode_workspace_bytes(int64_t batch, int64_t num_heads, int64_
                                         int64_t head_dim, int64_t page_size,
                                         int64_t max_blocks_per_seq);
 
+/* Diagnostics (no counterpart in the reference): where a stream-K paged
+ * decode launch of this shape leaves, in its workspace, the split count of
+ * every (row, kv slice) (int32 [batch][kv_slices], low 16 bits) and the
+ * number of tail tiles other workgroups took from each piece of it (int32
+ * [batch][kv_slices][max_splits], valid for pieces below the split count).
+ * layout[0] = byte offset of the split counts, layout[1] = byte offset of
+ * the taken counts (-1: this shape has no dynamic tail hand-out), layout[2]
+ * = max_splits, layout[3] = kv_slices.  Returns KVC_ERR_VALUE when the
+ * launch would not be stream-K.  Reading these after a launch tells how
+ * much work the dynamic hand-out moved. */
+int kvc_paged_decode_layout(int64_t batch, int64_t num_heads, int64_t num_kv_heads,
+                            int64_t head_dim, int64_t page_size, int64_t max_blocks_per_seq,
+                            int64_t* layout);
+
 /* Replaces paged_decode_attention / _paged_decode_kernel
  * (nanovllm/kernels/paged_attention.py:73-245):
  *   out[b, h] = softmax(q[b, h] . K[b, :ctx, h // G]^T * scale) . V[b, :ctx, h // G]

@@ -52,6 +52,8 @@ constexpr float kRescaleLog2 = 8.f;  // lazy-rescale threshold (log2 units)
 #define KVC_DEC_ROW_COST 3
 #endif
 constexpr int kDecRowCost = KVC_DEC_ROW_COST;
+// Tail tiles per share of the dynamic decode hand-out, at most.
+constexpr int kDecTailMax = 8;
 
 enum Enc : int { kBF16 = KVC_KV_BF16, kI8Tok = KVC_KV_INT8_TOKHEAD, kI8Chan = KVC_KV_INT8_CHAN };
 
@@ -115,6 +117,27 @@ struct AttnParams {
   const void* app_slots;
   int app_slot_bytes;
   int64_t app_num_slots;
+};
+
+// Dynamic tail hand-out of a bf16 stream-K decode (the kernels that take it
+// are separate instantiations; claims null: none).  Share w's last segment
+// ends in up to `tail` tiles that its owner claims one at a time from the
+// front while workgroups done with their own shares take them from the back
+// (claims[w]: front count | back count << 16 | tail tiles << 32).  A taken
+// tile is its own partial, at tail slot (w * kDecTailMax + j) of tail_o /
+// tail_lse ([slot][uh heads of the row unit][D]); stolen[row, kv slice,
+// piece] counts a piece's taken tiles, and sk_nseg then also carries the
+// row's first share (<< 16).
+struct StealArgs {
+  unsigned long long* claims;
+  int* dummy;
+  int* stolen;
+  float* tail_o;
+  float* tail_lse;
+  int tail;
+  int uh;
+  int grid;
+  int steal_min;
 };
 
 struct LaneId {
@@ -1054,21 +1077,53 @@ __device__ __forceinline__ void append_store(const AttnParams& p, int b, int kvg
 // One segment of a decode share: tiles t0 .. t1 of row b's kv group kvg,
 // written as a split partial when split >= 0.  (Block-table rows are formed
 // from the kernel argument where they are read, so the compiler keeps those
-// reads scalar.)
+// reads scalar.)  With the dynamic tail hand-out:
+// * tail > 0 (the owner's last segment): its last `tail` tiles are claimed
+//   one at a time from the front of the share's claim word and the segment
+//   ends early at the first tile another workgroup took;
+// * tslot >= 0 (a taken tile of another share): one tile, written to that
+//   tail slot.
 struct DecSeg {
   int b, kvg, ctx, t0, t1, split;
+  int tail, tslot;
 };
+
+// Claim-word fields (see StealArgs::claims).
+__device__ __forceinline__ int claim_front(unsigned long long o) { return int(o & 0xffffu); }
+__device__ __forceinline__ int claim_back(unsigned long long o) { return int((o >> 16) & 0xffffu); }
+__device__ __forceinline__ int claim_tiles(unsigned long long o) { return int((o >> 32) & 0xffffu); }
+
+// One claim on a share's word (lane 0 of a wave): `inc` 1 takes the next tile
+// from the front, 1 << 16 the next from the back; the returned word before
+// the add decides (valid iff front + back < tiles).  Eight ordinary stores to
+// the workgroup's dummy words follow, so the compiler's wait-count model sees
+// the atomic eight memory operations deep: any wait it inserts before the
+// result is used is then at most vmcnt(8), which in hardware never waits for
+// the tile loads issued after these stores (eight per wave per tile).
+__device__ __forceinline__ unsigned long long claim_word(unsigned long long* word,
+                                                         unsigned long long inc, int* dummy) {
+  const unsigned long long old =
+      __hip_atomic_fetch_add(word, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    __hip_atomic_store(dummy + i, i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  asm volatile("" ::: "memory");
+  return old;
+}
 
 // `next(nx)` names the share's next segment (false: none); it is asked
 // after this segment's first loads are issued, so its reads overlap them.
 // Returns whether a next segment was found (its first loads are then in
-// flight: call it with `pre`).
-template <typename NextFn>
+// flight: call it with `pre`).  s_claim: one LDS int, the verdict of the
+// owner's pending tail claim for every wave; w: this workgroup's share.
+template <bool kSteal = false, typename NextFn>
 __device__ __forceinline__ bool decode_segment_lds(const AttnParams& p, char* stage0, char* stage1,
                                                    char* qlds,
                                                    const int32_t* __restrict__ block_tables,
                                                    const DecSeg& sg, bool pre, NextFn&& next,
-                                                   DecSeg& nx) {
+                                                   DecSeg& nx, const StealArgs& sa, int* s_claim,
+                                                   int w) {
   const LaneId L = lane_id();
   const int wave = uniform(int(threadIdx.x >> 6));
   const int gl = wave & 3;   // kv head within the group
@@ -1079,14 +1134,19 @@ __device__ __forceinline__ bool decode_segment_lds(const AttnParams& p, char* st
   const int t0 = uniform(sg.t0);
   const int t1 = uniform(sg.t1);
   const int split = uniform(sg.split);
+  const int tail = kSteal ? uniform(sg.tail) : 0;
+  const int tslot = kSteal ? uniform(sg.tslot) : -1;
   const int g = kvg * 4 + gl;
-  const int ntiles = t1 > t0 ? t1 - t0 : 0;
+  const int nstatic = t1 > t0 ? t1 - t0 : 0;
+  int ntiles = nstatic;  // shrinks when another workgroup takes tail tiles
+  const int ft = nstatic - tail;  // first tail tile (tail <= nstatic - 4)
   const int c0 = t0 * kTile;
   // Fused append: the segment holding the row's last tile stores the new
   // token's K/V rows, and the wave whose DMA brings that token's row into
   // the last tile's stage overwrites it there with the same bytes (so the
-  // tile never depends on when the pool store lands).
-  const bool app = p.app_k != nullptr && ntiles > 0 && t1 == (ctx + kTile - 1) / kTile;
+  // tile never depends on when the pool store lands).  When the owner's
+  // last tile is taken, the taker does both.
+  const bool app = p.app_k != nullptr && nstatic > 0 && t1 == (ctx + kTile - 1) / kTile;
   const int app_row = (ctx - 1) & (kTile - 1);
   const bool app_wave = app && wave == (app_row & 7);
   u32x4_t app_kn, app_vn;
@@ -1095,6 +1155,20 @@ __device__ __forceinline__ bool decode_segment_lds(const AttnParams& p, char* st
   HalfState st;
   init_half(st);
   bool has_next = false;
+
+  // The owner's claims (lane 0 of wave 0): the claim for tile x is issued
+  // right after the DMA of tile x - 2 (step x - 4) and decided in step
+  // x - 2, before tile x's DMA, so like a tile it has two steps to return
+  // (loads complete in issue order: a claim issued ahead of a tile's DMA
+  // would have to return one step later, and an agent-scope atomic under
+  // full load takes longer).  After a step that issued a claim, wave 0's
+  // tile wait leaves that claim and its eight dummy stores outstanding too
+  // (vmcnt(17)).  claimed: the last tile whose claim went out.
+  unsigned long long cret[2] = {0, 0};  // claims in flight, by tile parity
+  int claimed = ft - 1;
+  int claim_step = -2;                  // the step that issued the last claim
+  unsigned long long* const cword = tail > 0 ? sa.claims + w : nullptr;
+  int* const cdummy = sa.dummy + int64_t(w) * 8;
 
   const int tok = int(p.tok_bytes);
   // Wave w loads rows w, w + 8, w + 16, w + 24 of K and of V of the tile at
@@ -1168,20 +1242,38 @@ __device__ __forceinline__ bool decode_segment_lds(const AttnParams& p, char* st
   // One step: tile j is in `stage`; tile j + 1 (if any) is already in flight.
   auto step = [&](int j, char* stage) {
     if (j + 1 < ntiles) {
-      __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8): this wave's loads of tile j
+      if (kSteal && wave == 0 && claim_step == j - 1) {
+        __builtin_amdgcn_s_waitcnt(0x4F71);  // vmcnt(17): tile j + 1, a claim, 8 stores
+      } else {
+        __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8): this wave's loads of tile j
+      }
     } else {
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     }
-    if (app_wave && j == ntiles - 1) {
+    // The claim for tile j + 2 went out in step j - 2: it is done.
+    const bool pend = tail > 0 && j + 2 >= ft && j + 2 <= claimed && j + 2 < ntiles;
+    if (pend && wave == 0 && L.lane == 0) {
+      const unsigned long long c = cret[j & 1];
+      *s_claim = claim_front(c) + claim_back(c) < claim_tiles(c) ? 1 : 0;
+    }
+    if (app_wave && j == nstatic - 1) {
       // this wave's DMA of the row has landed (vmcnt(0) above); the pool
       // store is issued after the segment's last tile
       *reinterpret_cast<u32x4_t*>(stage + app_row * kLdsPitch + L.lane * 16) = app_kn;
       *reinterpret_cast<u32x4_t*>(stage + kLdsTensor + app_row * kLdsPitch + L.lane * 16) = app_vn;
     }
     pf_barrier();
+    if (pend && uniform(*s_claim) == 0) ntiles = j + 2;
     read_stage(stage);
-    pf_barrier();  // every wave holds the stage in registers
-    if (j + 2 < ntiles) issue(j + 2, stage);
+    pf_barrier();  // every wave holds the stage in registers (and the verdict)
+    if (j + 2 < ntiles) {
+      issue(j + 2, stage);
+      if (tail > 0 && j + 4 >= ft && j + 4 < nstatic) {
+        if (wave == 0 && L.lane == 0) cret[j & 1] = claim_word(cword, 1ull, cdummy);
+        claimed = j + 4;
+        claim_step = j;
+      }
+    }
     if (has_next && j == ntiles - 1) {
       const int nb = uniform(nx.b);
       const int nkvg = uniform(nx.kvg);
@@ -1216,20 +1308,30 @@ __device__ __forceinline__ bool decode_segment_lds(const AttnParams& p, char* st
       for (int c = 0; c < 4; ++c)
         Q.op[0][c] = *reinterpret_cast<const u32x4_t*>(row + (((4 * c + L.lg) ^ L.lm) * 16));
     }
+    // The first tail tile is at least 4: its claim goes out in step 0,
+    // after tile 2's DMA.
     for (int j0 = 0; j0 < ntiles; j0 += 2) {
       step(j0, stage0);
       if (j0 + 1 < ntiles) step(j0 + 1, stage1);
     }
   }
 
-  if (app_wave) append_store(p, b, kvg, L.lane, app_kn, app_vn);
+  if (app_wave && ntiles == nstatic) append_store(p, b, kvg, L.lane, app_kn, app_vn);
+  // Tiles of the owner's tail that other workgroups took: they are pieces of
+  // their own, so this row is split even when the share held all of it.
+  const int taken = tail > 0 ? nstatic - ntiles : 0;
+  const int piece = split < 0 ? 0 : split;
+  const int out_split = split < 0 && taken > 0 ? 0 : split;
+  if (kSteal && tslot < 0 && wave == 0 && L.lane < 4)
+    sa.stolen[(int64_t(b) * (p.kvh * p.nslices) + kvg * 4 + L.lane) * p.max_splits + piece] =
+        taken;
   // Epilogue: lane (lm, lg) holds, for r = 0..3, dims 32lg + 8r + 4hf .. +3
   // of column lm; l is lane-partial over the key slots.
   const float l = rows4_sum(st.l);
   if (L.lm < p.hs) {
     const int head = g * p.group + L.lm;
     const float inv_l = 1.f / l;
-    if (split < 0) {
+    if (out_split < 0 && tslot < 0) {
       uint16_t* dst = p.out + int64_t(b) * p.o_st + int64_t(head) * p.o_sh;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -1239,15 +1341,25 @@ __device__ __forceinline__ bool decode_segment_lds(const AttnParams& p, char* st
                     pack_bf16x2_fast(st.o[2][r] * inv_l, st.o[3][r] * inv_l)};
       }
     } else {
-      const int64_t base = (int64_t(b) * p.num_heads + head) * p.max_splits + split;
+      float* po;
+      float* pl;
+      if (tslot >= 0) {
+        const int64_t base = int64_t(tslot) * sa.uh + gl * p.group + L.lm;
+        po = sa.tail_o + base * kD;
+        pl = sa.tail_lse + base;
+      } else {
+        const int64_t base = (int64_t(b) * p.num_heads + head) * p.max_splits + out_split;
+        po = p.part_o + base * kD;
+        pl = p.part_lse + base;
+      }
       const float il = l > 0.f ? inv_l : 0.f;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int d0 = 32 * L.lg + 8 * r + 4 * hf;
-        *reinterpret_cast<float4*>(p.part_o + base * kD + d0) =
+        *reinterpret_cast<float4*>(po + d0) =
             make_float4(st.o[0][r] * il, st.o[1][r] * il, st.o[2][r] * il, st.o[3][r] * il);
       }
-      if (L.lg == 0 && hf == 0) p.part_lse[base] = l > 0.f ? st.m + __log2f(l) : -INFINITY;
+      if (L.lg == 0 && hf == 0) *pl = l > 0.f ? st.m + __log2f(l) : -INFINITY;
     }
   }
   if (!has_next) {
@@ -2074,11 +2186,12 @@ __device__ void write_nan_rows(const AttnParams& p, int b, int kvg) {
 // kLds: 4 kv heads per workgroup staged through LDS, bf16
 // (decode_segment_lds: two stages in smem and smem1) or per-token-head int8
 // (decode_segment_lds_i8: a four-stage ring in smem); smem2 holds the query.
-template <int kEnc, bool kLds>
+template <int kEnc, bool kLds, bool kSteal = false>
 __device__ __forceinline__ void decode_sk_share(const AttnParams& p,
                                                 const int32_t* __restrict__ block_tables,
                                                 const int32_t* __restrict__ ctx_lens, int w,
-                                                int grid, char* smem, char* smem1, char* smem2) {
+                                                int grid, char* smem, char* smem1, char* smem2,
+                                                const StealArgs& sa) {
   constexpr bool kBfLds = kLds && kEnc == kBF16;
   constexpr bool kI8Lds = kLds && kEnc == kI8Tok;
   static_assert(!kLds || kBfLds || kI8Lds, "no LDS-staged form for this encoding");
@@ -2177,8 +2290,9 @@ __device__ __forceinline__ void decode_sk_share(const AttnParams& p,
           }
         } else if (share_of(P + row_cost) == w) {
           const int rb = row_of(r);
-          set_nseg(p, rb, r - rb * groups,
-                   share_of(P + row_cost + t - 1) - share_of(P + row_cost) + 1);
+          const int nseg = share_of(P + row_cost + t - 1) - share_of(P + row_cost) + 1;
+          // with the tail hand-out the merge also needs the row's first share
+          set_nseg(p, rb, r - rb * groups, kSteal ? nseg | (w << 16) : nseg);
         }
       }
       P += span;
@@ -2189,6 +2303,58 @@ __device__ __forceinline__ void decode_sk_share(const AttnParams& p,
   int r = __builtin_amdgcn_readlane(found_r, src);
   int P = __builtin_amdgcn_readlane(found_p, src);
   int ctx = __builtin_amdgcn_readlane(found_c, src);
+  // The last segment of share v (every lane of the wave takes part): its row
+  // unit, context, tiles [t0, t1) of the row and tail length.  The dynamic
+  // hand-out puts share v's tail there: min(tail, len - 4) tiles, so the
+  // owner keeps at least four (its first claim goes out in step 0).
+  struct TailGeo {
+    int r, ctx, t0, t1, n;
+  };
+  auto last_seg = [&](int v) -> TailGeo {
+    const int sv = share_start(v);
+    const int ev = min(W, share_start(v + 1));
+    int hr = -1, hp = 0, hc = 0, ht = 0;
+    int Q = excl;
+    for (int rr = r0; rr < r1; ++rr) {
+      const int c = ctx_of(rr);
+      const int t = ctx_tiles(c);
+      if (t > 0) {
+        const int Pr = Q + row_cost;
+        if (Pr < ev && Pr + t > sv) {
+          hr = rr;
+          hp = Pr;
+          hc = c;
+          ht = t;
+        }
+        Q += t + row_cost;
+      }
+    }
+    const unsigned long long m = __ballot(hr >= 0);
+    TailGeo tg{-1, 0, 0, 0, 0};
+    if (m != 0) {
+      const int src = uniform(63 - __clzll(m));  // the last row with tiles in the share
+      tg.r = __builtin_amdgcn_readlane(hr, src);
+      tg.ctx = __builtin_amdgcn_readlane(hc, src);
+      const int Pr = __builtin_amdgcn_readlane(hp, src);
+      const int t = __builtin_amdgcn_readlane(ht, src);
+      tg.t0 = max(sv, Pr) - Pr;
+      tg.t1 = min(ev, Pr + t) - Pr;
+      const int len = tg.t1 - tg.t0;
+      tg.n = len >= 5 ? min(sa.tail, len - 4) : 0;
+    }
+    return tg;
+  };
+  // The share's own tail; its owner announces the tail length in its claim
+  // word (a word still 0 offers nothing to take).
+  TailGeo own{-1, 0, 0, 0, 0};
+  if constexpr (kBfLds && kSteal) {
+    {
+      own = last_seg(w);
+      if (own.n > 0 && wave == 0 && lane == 0)
+        __hip_atomic_fetch_add(sa.claims + w, (unsigned long long)(own.n) << 32,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
   // The share's segments in order: each row unit with real tiles in
   // [start, end).
   auto next_seg = [&](DecSeg& sg) -> bool {
@@ -2201,7 +2367,7 @@ __device__ __forceinline__ void decode_sk_share(const AttnParams& p,
         const int first_share = share_of(Pr);
         const int nseg = share_of(Pr + t - 1) - first_share + 1;
         sg = DecSeg{b, r - b * groups, ctx, max(start, Pr) - Pr, min(end, Pr + t) - Pr,
-                    nseg == 1 ? -1 : w - first_share};
+                    nseg == 1 ? -1 : w - first_share, r == own.r ? own.n : 0, -1};
         hit = true;
       }
       P += t > 0 ? t + row_cost : 0;
@@ -2212,15 +2378,95 @@ __device__ __forceinline__ void decode_sk_share(const AttnParams& p,
     return false;
   };
   if constexpr (kBfLds) {
+    __shared__ int s_steal[12];  // [0]: owner claim verdict; [1..]: a taken tile
     // Each segment finds the next one (after issuing its own first loads)
     // and issues that one's first loads under its own last tile.
     DecSeg cur, nxt;
     bool have = next_seg(cur);
     bool pre = false;
     while (have) {
-      have = decode_segment_lds(p, smem, smem1, smem2, block_tables, cur, pre, next_seg, nxt);
+      have = decode_segment_lds<kSteal>(p, smem, smem1, smem2, block_tables, cur, pre, next_seg,
+                                        nxt, sa, s_steal, w);
       pre = have;
       cur = nxt;
+    }
+    if constexpr (kSteal) {
+      // Own share done: take single tail tiles from the back of other shares,
+      // the one with the most left first (then the nearest after this one).
+      // A taken tile is its own partial (tail slot v * kDecTailMax + j).  The
+      // claims are wave 0's; the others read the result from LDS.  Every
+      // failed claim leaves that share's word at or past its tail, so no
+      // share is tried twice and the loop ends.
+      int tv = -1, tleft = 0;
+      int* const dummy = sa.dummy + int64_t(w) * 8;
+      auto thief_next = [&](DecSeg& nx) -> bool {
+        if (wave == 0) {
+          int got = 0;
+          DecSeg out{0, 0, 0, 0, 0, -1, 0, -1};
+          for (int tries = 0; tries <= grid && got == 0; ++tries) {
+            if (tleft <= 0) {
+              int best = 0;
+              for (int v0 = 0; v0 < grid; v0 += 64) {
+                const int v = v0 + lane;
+                if (v < grid && v != w) {
+                  const unsigned long long o = __hip_atomic_load(
+                      sa.claims + v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                  const int rem = claim_tiles(o) - claim_front(o) - claim_back(o);
+                  const int dist = (v - w - 1 + grid) % grid;
+                  if (rem >= sa.steal_min) best = max(best, (rem << 9) | (511 - dist));
+                }
+              }
+              best = wave_max(best);
+              if (best == 0) break;
+              tv = (w + 1 + (511 - (best & 511))) % grid;
+              tleft = 1;
+            }
+            unsigned long long o = 0;
+            if (lane == 0) o = claim_word(sa.claims + tv, 1ull << 16, dummy);
+            const uint32_t lo = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(o))));
+            const uint32_t hi = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(o >> 32))));
+            o = (uint64_t(hi) << 32) | lo;
+            const int f = claim_front(o), bk = claim_back(o), n = claim_tiles(o);
+            // The word's tail length must be the one the partition gives that
+            // share (it always is while every launch's merge resets the words),
+            // so a taken tile is always one of the share's tail tiles.
+            const TailGeo tg = last_seg(tv);
+            if (f + bk < n && n == tg.n) {
+              tleft = n - f - bk - 1 >= sa.steal_min ? 1 : 0;
+              const int rb = uniform(row_of(tg.r));
+              out = DecSeg{rb, tg.r - rb * groups, tg.ctx, tg.t1 - 1 - bk, tg.t1 - bk, -1, 0,
+                           tv * kDecTailMax + bk};
+              got = 1;
+            } else {
+              tleft = 0;
+            }
+          }
+          if (lane == 0) {
+            s_steal[1] = got;
+            s_steal[2] = out.b;
+            s_steal[3] = out.kvg;
+            s_steal[4] = out.ctx;
+            s_steal[5] = out.t0;
+            s_steal[6] = out.t1;
+            s_steal[7] = out.tslot;
+          }
+        }
+        pf_barrier();
+        const int got = uniform(s_steal[1]);
+        if (got) {
+          nx = DecSeg{uniform(s_steal[2]), uniform(s_steal[3]), uniform(s_steal[4]),
+                      uniform(s_steal[5]), uniform(s_steal[6]), -1, 0, uniform(s_steal[7])};
+        }
+        return got != 0;
+      };
+      have = thief_next(cur);
+      pre = false;
+      while (have) {
+        have = decode_segment_lds<kSteal>(p, smem, smem1, smem2, block_tables, cur, pre,
+                                          thief_next, nxt, sa, s_steal, w);
+        pre = have;
+        cur = nxt;
+      }
     }
   } else {
     DecSeg sg;
@@ -2247,7 +2493,19 @@ paged_decode_sk_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
   __shared__ __align__(16) char smem2[kLds ? kLdsQ : 16];
   touch_kernel_args(int(sizeof(AttnParams) + 2 * sizeof(void*)));
   decode_sk_share<kEnc, kLds>(p, block_tables, ctx_lens, int(blockIdx.x), int(gridDim.x), smem,
-                              smem1, smem2);
+                              smem1, smem2, StealArgs{});
+}
+
+// The bf16 LDS decode with the dynamic tail hand-out.
+__global__ void __launch_bounds__(kThreads)
+paged_decode_steal_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
+                          const int32_t* __restrict__ ctx_lens, StealArgs sa) {
+  __shared__ __align__(16) char smem[kLdsStage];
+  __shared__ __align__(16) char smem1[kLdsStage];
+  __shared__ __align__(16) char smem2[kLdsQ];
+  touch_kernel_args(int(sizeof(AttnParams) + 2 * sizeof(void*) + sizeof(StealArgs)));
+  decode_sk_share<kBF16, true, true>(p, block_tables, ctx_lens, int(blockIdx.x), int(gridDim.x),
+                                     smem, smem1, smem2, sa);
 }
 
 // ---------------------------------------------------------------------------
@@ -2478,10 +2736,10 @@ mixed_sk_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t* _
           const int nseg = (P + t - 1) / S - P / S + 1;
           const int split = nseg == 1 ? -1 : w - P / S;
           if constexpr (kLds) {
-            const DecSeg sg{b, r - b * groups, ctx, t0, t1, split};
+            const DecSeg sg{b, r - b * groups, ctx, t0, t1, split, 0, -1};
             DecSeg unused;
             decode_segment_lds(p, smem, smem1, smem2, block_tables, sg, false,
-                               [](DecSeg&) { return false; }, unused);
+                               [](DecSeg&) { return false; }, unused, StealArgs{}, nullptr, w);
           } else {
             decode_segment<kEnc>(p, smem, block_tables + int64_t(b) * p.bt_stride, b,
                                  r - b * groups, ctx, t0, t1, split);
@@ -4000,7 +4258,7 @@ mixed_split_kernel(AttnParams pd, AttnParams pp, int dec_wgs) {
   const int b = int(blockIdx.x);
   if (b < dec_wgs) {
     decode_sk_share<kBF16, true>(pd, pd.block_tables, pd.ctx_lens, b, dec_wgs, lds,
-                                 lds + kLdsStage, lds + 2 * kLdsStage);
+                                 lds + kLdsStage, lds + 2 * kLdsStage, StealArgs{});
   } else {
     prefill_sk2_share<false>(pp, pp.cu_q, pp.cu_k, pp.block_tables, b - dec_wgs,
                              int(gridDim.x) - dec_wgs, lds,
@@ -4016,18 +4274,28 @@ mixed_split_kernel(AttnParams pd, AttnParams pp, int dec_wgs) {
 constexpr int kMergeWaves = 4;
 constexpr int kMergeBatch = 16;
 // Block `block` of the split merge of a decode launch (merge_kernel).
-__device__ __forceinline__ void merge_rows(const AttnParams& p, int num_rows, int64_t block) {
+template <bool kSteal = false>
+__device__ __forceinline__ void merge_rows(const AttnParams& p, int num_rows, int64_t block,
+                                           const StealArgs& sa = StealArgs{}) {
   const int lane = threadIdx.x & 63;
   const int64_t wv = block * kMergeWaves + (threadIdx.x >> 6);
   const int64_t row = wv / p.num_heads;
   if (row >= num_rows) return;
   const int head = int(wv - row * p.num_heads);
   int nsplit;
+  int first_share = 0;
+  int taken = 0;  // lane k: tiles other workgroups took from piece k (tail hand-out)
   if (p.sk_nseg != nullptr) {
     // Stream-K: the split count of the head's kv slice in this row.
     const int g = head / p.group;
     const int kvs = g * p.nslices + (head - g * p.group) / p.hs;
-    nsplit = p.sk_nseg[row * (p.kvh * p.nslices) + kvs];
+    const int64_t unit = row * (p.kvh * p.nslices) + kvs;
+    nsplit = p.sk_nseg[unit];
+    if constexpr (kSteal) {
+      if (lane < p.max_splits) taken = sa.stolen[unit * p.max_splits + lane];
+      first_share = nsplit >> 16;
+      nsplit &= 0xffff;
+    }
   } else if (row < p.n_dec) {
     const int ctx = p.ctx_lens[row];
     nsplit = ctx > 0 ? (ctx + p.chunk_tokens - 1) / p.chunk_tokens : 1;
@@ -4062,7 +4330,8 @@ __device__ __forceinline__ void merge_rows(const AttnParams& p, int num_rows, in
   const int first = min(p.merge_first, p.max_splits);
   load_batch(0, first);
   nsplit = uniform(nsplit);
-  if (nsplit <= 1) return;
+  const unsigned long long taken_mask = __ballot(lane < nsplit && taken > 0);
+  if (nsplit <= 1 && taken_mask == 0) return;
   float m = -INFINITY, l = 0.f, acc0 = 0.f, acc1 = 0.f;
   int s0 = 0, cnt = min(first, nsplit);
   while (true) {
@@ -4092,6 +4361,50 @@ __device__ __forceinline__ void merge_rows(const AttnParams& p, int num_rows, in
     cnt = min(kMergeBatch, nsplit - s0);
     load_batch(s0, cnt);
   }
+  // Tiles taken from piece k's tail: tail slots (first_share + k) *
+  // kDecTailMax + j, j < taken[k], of this head within its row unit.
+  if (kSteal && taken_mask != 0) {
+    const int g = head / p.group;
+    const int hu = head - (g & ~3) * p.group;  // 4 kv heads per row unit
+    unsigned long long mask = taken_mask;
+    while (mask != 0) {
+      const int k = uniform(int(__ffsll(mask)) - 1);
+      mask &= mask - 1;
+      const int c = min(kDecTailMax, uniform(__builtin_amdgcn_readlane(taken, k)));
+      const int64_t slot0 = int64_t(first_share + k) * kDecTailMax;
+      float tl[kDecTailMax];
+      float2 to[kDecTailMax];
+#pragma unroll
+      for (int j = 0; j < kDecTailMax; ++j) {
+        if (j < c) {
+          const int64_t base = (slot0 + j) * sa.uh + hu;
+          tl[j] = sa.tail_lse[base];
+          to[j] = *reinterpret_cast<const float2*>(sa.tail_o + base * kD + 2 * lane);
+        }
+      }
+      float bm = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < kDecTailMax; ++j)
+        if (j < c) bm = fmaxf(bm, tl[j]);
+      const float m_new = fmaxf(m, bm);
+      if (m_new != -INFINITY) {
+        const float a = __builtin_amdgcn_exp2f(m - m_new);
+        l *= a;
+        acc0 *= a;
+        acc1 *= a;
+#pragma unroll
+        for (int j = 0; j < kDecTailMax; ++j) {
+          if (j < c) {
+            const float wgt = __builtin_amdgcn_exp2f(tl[j] - m_new);
+            l += wgt;
+            acc0 += wgt * to[j].x;
+            acc1 += wgt * to[j].y;
+          }
+        }
+        m = m_new;
+      }
+    }
+  }
   const float inv = 1.f / l;
   uint16_t* dst = p.out + row * p.o_st + int64_t(head) * p.o_sh + 2 * lane;
   *reinterpret_cast<uint32_t*>(dst) = pack_bf16x2_fast(acc0 * inv, acc1 * inv);
@@ -4102,10 +4415,28 @@ __global__ void __launch_bounds__(64 * kMergeWaves) merge_kernel(AttnParams p, i
   merge_rows(p, num_rows, blockIdx.x);
 }
 
+// The merge of a decode launch with the dynamic tail hand-out: the taken
+// tiles' partials too.  The decode launch is over, so its claim words go
+// back to zero here for the next launch that uses this claim set.
+__global__ void __launch_bounds__(64 * kMergeWaves)
+merge_steal_kernel(AttnParams p, int num_rows, StealArgs sa) {
+  touch_kernel_args(int(sizeof(AttnParams) + sizeof(int) + sizeof(StealArgs)));
+  if (blockIdx.x == 0) {
+    for (int i = threadIdx.x; i < sa.grid; i += 64 * kMergeWaves) sa.claims[i] = 0;
+  }
+  merge_rows<true>(p, num_rows, blockIdx.x, sa);
+}
+
 void launch_merge(const AttnParams& p, int64_t rows, hipStream_t st) {
   const int64_t waves = rows * p.num_heads;
   merge_kernel<<<unsigned((waves + kMergeWaves - 1) / kMergeWaves), 64 * kMergeWaves, 0, st>>>(
       p, int(rows));
+}
+
+void launch_merge_steal(const AttnParams& p, int64_t rows, const StealArgs& sa, hipStream_t st) {
+  const int64_t waves = rows * p.num_heads;
+  merge_steal_kernel<<<unsigned((waves + kMergeWaves - 1) / kMergeWaves), 64 * kMergeWaves, 0,
+                       st>>>(p, int(rows), sa);
 }
 
 // Split-K merge of a stream-K prefill launch: one wave per (query row, kv
@@ -4353,6 +4684,26 @@ size_t sk_workspace_bytes(int64_t rows, int64_t heads, int64_t kv_slices, int ma
          256;
 }
 
+// Workspace of a stream-K paged decode whose shape can take the dynamic tail
+// hand-out (4 kv heads of one slice per workgroup): after the stream-K part,
+// the taken-tile counts per (row, kv slice, piece), the tail partials of
+// every share ([share][kDecTailMax][uh heads][D] fp32 and the matching
+// log2-sum-exps) and eight dummy words per workgroup.
+struct StealLayout {
+  size_t stolen, tail_o, tail_lse, dummy, total;
+};
+StealLayout steal_layout(size_t base, int64_t rows, int64_t kv_slices, int max_splits, int grid,
+                         int uh) {
+  auto al = [](size_t x) { return (x + 255) / 256 * 256; };
+  StealLayout L;
+  L.stolen = al(base);
+  L.tail_o = al(L.stolen + size_t(rows) * size_t(kv_slices) * size_t(max_splits) * sizeof(int));
+  L.tail_lse = al(L.tail_o + size_t(grid) * kDecTailMax * size_t(uh) * kD * sizeof(float));
+  L.dummy = al(L.tail_lse + size_t(grid) * kDecTailMax * size_t(uh) * sizeof(float));
+  L.total = al(L.dummy + size_t(grid) * 8 * sizeof(int));
+  return L;
+}
+
 // Keys per prefill split: an eighth of the longest key range, at least 512
 // (the long chunk of a mixed batch then fills the CUs with its splits).
 int plan_prefill_split(int64_t max_seqlen_k) {
@@ -4368,6 +4719,14 @@ struct HeadPlan {
   int kvs_per_wg;  // decode slices per workgroup
   int groups;      // decode slice groups: kvh * nslices / kvs_per_wg
 };
+
+// Shapes whose bf16 stream-K decode runs LDS-staged segments of 4 kv heads
+// (one slice each): the ones that can take the dynamic tail hand-out.
+bool steal_shape(const HeadPlan& hp) { return hp.kvs_per_wg == 4 && hp.nslices == 1; }
+// Default tail tiles per share, and the fewest tiles a share must have left
+// in its tail for another workgroup to take one.
+constexpr int kDecTailDefault = 6;
+constexpr int kStealMinDefault = 2;
 
 HeadPlan plan_heads(int64_t num_heads, int64_t kvh) {
   HeadPlan h;
@@ -4576,10 +4935,40 @@ extern "C" size_t kvc_paged_decode_workspace_bytes(int64_t batch, int64_t num_he
   const HeadPlan hp = plan_heads(num_heads, num_kv_heads);
   const int64_t max_ctx = max_blocks_per_seq * page_size;
   const SkPlan sp = plan_stream_k(batch, num_heads, max_ctx);
-  if (sp.on) return sk_workspace_bytes(batch, num_heads, num_kv_heads * hp.nslices, sp.max_splits);
+  if (sp.on) {
+    const size_t base = sk_workspace_bytes(batch, num_heads, num_kv_heads * hp.nslices,
+                                           sp.max_splits);
+    if (!steal_shape(hp)) return base;
+    return steal_layout(base, batch, num_kv_heads * hp.nslices, sp.max_splits, sp.grid,
+                        hp.kvs_per_wg * hp.hs)
+        .total;
+  }
   const int ch = plan_decode_chunk(batch, hp.groups, max_ctx);
   const int64_t splits = max_ctx > 0 ? (max_ctx + ch - 1) / ch : 1;
   return partial_bytes(batch, num_heads, splits);
+}
+
+extern "C" int kvc_paged_decode_layout(int64_t batch, int64_t num_heads, int64_t num_kv_heads,
+                                       int64_t head_dim, int64_t page_size,
+                                       int64_t max_blocks_per_seq, int64_t* layout) {
+  clear_error();
+  KVC_REQUIRE(layout != nullptr, KVC_ERR_VALUE, "paged_decode_layout: layout is required");
+  KVC_REQUIRE(batch > 0 && num_kv_heads > 0 && num_heads > 0 && num_heads % num_kv_heads == 0 &&
+                  head_dim == kD && page_size > 0 && max_blocks_per_seq > 0,
+              KVC_ERR_VALUE, "paged_decode_layout: bad launch shape");
+  const HeadPlan hp = plan_heads(num_heads, num_kv_heads);
+  const SkPlan sp = plan_stream_k(batch, num_heads, max_blocks_per_seq * page_size);
+  KVC_REQUIRE(sp.on, KVC_ERR_VALUE, "paged_decode_layout: the launch is not stream-K");
+  const int64_t kv_slices = num_kv_heads * hp.nslices;
+  const size_t base = sk_workspace_bytes(batch, num_heads, kv_slices, sp.max_splits);
+  layout[0] = int64_t(sk_partial_part(batch, num_heads, sp.max_splits));
+  layout[1] = steal_shape(hp) ? int64_t(steal_layout(base, batch, kv_slices, sp.max_splits,
+                                                     sp.grid, hp.kvs_per_wg * hp.hs)
+                                            .stolen)
+                              : -1;
+  layout[2] = sp.max_splits;
+  layout[3] = kv_slices;
+  return KVC_OK;
 }
 
 namespace {
@@ -4660,7 +5049,11 @@ int paged_decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, con
     // falls inside a row); longer rows of a ragged batch load the rest later.
     const int64_t units = batch * hp.groups;
     p.merge_first = int(std::min<int64_t>(kMergeBatch, (sp.grid + units - 1) / units + 1));
-    const size_t need = sk_workspace_bytes(batch, num_heads, num_kv_heads * hp.nslices, sp.max_splits);
+    const int64_t kv_slices = num_kv_heads * hp.nslices;
+    const size_t base = sk_workspace_bytes(batch, num_heads, kv_slices, sp.max_splits);
+    const StealLayout sl =
+        steal_layout(base, batch, kv_slices, sp.max_splits, sp.grid, hp.kvs_per_wg * hp.hs);
+    const size_t need = steal_shape(hp) ? sl.total : base;
     KVC_REQUIRE(workspace != nullptr && workspace_bytes >= need, KVC_ERR_WORKSPACE,
                 "paged_decode: workspace of %zu bytes needed (got %zu)", need, workspace_bytes);
     set_partials(p, workspace, batch);
@@ -4701,6 +5094,32 @@ int paged_decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, con
       tl_record->grid = sp.grid;
       tl_record->rows = batch;
       return KVC_OK;
+    }
+    // The dynamic tail hand-out (bf16 LDS segments): a zeroed claim set for
+    // this launch, the tail partials and counts in the workspace.
+    StealArgs sa{};
+    const int tail = std::min(kDecTailMax, std::max(0, env_int("KVC_DECODE_TAIL", kDecTailDefault)));
+    if (lds_bf16 && steal_shape(hp) && tail > 0 && env_int("KVC_DECODE_STEAL", 0) != 0) {
+      unsigned long long* claims = claim_set(st, sp.grid);
+      if (claims != nullptr) {
+        char* ws = static_cast<char*>(workspace);
+        sa.claims = claims;
+        sa.stolen = reinterpret_cast<int*>(ws + sl.stolen);
+        sa.tail_o = reinterpret_cast<float*>(ws + sl.tail_o);
+        sa.tail_lse = reinterpret_cast<float*>(ws + sl.tail_lse);
+        sa.dummy = reinterpret_cast<int*>(ws + sl.dummy);
+        sa.tail = tail;
+        sa.uh = hp.kvs_per_wg * hp.hs;
+        sa.grid = sp.grid;
+        sa.steal_min = std::max(1, env_int("KVC_STEAL_MIN", kStealMinDefault));
+      }
+    }
+    if (sa.claims != nullptr) {
+      paged_decode_steal_kernel<<<sp.grid, kThreads, 0, st>>>(p, block_tables, context_lens, sa);
+      rc = check_launch("paged_decode");
+      if (rc != KVC_OK) return rc;
+      launch_merge_steal(p, batch, sa, st);
+      return check_launch("paged_decode merge");
     }
     switch (kv_dtype) {
       case KVC_KV_BF16:

@@ -40,6 +40,12 @@ inline int check_launch(const char* what) {
 
 inline hipStream_t as_stream(kvc_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Zeroed claim words for one paged decode launch on `stream` with `words`
+// workgroups (kvc_claims.hip), or null: the launch then uses the static
+// partition alone.
+unsigned long long* claim_set(hipStream_t stream, int words);
+int claim_set_words();
+
 // ---------------------------------------------------------------------------
 // Device-side vector types and helpers.
 // ---------------------------------------------------------------------------

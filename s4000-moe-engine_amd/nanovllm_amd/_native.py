@@ -51,6 +51,7 @@ SIGNATURES = {
                                     _P]),
     "kvc_kv_calib_freeze": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P]),
     "kvc_paged_decode_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64]),
+    "kvc_paged_decode_layout": (_INT, [_I64, _I64, _I64, _I64, _I64, _I64, _P]),
     "kvc_paged_decode": (_INT, [_P, _I64, _I64, _P, _P, _I64, _I64, _I64, _I64, _INT,
                                 _P, _P, _P, _P, _P, _P, _I64, _P, _I64, _I64, _P, _I64,
                                 _I64, _F32, _P, _I64, _I64, _P, _SZ, _P]),

@@ -31,3 +31,13 @@ def pytest_collection_modifyitems(config, items):
     for item in items:
         if "gpu" in item.keywords:
             item.add_marker(skip)
+
+
+@pytest.fixture
+def deterministic_decode(monkeypatch):
+    """Paged decode without the dynamic tail hand-out (KVC_DECODE_STEAL=0):
+    which workgroup takes which tail tile depends on timing, and with it the
+    fp32 summation order of a split row, so bitwise comparisons of two
+    launches' outputs need the static partition alone.  Pool bytes are
+    bit-exact either way."""
+    monkeypatch.setenv("KVC_DECODE_STEAL", "0")

@@ -38,25 +38,56 @@ def test_abi_version_and_error_string():
     assert isinstance(lib.kvc_last_error(), bytes)
 
 
+def _al(x):
+    return (x + 255) // 256 * 256
+
+
+def _tail_region(base, rows, kvs, ms, uh, grid=256, tail_max=8):
+    """The dynamic tail hand-out's part of a decode workspace, after the
+    stream-K part: taken counts int32 [rows][kvs][ms], tail partials fp32
+    [grid][tail_max][uh][128], their log2-sum-exps [grid][tail_max][uh] and
+    eight dummy int32 words per workgroup, each 256-byte aligned."""
+    stolen = _al(base)
+    tail_o = _al(stolen + rows * kvs * ms * 4)
+    tail_lse = _al(tail_o + grid * tail_max * uh * 128 * 4)
+    dummy = _al(tail_lse + grid * tail_max * uh * 4)
+    return stolen, _al(dummy + grid * 8 * 4)
+
+
 def test_workspace_queries_are_host_only():
     # Pure host arithmetic (no GPU here; the plan assumes 256 CUs).  Paged
     # decode is stream-K: every workgroup takes an equal share (>= 8 tiles of
     # 32 keys) of all rows' tiles, so a row of up to 4096 keys (128 tiles) is
     # split at most 128 / 8 + 1 = 17 ways.  The workspace holds fp32 partials
     # (128 dims + 1 log-sum-exp per row, head and split), 256-byte aligned,
-    # then one int32 split count per (row, kv slice), plus 256 bytes.
+    # then one int32 split count per (row, kv slice), plus 256 bytes; shapes
+    # of 4 kv heads per workgroup (32q/4kv: 8 q heads per kv head) add the
+    # tail hand-out's region for 32 heads per row unit.
     q = _native.query
     part = 64 * 32 * 17 * 129 * 4
+    base = (part + 255) // 256 * 256 + 64 * 4 * 4 + 256
     assert q("kvc_paged_decode_workspace_bytes", 64, 32, 4, 128, 256, 16) == \
-        (part + 255) // 256 * 256 + 64 * 4 * 4 + 256
+        _tail_region(base, 64, 4, 17, 32)[1] == 51808512
     # Splits are capped at 64 however long the rows are.
     part = 4 * 32 * 64 * 129 * 4
+    base = (part + 255) // 256 * 256 + 4 * 4 * 4 + 256
     assert q("kvc_paged_decode_workspace_bytes", 4, 32, 4, 128, 256, 1024) == \
-        (part + 255) // 256 * 256 + 4 * 4 * 4 + 256
-    # 32 kv heads: 32 counts per row.
+        _tail_region(base, 4, 4, 64, 32)[1]
+    # 32 kv heads (8 per workgroup): 32 counts per row, no tail region.
     part = 8 * 32 * 17 * 129 * 4
     assert q("kvc_paged_decode_workspace_bytes", 8, 32, 32, 128, 256, 16) == \
         (part + 255) // 256 * 256 + 8 * 32 * 4 + 256
+
+
+def test_decode_layout_query():
+    import ctypes
+    lay = (ctypes.c_int64 * 4)()
+    _native.call("kvc_paged_decode_layout", 64, 32, 4, 128, 256, 16, lay)
+    part = _al(64 * 32 * 17 * 129 * 4)
+    base = part + 64 * 4 * 4 + 256
+    assert list(lay) == [part, _tail_region(base, 64, 4, 17, 32)[0], 17, 4]
+    _native.call("kvc_paged_decode_layout", 8, 32, 32, 128, 256, 16, lay)
+    assert list(lay) == [_al(8 * 32 * 17 * 129 * 4), -1, 17, 32]
 
 
 def test_bad_arguments_map_to_python_exceptions():

@@ -173,7 +173,7 @@ def test_pages_smaller_than_256(page, decode_path):
 
 @pytest.mark.parametrize("case", ["b64x4096", "ragged-with-empty", "int64-negative-slots",
                                   "unaligned-key-fallback", "two-kv-heads-fallback"])
-def test_decode_append_equals_store_then_decode(case, decode_path):
+def test_decode_append_equals_store_then_decode(case, decode_path, deterministic_decode):
     """paged_decode_append (the store inside the decode launch where the
     layout allows) against store_kvcache then paged_decode_attention: the
     same output bits and the same pool bytes."""

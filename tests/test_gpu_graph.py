@@ -61,7 +61,8 @@ def _eager_padded(kcs, vcs, q, k, v, slots, lens, tables, bucket, runner):
     return torch.stack(outs)[:, :bs]
 
 
-def test_graph_replays_match_eager_and_touch_only_live_slots_and_scratch():
+def test_graph_replays_match_eager_and_touch_only_live_slots_and_scratch(
+        deterministic_decode):
     g = torch.Generator().manual_seed(0)
     kcs = [torch.randn(NB + 1, PAGE, KVH, 128, generator=g).to(torch.bfloat16).to(DEV)
            for _ in range(L)]
@@ -119,7 +120,7 @@ def _runner_with_pool(init, async_groups):
     return r
 
 
-def test_graph_replay_after_async_eviction_of_the_appended_block():
+def test_graph_replay_after_async_eviction_of_the_appended_block(deterministic_decode):
     """An eviction put of block B on the copy streams, then a graph replay
     whose appends land in B (the block manager reallocated it): the runner
     built by from_kv_runner fences before the replay, so the host slot holds

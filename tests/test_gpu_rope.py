@@ -128,7 +128,7 @@ def test_empty_batch_and_no_cache():
 
 
 @pytest.mark.parametrize("mode", ["decode", "prefill"])
-def test_attention_forward_fused_equals_prologue_then_forward(mode):
+def test_attention_forward_fused_equals_prologue_then_forward(mode, deterministic_decode):
     """Attention.forward_fused (norm + rope + append in one launch, then
     attention without a second store) == the prologue without the append
     followed by the layer's ordinary forward (which appends), bit for bit."""

@@ -32,7 +32,7 @@ def _static_call(wl, k_cache, v_cache, out):
              torch.cuda.current_stream().cuda_stream)
 
 
-def test_static_scratch_equals_workspace_entry_point_twice():
+def test_static_scratch_equals_workspace_entry_point_twice(deterministic_decode):
     cases = [("64x4096", [4096] * 64, 1100, 3),
              ("ragged-smaller", uniform_lengths(9, 1, 2500, seed=5), 120, 4)]
     for label, lens, blocks, seed in cases:
