@@ -1052,9 +1052,10 @@ __device__ __forceinline__ void attend_tile_half(HalfState& st, const u32x4_t (&
 // The fused append's 16 bytes of lane `lane` of row b's new K and V, for kv
 // heads 4 kvg .. 4 kvg + 3: head 4 kvg + lane / 16, dims 8 (lane % 16) .. +7,
 // i.e. the bytes the lane's DMA slot covers in a token row of the pool.
+template <int kHeads = 4>
 __device__ __forceinline__ void append_load(const AttnParams& p, int b, int kvg, int lane,
                                             u32x4_t& kn, u32x4_t& vn) {
-  const int head = kvg * 4 + (lane >> 4);
+  const int head = kvg * kHeads + (lane >> 4);
   const int d = (lane & 15) * 8;
   kn = *reinterpret_cast<const u32x4_t*>(p.app_k + int64_t(b) * p.app_k_st +
                                          int64_t(head) * p.app_k_sh + d);
@@ -1063,13 +1064,14 @@ __device__ __forceinline__ void append_load(const AttnParams& p, int b, int kvg,
 }
 
 // Stores them at row b's slot (store_kvcache's rules for the slot).
+template <int kHeads = 4>
 __device__ __forceinline__ void append_store(const AttnParams& p, int b, int kvg, int lane,
                                              const u32x4_t& kn, const u32x4_t& vn) {
   const int64_t raw = p.app_slot_bytes == 8 ? load_index<8>(p.app_slots, b)
                                             : load_index<4>(p.app_slots, b);
   const int64_t slot = wrap_slot(raw, p.app_num_slots);
   if (slot < 0 || slot >= p.app_num_slots) return;
-  const int64_t off = slot * p.tok_bytes + int64_t(kvg) * 1024 + lane * 16;
+  const int64_t off = slot * p.tok_bytes + int64_t(kvg) * (kHeads * 256) + lane * 16;
   *reinterpret_cast<u32x4_t*>(const_cast<char*>(p.k_cache) + off) = kn;
   *reinterpret_cast<u32x4_t*>(const_cast<char*>(p.v_cache) + off) = vn;
 }
@@ -1360,6 +1362,261 @@ __device__ __forceinline__ bool decode_segment_lds(const AttnParams& p, char* st
             make_float4(st.o[0][r] * il, st.o[1][r] * il, st.o[2][r] * il, st.o[3][r] * il);
       }
       if (L.lg == 0 && hf == 0) *pl = l > 0.f ? st.m + __log2f(l) : -INFINITY;
+    }
+  }
+  if (!has_next) {
+    // nothing in flight for a next segment: drain and realign the waves
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+  return has_next;
+}
+
+// The LDS-staged segment for 2 kv heads per workgroup (bf16; the 16q/2kv
+// shard of a 2-way tensor-parallel rank): a token row is 512 B, so one
+// 66.5 KB stage holds 64 keys (two 32-key tiles) of K and V and a step
+// attends both.  Wave w serves kv head w & 1, dim half (w >> 1) & 1 and tile
+// w >> 2 of the step: per step every wave does exactly the work of the 4-head
+// segment (one head, one dim half, one 32-key tile) and issues the same 8
+// loads, so the wait counts are unchanged.  A direct-to-LDS load brings two
+// consecutive token rows (64 lanes x 16 B), stored as a pair at the 1040-byte
+// pitch.  A step's second tile past the segment loads nothing (a zero-length
+// buffer) and is not attended.  The two tiles' softmax states of a (head, dim
+// half) merge through LDS once, in the epilogue.
+constexpr int kLdsQ2 = 2 * 16 * 256;            // query block: [2 heads][16 columns][256 B]
+constexpr int kLds2Merge = 4 * 18 * 64 * 4;     // tile-1 waves' states: 16 O, m, l per lane
+constexpr int kLdsSmem2 = kLdsQ2 + kLds2Merge;
+static_assert(2 * kLdsStage + kLdsSmem2 <= 160 * 1024, "one workgroup per CU");
+
+template <typename NextFn>
+__device__ __forceinline__ bool decode_segment_lds2(const AttnParams& p, char* stage0,
+                                                    char* stage1, char* smem2,
+                                                    const int32_t* __restrict__ block_tables,
+                                                    const DecSeg& sg, bool pre, NextFn&& next,
+                                                    DecSeg& nx) {
+  const LaneId L = lane_id();
+  const int wave = uniform(int(threadIdx.x >> 6));
+  const int gl = wave & 1;         // kv head within the pair
+  const int hf = (wave >> 1) & 1;  // dim half
+  const int kt = wave >> 2;        // tile of the step
+  char* const qlds = smem2;
+  float* const mlds = reinterpret_cast<float*>(smem2 + kLdsQ2);
+  const int b = uniform(sg.b);
+  const int kvg = uniform(sg.kvg);
+  const int ctx = uniform(sg.ctx);
+  const int t0 = uniform(sg.t0);
+  const int t1 = uniform(sg.t1);
+  const int split = uniform(sg.split);
+  const int g = kvg * 2 + gl;
+  const int ntiles = t1 > t0 ? t1 - t0 : 0;
+  const int nsteps = (ntiles + 1) >> 1;
+  const int c0 = t0 * kTile;
+  // Fused append: the row's last tile is tile ntiles - 1 of this segment; its
+  // new token is stage row app_r of step app_step, brought by the lanes
+  // 32 (app_r & 1) .. + 31 of wave (app_r >> 1) & 7.
+  const bool app = p.app_k != nullptr && ntiles > 0 && t1 == (ctx + kTile - 1) / kTile;
+  const int app_r = ((ntiles - 1) & 1) * kTile + ((ctx - 1) & (kTile - 1));
+  const int app_step = (ntiles - 1) >> 1;
+  const bool app_wave = app && wave == ((app_r >> 1) & 7);
+  const bool app_lane = app_wave && (L.lane >> 5) == (app_r & 1);
+  u32x4_t app_kn, app_vn;
+
+  QOps<kBF16, 1> Q;
+  HalfState st;
+  init_half(st);
+  bool has_next = false;
+
+  const int tok = int(p.tok_bytes);
+  // Tile `key0` of a segment's row (b_) and kv pair (kvg_) as half `half` of
+  // a stage: wave w loads row pairs w and w + 8 of it, K and V.
+  auto issue_tile = [&](int b_, int kvg_, int key0, int half, bool live, char* base) {
+    i32x4_t kr, vr;
+    if (live) {
+      const int blk = table_entry(block_tables, int64_t(b_) * p.bt_stride + key0 / p.page);
+      const int64_t slot0 = int64_t(blk) * p.page + (key0 % p.page);
+      const int64_t grp_off = int64_t(kvg_) * 512;
+      kr = raw_rsrc(p.k_cache + slot0 * p.tok_bytes + grp_off, kTile * tok);
+      vr = raw_rsrc(p.v_cache + slot0 * p.tok_bytes + grp_off, kTile * tok);
+    } else {
+      kr = raw_rsrc(p.k_cache, 0);
+      vr = kr;
+    }
+    const uint32_t lb = lds_addr(base);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int pr = wave + 8 * q;  // row pair within the tile
+      const uint32_t dst = lb + (half * 16 + pr) * kLdsPitch;
+      dma_to_lds(kr, 2 * pr * tok + L.lane * 16, dst);
+      dma_to_lds(vr, 2 * pr * tok + L.lane * 16, dst + kLdsTensor);
+    }
+  };
+  // Step s of a segment starting at tile key c0_ with nt_ tiles.
+  auto issue_step = [&](int b_, int kvg_, int c0_, int nt_, int s_, char* base) {
+    issue_tile(b_, kvg_, uniform(c0_ + 2 * s_ * kTile), 0, true, base);
+    issue_tile(b_, kvg_, uniform(c0_ + (2 * s_ + 1) * kTile), 1, 2 * s_ + 1 < nt_, base);
+  };
+  // The query rides the same DMA ahead of a segment's first two steps: wave w
+  // brings columns 8 ((w >> 1) & 1) .. + 7 of kv head w & 1 (the waves of
+  // both tiles bring the same bytes to the same place).
+  auto issue_q = [&](int b_, int kvg_) {
+    const int g_ = kvg_ * 2 + gl;
+    const i32x4_t qr =
+        raw_rsrc(p.q + int64_t(b_) * p.q_st, int(int64_t(p.num_heads) * p.q_sh * 2));
+    const uint32_t lb = lds_addr(qlds);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int col = 8 * hf + 4 * s + (L.lane >> 4);
+      const int head = g_ * p.group + min(col, p.hs - 1);
+      const int chunk = (L.lane & 15) ^ col;
+      dma_to_lds(qr, int(int64_t(head) * p.q_sh * 2) + chunk * 16,
+                 lb + (gl * 16 + 8 * hf + 4 * s) * 256);
+    }
+  };
+
+  u32x4_t k[2][4];
+  u32x2_t vh[8];
+  // Key j of this wave's tile: stage row kt * 32 + j, pair (row >> 1).
+  auto row_addr = [&](const char* tb, int j) {
+    const int r = kt * kTile + j;
+    return tb + (r >> 1) * kLdsPitch + (r & 1) * 512 + gl * 256;
+  };
+  auto read_stage = [&](const char* kb) {
+    const char* vb = kb + kLdsTensor;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const char* row = row_addr(kb, h * 16 + L.lm) + L.lg * 16;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) k[h][c] = *reinterpret_cast<const u32x4_t*>(row + c * 64);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      vh[i] = *reinterpret_cast<const u32x2_t*>(row_addr(vb, key_of_slot(L.lg, i)) + L.lm * 16 +
+                                                hf * 8);
+  };
+  auto compute = [&](int s) {
+    const int tx = 2 * s + kt;
+    if (tx >= ntiles) return;  // the step's second tile past the segment
+    const int key0 = c0 + tx * kTile;
+    if (key0 + kTile <= ctx) {
+      attend_tile_half<false>(st, k, vh, Q, key0, ctx, ctx - 1, p.scale_log2, L);
+    } else {
+      attend_tile_half<true>(st, k, vh, Q, key0, ctx, ctx - 1, p.scale_log2, L);
+    }
+  };
+  auto step = [&](int s, char* stage) {
+    if (s + 1 < nsteps) {
+      __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8): this wave's loads of step s
+    } else {
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    }
+    if (app_lane && s == app_step) {
+      char* row = stage + (app_r >> 1) * kLdsPitch + (app_r & 1) * 512 + (L.lane & 31) * 16;
+      *reinterpret_cast<u32x4_t*>(row) = app_kn;
+      *reinterpret_cast<u32x4_t*>(row + kLdsTensor) = app_vn;
+    }
+    pf_barrier();
+    read_stage(stage);
+    pf_barrier();  // every wave holds the stage in registers
+    if (s + 2 < nsteps) issue_step(b, kvg, c0, ntiles, s + 2, stage);
+    if (has_next && s == nsteps - 1) {
+      const int nb = uniform(nx.b);
+      const int nkvg = uniform(nx.kvg);
+      const int nc0 = uniform(nx.t0) * kTile;
+      const int nnt = uniform(nx.t1) - uniform(nx.t0);
+      issue_q(nb, nkvg);
+      issue_step(nb, nkvg, nc0, nnt, 0, stage0);
+      if (nnt > 2) issue_step(nb, nkvg, nc0, nnt, 1, stage1);
+    }
+    compute(s);
+  };
+  if (ntiles > 0) {
+    if (!pre) {
+      issue_q(b, kvg);
+      issue_step(b, kvg, c0, ntiles, 0, stage0);
+      if (nsteps > 1) issue_step(b, kvg, c0, ntiles, 1, stage1);
+    }
+    has_next = next(nx);
+    if (app_lane) append_load<2>(p, b, kvg, L.lane & 31, app_kn, app_vn);
+    if (nsteps > 1) {
+      __builtin_amdgcn_s_waitcnt(0x4F70);  // vmcnt(16): this wave's query loads
+    } else {
+      __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8)
+    }
+    pf_barrier();
+    {
+      const char* row = qlds + (gl * 16 + L.lm) * 256;
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        Q.op[0][c] = *reinterpret_cast<const u32x4_t*>(row + (((4 * c + L.lg) ^ L.lm) * 16));
+    }
+    for (int s0 = 0; s0 < nsteps; s0 += 2) {
+      step(s0, stage0);
+      if (s0 + 1 < nsteps) step(s0 + 1, stage1);
+    }
+  }
+
+  if (app_lane) append_store<2>(p, b, kvg, L.lane & 31, app_kn, app_vn);
+  // The tile-1 waves hand their state to the tile-0 waves of the same (head,
+  // dim half): [pair (gl, hf)][16 O values, m, l][lane].
+  float* mb = mlds + (gl * 2 + hf) * 18 * 64 + L.lane;
+  if (kt == 1) {
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mb[(jj * 4 + r) * 64] = st.o[jj][r];
+    mb[16 * 64] = st.m;
+    mb[17 * 64] = st.l;
+  }
+  pf_barrier();
+  if (kt == 0) {
+    const float mo = mb[16 * 64];
+    if (mo != -INFINITY) {
+      const float lo = mb[17 * 64];
+      if (st.m == -INFINITY) {
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) st.o[jj][r] = mb[(jj * 4 + r) * 64];
+        st.l = lo;
+        st.m = mo;
+      } else {
+        const float mn = fmaxf(st.m, mo);
+        const float a = __builtin_amdgcn_exp2f(st.m - mn);
+        const float c = __builtin_amdgcn_exp2f(mo - mn);
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) st.o[jj][r] = st.o[jj][r] * a + mb[(jj * 4 + r) * 64] * c;
+        st.l = st.l * a + lo * c;
+        st.m = mn;
+      }
+    }
+    // Epilogue: lane (lm, lg) holds, for r = 0..3, dims 32lg + 8r + 4hf .. +3
+    // of column lm; l is lane-partial over the key slots.
+    const float l = rows4_sum(st.l);
+    if (L.lm < p.hs) {
+      const int head = g * p.group + L.lm;
+      const float inv_l = 1.f / l;
+      if (split < 0) {
+        uint16_t* dst = p.out + int64_t(b) * p.o_st + int64_t(head) * p.o_sh;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int d0 = 32 * L.lg + 8 * r + 4 * hf;
+          *reinterpret_cast<u32x2_t*>(dst + d0) =
+              u32x2_t{pack_bf16x2_fast(st.o[0][r] * inv_l, st.o[1][r] * inv_l),
+                      pack_bf16x2_fast(st.o[2][r] * inv_l, st.o[3][r] * inv_l)};
+        }
+      } else {
+        const int64_t base = (int64_t(b) * p.num_heads + head) * p.max_splits + split;
+        const float il = l > 0.f ? inv_l : 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int d0 = 32 * L.lg + 8 * r + 4 * hf;
+          *reinterpret_cast<float4*>(p.part_o + base * kD + d0) =
+              make_float4(st.o[0][r] * il, st.o[1][r] * il, st.o[2][r] * il, st.o[3][r] * il);
+        }
+        if (L.lg == 0 && hf == 0) p.part_lse[base] = l > 0.f ? st.m + __log2f(l) : -INFINITY;
+      }
     }
   }
   if (!has_next) {
@@ -2186,7 +2443,7 @@ __device__ void write_nan_rows(const AttnParams& p, int b, int kvg) {
 // kLds: 4 kv heads per workgroup staged through LDS, bf16
 // (decode_segment_lds: two stages in smem and smem1) or per-token-head int8
 // (decode_segment_lds_i8: a four-stage ring in smem); smem2 holds the query.
-template <int kEnc, bool kLds, bool kSteal = false>
+template <int kEnc, bool kLds, bool kSteal = false, int kHeads = 4>
 __device__ __forceinline__ void decode_sk_share(const AttnParams& p,
                                                 const int32_t* __restrict__ block_tables,
                                                 const int32_t* __restrict__ ctx_lens, int w,
@@ -2279,11 +2536,11 @@ __device__ __forceinline__ void decode_sk_share(const AttnParams& p,
             set_nseg(p, rb, rg, 0);
             if constexpr (kBfLds) {
               if (p.app_k != nullptr) {
-                // one lane holds this row unit here: it stores all 64 chunks
-                for (int c = 0; c < 64; ++c) {
+                // one lane holds this row unit here: it stores all its chunks
+                for (int c = 0; c < 16 * kHeads; ++c) {
                   u32x4_t kn, vn;
-                  append_load(p, rb, rg, c, kn, vn);
-                  append_store(p, rb, rg, c, kn, vn);
+                  append_load<kHeads>(p, rb, rg, c, kn, vn);
+                  append_store<kHeads>(p, rb, rg, c, kn, vn);
                 }
               }
             }
@@ -2377,7 +2634,16 @@ __device__ __forceinline__ void decode_sk_share(const AttnParams& p,
     }
     return false;
   };
-  if constexpr (kBfLds) {
+  if constexpr (kBfLds && kHeads == 2) {
+    DecSeg cur, nxt;
+    bool have = next_seg(cur);
+    bool pre = false;
+    while (have) {
+      have = decode_segment_lds2(p, smem, smem1, smem2, block_tables, cur, pre, next_seg, nxt);
+      pre = have;
+      cur = nxt;
+    }
+  } else if constexpr (kBfLds) {
     __shared__ int s_steal[12];  // [0]: owner claim verdict; [1..]: a taken tile
     // Each segment finds the next one (after issuing its own first loads)
     // and issues that one's first loads under its own last tile.
@@ -2494,6 +2760,18 @@ paged_decode_sk_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
   touch_kernel_args(int(sizeof(AttnParams) + 2 * sizeof(void*)));
   decode_sk_share<kEnc, kLds>(p, block_tables, ctx_lens, int(blockIdx.x), int(gridDim.x), smem,
                               smem1, smem2, StealArgs{});
+}
+
+// The bf16 LDS decode with 2 kv heads per workgroup.
+__global__ void __launch_bounds__(kThreads)
+paged_decode_sk2_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
+                        const int32_t* __restrict__ ctx_lens) {
+  __shared__ __align__(16) char smem[kLdsStage];
+  __shared__ __align__(16) char smem1[kLdsStage];
+  __shared__ __align__(16) char smem2[kLdsSmem2];
+  touch_kernel_args(int(sizeof(AttnParams) + 2 * sizeof(void*)));
+  decode_sk_share<kBF16, true, false, 2>(p, block_tables, ctx_lens, int(blockIdx.x),
+                                         int(gridDim.x), smem, smem1, smem2, StealArgs{});
 }
 
 // The bf16 LDS decode with the dynamic tail hand-out.
@@ -4624,10 +4902,12 @@ int device_cus() {
   return cached[dev];
 }
 
-// Kv slices per decode workgroup: the largest divisor of 8 that divides the
-// slice count, so the eight waves split evenly over slices and tile streams.
+// Kv slices per decode workgroup: the largest of 4, 2, 1 that divides the
+// slice count, so the eight waves split evenly over slices and tile streams
+// (4 slices of one head each are a 1 KiB slice of a token row: the LDS
+// segments stream those; 2 are a 512 B row of a 2-kv-head shard).
 int plan_kvs_per_wg(int64_t kvslices) {
-  int per = 8;
+  int per = 4;
   while (per > 1 && kvslices % per != 0) per >>= 1;
   return per;
 }
@@ -5060,11 +5340,17 @@ int paged_decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, con
     p.sk_nseg = reinterpret_cast<int*>(static_cast<char*>(workspace) +
                                        sk_partial_part(batch, num_heads, p.max_splits));
     p.chunk_tokens = kTile;
-    const bool lds_bf16 = kv_dtype == KVC_KV_BF16 && hp.kvs_per_wg == 4 && hp.nslices == 1 &&
+    // LDS-staged bf16 segments: 4 kv heads per workgroup (1 KiB token-row
+    // slices) or 2 (512 B rows, two tiles per stage).
+    // (A 2-head load brings two whole token rows, so that form needs rows of
+    // exactly 2 kv heads.)
+    const bool lds_bf16 = kv_dtype == KVC_KV_BF16 && hp.nslices == 1 &&
+                          (hp.kvs_per_wg == 4 || (hp.kvs_per_wg == 2 && num_kv_heads == 2)) &&
                           env_int("KVC_DECODE_LDS", 1) != 0;
+    const bool lds4 = lds_bf16 && hp.kvs_per_wg == 4;
     if (app.key != nullptr) {
-      // The LDS bf16 segments take the append in (16-byte rows of 4 kv heads);
-      // any other form gets the store launch first.
+      // The LDS bf16 segments take the append in (16-byte chunks of the kv
+      // group's token-row slice); any other form gets the store launch first.
       const bool fuse = lds_bf16 && (reinterpret_cast<uintptr_t>(app.key) % 16) == 0 &&
                         (reinterpret_cast<uintptr_t>(app.value) % 16) == 0 &&
                         app.key_stride_n % 8 == 0 && app.key_stride_h % 8 == 0 &&
@@ -5088,7 +5374,7 @@ int paged_decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, con
         if (rc != KVC_OK) return rc;
       }
     }
-    if (tl_record != nullptr && kv_dtype == KVC_KV_BF16 && lds_bf16 && p.app_k == nullptr) {
+    if (tl_record != nullptr && lds4 && p.app_k == nullptr) {
       tl_record->taken = true;
       tl_record->p = p;
       tl_record->grid = sp.grid;
@@ -5099,7 +5385,7 @@ int paged_decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, con
     // this launch, the tail partials and counts in the workspace.
     StealArgs sa{};
     const int tail = std::min(kDecTailMax, std::max(0, env_int("KVC_DECODE_TAIL", kDecTailDefault)));
-    if (lds_bf16 && steal_shape(hp) && tail > 0 && env_int("KVC_DECODE_STEAL", 0) != 0) {
+    if (lds4 && steal_shape(hp) && tail > 0 && env_int("KVC_DECODE_STEAL", 0) != 0) {
       unsigned long long* claims = claim_set(st, sp.grid);
       if (claims != nullptr) {
         char* ws = static_cast<char*>(workspace);
@@ -5123,9 +5409,11 @@ int paged_decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, con
     }
     switch (kv_dtype) {
       case KVC_KV_BF16:
-        if (lds_bf16) {
+        if (lds4) {
           paged_decode_sk_kernel<kBF16, true>
               <<<sp.grid, kThreads, 0, st>>>(p, block_tables, context_lens);
+        } else if (lds_bf16) {
+          paged_decode_sk2_kernel<<<sp.grid, kThreads, 0, st>>>(p, block_tables, context_lens);
         } else {
           paged_decode_sk_kernel<kBF16, false>
               <<<sp.grid, kThreads, 0, st>>>(p, block_tables, context_lens);

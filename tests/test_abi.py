@@ -73,10 +73,16 @@ def test_workspace_queries_are_host_only():
     base = (part + 255) // 256 * 256 + 4 * 4 * 4 + 256
     assert q("kvc_paged_decode_workspace_bytes", 4, 32, 4, 128, 256, 1024) == \
         _tail_region(base, 4, 4, 64, 32)[1]
-    # 32 kv heads (8 per workgroup): 32 counts per row, no tail region.
+    # 32 kv heads (4 per workgroup, 1 q head each): 32 counts per row and a
+    # tail region of 4 heads per row unit.
     part = 8 * 32 * 17 * 129 * 4
+    base = (part + 255) // 256 * 256 + 8 * 32 * 4 + 256
     assert q("kvc_paged_decode_workspace_bytes", 8, 32, 32, 128, 256, 16) == \
-        (part + 255) // 256 * 256 + 8 * 32 * 4 + 256
+        _tail_region(base, 8, 32, 17, 4)[1]
+    # 16q / 2kv (2 kv heads per workgroup): no tail region.
+    part = 8 * 16 * 17 * 129 * 4
+    assert q("kvc_paged_decode_workspace_bytes", 8, 16, 2, 128, 256, 16) == \
+        (part + 255) // 256 * 256 + 8 * 2 * 4 + 256
 
 
 def test_decode_layout_query():
@@ -86,8 +92,8 @@ def test_decode_layout_query():
     part = _al(64 * 32 * 17 * 129 * 4)
     base = part + 64 * 4 * 4 + 256
     assert list(lay) == [part, _tail_region(base, 64, 4, 17, 32)[0], 17, 4]
-    _native.call("kvc_paged_decode_layout", 8, 32, 32, 128, 256, 16, lay)
-    assert list(lay) == [_al(8 * 32 * 17 * 129 * 4), -1, 17, 32]
+    _native.call("kvc_paged_decode_layout", 8, 16, 2, 128, 256, 16, lay)
+    assert list(lay) == [_al(8 * 16 * 17 * 129 * 4), -1, 17, 2]
 
 
 def test_bad_arguments_map_to_python_exceptions():

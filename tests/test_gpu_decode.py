@@ -172,13 +172,13 @@ def test_pages_smaller_than_256(page, decode_path):
 
 
 @pytest.mark.parametrize("case", ["b64x4096", "ragged-with-empty", "int64-negative-slots",
-                                  "unaligned-key-fallback", "two-kv-heads-fallback"])
+                                  "unaligned-key-fallback", "two-kv-heads", "eight-kv-heads"])
 def test_decode_append_equals_store_then_decode(case, decode_path, deterministic_decode):
     """paged_decode_append (the store inside the decode launch where the
     layout allows) against store_kvcache then paged_decode_attention: the
     same output bits and the same pool bytes."""
     from nanovllm_amd.kernels.paged_attention import paged_decode_append
-    heads, kvh = (16, 2) if case == "two-kv-heads-fallback" else (32, 4)
+    heads, kvh = {"two-kv-heads": (16, 2), "eight-kv-heads": (16, 8)}.get(case, (32, 4))
     if case == "b64x4096":
         lens, nb = [4096] * 64, 1100
     elif case == "ragged-with-empty":
@@ -208,3 +208,37 @@ def test_decode_append_equals_store_then_decode(case, decode_path, deterministic
     torch.cuda.synchronize()
     assert np.array_equal(bits(out), bits(ref)), "outputs differ from store + decode"
     assert np.array_equal(bits(kc1), bits(kc0)) and np.array_equal(bits(vc1), bits(vc0))
+
+
+# The reference's published decode grid (benchmarks/archive/P15-pd-autotune.md:
+# 10-15) is at the engine's 2-way tensor-parallel shard, 16 q / 2 kv heads:
+# batch 1 / 8 / 16 / 32 x context 512-4096; plus the batch-64 x 4096 step.
+@pytest.mark.parametrize("batch,ctx", [(1, 512), (1, 4096), (8, 1024), (16, 2048), (32, 4096),
+                                       (64, 4096)])
+def test_tp2_shard_grid(batch, ctx, decode_path):
+    nb = batch * ctx // 256 + 8
+    wl = decode_workload(batch, 16, 2, nb, [ctx] * batch, seed=batch * 7 + ctx, device=DEV,
+                         pool_device_fill=True)
+    store_kvcache(wl.new_k, wl.new_v, wl.k_cache, wl.v_cache, wl.slot_mapping)
+    _check(wl.q, wl.k_cache, wl.v_cache, wl.block_tables, wl.context_lens, wl.scale,
+           f"tp2 b{batch} ctx{ctx}")
+
+
+def test_tp2_shard_ragged_fused_append(deterministic_decode):
+    """16q/2kv, batch 64 x U[512, 4096] over an 8192-block pool: the decode
+    step with the append fused (2-kv-head LDS segments) gives the same output
+    bits and pool bytes as store + decode, and matches the oracle."""
+    from nanovllm_amd.kernels.paged_attention import paged_decode_append
+    lens = uniform_lengths(64, 512, 4096, seed=21)
+    wl = decode_workload(64, 16, 2, 8192, lens, seed=22, device=DEV, pool_device_fill=True)
+    kc0, vc0 = wl.k_cache.clone(), wl.v_cache.clone()
+    store_kvcache(wl.new_k, wl.new_v, kc0, vc0, wl.slot_mapping)
+    ref = paged_decode_attention(wl.q, kc0, vc0, wl.block_tables, wl.context_lens, wl.scale, 0)
+    out = paged_decode_append(wl.q, wl.new_k, wl.new_v, wl.k_cache, wl.v_cache, wl.slot_mapping,
+                              wl.block_tables, wl.context_lens, wl.scale)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(out), bits(ref))
+    assert torch.equal(wl.k_cache.view(torch.int16), kc0.view(torch.int16))
+    assert torch.equal(wl.v_cache.view(torch.int16), vc0.view(torch.int16))
+    _check(wl.q, wl.k_cache, wl.v_cache, wl.block_tables, wl.context_lens, wl.scale,
+           "tp2 ragged after fused append")
