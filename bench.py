@@ -17,6 +17,7 @@ sample of the same workload on this host (cpu_baseline).
 from __future__ import annotations
 
 import argparse
+import math
 import json
 import os
 import statistics
@@ -39,8 +40,9 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "decode-dist", "int8", "mixed", "append", "swap", "copy",
-                             "rope", "decode-graph", "offload-overlap", "pd-wire"])
+                    choices=["decode", "decode-dist", "decode-tp2", "decode-cold", "cfg1",
+                             "p15-grid", "int8", "mixed", "append", "swap", "copy", "rope",
+                             "decode-graph", "offload-overlap", "pd-wire"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample", type=int, default=0,
                     help="sequences of the workload the CPU baseline runs (default: 64 of "
@@ -292,11 +294,27 @@ def cpu_swap_baseline(torch, L, kvh, reps=3):
 # ---------------------------------------------------------------------------
 # workloads
 # ---------------------------------------------------------------------------
+# Decode workloads: (batch, q heads, kv heads, pool blocks, context lengths,
+# description of the lengths).
+def decode_shape(workload: str):
+    from nanovllm_amd.workloads import uniform_lengths
+    if workload == "decode-dist":
+        return 64, 32, 4, 8192, uniform_lengths(64, 512, 4096, seed=2), "ctx U[512,4096]"
+    if workload == "decode-tp2":
+        # the engine's per-rank shape under 2-way tensor parallelism
+        # (nanovllm/models/qwen3.py:29-35, model_runner.py:407)
+        return 64, 16, 2, 8192, [4096] * 64, "ctx 4096"
+    if workload == "cfg1":
+        # Qwen3-0.6B-shaped layer: 16 q / 8 kv heads, batch 8 of U[128,1024]
+        # over a 64-block pool
+        return 8, 16, 8, 64, uniform_lengths(8, 128, 1024, seed=1), "ctx U[128,1024]"
+    return 64, 32, 4, 8192, [4096] * 64, "ctx 4096"
+
+
 def run_decode(args, torch, dist: bool, int8: bool = False):
     from nanovllm_amd.kernels.kv_int8 import store_kvcache_int8_tokhead
     from nanovllm_amd.kernels.paged_attention import paged_decode_append, paged_decode_attention
-    from nanovllm_amd.workloads import (decode_workload, int8_tokhead_decode_workload,
-                                        uniform_lengths)
+    from nanovllm_amd.workloads import decode_workload, int8_tokhead_decode_workload
 
     dev = torch.device("cuda:0")
     if int8:
@@ -304,12 +322,29 @@ def run_decode(args, torch, dist: bool, int8: bool = False):
         # appended through the per-token-head quantiser before the timed steps
         batch, heads, kvh, blocks = 16, 32, 4, 2048 + 16
         lens = [32768] * batch
+        ctx_desc = f"ctx {lens[0]}"
         wl = int8_tokhead_decode_workload(batch, heads, kvh, blocks, lens, seed=3, device=dev)
     else:
-        batch, heads, kvh, blocks = 64, 32, 4, 8192
-        lens = uniform_lengths(batch, 512, 4096, seed=2) if dist else [4096] * batch
+        batch, heads, kvh, blocks, lens, ctx_desc = decode_shape(args.workload)
+        # a 64-block pool is small enough to draw on the CPU (as the CPU path would)
         wl = decode_workload(batch, heads, kvh, blocks, lens, seed=3, device=dev,
-                             pool_device_fill=True)
+                             pool_device_fill=blocks > 64)
+    # decode-cold: the steps cycle through 8 disjoint block-table sets that
+    # cover the 8192-block pool, so a step never reads KV that one of the 7
+    # steps before it read (8 x 537 MB per cycle against a 256 MB Infinity
+    # Cache); every set is a seeded random permutation of its blocks.
+    sets = [(wl.block_tables, wl.slot_mapping)]
+    if args.workload == "decode-cold":
+        gen = torch.Generator().manual_seed(11)
+        perm = torch.randperm(blocks, generator=gen).to(torch.int32)
+        per = batch * (lens[0] // 256)
+        sets = []
+        for i in range(blocks // per):
+            bt = perm[i * per:(i + 1) * per].view(batch, -1).contiguous()
+            sm = bt[:, -1] * 256 + (lens[0] - 1) % 256
+            sets.append((bt.to(dev), sm.to(torch.int32).to(dev)))
+        ctx_desc += f", {len(sets)} disjoint table sets in turn"
+    cycle = [0]
 
     def step(timer=None):
         if int8:
@@ -322,10 +357,11 @@ def run_decode(args, torch, dist: bool, int8: bool = False):
         else:
             # the engine's decode step (store_kvcache + paged decode) in one call:
             # the append rides in the decode launch
+            bt, sm = sets[cycle[0] % len(sets)]
+            cycle[0] += 1
             s = timer.start() if timer else None
             out = paged_decode_append(wl.q, wl.new_k, wl.new_v, wl.k_cache, wl.v_cache,
-                                      wl.slot_mapping, wl.block_tables, wl.context_lens,
-                                      wl.scale)
+                                      sm, bt, wl.context_lens, wl.scale)
         if timer:
             timer.stop(s)
         return out
@@ -356,7 +392,6 @@ def run_decode(args, torch, dist: bool, int8: bool = False):
         other += 2 * 2 * batch * kvh * 128 * 2 + batch * 4  # the append: new rows in and out, slots
     algo = kv_bytes + other
     achieved = algo / (kernel_ms * 1e-3) / 1e9
-    ctx_desc = "ctx U[512,4096]" if dist else f"ctx {lens[0]}"
     res = {
         "metric": METRIC,
         "value": round(batch / (ms_per_step * 1e-3), 1),
@@ -377,7 +412,7 @@ def run_decode(args, torch, dist: bool, int8: bool = False):
                          f"{'int8 per-token-head' if int8 else 'bf16'}, batch {batch} x "
                          f"{ctx_desc}, page 256, {blocks}-block pool"),
             "batch": batch,
-            "context": "U[512,4096]" if dist else lens[0],
+            "context": ctx_desc[4:],
             "heads": heads,
             "kv_heads": kvh,
             "head_dim": 128,
@@ -402,6 +437,77 @@ def run_decode(args, torch, dist: bool, int8: bool = False):
         sample = args.cpu_sample if args.cpu_sample else (2 if int8 else 64)
         res["cpu_baseline"] = cpu_decode_baseline(torch, wl, sample, tok_bytes, int8=int8)
     return res
+
+
+# The reference's published decode grid (benchmarks/archive/P15-pd-autotune.md:
+# 10-15, Triton on an MTT S4000, geomean over contexts 512/1024/2048/4096 per
+# batch, 16 q / 2 kv heads, head_dim 128, page 256): default config and
+# autotuned per-batch config, in ms per kernel.
+P15_REFERENCE_MS = {1: (0.311, 0.180), 8: (0.487, 0.307), 16: (0.806, 0.365),
+                    32: (1.586, 0.547)}
+
+
+def run_p15_grid(args, torch):
+    """Paged decode (no append: the reference times the kernel) at the
+    reference's published grid: batch 1 / 8 / 16 / 32 x context 512 / 1024 /
+    2048 / 4096 at 16 q / 2 kv heads.  Each point: the decode call captured
+    in a HIP graph (as the engine replays its decode steps, so host
+    submission is not in the time), HIP events around each replay, mean over
+    the timed replays; the geomean over contexts per batch sits beside the
+    reference's (other hardware)."""
+    from nanovllm_amd.kernels.paged_attention import paged_decode_attention
+    from nanovllm_amd.workloads import decode_workload
+    dev = torch.device("cuda:0")
+    grid, geo = {}, {}
+    steps = max(5, args.steps)
+    for batch in (1, 8, 16, 32):
+        logs = []
+        for ctx in (512, 1024, 2048, 4096):
+            wl = decode_workload(batch, 16, 2, batch * ctx // 256 + 8, [ctx] * batch,
+                                 seed=batch + ctx, device=dev, pool_device_fill=True)
+
+            def call():
+                return paged_decode_attention(wl.q, wl.k_cache, wl.v_cache, wl.block_tables,
+                                              wl.context_lens, wl.scale, ctx)
+            for _ in range(max(1, args.warmup)):
+                call()
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                call()
+            torch.cuda.synchronize()
+            for _ in range(3):
+                graph.replay()
+            timer = EventTimer(torch)
+            for _ in range(steps):
+                s = timer.start()
+                graph.replay()
+                timer.stop(s)
+            torch.cuda.synchronize()
+            del graph
+            us = timer.mean_ms() * 1e3
+            kv = batch * ctx * 2 * 2 * 128 * 2
+            grid[f"b{batch}x{ctx}"] = {"us": round(us, 2), "kv_GBps": round(kv / us / 1e3, 1)}
+            logs.append(math.log(us))
+            del wl
+        geo[batch] = math.exp(sum(logs) / len(logs))
+    out_geo = {f"b{b}": {"geomean_us": round(v, 2),
+                         "reference_default_us": P15_REFERENCE_MS[b][0] * 1e3,
+                         "reference_tuned_us": P15_REFERENCE_MS[b][1] * 1e3}
+               for b, v in geo.items()}
+    b32 = grid["b32x4096"]
+    return {
+        "metric": "paged decode call time at the reference's published grid (16q/2kv/128)",
+        "value": b32["us"],
+        "unit": "us (b32 x 4096)",
+        "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+        "ms_per_step": round(b32["us"] / 1e3, 4),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q/k/v, random non-contiguous block tables)",
+        "config": {"workload": "paged decode call (graph replay), 16q/2kv/128 bf16, page 256, "
+                               "batch 1/8/16/32 x ctx 512/1024/2048/4096",
+                   "grid": grid, "geomean_by_batch": out_geo},
+    }
 
 
 def run_mixed(args, torch):
@@ -917,9 +1023,11 @@ def main():
         print("bench.py needs an MI355X (no GPU visible)", file=sys.stderr)
         sys.exit(2)
     torch.cuda.set_device(0)
-    if args.workload in ("decode", "decode-dist", "int8"):
+    if args.workload in ("decode", "decode-dist", "decode-tp2", "decode-cold", "cfg1", "int8"):
         res = run_decode(args, torch, dist=args.workload == "decode-dist",
                          int8=args.workload == "int8")
+    elif args.workload == "p15-grid":
+        res = run_p15_grid(args, torch)
     elif args.workload == "mixed":
         res = run_mixed(args, torch)
     elif args.workload == "append":

@@ -4933,6 +4933,8 @@ int plan_decode_chunk(int64_t rows, int64_t groups, int64_t max_ctx) {
 // so the partials stay within kSkMaxPartialBytes).  KVC_DECODE_STREAMK=0
 // selects the fixed-chunk partition instead.
 constexpr int kSkMinShare = 8;
+// The device-side share floor (tiles): small batches spread over every CU.
+constexpr int kSkMinShareDev = 2;
 constexpr int64_t kSkMaxPartialBytes = int64_t(256) << 20;
 
 struct SkPlan {
@@ -4941,10 +4943,14 @@ struct SkPlan {
   int max_splits;
 };
 
-SkPlan plan_stream_k(int64_t rows, int64_t heads, int64_t max_ctx) {
+SkPlan plan_stream_k(int64_t rows, int64_t heads, int64_t max_ctx, int64_t units) {
   SkPlan sp{env_int("KVC_DECODE_STREAMK", 1) != 0, launch_cus(), 2};
   const int64_t max_tiles = (max_ctx + kTile - 1) / kTile;
   int64_t ms = (max_tiles + kSkMinShare - 1) / kSkMinShare + 1;
+  // A batch with fewer row units than CUs lets each unit split over about
+  // CUs / units workgroups (every CU then streams a few tiles); larger
+  // batches keep the 8-tile bound.
+  if (units > 0 && units < sp.grid) ms = std::max<int64_t>(ms, (sp.grid + units - 1) / units + 1);
   const int64_t per_split = rows * heads * (kD + 1) * int64_t(sizeof(float));
   const int64_t cap = per_split > 0 ? kSkMaxPartialBytes / per_split : 64;
   ms = ms > 64 ? 64 : ms;
@@ -5214,7 +5220,7 @@ extern "C" size_t kvc_paged_decode_workspace_bytes(int64_t batch, int64_t num_he
   if (batch <= 0 || num_kv_heads <= 0 || head_dim != kD) return 0;
   const HeadPlan hp = plan_heads(num_heads, num_kv_heads);
   const int64_t max_ctx = max_blocks_per_seq * page_size;
-  const SkPlan sp = plan_stream_k(batch, num_heads, max_ctx);
+  const SkPlan sp = plan_stream_k(batch, num_heads, max_ctx, batch * hp.groups);
   if (sp.on) {
     const size_t base = sk_workspace_bytes(batch, num_heads, num_kv_heads * hp.nslices,
                                            sp.max_splits);
@@ -5237,7 +5243,8 @@ extern "C" int kvc_paged_decode_layout(int64_t batch, int64_t num_heads, int64_t
                   head_dim == kD && page_size > 0 && max_blocks_per_seq > 0,
               KVC_ERR_VALUE, "paged_decode_layout: bad launch shape");
   const HeadPlan hp = plan_heads(num_heads, num_kv_heads);
-  const SkPlan sp = plan_stream_k(batch, num_heads, max_blocks_per_seq * page_size);
+  const SkPlan sp =
+      plan_stream_k(batch, num_heads, max_blocks_per_seq * page_size, batch * hp.groups);
   KVC_REQUIRE(sp.on, KVC_ERR_VALUE, "paged_decode_layout: the launch is not stream-K");
   const int64_t kv_slices = num_kv_heads * hp.nslices;
   const size_t base = sk_workspace_bytes(batch, num_heads, kv_slices, sp.max_splits);
@@ -5316,10 +5323,10 @@ int paged_decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, con
   const int64_t max_ctx = max_blocks_per_seq * page_size;
   p.kvs_per_wg = hp.kvs_per_wg;
   hipStream_t st = as_stream(stream);
-  const SkPlan sp = plan_stream_k(batch, num_heads, max_ctx);
+  const SkPlan sp = plan_stream_k(batch, num_heads, max_ctx, batch * hp.groups);
   if (sp.on) {
     p.max_splits = sp.max_splits;
-    p.sk_min_share = kSkMinShare;
+    p.sk_min_share = std::max(1, env_int("KVC_SK_MIN_SHARE", kSkMinShareDev));
     // bf16 pools are HBM-bound and profit; the int8 segments are bound by their
     // arithmetic, which the XCDs share evenly.
     p.xcd_skew = kv_dtype == KVC_KV_BF16

@@ -79,8 +79,9 @@ def test_workspace_queries_are_host_only():
     base = (part + 255) // 256 * 256 + 8 * 32 * 4 + 256
     assert q("kvc_paged_decode_workspace_bytes", 8, 32, 32, 128, 256, 16) == \
         _tail_region(base, 8, 32, 17, 4)[1]
-    # 16q / 2kv (2 kv heads per workgroup): no tail region.
-    part = 8 * 16 * 17 * 129 * 4
+    # 16q / 2kv (2 kv heads per workgroup): no tail region; 8 row units on
+    # 256 CUs may split 256 / 8 + 1 = 33 ways.
+    part = 8 * 16 * 33 * 129 * 4
     assert q("kvc_paged_decode_workspace_bytes", 8, 16, 2, 128, 256, 16) == \
         (part + 255) // 256 * 256 + 8 * 2 * 4 + 256
 
@@ -93,7 +94,7 @@ def test_decode_layout_query():
     base = part + 64 * 4 * 4 + 256
     assert list(lay) == [part, _tail_region(base, 64, 4, 17, 32)[0], 17, 4]
     _native.call("kvc_paged_decode_layout", 8, 16, 2, 128, 256, 16, lay)
-    assert list(lay) == [_al(8 * 16 * 17 * 129 * 4), -1, 17, 2]
+    assert list(lay) == [_al(8 * 16 * 33 * 129 * 4), -1, 33, 2]
 
 
 def test_bad_arguments_map_to_python_exceptions():
