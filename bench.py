@@ -312,8 +312,8 @@ def decode_shape(workload: str):
 
 
 def run_decode(args, torch, dist: bool, int8: bool = False):
-    from nanovllm_amd.kernels.kv_int8 import store_kvcache_int8_tokhead
-    from nanovllm_amd.kernels.paged_attention import paged_decode_append, paged_decode_attention
+    from nanovllm_amd.kernels.paged_attention import (paged_decode_append,
+                                                      paged_decode_append_int8_tokhead)
     from nanovllm_amd.workloads import decode_workload, int8_tokhead_decode_workload
 
     dev = torch.device("cuda:0")
@@ -348,12 +348,13 @@ def run_decode(args, torch, dist: bool, int8: bool = False):
 
     def step(timer=None):
         if int8:
-            store_kvcache_int8_tokhead(wl.new_k, wl.new_v, wl.k_cache, wl.v_cache, wl.k_scale,
-                                       wl.v_scale, wl.slot_mapping)
+            # the per-token-head step (quantise-on-append + decode) in one call:
+            # the quantiser rides in the decode launch
             s = timer.start() if timer else None
-            out = paged_decode_attention(wl.q, wl.k_cache, wl.v_cache, wl.block_tables,
-                                         wl.context_lens, wl.scale, max(lens),
-                                         k_scale=wl.k_scale, v_scale=wl.v_scale)
+            out = paged_decode_append_int8_tokhead(wl.q, wl.new_k, wl.new_v, wl.k_cache,
+                                                   wl.v_cache, wl.k_scale, wl.v_scale,
+                                                   wl.slot_mapping, wl.block_tables,
+                                                   wl.context_lens, wl.scale)
         else:
             # the engine's decode step (store_kvcache + paged decode) in one call:
             # the append rides in the decode launch
@@ -388,7 +389,10 @@ def run_decode(args, torch, dist: bool, int8: bool = False):
     tok_bytes = 2 * kvh * 128 * (1 if int8 else 2) + (2 * kvh * 4 if int8 else 0)
     kv_bytes = sum(lens) * tok_bytes
     other = 2 * batch * heads * 128 * 2 + wl.block_tables.numel() * 4 + batch * 4
-    if not int8:
+    if int8:
+        # the quantise-on-append: bf16 rows in, codes and fp32 scales out, slots
+        other += 2 * batch * kvh * 128 * 2 + 2 * batch * kvh * (128 + 4) + batch * 4
+    else:
         other += 2 * 2 * batch * kvh * 128 * 2 + batch * 4  # the append: new rows in and out, slots
     algo = kv_bytes + other
     achieved = algo / (kernel_ms * 1e-3) / 1e9

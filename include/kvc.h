@@ -218,6 +218,33 @@ int kvc_paged_decode_append(const void* q, int64_t q_stride_b, int64_t q_stride_
                             int64_t out_stride_b, int64_t out_stride_h, void* workspace,
                             size_t workspace_bytes, kvc_stream_t stream);
 
+/* The decode step over a per-token-head int8 pool in one call: the new
+ * token's K/V rows (bf16, [batch, num_kv_heads, 128], own strides) are
+ * quantised as kvc_store_int8_tokhead does (codes and fp32 scales at
+ * slot_mapping[b]), then kvc_paged_decode runs over context_lens with that
+ * pool.  Replaces the step of the per-token-head mode
+ * (scripts/archive/p14_int8_kv_probe.py:37-46: quantise-on-append, then the
+ * decode that dequantises on read; nanovllm/kernels/paged_attention.py:
+ * 193-245).  Where the decode launch stages 4 kv heads per workgroup and the
+ * rows are 16-byte aligned, the quantiser runs inside the decode launch: the
+ * workgroup holding a row's last tile quantises and stores the row and uses
+ * the codes and scales straight from registers.  That form requires the
+ * engine's decode slots (as kvc_paged_decode_append); otherwise the store
+ * runs as its own launch first.  Codes, scales and outputs equal the two
+ * calls' bit for bit. */
+int kvc_paged_decode_append_int8(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                 const void* key, int64_t key_stride_n, int64_t key_stride_h,
+                                 const void* value, int64_t value_stride_n,
+                                 int64_t value_stride_h, const void* slot_mapping,
+                                 int slot_index_bytes, int8_t* k_cache, int8_t* v_cache,
+                                 float* k_scale, float* v_scale, int64_t num_cache_blocks,
+                                 int64_t page_size, int64_t num_kv_heads, int64_t head_dim,
+                                 const int32_t* block_tables, int64_t bt_stride,
+                                 int64_t max_blocks_per_seq, const int32_t* context_lens,
+                                 int64_t batch, int64_t num_heads, float scale, void* out,
+                                 int64_t out_stride_b, int64_t out_stride_h, void* workspace,
+                                 size_t workspace_bytes, kvc_stream_t stream);
+
 /* Bytes of device scratch kvc_paged_decode_append_static holds on each GPU
  * it runs on: 64 MiB.  At 32 q / 4 kv heads and pages of 256 that covers
  * batch 32 at any table width, batch 64 with tables of up to 62 pages

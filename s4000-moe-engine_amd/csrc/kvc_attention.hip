@@ -1820,7 +1820,8 @@ __device__ __forceinline__ void attend_key_half_i8(KeyHalfState& st, const u32x4
 constexpr int kI8Rows = kTile * 512;
 constexpr int kI8Stage = 2 * kI8Rows + 2 * 1024;
 constexpr int kI8Ring = 4;
-constexpr int kLdsI8 = kI8Ring * kI8Stage + 1024;  // + the dummy block
+// + the dummy block, + the fused append's new K and V rows (1 KiB each)
+constexpr int kLdsI8 = kI8Ring * kI8Stage + 1024 + 2048;
 constexpr int kI8LoadsPerTile = 5;
 constexpr int kI8MergePitch = kD + 4;  // floats per (head, column) row of the merge block
 static_assert(4 * 16 * kI8MergePitch * 4 + 4 * 16 * 8 <= kI8Stage, "merge block fits a stage");
@@ -1839,6 +1840,36 @@ __device__ __forceinline__ void wait_tiles_left(int tiles) {
   }
 }
 
+// The fused int8 append of a row with no context (its NaN-row owner): one
+// lane quantises and stores the group's 4 heads of the new K and V rows with
+// the arithmetic of quant_tokhead_row (amax over the 128 dims, scale
+// max(amax, 1e-6) / 127, codes rint(x / scale) clamped to +-127).
+__device__ void append_i8_row_lane(const AttnParams& p, int b, int kvg) {
+  const int64_t raw = p.app_slot_bytes == 8 ? load_index<8>(p.app_slots, b)
+                                            : load_index<4>(p.app_slots, b);
+  const int64_t slot = wrap_slot(raw, p.app_num_slots);
+  if (slot < 0 || slot >= p.app_num_slots) return;
+  for (int side = 0; side < 2; ++side) {
+    for (int hh = 0; hh < 4; ++hh) {
+      const int head = kvg * 4 + hh;
+      const uint16_t* src = side == 0 ? p.app_k + int64_t(b) * p.app_k_st + head * p.app_k_sh
+                                      : p.app_v + int64_t(b) * p.app_v_st + head * p.app_v_sh;
+      float amax = 0.f;
+      for (int d = 0; d < kD; ++d) amax = fmaxf(amax, fabsf(bf16_bits_to_f32(src[d])));
+      const float s = fmaxf(amax, 1e-6f) / 127.0f;
+      int8_t* dst = const_cast<int8_t*>(reinterpret_cast<const int8_t*>(
+                        side == 0 ? p.k_cache : p.v_cache)) +
+                    slot * p.tok_bytes + head * kD;
+      for (int d = 0; d < kD; ++d) {
+        const float q = fminf(fmaxf(__builtin_rintf(bf16_bits_to_f32(src[d]) / s), -127.0f),
+                              127.0f);
+        dst[d] = int8_t(int(q));
+      }
+      const_cast<float*>(side == 0 ? p.k_scale : p.v_scale)[slot * p.kvh + head] = s;
+    }
+  }
+}
+
 __device__ void decode_segment_lds_i8(const AttnParams& p, char* ring, char* qlds,
                                       const int32_t* bt, int b, int kvg, int ctx, int t0, int t1,
                                       int split) {
@@ -1853,6 +1884,26 @@ __device__ void decode_segment_lds_i8(const AttnParams& p, char* ring, char* qld
   t1 = uniform(t1);
   const int ntiles = t1 > t0 ? t1 - t0 : 0;
   const int c0 = t0 * kTile;
+  // Fused append (per-token-head quantise-on-append): the segment holding
+  // the row's last tile quantises the new token's K and V rows of the group's
+  // 4 heads exactly as store_int8_tokhead_kernel does and stores codes and
+  // scales to the pool.  The rows come into LDS by DMA ahead of the query
+  // (waves 0 and 1), so they have landed with it and the quantiser runs
+  // under the first tiles' loads.  The last tile's stage is patched before
+  // any wave reads it: the wave whose DMA brought the token's code rows
+  // (pair app_r >> 1) overwrites them, wave 0 the token's K scales, wave 1
+  // its V scales, each after its own wait for that tile and before the
+  // barrier.  (The pool store may land before or after that tile's DMA
+  // reads the slot: the bytes are the same.)
+  const bool app = p.app_k != nullptr && ntiles > 0 && t1 == (ctx + kTile - 1) / kTile;
+  const int app_r = (ctx - 1) & (kTile - 1);
+  const bool app_codes = app && wave == ((app_r >> 1) & 7);
+  const bool app_ks = app && wave == 0;
+  const bool app_vs = app && wave == 1;
+  const bool app_any = app_codes || app_ks || app_vs;
+  char* const app_rows = ring + kI8Ring * kI8Stage + 1024;  // [K row 1 KiB][V row 1 KiB]
+  u32x2_t app_kc{0u, 0u}, app_vc{0u, 0u};
+  float app_ksc = 0.f, app_vsc = 0.f;
 
   QueryI8 Q;
   KeyHalfState st;
@@ -1909,6 +1960,56 @@ __device__ void decode_segment_lds_i8(const AttnParams& p, char* ring, char* qld
     }
   };
 
+  // Quantise the new rows (from LDS, after the barrier that follows their
+  // DMA) and store them to the pool; the codes and scales stay in registers
+  // for the patch.
+  auto quantise_append = [&]() {
+    if (!app_any) return;
+    float kx[8], vx[8];
+    unpack8(*reinterpret_cast<const u32x4_t*>(app_rows + L.lane * 16), kx);
+    unpack8(*reinterpret_cast<const u32x4_t*>(app_rows + 1024 + L.lane * 16), vx);
+    int kc[8], vc[8];
+    app_ksc = quant_tokhead_row(kx, kc);
+    app_vsc = quant_tokhead_row(vx, vc);
+    app_kc = u32x2_t{pack_codes4(kc, 0), pack_codes4(kc, 4)};
+    app_vc = u32x2_t{pack_codes4(vc, 0), pack_codes4(vc, 4)};
+    if (app_codes) {
+      // the pool, at row b's slot (store_kvcache's rules for the slot)
+      const int64_t raw = p.app_slot_bytes == 8 ? load_index<8>(p.app_slots, b)
+                                                : load_index<4>(p.app_slots, b);
+      const int64_t slot = wrap_slot(raw, p.app_num_slots);
+      if (slot >= 0 && slot < p.app_num_slots) {
+        const int h = L.lane >> 4;
+        const int64_t dst = slot * p.tok_bytes + grp_off + h * kD + (L.lane & 15) * 8;
+        *reinterpret_cast<u32x2_t*>(const_cast<char*>(p.k_cache) + dst) = app_kc;
+        *reinterpret_cast<u32x2_t*>(const_cast<char*>(p.v_cache) + dst) = app_vc;
+        if ((L.lane & 15) == 0) {
+          const_cast<float*>(p.k_scale)[slot * p.kvh + kvg * 4 + h] = app_ksc;
+          const_cast<float*>(p.v_scale)[slot * p.kvh + kvg * 4 + h] = app_vsc;
+        }
+      }
+    }
+  };
+  // The patch of the last tile's stage (after this wave's wait for it).
+  auto patch_append = [&]() {
+    if (!app_any) return;
+    char* base = stage_of(ntiles - 1);
+    const int h = L.lane >> 4;
+    if (app_codes) {
+      // lane l holds dims 8 (l & 15) .. + 7 of head l >> 4: half (l & 1) of
+      // 16-byte chunk 8 h + (l & 15) / 2, stored at chunk ^ (row & 15)
+      const int chunk = (8 * h + ((L.lane & 15) >> 1)) ^ (app_r & 15);
+      const int off = app_r * 512 + chunk * 16 + 8 * (L.lane & 1);
+      *reinterpret_cast<u32x2_t*>(base + off) = app_kc;
+      *reinterpret_cast<u32x2_t*>(base + kI8Rows + off) = app_vc;
+    }
+    if ((L.lane & 15) == 0) {
+      char* sb = base + 2 * kI8Rows + app_r * 16 + h * 4;
+      if (app_ks) *reinterpret_cast<float*>(sb) = app_ksc;
+      if (app_vs) *reinterpret_cast<float*>(sb + 1024) = app_vsc;
+    }
+  };
+
   // One tile's operands of this wave, read from its stage.
   struct Regs {
     u32x4_t kc[2];
@@ -1950,6 +2051,7 @@ __device__ void decode_segment_lds_i8(const AttnParams& p, char* ring, char* qld
   // computed while those reads are in flight.
   auto step = [&](int j, const Regs& cur, Regs& nxt) {
     if (j + 1 < ntiles) wait_tiles_left(min(ntiles - 2 - j, kI8Ring - 2));
+    if (j + 2 == ntiles) patch_append();  // the last tile has landed (vmcnt(0) above)
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): `cur` has arrived
     __syncthreads();
     if (j + kI8Ring < ntiles) issue(j + kI8Ring);
@@ -1958,11 +2060,23 @@ __device__ void decode_segment_lds_i8(const AttnParams& p, char* ring, char* qld
   };
 
   if (ntiles > 0) {
+    if (app && wave < 2) {
+      // The new K (wave 0) or V (wave 1) row of the group's 4 heads: lane l
+      // brings dims 8 (l & 15) .. + 7 of head l >> 4.  Issued first, so the
+      // query wait below covers it.
+      const uint16_t* src = wave == 0 ? p.app_k + int64_t(b) * p.app_k_st + kvg * 4 * p.app_k_sh
+                                      : p.app_v + int64_t(b) * p.app_v_st + kvg * 4 * p.app_v_sh;
+      const int64_t sh = wave == 0 ? p.app_k_sh : p.app_v_sh;
+      const i32x4_t ar = raw_rsrc(src, int((3 * sh + kD) * 2));
+      dma_to_lds(ar, int(((L.lane >> 4) * sh + (L.lane & 15) * 8) * 2),
+                 lds_addr(app_rows + wave * 1024));
+    }
     issue_q();
     const int first = min(ntiles, kI8Ring);
     for (int j = 0; j < first; ++j) issue(j);
-    wait_tiles_left(first);  // the query loads, issued first, have landed
+    wait_tiles_left(first);  // the query loads (and the new rows), issued first, have landed
     __syncthreads();
+    quantise_append();
     {
       const char* row = qlds + (gl * 16 + L.lm) * 256;
       float qf[32];
@@ -1984,6 +2098,7 @@ __device__ void decode_segment_lds_i8(const AttnParams& p, char* ring, char* qld
     Regs ra, rb;
     // Tile 0 lands (tiles 1 .. min(3, ntiles - 1) may still be in flight).
     wait_tiles_left(min(ntiles - 1, kI8Ring - 1));
+    if (ntiles == 1) patch_append();  // vmcnt(0) above
     __syncthreads();
     read_stage(stage_of(0), ra);
     for (int j = 0; j < ntiles; j += 2) {
@@ -2534,6 +2649,9 @@ __device__ __forceinline__ void decode_sk_share(const AttnParams& p,
             const int rb = row_of(r), rg = r - rb * groups;
             write_nan_rows(p, rb, rg);
             set_nseg(p, rb, rg, 0);
+            if constexpr (kI8Lds) {
+              if (p.app_k != nullptr) append_i8_row_lane(p, rb, rg);
+            }
             if constexpr (kBfLds) {
               if (p.app_k != nullptr) {
                 // one lane holds this row unit here: it stores all its chunks
@@ -5269,6 +5387,26 @@ struct DecodeAppend {
   int slot_index_bytes;
 };
 
+// The step's append as its own launch (before a decode launch that cannot
+// take it in): store_kvcache, or the per-token-head int8 quantiser.
+int store_append(const DecodeAppend& app, const void* k_cache, const void* v_cache,
+                 const float* k_scale, const float* v_scale, int64_t num_slots, int64_t batch,
+                 int64_t num_kv_heads, int kv_dtype, kvc_stream_t stream) {
+  if (kv_dtype == KVC_KV_INT8_TOKHEAD) {
+    return kvc_store_int8_tokhead(app.key, app.key_stride_n, app.key_stride_h, app.value,
+                                  app.value_stride_n, app.value_stride_h,
+                                  static_cast<int8_t*>(const_cast<void*>(k_cache)),
+                                  static_cast<int8_t*>(const_cast<void*>(v_cache)),
+                                  const_cast<float*>(k_scale), const_cast<float*>(v_scale),
+                                  num_slots, app.slot_mapping, app.slot_index_bytes, batch,
+                                  num_kv_heads, kD, stream);
+  }
+  return kvc_store_kv(app.key, app.key_stride_n, app.key_stride_h, app.value,
+                      app.value_stride_n, app.value_stride_h, const_cast<void*>(k_cache),
+                      const_cast<void*>(v_cache), num_slots, app.slot_mapping,
+                      app.slot_index_bytes, batch, num_kv_heads, kD, 2, stream);
+}
+
 int paged_decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_cache,
                       const void* v_cache, int64_t num_cache_blocks, int64_t page_size,
                       int64_t num_kv_heads, int64_t head_dim, int kv_dtype, const float* k_scale,
@@ -5356,9 +5494,12 @@ int paged_decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, con
                           env_int("KVC_DECODE_LDS", 1) != 0;
     const bool lds4 = lds_bf16 && hp.kvs_per_wg == 4;
     if (app.key != nullptr) {
-      // The LDS bf16 segments take the append in (16-byte chunks of the kv
-      // group's token-row slice); any other form gets the store launch first.
-      const bool fuse = lds_bf16 && (reinterpret_cast<uintptr_t>(app.key) % 16) == 0 &&
+      // The LDS segments take the append in (16-byte chunks of the kv group's
+      // token-row slice: bf16 rows, or the per-token-head int8 quantiser's
+      // input); any other form gets the store launch first.
+      const bool lds_i8 = kv_dtype == KVC_KV_INT8_TOKHEAD && hp.kvs_per_wg == 4 &&
+                          hp.nslices == 1 && env_int("KVC_DECODE_LDS", 1) != 0;
+      const bool fuse = (lds_bf16 || lds_i8) && (reinterpret_cast<uintptr_t>(app.key) % 16) == 0 &&
                         (reinterpret_cast<uintptr_t>(app.value) % 16) == 0 &&
                         app.key_stride_n % 8 == 0 && app.key_stride_h % 8 == 0 &&
                         app.value_stride_n % 8 == 0 && app.value_stride_h % 8 == 0;
@@ -5373,11 +5514,8 @@ int paged_decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, con
         p.app_slot_bytes = app.slot_index_bytes;
         p.app_num_slots = num_cache_blocks * page_size;
       } else {
-        rc = kvc_store_kv(app.key, app.key_stride_n, app.key_stride_h, app.value,
-                          app.value_stride_n, app.value_stride_h, const_cast<void*>(k_cache),
-                          const_cast<void*>(v_cache), num_cache_blocks * page_size,
-                          app.slot_mapping, app.slot_index_bytes, batch, num_kv_heads, head_dim,
-                          2, stream);
+        rc = store_append(app, k_cache, v_cache, k_scale, v_scale, num_cache_blocks * page_size,
+                          batch, num_kv_heads, kv_dtype, stream);
         if (rc != KVC_OK) return rc;
       }
     }
@@ -5446,10 +5584,8 @@ int paged_decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, con
     return check_launch("paged_decode merge");
   }
   if (app.key != nullptr) {
-    rc = kvc_store_kv(app.key, app.key_stride_n, app.key_stride_h, app.value,
-                      app.value_stride_n, app.value_stride_h, const_cast<void*>(k_cache),
-                      const_cast<void*>(v_cache), num_cache_blocks * page_size, app.slot_mapping,
-                      app.slot_index_bytes, batch, num_kv_heads, head_dim, 2, stream);
+    rc = store_append(app, k_cache, v_cache, k_scale, v_scale, num_cache_blocks * page_size,
+                      batch, num_kv_heads, kv_dtype, stream);
     if (rc != KVC_OK) return rc;
   }
   p.chunk_tokens = plan_decode_chunk(batch, hp.groups, max_ctx);
@@ -5519,6 +5655,30 @@ extern "C" int kvc_paged_decode_append(
                            nullptr, nullptr, nullptr, nullptr, 0, block_tables, bt_stride,
                            max_blocks_per_seq, context_lens, batch, num_heads, scale, out,
                            out_stride_b, out_stride_h, workspace, workspace_bytes, app, stream);
+}
+
+extern "C" int kvc_paged_decode_append_int8(
+    const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* key, int64_t key_stride_n,
+    int64_t key_stride_h, const void* value, int64_t value_stride_n, int64_t value_stride_h,
+    const void* slot_mapping, int slot_index_bytes, int8_t* k_cache, int8_t* v_cache,
+    float* k_scale, float* v_scale, int64_t num_cache_blocks, int64_t page_size,
+    int64_t num_kv_heads, int64_t head_dim, const int32_t* block_tables, int64_t bt_stride,
+    int64_t max_blocks_per_seq, const int32_t* context_lens, int64_t batch, int64_t num_heads,
+    float scale, void* out, int64_t out_stride_b, int64_t out_stride_h, void* workspace,
+    size_t workspace_bytes, kvc_stream_t stream) {
+  clear_error();
+  KVC_REQUIRE(key != nullptr && value != nullptr && slot_mapping != nullptr, KVC_ERR_VALUE,
+              "paged_decode_append_int8: key, value and slot_mapping are required");
+  KVC_REQUIRE(slot_index_bytes == 4 || slot_index_bytes == 8, KVC_ERR_VALUE,
+              "paged_decode_append_int8: slot_mapping must be int32 or int64");
+  const DecodeAppend app{key, key_stride_n, key_stride_h, value, value_stride_n, value_stride_h,
+                         slot_mapping, slot_index_bytes};
+  return paged_decode_impl(q, q_stride_b, q_stride_h, k_cache, v_cache, num_cache_blocks,
+                           page_size, num_kv_heads, head_dim, KVC_KV_INT8_TOKHEAD, k_scale,
+                           v_scale, nullptr, nullptr, nullptr, nullptr, 0, block_tables,
+                           bt_stride, max_blocks_per_seq, context_lens, batch, num_heads, scale,
+                           out, out_stride_b, out_stride_h, workspace, workspace_bytes, app,
+                           stream);
 }
 
 // ---------------------------------------------------------------------------

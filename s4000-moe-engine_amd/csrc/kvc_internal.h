@@ -225,4 +225,45 @@ __device__ __forceinline__ int64_t load_index(const void* p, int64_t i) {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// ---------------------------------------------------------------------------
+// Per-token-head int8 quantisation of one 16-lane group's row (8 dims per
+// lane), shared by the store kernel and the decode launch's fused append.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void unpack8(const u32x4_t& w, float (&x)[8]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[2 * i] = bf16_bits_to_f32(w[i] & 0xffffu);
+    x[2 * i + 1] = bf16_bits_to_f32(w[i] >> 16);
+  }
+}
+
+__device__ __forceinline__ float group16_max(float v) {
+#pragma unroll
+  for (int m = 8; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
+}
+
+__device__ __forceinline__ uint32_t pack_codes4(const int (&c)[8], int base) {
+  return (uint32_t(c[base]) & 0xffu) | ((uint32_t(c[base + 1]) & 0xffu) << 8) |
+         ((uint32_t(c[base + 2]) & 0xffu) << 16) | ((uint32_t(c[base + 3]) & 0xffu) << 24);
+}
+
+// Per-token-head symmetric quantisation, rounding half to even.
+__device__ __forceinline__ float quant_tokhead_row(const float (&x)[8], int (&code)[8]) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(x[i]));
+  amax = group16_max(amax);
+  amax = fmaxf(amax, 1e-6f);
+  const float s = amax / 127.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float q = __builtin_rintf(x[i] / s);
+    q = fminf(fmaxf(q, -127.0f), 127.0f);
+    code[i] = int(q);
+  }
+  return s;
+}
+
+
 }  // namespace kvc

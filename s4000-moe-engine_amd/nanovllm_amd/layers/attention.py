@@ -24,7 +24,8 @@ from torch import nn
 
 from .. import _native as nat
 from ..kernels.kv_int8 import store_kvcache_int8
-from ..kernels.paged_attention import paged_decode_append, paged_decode_attention
+from ..kernels.paged_attention import (paged_decode_append, paged_decode_append_int8_tokhead,
+                                       paged_decode_attention)
 from ..kernels.varlen import varlen_attention
 from ..utils.context import get_context
 from .rotary import qk_norm_rope_store
@@ -147,10 +148,11 @@ class Attention(nn.Module):
         k_cache, v_cache = self.k_cache, self.v_cache
         if k_cache.numel() and self.block_size is None:
             self.block_size = k_cache.size(1)
-        # A decode step on a bf16 pool appends inside the decode call.
+        # A decode step on a bf16 or per-token-head int8 pool appends inside
+        # the decode call.
         fuse_append = (not kv_stored and not (context.is_mixed or context.is_prefill)
                        and bool(k_cache.numel() and v_cache.numel())
-                       and not self.kv_cache_is_int8)
+                       and (not self.kv_cache_is_int8 or self._int8_tokhead()))
         if k_cache.numel() and v_cache.numel() and not kv_stored and not fuse_append:
             with self._profile("attention.kv_store"):
                 if self.kv_cache_is_int8:
@@ -180,6 +182,14 @@ class Attention(nn.Module):
                     out_idx2d=self.out_idx2d if side else None,
                     head_n_out=self.head_n_out if side else None,
                 )
+        if fuse_append and self.kv_cache_is_int8:
+            with self._profile("attention.paged_decode"):
+                return paged_decode_append_int8_tokhead(
+                    q.view(-1, self.num_heads, self.head_dim),
+                    k.view(-1, self.num_kv_heads, self.head_dim),
+                    v.view(-1, self.num_kv_heads, self.head_dim), k_cache, v_cache,
+                    self.k_scale, self.v_scale, context.slot_mapping, context.block_tables,
+                    context.context_lens, self.scale)
         if fuse_append:
             with self._profile("attention.paged_decode"):
                 return paged_decode_append(

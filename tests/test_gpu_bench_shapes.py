@@ -82,15 +82,16 @@ def test_headline_decode_append_b64x4096_pool8192():
 
 def test_config4_int8_tokhead_b16x32k_outliers():
     """The int8 line's workload and step: history appended through the
-    quantiser, then store the step's token and decode."""
+    quantiser, then the step in one call (quantise-on-append inside the
+    decode launch)."""
+    from nanovllm_amd.kernels.paged_attention import paged_decode_append_int8_tokhead
     lens = [32768] * 16
     wl = int8_tokhead_decode_workload(16, 32, 4, 2048 + 16, lens, seed=3, device=DEV,
                                       keep_raw=True)
     print("[bench-shapes] int8 per-token-head 16 x 32768 with x20 key outliers", flush=True)
-    store_kvcache_int8_tokhead(wl.new_k, wl.new_v, wl.k_cache, wl.v_cache, wl.k_scale,
-                               wl.v_scale, wl.slot_mapping)
-    out = paged_decode_attention(wl.q, wl.k_cache, wl.v_cache, wl.block_tables, wl.context_lens,
-                                 wl.scale, max(lens), k_scale=wl.k_scale, v_scale=wl.v_scale)
+    out = paged_decode_append_int8_tokhead(wl.q, wl.new_k, wl.new_v, wl.k_cache, wl.v_cache,
+                                           wl.k_scale, wl.v_scale, wl.slot_mapping,
+                                           wl.block_tables, wl.context_lens, wl.scale)
     torch.cuda.synchronize()
     kvh, d = 4, 128
     flat_k = wl.k_cache.view(-1, kvh, d)

@@ -340,3 +340,69 @@ def test_chan_calibration_follows_the_engine_hook_over_forwards():
                               want[4][h, :n_got[h]])
     head0 = set(want[4][0, :want[5][0]].tolist())
     assert dims["hook_out"] in head0 and dims["hook_in"] not in head0
+
+
+@pytest.mark.parametrize("case", ["b16x4096", "ragged-with-empty", "int64-negative-slots",
+                                  "unaligned-key-refused", "two-kv-heads-fallback",
+                                  "eight-kv-heads"])
+def test_int8_tokhead_decode_append_equals_store_then_decode(case, decode_path):
+    """paged_decode_append_int8_tokhead (the per-token-head quantiser inside
+    the decode launch where the layout allows) against
+    store_kvcache_int8_tokhead then paged_decode_attention: the same output
+    bits, codes and scales, and the codes and scales of the new tokens are
+    the oracle's (scripts/archive/p14_int8_kv_probe.py:37-41)."""
+    from nanovllm_amd.kernels.paged_attention import paged_decode_append_int8_tokhead
+    heads, kvh = {"two-kv-heads-fallback": (16, 2), "eight-kv-heads": (16, 8)}.get(case, (32, 4))
+    if case == "b16x4096":
+        lens, nb = [4096] * 16, 300
+    elif case == "ragged-with-empty":
+        lens, nb = [1, 0, 33, 4096, 257, 0, 9000, 31], 80
+    else:
+        lens, nb = uniform_lengths(20, 1, 5000, seed=63), 600
+    wl = decode_workload(len(lens), heads, kvh, nb, [max(1, n) for n in lens], seed=len(lens) + 5,
+                         device=DEV, pool_device_fill=True, kv_dtype="int8_tokhead")
+    wl.context_lens = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    slots = wl.slot_mapping.clone()
+    num_slots = wl.k_cache.size(0) * wl.k_cache.size(1)
+    if case == "int64-negative-slots":
+        slots = slots.long()
+        slots[::3] -= num_slots
+    g = torch.Generator(device=DEV).manual_seed(9)
+    key = (torch.randn(wl.new_k.shape, generator=g, device=DEV) *
+           torch.where(torch.rand(wl.new_k.shape, generator=g, device=DEV) < 0.02, 20.0, 1.0)
+           ).to(torch.bfloat16)
+    value = wl.new_v
+    if case == "unaligned-key-refused":
+        big = torch.randn(len(lens), kvh * 128 + 4, dtype=torch.bfloat16, device=DEV)
+        big[:, 4:] = key.reshape(len(lens), -1)
+        key = big[:, 4:].view(len(lens), kvh, 128)
+    print(f"[int8-tokhead] fused append {case}: B={len(lens)} {heads}q/{kvh}kv", flush=True)
+    if case == "unaligned-key-refused":
+        # the quantiser reads 16-byte vectors: both forms refuse 8-byte aligned rows
+        with pytest.raises(AssertionError, match="16-byte aligned"):
+            store_kvcache_int8_tokhead(key, value, wl.k_cache, wl.v_cache, wl.k_scale,
+                                       wl.v_scale, slots)
+        with pytest.raises(AssertionError, match="16-byte aligned"):
+            paged_decode_append_int8_tokhead(wl.q, key, value, wl.k_cache, wl.v_cache,
+                                             wl.k_scale, wl.v_scale, slots, wl.block_tables,
+                                             wl.context_lens, wl.scale)
+        return
+    kc0, vc0 = wl.k_cache.clone(), wl.v_cache.clone()
+    ks0, vs0 = wl.k_scale.clone(), wl.v_scale.clone()
+    store_kvcache_int8_tokhead(key, value, kc0, vc0, ks0, vs0, slots)
+    ref = paged_decode_attention(wl.q, kc0, vc0, wl.block_tables, wl.context_lens, wl.scale, 0,
+                                 k_scale=ks0, v_scale=vs0)
+    out = paged_decode_append_int8_tokhead(wl.q, key, value, wl.k_cache, wl.v_cache, wl.k_scale,
+                                           wl.v_scale, slots, wl.block_tables, wl.context_lens,
+                                           wl.scale)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(out), bits(ref)), "outputs differ from store + decode"
+    assert torch.equal(wl.k_cache, kc0) and torch.equal(wl.v_cache, vc0)
+    assert torch.equal(wl.k_scale.view(torch.int32), ks0.view(torch.int32))
+    assert torch.equal(wl.v_scale.view(torch.int32), vs0.view(torch.int32))
+    sl = slots.long() % num_slots
+    for x, codes, sc in ((key, wl.k_cache, wl.k_scale), (value, wl.v_cache, wl.v_scale)):
+        want_c, want_s = ko.quant_tokhead(bits(x))
+        assert np.array_equal(codes.view(-1, kvh, 128)[sl].cpu().numpy(), want_c)
+        assert np.array_equal(sc.view(-1, kvh)[sl].cpu().numpy().view(np.uint32),
+                              want_s.view(np.uint32))
