@@ -2904,19 +2904,8 @@ paged_decode_steal_kernel(AttnParams p, const int32_t* __restrict__ block_tables
                                      smem, smem1, smem2, sa);
 }
 
-// ---------------------------------------------------------------------------
-// Stream-K mixed launch.  The work list is every prefill item (chunk i, kv
-// slice, query tile; query tile fastest) followed by every decode row unit
-// (row, slice group), each a run of 32-key tiles: a prefill item's tiles stop
-// at the last key its queries see, a decode unit has ceil(ctx / 32).  The
-// concatenated tiles are cut into equal shares exactly as in the paged decode
-// launch, so one long prefill chunk, many short ones and the decode rows all
-// spread over every CU; a prefill tile (32 keys x one query tile of every
-// head of the slice) and a decode tile (32 keys x every head of the group)
-// count the same.  Items that span several shares write partials; sk_nseg
-// [row, kv slice] gets every row's split count from the workgroup holding the
-// item's first tile.
-// ---------------------------------------------------------------------------
+// Geometry of prefill chunk i: its query rows, key rows, the keys before its
+// first query (prefix) and its query tiles of qtile tokens.
 struct ChunkGeo {
   int sq, sk, prefix, ntq;
 };
@@ -2953,204 +2942,6 @@ __device__ __forceinline__ int64_t qtile_cum(const ChunkGeo& c, int tpb, int q) 
   return s;
 }
 
-template <int kEnc, bool kFresh, bool kLds>
-__global__ void __launch_bounds__(kThreads)
-mixed_sk_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k,
-                const int32_t* __restrict__ ctx_lens, const int32_t* __restrict__ block_tables) {
-  static_assert(kSmemBytes >= kLdsStage, "the first LDS stage doubles as the scratch");
-  __shared__ __align__(16) char smem[kSmemBytes];
-  __shared__ __align__(16) char smem1[kLds ? kLdsStage : 16];
-  __shared__ __align__(16) char smem2[kLds ? kLdsQ : 16];
-  touch_kernel_args(int(sizeof(AttnParams) + 4 * sizeof(void*)));
-  const int kvs_total = p.kvh * p.nslices;
-  const int qtile = kWaves * kPreNCB * p.tpb;
-  const int w = blockIdx.x;
-  const int lane = threadIdx.x & 63;
-  const int wave = uniform(int(threadIdx.x >> 6));
-
-  // Prefill tiles, 64 chunks per pass: lane l takes chunk c0 + l.
-  auto chunk_tiles = [&](int i, int& tmax) {
-    tmax = 0;
-    if (i >= p.n_pre) return 0;
-    const ChunkGeo c = chunk_geo(cu_q, cu_k, i, qtile);
-    if (c.ntq == 0) return 0;
-    tmax = (c.sk + kTile - 1) / kTile;
-    return kvs_total * int(qtile_cum(c, p.tpb, c.ntq));
-  };
-  int Wpre = 0, Tmax = 0;
-  for (int c0 = 0; c0 < p.n_pre; c0 += 64) {
-    int tm;
-    const int t = chunk_tiles(c0 + lane, tm);
-    Wpre += wave_sum(t);
-    Tmax = max(Tmax, wave_max(tm));
-  }
-  Wpre = uniform(Wpre);
-
-  // Decode row units, as in the paged decode launch.
-  const int groups = kvs_total / p.kvs_per_wg;
-  const int R = p.n_dec * groups;
-  const int per_lane = (R + 63) / 64;
-  const int r0 = min(R, lane * per_lane);
-  const int r1 = min(R, r0 + per_lane);
-  constexpr int kCached = 4;
-  int cl[kCached];
-#pragma unroll
-  for (int i = 0; i < kCached; ++i) cl[i] = r0 + i < r1 ? ctx_lens[(r0 + i) / groups] : 0;
-  auto ctx_of = [&](int r) {
-    int c = 0;
-#pragma unroll
-    for (int i = 0; i < kCached; ++i) c = (r == r0 + i) ? cl[i] : c;
-    return r - r0 < kCached ? c : ctx_lens[r / groups];
-  };
-  int mine = 0, tmax = 0;
-  for (int r = r0; r < r1; ++r) {
-    const int t = ctx_tiles(ctx_of(r));
-    mine += t;
-    tmax = max(tmax, t);
-  }
-  const int incl = wave_scan_add(mine);
-  const int Wdec = uniform(__builtin_amdgcn_readlane(incl, 63));
-  Tmax = uniform(max(Tmax, wave_max(tmax)));
-  const int W = Wpre + Wdec;
-  int S = max(p.sk_min_share, (W + int(gridDim.x) - 1) / int(gridDim.x));
-  if (p.max_splits > 1) S = max(S, (Tmax + p.max_splits - 2) / (p.max_splits - 1));
-  const int start = w * S;
-  const int end = min(W, start + S);
-
-  // Decode rows: split counts and NaN rows of empty contexts (wave 0), and
-  // the row unit holding `start` if it falls in the decode part.
-  int found_r = R, found_p = 0, found_c = 0;
-  {
-    int P = Wpre + incl - mine;
-    for (int r = r0; r < r1; ++r) {
-      const int c = ctx_of(r);
-      const int t = ctx_tiles(c);
-      if (P <= start && start < P + t) {
-        found_r = r;
-        found_p = P;
-        found_c = c;
-      }
-      if (wave == 0) {
-        if (t == 0) {
-          const int owner = W > 0 ? min(P, W - 1) / S : 0;
-          if (owner == w) {
-            write_nan_rows(p, r / groups, r % groups);
-            set_nseg(p, r / groups, r % groups, 0);
-          }
-        } else if (P / S == w) {
-          set_nseg(p, r / groups, r % groups, (P + t - 1) / S - P / S + 1);
-        }
-      }
-      P += t;
-    }
-  }
-  if (start >= end) return;
-
-  // Walk state: prefill item (i, kvs, qt) or decode row unit r; P = the
-  // item's first tile.
-  bool pre = start < Wpre;
-  int i = 0, kvs = 0, qt = 0, r = R, P = 0, ctx = 0;
-  ChunkGeo geo{0, 0, 0, 0};
-  if (pre) {
-    int base = 0;
-    for (int c0 = 0; c0 < p.n_pre; c0 += 64) {
-      int tm;
-      const int t = chunk_tiles(c0 + lane, tm);
-      const int inc = wave_scan_add(t);
-      const int total = uniform(__builtin_amdgcn_readlane(inc, 63));
-      if (start < base + total) {
-        const unsigned long long hit = __ballot(t > 0 && base + inc - t <= start && start < base + inc);
-        const int src = __ffsll(hit) - 1;
-        i = uniform(c0 + src);
-        P = uniform(base + __builtin_amdgcn_readlane(inc - t, src));
-        break;
-      }
-      base += total;
-    }
-    geo = chunk_geo(cu_q, cu_k, i, qtile);
-    const int per_kvs = int(qtile_cum(geo, p.tpb, geo.ntq));
-    int off = start - P;
-    kvs = off / per_kvs;
-    off -= kvs * per_kvs;
-    int lo = 0, hi = geo.ntq - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (qtile_cum(geo, p.tpb, mid) <= off) lo = mid; else hi = mid - 1;
-    }
-    qt = uniform(lo);
-    kvs = uniform(kvs);
-    P = uniform(P + kvs * per_kvs + int(qtile_cum(geo, p.tpb, qt)));
-  } else {
-    const unsigned long long hit = __ballot(found_r < R);
-    const int src = hit ? __ffsll(hit) - 1 : 0;
-    r = uniform(__builtin_amdgcn_readlane(found_r, src));
-    P = uniform(__builtin_amdgcn_readlane(found_p, src));
-    ctx = uniform(__builtin_amdgcn_readlane(found_c, src));
-  }
-
-  while (P < end) {
-    if (pre) {
-      const int T = qtile_tiles(geo, qtile, qt);
-      const int t0 = max(start, P) - P;
-      const int t1 = min(end, P + T) - P;
-      const int nseg = (P + T - 1) / S - P / S + 1;
-      if (P >= start) {
-        // This share holds the item's first tile: record the rows' split count.
-        const int q0 = qt * qtile;
-        const int nq = min(qtile, geo.sq - q0);
-        if (int(threadIdx.x) < nq) {
-          const int64_t row = int64_t(p.n_dec) + cu_q[i] + q0 + threadIdx.x;
-          p.sk_nseg[row * kvs_total + kvs] = nseg;
-        }
-      }
-      prefill_segment<kEnc, kFresh>(p, smem, block_tables, i, qt, kvs, t0, t1,
-                                    nseg == 1 ? -1 : w - P / S);
-      P += T;
-      if (++qt == geo.ntq) {
-        qt = 0;
-        if (++kvs == kvs_total) {
-          kvs = 0;
-          do {
-            ++i;
-            if (i < p.n_pre) geo = chunk_geo(cu_q, cu_k, i, qtile);
-          } while (i < p.n_pre && geo.ntq == 0);
-          if (i >= p.n_pre) {
-            pre = false;
-            r = 0;
-            ctx = R > 0 ? uniform(ctx_lens[0]) : 0;
-          }
-        }
-      }
-    } else {
-      if constexpr (!kFresh) {
-        if (r >= R) break;
-        const int b = r / groups;
-        const int t = ctx_tiles(ctx);
-        if (t > 0) {
-          const int t0 = max(start, P) - P;
-          const int t1 = min(end, P + t) - P;
-          const int nseg = (P + t - 1) / S - P / S + 1;
-          const int split = nseg == 1 ? -1 : w - P / S;
-          if constexpr (kLds) {
-            const DecSeg sg{b, r - b * groups, ctx, t0, t1, split, 0, -1};
-            DecSeg unused;
-            decode_segment_lds(p, smem, smem1, smem2, block_tables, sg, false,
-                               [](DecSeg&) { return false; }, unused, StealArgs{}, nullptr, w);
-          } else {
-            decode_segment<kEnc>(p, smem, block_tables + int64_t(b) * p.bt_stride, b,
-                                 r - b * groups, ctx, t0, t1, split);
-          }
-        }
-        P += t;
-        ++r;
-        if (r < R && P < end) ctx = uniform(ctx_lens[r / groups]);
-      } else {
-        break;
-      }
-    }
-  }
-}
-
 // Locate prefill unit u: chunk i, query tile, kv slice, split (query tile
 // fastest so that units sharing K/V are adjacent).
 __device__ __forceinline__ bool find_prefill_unit(const AttnParams& p, int u, int& i, int& qt,
@@ -3176,21 +2967,14 @@ __device__ __forceinline__ bool find_prefill_unit(const AttnParams& p, int u, in
   return false;
 }
 
-// Grid order: the prefill units first, then the decode units, so that the
-// long prefill units do not start after the memory-bound decode units.
+// One workgroup per prefill unit (chunk, query tile, kv slice, key split):
+// the launch for int8 pools and for KVC_PREFILL_SK=0.
 template <int kEnc, bool kFresh>
 __global__ void __launch_bounds__(kThreads)
 varlen_kernel(AttnParams p, const int32_t* __restrict__ block_tables) {
   __shared__ __align__(16) char smem[kSmemBytes];
   const int u = blockIdx.x;
-  if (u >= p.pre_units) {
-    if constexpr (!kFresh) {
-      int b, kvg, chunk;
-      decode_unit_of(p, u - p.pre_units, b, kvg, chunk);
-      decode_unit<kEnc>(p, smem, block_tables, b, kvg, chunk);
-    }
-    return;
-  }
+  if (u >= p.pre_units) return;
   int i, qt, kvs, split;
   if (!find_prefill_unit(p, u, i, qt, kvs, split)) return;
   const int sk = p.cu_k[i + 1] - p.cu_k[i];
@@ -3204,19 +2988,15 @@ varlen_kernel(AttnParams p, const int32_t* __restrict__ block_tables) {
 // Stream-K prefill launch over bf16 keys (a paged bf16 pool, or the step's
 // fresh k/v when there is no prefix cache).  Items are (chunk i, kv slice,
 // query tile), query tile fastest; each is a run of 32-key tiles that stops
-// at the last key its queries see.  The concatenated tiles are cut into one
-// equal share per workgroup, so chunks of any length mix spread evenly over
-// the CUs.  A workgroup streams its share through a kPfStages-deep LDS ring
-// with no break at item boundaries: tiles j + 1 .. j + 3 are in flight
-// (direct-to-LDS loads) while tile j is attended, whichever item they belong
-// to, and the query block of the next item rides the same DMA while the
-// current item runs, so an item boundary costs its epilogue and not a
-// pipeline refill.
-// Items spanning several shares write split-K partials; the share holding an
-// item's first tile records the split count of its rows for the merge.
+// at the last key its queries see.  The concatenated tiles (plus a fixed cost
+// per item) are cut into one equal share per workgroup, so chunks of any
+// length mix spread evenly over the CUs, and a workgroup streams its share
+// with no break at item boundaries.  Items spanning several shares write
+// split-K partials; the share holding an item's first tile records the split
+// count of its rows for the merge.
 //
-// LDS rows are 256 bytes padded to 272 (17 chunks of 16 bytes): 16 rows read
-// at one column offset touch 16 different bank groups, and every operand
+// K rows in LDS are 256 bytes padded to 272 (17 chunks of 16 bytes): 16 rows
+// read at one column offset touch 16 different bank groups, and every operand
 // read is a per-lane base plus an immediate.  A 64-lane direct-to-LDS load
 // fills 64 consecutive chunks, so lane l of load k fetches whichever chunk
 // belongs at slot 64 k + l (pad slots and rows past the tile read 0).
@@ -3226,37 +3006,15 @@ constexpr int kPfPitch = kPfRowSlots * 16;                          // 272
 constexpr int kPfLoadsPerTensor = (kTile * kPfRowSlots + 63) / 64;  // 9
 constexpr int kPfTensor = kPfLoadsPerTensor * 1024;
 constexpr int kPfStage = 2 * kPfTensor;  // K then V
-#ifndef KVC_PF_STAGES
-#define KVC_PF_STAGES 4
-#endif
-constexpr int kPfStages = KVC_PF_STAGES;  // tile j + kPfStages - 1 loads while tile j is attended
 constexpr int kPfTileLoads = (2 * kPfLoadsPerTensor + kWaves - 1) / kWaves;  // per wave: 3
-constexpr int kPfCols = kWaves * kPreNCB * 16;                     // query columns per item
-constexpr int kPfQLoads = (kPfCols * kPfRowSlots + 63) / 64;       // 68
-constexpr int kPfQLoadsPerWave = (kPfQLoads + kWaves - 1) / kWaves;  // 9
-constexpr int kPfQOff = kPfStages * kPfStage;
-constexpr int kPfDummyOff = kPfQOff + kPfQLoads * 1024;
-constexpr int kPfSmem = kPfDummyOff + 1024;
 constexpr int kPfMinShare = 4;
-#ifndef KVC_PF_NT
-#define KVC_PF_NT 0
-#endif
-// Prefill keys are read by every query tile of their chunk: keep them cached.
-constexpr bool kPfNonTemporal = KVC_PF_NT != 0;
 constexpr int kOob = 0x40000000;  // a buffer offset past every resource: reads 0, no traffic
-static_assert(kPfTileLoads == 3 && kPfQLoadsPerWave == 9, "wait counts below assume these");
-static_assert(kPfStages >= 3 && 3 * (kPfStages - 1) + 9 * (kPfStages - 2) <= 45, "pf_wait_vm range");
-static_assert(kPfSmem <= 160 * 1024, "one workgroup per CU");
-
-// Each item also carries kPfItemCost virtual tiles in the partition: a
-// segment costs its query load, its epilogue and a pipeline bubble (about
-// two tiles' time), so shares that chain many short items get fewer tiles.
-constexpr int kPfItemCost = 2;
+static_assert(kPfTileLoads == 3, "wait counts below assume three tile loads per wave");
 
 struct PfItem {
   int i, kvs, qt;  // chunk, kv slice, query tile
   int g, s;        // kv head and slice within its group: kvs = g * nslices + s
-  int P;           // weighted position of the item's span (kPfItemCost + T long)
+  int P;           // weighted position of the item's span (item cost + T long)
   int T;           // tiles of the item
   int cq0, ck0;    // chunk's first query row / key row (prefill-relative)
   ChunkGeo geo;
@@ -3269,52 +3027,6 @@ __device__ __forceinline__ void pf_load_chunk(PfItem& it, const int32_t* cu_q, c
   it.ck0 = cu_k[it.i];
 }
 
-// The item after `it` (T = 0 past the last one).
-__device__ __forceinline__ void pf_next_item(PfItem& it, const int32_t* cu_q, const int32_t* cu_k,
-                                             int n_pre, int kvs_total, int nslices, int qtile) {
-  it.P += kPfItemCost + it.T;
-  if (++it.qt == it.geo.ntq) {
-    it.qt = 0;
-    ++it.kvs;
-    if (++it.s == nslices) {
-      it.s = 0;
-      ++it.g;
-    }
-    if (it.kvs == kvs_total) {
-      it.kvs = it.g = it.s = 0;
-      do {
-        ++it.i;
-        if (it.i < n_pre) pf_load_chunk(it, cu_q, cu_k, qtile);
-      } while (it.i < n_pre && it.geo.ntq == 0);
-    }
-  }
-  it.T = it.i < n_pre ? qtile_tiles(it.geo, qtile, it.qt) : 0;
-}
-
-// Wait until at most n of this wave's vector memory operations are pending
-// (n = the loads issued after the ones waited for).
-// n is a multiple of 3 (tile loads and query loads come in threes and nines)
-// below 3 (kPfStages - 1) + 9 (kPfStages - 2) <= 45.
-__device__ __forceinline__ void pf_wait_vm(int n) {
-  switch (n / 3) {
-    case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
-    case 1: __builtin_amdgcn_s_waitcnt(0x0F73); break;
-    case 2: __builtin_amdgcn_s_waitcnt(0x0F76); break;
-    case 3: __builtin_amdgcn_s_waitcnt(0x0F79); break;
-    case 4: __builtin_amdgcn_s_waitcnt(0x0F7C); break;
-    case 5: __builtin_amdgcn_s_waitcnt(0x0F7F); break;
-    case 6: __builtin_amdgcn_s_waitcnt(0x4F72); break;  // 18
-    case 7: __builtin_amdgcn_s_waitcnt(0x4F75); break;  // 21
-    case 8: __builtin_amdgcn_s_waitcnt(0x4F78); break;  // 24
-    case 9: __builtin_amdgcn_s_waitcnt(0x4F7B); break;  // 27
-    case 10: __builtin_amdgcn_s_waitcnt(0x4F7E); break;  // 30
-    case 11: __builtin_amdgcn_s_waitcnt(0x8F71); break;  // 33
-    case 12: __builtin_amdgcn_s_waitcnt(0x8F74); break;  // 36
-    case 13: __builtin_amdgcn_s_waitcnt(0x8F77); break;  // 39
-    case 14: __builtin_amdgcn_s_waitcnt(0x8F7A); break;  // 42
-    default: __builtin_amdgcn_s_waitcnt(0x8F7D); break;  // 45
-  }
-}
 
 
 // One 32-key tile of the stream-K prefill against the wave's kPreNCB column
@@ -3525,468 +3237,9 @@ __device__ __forceinline__ void pf_pv(PfState& st, const u32x4_t (&va)[8],
   }
 }
 
-// Weighted tiles of query tiles [0, q) of chunk c.
-__device__ __forceinline__ int pf_qcum(const ChunkGeo& c, int tpb, int q) {
-  return int(qtile_cum(c, tpb, q)) + kPfItemCost * q;
-}
-
-template <bool kFresh>
-__global__ void __launch_bounds__(kThreads)
-prefill_sk_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k,
-                  const int32_t* __restrict__ block_tables) {
-  __shared__ __align__(16) char lds[kPfSmem];
-  touch_kernel_args(int(sizeof(AttnParams) + 3 * sizeof(void*)));
-  auto pf_dma = [](const i32x4_t& r, int voff, uint32_t dst) {
-    if constexpr (kPfNonTemporal) {
-      dma_to_lds(r, voff, dst);
-    } else {
-      dma_to_lds_cached(r, voff, dst);
-    }
-  };
-  const LaneId L = lane_id();
-  const int wave = uniform(int(threadIdx.x >> 6));
-  const int kvs_total = p.kvh * p.nslices;
-  const int qtile = kWaves * kPreNCB * p.tpb;
-  // Consecutive shares run on one XCD (workgroup v is placed on XCD v mod 8),
-  // so the query tiles of an item that read the same keys at the same time
-  // share that XCD's L2.
-  const int G = int(gridDim.x);
-  const int v = int(blockIdx.x);
-  const int w = (G % 8 == 0) ? (v % 8) * (G / 8) + v / 8 : v;
-
-  // Weighted total W and the longest item; shares of S.  Lane l holds chunk
-  // c0 + l of the first 64 (one memory round trip for the usual batch of at
-  // most 64 chunks); its counts stay in registers for the search.
-  int W = 0, Tmax = 0;
-  int t_first = 0;
-  int cq_first = 0, ck_first = 0;
-  ChunkGeo g_first{0, 0, 0, 0};
-  for (int c0 = 0; c0 < p.n_pre; c0 += 64) {
-    const int ci = c0 + L.lane;
-    int t = 0, tm = 0;
-    if (ci < p.n_pre) {
-      const ChunkGeo c = chunk_geo(cu_q, cu_k, ci, qtile);
-      if (c.ntq > 0) {
-        tm = (c.sk + kTile - 1) / kTile;
-        t = kvs_total * pf_qcum(c, p.tpb, c.ntq);
-      }
-      if (c0 == 0) {
-        g_first = c;
-        cq_first = cu_q[ci];
-        ck_first = cu_k[ci];
-      }
-    }
-    if (c0 == 0) t_first = t;
-    W += wave_sum(t);
-    Tmax = max(Tmax, wave_max(tm));
-  }
-  W = uniform(W);
-  Tmax = uniform(Tmax);
-  int S = max(p.sk_min_share, (W + G - 1) / G);
-  if (p.max_splits > 1) S = max(S, (Tmax + kPfItemCost + p.max_splits - 2) / (p.max_splits - 1));
-  S = uniform(S);
-  if (int64_t(w) * S >= W) return;
-  const int start = w * S;
-  const int end = min(W, start + S);
-
-  // The item whose weighted span holds `start`: its chunk by a 64-wide scan
-  // (the first 64 chunks from registers), its kv slice by division, its query
-  // tile by bisection of the closed-form counts.
-  PfItem it;
-  {
-    int base = 0, ci = -1, P = 0;
-    for (int c0 = 0; c0 < p.n_pre && ci < 0; c0 += 64) {
-      int t = t_first;
-      if (c0 > 0) {
-        t = 0;
-        if (c0 + L.lane < p.n_pre) {
-          const ChunkGeo c = chunk_geo(cu_q, cu_k, c0 + L.lane, qtile);
-          if (c.ntq > 0) t = kvs_total * pf_qcum(c, p.tpb, c.ntq);
-        }
-      }
-      const int inc = wave_scan_add(t);
-      const int total = uniform(__builtin_amdgcn_readlane(inc, 63));
-      if (start < base + total) {
-        const unsigned long long hit =
-            __ballot(t > 0 && base + inc - t <= start && start < base + inc);
-        const int src = __ffsll(hit) - 1;
-        ci = uniform(c0 + src);
-        P = uniform(base + __builtin_amdgcn_readlane(inc - t, src));
-        if (c0 == 0) {
-          it.geo.sq = uniform(__builtin_amdgcn_readlane(g_first.sq, src));
-          it.geo.sk = uniform(__builtin_amdgcn_readlane(g_first.sk, src));
-          it.geo.prefix = it.geo.sk - it.geo.sq;
-          it.geo.ntq = uniform(__builtin_amdgcn_readlane(g_first.ntq, src));
-          it.cq0 = uniform(__builtin_amdgcn_readlane(cq_first, src));
-          it.ck0 = uniform(__builtin_amdgcn_readlane(ck_first, src));
-        }
-      }
-      base += total;
-    }
-    it.i = ci;
-    if (ci >= 64) pf_load_chunk(it, cu_q, cu_k, qtile);
-    const int per_kvs = pf_qcum(it.geo, p.tpb, it.geo.ntq);
-    int off = start - P;
-    it.kvs = uniform(off / per_kvs);
-    off -= it.kvs * per_kvs;
-    int lo = 0, hi = it.geo.ntq - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (pf_qcum(it.geo, p.tpb, mid) <= off) lo = mid; else hi = mid - 1;
-    }
-    it.qt = uniform(lo);
-    it.g = uniform(it.kvs / p.nslices);
-    it.s = it.kvs - it.g * p.nslices;
-    it.P = uniform(P + it.kvs * per_kvs + pf_qcum(it.geo, p.tpb, it.qt));
-    it.T = qtile_tiles(it.geo, qtile, it.qt);
-  }
-  // Real tile t of item x sits at weighted position x.P + kPfItemCost + t;
-  // the share owns the real tiles whose positions fall in [start, end).
-  int ct = max(0, start - it.P - kPfItemCost);  // consumer's tile in `it`
-
-  // Tile loads: wave w issues loads w, w + 8, w + 16 of the 18 per tile (9 of
-  // K, 9 of V; the six past 18 are zero loads into a dummy block, so every
-  // wave waits with the same counts).  Lane slots are fixed; the offsets
-  // change with the item's kv head.
-  const uint32_t lds0 = lds_addr(lds);
-  int boff[kPfTileLoads];  // lane offset of load jj inside a tile, before the kv head's
-#pragma unroll
-  for (int jj = 0; jj < kPfTileLoads; ++jj) {
-    const int k = wave + kWaves * jj;
-    const int sl = (k % kPfLoadsPerTensor) * 64 + L.lane;
-    const int slots = k < kPfLoadsPerTensor ? kPfRowSlots : kPfVRowSlots;  // K 272 B, V 288 B rows
-    const int row = sl / slots;
-    const int ch = sl - row * slots;
-    int rs;
-    if constexpr (kFresh) {
-      rs = int((k >= kPfLoadsPerTensor ? p.vf_st : p.kf_st) * 2);
-    } else {
-      rs = int(p.tok_bytes);
-    }
-    const bool ok = k < 2 * kPfLoadsPerTensor && row < kTile && ch < 16;
-    boff[jj] = ok ? row * rs + ch * 16 : kOob;
-  }
-
-  // LDS targets of this wave's three loads (load jj is number wave + 8 jj of
-  // the tile's 18; stage-relative, the dummy block aside).
-  static_assert(kWaves == 8 && kPfLoadsPerTensor == 9 && kPfTileLoads == 3,
-                "the load pattern below");
-  const bool w0 = wave == 0;
-  const bool w01 = wave < 2;
-  const uint32_t dst0 = uint32_t(wave) * 1024;
-  const uint32_t dst1 = w0 ? 8 * 1024 : kPfTensor + uint32_t(wave - 1) * 1024;
-  const uint32_t dst2 = kPfTensor + uint32_t(7 + wave) * 1024;  // used by waves 0 and 1
-
-  // Producer cursor: real tile pt of item pi.  Paged keys: the block-table
-  // entry of the tile's page (pblk) is kept in pblk_val, the next page's
-  // entry is loaded a page ahead (reads stay inside the item's keys).  The
-  // table is read through the __restrict__ kernel argument itself, so these
-  // are scalar loads; a vector load's wait would drain the ring.
-  PfItem pi = it;
-  int pt = ct;
-  int pblk = 0, poff = 0, pblk_val = 0, pnext_val = 0, plast = 0;
-  int64_t pbt = 0;  // element offset of the producer item's table row
-  auto table_setup = [&]() {
-    if constexpr (!kFresh) {
-      pbt = int64_t(p.n_dec + pi.i) * p.bt_stride;
-      const int key0 = pt * kTile;
-      pblk = uniform(key0 / p.page);
-      poff = uniform(key0 - pblk * p.page);
-      plast = uniform((pi.geo.sk - 1) / p.page);  // last page holding keys of the chunk
-      pblk_val = block_tables[pbt + pblk];
-      pnext_val = block_tables[pbt + min(pblk + 1, plast)];
-    }
-  };
-  table_setup();
-  auto produce = [&](int stage) {
-    const int nvalid = min(kTile, pi.geo.sk - pt * kTile);
-    int hk, hv;  // byte offset of kv head g inside a K / V row
-    const char* kb;
-    const char* vb;
-    int kbytes, vbytes;
-    if constexpr (kFresh) {
-      hk = int(pi.g * p.kf_sh * 2);
-      hv = int(pi.g * p.vf_sh * 2);
-      const int64_t r0 = int64_t(pi.ck0) + pt * kTile;
-      kb = reinterpret_cast<const char*>(p.kf + r0 * p.kf_st);
-      vb = reinterpret_cast<const char*>(p.vf + r0 * p.vf_st);
-      kbytes = int(nvalid * p.kf_st * 2);
-      vbytes = int(nvalid * p.vf_st * 2);
-    } else {
-      hk = hv = pi.g * kD * 2;
-      const int64_t slot0 = int64_t(pblk_val) * p.page + poff;
-      kb = p.k_cache + slot0 * p.tok_bytes;
-      vb = p.v_cache + slot0 * p.tok_bytes;
-      kbytes = vbytes = nvalid * int(p.tok_bytes);
-    }
-    const i32x4_t rk = raw_rsrc(kb, kbytes);
-    const i32x4_t rv = raw_rsrc(vb, vbytes);
-    const uint32_t sb = lds0 + stage * kPfStage;
-    // Selects, not branches: load 0 of every wave is a K block, load 1 is K
-    // for wave 0 and V otherwise, load 2 is V for waves 0 and 1 and a zero
-    // load (boff = kOob) into the dummy block otherwise.
-    pf_dma(rk, boff[0] + hk, sb + dst0);
-    pf_dma(w0 ? rk : rv, boff[1] + (w0 ? hk : hv), sb + dst1);
-    pf_dma(rv, boff[2] + hv, w01 ? sb + dst2 : lds0 + kPfDummyOff);
-    // Advance to the next real tile.
-    if (++pt == pi.T) {
-      pf_next_item(pi, cu_q, cu_k, p.n_pre, kvs_total, p.nslices, qtile);
-      pt = 0;
-      if (pi.P + kPfItemCost < end) table_setup();
-    } else if constexpr (!kFresh) {
-      poff += kTile;
-      if (poff == p.page) {
-        poff = 0;
-        ++pblk;
-        pblk_val = pnext_val;
-        pnext_val = block_tables[pbt + min(pblk + 1, plast)];
-      }
-    }
-    smem_drain();
-  };
-  auto prod_live = [&]() { return pi.P + kPfItemCost + pt < end; };
-
-  // Query block of item x: column c (16-column block c / 16, lane c % 16) at
-  // slots 17 c .. 17 c + 15; columns past the chunk or the slice read 0.
-  const float inv_hs = 1.f / float(p.hs);
-  auto issue_q = [&](const PfItem& x) {
-    const int hs = min(p.hs, p.group - x.s * p.hs);
-    const int q0 = x.qt * qtile;
-    const uint16_t* qb = p.q + (int64_t(p.n_dec) + x.cq0) * p.q_st;
-    const i32x4_t rq = raw_rsrc(qb, int(int64_t(x.geo.sq) * p.q_st * 2));
-#pragma unroll
-    for (int jj = 0; jj < kPfQLoadsPerWave; ++jj) {
-      const int k = wave + kWaves * jj;
-      const int sl = k * 64 + L.lane;
-      const int col = sl / kPfRowSlots;
-      const int ch = sl - col * kPfRowSlots;
-      const int lm = col & 15;
-      const int tdiv = int((float(lm) + 0.5f) * inv_hs);  // lm / hs (lm < 16)
-      const int hh = lm - tdiv * p.hs;
-      const int tq = q0 + (col >> 4) * p.tpb + tdiv;
-      const bool ok = k < kPfQLoads && ch < 16 && lm < p.tpb * p.hs && hh < hs && tq < x.geo.sq;
-      const int off =
-          ok ? int((int64_t(tq) * p.q_st + int64_t(x.g * p.group + x.s * p.hs + hh) * p.q_sh) *
-                   2) +
-                   ch * 16
-             : kOob;
-      pf_dma(rq, off, k < kPfQLoads ? lds0 + kPfQOff + k * 1024 : lds0 + kPfDummyOff);
-    }
-  };
-
-  // Prologue: the first item's query, then the first kPfStages tiles (every
-  // stage).  `issued` counts this wave's loads; mk[k] = its value right after
-  // the loads of the tile k + 1 ahead of the one being attended, q_mark right
-  // after the latest query loads, so the wait for a tile (and for its
-  // segment's query) is issued - mark.
-  int issued = 0;
-  issue_q(it);
-  issued += kPfQLoadsPerWave;
-  int q_mark = issued;
-  int q_issued_for = it.P;  // item (by its span start) whose query was loaded last
-  int mk0 = 0;              // after the first tile's loads
-  int mk[kPfStages - 1];
-#pragma unroll
-  for (int k = 0; k < kPfStages; ++k) {
-    if (prod_live()) {
-      produce(k);
-      issued += kPfTileLoads;
-    }
-    if (k == 0) {
-      mk0 = issued;
-    } else {
-      mk[k - 1] = issued;
-    }
-  }
-
-  // K operands of the tile about to be attended: read one step ahead, under
-  // the previous tile's P V MFMAs (lane (lm, lg) holds key lm (+ 16 for the
-  // second half) at dims 32 c + 8 lg .. + 7).
-  u32x4_t kop[2][4];
-  auto read_k = [&](int stg) {
-    const char* kb = lds + stg * kPfStage + L.lm * kPfPitch + L.lg * 16;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-        kop[h][c] = *reinterpret_cast<const u32x4_t*>(kb + h * 16 * kPfPitch + c * 64);
-    }
-  };
-  if (it.P + kPfItemCost + ct < end) {
-    pf_wait_vm(issued - mk0);  // the first tile and the first query
-    pf_barrier();
-    read_k(0);
-  }
-
-  int stage = 0;
-  bool first = true;
-  PfState st;
-  QOps<kBF16, kPreNCB> Q;
-  int klim[kPreNCB];
-  int min_klim = 0, split = -1;
-
-  // Per tile: (a) V^T operands, (b) S^T and the softmax, (c) the wait for the
-  // next tile and the barrier, (d) the next query and tile loads into the
-  // stages every wave is done with, (e) the next tile's K operands, (f) P V,
-  // (g) the epilogue at a segment end.  The K reads of (e) run under the MFMAs
-  // of (f), the V reads of (a) under those of (b).
-  while (it.P + kPfItemCost + ct < end) {
-    const bool seg_start = first || ct == 0;
-    const bool seg_end = ct + 1 == it.T || it.P + kPfItemCost + ct + 1 >= end;
-    const bool has_next = it.P + kPfItemCost + ct + 1 < end;
-    first = false;
-    if (seg_start) {
-      if (q_issued_for != it.P) {
-        // The previous segment was one tile long: load this one's query now.
-        issue_q(it);
-        issued += kPfQLoadsPerWave;
-        q_mark = issued;
-        q_issued_for = it.P;
-        pf_wait_vm(0);
-        pf_barrier();
-      }
-      const int hs = min(p.hs, p.group - it.s * p.hs);
-      const int q0 = it.qt * qtile;
-      const int prefix = it.geo.sk - it.geo.sq;
-      const char* qrow = lds + kPfQOff + (32 * wave + L.lm) * kPfPitch + L.lg * 16;
-#pragma unroll
-      for (int cb = 0; cb < kPreNCB; ++cb) {
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-          Q.op[cb][c] = *reinterpret_cast<const u32x4_t*>(qrow + cb * 16 * kPfPitch + c * 64);
-        const int tq = q0 + (wave * kPreNCB + cb) * p.tpb + L.lm / p.hs;
-        const int hh = L.lm % p.hs;
-        const bool ok = (L.lm < p.tpb * p.hs) && hh < hs && tq < it.geo.sq;
-        klim[cb] = ok ? prefix + tq : -1;
-      }
-      min_klim = 0x7fffffff;
-#pragma unroll
-      for (int cb = 0; cb < kPreNCB; ++cb)
-        if (klim[cb] >= 0) min_klim = min(min_klim, klim[cb]);
-    #pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) min_klim = min(min_klim, __shfl_xor(min_klim, m, 64));
-      pf_init(st);
-      // Split bookkeeping: the item's real tiles span shares [f, l].
-      const int f = (it.P + kPfItemCost) / S;
-      const int nseg = (it.P + kPfItemCost + it.T - 1) / S - f + 1;
-      split = nseg == 1 ? -1 : w - f;
-      if (f == w && int(threadIdx.x) < min(qtile, it.geo.sq - q0) && p.sk_nseg != nullptr)
-        p.sk_nseg[(int64_t(p.n_dec) + it.cq0 + q0 + threadIdx.x) * kvs_total + it.kvs] = nseg;
-    }
-    // (a) This tile's V^T operands through transposing reads (lane (lm, lg)
-    // addresses key key_of_slot(lg, lm / 4) (+ 16 for the second half) at
-    // dims 16 jj + 4 (lm % 4)).
-    u32x4_t va[8];
-    {
-      const char* vb = lds + stage * kPfStage + kPfTensor +
-                       (4 * L.lg + (L.lm >> 2)) * kPfPitchV + (L.lm & 3) * 8;
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) {
-        const u32x2_t lo = lds_read_tr16(vb + jj * 32);
-        const u32x2_t hi = lds_read_tr16(vb + 16 * kPfPitchV + jj * 32);
-        va[jj] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
-      }
-    }
-    // (b) S^T and the softmax: the unmasked form when every key exists and
-    // every valid column sees all 32.
-    const int key0 = ct * kTile;
-    u32x4_t pb[kPreNCB];
-    if (key0 + kTile <= it.geo.sk && key0 + kTile - 1 <= min_klim) {
-      pf_score<false>(st, kop, Q, klim, key0, it.geo.sk, p.scale_log2, L, pb);
-    } else {
-      pf_score<true>(st, kop, Q, klim, key0, it.geo.sk, p.scale_log2, L, pb);
-    }
-    const int next_stage = stage == kPfStages - 1 ? 0 : stage + 1;
-    if (has_next) {
-      // (c) This wave's loads of the next tile (and, when the next tile starts
-      // the next segment, of its prefetched query) have landed, and every
-      // wave's: the next stage is complete, and every wave is done with this
-      // tile's K and V and with this segment's query block.
-      const int nP = it.P + kPfItemCost + it.T;  // span start of the next item
-      int need = mk[0];
-      if (seg_end && q_issued_for == nP) need = max(need, q_mark);
-      if (issued - need == kPfTileLoads * (kPfStages - 2)) {
-        pf_wait_vm(kPfTileLoads * (kPfStages - 2));  // steady state: an immediate
-      } else {
-        pf_wait_vm(issued - need);
-      }
-      pf_barrier();
-      // (d) The next item's query, unless the next tile starts it (no barrier
-      // would separate its loads from the reads), then the tile kPfStages
-      // ahead into this tile's stage.
-      if (!seg_end && nP + kPfItemCost < end && q_issued_for != nP) {
-        PfItem nx = it;
-        pf_next_item(nx, cu_q, cu_k, p.n_pre, kvs_total, p.nslices, qtile);
-        smem_drain();
-        issue_q(nx);
-        issued += kPfQLoadsPerWave;
-        q_mark = issued;
-        q_issued_for = nP;
-      }
-      if (prod_live()) {
-        produce(stage);
-        issued += kPfTileLoads;
-      }
-#pragma unroll
-      for (int k = 0; k + 1 < kPfStages - 1; ++k) mk[k] = mk[k + 1];
-      mk[kPfStages - 2] = issued;
-      // (e) The next tile's K operands.
-      read_k(next_stage);
-    }
-    // (f) O^T += V^T P^T.
-    pf_pv(st, va, pb);
-    // (g) Segment end: store (lane (lm, lg) holds dims 16 jj + 4 lg .. + 3 of
-    // column lm for every jj), then move to the next item.
-    if (seg_end) {
-      const int q0 = it.qt * qtile;
-      const int hs = min(p.hs, p.group - it.s * p.hs);
-#pragma unroll
-      for (int cb = 0; cb < kPreNCB; ++cb) {
-        const int tq = q0 + (wave * kPreNCB + cb) * p.tpb + L.lm / p.hs;
-        const int hh = L.lm % p.hs;
-        if ((L.lm < p.tpb * p.hs) && hh < hs && tq < it.geo.sq) {
-          const int64_t row = int64_t(p.n_dec) + it.cq0 + tq;
-          const int head = it.g * p.group + it.s * p.hs + hh;
-          const float l = st.l[cb][0];
-          if (split < 0) {
-            const float inv = 1.f / l;
-            uint16_t* dst = p.out + row * p.o_st + int64_t(head) * p.o_sh + 4 * L.lg;
-#pragma unroll
-            for (int jj = 0; jj < 8; ++jj) {
-              *reinterpret_cast<u32x2_t*>(dst + 16 * jj) =
-                  u32x2_t{pack_bf16x2_fast(st.o[cb][jj][0] * inv, st.o[cb][jj][1] * inv),
-                          pack_bf16x2_fast(st.o[cb][jj][2] * inv, st.o[cb][jj][3] * inv)};
-            }
-          } else {
-            const int64_t base = (row * p.num_heads + head) * p.max_splits + split;
-            const float il = l > 0.f ? 1.f / l : 0.f;
-            float* dst = p.part_o + base * kD + 4 * L.lg;
-#pragma unroll
-            for (int jj = 0; jj < 8; ++jj)
-              *reinterpret_cast<float4*>(dst + 16 * jj) =
-                  make_float4(st.o[cb][jj][0] * il, st.o[cb][jj][1] * il, st.o[cb][jj][2] * il,
-                              st.o[cb][jj][3] * il);
-            if (L.lg == 0) p.part_lse[base] = l > 0.f ? st.m[cb] + __log2f(l) : -INFINITY;
-          }
-        }
-      }
-    }
-    if (++ct == it.T) {
-      if (it.P + kPfItemCost + it.T >= end) break;
-      pf_next_item(it, cu_q, cu_k, p.n_pre, kvs_total, p.nslices, qtile);
-      smem_drain();
-      ct = 0;
-    }
-    stage = next_stage;
-  }
-  __builtin_amdgcn_s_waitcnt(0);
-}
-
 // ---------------------------------------------------------------------------
-// Stream-K prefill over bf16 keys, lean ring (prefill_sk2_kernel).
-//
-// The same items, partition, split bookkeeping and output formats as
-// prefill_sk_kernel, with a cheaper tile loop:
+// Stream-K prefill over bf16 keys (prefill_sk2_kernel), with a lean tile
+// loop:
 //  * each wave stages its own 32 query columns in a private LDS region by
 //    direct-to-LDS loads and reads them back after its own vmcnt wait, so a
 //    query reload needs no workgroup barrier.  The next segment's query is
@@ -4065,12 +3318,12 @@ __device__ __forceinline__ void p2_load_chunk(PfItem& it, const int4* ctab, cons
 #endif
 constexpr int kP2ItemCost = KVC_P2_ITEM_COST;
 
-// Weighted tiles of query tiles [0, q) of chunk c (pf_qcum with kP2ItemCost).
+// Weighted tiles of query tiles [0, q) of chunk c.
 __device__ __forceinline__ int p2_qcum(const ChunkGeo& c, int tpb, int q) {
   return int(qtile_cum(c, tpb, q)) + kP2ItemCost * q;
 }
 
-// pf_next_item with the chunk table.
+// The item after `it` (T = 0 past the last one), chunks read from the table.
 __device__ __forceinline__ void p2_next_item(PfItem& it, const int4* ctab, const int32_t* cu_q,
                                              const int32_t* cu_k, int n_pre, int kvs_total,
                                              int nslices, int qtile) {
@@ -4223,7 +3476,8 @@ __device__ __forceinline__ void prefill_sk2_share(const AttnParams& p,
   const uint32_t dst1 = w0 ? 8 * 1024 : kPfTensor + uint32_t(wave - 1) * 1024;
   const uint32_t dst2 = kPfTensor + uint32_t(7 + wave) * 1024;
 
-  // Producer cursor (as in prefill_sk_kernel).
+  // Producer cursor: the item and tile whose loads are issued next, running
+  // ahead of the consumer (it, ct) by the ring depth.
   PfItem pi = it;
   int pt = ct;
   int pblk = 0, poff = 0, pblk_val = 0, pnext_val = 0, plast = 0;
@@ -5202,53 +4456,17 @@ void launch_decode_enc(const AttnParams& p, int grid, hipStream_t st) {
   paged_decode_kernel<kEnc><<<grid, kThreads, 0, st>>>(p);
 }
 
-template <int kEnc>
-void launch_mixed_enc(const AttnParams& p, int grid, bool fresh, bool lds, hipStream_t st) {
-  if (fresh) {
-    if constexpr (kEnc == kBF16)
-      mixed_sk_kernel<kBF16, true, false><<<grid, kThreads, 0, st>>>(p, p.cu_q, p.cu_k, p.ctx_lens,
-                                                                 p.block_tables);
-  } else if (lds) {
-    if constexpr (kEnc == kBF16)
-      mixed_sk_kernel<kBF16, false, true><<<grid, kThreads, 0, st>>>(p, p.cu_q, p.cu_k, p.ctx_lens,
-                                                                 p.block_tables);
-  } else {
-    mixed_sk_kernel<kEnc, false, false><<<grid, kThreads, 0, st>>>(p, p.cu_q, p.cu_k, p.ctx_lens,
-                                                                 p.block_tables);
-  }
-}
 
-// Stream-K plan of a mixed launch: the split cap of the paged decode plan
-// over the longest item (decode context or prefill key range).
-// Shares can be one tile, so an item of T tiles may span T + 1 workgroups;
-// the cap is 64 splits and the partials' byte bound.
-SkPlan plan_mixed(int64_t num_q_tokens, int64_t num_heads, int64_t num_decode_rows,
-                  int64_t max_ctx, int64_t max_seqlen_k) {
-  const int64_t longest = std::max<int64_t>(num_decode_rows > 0 ? max_ctx : 0, max_seqlen_k);
-  SkPlan sp{true, int(device_cus()), 2};
-  int64_t ms = (longest + kTile - 1) / kTile + 1;
-  const int64_t per_split = num_q_tokens * num_heads * (kD + 1) * int64_t(sizeof(float));
-  const int64_t cap = per_split > 0 ? kSkMaxPartialBytes / per_split : 64;
-  ms = std::min<int64_t>(std::min<int64_t>(ms, 64), cap);
-  sp.max_splits = int(ms < 2 ? 2 : ms);
-  return sp;
-}
 
-// The stream-K mixed partition is opt-in (KVC_MIXED_STREAMK=1): a prefill
-// segment carries a query load and a partial write, and shares that chain
-// several short items pay them in sequence, so one workgroup per unit is
-// still the faster default.
-bool mixed_stream_k() { return env_int("KVC_MIXED_STREAMK", 0) != 0; }
 
 // A varlen call with decode rows over a paged pool runs them as a paged decode
-// launch (stream-K, LDS-staged) and the prefill rows as a second launch on the
-// same stream: one combined launch costs the sum of its two halves anyway
-// (the compute-bound prefill units occupy every CU before the decode units
-// start), and the decode rows run faster in the decode kernel.
-// KVC_MIXED_SPLIT=0 keeps the single launch.
+// (stream-K) and the prefill rows as a stream-K prefill: in one launch over a
+// CU split where both sides allow it (mixed_split_kernel), else one launch
+// after the other on the same stream.  (One combined launch of decode and
+// prefill units, and one stream-K launch over both, both measured slower on
+// every mix.)
 bool split_mixed(int64_t num_decode_rows, int64_t page_size) {
-  return num_decode_rows > 0 && page_size > 0 && !mixed_stream_k() &&
-         env_int("KVC_MIXED_SPLIT", 1) != 0;
+  return num_decode_rows > 0 && page_size > 0;
 }
 
 // Workgroups (= CUs) the decode side of a mixed call's split launch gets
@@ -5265,9 +4483,8 @@ bool split_mixed(int64_t num_decode_rows, int64_t page_size) {
 int mixed_decode_cus(int64_t num_decode_rows, int64_t num_prefill_tokens, int kv_dtype,
                      int64_t num_heads, int64_t num_kv_heads) {
   if (num_decode_rows <= 0 || num_prefill_tokens <= 0) return 0;
-  if (kv_dtype != KVC_KV_BF16 || mixed_stream_k() || env_int("KVC_DECODE_STREAMK", 1) == 0 ||
-      env_int("KVC_DECODE_LDS", 1) == 0 || env_int("KVC_PREFILL_SK", 1) == 0 ||
-      env_int("KVC_PF_RING", 0) != 0)
+  if (kv_dtype != KVC_KV_BF16 || env_int("KVC_DECODE_STREAMK", 1) == 0 ||
+      env_int("KVC_DECODE_LDS", 1) == 0 || env_int("KVC_PREFILL_SK", 1) == 0)
     return 0;
   const HeadPlan hp = plan_heads(num_heads, num_kv_heads);
   if (hp.kvs_per_wg != 4 || hp.nslices != 1) return 0;
@@ -5280,12 +4497,12 @@ int mixed_decode_cus(int64_t num_decode_rows, int64_t num_prefill_tokens, int kv
 }
 
 // Prefill-only launches over bf16 keys run as one stream-K launch
-// (prefill_sk_kernel) unless KVC_PREFILL_SK=0 selects one workgroup per
+// (prefill_sk2_kernel) unless KVC_PREFILL_SK=0 selects one workgroup per
 // prefill unit.  The workspace query cannot see the key encoding or the
 // query strides, so it sizes for both; the launch also needs every chunk's
 // query rows below 2 GiB (one buffer resource).
 bool prefill_stream_k(int64_t num_decode_rows) {
-  return num_decode_rows == 0 && !mixed_stream_k() && env_int("KVC_PREFILL_SK", 1) != 0;
+  return num_decode_rows == 0 && env_int("KVC_PREFILL_SK", 1) != 0;
 }
 
 // Split cap of a stream-K prefill launch: an item of T tiles spans at most
@@ -5301,14 +4518,6 @@ SkPlan plan_prefill_sk(int64_t num_q_tokens, int64_t num_heads, int64_t max_seql
 }
 
 void launch_prefill_sk(const AttnParams& p, int grid, bool fresh, hipStream_t st) {
-  if (env_int("KVC_PF_RING", 0) != 0) {
-    if (fresh) {
-      prefill_sk_kernel<true><<<grid, kThreads, 0, st>>>(p, p.cu_q, p.cu_k, p.block_tables);
-    } else {
-      prefill_sk_kernel<false><<<grid, kThreads, 0, st>>>(p, p.cu_q, p.cu_k, p.block_tables);
-    }
-    return;
-  }
   if (fresh) {
     prefill_sk2_kernel<true><<<grid, kThreads, 0, st>>>(p, p.cu_q, p.cu_k, p.block_tables);
   } else {
@@ -5804,17 +5013,8 @@ extern "C" size_t kvc_varlen_workspace_bytes(int64_t num_q_tokens, int64_t num_h
                                                   page_size, max_blocks_per_seq);
     return (dec + 255) / 256 * 256 + pre;
   }
-  if (mixed_stream_k()) {
-    const SkPlan sp = plan_mixed(num_q_tokens, num_heads, num_decode_rows,
-                                 max_blocks_per_seq * page_size, max_seqlen_k);
-    return sk_workspace_bytes(num_q_tokens, num_heads, num_kv_heads * hp.nslices, sp.max_splits);
-  }
+  // Prefill rows only (decode rows without a paged pool are refused).
   int64_t splits = 1;
-  if (num_decode_rows > 0) {
-    const int64_t max_ctx = max_blocks_per_seq * page_size;
-    const int ch = plan_decode_chunk(num_decode_rows, hp.groups, max_ctx);
-    splits = max_ctx > 0 ? (max_ctx + ch - 1) / ch : 1;
-  }
   if (max_seqlen_k > 0) {
     const int ks = plan_prefill_split(max_seqlen_k);
     const int64_t ps = (max_seqlen_k + ks - 1) / ks;
@@ -5968,6 +5168,9 @@ extern "C" int kvc_varlen_attention(
         out_stride_t, out_stride_h, pre_ws ? ws + dec_span : nullptr, pre_ws, stream);
   }
 
+  // Prefill rows only from here: decode rows went to the paged decode above
+  // (with block tables the page size is positive; without, decode rows are
+  // refused).
   const HeadPlan hp = plan_heads(num_heads, num_kv_heads);
   AttnParams p{};
   p.merge_first = 0;  // most rows of these launches are not split
@@ -5988,19 +5191,10 @@ extern "C" int kvc_varlen_attention(
           v_scale, side_k, side_v, out_idx2d, head_n_out, n_out_max);
   p.block_tables = block_tables;
   p.bt_stride = bt_stride;
-  p.n_dec = int(num_decode_rows);
-  p.ctx_lens = decode_context_lens;
+  p.n_dec = 0;
   int64_t max_splits = 1;
   p.chunk_tokens = kTile;
   p.dec_max_chunks = 0;
-  if (num_decode_rows > 0) {
-    KVC_REQUIRE(decode_context_lens != nullptr, KVC_ERR_VALUE,
-                "varlen_attention: decode rows need decode_context_lens");
-    const int64_t max_ctx = max_blocks_per_seq * page_size;
-    p.chunk_tokens = plan_decode_chunk(num_decode_rows, hp.groups, max_ctx);
-    p.dec_max_chunks = int((max_ctx + p.chunk_tokens - 1) / p.chunk_tokens);
-    max_splits = p.dec_max_chunks;
-  }
   p.n_pre = int(num_prefill);
   p.cu_q = cu_seqlens_q;
   p.cu_k = cu_seqlens_k;
@@ -6015,49 +5209,10 @@ extern "C" int kvc_varlen_attention(
   p.vf = static_cast<const uint16_t*>(v_fresh);
   p.vf_st = vf_stride_t;
   p.vf_sh = vf_stride_h;
-  if (mixed_stream_k()) {
-    // One workgroup per CU over the concatenated tiles of every prefill item
-    // and decode row unit (mixed_sk_kernel), then the merge over every row.
-    const int64_t kv_slices = num_kv_heads * hp.nslices;
-    const int64_t max_ctx = max_blocks_per_seq * page_size;
-    const int64_t qtile = int64_t(kWaves) * kPreNCB * hp.tpb;
-    const int64_t pre_bound =
-        kv_slices * (num_q_tokens / qtile + num_prefill + 1) * ((max_seqlen_k + kTile - 1) / kTile);
-    const int64_t dec_bound = num_decode_rows * kv_slices * ((max_ctx + kTile - 1) / kTile);
-    KVC_REQUIRE(pre_bound + dec_bound < (int64_t(1) << 30), KVC_ERR_VALUE,
-                "varlen_attention: launch too large");
-    const SkPlan sp = plan_mixed(num_q_tokens, num_heads, num_decode_rows, max_ctx, max_seqlen_k);
-    p.chunk_tokens = kTile;
-    p.max_splits = sp.max_splits;
-    // Shares as small as one tile: a prefill segment costs a query load and
-    // an epilogue, so short items are better spread than queued.
-    p.sk_min_share = 1;
-    p.merge_first = 0;
-    const size_t need = sk_workspace_bytes(num_q_tokens, num_heads, kv_slices, sp.max_splits);
-    KVC_REQUIRE(workspace != nullptr && workspace_bytes >= need, KVC_ERR_WORKSPACE,
-                "varlen_attention: workspace of %zu bytes needed (got %zu)", need,
-                workspace_bytes);
-    set_partials(p, workspace, num_q_tokens);
-    p.sk_nseg = reinterpret_cast<int*>(static_cast<char*>(workspace) +
-                                       sk_partial_part(num_q_tokens, num_heads, p.max_splits));
-    hipStream_t st = as_stream(stream);
-    const int enc = fresh ? KVC_KV_BF16 : kv_dtype;
-    const bool lds = !fresh && enc == KVC_KV_BF16 && hp.kvs_per_wg == 4 && hp.nslices == 1 &&
-                     env_int("KVC_DECODE_LDS", 1) != 0;
-    switch (enc) {
-      case KVC_KV_BF16: launch_mixed_enc<kBF16>(p, sp.grid, fresh, lds, st); break;
-      case KVC_KV_INT8_TOKHEAD: launch_mixed_enc<kI8Tok>(p, sp.grid, false, false, st); break;
-      default: launch_mixed_enc<kI8Chan>(p, sp.grid, false, false, st); break;
-    }
-    rc = check_launch("varlen_attention");
-    if (rc != KVC_OK) return rc;
-    launch_merge(p, num_q_tokens, st);
-    return check_launch("varlen_attention merge");
-  }
   if (prefill_stream_k(num_decode_rows) && (fresh || kv_dtype == KVC_KV_BF16) &&
       num_q_tokens * q_stride_t * 2 < (int64_t(1) << 31)) {
     // Prefill rows only, bf16 keys: one workgroup per CU over the
-    // concatenated tiles of every item (prefill_sk_kernel), then the merge.
+    // concatenated tiles of every item (prefill_sk2_kernel), then the merge.
     const int64_t kv_slices = num_kv_heads * hp.nslices;
     const int64_t qtile = int64_t(kWaves) * kPreNCB * hp.tpb;
     const int64_t bound =
@@ -6075,7 +5230,7 @@ extern "C" int kvc_varlen_attention(
     p.sk_nseg = reinterpret_cast<int*>(static_cast<char*>(workspace) +
                                        sk_partial_part(num_q_tokens, num_heads, p.max_splits));
     hipStream_t st = as_stream(stream);
-    if (num_prefill > 0 && tl_record != nullptr && !fresh && env_int("KVC_PF_RING", 0) == 0) {
+    if (num_prefill > 0 && tl_record != nullptr && !fresh) {
       tl_record->taken = true;
       tl_record->p = p;
       tl_record->grid = sp.grid;
@@ -6097,12 +5252,11 @@ extern "C" int kvc_varlen_attention(
               "varlen_attention: workspace of %zu bytes needed (got %zu)", need,
               workspace_bytes);
   set_partials(p, workspace, num_q_tokens);
-  const int64_t dec_units = num_decode_rows * hp.groups * p.dec_max_chunks;
-  KVC_REQUIRE(dec_units + num_prefill_units < (int64_t(1) << 31) && num_prefill_units >= 0,
-              KVC_ERR_VALUE, "varlen_attention: launch too large");
-  p.dec_units = int(dec_units);
+  KVC_REQUIRE(num_prefill_units < (int64_t(1) << 31) && num_prefill_units >= 0, KVC_ERR_VALUE,
+              "varlen_attention: launch too large");
+  p.dec_units = 0;
   p.pre_units = int(num_prefill_units);
-  const int grid = int(dec_units + num_prefill_units);
+  const int grid = int(num_prefill_units);
   hipStream_t st = as_stream(stream);
   if (grid > 0) {
     switch (fresh ? KVC_KV_BF16 : kv_dtype) {

@@ -20,24 +20,16 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-@pytest.fixture(params=["prefill-sk", "prefill-ring", "split-64", "serial", "units",
-                        "stream-k", "combined"])
+@pytest.fixture(params=["prefill-sk", "split-64", "serial", "units"])
 def partition(request, monkeypatch):
     """Every launch partition: prefill rows over bf16 keys as one stream-K
     prefill launch and a mixed call's decode and prefill rows as one launch
     over a static CU split with the default decode share (the defaults), the
-    same items through the first form of the prefill launch (KVC_PF_RING=1,
-    mixed calls then run their two launches in turn), the split with 64
-    decode CUs (KVC_MIXED_DECODE_CUS=64), the decode launch and then the
-    prefill launch (KVC_MIXED_DECODE_CUS=0), one workgroup per prefill unit
-    (KVC_PREFILL_SK=0), the single stream-K launch of decode and prefill
-    items together (KVC_MIXED_STREAMK=1), and the single unit launch of
-    decode and prefill units together (KVC_MIXED_SPLIT=0; without decode rows
-    it is the default launch)."""
-    monkeypatch.setenv("KVC_MIXED_STREAMK", "1" if request.param == "stream-k" else "0")
+    split with 64 decode CUs (KVC_MIXED_DECODE_CUS=64), the decode launch and
+    then the prefill launch (KVC_MIXED_DECODE_CUS=0), and one workgroup per
+    prefill unit (KVC_PREFILL_SK=0; a mixed call then runs its decode launch
+    and its unit launch in turn)."""
     monkeypatch.setenv("KVC_PREFILL_SK", "0" if request.param == "units" else "1")
-    monkeypatch.setenv("KVC_MIXED_SPLIT", "0" if request.param == "combined" else "1")
-    monkeypatch.setenv("KVC_PF_RING", "1" if request.param == "prefill-ring" else "0")
     if request.param == "split-64":
         monkeypatch.setenv("KVC_MIXED_DECODE_CUS", "64")
     elif request.param == "serial":
