@@ -246,7 +246,9 @@ int kvc_paged_decode_append_int8(const void* q, int64_t q_stride_b, int64_t q_st
                                  size_t workspace_bytes, kvc_stream_t stream);
 
 /* Bytes of device scratch kvc_paged_decode_append_static holds on each GPU
- * it runs on: 64 MiB.  At 32 q / 4 kv heads and pages of 256 that covers
+ * it runs on: 64 MiB, reserved by the first static call on that GPU (the
+ * array is a code object of its own, loaded when first used) and held until
+ * the process ends; processes that never call it reserve none.  At 32 q / 4 kv heads and pages of 256 that covers
  * batch 32 at any table width, batch 64 with tables of up to 62 pages
  * (15872 tokens), batch 128 up to 30 pages, batch 256 up to 14 pages. */
 #define KVC_STATIC_SCRATCH_BYTES (64u << 20)
@@ -264,7 +266,8 @@ int kvc_paged_decode_append_int8(const void* q, int64_t q_stride_b, int64_t q_st
  * that GPU's scratch, which keeps the last call's contents: calls that
  * overlap on one GPU (on different streams or from different threads) race
  * and must be ordered by the caller, e.g. on one stream.  The scratch is
- * that of the device `stream` belongs to. */
+ * that of the device `stream` belongs to.  The first call on a device
+ * resolves (and loads) its scratch: make it before any graph capture. */
 int kvc_paged_decode_append_static(
     const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* key, int64_t key_stride_n,
     int64_t key_stride_h, const void* value, int64_t value_stride_n, int64_t value_stride_h,

@@ -4890,74 +4890,10 @@ extern "C" int kvc_paged_decode_append_int8(
                            stream);
 }
 
-// ---------------------------------------------------------------------------
 // The decode step without a caller workspace: the split-K partials and split
-// counts live in `scratch`, one array per GPU (each device that loads the
-// library's code object holds its own copy, until the process ends).  Host
-// code never uses the array's name as an address: the first call on a device
-// resolves that device's copy with hipGetSymbolAddress (the device current
-// while it does so) and every later call on it passes the cached pointer.
-// The array needs no clearing: each launch writes every split count and
-// partial its merge reads.
-// ---------------------------------------------------------------------------
-static __device__ __align__(256) unsigned char scratch[KVC_STATIC_SCRATCH_BYTES];
-
-namespace {
-constexpr int kMaxScratchDevices = 64;
-std::atomic<void*> g_scratch_ptr[kMaxScratchDevices];
-std::mutex g_scratch_mu;
-
-// The device `stream` runs on (the current device for the NULL stream).
-int stream_device(hipStream_t stream, int* dev) {
-  hipError_t e = hipGetDevice(dev);
-  KVC_REQUIRE(e == hipSuccess, KVC_ERR_RUNTIME, "paged_decode_append_static: hipGetDevice: %s",
-              hipGetErrorString(e));
-  if (stream != nullptr) {
-    e = hipStreamGetDevice(stream, dev);
-    KVC_REQUIRE(e == hipSuccess, KVC_ERR_RUNTIME,
-                "paged_decode_append_static: hipStreamGetDevice: %s", hipGetErrorString(e));
-  }
-  KVC_REQUIRE(*dev >= 0 && *dev < kMaxScratchDevices, KVC_ERR_RUNTIME,
-              "paged_decode_append_static: device %d out of range", *dev);
-  return KVC_OK;
-}
-
-// Address of device `dev`'s scratch array, resolved once per device.
-int scratch_for_device(int dev, void** ptr) {
-  void* cached = g_scratch_ptr[dev].load(std::memory_order_acquire);
-  if (cached != nullptr) {
-    *ptr = cached;
-    return KVC_OK;
-  }
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  cached = g_scratch_ptr[dev].load(std::memory_order_relaxed);
-  if (cached == nullptr) {
-    int prev = 0;
-    hipError_t e = hipGetDevice(&prev);
-    KVC_REQUIRE(e == hipSuccess, KVC_ERR_RUNTIME, "paged_decode_append_static: hipGetDevice: %s",
-                hipGetErrorString(e));
-    if (prev != dev) {
-      e = hipSetDevice(dev);
-      KVC_REQUIRE(e == hipSuccess, KVC_ERR_RUNTIME,
-                  "paged_decode_append_static: hipSetDevice(%d): %s", dev, hipGetErrorString(e));
-    }
-    void* p = nullptr;
-    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    const hipError_t restore = prev != dev ? hipSetDevice(prev) : hipSuccess;
-    KVC_REQUIRE(e == hipSuccess && p != nullptr, KVC_ERR_RUNTIME,
-                "paged_decode_append_static: hipGetSymbolAddress(scratch) on device %d: %s", dev,
-                hipGetErrorString(e));
-    KVC_REQUIRE(restore == hipSuccess, KVC_ERR_RUNTIME,
-                "paged_decode_append_static: hipSetDevice(%d): %s", prev,
-                hipGetErrorString(restore));
-    g_scratch_ptr[dev].store(p, std::memory_order_release);
-    cached = p;
-  }
-  *ptr = cached;
-  return KVC_OK;
-}
-}  // namespace
-
+// counts live in the library's static scratch array of the stream's device
+// (kvc_scratch.hip).  The array needs no clearing: each launch writes every
+// split count and partial its merge reads.
 extern "C" int kvc_paged_decode_append_static(
     const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* key, int64_t key_stride_n,
     int64_t key_stride_h, const void* value, int64_t value_stride_n, int64_t value_stride_h,

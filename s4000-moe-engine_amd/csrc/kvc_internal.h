@@ -46,6 +46,14 @@ inline hipStream_t as_stream(kvc_stream_t s) { return reinterpret_cast<hipStream
 unsigned long long* claim_set(hipStream_t stream, int words);
 int claim_set_words();
 
+// The device `stream` runs on (the current device for the NULL stream), for
+// kvc_paged_decode_append_static (kvc_scratch.hip).
+int stream_device(hipStream_t stream, int* dev);
+
+// Address of device `dev`'s copy of the static scratch array
+// (KVC_STATIC_SCRATCH_BYTES, kvc_scratch.hip), resolved once per device.
+int scratch_for_device(int dev, void** ptr);
+
 // ---------------------------------------------------------------------------
 // Device-side vector types and helpers.
 // ---------------------------------------------------------------------------

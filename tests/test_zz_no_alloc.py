@@ -3,14 +3,15 @@ per-GPU scratch instead of a caller workspace) called through the C ABI,
 against kvc_paged_decode_append with a workspace: the same output bits and
 the same pool bytes, on two calls in a row (the headline batch 64 x 4096,
 then a smaller ragged batch that reuses the scratch the first call left
-behind), and a clear error for a launch the scratch cannot hold."""
+behind), the Python wrapper captured into a graph and replayed with new
+inputs, and a clear error for a launch the scratch cannot hold."""
 import numpy as np
 import pytest
 import torch
 
 from helpers import bits
 from nanovllm_amd import _native as nat
-from nanovllm_amd.kernels.paged_attention import paged_decode_append
+from nanovllm_amd.kernels.paged_attention import paged_decode_append, paged_decode_append_static
 from nanovllm_amd.workloads import decode_workload, uniform_lengths
 
 pytestmark = pytest.mark.gpu
@@ -50,6 +51,49 @@ def test_static_scratch_equals_workspace_entry_point_twice(deterministic_decode)
         assert torch.equal(kc1.view(torch.int16), kc0.view(torch.int16)), f"{label}: K pool"
         assert torch.equal(vc1.view(torch.int16), vc0.view(torch.int16)), f"{label}: V pool"
         print(f"[no-alloc] {label}: bit-exact", flush=True)
+
+
+def test_static_entry_point_in_a_graph_replays_like_the_workspace_path(deterministic_decode):
+    """paged_decode_append_static captured once into a torch CUDA graph (its
+    first call, which resolves the scratch, made eagerly beforehand), then
+    replayed with new q / key / value written into the captured buffers
+    between replays: every replay's output bits and pool bytes equal
+    paged_decode_append's (with a workspace) on the same inputs."""
+    lens = uniform_lengths(13, 1, 3000, seed=8)
+    wl = decode_workload(len(lens), 32, 4, 200, lens, seed=9, device=DEV, pool_device_fill=True)
+    kc_init, vc_init = wl.k_cache.clone(), wl.v_cache.clone()
+    q, key, value = wl.q.clone(), wl.new_k.clone(), wl.new_v.clone()
+    out = torch.empty_like(q)
+
+    def step():
+        paged_decode_append_static(q, key, value, wl.k_cache, wl.v_cache, wl.slot_mapping,
+                                   wl.block_tables, wl.context_lens, wl.scale, out)
+
+    step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    torch.cuda.synchronize()
+    g = torch.Generator().manual_seed(21)
+    for rep in range(3):
+        q.copy_(torch.randn(q.shape, generator=g).to(torch.bfloat16))
+        key.copy_(torch.randn(key.shape, generator=g).to(torch.bfloat16))
+        value.copy_(torch.randn(value.shape, generator=g).to(torch.bfloat16))
+        torch.cuda.synchronize()
+        print(f"[no-alloc] graph replay {rep}: B={len(lens)}", flush=True)
+        graph.replay()
+        torch.cuda.synchronize()
+        kc_ref, vc_ref = kc_init.clone(), vc_init.clone()
+        ref = paged_decode_append(q, key, value, kc_ref, vc_ref, wl.slot_mapping,
+                                  wl.block_tables, wl.context_lens, wl.scale)
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(out), bits(ref)), f"replay {rep}: outputs differ"
+        assert torch.equal(wl.k_cache.view(torch.int16), kc_ref.view(torch.int16)), \
+            f"replay {rep}: K pool"
+        assert torch.equal(wl.v_cache.view(torch.int16), vc_ref.view(torch.int16)), \
+            f"replay {rep}: V pool"
+    del graph
 
 
 def test_static_scratch_rejects_launches_it_cannot_hold():
