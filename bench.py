@@ -11,7 +11,7 @@ torch CPU decode path (gather + GQA expand + masked SDPA) timed on a bounded
 sample of the same workload on this host (cpu_baseline).
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 10]
-    python bench.py --workload mixed|int8|decode-dist|append|swap|copy|rope|
+    python bench.py --workload mixed|mixed16|int8|decode-dist|append|swap|copy|rope|
                      decode-graph|offload-overlap|pd-wire      (extra lines)
 """
 from __future__ import annotations
@@ -41,9 +41,12 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="decode",
                     choices=["decode", "decode-dist", "decode-tp2", "decode-cold", "cfg1",
-                             "p15-grid", "int8", "mixed", "append", "swap", "copy", "rope",
-                             "decode-graph", "offload-overlap", "pd-wire"])
+                             "p15-grid", "int8", "mixed", "mixed16", "append", "swap", "copy",
+                             "rope", "decode-graph", "offload-overlap", "pd-wire"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--mixed-call-only", action="store_true",
+                    help="mixed workloads: run only the hinted call in every timed slot (for "
+                         "kernel traces of that call; the other fields then repeat it)")
     ap.add_argument("--cpu-sample", type=int, default=0,
                     help="sequences of the workload the CPU baseline runs (default: 64 of "
                          "the bf16 decode batch, 2 of the 32k-context int8 batch)")
@@ -514,18 +517,28 @@ def run_p15_grid(args, torch):
     }
 
 
-def run_mixed(args, torch):
-    from nanovllm_amd.kernels.varlen import varlen_attention
+MIXES = {
+    # name: (decode rows, their context range, prefill chunks as (prefix, tokens))
+    "mixed": (60, (256, 4096), [(0, 256), (512, 256), (2048, 256), (8192, 256)]),
+    "mixed16": (16, (256, 4096), [(0, 512), (512, 512), (2048, 512), (8192, 512)]),
+}
+
+
+def run_mixed(args, torch, mix="mixed"):
+    from nanovllm_amd.kernels.varlen import (varlen_attention, varlen_attention_append,
+                                             varlen_decode_cus)
+    from nanovllm_amd.layers.attention import store_kvcache
     from nanovllm_amd.workloads import build_block_tables, uniform_lengths
 
     dev = torch.device("cuda:0")
     heads, kvh = 32, 4
-    dec = uniform_lengths(60, 256, 4096, seed=3)
-    chunks = [(0, 256), (512, 256), (2048, 256), (8192, 256)]
+    n_dec, (lo, hi), chunks = MIXES[mix]
+    dec = uniform_lengths(n_dec, lo, hi, seed=3)
     all_lens = dec + [p + c for p, c in chunks]
     g = torch.Generator().manual_seed(4)
     blocks = sum((n + 255) // 256 for n in all_lens) + 8
-    bt = build_block_tables(all_lens, blocks, 256, g).to(dev)
+    bt_cpu = build_block_tables(all_lens, blocks, 256, g)
+    bt = bt_cpu.to(dev)
     dg = torch.Generator(device=dev).manual_seed(5)
     kc = torch.randn(blocks, 256, kvh, 128, generator=dg, device=dev, dtype=torch.bfloat16)
     vc = torch.randn(blocks, 256, kvh, 128, generator=dg, device=dev, dtype=torch.bfloat16)
@@ -538,12 +551,32 @@ def run_mixed(args, torch):
     dlen = torch.tensor(dec, dtype=torch.int32, device=dev)
     cq = torch.tensor(cu_q, dtype=torch.int32, device=dev)
     ck = torch.tensor(cu_k, dtype=torch.int32, device=dev)
+    # The step's new rows: decode row i at its last position, chunk j's tokens
+    # at positions prefix_j .. prefix_j + c_j - 1.
+    slots = [int(bt_cpu[i, (n - 1) // 256]) * 256 + (n - 1) % 256 for i, n in enumerate(dec)]
+    for j, (p, c) in enumerate(chunks):
+        row = len(dec) + j
+        slots += [int(bt_cpu[row, t // 256]) * 256 + t % 256 for t in range(p, p + c)]
+    slot_t = torch.tensor(slots, dtype=torch.int32, device=dev)
+    kv_new = torch.randn(T, 2, kvh, 128, generator=dg, device=dev, dtype=torch.bfloat16)
+    key, value = kv_new[:, 0], kv_new[:, 1]
+    kw = dict(scale=128 ** -0.5, block_tables=bt, num_decode_rows=len(dec),
+              decode_context_lens=dlen, cu_seqlens_q=cq, cu_seqlens_k=ck,
+              cu_seqlens_q_list=cu_q, cu_seqlens_k_list=cu_k)
 
     def call():
-        return varlen_attention(q, kc, vc, scale=128 ** -0.5, block_tables=bt,
-                                num_decode_rows=len(dec), decode_context_lens=dlen,
-                                cu_seqlens_q=cq, cu_seqlens_k=ck, cu_seqlens_q_list=cu_q,
-                                cu_seqlens_k_list=cu_k)
+        return varlen_attention(q, kc, vc, decode_context_lens_list=dec, **kw)
+
+    def call_unhinted():
+        return varlen_attention(q, kc, vc, **kw)
+
+    def step_store_then_call():
+        store_kvcache(key, value, kc, vc, slot_t)
+        return varlen_attention(q, kc, vc, decode_context_lens_list=dec, **kw)
+
+    def step_append():
+        return varlen_attention_append(q, key, value, kc, vc, slot_t,
+                                       decode_context_lens_list=dec, **kw)
 
     # The same prefill rows alone (their block-table rows and queries), to
     # price the prefill launch against the MFMA roofline.
@@ -555,30 +588,41 @@ def run_mixed(args, torch):
                                 cu_seqlens_q=cq, cu_seqlens_k=ck, cu_seqlens_q_list=cu_q,
                                 cu_seqlens_k_list=cu_k)
 
-    def timed(fn):
-        for _ in range(args.warmup):
+    # Every form is timed in each step, one after the other, so that all see
+    # the same clocks and caches (a form timed alone after another one ran
+    # at a different clock state).
+    forms = [call, call_unhinted, step_store_then_call, step_append, call_prefill]
+    if args.mixed_call_only:
+        forms = [call] * len(forms)  # kernel traces of the hinted call alone
+    for _ in range(args.warmup):
+        for fn in forms:
             fn()
-        torch.cuda.synchronize()
-        timer = EventTimer(torch)
-        for _ in range(args.steps):
+    torch.cuda.synchronize()
+    timers = [EventTimer(torch) for _ in forms]
+    for _ in range(args.steps):
+        for fn, timer in zip(forms, timers):
             s = timer.start()
             fn()
             timer.stop(s)
-        torch.cuda.synchronize()
-        return timer.mean_ms()
-
-    ms = timed(call)
-    ms_pre = timed(call_prefill)
+    torch.cuda.synchronize()
+    ms, ms_unhinted, ms_step_store, ms_step_append, ms_pre = (t.mean_ms() for t in timers)
     flops = 0
     for p, c in chunks:
         for r in range(c):
             flops += 4 * 128 * heads * (p + r + 1)
     kv = sum(dec) * 2 * kvh * 128 * 2
     pre_tflops = flops / (ms_pre * 1e-3) / 1e12
-    res = {"workload": "mixed: 60 decode rows ctx U[256,4096] + 4x256-token prefill chunks "
-                        "(prefix 0/512/2048/8192): one launch over a CU split (stream-K decode "
-                        "+ stream-K prefill) + one merge launch",
-            "ms": round(ms, 4), "prefill_gflop": round(flops / 1e9, 2),
+    split = varlen_decode_cus(nd, T - nd, heads, kvh, dec, cu_q, cu_k)
+    chunk_desc = "/".join(str(p) for p, _ in chunks)
+    res = {"workload": f"{mix}: {nd} decode rows ctx U[{lo},{hi}] + {len(chunks)}x"
+                       f"{chunks[0][1]}-token prefill chunks (prefix {chunk_desc}): one launch "
+                       "over a CU split sized from the host's work hints (stream-K decode + "
+                       "stream-K prefill) + one merge launch",
+            "ms": round(ms, 4), "decode_cus": split,
+            "ms_fixed_3_8_split": round(ms_unhinted, 4),
+            "step_store_then_call_ms": round(ms_step_store, 4),
+            "step_append_ms": round(ms_step_append, 4),
+            "prefill_gflop": round(flops / 1e9, 2),
             "prefill_only_ms": round(ms_pre, 4),
             "prefill_TFLOPs": round(pre_tflops, 1),
             "prefill_mfma_frac": round(pre_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
@@ -1032,8 +1076,8 @@ def main():
                          int8=args.workload == "int8")
     elif args.workload == "p15-grid":
         res = run_p15_grid(args, torch)
-    elif args.workload == "mixed":
-        res = run_mixed(args, torch)
+    elif args.workload in MIXES:
+        res = run_mixed(args, torch, args.workload)
     elif args.workload == "append":
         res = run_append(args, torch)
     elif args.workload == "copy":

@@ -309,7 +309,14 @@ int64_t kvc_varlen_prefill_units(const int32_t* cu_q_host, const int32_t* cu_k_h
  *     prefix cache, attention.py:195-199), from the bf16 k_fresh/v_fresh
  *     [tokens, KVH, D] rows cu_seqlens_k[i] .. (then num_decode_rows == 0).
  * cu_seqlens_q/k are int32 device arrays of num_prefill + 1 entries;
- * num_prefill_units comes from kvc_varlen_prefill_units. */
+ * num_prefill_units comes from kvc_varlen_prefill_units.
+ * decode_ctx_tokens and prefill_kq_pairs are host-side hints (0: none) that
+ * size the two sides of the one-launch form over a bf16 pool: the sum of the
+ * decode rows' context lengths (the runner holds them as ints,
+ * nanovllm/engine/model_runner.py:595-674) and the prefill's query-key pairs
+ * per head, sum over chunks of sq_i (sk_i - sq_i) + sq_i (sq_i + 1) / 2; see
+ * kvc_varlen_decode_cus.  They change the work split, never the result
+ * beyond floating-point summation order. */
 int kvc_varlen_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h,
                          int64_t num_q_tokens, int64_t num_heads,
                          const void* k_cache, const void* v_cache, int64_t num_cache_blocks,
@@ -323,9 +330,45 @@ int kvc_varlen_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h,
                          int64_t num_decode_rows, const int32_t* decode_context_lens,
                          int64_t num_prefill, const int32_t* cu_seqlens_q,
                          const int32_t* cu_seqlens_k, int64_t num_prefill_units,
-                         int64_t max_seqlen_k, float scale, void* out, int64_t out_stride_t,
-                         int64_t out_stride_h, void* workspace, size_t workspace_bytes,
-                         kvc_stream_t stream);
+                         int64_t max_seqlen_k, int64_t decode_ctx_tokens,
+                         int64_t prefill_kq_pairs, float scale, void* out,
+                         int64_t out_stride_t, int64_t out_stride_h, void* workspace,
+                         size_t workspace_bytes, kvc_stream_t stream);
+
+/* The step's store and the mixed call together, over a bf16 pool: replaces
+ * store_kvcache (nanovllm/layers/attention.py:138-140) followed by the mixed
+ * / prefill branches (:146-173).  Row t of key / value ([T, KVH, D] bf16,
+ * element strides, 16-byte rows) goes to pool slot slot_mapping[t] (int32 or
+ * int64, kvc_store_kv's slot rules) for every query row t; then attention as
+ * kvc_varlen_attention (same rows, tables, hints and workspace).  The prefill
+ * rows' k/v are stored by one launch ahead of the attention (the prefill
+ * reads them back from the pool); the decode rows' k/v are appended inside
+ * the decode launch (or the decode side of the one-launch form), as
+ * kvc_paged_decode_append does, so a decode row's slot must be position
+ * decode_context_lens[i] - 1 of its own table row. */
+int kvc_varlen_attention_append(
+    const void* q, int64_t q_stride_t, int64_t q_stride_h, int64_t num_q_tokens,
+    int64_t num_heads, const void* key, int64_t key_stride_t, int64_t key_stride_h,
+    const void* value, int64_t value_stride_t, int64_t value_stride_h,
+    const void* slot_mapping, int slot_index_bytes, void* k_cache, void* v_cache,
+    int64_t num_cache_blocks, int64_t page_size, int64_t num_kv_heads, int64_t head_dim,
+    const int32_t* block_tables, int64_t bt_stride, int64_t max_blocks_per_seq,
+    int64_t num_decode_rows, const int32_t* decode_context_lens, int64_t num_prefill,
+    const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int64_t num_prefill_units,
+    int64_t max_seqlen_k, int64_t decode_ctx_tokens, int64_t prefill_kq_pairs, float scale,
+    void* out, int64_t out_stride_t, int64_t out_stride_h, void* workspace,
+    size_t workspace_bytes, kvc_stream_t stream);
+
+/* CUs the decode side of a mixed call's one-launch form gets for these sizes
+ * and hints (0: the decode launch and the prefill launch run in turn).  No
+ * reference counterpart (the reference runs the two sub-paths in turn,
+ * nanovllm/layers/attention.py:146-166).  With both hints the split follows
+ * the two sides' CU-time at their measured per-CU rates; without, 3/8 of the
+ * CUs; KVC_MIXED_DECODE_CUS overrides.  Host only: reads the device's CU
+ * count (256 when no device is visible). */
+int kvc_varlen_decode_cus(int64_t num_decode_rows, int64_t num_prefill_tokens, int64_t num_heads,
+                          int64_t num_kv_heads, int kv_dtype, int64_t decode_ctx_tokens,
+                          int64_t prefill_kq_pairs);
 
 /* ---------------------------------------------------------------------------
  * Dequantise gathered int8 rows (the torch-side read path).

@@ -4469,19 +4469,30 @@ bool split_mixed(int64_t num_decode_rows, int64_t page_size) {
   return num_decode_rows > 0 && page_size > 0;
 }
 
+// Per-CU rates of the two sides of a mixed launch, measured on MI355X with
+// the other side idle and each side held to n workgroups (n = 16 .. 192; the
+// time of a side fits c + work / n there): the LDS-staged decode streams
+// about 41 GB/s of bf16 K/V per CU, the stream-K prefill about 4.3 TFLOP/s
+// per CU.
+constexpr double kMixDecodeBytesPerCuUs = 41.0e3;
+constexpr double kMixPrefillFlopsPerCuUs = 4.3e6;
+
 // Workgroups (= CUs) the decode side of a mixed call's split launch gets
-// (mixed_split_kernel: decode rows on dec_wgs CUs, prefill rows on the rest
+// (mixed_split_kernel: decode rows on that many CUs, prefill rows on the rest
 // at once; 0: the decode launch, then the prefill launch).  The split form
 // needs both sides in their stream-K forms: a bf16 pool with 4 kv heads per
 // decode workgroup (LDS-staged) and the stream-K prefill.
-// KVC_MIXED_DECODE_CUS sets the count (rounded down to a multiple of 8; 0:
-// the two launches one after the other).  By default the decode side gets
-// 3/8 of the CUs: the decode rows are HBM-bound and keep most of their rate
-// on fewer CUs, the prefill is MFMA-bound and scales with its CUs (on a mix
-// of 60 decode rows of U[256,4096] and four 256-token chunks the two sides
-// then take about the same time).
+// With the host's hints (the decode rows' total context in tokens, and the
+// prefill's query-key pairs per head: sum over chunks of
+// sq (sk - sq) + sq (sq + 1) / 2), the CUs split in proportion to the two
+// sides' CU-time at the rates above, so that both end together (rounded to
+// a multiple of 8, at least 8 on each side).  Without hints the decode side
+// gets 3/8 of the CUs, the balance of 60 decode rows of U[256,4096] and four
+// 256-token chunks.  KVC_MIXED_DECODE_CUS overrides both (rounded down to a
+// multiple of 8; 0: the two launches one after the other).
 int mixed_decode_cus(int64_t num_decode_rows, int64_t num_prefill_tokens, int kv_dtype,
-                     int64_t num_heads, int64_t num_kv_heads) {
+                     int64_t num_heads, int64_t num_kv_heads, int64_t decode_ctx_tokens,
+                     int64_t prefill_kq_pairs) {
   if (num_decode_rows <= 0 || num_prefill_tokens <= 0) return 0;
   if (kv_dtype != KVC_KV_BF16 || env_int("KVC_DECODE_STREAMK", 1) == 0 ||
       env_int("KVC_DECODE_LDS", 1) == 0 || env_int("KVC_PREFILL_SK", 1) == 0)
@@ -4491,7 +4502,18 @@ int mixed_decode_cus(int64_t num_decode_rows, int64_t num_prefill_tokens, int kv
   const int total = device_cus();
   if (total < 16 || total % 8 != 0) return 0;
   int n = env_int("KVC_MIXED_DECODE_CUS", -1);
-  if (n < 0) n = total * 3 / 8;
+  if (n < 0) {
+    if (decode_ctx_tokens > 0 && prefill_kq_pairs > 0) {
+      const double dec = double(decode_ctx_tokens) * double(num_kv_heads) * (2.0 * kD * 2.0) /
+                         kMixDecodeBytesPerCuUs;
+      const double pre =
+          4.0 * kD * double(num_heads) * double(prefill_kq_pairs) / kMixPrefillFlopsPerCuUs;
+      n = int(std::lround(double(total) * dec / (dec + pre) / 8.0)) * 8;
+      n = std::min(std::max(n, 8), total - 8);
+    } else {
+      n = total * 3 / 8;
+    }
+  }
   n = n / 8 * 8;
   return (n >= 8 && n <= total - 8) ? n : 0;
 }
@@ -4728,7 +4750,9 @@ int paged_decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, con
         if (rc != KVC_OK) return rc;
       }
     }
-    if (tl_record != nullptr && lds4 && p.app_k == nullptr) {
+    // (mixed_split_kernel's decode side is this launch's kernel, the append
+    // included.)
+    if (tl_record != nullptr && lds4) {
       tl_record->taken = true;
       tl_record->p = p;
       tl_record->grid = sp.grid;
@@ -4966,7 +4990,11 @@ extern "C" size_t kvc_varlen_workspace_bytes(int64_t num_q_tokens, int64_t num_h
   return units;
 }
 
-extern "C" int kvc_varlen_attention(
+namespace {
+// kvc_varlen_attention with the decode rows' append (app.key null: none; rows
+// [0, num_decode_rows) of app's key / value / slot_mapping) and the split
+// hints of mixed_decode_cus.
+int varlen_impl(
     const void* q, int64_t q_stride_t, int64_t q_stride_h, int64_t num_q_tokens,
     int64_t num_heads, const void* k_cache, const void* v_cache, int64_t num_cache_blocks,
     int64_t page_size, int64_t num_kv_heads, int64_t head_dim, int kv_dtype,
@@ -4976,9 +5004,9 @@ extern "C" int kvc_varlen_attention(
     int64_t vf_stride_h, const int32_t* block_tables, int64_t bt_stride,
     int64_t max_blocks_per_seq, int64_t num_decode_rows, const int32_t* decode_context_lens,
     int64_t num_prefill, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
-    int64_t num_prefill_units, int64_t max_seqlen_k, float scale, void* out,
-    int64_t out_stride_t, int64_t out_stride_h, void* workspace, size_t workspace_bytes,
-    kvc_stream_t stream) {
+    int64_t num_prefill_units, int64_t max_seqlen_k, int64_t decode_ctx_tokens,
+    int64_t prefill_kq_pairs, float scale, void* out, int64_t out_stride_t, int64_t out_stride_h,
+    void* workspace, size_t workspace_bytes, const DecodeAppend& app, kvc_stream_t stream) {
   clear_error();
   KVC_REQUIRE(head_dim == kD, KVC_ERR_VALUE, "varlen_attention: head_dim must be 128 (got %lld)",
               (long long)head_dim);
@@ -5029,7 +5057,8 @@ extern "C" int kvc_varlen_attention(
                 dec_span + pre_ws, workspace_bytes);
     char* ws = static_cast<char*>(workspace);
     const int64_t nd = num_decode_rows;
-    const int dec_cus = mixed_decode_cus(nd, num_q_tokens - nd, kv_dtype, num_heads, num_kv_heads);
+    const int dec_cus = mixed_decode_cus(nd, num_q_tokens - nd, kv_dtype, num_heads, num_kv_heads,
+                                         decode_ctx_tokens, prefill_kq_pairs);
     if (dec_cus > 0) {
       // One launch over a static CU split (mixed_split_kernel): the decode
       // rows planned for dec_cus workgroups, the prefill rows for the rest,
@@ -5039,26 +5068,26 @@ extern "C" int kvc_varlen_attention(
       {
         LaunchCus cus(dec_cus);
         RecordInto rec(&rd);
-        rc = kvc_paged_decode(q, q_stride_t, q_stride_h, k_cache, v_cache, num_cache_blocks,
-                              page_size, num_kv_heads, head_dim, kv_dtype, k_scale, v_scale,
-                              side_k, side_v, out_idx2d, head_n_out, n_out_max, block_tables,
-                              bt_stride, max_blocks_per_seq, decode_context_lens, nd, num_heads,
-                              scale, out, out_stride_t, out_stride_h, dec_ws ? ws : nullptr,
-                              dec_ws, stream);
+        rc = paged_decode_impl(q, q_stride_t, q_stride_h, k_cache, v_cache, num_cache_blocks,
+                               page_size, num_kv_heads, head_dim, kv_dtype, k_scale, v_scale,
+                               side_k, side_v, out_idx2d, head_n_out, n_out_max, block_tables,
+                               bt_stride, max_blocks_per_seq, decode_context_lens, nd, num_heads,
+                               scale, out, out_stride_t, out_stride_h, dec_ws ? ws : nullptr,
+                               dec_ws, app, stream);
       }
       if (rc != KVC_OK) return rc;
       {
         LaunchCus cus(device_cus() - dec_cus);
         RecordInto rec(&rp);
-        rc = kvc_varlen_attention(
+        rc = varlen_impl(
             static_cast<const uint16_t*>(q) + nd * q_stride_t, q_stride_t, q_stride_h,
             num_q_tokens - nd, num_heads, k_cache, v_cache, num_cache_blocks, page_size,
             num_kv_heads, head_dim, kv_dtype, k_scale, v_scale, side_k, side_v, out_idx2d,
             head_n_out, n_out_max, nullptr, 0, 0, nullptr, 0, 0, block_tables + nd * bt_stride,
             bt_stride, max_blocks_per_seq, 0, nullptr, num_prefill, cu_seqlens_q, cu_seqlens_k,
-            num_prefill_units, max_seqlen_k, scale,
+            num_prefill_units, max_seqlen_k, 0, 0, scale,
             static_cast<uint16_t*>(out) + nd * out_stride_t, out_stride_t, out_stride_h,
-            pre_ws ? ws + dec_span : nullptr, pre_ws, stream);
+            pre_ws ? ws + dec_span : nullptr, pre_ws, DecodeAppend{}, stream);
       }
       if (rc != KVC_OK) return rc;
       if (rd.taken && rp.taken) {
@@ -5087,21 +5116,22 @@ extern "C" int kvc_varlen_attention(
       }
       return check_launch("varlen_attention merge");
     }
-    rc = kvc_paged_decode(q, q_stride_t, q_stride_h, k_cache, v_cache, num_cache_blocks,
-                          page_size, num_kv_heads, head_dim, kv_dtype, k_scale, v_scale, side_k,
-                          side_v, out_idx2d, head_n_out, n_out_max, block_tables, bt_stride,
-                          max_blocks_per_seq, decode_context_lens, num_decode_rows, num_heads,
-                          scale, out, out_stride_t, out_stride_h, dec_ws ? ws : nullptr, dec_ws,
-                          stream);
+    rc = paged_decode_impl(q, q_stride_t, q_stride_h, k_cache, v_cache, num_cache_blocks,
+                           page_size, num_kv_heads, head_dim, kv_dtype, k_scale, v_scale, side_k,
+                           side_v, out_idx2d, head_n_out, n_out_max, block_tables, bt_stride,
+                           max_blocks_per_seq, decode_context_lens, num_decode_rows, num_heads,
+                           scale, out, out_stride_t, out_stride_h, dec_ws ? ws : nullptr, dec_ws,
+                           app, stream);
     if (rc != KVC_OK || num_q_tokens == num_decode_rows) return rc;
-    return kvc_varlen_attention(
+    return varlen_impl(
         static_cast<const uint16_t*>(q) + nd * q_stride_t, q_stride_t, q_stride_h,
         num_q_tokens - nd, num_heads, k_cache, v_cache, num_cache_blocks, page_size,
         num_kv_heads, head_dim, kv_dtype, k_scale, v_scale, side_k, side_v, out_idx2d,
         head_n_out, n_out_max, nullptr, 0, 0, nullptr, 0, 0, block_tables + nd * bt_stride,
         bt_stride, max_blocks_per_seq, 0, nullptr, num_prefill, cu_seqlens_q, cu_seqlens_k,
-        num_prefill_units, max_seqlen_k, scale, static_cast<uint16_t*>(out) + nd * out_stride_t,
-        out_stride_t, out_stride_h, pre_ws ? ws + dec_span : nullptr, pre_ws, stream);
+        num_prefill_units, max_seqlen_k, 0, 0, scale,
+        static_cast<uint16_t*>(out) + nd * out_stride_t, out_stride_t, out_stride_h,
+        pre_ws ? ws + dec_span : nullptr, pre_ws, DecodeAppend{}, stream);
   }
 
   // Prefill rows only from here: decode rows went to the paged decode above
@@ -5208,6 +5238,91 @@ extern "C" int kvc_varlen_attention(
     rc = check_launch("varlen_attention merge");
   }
   return rc;
+}
+
+}  // namespace
+
+extern "C" int kvc_varlen_attention(
+    const void* q, int64_t q_stride_t, int64_t q_stride_h, int64_t num_q_tokens,
+    int64_t num_heads, const void* k_cache, const void* v_cache, int64_t num_cache_blocks,
+    int64_t page_size, int64_t num_kv_heads, int64_t head_dim, int kv_dtype,
+    const float* k_scale, const float* v_scale, const void* side_k, const void* side_v,
+    const int32_t* out_idx2d, const int32_t* head_n_out, int64_t n_out_max, const void* k_fresh,
+    int64_t kf_stride_t, int64_t kf_stride_h, const void* v_fresh, int64_t vf_stride_t,
+    int64_t vf_stride_h, const int32_t* block_tables, int64_t bt_stride,
+    int64_t max_blocks_per_seq, int64_t num_decode_rows, const int32_t* decode_context_lens,
+    int64_t num_prefill, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+    int64_t num_prefill_units, int64_t max_seqlen_k, int64_t decode_ctx_tokens,
+    int64_t prefill_kq_pairs, float scale, void* out, int64_t out_stride_t, int64_t out_stride_h,
+    void* workspace, size_t workspace_bytes, kvc_stream_t stream) {
+  return varlen_impl(q, q_stride_t, q_stride_h, num_q_tokens, num_heads, k_cache, v_cache,
+                     num_cache_blocks, page_size, num_kv_heads, head_dim, kv_dtype, k_scale,
+                     v_scale, side_k, side_v, out_idx2d, head_n_out, n_out_max, k_fresh,
+                     kf_stride_t, kf_stride_h, v_fresh, vf_stride_t, vf_stride_h, block_tables,
+                     bt_stride, max_blocks_per_seq, num_decode_rows, decode_context_lens,
+                     num_prefill, cu_seqlens_q, cu_seqlens_k, num_prefill_units, max_seqlen_k,
+                     decode_ctx_tokens, prefill_kq_pairs, scale, out, out_stride_t, out_stride_h,
+                     workspace, workspace_bytes, DecodeAppend{}, stream);
+}
+
+// The step's store and the mixed call together (bf16 pool): the prefill rows'
+// k/v go to their slots first (one store launch: the prefill attention reads
+// them back from the pool), then the call runs as kvc_varlen_attention with
+// the decode rows' k/v appended inside the decode launch (or the decode side
+// of the split launch), as kvc_paged_decode_append does.
+extern "C" int kvc_varlen_attention_append(
+    const void* q, int64_t q_stride_t, int64_t q_stride_h, int64_t num_q_tokens,
+    int64_t num_heads, const void* key, int64_t key_stride_t, int64_t key_stride_h,
+    const void* value, int64_t value_stride_t, int64_t value_stride_h,
+    const void* slot_mapping, int slot_index_bytes, void* k_cache, void* v_cache,
+    int64_t num_cache_blocks, int64_t page_size, int64_t num_kv_heads, int64_t head_dim,
+    const int32_t* block_tables, int64_t bt_stride, int64_t max_blocks_per_seq,
+    int64_t num_decode_rows, const int32_t* decode_context_lens, int64_t num_prefill,
+    const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int64_t num_prefill_units,
+    int64_t max_seqlen_k, int64_t decode_ctx_tokens, int64_t prefill_kq_pairs, float scale,
+    void* out, int64_t out_stride_t, int64_t out_stride_h, void* workspace,
+    size_t workspace_bytes, kvc_stream_t stream) {
+  clear_error();
+  KVC_REQUIRE(key != nullptr && value != nullptr && slot_mapping != nullptr, KVC_ERR_VALUE,
+              "varlen_attention_append: key, value and slot_mapping are required");
+  KVC_REQUIRE(slot_index_bytes == 4 || slot_index_bytes == 8, KVC_ERR_VALUE,
+              "varlen_attention_append: slot_mapping must be int32 or int64");
+  KVC_REQUIRE(block_tables != nullptr && k_cache != nullptr && v_cache != nullptr, KVC_ERR_VALUE,
+              "varlen_attention_append: a paged pool and block_tables are required");
+  KVC_REQUIRE(num_decode_rows >= 0 && num_decode_rows <= num_q_tokens, KVC_ERR_VALUE,
+              "varlen_attention_append: fewer query rows than decode rows");
+  KVC_REQUIRE(page_size > 0 && num_cache_blocks >= 0, KVC_ERR_VALUE,
+              "varlen_attention_append: bad pool shape");
+  const int64_t nd = num_decode_rows;
+  if (num_q_tokens > nd) {
+    const int rc = kvc_store_kv(
+        static_cast<const uint16_t*>(key) + nd * key_stride_t, key_stride_t, key_stride_h,
+        static_cast<const uint16_t*>(value) + nd * value_stride_t, value_stride_t,
+        value_stride_h, k_cache, v_cache, num_cache_blocks * page_size,
+        static_cast<const char*>(slot_mapping) + nd * slot_index_bytes, slot_index_bytes,
+        num_q_tokens - nd, num_kv_heads, head_dim, 2, stream);
+    if (rc != KVC_OK) return rc;
+  }
+  const DecodeAppend app{key, key_stride_t, key_stride_h, value, value_stride_t, value_stride_h,
+                         slot_mapping, slot_index_bytes};
+  return varlen_impl(q, q_stride_t, q_stride_h, num_q_tokens, num_heads, k_cache, v_cache,
+                     num_cache_blocks, page_size, num_kv_heads, head_dim, KVC_KV_BF16, nullptr,
+                     nullptr, nullptr, nullptr, nullptr, nullptr, 0, nullptr, 0, 0, nullptr, 0,
+                     0, block_tables, bt_stride, max_blocks_per_seq, num_decode_rows,
+                     decode_context_lens, num_prefill, cu_seqlens_q, cu_seqlens_k,
+                     num_prefill_units, max_seqlen_k, decode_ctx_tokens, prefill_kq_pairs, scale,
+                     out, out_stride_t, out_stride_h, workspace, workspace_bytes,
+                     nd > 0 ? app : DecodeAppend{}, stream);
+}
+
+// Decode CUs of a mixed call's split launch for these sizes and hints (0: the
+// decode launch, then the prefill launch).
+extern "C" int kvc_varlen_decode_cus(int64_t num_decode_rows, int64_t num_prefill_tokens,
+                                     int64_t num_heads, int64_t num_kv_heads, int kv_dtype,
+                                     int64_t decode_ctx_tokens, int64_t prefill_kq_pairs) {
+  if (num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads != 0) return 0;
+  return mixed_decode_cus(num_decode_rows, num_prefill_tokens, kv_dtype, num_heads, num_kv_heads,
+                          decode_ctx_tokens, prefill_kq_pairs);
 }
 
 // Number of prefill workgroups for the given chunk lengths (host arrays of

@@ -22,4 +22,4 @@ void clear_error() { g_last_error[0] = '\0'; }
 
 extern "C" const char* kvc_last_error(void) { return kvc::g_last_error; }
 
-extern "C" int kvc_abi_version(void) { return 1; }
+extern "C" int kvc_abi_version(void) { return 2; }

@@ -71,7 +71,14 @@ SIGNATURES = {
     "kvc_varlen_attention": (_INT, [_P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _I64,
                                     _I64, _INT, _P, _P, _P, _P, _P, _P, _I64, _P, _I64,
                                     _I64, _P, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64,
-                                    _P, _P, _I64, _I64, _F32, _P, _I64, _I64, _P, _SZ, _P]),
+                                    _P, _P, _I64, _I64, _I64, _I64, _F32, _P, _I64, _I64, _P,
+                                    _SZ, _P]),
+    "kvc_varlen_attention_append": (_INT, [_P, _I64, _I64, _I64, _I64, _P, _I64, _I64, _P,
+                                           _I64, _I64, _P, _INT, _P, _P, _I64, _I64, _I64,
+                                           _I64, _P, _I64, _I64, _I64, _P, _I64, _P, _P, _I64,
+                                           _I64, _I64, _I64, _F32, _P, _I64, _I64, _P, _SZ,
+                                           _P]),
+    "kvc_varlen_decode_cus": (_INT, [_I64, _I64, _I64, _I64, _INT, _I64, _I64]),
     "kvc_dequant_chan": (_INT, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P]),
     "kvc_dequant_tokhead": (_INT, [_P, _P, _I64, _I64, _I64, _P, _P]),
     "kvc_block_gather": (_INT, [_P, _I64, _I64, _I64, _P, _I64, _P, _I64, _I64, _P]),

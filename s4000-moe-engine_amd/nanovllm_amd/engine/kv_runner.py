@@ -452,7 +452,8 @@ class KVCacheRunner:
                         cu_seqlens_q_list=cu_q, cu_seqlens_k_list=cu_k, is_mixed=True,
                         num_decode_rows=n_dec,
                         decode_context_lens=self._h2d(dec_lens, torch.int32),
-                        decode_max_context_len=max(dec_lens) if dec_lens else 0)
+                        decode_max_context_len=max(dec_lens) if dec_lens else 0,
+                        decode_context_lens_list=dec_lens)
         else:
             set_context(True, cu_q_t, cu_k_t, max_q, max_k, slot_t, None, block_tables,
                         cu_seqlens_q_list=cu_q, cu_seqlens_k_list=cu_k)

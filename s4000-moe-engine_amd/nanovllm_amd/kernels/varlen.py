@@ -26,104 +26,212 @@ def _host_list(lst, dev_tensor):
     return dev_tensor.tolist()   # host sync, as the reference does when lists are absent
 
 
-def varlen_attention(q, k_cache, v_cache, *, scale, block_tables=None,
-                     num_decode_rows=0, decode_context_lens=None,
-                     cu_seqlens_q=None, cu_seqlens_k=None,
-                     cu_seqlens_q_list=None, cu_seqlens_k_list=None,
-                     k=None, v=None,
-                     k_scale=None, v_scale=None, side_k=None, side_v=None,
-                     out_idx2d=None, head_n_out=None):
-    """q: [T, H, D] bf16 with T = num_decode_rows + prefill tokens.
-    k/v: the step's fresh [T_k, KVH, D] bf16 keys/values, used only when
-    block_tables is None (pure prefill without a prefix cache).
-    Returns out [T, H, D] bf16."""
+def _prefill_kq_pairs(cu_q, cu_k) -> int:
+    """Query-key pairs per head of the prefill chunks (the work hint of
+    kvc_varlen_attention): chunk i's query r sees sk - sq + r + 1 keys."""
+    pairs = 0
+    for i in range(len(cu_q) - 1):
+        sq = cu_q[i + 1] - cu_q[i]
+        sk = cu_k[i + 1] - cu_k[i]
+        if sq > 0 and sk > 0:
+            pairs += sq * (sk - sq) + sq * (sq + 1) // 2
+    return pairs
+
+
+class _Call:
+    """The checked, converted arguments shared by both entry points."""
+
+
+def _prepare(q, k_cache, v_cache, block_tables, num_decode_rows, decode_context_lens,
+             decode_context_lens_list, cu_seqlens_q, cu_seqlens_k, cu_seqlens_q_list,
+             cu_seqlens_k_list, k, v, k_scale):
+    c = _Call()
     T, num_heads, head_dim = q.shape
     if head_dim != 128:
         raise ValueError("varlen attention requires head_dim=128")
     if q.dtype != torch.bfloat16:
         raise ValueError(f"q must be bf16 (got {q.dtype})")
-    fresh = block_tables is None
-    if fresh:
+    c.fresh = block_tables is None
+    if c.fresh:
         if k is None or v is None:
             raise ValueError("without block_tables the keys come from k/v")
-        num_kv_heads = k.size(1)
-        page_size = 0
-        enc = nat.KVC_KV_BF16
+        c.num_kv_heads = k.size(1)
+        c.page_size = 0
+        c.enc = nat.KVC_KV_BF16
     else:
-        num_kv_heads = k_cache.size(2)
-        page_size = k_cache.size(1)
-        if page_size % 32:
+        c.num_kv_heads = k_cache.size(2)
+        c.page_size = k_cache.size(1)
+        if c.page_size % 32:
             raise ValueError("page_size must be a multiple of 32")
-        enc = _kv_encoding(k_cache, k_scale)
+        c.enc = _kv_encoding(k_cache, k_scale)
         assert k_cache.is_contiguous() and v_cache.is_contiguous()
-    if num_heads % num_kv_heads:
+    if num_heads % c.num_kv_heads:
         raise ValueError("num_heads must be a multiple of num_kv_heads")
     nat.require_device(q)
     if q.stride(2) != 1:
         q = q.contiguous()
-    out = torch.empty((T, num_heads, head_dim), dtype=q.dtype, device=q.device)
+    c.q = q
+    c.out = torch.empty((T, num_heads, head_dim), dtype=q.dtype, device=q.device)
+    c.T, c.num_heads, c.head_dim = T, num_heads, head_dim
     if T == 0:
-        return out
+        return c
 
     cu_q = _host_list(cu_seqlens_q_list, cu_seqlens_q) or [0]
     cu_k = _host_list(cu_seqlens_k_list, cu_seqlens_k) or [0]
-    num_prefill = len(cu_q) - 1
+    c.num_prefill = len(cu_q) - 1
     if num_decode_rows + cu_q[-1] != T:
         raise ValueError(f"{T} query rows but {num_decode_rows} decode rows + "
                          f"{cu_q[-1]} prefill tokens")
-    sq = [cu_q[i + 1] - cu_q[i] for i in range(num_prefill)]
-    sk = [cu_k[i + 1] - cu_k[i] for i in range(num_prefill)]
+    sq = [cu_q[i + 1] - cu_q[i] for i in range(c.num_prefill)]
+    sk = [cu_k[i + 1] - cu_k[i] for i in range(c.num_prefill)]
     for a, b in zip(sq, sk):
         if a > 0 and b < a:
             raise ValueError("a prefill chunk has fewer keys than queries")
-    max_seqlen_k = max(sk) if sk else 0
+    c.max_seqlen_k = max(sk) if sk else 0
     cu_q_np = np.asarray(cu_q, dtype=np.int32)
     cu_k_np = np.asarray(cu_k, dtype=np.int32)
-    pre_units = nat.query("kvc_varlen_prefill_units", cu_q_np.ctypes.data, cu_k_np.ctypes.data,
-                          num_prefill, num_heads, num_kv_heads, max_seqlen_k)
-    if num_prefill:
+    c.pre_units = nat.query("kvc_varlen_prefill_units", cu_q_np.ctypes.data, cu_k_np.ctypes.data,
+                            c.num_prefill, num_heads, c.num_kv_heads, c.max_seqlen_k)
+    if c.num_prefill:
         if cu_seqlens_q is None or cu_seqlens_q.device != q.device:
             cu_seqlens_q = torch.from_numpy(cu_q_np).to(q.device, non_blocking=True)
         if cu_seqlens_k is None or cu_seqlens_k.device != q.device:
             cu_seqlens_k = torch.from_numpy(cu_k_np).to(q.device, non_blocking=True)
         cu_seqlens_q = cu_seqlens_q.to(torch.int32).contiguous()
         cu_seqlens_k = cu_seqlens_k.to(torch.int32).contiguous()
+    c.cu_seqlens_q, c.cu_seqlens_k = cu_seqlens_q, cu_seqlens_k
+    # Work hints for the CU split of a mixed call (0: none).
+    c.decode_ctx_tokens = int(sum(decode_context_lens_list)) \
+        if num_decode_rows and decode_context_lens_list is not None else 0
+    c.prefill_kq_pairs = _prefill_kq_pairs(cu_q, cu_k) if num_decode_rows else 0
 
-    max_blocks = 0
-    if not fresh:
+    c.max_blocks = 0
+    if not c.fresh:
         if block_tables.dtype != torch.int32:
             block_tables = block_tables.to(torch.int32)
         if block_tables.stride(1) != 1:
             block_tables = block_tables.contiguous()
-        max_blocks = block_tables.size(1)
+        c.max_blocks = block_tables.size(1)
+    c.block_tables = block_tables
     if num_decode_rows:
         decode_context_lens = decode_context_lens.to(torch.int32).contiguous()
+    c.decode_context_lens = decode_context_lens
+    c.ws_bytes = nat.query("kvc_varlen_workspace_bytes", T, num_heads, c.num_kv_heads, head_dim,
+                           num_decode_rows, c.max_seqlen_k, c.page_size, c.max_blocks)
+    c.ws = nat.workspace(c.ws_bytes, q.device)
+    return c
+
+
+def varlen_attention(q, k_cache, v_cache, *, scale, block_tables=None,
+                     num_decode_rows=0, decode_context_lens=None,
+                     cu_seqlens_q=None, cu_seqlens_k=None,
+                     cu_seqlens_q_list=None, cu_seqlens_k_list=None,
+                     k=None, v=None,
+                     k_scale=None, v_scale=None, side_k=None, side_v=None,
+                     out_idx2d=None, head_n_out=None, decode_context_lens_list=None):
+    """q: [T, H, D] bf16 with T = num_decode_rows + prefill tokens.
+    k/v: the step's fresh [T_k, KVH, D] bf16 keys/values, used only when
+    block_tables is None (pure prefill without a prefix cache).
+    decode_context_lens_list: the decode rows' context lengths as host ints
+    (optional; with them a mixed call over a bf16 pool sizes its CU split to
+    the work of both sides).
+    Returns out [T, H, D] bf16."""
+    c = _prepare(q, k_cache, v_cache, block_tables, num_decode_rows, decode_context_lens,
+                 decode_context_lens_list, cu_seqlens_q, cu_seqlens_k, cu_seqlens_q_list,
+                 cu_seqlens_k_list, k, v, k_scale)
+    if c.T == 0:
+        return c.out
+    enc, fresh, q = c.enc, c.fresh, c.q
     has_side = enc == nat.KVC_KV_INT8_CHAN and side_k is not None and head_n_out is not None
     if enc == nat.KVC_KV_INT8_TOKHEAD:
         k_scale, v_scale = k_scale.contiguous(), v_scale.contiguous()
     elif enc == nat.KVC_KV_INT8_CHAN:
         k_scale = k_scale.to(torch.float32).contiguous()
         v_scale = v_scale.to(torch.float32).contiguous()
-    ws_bytes = nat.query("kvc_varlen_workspace_bytes", T, num_heads, num_kv_heads, head_dim,
-                         num_decode_rows, max_seqlen_k, page_size, max_blocks)
-    ws = nat.workspace(ws_bytes, q.device)
     nat.call(
         "kvc_varlen_attention",
-        q.data_ptr(), q.stride(0), q.stride(1), T, num_heads,
+        q.data_ptr(), q.stride(0), q.stride(1), c.T, c.num_heads,
         nat.ptr(k_cache) if not fresh else None, nat.ptr(v_cache) if not fresh else None,
-        k_cache.size(0) if not fresh else 0, page_size, num_kv_heads, head_dim, enc,
+        k_cache.size(0) if not fresh else 0, c.page_size, c.num_kv_heads, c.head_dim, enc,
         nat.ptr(k_scale), nat.ptr(v_scale),
         nat.ptr(side_k) if has_side else None, nat.ptr(side_v) if has_side else None,
         nat.ptr(out_idx2d) if has_side else None, nat.ptr(head_n_out) if has_side else None,
         side_k.size(-1) if has_side else 0,
         nat.ptr(k) if fresh else None, k.stride(0) if fresh else 0, k.stride(1) if fresh else 0,
         nat.ptr(v) if fresh else None, v.stride(0) if fresh else 0, v.stride(1) if fresh else 0,
-        nat.ptr(block_tables) if not fresh else None,
-        block_tables.stride(0) if not fresh else 0, max_blocks,
-        num_decode_rows, nat.ptr(decode_context_lens) if num_decode_rows else None,
-        num_prefill, nat.ptr(cu_seqlens_q) if num_prefill else None,
-        nat.ptr(cu_seqlens_k) if num_prefill else None, pre_units, max_seqlen_k,
-        float(scale), out.data_ptr(), out.stride(0), out.stride(1),
-        nat.ptr(ws), ws_bytes, nat.stream_of(q),
+        nat.ptr(c.block_tables) if not fresh else None,
+        c.block_tables.stride(0) if not fresh else 0, c.max_blocks,
+        num_decode_rows, nat.ptr(c.decode_context_lens) if num_decode_rows else None,
+        c.num_prefill, nat.ptr(c.cu_seqlens_q) if c.num_prefill else None,
+        nat.ptr(c.cu_seqlens_k) if c.num_prefill else None, c.pre_units, c.max_seqlen_k,
+        c.decode_ctx_tokens, c.prefill_kq_pairs,
+        float(scale), c.out.data_ptr(), c.out.stride(0), c.out.stride(1),
+        nat.ptr(c.ws), c.ws_bytes, nat.stream_of(q),
     )
-    return out
+    return c.out
+
+
+def varlen_attention_append(q, key, value, k_cache, v_cache, slot_mapping, *, scale,
+                            block_tables, num_decode_rows=0, decode_context_lens=None,
+                            cu_seqlens_q=None, cu_seqlens_k=None,
+                            cu_seqlens_q_list=None, cu_seqlens_k_list=None,
+                            decode_context_lens_list=None):
+    """store_kvcache(key, value, k_cache, v_cache, slot_mapping) followed by
+    varlen_attention over a bf16 pool (nanovllm/layers/attention.py:138-140,
+    :146-173), in kvc_varlen_attention_append: the prefill rows' k/v are
+    stored ahead of the attention, the decode rows' k/v are appended inside
+    the decode launch.  key / value [T, KVH, 128] bf16 (strided views of the
+    qkv projection are fine); slot_mapping [T] int32 or int64.  The decode
+    rows must use the engine's decode slots (row i's slot is position
+    decode_context_lens[i] - 1 of its own table row), as for
+    paged_decode_append.  Same results and pool contents as the two calls."""
+    if block_tables is None:
+        raise ValueError("varlen_attention_append needs a paged pool and block_tables")
+    if not (q.dtype == key.dtype == value.dtype == k_cache.dtype == torch.bfloat16):
+        raise ValueError("varlen_attention_append takes a bf16 pool and bf16 q/k/v")
+    if key.ndim != 3 or value.shape != key.shape or key.size(0) != q.size(0) \
+            or key.size(1) != k_cache.size(2) or slot_mapping.numel() != q.size(0):
+        raise ValueError("expected key/value=[T,kv_heads,dim] and slot_mapping=[T] for q=[T,...]")
+    assert key.stride(-1) == 1 and value.stride(-1) == 1
+    c = _prepare(q, k_cache, v_cache, block_tables, num_decode_rows, decode_context_lens,
+                 decode_context_lens_list, cu_seqlens_q, cu_seqlens_k, cu_seqlens_q_list,
+                 cu_seqlens_k_list, None, None, None)
+    if c.T == 0:
+        return c.out
+    nat.require_device(key, value, k_cache, v_cache, slot_mapping)
+    if slot_mapping.dtype == torch.int64:
+        sb = 8
+    else:
+        slot_mapping = slot_mapping.to(torch.int32)
+        sb = 4
+    slot_mapping = slot_mapping.contiguous()
+    q = c.q
+    nat.call(
+        "kvc_varlen_attention_append",
+        q.data_ptr(), q.stride(0), q.stride(1), c.T, c.num_heads,
+        key.data_ptr(), key.stride(0), key.stride(1),
+        value.data_ptr(), value.stride(0), value.stride(1),
+        slot_mapping.data_ptr(), sb,
+        k_cache.data_ptr(), v_cache.data_ptr(), k_cache.size(0), c.page_size, c.num_kv_heads,
+        c.head_dim, c.block_tables.data_ptr(), c.block_tables.stride(0), c.max_blocks,
+        num_decode_rows, nat.ptr(c.decode_context_lens) if num_decode_rows else None,
+        c.num_prefill, nat.ptr(c.cu_seqlens_q) if c.num_prefill else None,
+        nat.ptr(c.cu_seqlens_k) if c.num_prefill else None, c.pre_units, c.max_seqlen_k,
+        c.decode_ctx_tokens, c.prefill_kq_pairs,
+        float(scale), c.out.data_ptr(), c.out.stride(0), c.out.stride(1),
+        nat.ptr(c.ws), c.ws_bytes, nat.stream_of(q),
+    )
+    return c.out
+
+
+def varlen_decode_cus(num_decode_rows, num_prefill_tokens, num_heads, num_kv_heads,
+                      decode_context_lens_list=None, cu_seqlens_q_list=None,
+                      cu_seqlens_k_list=None, kv_dtype=nat.KVC_KV_BF16) -> int:
+    """CUs the decode side of a mixed call's one launch gets (0: the decode and
+    prefill launches run in turn), from the same hints varlen_attention
+    passes (kvc_varlen_decode_cus)."""
+    dec = int(sum(decode_context_lens_list)) if decode_context_lens_list is not None else 0
+    pairs = _prefill_kq_pairs(list(cu_seqlens_q_list), list(cu_seqlens_k_list)) \
+        if cu_seqlens_q_list is not None else 0
+    return nat.query("kvc_varlen_decode_cus", num_decode_rows, num_prefill_tokens, num_heads,
+                     num_kv_heads, kv_dtype, dec, pairs)

@@ -26,7 +26,7 @@ from .. import _native as nat
 from ..kernels.kv_int8 import store_kvcache_int8
 from ..kernels.paged_attention import (paged_decode_append, paged_decode_append_int8_tokhead,
                                        paged_decode_attention)
-from ..kernels.varlen import varlen_attention
+from ..kernels.varlen import varlen_attention, varlen_attention_append
 from ..utils.context import get_context
 from .rotary import qk_norm_rope_store
 
@@ -153,6 +153,26 @@ class Attention(nn.Module):
         fuse_append = (not kv_stored and not (context.is_mixed or context.is_prefill)
                        and bool(k_cache.numel() and v_cache.numel())
                        and (not self.kv_cache_is_int8 or self._int8_tokhead()))
+        # A mixed (or prefix-cached prefill) step on a bf16 pool stores and
+        # attends in one call: the decode rows append inside the decode launch.
+        varlen_append = (not kv_stored and (context.is_mixed or context.is_prefill)
+                         and context.block_tables is not None
+                         and bool(k_cache.numel() and v_cache.numel())
+                         and not self.kv_cache_is_int8)
+        if varlen_append:
+            with self._profile("attention.mixed" if context.is_mixed else "attention.prefill"):
+                return varlen_attention_append(
+                    q.view(-1, self.num_heads, self.head_dim),
+                    k.view(-1, self.num_kv_heads, self.head_dim),
+                    v.view(-1, self.num_kv_heads, self.head_dim), k_cache, v_cache,
+                    context.slot_mapping, scale=self.scale, block_tables=context.block_tables,
+                    num_decode_rows=context.num_decode_rows if context.is_mixed else 0,
+                    decode_context_lens=context.decode_context_lens if context.is_mixed else None,
+                    cu_seqlens_q=context.cu_seqlens_q, cu_seqlens_k=context.cu_seqlens_k,
+                    cu_seqlens_q_list=context.cu_seqlens_q_list,
+                    cu_seqlens_k_list=context.cu_seqlens_k_list,
+                    decode_context_lens_list=(context.decode_context_lens_list
+                                              if context.is_mixed else None))
         if k_cache.numel() and v_cache.numel() and not kv_stored and not fuse_append:
             with self._profile("attention.kv_store"):
                 if self.kv_cache_is_int8:
@@ -181,6 +201,8 @@ class Attention(nn.Module):
                     side_v=self.side_v if side else None,
                     out_idx2d=self.out_idx2d if side else None,
                     head_n_out=self.head_n_out if side else None,
+                    decode_context_lens_list=(context.decode_context_lens_list
+                                              if context.is_mixed else None),
                 )
         if fuse_append and self.kv_cache_is_int8:
             with self._profile("attention.paged_decode"):

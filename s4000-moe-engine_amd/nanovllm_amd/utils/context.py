@@ -3,7 +3,10 @@
 Same fields, order and setters as nanovllm/utils/context.py:5-50, so an engine
 that builds a Context for its own attention builds one for this attention too.
 All cu_seqlens fields are prefill-only in a mixed batch; decode rows carry
-their own context lengths (nanovllm/utils/context.py:21-28).
+their own context lengths (nanovllm/utils/context.py:21-28).  One field is
+added at the end: decode_context_lens_list, the decode rows' context lengths
+as host ints (the runner's dec_ctx_lens, nanovllm/engine/model_runner.py:
+597-602), which lets a mixed call size its CU split without a device read.
 """
 from dataclasses import dataclass
 
@@ -27,6 +30,7 @@ class Context:
     num_decode_rows: int = 0
     decode_context_lens: torch.Tensor | None = None
     decode_max_context_len: int = 0
+    decode_context_lens_list: list | None = None
 
 
 _CURRENT = Context()
@@ -40,7 +44,8 @@ def set_context(is_prefill, cu_seqlens_q=None, cu_seqlens_k=None, max_seqlen_q=0
                 slot_mapping=None, context_lens=None, block_tables=None, max_context_len=0,
                 cu_seqlens_q_list=None, cu_seqlens_k_list=None,
                 is_mixed=False, num_decode_rows=0,
-                decode_context_lens=None, decode_max_context_len=0):
+                decode_context_lens=None, decode_max_context_len=0,
+                decode_context_lens_list=None):
     global _CURRENT
     _CURRENT = Context(
         is_prefill=is_prefill,
@@ -58,6 +63,7 @@ def set_context(is_prefill, cu_seqlens_q=None, cu_seqlens_k=None, max_seqlen_q=0
         num_decode_rows=num_decode_rows,
         decode_context_lens=decode_context_lens,
         decode_max_context_len=decode_max_context_len,
+        decode_context_lens_list=decode_context_lens_list,
     )
 
 

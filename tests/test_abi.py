@@ -34,7 +34,7 @@ def test_binding_covers_the_header_exactly():
 
 def test_abi_version_and_error_string():
     lib = _native.load()
-    assert lib.kvc_abi_version() == 1
+    assert lib.kvc_abi_version() == 2
     assert isinstance(lib.kvc_last_error(), bytes)
 
 
@@ -116,3 +116,41 @@ def test_binding_argument_counts_match_the_header():
         params = m.group(1).strip()
         n = 0 if params in ("", "void") else params.count(",") + 1
         assert n == len(argtypes), f"{name}: header has {n} parameters, binding {len(argtypes)}"
+
+
+def test_mixed_split_from_the_work_hints(monkeypatch):
+    # Host only (256 CUs without a device).  The decode side's share follows
+    # the two sides' CU-time: the split sweep of 60 decode rows U[256,4096]
+    # plus four 256-token chunks (prefixes 0/512/2048/8192) was fastest at 96
+    # decode CUs, 16 rows plus four 512-token chunks at 16-32, and 128 rows
+    # plus two 128-token chunks kept getting faster up to the 128 measured.
+    from nanovllm_amd.kernels.varlen import varlen_decode_cus
+    from nanovllm_amd.workloads import uniform_lengths
+    monkeypatch.delenv("KVC_MIXED_DECODE_CUS", raising=False)
+
+    def split(n, chunks, hinted=True, **kw):
+        dec = uniform_lengths(n, 256, 4096, seed=3)
+        cq, ck = [0], [0]
+        for p, c in chunks:
+            cq.append(cq[-1] + c)
+            ck.append(ck[-1] + p + c)
+        if not hinted:
+            return varlen_decode_cus(n, cq[-1], 32, 4, **kw)
+        return varlen_decode_cus(n, cq[-1], 32, 4, dec, cq, ck, **kw)
+
+    cfg3 = [(0, 256), (512, 256), (2048, 256), (8192, 256)]
+    assert split(60, cfg3) == 96
+    assert split(60, cfg3, hinted=False) == 96  # 3/8 of the CUs without hints
+    assert 16 <= split(16, [(0, 512), (512, 512), (2048, 512), (8192, 512)]) <= 32
+    assert split(128, [(0, 128), (4096, 128)]) >= 192
+    # Tiny sides keep at least 8 CUs each.
+    assert split(1, [(0, 4096)] * 4) == 8
+    assert split(256, [(0, 1)]) == 248
+    # int8 pools and groupings without the 4-head LDS decode run in turn.
+    assert split(60, cfg3, kv_dtype=_native.KVC_KV_INT8_TOKHEAD) == 0
+    assert _native.query("kvc_varlen_decode_cus", 60, 1024, 16, 2, _native.KVC_KV_BF16,
+                         100000, 10 ** 7) == 0
+    monkeypatch.setenv("KVC_MIXED_DECODE_CUS", "70")
+    assert split(60, cfg3) == 64
+    monkeypatch.setenv("KVC_MIXED_DECODE_CUS", "0")
+    assert split(60, cfg3) == 0

@@ -10,8 +10,9 @@ import torch
 
 from helpers import assert_attention_close, bits, gathered_pool, p17_unit_inputs
 from nanovllm_amd.kernels.kv_int8 import store_kvcache_int8
-from nanovllm_amd.kernels.varlen import varlen_attention
-from nanovllm_amd.layers.attention import Attention
+from nanovllm_amd.kernels.varlen import (varlen_attention, varlen_attention_append,
+                                         varlen_decode_cus)
+from nanovllm_amd.layers.attention import Attention, store_kvcache
 from nanovllm_amd.utils.context import reset_context, set_context
 from nanovllm_amd.workloads import build_block_tables, uniform_lengths
 from oracle import kv_oracle as ko
@@ -20,15 +21,21 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-@pytest.fixture(params=["prefill-sk", "split-64", "serial", "units"])
+_HINTS = {"on": False}
+
+
+@pytest.fixture(params=["prefill-sk", "hinted", "split-64", "serial", "units"])
 def partition(request, monkeypatch):
     """Every launch partition: prefill rows over bf16 keys as one stream-K
     prefill launch and a mixed call's decode and prefill rows as one launch
     over a static CU split with the default decode share (the defaults), the
-    split with 64 decode CUs (KVC_MIXED_DECODE_CUS=64), the decode launch and
-    then the prefill launch (KVC_MIXED_DECODE_CUS=0), and one workgroup per
-    prefill unit (KVC_PREFILL_SK=0; a mixed call then runs its decode launch
-    and its unit launch in turn)."""
+    same with the split sized from the host's work hints (the decode rows'
+    context lengths as host ints), the split with 64 decode CUs
+    (KVC_MIXED_DECODE_CUS=64), the decode launch and then the prefill launch
+    (KVC_MIXED_DECODE_CUS=0), and one workgroup per prefill unit
+    (KVC_PREFILL_SK=0; a mixed call then runs its decode launch and its unit
+    launch in turn)."""
+    monkeypatch.setitem(_HINTS, "on", request.param == "hinted")
     monkeypatch.setenv("KVC_PREFILL_SK", "0" if request.param == "units" else "1")
     if request.param == "split-64":
         monkeypatch.setenv("KVC_MIXED_DECODE_CUS", "64")
@@ -68,7 +75,8 @@ def _check_mixed(c, label, scale=128 ** -0.5):
         num_decode_rows=c["n_dec"], decode_context_lens=c["dec_lens"] if c["n_dec"] else None,
         cu_seqlens_q=torch.tensor(c["cu_q"], dtype=torch.int32, device=DEV),
         cu_seqlens_k=torch.tensor(c["cu_k"], dtype=torch.int32, device=DEV),
-        cu_seqlens_q_list=c["cu_q"], cu_seqlens_k_list=c["cu_k"])
+        cu_seqlens_q_list=c["cu_q"], cu_seqlens_k_list=c["cu_k"],
+        decode_context_lens_list=c["dec_lens"].tolist() if _HINTS["on"] and c["n_dec"] else None)
     torch.cuda.synchronize()
     kc, bt = gathered_pool(c["k_cache"], c["bt"])
     vc, _ = gathered_pool(c["v_cache"], c["bt"])
@@ -298,6 +306,88 @@ def test_attention_forward_mixed_matches_decode_and_prefill_paths():
     ref = ko.mixed_ref(bits(q), ko.bf16_to_f32(bits(kc)), ko.bf16_to_f32(bits(vc)), btn,
                        len(dec_lens), np.asarray(dec_lens), cu_q, cu_k, D ** -0.5)
     assert_attention_close(out, ref, "forward-mixed")
+
+
+def _step_slots(c, page=256):
+    """The engine's slots for a mixed step: decode row i appends at its last
+    position ctx_i - 1, prefill chunk j's tokens sit at positions
+    prefix_j .. prefix_j + sq_j - 1 of table row n_dec + j."""
+    bt = c["bt"].cpu()
+    slots = []
+    for i, n in enumerate(c["dec_lens"].tolist()):
+        slots.append(int(bt[i, (n - 1) // page]) * page + (n - 1) % page)
+    for j in range(len(c["cu_q"]) - 1):
+        sq = c["cu_q"][j + 1] - c["cu_q"][j]
+        sk = c["cu_k"][j + 1] - c["cu_k"][j]
+        row = c["n_dec"] + j
+        for t in range(sk - sq, sk):
+            slots.append(int(bt[row, t // page]) * page + t % page)
+    return slots
+
+
+@pytest.mark.parametrize("case", ["small", "mix16", "decode-only", "prefill-only",
+                                  "int64-slots", "tp2-shard"])
+@pytest.mark.parametrize("hinted", [False, True])
+def test_varlen_append_equals_store_then_varlen(case, hinted):
+    """varlen_attention_append (the prefill rows stored ahead, the decode rows
+    appended inside the decode launch or the split launch's decode side)
+    against store_kvcache of every row then varlen_attention with the same
+    hints: the same output bits and the same pool bytes."""
+    H, KVH = (16, 2) if case == "tp2-shard" else (32, 4)
+    if case == "mix16":
+        dec = uniform_lengths(16, 256, 4096, seed=3)
+        chunks = [(0, 512), (512, 512), (2048, 512), (8192, 512)]
+    elif case == "decode-only":
+        dec, chunks = [1, 31, 32, 33, 700, 4096], []
+    elif case == "prefill-only":
+        dec, chunks = [], [(0, 40), (300, 17), (1000, 256)]
+    else:
+        dec, chunks = [1, 255, 256, 257, 3000], [(0, 33), (512, 64), (2048, 100)]
+    c = _mixed_case(H, KVH, dec, chunks, seed=17 + len(case))
+    slots = torch.tensor(_step_slots(c), dtype=torch.int64 if case == "int64-slots"
+                         else torch.int32, device=DEV)
+    T = c["q"].shape[0]
+    g = torch.Generator().manual_seed(99)
+    qkv = torch.randn(T, H + 2 * KVH, 128, generator=g).to(torch.bfloat16).to(DEV)
+    q, key, value = qkv[:, :H].contiguous(), qkv[:, H:H + KVH], qkv[:, H + KVH:]
+    nd = c["n_dec"]
+    kw = dict(scale=128 ** -0.5, block_tables=c["bt"], num_decode_rows=nd,
+              decode_context_lens=c["dec_lens"] if nd else None,
+              cu_seqlens_q_list=c["cu_q"], cu_seqlens_k_list=c["cu_k"],
+              decode_context_lens_list=c["dec_lens"].tolist() if hinted and nd else None)
+    kc0, vc0 = c["k_cache"].clone(), c["v_cache"].clone()
+    print(f"[varlen-append] {case} hinted={hinted}: T={T} dec={nd}", flush=True)
+    store_kvcache(key, value, kc0, vc0, slots)
+    ref = varlen_attention(q, kc0, vc0, **kw)
+    kc1, vc1 = c["k_cache"].clone(), c["v_cache"].clone()
+    out = varlen_attention_append(q, key, value, kc1, vc1, slots, **kw)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(out), bits(ref)), f"{case}: outputs differ"
+    assert torch.equal(kc1.view(torch.int16), kc0.view(torch.int16)), f"{case}: K pool"
+    assert torch.equal(vc1.view(torch.int16), vc0.view(torch.int16)), f"{case}: V pool"
+
+
+def test_hinted_split_follows_the_mix(monkeypatch):
+    """The decode side's CUs from the host hints on the device's CU count:
+    about 3/8 for 60 decode rows and four 256-token chunks (the measured
+    balance), few for 16 rows and four 512-token chunks, most for 128 rows
+    and two 128-token chunks."""
+    monkeypatch.delenv("KVC_MIXED_DECODE_CUS", raising=False)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+
+    def split(n, chunks):
+        dec = uniform_lengths(n, 256, 4096, seed=3)
+        cq, ck = [0], [0]
+        for p, c in chunks:
+            cq.append(cq[-1] + c)
+            ck.append(ck[-1] + p + c)
+        return varlen_decode_cus(n, cq[-1], 32, 4, dec, cq, ck)
+
+    a = split(60, [(0, 256), (512, 256), (2048, 256), (8192, 256)])
+    b = split(16, [(0, 512), (512, 512), (2048, 512), (8192, 512)])
+    d = split(128, [(0, 128), (4096, 128)])
+    assert 8 <= b < a < d <= cus - 8, (a, b, d)
+    assert abs(a - cus * 3 // 8) <= 16
 
 
 @pytest.mark.parametrize("page", [32, 64, 128])
