@@ -42,7 +42,8 @@ def parse_args():
     ap.add_argument("--workload", default="decode",
                     choices=["decode", "decode-dist", "decode-tp2", "decode-cold", "cfg1",
                              "p15-grid", "int8", "mixed", "mixed16", "append", "swap", "copy",
-                             "rope", "decode-graph", "offload-overlap", "pd-wire"])
+                             "rope", "decode-graph", "offload-overlap", "pd-wire",
+                             "block-manager"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--mixed-call-only", action="store_true",
                     help="mixed workloads: run only the hinted call in every timed slot (for "
@@ -1060,8 +1061,68 @@ def run_copy(args, torch):
             "ms": round(ms, 4), "GBps": round(2 * nbytes / (ms * 1e-3) / 1e9, 1)}
 
 
+def run_block_manager(args):
+    """Host bookkeeping of the paged pool (engine/block_manager.py, the
+    reference's algorithm on intrusive rings): a decode step of 64 sequences
+    at context ~4096 (may_append, then the filled-block hash and the token
+    append after the forward), averaged over 256 steps so every sequence
+    crosses one block boundary; and admitting then freeing a 4096-token
+    prompt (can_allocate, allocate, hashing its 16 blocks, deallocate).
+    Host CPU only; the decode attention the step would launch is timed by
+    the default workload."""
+    import random
+    from nanovllm_amd.engine.block_manager import BlockManager
+    from nanovllm_amd.engine.sequence import Sequence
+    rng = random.Random(7)
+    bs = 256
+    bm = BlockManager(8192, bs)
+    seqs = []
+    for _ in range(64):
+        seq = Sequence([rng.randrange(151936) for _ in range(4096 - 3)])
+        seq.block_size = bs
+        bm.allocate(seq, bm.can_allocate(seq))
+        seq.num_cached_tokens, seq.num_scheduled_tokens = 0, len(seq)
+        bm.hash_blocks(seq)
+        seq.is_prefill = False
+        seqs.append(seq)
+    steps = 256
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        for seq in seqs:
+            bm.may_append(seq)
+        for seq in seqs:
+            seq.num_cached_tokens, seq.num_scheduled_tokens = len(seq) - 1, 1
+            bm.hash_blocks(seq)
+            seq.append_token(rng.randrange(151936))
+    step_us = (time.perf_counter() - t0) / steps * 1e6
+    for seq in seqs:
+        bm.deallocate(seq)
+    prompts = [[rng.randrange(151936) for _ in range(4096)] for _ in range(16)]
+    t0 = time.perf_counter()
+    for toks in prompts:
+        seq = Sequence(toks)
+        seq.block_size = bs
+        bm.allocate(seq, bm.can_allocate(seq))
+        seq.num_cached_tokens, seq.num_scheduled_tokens = 0, len(seq)
+        bm.hash_blocks(seq)
+        bm.deallocate(seq)
+    admit_us = (time.perf_counter() - t0) / len(prompts) * 1e6
+    return {"workload": "block-manager host bookkeeping (engine/block_manager.py): decode step "
+                        "of 64 sequences at context ~4096; admit + free of a 4096-token prompt",
+            "decode_step_us": round(step_us, 1), "prompt_admit_free_us": round(admit_us, 1),
+            "host": platform_name()}
+
+
+def platform_name():
+    import platform
+    return f"{platform.processor() or platform.machine()}, {os.cpu_count()} CPUs visible"
+
+
 def main():
     args = parse_args()
+    if args.workload == "block-manager":
+        print(json.dumps(run_block_manager(args)), flush=True)
+        return
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU; --gpus {args.gpus} is not supported "
               f"(the paged KV path has no cross-GPU exchange to measure)", file=sys.stderr)
