@@ -94,6 +94,7 @@ SIGNATURES = {
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
+_fns: dict = {}  # name -> bound ctypes function (looked up once)
 
 
 def load() -> ctypes.CDLL:
@@ -112,39 +113,50 @@ def load() -> ctypes.CDLL:
                 fn = getattr(lib, name)
                 fn.restype = res
                 fn.argtypes = args
+                _fns[name] = fn
             _lib = lib
     return _lib
 
 
 def call(name: str, *args) -> int:
     """Invoke entry point `name`; raise the mapped exception on a nonzero status."""
-    lib = load()
-    rc = getattr(lib, name)(*args)
+    fn = _fns.get(name)
+    if fn is None:
+        fn = getattr(load(), name)
+    rc = fn(*args)
     if rc != 0:
-        msg = lib.kvc_last_error().decode(errors="replace")
+        msg = _lib.kvc_last_error().decode(errors="replace")
         raise _ERRORS.get(rc, RuntimeError)(msg or f"{name} failed with status {rc}")
     return rc
 
 
 def query(name: str, *args):
     """Invoke a size/count query (no status code)."""
-    return getattr(load(), name)(*args)
+    fn = _fns.get(name)
+    if fn is None:
+        fn = getattr(load(), name)
+    return fn(*args)
 
 
 def ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(t: torch.Tensor) -> int:
     """Handle of torch's current stream on t's device (all work is stream-ordered)."""
-    if t.device.type != "cuda":
+    if not t.is_cuda:
         raise RuntimeError(f"the HIP KV path needs device tensors, got {t.device}")
+    if _raw_stream is not None:
+        return _raw_stream(t.get_device())
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
 def require_device(*tensors: torch.Tensor | None) -> None:
     for t in tensors:
-        if t is not None and t.device.type != "cuda":
+        if t is not None and not t.is_cuda:
             raise RuntimeError(f"the HIP KV path needs device tensors, got {t.device}")
 
 

@@ -202,16 +202,17 @@ def paged_decode_append(q, key, value, k_cache, v_cache, slot_mapping, block_tab
     ws_bytes = nat.query("kvc_paged_decode_workspace_bytes", batch, num_heads, num_kv_heads,
                          head_dim, page_size, max_blocks)
     ws = nat.workspace(ws_bytes, q.device)
+    qs, ks, vs, os_ = q.stride(), key.stride(), value.stride(), output.stride()
     nat.call(
         "kvc_paged_decode_append",
-        q.data_ptr(), q.stride(0), q.stride(1),
-        key.data_ptr(), key.stride(0), key.stride(1),
-        value.data_ptr(), value.stride(0), value.stride(1),
+        q.data_ptr(), qs[0], qs[1],
+        key.data_ptr(), ks[0], ks[1],
+        value.data_ptr(), vs[0], vs[1],
         slot_mapping.data_ptr(), sb,
         k_cache.data_ptr(), v_cache.data_ptr(), k_cache.size(0), page_size, num_kv_heads,
         head_dim, block_tables.data_ptr(), block_tables.stride(0), max_blocks,
         context_lens.data_ptr(), batch, num_heads, float(scale),
-        output.data_ptr(), output.stride(0), output.stride(1),
+        output.data_ptr(), os_[0], os_[1],
         nat.ptr(ws), ws_bytes, nat.stream_of(q),
     )
     return output
