@@ -45,6 +45,9 @@ def parse_args():
                              "rope", "decode-graph", "offload-overlap", "pd-wire",
                              "block-manager"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--stamps", action="store_true",
+                    help="decode workloads: also report the per-workgroup end times of the "
+                         "decode kernel (KVC_DECODE_STAMPS), measured after the timed region")
     ap.add_argument("--mixed-call-only", action="store_true",
                     help="mixed workloads: run only the hinted call in every timed slot (for "
                          "kernel traces of that call; the other fields then repeat it)")
@@ -441,10 +444,47 @@ def run_decode(args, torch, dist: bool, int8: bool = False):
                               "committed under profiles/ (not measured in this run)",
         },
     }
+    if args.stamps:
+        res["workgroup_end_us"] = decode_stamps(torch, step)
     if not args.no_cpu_baseline:
         sample = args.cpu_sample if args.cpu_sample else (2 if int8 else 64)
         res["cpu_baseline"] = cpu_decode_baseline(torch, wl, sample, tok_bytes, int8=int8)
     return res
+
+
+def decode_stamps(torch, step, reps=20):
+    """Per-workgroup end times of the decode kernel (after the timed region):
+    KVC_DECODE_STAMPS=1 makes every workgroup record its start and end
+    wall-clock stamps; per step, times are taken from the earliest start.
+    Returns the medians over `reps` steps of the first, median and last
+    workgroup end, the spread (last - first), and each XCD's median end
+    (workgroup v runs on XCD v mod 8)."""
+    import ctypes
+    from nanovllm_amd import _native as nat
+    os.environ["KVC_DECODE_STAMPS"] = "1"
+    buf = (ctypes.c_ulonglong * (2 * 4096))()
+    n, khz = ctypes.c_int(0), ctypes.c_int(0)
+    rows = []
+    try:
+        for _ in range(reps):
+            step()
+            torch.cuda.synchronize()
+            nat.call("kvc_decode_stamps", ctypes.addressof(buf), 4096, ctypes.addressof(n),
+                     ctypes.addressof(khz))
+            g = n.value
+            us_per_tick = 1e3 / khz.value
+            t0 = min(buf[2 * v] for v in range(g))
+            ends = [(buf[2 * v + 1] - t0) * us_per_tick for v in range(g)]
+            srt = sorted(ends)
+            xcd = [statistics.median(ends[x::8]) for x in range(8)]
+            rows.append((srt[0], srt[g // 2], srt[-1], xcd))
+    finally:
+        del os.environ["KVC_DECODE_STAMPS"]
+    med = lambda i: round(statistics.median(r[i] for r in rows), 2)
+    return {"first": med(0), "median": med(1), "last": med(2),
+            "spread": round(statistics.median(r[2] - r[0] for r in rows), 2),
+            "xcd_median": [round(statistics.median(r[3][x] for r in rows), 2) for x in range(8)],
+            "workgroups": n.value, "clock_khz": khz.value, "steps": reps}
 
 
 # The reference's published decode grid (benchmarks/archive/P15-pd-autotune.md:

@@ -277,6 +277,17 @@ int kvc_paged_decode_append_static(
     const int32_t* context_lens, int64_t batch, int64_t num_heads, float scale, void* out,
     int64_t out_stride_b, int64_t out_stride_h, kvc_stream_t stream);
 
+/* Diagnostics, no reference counterpart: with KVC_DECODE_STAMPS=1 in the
+ * environment, every stream-K decode launch (up to 4096 workgroups) has each
+ * workgroup w record its start and end wall-clock stamps; this copies the
+ * last recording launch's stamps on the current device to host_out
+ * ([2 w] start, [2 w + 1] end, up to max_workgroups workgroups; a blocking
+ * copy, so synchronise the launch's stream first) and reports the number of
+ * workgroups and the stamp clock's rate in kHz.  KVC_ERR_VALUE when no launch
+ * recorded. */
+int kvc_decode_stamps(unsigned long long* host_out, int max_workgroups, int* workgroups,
+                      int* clock_khz);
+
 /* ---------------------------------------------------------------------------
  * Mixed decode + chunked-prefill attention in one launch.
  * ------------------------------------------------------------------------- */

@@ -107,6 +107,9 @@ struct AttnParams {
   // the number of workgroups that row unit r (= row * groups + group) spans.
   int sk_min_share;
   int* sk_nseg;
+  // Diagnostics (null: off): workgroup w of a stream-K decode writes its
+  // start and end wall-clock stamps to wg_stamps[2 w], [2 w + 1].
+  unsigned long long* wg_stamps;
   // Paged decode with the step's append fused (app_k null: no append): row b
   // of app_k / app_v (element strides) goes to pool slot app_slots[b]
   // (int32 or int64, wrapped like a Python index, skipped when outside
@@ -2567,6 +2570,8 @@ __device__ __forceinline__ void decode_sk_share(const AttnParams& p,
   constexpr bool kBfLds = kLds && kEnc == kBF16;
   constexpr bool kI8Lds = kLds && kEnc == kI8Tok;
   static_assert(!kLds || kBfLds || kI8Lds, "no LDS-staged form for this encoding");
+  const unsigned long long t_start =
+      p.wg_stamps != nullptr ? __builtin_amdgcn_s_memrealtime() : 0ull;
   // kvs_per_wg divides 8 (a power of two)
   const int groups = (p.kvh * p.nslices) >> __builtin_ctz(unsigned(p.kvs_per_wg));
   const float rgroups = __builtin_amdgcn_rcpf(float(groups));
@@ -2862,6 +2867,13 @@ __device__ __forceinline__ void decode_sk_share(const AttnParams& p,
         decode_segment<kEnc>(p, smem, block_tables + int64_t(sg.b) * p.bt_stride, sg.b, sg.kvg,
                              sg.ctx, sg.t0, sg.t1, sg.split);
       }
+    }
+  }
+  if (p.wg_stamps != nullptr) {
+    __syncthreads();  // every wave has issued its last stores
+    if (threadIdx.x == 0) {
+      p.wg_stamps[2 * w] = t_start;
+      p.wg_stamps[2 * w + 1] = __builtin_amdgcn_s_memrealtime();
     }
   }
 }
@@ -4221,10 +4233,16 @@ float env_float(const char* name, float fallback) {
 }
 
 // Share skew of the stream-K decode between even and odd workgroups (XCDs):
-// on MI355X the odd XCDs stream the same share ~8 % slower (per-workgroup
-// timestamps, stable across runs and when the shares are rotated by one
-// workgroup), so they take 4 % less of a bf16 decode.
+// with the 4-kv-head LDS segment the odd XCDs stream the same share ~8-14 %
+// slower (per-workgroup stamps, KVC_DECODE_STAMPS; 4.4-7.4 us later median
+// ends at batch 64 x 4096 without skew), so they take 4 % less of a bf16
+// decode (0.04-0.06 measured alike).  The 2-kv-head segment shows no such gap
+// (odd XCDs 1.4-1.6 us later without skew, 1.5 us earlier with 0.04) and
+// runs without skew.  The per-token-head int8 segment's odd XCDs end 4.5-5 us
+// later at batch 16 x 32768 without skew; 0.03 brings that to 1 us (kernel
+// 92.6 us against 93.1-94.4 us).
 constexpr float kXcdSkew = 0.04f;
+constexpr float kXcdSkewI8 = 0.03f;
 
 // Workgroups of a stream-K launch: one per CU, or the CUs this thread's
 // current launch may occupy (a mixed call running its decode and prefill
@@ -4696,11 +4714,13 @@ int paged_decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, con
   if (sp.on) {
     p.max_splits = sp.max_splits;
     p.sk_min_share = std::max(1, env_int("KVC_SK_MIN_SHARE", kSkMinShareDev));
-    // bf16 pools are HBM-bound and profit; the int8 segments are bound by their
-    // arithmetic, which the XCDs share evenly.
-    p.xcd_skew = kv_dtype == KVC_KV_BF16
-                     ? std::min(0.25f, std::max(0.f, env_float("KVC_XCD_SKEW", kXcdSkew)))
-                     : 0.f;
+    // The per-channel int8 segment runs without skew (not measured).
+    {
+      const float dflt = kv_dtype == KVC_KV_BF16 ? (hp.kvs_per_wg == 4 ? kXcdSkew : 0.f)
+                         : kv_dtype == KVC_KV_INT8_TOKHEAD ? kXcdSkewI8
+                                                           : 0.f;
+      p.xcd_skew = std::min(0.25f, std::max(0.f, env_float("KVC_XCD_SKEW", dflt)));
+    }
     // Equal rows split into grid / units shares (+1 where a share boundary
     // falls inside a row); longer rows of a ragged batch load the rest later.
     const int64_t units = batch * hp.groups;
@@ -4750,6 +4770,10 @@ int paged_decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, con
         if (rc != KVC_OK) return rc;
       }
     }
+    // Per-workgroup stamps for diagnostics (KVC_DECODE_STAMPS=1; the buffer
+    // holds up to kvc::stamp_slots() workgroups; kvc_decode_stamps reads it).
+    if (env_int("KVC_DECODE_STAMPS", 0) != 0 && sp.grid <= stamp_slots())
+      p.wg_stamps = stamp_buffer(sp.grid);
     // (mixed_split_kernel's decode side is this launch's kernel, the append
     // included.)
     if (tl_record != nullptr && lds4) {

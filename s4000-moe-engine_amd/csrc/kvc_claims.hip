@@ -79,3 +79,70 @@ unsigned long long* claim_set(hipStream_t stream, int words) {
 }
 
 }  // namespace kvc
+
+// ---------------------------------------------------------------------------
+// Per-workgroup wall-clock stamps of a stream-K decode launch (diagnostics,
+// KVC_DECODE_STAMPS=1): one buffer per device, overwritten by every launch
+// that records; kvc_decode_stamps copies the last one to the host.
+// ---------------------------------------------------------------------------
+namespace {
+constexpr int kStampSlots = 4096;
+}  // namespace
+
+static __device__ __align__(256) unsigned long long wg_stamps[2 * kStampSlots];
+
+namespace kvc {
+namespace {
+unsigned long long* g_stamp_ptr[kMaxClaimDevices];
+int g_stamp_grid[kMaxClaimDevices];
+std::mutex g_stamp_mu;
+}  // namespace
+
+int stamp_slots() { return kStampSlots; }
+
+unsigned long long* stamp_buffer(int grid) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxClaimDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_stamp_mu);
+  if (g_stamp_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(wg_stamps)) != hipSuccess || p == nullptr)
+      return nullptr;
+    g_stamp_ptr[dev] = static_cast<unsigned long long*>(p);
+  }
+  g_stamp_grid[dev] = grid;
+  return g_stamp_ptr[dev];
+}
+}  // namespace kvc
+
+extern "C" int kvc_decode_stamps(unsigned long long* host_out, int max_workgroups, int* workgroups,
+                                 int* clock_khz) {
+  kvc::clear_error();
+  KVC_REQUIRE(host_out != nullptr && workgroups != nullptr && clock_khz != nullptr, KVC_ERR_VALUE,
+              "decode_stamps: output pointers are required");
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  KVC_REQUIRE(e == hipSuccess && dev >= 0 && dev < kMaxClaimDevices, KVC_ERR_RUNTIME,
+              "decode_stamps: hipGetDevice: %s", hipGetErrorString(e));
+  unsigned long long* src = nullptr;
+  int grid = 0;
+  {
+    std::lock_guard<std::mutex> lock(kvc::g_stamp_mu);
+    src = kvc::g_stamp_ptr[dev];
+    grid = kvc::g_stamp_grid[dev];
+  }
+  KVC_REQUIRE(src != nullptr && grid > 0, KVC_ERR_VALUE,
+              "decode_stamps: no launch on this device recorded stamps (KVC_DECODE_STAMPS=1)");
+  const int n = grid < max_workgroups ? grid : max_workgroups;
+  e = hipMemcpy(host_out, src, size_t(n) * 2 * sizeof(unsigned long long), hipMemcpyDeviceToHost);
+  KVC_REQUIRE(e == hipSuccess, KVC_ERR_RUNTIME, "decode_stamps: hipMemcpy: %s",
+              hipGetErrorString(e));
+  int khz = 0;
+  e = hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev);
+  KVC_REQUIRE(e == hipSuccess, KVC_ERR_RUNTIME, "decode_stamps: wall clock rate: %s",
+              hipGetErrorString(e));
+  *workgroups = n;
+  *clock_khz = khz;
+  return KVC_OK;
+}
+

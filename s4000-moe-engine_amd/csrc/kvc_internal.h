@@ -46,6 +46,12 @@ inline hipStream_t as_stream(kvc_stream_t s) { return reinterpret_cast<hipStream
 unsigned long long* claim_set(hipStream_t stream, int words);
 int claim_set_words();
 
+// The device's per-workgroup stamp buffer of the stream-K decode's
+// diagnostics (kvc_claims.hip; 2 stamps per workgroup), recording that the
+// next launch has `grid` workgroups; null when it cannot be resolved.
+unsigned long long* stamp_buffer(int grid);
+int stamp_slots();
+
 // The device `stream` runs on (the current device for the NULL stream), for
 // kvc_paged_decode_append_static (kvc_scratch.hip).
 int stream_device(hipStream_t stream, int* dev);

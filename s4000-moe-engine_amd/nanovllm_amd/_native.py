@@ -66,6 +66,7 @@ SIGNATURES = {
                                               _P, _INT, _P, _P, _I64, _I64, _I64, _I64, _P,
                                               _I64, _I64, _P, _I64, _I64, _F32, _P, _I64, _I64,
                                               _P]),
+    "kvc_decode_stamps": (_INT, [_P, _INT, _P, _P]),
     "kvc_varlen_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64]),
     "kvc_varlen_prefill_units": (_I64, [_P, _P, _I64, _I64, _I64, _I64]),
     "kvc_varlen_attention": (_INT, [_P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _I64,

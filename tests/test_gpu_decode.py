@@ -242,3 +242,34 @@ def test_tp2_shard_ragged_fused_append(deterministic_decode):
     assert torch.equal(wl.v_cache.view(torch.int16), vc0.view(torch.int16))
     _check(wl.q, wl.k_cache, wl.v_cache, wl.block_tables, wl.context_lens, wl.scale,
            "tp2 ragged after fused append")
+
+
+def test_decode_stamps_record_every_workgroup(monkeypatch):
+    """KVC_DECODE_STAMPS=1: every workgroup of the stream-K decode launch
+    records a start and an end stamp (end >= start, all within the launch),
+    kvc_decode_stamps reports one pair per workgroup, and the outputs are the
+    same bits as without the stamps."""
+    import ctypes
+    from nanovllm_amd import _native as nat
+    lens = uniform_lengths(12, 1, 3000, seed=4)
+    wl = decode_workload(len(lens), 32, 4, 200, lens, seed=6, device=DEV)
+    monkeypatch.setenv("KVC_DECODE_STREAMK", "1")
+    monkeypatch.delenv("KVC_DECODE_STAMPS", raising=False)
+    ref = paged_decode_attention(wl.q, wl.k_cache, wl.v_cache, wl.block_tables,
+                                 wl.context_lens, wl.scale, max(lens))
+    monkeypatch.setenv("KVC_DECODE_STAMPS", "1")
+    print("[decode-stamps] B=12", flush=True)
+    out = paged_decode_attention(wl.q, wl.k_cache, wl.v_cache, wl.block_tables,
+                                 wl.context_lens, wl.scale, max(lens))
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(out), bits(ref))
+    buf = (ctypes.c_ulonglong * (2 * 4096))()
+    n, khz = ctypes.c_int(0), ctypes.c_int(0)
+    nat.call("kvc_decode_stamps", ctypes.addressof(buf), 4096, ctypes.addressof(n),
+             ctypes.addressof(khz))
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    assert n.value == cus and khz.value > 0
+    starts = [buf[2 * v] for v in range(n.value)]
+    ends = [buf[2 * v + 1] for v in range(n.value)]
+    assert all(s > 0 and e >= s for s, e in zip(starts, ends))
+    assert (max(ends) - min(starts)) / khz.value < 1000.0  # under a second
