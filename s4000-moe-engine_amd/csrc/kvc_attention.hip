@@ -4103,9 +4103,12 @@ void launch_merge_steal(const AttnParams& p, int64_t rows, const StealArgs& sa, 
 
 // Split-K merge of a stream-K prefill launch: one wave per (query row, kv
 // slice).  The wave reads the slice's split count once; lane l then owns
-// head l / 8 of the slice (eight heads per pass) and dims 16 (l % 8) .. +15,
-// so a whole slice's partials are in flight together and a row costs two
-// memory round trips (the count, then the partials) whatever its head count.
+// head l / 8 of the slice (eight heads per pass) and dims 32 q + 4 (l % 8)
+// .. + 3 (q < 4: each load instruction reads 128 contiguous bytes of a head's
+// partial row, 0.8 us faster on config 3's merge than 16 contiguous dims per
+// lane), so a whole slice's partials are in flight together and a row costs
+// two memory round trips (the count, then the partials) whatever its head
+// count.
 constexpr int kSliceBatch = 4;  // splits per load batch (124 VGPRs: every wave resident)
 // Block `block` of the split merge of a stream-K prefill launch
 // (merge_slices_kernel).
@@ -4143,9 +4146,11 @@ __device__ __forceinline__ void merge_slice_rows(const AttnParams& p, int num_ro
       for (int k = 0; k < kSliceBatch; ++k) {
         if (k < cnt) {
           lse[k] = part_lse[base + s0 + k];
-          const float4* src = reinterpret_cast<const float4*>(part_o + (base + s0 + k) * kD) + 4 * sub;
+          // lane sub: dims 32 q + 4 sub .. + 3, so each load of a wave reads
+          // 128 contiguous bytes per head
+          const float4* src = reinterpret_cast<const float4*>(part_o + (base + s0 + k) * kD) + sub;
 #pragma unroll
-          for (int q = 0; q < 4; ++q) o[k][q] = src[q];
+          for (int q = 0; q < 4; ++q) o[k][q] = src[8 * q];
         }
       }
       float bm = -INFINITY;
@@ -4177,14 +4182,12 @@ __device__ __forceinline__ void merge_slice_rows(const AttnParams& p, int num_ro
     }
     if (hb + e < hs) {
       const float inv = 1.f / l;
-      uint16_t* dst = p.out + row * p.o_st + int64_t(h0 + hb + e) * p.o_sh + 16 * sub;
+      uint16_t* dst = p.out + row * p.o_st + int64_t(h0 + hb + e) * p.o_sh + 4 * sub;
 #pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        *reinterpret_cast<u32x4_t*>(dst + 8 * q) =
-            u32x4_t{pack_bf16x2_fast(acc[8 * q + 0] * inv, acc[8 * q + 1] * inv),
-                    pack_bf16x2_fast(acc[8 * q + 2] * inv, acc[8 * q + 3] * inv),
-                    pack_bf16x2_fast(acc[8 * q + 4] * inv, acc[8 * q + 5] * inv),
-                    pack_bf16x2_fast(acc[8 * q + 6] * inv, acc[8 * q + 7] * inv)};
+      for (int q = 0; q < 4; ++q) {
+        *reinterpret_cast<u32x2_t*>(dst + 32 * q) =
+            u32x2_t{pack_bf16x2_fast(acc[4 * q + 0] * inv, acc[4 * q + 1] * inv),
+                    pack_bf16x2_fast(acc[4 * q + 2] * inv, acc[4 * q + 3] * inv)};
       }
     }
   }
