@@ -397,3 +397,25 @@ def test_pages_smaller_than_256(page, partition):
     c = _mixed_case(32, 4, [1, page - 1, page, page + 1, 700],
                     [(0, 40), (page + 3, 33), (5 * page, 64)], seed=page, page=page)
     _check_mixed(c, f"page-{page}")
+
+
+@pytest.mark.parametrize("case", ["decode-side-8", "prefill-side-8"])
+def test_hinted_split_at_its_extremes(case, monkeypatch):
+    """A mixed call whose hints give one side the minimum of 8 CUs: one short
+    decode row beside two long chunks, and 200 decode rows beside one
+    16-token chunk; both against the oracle."""
+    monkeypatch.delenv("KVC_MIXED_DECODE_CUS", raising=False)
+    monkeypatch.setitem(_HINTS, "on", True)
+    if case == "decode-side-8":
+        dec, chunks = [100], [(0, 1024), (4096, 1024)]
+    else:
+        dec, chunks = uniform_lengths(200, 256, 4096, seed=12), [(100, 16)]
+    cq, ck = [0], [0]
+    for p, c in chunks:
+        cq.append(cq[-1] + c)
+        ck.append(ck[-1] + p + c)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    n = varlen_decode_cus(len(dec), cq[-1], 32, 4, dec, cq, ck)
+    assert n == (8 if case == "decode-side-8" else cus - 8), n
+    c = _mixed_case(32, 4, dec, chunks, seed=31 + len(dec))
+    _check_mixed(c, f"hinted-{case}")
