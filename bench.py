@@ -43,7 +43,7 @@ def parse_args():
                     choices=["decode", "decode-dist", "decode-tp2", "decode-cold", "cfg1",
                              "p15-grid", "int8", "mixed", "mixed16", "append", "swap", "copy",
                              "rope", "decode-graph", "offload-overlap", "pd-wire",
-                             "block-manager"])
+                             "block-manager", "int8-chan"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--stamps", action="store_true",
                     help="decode workloads: also report the per-workgroup end times of the "
@@ -449,6 +449,83 @@ def run_decode(args, torch, dist: bool, int8: bool = False):
     if not args.no_cpu_baseline:
         sample = args.cpu_sample if args.cpu_sample else (2 if int8 else 64)
         res["cpu_baseline"] = cpu_decode_baseline(torch, wl, sample, tok_bytes, int8=int8)
+    return res
+
+
+def run_int8_chan(args, torch):
+    """The per-channel int8 decode step (the engine's int8 mode,
+    nanovllm/kernels/kv_int8.py:29-93, paged_attention.py:101-172) at the
+    int8 configuration's shape: batch 16 x context 32768, 32 q / 4 kv heads,
+    page 256.  The pool holds random codes, per-channel store / read scales
+    and a side pool of 4 outlier dims per kv head (2 used).  One step =
+    store_kvcache_int8 of one token per sequence (quantise, outlier dims to
+    the side pool) + paged decode (the register segment: dequantise by the
+    read scales, outlier values from the side pool)."""
+    from nanovllm_amd.kernels.kv_int8 import store_kvcache_int8
+    from nanovllm_amd.kernels.paged_attention import paged_decode_attention
+    from nanovllm_amd.workloads import build_block_tables, slots_for_last_token
+    dev = torch.device("cuda:0")
+    batch, heads, kvh, ctx, n_out = 16, 32, 4, 32768, 4
+    blocks = batch * ctx // 256 + 16
+    lens = [ctx] * batch
+    gen = torch.Generator().manual_seed(9)
+    bt = build_block_tables(lens, blocks, 256, gen)
+    slots = slots_for_last_token(bt, lens, 256).to(dev)
+    bt = bt.to(dev)
+    cl = torch.tensor(lens, dtype=torch.int32, device=dev)
+    g = torch.Generator(device=dev).manual_seed(10)
+    kc = torch.randint(-127, 128, (blocks, 256, kvh, 128), generator=g, device=dev,
+                       dtype=torch.int8)
+    vc = torch.randint(-127, 128, (blocks, 256, kvh, 128), generator=g, device=dev,
+                       dtype=torch.int8)
+    s_k = (torch.rand(kvh, 128, generator=g, device=dev) * 0.02 + 0.01)
+    s_v = (torch.rand(kvh, 128, generator=g, device=dev) * 0.02 + 0.01)
+    out_idx2d = torch.tensor([[3, 77, 0, 0]] * kvh, dtype=torch.int32, device=dev)
+    head_n_out = torch.full((kvh,), 2, dtype=torch.int32, device=dev)
+    ds_k, ds_v = s_k.clone(), s_v.clone()
+    ds_k[:, 3] = 0.0
+    ds_k[:, 77] = 0.0
+    ds_v[:, 3] = 0.0
+    ds_v[:, 77] = 0.0
+    sk = torch.randn(blocks, 256, kvh, n_out, generator=g, device=dev).to(torch.bfloat16)
+    sv = torch.randn(blocks, 256, kvh, n_out, generator=g, device=dev).to(torch.bfloat16)
+    q = torch.randn(batch, heads, 128, generator=g, device=dev).to(torch.bfloat16)
+    nk = torch.randn(batch, kvh, 128, generator=g, device=dev).to(torch.bfloat16)
+    nv = torch.randn(batch, kvh, 128, generator=g, device=dev).to(torch.bfloat16)
+
+    def step(timer=None):
+        s = timer.start() if timer else None
+        store_kvcache_int8(nk, nv, kc, vc, s_k, s_v, sk, sv, out_idx2d, head_n_out, slots)
+        out = paged_decode_attention(q, kc, vc, bt, cl, 128 ** -0.5, ctx, k_scale=ds_k,
+                                     v_scale=ds_v, side_k=sk, side_v=sv, out_idx2d=out_idx2d,
+                                     head_n_out=head_n_out)
+        if timer:
+            timer.stop(s)
+        return out
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / args.steps * 1e3
+    timer = EventTimer(torch)
+    for _ in range(args.steps):
+        step(timer)
+    torch.cuda.synchronize()
+    call_ms = timer.mean_ms()
+    # codes, and the side pool's used outlier dims, of every context token
+    kv_bytes = batch * ctx * (2 * kvh * 128 + 2 * kvh * n_out * 2)
+    res = {"workload": f"int8 per-channel decode step (store_kvcache_int8 + paged decode), "
+                       f"{heads}q/{kvh}kv/128, batch {batch} x ctx {ctx}, page 256, side pool of "
+                       f"{n_out} outlier dims per kv head",
+           "tokens_per_s": round(batch / (ms * 1e-3), 1), "ms_per_step": round(ms, 4),
+           "step_call_us": round(call_ms * 1e3, 2), "kv_bytes": kv_bytes,
+           "kv_read_GBps_at_call": round(kv_bytes / (call_ms * 1e-3) / 1e9, 1)}
+    if args.stamps:
+        res["workgroup_end_us"] = decode_stamps(torch, step)
     return res
 
 
@@ -1177,6 +1254,8 @@ def main():
                          int8=args.workload == "int8")
     elif args.workload == "p15-grid":
         res = run_p15_grid(args, torch)
+    elif args.workload == "int8-chan":
+        res = run_int8_chan(args, torch)
     elif args.workload in MIXES:
         res = run_mixed(args, torch, args.workload)
     elif args.workload == "append":
