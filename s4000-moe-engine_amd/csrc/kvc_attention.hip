@@ -32,6 +32,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <mutex>
+#include <type_traits>
 
 #include "kvc_internal.h"
 
@@ -187,19 +188,26 @@ template <>
 struct Tile<kI8Chan> {
   u32x4_t k[2][2];
   u32x2_t v[8];
+  // Side-pool rows (decode ring only): lane (lm, lg) with lm < 8 holds the
+  // n_out_max bf16 outlier values of key key_of_slot(lg, lm), K in sk and V
+  // in sv (dword d = values 2d, 2d + 1; only the first max(1, n_out_max / 2)
+  // dwords are used).  Slot i's row is read from lane i of the lane's
+  // 16-lane row.
+  uint32_t sk[4], sv[4];
 };
 
-template <int NCB>
+// kSideN bounds the per-channel side-pool width (n_out_max <= kSideN).
+template <int NCB, int kSideN = kSideMax>
 struct ColState {
   f32x4_t o[NCB][8];  // O^T: [col block][d chunk jj], row r -> d = 32lg + 8r + jj
   float m[NCB];       // running max (log2 domain), identical on the 4 lanes of a column
   float l[NCB];       // lane-partial softmax sum
   float vb[NCB];      // lane-partial sum of the bf16 P operand (int8 bias correction)
-  float sd[NCB][kSideMax];  // lane-partial side-pool PV (per-channel int8 only)
+  float sd[NCB][kSideN];  // lane-partial side-pool PV (per-channel int8 only)
 };
 
-template <int NCB>
-__device__ __forceinline__ void init_state(ColState<NCB>& st) {
+template <int NCB, int kSideN>
+__device__ __forceinline__ void init_state(ColState<NCB, kSideN>& st) {
 #pragma unroll
   for (int cb = 0; cb < NCB; ++cb) {
 #pragma unroll
@@ -208,7 +216,7 @@ __device__ __forceinline__ void init_state(ColState<NCB>& st) {
     st.l[cb] = 0.f;
     st.vb[cb] = 0.f;
 #pragma unroll
-    for (int j = 0; j < kSideMax; ++j) st.sd[cb][j] = 0.f;
+    for (int j = 0; j < kSideN; ++j) st.sd[cb][j] = 0.f;
   }
 }
 
@@ -249,6 +257,21 @@ constexpr int kStreamCPol = 2;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, int bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, kBufWord3);
+}
+
+// The same for a base and size that are wave-uniform by construction: taking
+// them through readfirstlane puts the resource in scalar registers even where
+// the compiler cannot prove the uniformity itself (it would otherwise wrap
+// each load in a loop over the distinct resources of the wave's lanes).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t wave_rsrc(const void* base, int bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  // (readfirstlane returns int: each half goes back through uint32_t so the
+  // low half is zero-extended, not sign-extended into the high word)
+  const uint32_t hi = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(a >> 32))));
+  const uint32_t lo = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(a))));
+  const uint64_t u = (uint64_t(hi) << 32) | uint64_t(lo);
+  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(u), 0,
+                                           __builtin_amdgcn_readfirstlane(bytes), kBufWord3);
 }
 
 struct TileOffsets {
@@ -292,6 +315,78 @@ __device__ __forceinline__ void load_tile_buf_i8(Tile<kEnc>& t, __amdgpu_buffer_
 #pragma unroll
   for (int i = 0; i < 8; ++i)
     t.v[i] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(vr, o.v[i], 0, kStreamCPol));
+}
+
+// Side-pool rows of a tile (per-channel int8), loaded with the tile so that
+// the attend step waits for them with the tile's own loads.  A row is the
+// kN = n_out_max bf16 outlier values of one (slot, kv head); kN is 1, 2, 4 or
+// 8, so a row is one 2-, 4-, 8- or 16-byte load at a multiple of its size.
+// Lane (lm, lg) with lm < 8 loads the row of key key_of_slot(lg, lm); the
+// other lanes read past num_records (0, no memory traffic), and so does every
+// lane when `live` is false.
+template <int kN>
+__device__ __forceinline__ void load_side_row(uint32_t (&w)[4], __amdgpu_buffer_rsrc_t r, int off) {
+  if constexpr (kN == 8) {
+    const u32x4_t v =
+        __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kStreamCPol));
+    w[0] = v[0];
+    w[1] = v[1];
+    w[2] = v[2];
+    w[3] = v[3];
+  } else if constexpr (kN == 4) {
+    const u32x2_t v =
+        __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kStreamCPol));
+    w[0] = v[0];
+    w[1] = v[1];
+  } else if constexpr (kN == 2) {
+    w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kStreamCPol);
+  } else {
+    static_assert(kN == 1, "side rows of 1, 2, 4 or 8 values");
+    w[0] = __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, kStreamCPol);
+  }
+}
+
+template <int kN>
+__device__ __forceinline__ void load_side_buf(Tile<kI8Chan>& t, const AttnParams& p,
+                                              int64_t slot0, int g, bool live, const LaneId& L) {
+  constexpr int kRow = 2 * kN;  // bytes of one (slot, kv head) row
+  const int64_t first = (slot0 * p.kvh + g) * kN;
+  const int bytes = live ? ((kTile - 1) * p.kvh + 1) * kRow : 0;
+  const int off = L.lm < 8 ? key_of_slot(L.lg, L.lm) * p.kvh * kRow : 0x40000000;
+  load_side_row<kN>(t.sk, wave_rsrc(live ? p.side_k + first : p.side_k, bytes), off);
+  load_side_row<kN>(t.sv, wave_rsrc(live ? p.side_v + first : p.side_v, bytes), off);
+}
+
+// Dword d of the row of key slot i: lane i of this lane's 16-lane row holds
+// it (DPP row broadcast, no LDS).
+__device__ __forceinline__ uint32_t row_lane(uint32_t v, int i) {
+#define KVC_ROW_LANE(n) \
+  case n:               \
+    return uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0x150 + n, 0xf, 0xf, false));
+  switch (i) {
+    KVC_ROW_LANE(0)
+    KVC_ROW_LANE(1)
+    KVC_ROW_LANE(2)
+    KVC_ROW_LANE(3)
+    KVC_ROW_LANE(4)
+    KVC_ROW_LANE(5)
+    KVC_ROW_LANE(6)
+    default:
+      return uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0x150 + 7, 0xf, 0xf, false));
+  }
+#undef KVC_ROW_LANE
+}
+
+// The kN values of key slot i's row, as bf16 bit patterns in dwords.
+template <int kN>
+__device__ __forceinline__ void side_row_of_slot(uint32_t (&w)[4], const uint32_t (&rows)[4],
+                                                 int i) {
+#pragma unroll
+  for (int d = 0; d < 4; ++d) w[d] = (2 * d < kN) ? row_lane(rows[d], i) : 0u;
+}
+
+__device__ __forceinline__ float side_value(const uint32_t (&w)[4], int j) {
+  return bf16_bits_to_f32((j & 1) ? (w[j >> 1] >> 16) : (w[j >> 1] & 0xffffu));
 }
 
 // ---------------------------------------------------------------------------
@@ -355,7 +450,7 @@ struct ColInfo {
   int klim;     // largest key index the column may attend (inclusive)
 };
 
-template <int kEnc, int NCB>
+template <int kEnc, int NCB, int kSideN = kSideMax>
 struct QOps {
   u32x4_t op[NCB][4];
   // Per-channel int8 folds the read scale into the query, q' = q * s; q' is
@@ -363,11 +458,12 @@ struct QOps {
   // bf16 rounding of a large-scale channel moves logits visibly.
   u32x4_t lo[NCB][4];
   float qsum[NCB];           // int8: sum over d of the query operand(s)
-  float qout[NCB][kSideMax]; // per-channel int8: query at the head's outlier dims
+  float qout[NCB][kSideN];   // per-channel int8: query at the head's outlier dims
+  int n_out;                 // per-channel int8: the kv head's outlier count (wave-uniform)
 };
 
-template <int kEnc, int NCB>
-__device__ __forceinline__ void build_q(QOps<kEnc, NCB>& Q, const AttnParams& p,
+template <int kEnc, int NCB, int kSideN>
+__device__ __forceinline__ void build_q(QOps<kEnc, NCB, kSideN>& Q, const AttnParams& p,
                                         const ColInfo (&ci)[NCB], int g, const LaneId& L) {
 #pragma unroll
   for (int cb = 0; cb < NCB; ++cb) {
@@ -406,9 +502,10 @@ __device__ __forceinline__ void build_q(QOps<kEnc, NCB>& Q, const AttnParams& p,
       Q.qsum[cb] = part;
     }
     if constexpr (kEnc == kI8Chan) {
-      const int n_out = p.head_n_out != nullptr ? p.head_n_out[g] : 0;
+      const int n_out = p.head_n_out != nullptr ? uniform(p.head_n_out[g]) : 0;
+      Q.n_out = n_out;
 #pragma unroll
-      for (int j = 0; j < kSideMax; ++j) {
+      for (int j = 0; j < kSideN; ++j) {
         float v = 0.f;
         if (ci[cb].valid && j < n_out) v = bf16_bits_to_f32(qrow[p.out_idx[g * p.n_out_max + j]]);
         Q.qout[cb][j] = v;
@@ -425,10 +522,13 @@ __device__ __forceinline__ void build_q(QOps<kEnc, NCB>& Q, const AttnParams& p,
 //   slot0      pool slot of the tile's first key (side pool rows)
 // kMasked = false is the fast path for tiles whose 32 keys are all visible to
 // every valid column (all but the last tile of a decode row).
+// kSideRegs (per-channel int8): the side-pool rows came with the tile (t.sk,
+// t.sv) instead of being read from HBM here.
 // ---------------------------------------------------------------------------
-template <int kEnc, int NCB, bool kMasked>
-__device__ __forceinline__ void attend_tile(ColState<NCB>& st, const Tile<kEnc>& t,
-                                            const QOps<kEnc, NCB>& Q, const ColInfo (&ci)[NCB],
+template <int kEnc, int NCB, bool kMasked, bool kSideRegs = false, int kSideN = kSideMax>
+__device__ __forceinline__ void attend_tile(ColState<NCB, kSideN>& st, const Tile<kEnc>& t,
+                                            const QOps<kEnc, NCB, kSideN>& Q,
+                                            const ColInfo (&ci)[NCB],
                                             int key0, int valid_end, int64_t slot0,
                                             const AttnParams& p, int g, const LaneId& L) {
   bool kvalid[8];
@@ -465,9 +565,7 @@ __device__ __forceinline__ void attend_tile(ColState<NCB>& st, const Tile<kEnc>&
   }
 
   int n_out = 0;
-  if constexpr (kEnc == kI8Chan) {
-    if (p.head_n_out != nullptr) n_out = p.head_n_out[g];
-  }
+  if constexpr (kEnc == kI8Chan) n_out = Q.n_out;
 
   // S^T of every column block first: the K operands die before the softmax,
   // and a later block's MFMAs can run under an earlier block's softmax.
@@ -515,12 +613,20 @@ __device__ __forceinline__ void attend_tile(ColState<NCB>& st, const Tile<kEnc>&
       if (n_out > 0) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const uint16_t* srow =
-              p.side_k + ((slot0 + key_of_slot(L.lg, i)) * p.kvh + g) * p.n_out_max;
           float acc = 0.f;
+          if constexpr (kSideRegs) {
+            uint32_t w[4];
+            side_row_of_slot<kSideN>(w, t.sk, i);
 #pragma unroll
-          for (int j = 0; j < kSideMax; ++j)
-            if (j < n_out) acc += Q.qout[cb][j] * bf16_bits_to_f32(srow[j]);
+            for (int j = 0; j < kSideN; ++j)
+              if (j < n_out) acc += Q.qout[cb][j] * side_value(w, j);
+          } else {
+            const uint16_t* srow =
+                p.side_k + ((slot0 + key_of_slot(L.lg, i)) * p.kvh + g) * p.n_out_max;
+#pragma unroll
+            for (int j = 0; j < kSideN; ++j)
+              if (j < n_out) acc += Q.qout[cb][j] * bf16_bits_to_f32(srow[j]);
+          }
           x[i] += acc;
         }
       }
@@ -588,15 +694,26 @@ __device__ __forceinline__ void attend_tile(ColState<NCB>& st, const Tile<kEnc>&
     if constexpr (kEnc == kI8Chan) {
       if (n_out > 0) {
 #pragma unroll
-        for (int j = 0; j < kSideMax; ++j) st.sd[cb][j] *= alpha;
+        for (int j = 0; j < kSideN; ++j) st.sd[cb][j] *= alpha;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          if (!kvalid[i]) continue;
-          const uint16_t* srow =
-              p.side_v + ((slot0 + key_of_slot(L.lg, i)) * p.kvh + g) * p.n_out_max;
+          if constexpr (kSideRegs) {
+            // Every lane of a 16-lane row shares kvalid[i]: the row read
+            // stays outside the branch all the same.
+            uint32_t w[4];
+            side_row_of_slot<kSideN>(w, t.sv, i);
+            if (!kvalid[i]) continue;
 #pragma unroll
-          for (int j = 0; j < kSideMax; ++j)
-            if (j < n_out) st.sd[cb][j] += pr[i] * bf16_bits_to_f32(srow[j]);
+            for (int j = 0; j < kSideN; ++j)
+              if (j < n_out) st.sd[cb][j] += pr[i] * side_value(w, j);
+          } else {
+            if (!kvalid[i]) continue;
+            const uint16_t* srow =
+                p.side_v + ((slot0 + key_of_slot(L.lg, i)) * p.kvh + g) * p.n_out_max;
+#pragma unroll
+            for (int j = 0; j < kSideN; ++j)
+              if (j < n_out) st.sd[cb][j] += pr[i] * bf16_bits_to_f32(srow[j]);
+          }
         }
       }
     }
@@ -617,15 +734,15 @@ __device__ __forceinline__ void attend_tile(ColState<NCB>& st, const Tile<kEnc>&
 
 // Full tiles take the unmasked path; a tile with a key at or past valid_end,
 // or past some valid column's limit, takes the masked one.
-template <int kEnc, int NCB>
-__device__ __forceinline__ void attend(ColState<NCB>& st, const Tile<kEnc>& t,
-                                       const QOps<kEnc, NCB>& Q, const ColInfo (&ci)[NCB],
+template <int kEnc, int NCB, bool kSideRegs = false, int kSideN = kSideMax>
+__device__ __forceinline__ void attend(ColState<NCB, kSideN>& st, const Tile<kEnc>& t,
+                                       const QOps<kEnc, NCB, kSideN>& Q, const ColInfo (&ci)[NCB],
                                        int key0, int valid_end, int min_klim, int64_t slot0,
                                        const AttnParams& p, int g, const LaneId& L) {
   if (key0 + kTile <= valid_end && key0 + kTile - 1 <= min_klim) {
-    attend_tile<kEnc, NCB, false>(st, t, Q, ci, key0, valid_end, slot0, p, g, L);
+    attend_tile<kEnc, NCB, false, kSideRegs>(st, t, Q, ci, key0, valid_end, slot0, p, g, L);
   } else {
-    attend_tile<kEnc, NCB, true>(st, t, Q, ci, key0, valid_end, slot0, p, g, L);
+    attend_tile<kEnc, NCB, true, kSideRegs>(st, t, Q, ci, key0, valid_end, slot0, p, g, L);
   }
 }
 
@@ -639,8 +756,8 @@ struct WaveOut {
   float l[16];
 };
 
-template <int kEnc, int NCB>
-__device__ __forceinline__ void dump_block(WaveOut& wo, const ColState<NCB>& st, int cb,
+template <int kEnc, int NCB, int kSideN>
+__device__ __forceinline__ void dump_block(WaveOut& wo, const ColState<NCB, kSideN>& st, int cb,
                                            const AttnParams& p, int g, const LaneId& L) {
   float l = st.l[cb];
   l += shfl_xor(l, 16);
@@ -673,9 +790,9 @@ __device__ __forceinline__ void dump_block(WaveOut& wo, const ColState<NCB>& st,
   }
   if constexpr (kEnc == kI8Chan) {
     const int n_out = p.head_n_out != nullptr ? p.head_n_out[g] : 0;
-    float sd[kSideMax];
+    float sd[kSideN];
 #pragma unroll
-    for (int j = 0; j < kSideMax; ++j) {
+    for (int j = 0; j < kSideN; ++j) {
       float s = st.sd[cb][j];
       s += shfl_xor(s, 16);
       s += shfl_xor(s, 32);
@@ -687,7 +804,7 @@ __device__ __forceinline__ void dump_block(WaveOut& wo, const ColState<NCB>& st,
     __builtin_amdgcn_wave_barrier();
     if (L.lg == 0) {
 #pragma unroll
-      for (int j = 0; j < kSideMax; ++j)
+      for (int j = 0; j < kSideN; ++j)
         if (j < n_out) wo.o[L.lm][p.out_idx[g * p.n_out_max + j]] = sd[j];
     }
   }
@@ -734,9 +851,13 @@ constexpr int kSmemBytes = kDecodeSmem > kPrefillSmem ? kDecodeSmem : kPrefillSm
 // `split`.  Ends with a barrier, so LDS can be reused right after.
 // ---------------------------------------------------------------------------
 template <int kEnc>
-__device__ void decode_segment(const AttnParams& p, char* smem, const int32_t* bt, int b, int kvg,
+__device__ __forceinline__ void decode_segment(const AttnParams& p, char* smem, const int32_t* bt, int b, int kvg,
                                int ctx, int t0, int t1, int split) {
   b = uniform(b);
+  // The kv group too: it sets every tile's buffer resource, which must sit in
+  // scalar registers (a resource the compiler cannot prove uniform becomes a
+  // loop over lanes around each load).
+  kvg = uniform(kvg);
   const LaneId L = lane_id();
   const int wave = uniform(int(threadIdx.x >> 6));  // wave-uniform (scalar) index
   const int per = p.kvs_per_wg;
@@ -766,10 +887,6 @@ __device__ void decode_segment(const AttnParams& p, char* smem, const int32_t* b
   ci[0].head = g * p.group + s * p.hs + L.lm;
   ci[0].valid = L.lm < hs;
   ci[0].klim = ctx - 1;
-  QOps<kEnc, 1> Q;
-  build_q<kEnc, 1>(Q, p, ci, g, L);
-  ColState<1> st;
-  init_state(st);
 
   const int64_t head_off = int64_t(g) * ((kEnc == kBF16) ? kD * 2 : kD);
   const int tok = int(p.tok_bytes);
@@ -779,53 +896,73 @@ __device__ void decode_segment(const AttnParams& p, char* smem, const int32_t* b
   auto tile_of = [&](int j) { return stream + j * streams; };
   auto tile_slot0 = [&](int tix) -> int64_t {
     const int key0 = uniform(c0 + tix * kTile);
-    const int blk = uniform(bt[key0 / p.page]);
+    const int blk = table_entry(bt, key0 / p.page);
     return int64_t(blk) * p.page + (key0 % p.page);
   };
-  // live == false turns the tile's loads into no-ops (num_records = 0).
-  auto load = [&](Tile<kEnc>& t, int64_t slot0, bool live) {
-    const char* kb = p.k_cache + slot0 * p.tok_bytes + head_off;
-    const char* vb = p.v_cache + slot0 * p.tok_bytes + head_off;
-    const int nrec = live ? span : 0;
-    if constexpr (kEnc == kBF16) {
-      load_tile_buf(t, tile_rsrc(kb, nrec), tile_rsrc(vb, nrec), off);
-    } else {
-      load_tile_buf_i8<kEnc>(t, tile_rsrc(kb, nrec), tile_rsrc(vb, nrec), off);
-    }
-    if constexpr (kEnc == kI8Tok) {
-      load_scales_buf(p.k_scale + slot0 * p.kvh, p.v_scale + slot0 * p.kvh, p.kvh, g, live, L,
-                      t.sck, t.scv);
-    }
-  };
+  WaveOut* wo = reinterpret_cast<WaveOut*>(smem);
+  // The tile loop, for a side-pool width of kN values (per-channel int8: the
+  // pool's n_out_max, which sizes the side loads and the side state; 1 for
+  // the other encodings, which have no side pool).
+  auto run = [&](auto side_width) {
+    constexpr int kN = decltype(side_width)::value;
+    QOps<kEnc, 1, kN> Q;
+    build_q<kEnc, 1>(Q, p, ci, g, L);
+    ColState<1, kN> st;
+    init_state(st);
+    // live == false turns the tile's loads into no-ops (num_records = 0).
+    auto load = [&](Tile<kEnc>& t, int64_t slot0, bool live) {
+      const char* kb = p.k_cache + slot0 * p.tok_bytes + head_off;
+      const char* vb = p.v_cache + slot0 * p.tok_bytes + head_off;
+      const int nrec = live ? span : 0;
+      if constexpr (kEnc == kBF16) {
+        load_tile_buf(t, wave_rsrc(kb, nrec), wave_rsrc(vb, nrec), off);
+      } else {
+        load_tile_buf_i8<kEnc>(t, wave_rsrc(kb, nrec), wave_rsrc(vb, nrec), off);
+      }
+      if constexpr (kEnc == kI8Tok) {
+        load_scales_buf(p.k_scale + slot0 * p.kvh, p.v_scale + slot0 * p.kvh, p.kvh, g, live, L,
+                        t.sck, t.scv);
+      }
+      if constexpr (kEnc == kI8Chan) load_side_buf<kN>(t, p, slot0, g, live && Q.n_out > 0, L);
+    };
 
-  if (my_tiles > 0) {
-    // Ring of kRing tile buffers: tile j is computed from buffer j % kRing
-    // while the next kRing - 1 tiles are in flight; the buffer is refilled
-    // with tile j + kRing right after.
-    constexpr int kRing = 2;
-    Tile<kEnc> ring[kRing];
-    int64_t slot[kRing];
-#pragma unroll
-    for (int r = 0; r < kRing; ++r) {
-      slot[r] = tile_slot0(tile_of(min(r, my_tiles - 1)));
-      load(ring[r], slot[r], r < my_tiles);
-    }
-    for (int j0 = 0; j0 < my_tiles; j0 += kRing) {
+    if (my_tiles > 0) {
+      // Ring of kRing tile buffers: tile j is computed from buffer j % kRing
+      // while the next kRing - 1 tiles are in flight; the buffer is refilled
+      // with tile j + kRing right after.
+      constexpr int kRing = 2;
+      Tile<kEnc> ring[kRing];
+      int64_t slot[kRing];
 #pragma unroll
       for (int r = 0; r < kRing; ++r) {
-        const int j = j0 + r;
-        if (j < my_tiles)
-          attend<kEnc, 1>(st, ring[r], Q, ci, c0 + tile_of(j) * kTile, ctx, ctx - 1, slot[r], p,
-                          g, L);
-        const int nxt = j + kRing;
-        slot[r] = tile_slot0(tile_of(min(nxt, my_tiles - 1)));
-        load(ring[r], slot[r], nxt < my_tiles);
+        slot[r] = tile_slot0(tile_of(min(r, my_tiles - 1)));
+        load(ring[r], slot[r], r < my_tiles);
+      }
+      for (int j0 = 0; j0 < my_tiles; j0 += kRing) {
+#pragma unroll
+        for (int r = 0; r < kRing; ++r) {
+          const int j = j0 + r;
+          if (j < my_tiles)
+            attend<kEnc, 1, kEnc == kI8Chan>(st, ring[r], Q, ci, c0 + tile_of(j) * kTile, ctx,
+                                             ctx - 1, slot[r], p, g, L);
+          const int nxt = j + kRing;
+          slot[r] = tile_slot0(tile_of(min(nxt, my_tiles - 1)));
+          load(ring[r], slot[r], nxt < my_tiles);
+        }
       }
     }
+    dump_block<kEnc, 1>(wo[wave], st, 0, p, g, L);
+  };
+  if constexpr (kEnc == kI8Chan) {
+    switch (p.n_out_max) {
+      case 1: run(std::integral_constant<int, 1>{}); break;
+      case 2: run(std::integral_constant<int, 2>{}); break;
+      case 4: run(std::integral_constant<int, 4>{}); break;
+      default: run(std::integral_constant<int, 8>{}); break;
+    }
+  } else {
+    run(std::integral_constant<int, 1>{});
   }
-
-  WaveOut* wo = reinterpret_cast<WaveOut*>(smem);
-  dump_block<kEnc, 1>(wo[wave], st, 0, p, g, L);
   __syncthreads();
   // Merge the streams of every slice: 16 threads per (slice, column), each
   // owning 8 dims; 32 columns per pass over the workgroup.
@@ -4446,9 +4583,16 @@ int check_kv_args(int kv_dtype, const float* k_scale, const float* v_scale, cons
   if (kv_dtype == KVC_KV_INT8_CHAN && head_n_out != nullptr) {
     KVC_REQUIRE(side_k != nullptr && side_v != nullptr && out_idx2d != nullptr, KVC_ERR_VALUE,
                 "%s: outlier dims need side pools and out_idx2d", what);
-    KVC_REQUIRE(n_out_max >= 1 && n_out_max <= kSideMax, KVC_ERR_VALUE,
-                "%s: n_out_max must be in [1, %d] (got %lld)", what, kSideMax,
+    // A power of two, as the reference kernel's tl.arange(0, N_OUT_MAX)
+    // requires (nanovllm/kernels/paged_attention.py:107): a side row is then
+    // one aligned 2-, 4-, 8- or 16-byte load.
+    KVC_REQUIRE(n_out_max >= 1 && n_out_max <= kSideMax && (n_out_max & (n_out_max - 1)) == 0,
+                KVC_ERR_VALUE, "%s: n_out_max must be 1, 2, 4 or 8 (got %lld)", what,
                 (long long)n_out_max);
+    const uintptr_t row_align = uintptr_t(n_out_max >= 2 ? 4 : 2);
+    KVC_REQUIRE(reinterpret_cast<uintptr_t>(side_k) % row_align == 0 &&
+                    reinterpret_cast<uintptr_t>(side_v) % row_align == 0,
+                KVC_ERR_VALUE, "%s: side pools must be %d-byte aligned", what, int(row_align));
   }
   return KVC_OK;
 }

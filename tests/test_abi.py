@@ -108,6 +108,27 @@ def test_bad_arguments_map_to_python_exceptions():
         _native.call("kvc_block_gather", None, 1, 16, 15, None, 1, None, 16, 16, None)
 
 
+def test_side_pool_widths_and_alignment():
+    import pytest
+    # Per-channel side pools (kv_dtype 2): n_out_max must be 1, 2, 4 or 8 and
+    # the pools aligned for one load per row; both are checked on the host
+    # before any device work (the pointers are never dereferenced here).
+
+    def decode(n_out_max, side=4096):
+        _native.call("kvc_paged_decode", None, 0, 0, None, None, 0, 256, 4, 128, 2, 64, 64,
+                     side, side, 64, 64, n_out_max, None, 0, 1, None, 0, 32, 1.0, None, 0, 0,
+                     None, 0, None)
+
+    for n in (1, 2, 4, 8):
+        decode(n)   # batch 0: validated, then nothing to do
+    for n in (0, 3, 5, 6, 7, 9, 16):
+        with pytest.raises(ValueError, match="n_out_max"):
+            decode(n)
+    with pytest.raises(ValueError, match="aligned"):
+        decode(4, side=4098)
+    decode(1, side=4098)
+
+
 def test_binding_argument_counts_match_the_header():
     text = re.sub(r"/\*.*?\*/", "", (REPO / "include" / "kvc.h").read_text(), flags=re.S)
     for name, (_, argtypes) in _native.SIGNATURES.items():

@@ -244,6 +244,50 @@ def test_int8_chan_decode_with_side_pool(decode_path):
     assert_attention_close(out, ref, "chan-side")
 
 
+@pytest.mark.parametrize("n_out_max", [1, 2, 4, 8])
+def test_int8_chan_decode_side_widths(decode_path, n_out_max):
+    """Per-channel decode at every side-pool width the reference kernel admits
+    (tl.arange(0, N_OUT_MAX) needs a power of two; paged_attention.py:107):
+    kv heads with 0, 1, ..., n_out_max outlier dims, contexts across page and
+    tile boundaries, and NaN in the side slots past each head's count (no
+    such slot may reach the output)."""
+    B, H, KVH, D, page, blocks = 5, 32, 4, 128, 256, 48
+    lens = [4097, 300, 1, 2500, 256 * 7 + 31]
+    g = torch.Generator().manual_seed(40 + n_out_max)
+    bt = build_block_tables(lens, blocks, page, g)
+    kc = torch.randint(-127, 128, (blocks, page, KVH, D), generator=g, dtype=torch.int8)
+    vc = torch.randint(-127, 128, (blocks, page, KVH, D), generator=g, dtype=torch.int8)
+    counts = [n_out_max, 0, max(n_out_max - 1, 1), n_out_max // 2]
+    head_n_out = torch.tensor(counts, dtype=torch.int32)
+    out_idx2d = torch.zeros(KVH, n_out_max, dtype=torch.int32)
+    ds_k = torch.rand(KVH, D, generator=g) * 0.02 + 0.01
+    ds_v = torch.rand(KVH, D, generator=g) * 0.02 + 0.01
+    for h in range(KVH):
+        dims = torch.randperm(D, generator=g)[:n_out_max].to(torch.int32)
+        out_idx2d[h] = dims
+        ds_k[h, dims[:counts[h]].long()] = 0.0
+        ds_v[h, dims[:counts[h]].long()] = 0.0
+    sk = (torch.randn(blocks, page, KVH, n_out_max, generator=g) * 4).to(torch.bfloat16)
+    sv = (torch.randn(blocks, page, KVH, n_out_max, generator=g) * 4).to(torch.bfloat16)
+    for h in range(KVH):
+        sk[:, :, h, counts[h]:] = float("nan")
+        sv[:, :, h, counts[h]:] = float("nan")
+    q = torch.randn(B, H, D, generator=g).to(torch.bfloat16)
+    print(f"[int8-chan-widths] n_out_max={n_out_max} counts={counts} lens={lens}", flush=True)
+    out = paged_decode_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), bt.to(DEV),
+                                 torch.tensor(lens, dtype=torch.int32, device=DEV), D ** -0.5,
+                                 max(lens), k_scale=ds_k.to(DEV), v_scale=ds_v.to(DEV),
+                                 side_k=sk.to(DEV), side_v=sv.to(DEV),
+                                 out_idx2d=out_idx2d.to(DEV), head_n_out=head_n_out.to(DEV))
+    torch.cuda.synchronize()
+    kf = ko.kv_float(kc.numpy(), "int8_chan", ds_k.numpy(), bits(sk), out_idx2d.numpy(),
+                     head_n_out.numpy())
+    vf = ko.kv_float(vc.numpy(), "int8_chan", ds_v.numpy(), bits(sv), out_idx2d.numpy(),
+                     head_n_out.numpy())
+    ref = ko.paged_decode_ref(bits(q), kf, vf, bt.numpy(), np.asarray(lens), D ** -0.5)
+    assert_attention_close(out, ref, f"chan-widths-{n_out_max}")
+
+
 def test_chan_calibration_on_device_matches_p17_unit_case():
     """KVCacheRunner.kv_calibrate_begin / the bound layer's kv_observe hook /
     kv_calibrate_freeze (model_runner.py:510-577) on the seeded unit case of
