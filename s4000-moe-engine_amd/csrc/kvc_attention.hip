@@ -1852,7 +1852,7 @@ __device__ __forceinline__ void init_key_half(KeyHalfState& st) {
 template <bool kMasked>
 __device__ __forceinline__ void key_half_pv_i8(KeyHalfState& st, const float (&x)[4],
                                                const bool (&kvalid)[4], const u32x2_t (&vr)[4],
-                                               const float (&vsc)[4]) {
+                                               const float (&vsc)[4], u32x2_t& pb) {
   float pr[4], pv[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -1860,7 +1860,7 @@ __device__ __forceinline__ void key_half_pv_i8(KeyHalfState& st, const float (&x
     pv[i] = kvalid[i] ? pr[i] * vsc[i] : 0.f;
   }
   st.l += (pr[0] + pr[1]) + (pr[2] + pr[3]);
-  const u32x2_t pb = {pack_bf16x2_fast(pv[0], pv[1]), pack_bf16x2_fast(pv[2], pv[3])};
+  pb = u32x2_t{pack_bf16x2_fast(pv[0], pv[1]), pack_bf16x2_fast(pv[2], pv[3])};
   // Column sums of the P operand as rounded, from a ones operand: the
   // +128 bias of V comes off exactly at the end.
   st.vb = mfma_bf16_k16(u32x2_t{0x3f803f80u, 0x3f803f80u}, pb, st.vb);
@@ -1936,10 +1936,134 @@ __device__ __forceinline__ void attend_key_half_i8(KeyHalfState& st, const u32x4
     st.vb[1] *= alpha;
     st.vb[2] *= alpha;
     st.vb[3] *= alpha;
-    key_half_pv_i8<kMasked>(st, x, kvalid, vr, vsc);
+    u32x2_t pb;
+    key_half_pv_i8<kMasked>(st, x, kvalid, vr, vsc, pb);
   } else {
-    key_half_pv_i8<kMasked>(st, x, kvalid, vr, vsc);
+    u32x2_t pb;
+    key_half_pv_i8<kMasked>(st, x, kvalid, vr, vsc, pb);
   }
+}
+
+// Per-channel int8 on the LDS ring: the query q' = q * s_k (the read scales
+// folded in, as the register segment does) rides the same int8 hi / lo
+// MFMAs.  The side pool's outlier dims come in through two 16-deep bf16
+// MFMAs per key half, with the outlier index j as the inner dimension:
+//   K side  S[key][col] += sum_j side_k[key][j] q[col][out_idx[j]]
+//   V side  O[j][col]   += sum_key side_v[key][j] P[key][col]
+// Lane (lm, lg) holds j = 4 lg .. + 3 of each operand.
+struct ChanSide {
+  u32x2_t qop;     // K side B operand: bf16 q[col lm][out_idx[j]], 0 past the head's count
+  u32x2_t kmask;   // K side A operand mask: j past the head's count reads as 0
+  f32x4_t sd;      // V side accumulator: j = 4 lg + r of column lm
+  int n_out;       // the kv head's outlier count (wave-uniform)
+};
+
+// K side A operand: key row r of the staged tile, this wave's head gl,
+// values j = 4 lg .. + 3 (side block layout [key][4 heads][kN] bf16).
+template <int kN>
+__device__ __forceinline__ u32x2_t side_k_operand(const char* side, int r, int gl,
+                                                  const LaneId& L) {
+  const char* a = side + r * (8 * kN) + gl * (2 * kN) + 8 * L.lg;
+  if constexpr (kN == 8) {
+    return L.lg < 2 ? *reinterpret_cast<const u32x2_t*>(a) : u32x2_t{0u, 0u};
+  } else if constexpr (kN == 4) {
+    return L.lg == 0 ? *reinterpret_cast<const u32x2_t*>(a) : u32x2_t{0u, 0u};
+  } else {
+    static_assert(kN == 2, "LDS side blocks of 2, 4 or 8 values");
+    return u32x2_t{L.lg == 0 ? *reinterpret_cast<const uint32_t*>(a) : 0u, 0u};
+  }
+}
+
+// V side A operand: row j = lm, keys r0 .. r0 + 3 (r0 = the lane's first key
+// row), bf16 side_v[key][j]; rows past the head's count and invalid keys 0.
+template <int kN, bool kMasked>
+__device__ __forceinline__ u32x2_t side_v_operand(const char* side, int r0, int gl, int n_out,
+                                                  const bool (&kvalid)[4], const LaneId& L) {
+  uint32_t e[4] = {0u, 0u, 0u, 0u};
+  if (L.lm < kN && L.lm < n_out) {
+    const char* a = side + r0 * (8 * kN) + gl * (2 * kN) + 2 * L.lm;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t v = *reinterpret_cast<const uint16_t*>(a + i * (8 * kN));
+      e[i] = (!kMasked || kvalid[i]) ? v : 0u;
+    }
+  }
+  return u32x2_t{e[0] | (e[1] << 16), e[2] | (e[3] << 16)};
+}
+
+// One wave's key half of a per-channel tile (attend_key_half_i8 with no
+// per-key scales and the side terms).  `side` is the tile's side block (K
+// rows, then V rows kSideSlot bytes on).
+template <bool kMasked, int kN, int kSideSlot>
+__device__ __forceinline__ void attend_key_half_chan(KeyHalfState& st, ChanSide& cs,
+                                                     const u32x4_t (&kc)[2],
+                                                     const u32x2_t (&vr)[4], const char* side,
+                                                     const QueryI8& Q, int key0, int valid_end,
+                                                     int klim, float scale_log2, int gl,
+                                                     const LaneId& L) {
+  bool kvalid[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) kvalid[i] = !kMasked || (key0 + 4 * L.lg + i < valid_end);
+  const int rh = key0 & 31;  // the key half's first row in the tile
+  u32x2_t ka = side_k_operand<kN>(side, rh + L.lm, gl, L);
+  ka[0] &= cs.kmask[0];
+  ka[1] &= cs.kmask[1];
+  const u32x2_t va = side_v_operand<kN, kMasked>(side + kSideSlot, rh + 4 * L.lg, gl, cs.n_out,
+                                                 kvalid, L);
+  i32x4v_t h = {0, 0, 0, 0}, lo = h;
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    h = mfma_i8(kc[c], Q.hi[c], h);
+    lo = mfma_i8(kc[c], Q.lo[c], lo);
+  }
+  const f32x4_t sdot = mfma_bf16_k16(ka, cs.qop, f32x4_t{0.f, 0.f, 0.f, 0.f});
+  const float qs = Q.scale * scale_log2 * (1.f / 254.f);
+  float x[4];
+  float tmax = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float v = fmaf(float(__mul24(h[i], 254) + lo[i]), qs, fmaf(sdot[i], scale_log2, -st.mu));
+    if constexpr (kMasked) {
+      const bool ok = kvalid[i] && (key0 + 4 * L.lg + i <= klim);
+      x[i] = ok ? v : -INFINITY;
+    } else {
+      x[i] = v;
+    }
+    tmax = fmaxf(tmax, x[i]);
+  }
+  const float ones[4] = {1.f, 1.f, 1.f, 1.f};
+  u32x2_t pb;
+  if (__builtin_expect(__ballot(tmax > st.thr) != 0, 0)) {
+    const float m_new = fmaxf(st.m, rows4_max(tmax + st.mu));
+    const float mu_new = (m_new == -INFINITY) ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(st.m - mu_new);
+    const float shift = st.mu - mu_new;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] += shift;
+    st.m = m_new;
+    st.mu = mu_new;
+    st.thr = (m_new == -INFINITY) ? -INFINITY : kRescaleLog2;
+    st.l *= alpha;
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      st.o[jj][0] *= alpha;
+      st.o[jj][1] *= alpha;
+      st.o[jj][2] *= alpha;
+      st.o[jj][3] *= alpha;
+    }
+    st.vb[0] *= alpha;
+    st.vb[1] *= alpha;
+    st.vb[2] *= alpha;
+    st.vb[3] *= alpha;
+    cs.sd[0] *= alpha;
+    cs.sd[1] *= alpha;
+    cs.sd[2] *= alpha;
+    cs.sd[3] *= alpha;
+    key_half_pv_i8<kMasked>(st, x, kvalid, vr, ones, pb);
+  } else {
+    key_half_pv_i8<kMasked>(st, x, kvalid, vr, ones, pb);
+  }
+  cs.sd = mfma_bf16_k16(va, pb, cs.sd);
 }
 
 // ---------------------------------------------------------------------------
@@ -1965,6 +2089,40 @@ constexpr int kLdsI8 = kI8Ring * kI8Stage + 1024 + 2048;
 constexpr int kI8LoadsPerTile = 5;
 constexpr int kI8MergePitch = kD + 4;  // floats per (head, column) row of the merge block
 static_assert(4 * 16 * kI8MergePitch * 4 + 4 * 16 * 8 <= kI8Stage, "merge block fits a stage");
+
+// The ring's layout in LDS.  Per-token-head: kI8Ring stages of (K rows, V
+// rows, K and V scale blocks), the dummy block, the fused append's rows.
+// Per-channel (side width kN = 2, 4 or 8): stages of K and V rows only, a
+// ring of side blocks one slot deeper ([K side][V side], kSideSlot bytes
+// each: 32 keys x 4 heads x kN bf16, at least the 1 KiB one load writes),
+// the dummy block and the group's K read scales (2 KiB); kN = 8 runs three
+// stages, so that the ring and the query block fit 160 KiB.
+template <int kEnc, int kN>
+struct I8LdsLayout {
+  static constexpr int kRing = kI8Ring;
+  static constexpr int kStage = kI8Stage;
+  static constexpr int kSideSlot = 1024;
+  static constexpr int kSide = 0;
+  static constexpr int kDummy = kI8Ring * kI8Stage;
+  static constexpr int kScales = 0;
+  static constexpr int kBytes = kLdsI8;
+};
+template <int kN>
+struct I8LdsLayout<kI8Chan, kN> {
+  static_assert(kN == 2 || kN == 4 || kN == 8, "LDS side blocks of 2, 4 or 8 values");
+  static constexpr int kRing = kN == 8 ? 3 : 4;
+  static constexpr int kStage = 2 * kI8Rows;
+  static constexpr int kSideSlot = kN * 256 > 1024 ? kN * 256 : 1024;
+  static constexpr int kSide = kRing * kStage;
+  static constexpr int kDummy = kSide + (kRing + 1) * 2 * kSideSlot;
+  static constexpr int kScales = kDummy + 1024;
+  static constexpr int kBytes = kScales + 2048;
+};
+constexpr int cmax(int a, int b) { return a > b ? a : b; }
+constexpr int kLdsChan = cmax(I8LdsLayout<kI8Chan, 2>::kBytes,
+                              cmax(I8LdsLayout<kI8Chan, 4>::kBytes, I8LdsLayout<kI8Chan, 8>::kBytes));
+static_assert(4 * 16 * kI8MergePitch * 4 + 4 * 16 * (2 + 16) * 4 <= I8LdsLayout<kI8Chan, 8>::kSide,
+              "per-channel merge block fits the stages");
 
 constexpr int vmcnt_imm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
 
@@ -2010,9 +2168,13 @@ __device__ void append_i8_row_lane(const AttnParams& p, int b, int kvg) {
   }
 }
 
+template <int kEnc, int kN>
 __device__ void decode_segment_lds_i8(const AttnParams& p, char* ring, char* qlds,
                                       const int32_t* bt, int b, int kvg, int ctx, int t0, int t1,
                                       int split) {
+  constexpr bool kChan = kEnc == kI8Chan;
+  using Lay = I8LdsLayout<kEnc, kN>;
+  constexpr int kRingN = Lay::kRing;
   const LaneId L = lane_id();
   const int wave = uniform(int(threadIdx.x >> 6));
   const int gl = wave & 3;   // kv head within the group
@@ -2041,21 +2203,33 @@ __device__ void decode_segment_lds_i8(const AttnParams& p, char* ring, char* qld
   const bool app_ks = app && wave == 0;
   const bool app_vs = app && wave == 1;
   const bool app_any = app_codes || app_ks || app_vs;
-  char* const app_rows = ring + kI8Ring * kI8Stage + 1024;  // [K row 1 KiB][V row 1 KiB]
+  char* const app_rows = ring + Lay::kDummy + 1024;  // [K row 1 KiB][V row 1 KiB]
   u32x2_t app_kc{0u, 0u}, app_vc{0u, 0u};
   float app_ksc = 0.f, app_vsc = 0.f;
 
   QueryI8 Q;
   KeyHalfState st;
   init_key_half(st);
+  ChanSide cs;
+  if constexpr (kChan) {
+    cs.sd = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    cs.n_out = p.head_n_out != nullptr ? min(table_entry(p.head_n_out, g), kN) : 0;
+  }
 
   const int tok = int(p.tok_bytes);
   const int64_t grp_off = int64_t(kvg) * 512;
   const int sc_tok = p.kvh * 4;  // bytes of scales per token
-  const uint32_t dummy = lds_addr(ring + kI8Ring * kI8Stage);
-  auto stage_of = [&](int j) { return ring + (j & (kI8Ring - 1)) * kI8Stage; };
+  const uint32_t dummy = lds_addr(ring + Lay::kDummy);
+  auto stage_of = [&](int j) { return ring + (unsigned(j) % kRingN) * Lay::kStage; };
+  // (per-channel) the side block of tile j, one ring slot deeper than the
+  // stages: it is read while its tile is computed, after the stage itself
+  // has been handed to the DMA of a later tile.
+  auto side_of = [&](int j) {
+    return ring + Lay::kSide + (unsigned(j) % (kRingN + 1)) * (2 * Lay::kSideSlot);
+  };
   // Wave w brings rows 2n, 2n + 1 (n = w, w + 8) of K and of V, then one
-  // scale block or the dummy load.
+  // scale block (per-token-head), one 1 KiB piece of the side rows
+  // (per-channel) or the dummy load.
   auto issue = [&](int tix) {
     char* base = stage_of(tix);
     const int key0 = uniform(c0 + tix * kTile);
@@ -2073,7 +2247,36 @@ __device__ void decode_segment_lds_i8(const AttnParams& p, char* ring, char* qld
       dma_to_lds(kr, voff, lb + n * 1024);
       dma_to_lds(vr, voff, lb + kI8Rows + n * 1024);
     }
-    if (wave < 2) {
+    if constexpr (kChan) {
+      // Side rows of the tile's 32 keys for the group's 4 heads: 8 kN bytes
+      // per key at a stride of kvh * kN * 2 bytes, kN / 2 lanes of 16 bytes
+      // each per key; kN = 8 takes two 1 KiB pieces per side (waves 0-3),
+      // smaller widths one (waves 0 and 1; lanes past the 32 keys read 0).
+      constexpr int kPieces = kN == 8 ? 2 : 1;
+      constexpr int kLanesPerKey = kN / 2;
+      if (wave < 2 * kPieces) {
+        const int sidew = wave / kPieces;  // 0: K, 1: V
+        const int piece = wave - sidew * kPieces;
+        // (the rows of all 4 heads: whether this wave's own head has
+        // outliers does not matter)
+        const bool has = p.head_n_out != nullptr;
+        // (the pool is picked arithmetically: a select between the two
+        // parameter fields compiles to an indexed read of a private copy)
+        const uint64_t kb = reinterpret_cast<uint64_t>(p.side_k);
+        const uint64_t side_base = kb + (reinterpret_cast<uint64_t>(p.side_v) - kb) * uint64_t(sidew);
+        const uint16_t* sp = !has ? reinterpret_cast<const uint16_t*>(p.k_scale)
+                                  : reinterpret_cast<const uint16_t*>(side_base) +
+                                        (slot0 * p.kvh + kvg * 4) * kN;
+        const int stride = p.kvh * kN * 2;
+        const int nrec = has ? (kTile - 1) * stride + 8 * kN : 0;
+        const int key = piece * (64 / kLanesPerKey) + L.lane / kLanesPerKey;
+        const int soff = key < kTile ? key * stride + (L.lane % kLanesPerKey) * 16 : 0x40000000;
+        dma_to_lds(raw_rsrc(sp, nrec), soff,
+                   lds_addr(side_of(tix)) + sidew * Lay::kSideSlot + piece * 1024);
+      } else {
+        dma_to_lds(raw_rsrc(p.k_scale, 0), 0, dummy);
+      }
+    } else if (wave < 2) {
       const float* sp = (wave == 0 ? p.k_scale : p.v_scale) + slot0 * p.kvh;
       const i32x4_t sr = raw_rsrc(sp, kTile * sc_tok);
       const int soff = L.lane < kTile ? L.lane * sc_tok + kvg * 16 : 0x40000000;
@@ -2097,6 +2300,17 @@ __device__ void decode_segment_lds_i8(const AttnParams& p, char* ring, char* qld
       const int chunk = (L.lane & 15) ^ col;
       dma_to_lds(qr, int(int64_t(head) * p.q_sh * 2) + chunk * 16,
                  lb + (gl * 16 + 8 * kh + 4 * s) * 256);
+    }
+    if constexpr (kChan) {
+      // The group's read scales s_k [4 heads][128] fp32 (2 KiB): waves 0
+      // and 1 bring one half each, the others a dummy load, so every wave
+      // issues three loads here.
+      if (wave < 2) {
+        dma_to_lds(raw_rsrc(p.k_scale + (kvg * 4 + 2 * wave) * kD, 1024), L.lane * 16,
+                   lds_addr(ring + Lay::kScales) + wave * 1024);
+      } else {
+        dma_to_lds(raw_rsrc(p.k_scale, 0), 0, dummy);
+      }
     }
   };
 
@@ -2170,14 +2384,24 @@ __device__ void decode_segment_lds_i8(const AttnParams& p, char* ring, char* qld
       const int row = 16 * kh + 4 * L.lg + i;
       const int chunk = (8 * gl + (L.lm >> 1)) ^ (row & 15);
       r.vr[i] = *reinterpret_cast<const u32x2_t*>(vb + row * 512 + chunk * 16 + 8 * (L.lm & 1));
-      r.ksc[i] = *reinterpret_cast<const float*>(sb + row * 16 + gl * 4);
-      r.vsc[i] = *reinterpret_cast<const float*>(sb + 1024 + row * 16 + gl * 4);
+      if constexpr (!kChan) {
+        r.ksc[i] = *reinterpret_cast<const float*>(sb + row * 16 + gl * 4);
+        r.vsc[i] = *reinterpret_cast<const float*>(sb + 1024 + row * 16 + gl * 4);
+      }
     }
   };
   auto compute = [&](int j, const Regs& r) {
     const int key0 = c0 + j * kTile;
     const int hkey0 = key0 + 16 * kh;
-    if (key0 + kTile <= ctx) {
+    if constexpr (kChan) {
+      if (key0 + kTile <= ctx) {
+        attend_key_half_chan<false, kN, Lay::kSideSlot>(st, cs, r.kc, r.vr, side_of(j), Q, hkey0,
+                                                        ctx, ctx - 1, p.scale_log2, gl, L);
+      } else {
+        attend_key_half_chan<true, kN, Lay::kSideSlot>(st, cs, r.kc, r.vr, side_of(j), Q, hkey0,
+                                                       ctx, ctx - 1, p.scale_log2, gl, L);
+      }
+    } else if (key0 + kTile <= ctx) {
       attend_key_half_i8<false>(st, r.kc, r.vr, r.ksc, r.vsc, Q, hkey0, ctx, ctx - 1,
                                 p.scale_log2, L);
     } else {
@@ -2190,11 +2414,11 @@ __device__ void decode_segment_lds_i8(const AttnParams& p, char* ring, char* qld
   // refilled with tile j + 4, tile j + 1 is read into `nxt`, and tile j is
   // computed while those reads are in flight.
   auto step = [&](int j, const Regs& cur, Regs& nxt) {
-    if (j + 1 < ntiles) wait_tiles_left(min(ntiles - 2 - j, kI8Ring - 2));
+    if (j + 1 < ntiles) wait_tiles_left(min(ntiles - 2 - j, kRingN - 2));
     if (j + 2 == ntiles) patch_append();  // the last tile has landed (vmcnt(0) above)
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): `cur` has arrived
     __syncthreads();
-    if (j + kI8Ring < ntiles) issue(j + kI8Ring);
+    if (j + kRingN < ntiles) issue(j + kRingN);
     if (j + 1 < ntiles) read_stage(stage_of(j + 1), nxt);
     compute(j, cur);
   };
@@ -2212,11 +2436,11 @@ __device__ void decode_segment_lds_i8(const AttnParams& p, char* ring, char* qld
                  lds_addr(app_rows + wave * 1024));
     }
     issue_q();
-    const int first = min(ntiles, kI8Ring);
+    const int first = min(ntiles, kRingN);
     for (int j = 0; j < first; ++j) issue(j);
     wait_tiles_left(first);  // the query loads (and the new rows), issued first, have landed
     __syncthreads();
-    quantise_append();
+    if constexpr (!kChan) quantise_append();
     {
       const char* row = qlds + (gl * 16 + L.lm) * 256;
       float qf[32];
@@ -2233,11 +2457,45 @@ __device__ void decode_segment_lds_i8(const AttnParams& p, char* ring, char* qld
           }
         }
       }
+      if constexpr (kChan) {
+        // q' = q * s_k: dims 64 c + 16 lg + 8 e + m of the lane's column.
+        const float* sc = reinterpret_cast<const float*>(ring + Lay::kScales) + gl * kD;
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const float* s8 = sc + 64 * c + 16 * L.lg + 8 * e;
+            const float4 s0 = *reinterpret_cast<const float4*>(s8);
+            const float4 s1 = *reinterpret_cast<const float4*>(s8 + 4);
+            const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+            for (int m = 0; m < 8; ++m) qf[16 * c + 8 * e + m] *= sv[m];
+          }
+        }
+        // The K side's B operand: the column's query at the head's outlier
+        // dims j = 4 lg .. + 3 (unscaled: the side pool holds the keys' own
+        // values there), and the mask of the j below the head's count.
+        uint32_t qv[4] = {0u, 0u, 0u, 0u}, km[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int j = 0; j < kN; ++j) {
+          if (j < cs.n_out) {
+            const int d = table_entry(p.out_idx, int64_t(g) * p.n_out_max + j);
+            const uint32_t v =
+                *reinterpret_cast<const uint16_t*>(row + (((d >> 3) ^ L.lm) * 16) + (d & 7) * 2);
+            if ((j >> 2) == L.lg) {
+              qv[j & 3] = v;
+              km[j & 3] = 0xffffu;
+            }
+          }
+        }
+        cs.qop = u32x2_t{qv[0] | (qv[1] << 16), qv[2] | (qv[3] << 16)};
+        cs.kmask = u32x2_t{km[0] | (km[1] << 16), km[2] | (km[3] << 16)};
+      }
       Q = quantise_query(qf);
     }
     Regs ra, rb;
     // Tile 0 lands (tiles 1 .. min(3, ntiles - 1) may still be in flight).
-    wait_tiles_left(min(ntiles - 1, kI8Ring - 1));
+    wait_tiles_left(min(ntiles - 1, kRingN - 1));
     if (ntiles == 1) patch_append();  // vmcnt(0) above
     __syncthreads();
     read_stage(stage_of(0), ra);
@@ -2254,8 +2512,16 @@ __device__ void decode_segment_lds_i8(const AttnParams& p, char* ring, char* qld
   const float bias = 128.f * st.vb[0];
   float* mo = reinterpret_cast<float*>(ring);
   float* mml = mo + 4 * 16 * kI8MergePitch;
+  // per-channel: both key halves' side sums, [kh][head][column][8]
+  float* msd = mml + 4 * 16 * 2;
   float* orow = mo + (gl * 16 + L.lm) * kI8MergePitch + 32 * L.lg;
   __syncthreads();
+  if constexpr (kChan) {
+    if (4 * L.lg < kN) {
+      float* d = msd + ((kh * 4 + gl) * 16 + L.lm) * 8 + 4 * L.lg;
+      *reinterpret_cast<float4*>(d) = make_float4(cs.sd[0], cs.sd[1], cs.sd[2], cs.sd[3]);
+    }
+  }
   if (kh == 1) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -2285,6 +2551,33 @@ __device__ void decode_segment_lds_i8(const AttnParams& p, char* ring, char* qld
       const float o1[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
 #pragma unroll
       for (int jj = 0; jj < 8; ++jj) v[i][jj] = a0 * (st.o[jj][i] - bias) + a1 * o1[jj];
+    }
+    if constexpr (kChan) {
+      // V's read scales (0 at the outlier dims), then the side pool's exact
+      // values in the outlier dims' place.
+      const float* vs = p.v_scale + int64_t(g) * kD + 32 * L.lg;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float4 s0 = reinterpret_cast<const float4*>(vs + 8 * i)[0];
+        const float4 s1 = reinterpret_cast<const float4*>(vs + 8 * i)[1];
+        const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) v[i][jj] *= sv[jj];
+      }
+#pragma unroll
+      for (int j = 0; j < kN; ++j) {
+        if (j < cs.n_out) {
+          const float sdt = a0 * msd[(gl * 16 + L.lm) * 8 + j] +
+                            a1 * msd[((4 + gl) * 16 + L.lm) * 8 + j];
+          const int d = table_entry(p.out_idx, int64_t(g) * p.n_out_max + j);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj)
+              if (32 * L.lg + 8 * i + jj == d) v[i][jj] = sdt;
+          }
+        }
+      }
     }
     if (split < 0) {
       const float inv = 1.f / lt;
@@ -2705,7 +2998,7 @@ __device__ __forceinline__ void decode_sk_share(const AttnParams& p,
                                                 int grid, char* smem, char* smem1, char* smem2,
                                                 const StealArgs& sa) {
   constexpr bool kBfLds = kLds && kEnc == kBF16;
-  constexpr bool kI8Lds = kLds && kEnc == kI8Tok;
+  constexpr bool kI8Lds = kLds && (kEnc == kI8Tok || kEnc == kI8Chan);
   static_assert(!kLds || kBfLds || kI8Lds, "no LDS-staged form for this encoding");
   const unsigned long long t_start =
       p.wg_stamps != nullptr ? __builtin_amdgcn_s_memrealtime() : 0ull;
@@ -2791,7 +3084,7 @@ __device__ __forceinline__ void decode_sk_share(const AttnParams& p,
             const int rb = row_of(r), rg = r - rb * groups;
             write_nan_rows(p, rb, rg);
             set_nseg(p, rb, rg, 0);
-            if constexpr (kI8Lds) {
+            if constexpr (kI8Lds && kEnc == kI8Tok) {
               if (p.app_k != nullptr) append_i8_row_lane(p, rb, rg);
             }
             if constexpr (kBfLds) {
@@ -2997,9 +3290,26 @@ __device__ __forceinline__ void decode_sk_share(const AttnParams& p,
   } else {
     DecSeg sg;
     while (next_seg(sg)) {
-      if constexpr (kI8Lds) {
-        decode_segment_lds_i8(p, smem, smem2, block_tables + int64_t(sg.b) * p.bt_stride, sg.b,
-                              sg.kvg, sg.ctx, sg.t0, sg.t1, sg.split);
+      if constexpr (kI8Lds && kEnc == kI8Chan) {
+        const int32_t* bt = block_tables + int64_t(sg.b) * p.bt_stride;
+        switch (p.n_out_max) {
+          case 2:
+            decode_segment_lds_i8<kI8Chan, 2>(p, smem, smem2, bt, sg.b, sg.kvg, sg.ctx, sg.t0,
+                                              sg.t1, sg.split);
+            break;
+          case 8:
+            decode_segment_lds_i8<kI8Chan, 8>(p, smem, smem2, bt, sg.b, sg.kvg, sg.ctx, sg.t0,
+                                              sg.t1, sg.split);
+            break;
+          default:  // 4, or no side pool
+            decode_segment_lds_i8<kI8Chan, 4>(p, smem, smem2, bt, sg.b, sg.kvg, sg.ctx, sg.t0,
+                                              sg.t1, sg.split);
+            break;
+        }
+      } else if constexpr (kI8Lds) {
+        decode_segment_lds_i8<kI8Tok, 0>(p, smem, smem2,
+                                         block_tables + int64_t(sg.b) * p.bt_stride, sg.b,
+                                         sg.kvg, sg.ctx, sg.t0, sg.t1, sg.split);
       } else {
         decode_segment<kEnc>(p, smem, block_tables + int64_t(sg.b) * p.bt_stride, sg.b, sg.kvg,
                              sg.ctx, sg.t0, sg.t1, sg.split);
@@ -3021,7 +3331,9 @@ paged_decode_sk_kernel(AttnParams p, const int32_t* __restrict__ block_tables,
                        const int32_t* __restrict__ ctx_lens) {
   constexpr bool kBfLds = kLds && kEnc == kBF16;
   constexpr bool kI8Lds = kLds && kEnc == kI8Tok;
-  __shared__ __align__(16) char smem[kBfLds ? kLdsStage : (kI8Lds ? kLdsI8 : kDecodeSmem)];
+  constexpr bool kChLds = kLds && kEnc == kI8Chan;
+  __shared__ __align__(16) char
+      smem[kBfLds ? kLdsStage : (kI8Lds ? kLdsI8 : (kChLds ? kLdsChan : kDecodeSmem))];
   __shared__ __align__(16) char smem1[kBfLds ? kLdsStage : 16];
   __shared__ __align__(16) char smem2[kLds ? kLdsQ : 16];
   touch_kernel_args(int(sizeof(AttnParams) + 2 * sizeof(void*)));
@@ -4978,8 +5290,16 @@ int paged_decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, con
         }
         break;
       default:
-        paged_decode_sk_kernel<kI8Chan, false>
-            <<<sp.grid, kThreads, 0, st>>>(p, block_tables, context_lens);
+        // The LDS ring takes side widths of 2, 4 or 8 (16-byte loads of whole
+        // side rows); width 1 runs the register segment.
+        if (hp.kvs_per_wg == 4 && hp.nslices == 1 && env_int("KVC_DECODE_LDS", 1) != 0 &&
+            (head_n_out == nullptr || n_out_max >= 2)) {
+          paged_decode_sk_kernel<kI8Chan, true>
+              <<<sp.grid, kThreads, 0, st>>>(p, block_tables, context_lens);
+        } else {
+          paged_decode_sk_kernel<kI8Chan, false>
+              <<<sp.grid, kThreads, 0, st>>>(p, block_tables, context_lens);
+        }
         break;
     }
     rc = check_launch("paged_decode");
