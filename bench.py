@@ -459,8 +459,8 @@ def run_int8_chan(args, torch):
     page 256.  The pool holds random codes, per-channel store / read scales
     and a side pool of 4 outlier dims per kv head (2 used).  One step =
     store_kvcache_int8 of one token per sequence (quantise, outlier dims to
-    the side pool) + paged decode (the register segment: dequantise by the
-    read scales, outlier values from the side pool)."""
+    the side pool) + paged decode (the per-channel LDS ring: the read scales
+    folded into the query, outlier values from the side pool)."""
     from nanovllm_amd.kernels.kv_int8 import store_kvcache_int8
     from nanovllm_amd.kernels.paged_attention import paged_decode_attention
     from nanovllm_amd.workloads import build_block_tables, slots_for_last_token
