@@ -51,6 +51,9 @@ def parse_args():
     ap.add_argument("--mixed-call-only", action="store_true",
                     help="mixed workloads: run only the hinted call in every timed slot (for "
                          "kernel traces of that call; the other fields then repeat it)")
+    ap.add_argument("--side-slots", type=int, default=8, choices=[1, 2, 4, 8],
+                    help="int8-chan: side-pool slots per kv head (the engine's KV_N_OUT_MAX "
+                         "is 8), half of them holding outlier dims")
     ap.add_argument("--cpu-sample", type=int, default=0,
                     help="sequences of the workload the CPU baseline runs (default: 64 of "
                          "the bf16 decode batch, 2 of the 32k-context int8 batch)")
@@ -457,7 +460,9 @@ def run_int8_chan(args, torch):
     nanovllm/kernels/kv_int8.py:29-93, paged_attention.py:101-172) at the
     int8 configuration's shape: batch 16 x context 32768, 32 q / 4 kv heads,
     page 256.  The pool holds random codes, per-channel store / read scales
-    and a side pool of 4 outlier dims per kv head (2 used).  One step =
+    and a side pool of --side-slots slots per kv head (8 in the engine,
+    nanovllm/engine/model_runner.py:100), half of them holding outlier dims.
+    One step =
     store_kvcache_int8 of one token per sequence (quantise, outlier dims to
     the side pool) + paged decode (the per-channel LDS ring: the read scales
     folded into the query, outlier values from the side pool)."""
@@ -465,7 +470,8 @@ def run_int8_chan(args, torch):
     from nanovllm_amd.kernels.paged_attention import paged_decode_attention
     from nanovllm_amd.workloads import build_block_tables, slots_for_last_token
     dev = torch.device("cuda:0")
-    batch, heads, kvh, ctx, n_out = 16, 32, 4, 32768, 4
+    batch, heads, kvh, ctx, n_out = 16, 32, 4, 32768, args.side_slots
+    used = max(1, n_out // 2)
     blocks = batch * ctx // 256 + 16
     lens = [ctx] * batch
     gen = torch.Generator().manual_seed(9)
@@ -480,13 +486,13 @@ def run_int8_chan(args, torch):
                        dtype=torch.int8)
     s_k = (torch.rand(kvh, 128, generator=g, device=dev) * 0.02 + 0.01)
     s_v = (torch.rand(kvh, 128, generator=g, device=dev) * 0.02 + 0.01)
-    out_idx2d = torch.tensor([[3, 77, 0, 0]] * kvh, dtype=torch.int32, device=dev)
-    head_n_out = torch.full((kvh,), 2, dtype=torch.int32, device=dev)
+    dims = [3, 77, 20, 101, 45, 64, 9, 120][:n_out]
+    out_idx2d = torch.tensor([dims] * kvh, dtype=torch.int32, device=dev)
+    head_n_out = torch.full((kvh,), used, dtype=torch.int32, device=dev)
     ds_k, ds_v = s_k.clone(), s_v.clone()
-    ds_k[:, 3] = 0.0
-    ds_k[:, 77] = 0.0
-    ds_v[:, 3] = 0.0
-    ds_v[:, 77] = 0.0
+    for d in dims[:used]:
+        ds_k[:, d] = 0.0
+        ds_v[:, d] = 0.0
     sk = torch.randn(blocks, 256, kvh, n_out, generator=g, device=dev).to(torch.bfloat16)
     sv = torch.randn(blocks, 256, kvh, n_out, generator=g, device=dev).to(torch.bfloat16)
     q = torch.randn(batch, heads, 128, generator=g, device=dev).to(torch.bfloat16)
@@ -516,11 +522,12 @@ def run_int8_chan(args, torch):
         step(timer)
     torch.cuda.synchronize()
     call_ms = timer.mean_ms()
-    # codes, and the side pool's used outlier dims, of every context token
+    # codes, and the side pool's rows (every slot: the rows are read whole),
+    # of every context token
     kv_bytes = batch * ctx * (2 * kvh * 128 + 2 * kvh * n_out * 2)
     res = {"workload": f"int8 per-channel decode step (store_kvcache_int8 + paged decode), "
                        f"{heads}q/{kvh}kv/128, batch {batch} x ctx {ctx}, page 256, side pool of "
-                       f"{n_out} outlier dims per kv head",
+                       f"{n_out} slots per kv head, {used} outlier dims in use",
            "tokens_per_s": round(batch / (ms * 1e-3), 1), "ms_per_step": round(ms, 4),
            "step_call_us": round(call_ms * 1e3, 2), "kv_bytes": kv_bytes,
            "kv_read_GBps_at_call": round(kv_bytes / (call_ms * 1e-3) / 1e9, 1)}
