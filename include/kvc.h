@@ -248,6 +248,32 @@ int kvc_paged_decode_append_int8(const void* q, int64_t q_stride_b, int64_t q_st
                                  int64_t out_stride_b, int64_t out_stride_h, void* workspace,
                                  size_t workspace_bytes, kvc_stream_t stream);
 
+/* The decode step over a per-channel int8 pool in one call: the new token's
+ * K/V rows (bf16, [batch, num_kv_heads, 128], own strides) go to the pool as
+ * kvc_store_int8_chan stores them (codes against the store scales k_scale /
+ * v_scale [KVH, D], 0 at each head's outlier dims, whose bf16 values go to
+ * the side pools at slot_mapping[b]), then kvc_paged_decode runs over
+ * context_lens with the read scales k_dscale / v_dscale and the side pools.
+ * Replaces the per-channel int8 step of Attention.forward
+ * (nanovllm/layers/attention.py:130-177: store_kvcache_int8,
+ * nanovllm/kernels/kv_int8.py:29-93, then paged_decode_attention's int8 path,
+ * nanovllm/kernels/paged_attention.py:101-172).
+ * The store runs as its own launch ahead of the decode (inside the decode's
+ * LDS ring the quantiser's registers spilled the tile loop, which cost more
+ * than the launch it saves).  Codes, side values and outputs equal the two
+ * calls' bit for bit. */
+int kvc_paged_decode_append_int8_chan(
+    const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* key, int64_t key_stride_n,
+    int64_t key_stride_h, const void* value, int64_t value_stride_n, int64_t value_stride_h,
+    const void* slot_mapping, int slot_index_bytes, int8_t* k_cache, int8_t* v_cache,
+    const float* k_scale, const float* v_scale, const float* k_dscale, const float* v_dscale,
+    void* side_k, void* side_v, const int32_t* out_idx2d, const int32_t* head_n_out,
+    int64_t n_out_max, int64_t num_cache_blocks, int64_t page_size, int64_t num_kv_heads,
+    int64_t head_dim, const int32_t* block_tables, int64_t bt_stride, int64_t max_blocks_per_seq,
+    const int32_t* context_lens, int64_t batch, int64_t num_heads, float scale, void* out,
+    int64_t out_stride_b, int64_t out_stride_h, void* workspace, size_t workspace_bytes,
+    kvc_stream_t stream);
+
 /* Bytes of device scratch kvc_paged_decode_append_static holds on each GPU
  * it runs on: 64 MiB, reserved by the first static call on that GPU (the
  * array is a code object of its own, loaded when first used) and held until

@@ -5093,13 +5093,38 @@ struct DecodeAppend {
   int64_t value_stride_n, value_stride_h;
   const void* slot_mapping;
   int slot_index_bytes;
+  // per-channel int8: the store scales [KVH, D] (the decode reads with its
+  // own read scales)
+  const float* store_k_scale = nullptr;
+  const float* store_v_scale = nullptr;
+};
+
+// The side pool arguments of a per-channel int8 decode.
+struct SidePool {
+  const void* side_k;
+  const void* side_v;
+  const int32_t* out_idx2d;
+  const int32_t* head_n_out;
+  int64_t n_out_max;
 };
 
 // The step's append as its own launch (before a decode launch that cannot
-// take it in): store_kvcache, or the per-token-head int8 quantiser.
+// take it in): store_kvcache, or the int8 quantisers.
 int store_append(const DecodeAppend& app, const void* k_cache, const void* v_cache,
-                 const float* k_scale, const float* v_scale, int64_t num_slots, int64_t batch,
-                 int64_t num_kv_heads, int kv_dtype, kvc_stream_t stream) {
+                 const float* k_scale, const float* v_scale, const SidePool& side,
+                 int64_t num_slots, int64_t batch, int64_t num_kv_heads, int kv_dtype,
+                 kvc_stream_t stream) {
+  if (kv_dtype == KVC_KV_INT8_CHAN) {
+    return kvc_store_int8_chan(app.key, app.key_stride_n, app.key_stride_h, app.value,
+                               app.value_stride_n, app.value_stride_h,
+                               static_cast<int8_t*>(const_cast<void*>(k_cache)),
+                               static_cast<int8_t*>(const_cast<void*>(v_cache)),
+                               app.store_k_scale, app.store_v_scale,
+                               const_cast<void*>(side.side_k), const_cast<void*>(side.side_v),
+                               side.n_out_max, side.out_idx2d, side.head_n_out, num_slots,
+                               app.slot_mapping, app.slot_index_bytes, batch, num_kv_heads, kD,
+                               stream);
+  }
   if (kv_dtype == KVC_KV_INT8_TOKHEAD) {
     return kvc_store_int8_tokhead(app.key, app.key_stride_n, app.key_stride_h, app.value,
                                   app.value_stride_n, app.value_stride_h,
@@ -5224,7 +5249,9 @@ int paged_decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, con
         p.app_slot_bytes = app.slot_index_bytes;
         p.app_num_slots = num_cache_blocks * page_size;
       } else {
-        rc = store_append(app, k_cache, v_cache, k_scale, v_scale, num_cache_blocks * page_size,
+        rc = store_append(app, k_cache, v_cache, k_scale, v_scale,
+                          SidePool{side_k, side_v, out_idx2d, head_n_out, n_out_max},
+                          num_cache_blocks * page_size,
                           batch, num_kv_heads, kv_dtype, stream);
         if (rc != KVC_OK) return rc;
       }
@@ -5308,7 +5335,9 @@ int paged_decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, con
     return check_launch("paged_decode merge");
   }
   if (app.key != nullptr) {
-    rc = store_append(app, k_cache, v_cache, k_scale, v_scale, num_cache_blocks * page_size,
+    rc = store_append(app, k_cache, v_cache, k_scale, v_scale,
+                      SidePool{side_k, side_v, out_idx2d, head_n_out, n_out_max},
+                      num_cache_blocks * page_size,
                       batch, num_kv_heads, kv_dtype, stream);
     if (rc != KVC_OK) return rc;
   }
@@ -5403,6 +5432,36 @@ extern "C" int kvc_paged_decode_append_int8(
                            bt_stride, max_blocks_per_seq, context_lens, batch, num_heads, scale,
                            out, out_stride_b, out_stride_h, workspace, workspace_bytes, app,
                            stream);
+}
+
+extern "C" int kvc_paged_decode_append_int8_chan(
+    const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* key, int64_t key_stride_n,
+    int64_t key_stride_h, const void* value, int64_t value_stride_n, int64_t value_stride_h,
+    const void* slot_mapping, int slot_index_bytes, int8_t* k_cache, int8_t* v_cache,
+    const float* k_scale, const float* v_scale, const float* k_dscale, const float* v_dscale,
+    void* side_k, void* side_v, const int32_t* out_idx2d, const int32_t* head_n_out,
+    int64_t n_out_max, int64_t num_cache_blocks, int64_t page_size, int64_t num_kv_heads,
+    int64_t head_dim, const int32_t* block_tables, int64_t bt_stride, int64_t max_blocks_per_seq,
+    const int32_t* context_lens, int64_t batch, int64_t num_heads, float scale, void* out,
+    int64_t out_stride_b, int64_t out_stride_h, void* workspace, size_t workspace_bytes,
+    kvc_stream_t stream) {
+  clear_error();
+  KVC_REQUIRE(key != nullptr && value != nullptr && slot_mapping != nullptr, KVC_ERR_VALUE,
+              "paged_decode_append_int8_chan: key, value and slot_mapping are required");
+  KVC_REQUIRE(slot_index_bytes == 4 || slot_index_bytes == 8, KVC_ERR_VALUE,
+              "paged_decode_append_int8_chan: slot_mapping must be int32 or int64");
+  KVC_REQUIRE(k_scale != nullptr && v_scale != nullptr, KVC_ERR_VALUE,
+              "paged_decode_append_int8_chan: the store scales are required");
+  DecodeAppend app{key, key_stride_n, key_stride_h, value, value_stride_n, value_stride_h,
+                   slot_mapping, slot_index_bytes};
+  app.store_k_scale = k_scale;
+  app.store_v_scale = v_scale;
+  return paged_decode_impl(q, q_stride_b, q_stride_h, k_cache, v_cache, num_cache_blocks,
+                           page_size, num_kv_heads, head_dim, KVC_KV_INT8_CHAN, k_dscale,
+                           v_dscale, side_k, side_v, out_idx2d, head_n_out, n_out_max,
+                           block_tables, bt_stride, max_blocks_per_seq, context_lens, batch,
+                           num_heads, scale, out, out_stride_b, out_stride_h, workspace,
+                           workspace_bytes, app, stream);
 }
 
 // The decode step without a caller workspace: the split-K partials and split

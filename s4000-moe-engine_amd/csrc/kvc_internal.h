@@ -279,5 +279,19 @@ __device__ __forceinline__ float quant_tokhead_row(const float (&x)[8], int (&co
   return s;
 }
 
+// Per-channel quantisation of 8 dims against their store scales:
+// clamp(floor(x / s + 0.5), -127, 127), IEEE division (the store kernel's and
+// the decode launch's fused append's arithmetic).
+__device__ __forceinline__ int quant_chan1(float x, float s) {
+  const float q = floorf(x / s + 0.5f);
+  return int(fminf(fmaxf(q, -127.0f), 127.0f));
+}
+
+__device__ __forceinline__ void quant_chan8(const float (&x)[8], const float (&s)[8],
+                                            int (&code)[8]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) code[i] = quant_chan1(x[i], s[i]);
+}
+
 
 }  // namespace kvc

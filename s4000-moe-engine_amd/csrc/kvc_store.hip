@@ -148,13 +148,8 @@ store_int8_chan_kernel(const uint16_t* __restrict__ key, int64_t k_sn, int64_t k
   const float ks[8] = {ks0.x, ks0.y, ks0.z, ks0.w, ks1.x, ks1.y, ks1.z, ks1.w};
   const float vs[8] = {vs0.x, vs0.y, vs0.z, vs0.w, vs1.x, vs1.y, vs1.z, vs1.w};
   int kc[8], vc[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    float qk = floorf(kx[i] / ks[i] + 0.5f);
-    float qv = floorf(vx[i] / vs[i] + 0.5f);
-    kc[i] = int(fminf(fmaxf(qk, -127.0f), 127.0f));
-    vc[i] = int(fminf(fmaxf(qv, -127.0f), 127.0f));
-  }
+  quant_chan8(kx, ks, kc);
+  quant_chan8(vx, vs, vc);
   const int n_out = head_n_out != nullptr ? head_n_out[h] : 0;
   for (int j = 0; j < n_out; ++j) {
     const int d = out_idx2d[h * n_out_max + j];

@@ -62,6 +62,11 @@ SIGNATURES = {
                                             _P, _INT, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
                                             _P, _I64, _I64, _P, _I64, _I64, _F32, _P, _I64,
                                             _I64, _P, _SZ, _P]),
+    "kvc_paged_decode_append_int8_chan": (_INT, [_P, _I64, _I64, _P, _I64, _I64, _P, _I64,
+                                                 _I64, _P, _INT, _P, _P, _P, _P, _P, _P, _P,
+                                                 _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P,
+                                                 _I64, _I64, _P, _I64, _I64, _F32, _P, _I64,
+                                                 _I64, _P, _SZ, _P]),
     "kvc_paged_decode_append_static": (_INT, [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,
                                               _P, _INT, _P, _P, _I64, _I64, _I64, _I64, _P,
                                               _I64, _I64, _P, _I64, _I64, _F32, _P, _I64, _I64,

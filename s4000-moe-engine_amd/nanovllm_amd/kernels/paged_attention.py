@@ -293,6 +293,89 @@ def paged_decode_append_int8_tokhead(q, key, value, k_cache, v_cache, k_scale, v
     return output
 
 
+def paged_decode_append_int8_chan(q, key, value, k_cache, v_cache, k_scale, v_scale,
+                                  k_dscale, v_dscale, side_k, side_v, out_idx2d, head_n_out,
+                                  slot_mapping, block_tables, context_lens, scale):
+    """The decode step over a per-channel int8 pool in one call:
+    store_kvcache_int8(key, value, k_cache, v_cache, k_scale, v_scale,
+    side_k, side_v, out_idx2d, head_n_out, slot_mapping) then
+    paged_decode_attention(q, ..., k_scale=k_dscale, v_scale=v_dscale,
+    side_k=side_k, side_v=side_v, out_idx2d=out_idx2d,
+    head_n_out=head_n_out) (the engine's int8 step,
+    nanovllm/layers/attention.py:130-177 with nanovllm/kernels/kv_int8.py:
+    29-93 and paged_attention.py:101-172).  Same codes, side values and
+    outputs as the two calls."""
+    if q.ndim != 3 or key.ndim != 3 or value.shape != key.shape or k_cache.ndim != 4 \
+            or v_cache.shape != k_cache.shape:
+        raise ValueError("expected q=[batch,heads,dim], key/value=[batch,kv_heads,dim], "
+                         "kv=[pages,page,kv_heads,dim]")
+    batch, num_heads, head_dim = q.shape
+    pages, page_size, num_kv_heads = k_cache.shape[:3]
+    if head_dim != 128 or page_size % 32 or num_heads % num_kv_heads:
+        raise ValueError(
+            "paged decode requires head_dim=128, page_size a multiple of 32 and "
+            "GQA-divisible heads")
+    if not (q.dtype == key.dtype == value.dtype == torch.bfloat16
+            and k_cache.dtype == v_cache.dtype == torch.int8):
+        raise ValueError("paged_decode_append_int8_chan takes an int8 pool and bf16 q/k/v")
+    for t in (k_scale, v_scale, k_dscale, v_dscale):
+        if t.shape != (num_kv_heads, head_dim) or t.dtype != torch.float32:
+            raise ValueError("per-channel store / read scales are fp32 [kv_heads, dim]")
+    n_out_max = out_idx2d.size(-1)
+    if side_k.shape != (pages, page_size, num_kv_heads, n_out_max) or side_v.shape != side_k.shape \
+            or side_k.dtype != torch.bfloat16 or side_v.dtype != torch.bfloat16:
+        raise ValueError("side pools are bf16 [pages, page, kv_heads, n_out_max]")
+    assert key.size(0) == batch and key.size(1) == num_kv_heads and slot_mapping.numel() == batch
+    assert key.stride(-1) == 1 and value.stride(-1) == 1
+    nat.require_device(q, key, value, k_cache, v_cache, k_scale, v_scale, k_dscale, v_dscale,
+                       side_k, side_v, out_idx2d, head_n_out, slot_mapping, block_tables,
+                       context_lens)
+    if q.stride(2) != 1:
+        q = q.contiguous()
+    for t in (k_cache, v_cache, k_scale, v_scale, k_dscale, v_dscale, side_k, side_v):
+        if not t.is_contiguous():
+            raise AssertionError("KV pools, scales and side pools must be contiguous")
+    out_idx2d = out_idx2d.to(torch.int32).contiguous()
+    head_n_out = head_n_out.to(torch.int32).contiguous()
+    if block_tables.dtype != torch.int32:
+        block_tables = block_tables.to(torch.int32)
+    if block_tables.stride(1) != 1:
+        block_tables = block_tables.contiguous()
+    if context_lens.dtype != torch.int32 or not context_lens.is_contiguous():
+        context_lens = context_lens.to(torch.int32).contiguous()
+    if slot_mapping.dtype == torch.int64:
+        sb = 8
+    else:
+        slot_mapping = slot_mapping.to(torch.int32)
+        sb = 4
+    slot_mapping = slot_mapping.contiguous()
+    output = torch.empty_like(q)
+    if output.stride(2) != 1:
+        output = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    if batch == 0:
+        return output
+    max_blocks = block_tables.size(1)
+    ws_bytes = nat.query("kvc_paged_decode_workspace_bytes", batch, num_heads, num_kv_heads,
+                         head_dim, page_size, max_blocks)
+    ws = nat.workspace(ws_bytes, q.device)
+    nat.call(
+        "kvc_paged_decode_append_int8_chan",
+        q.data_ptr(), q.stride(0), q.stride(1),
+        key.data_ptr(), key.stride(0), key.stride(1),
+        value.data_ptr(), value.stride(0), value.stride(1),
+        slot_mapping.data_ptr(), sb,
+        k_cache.data_ptr(), v_cache.data_ptr(), k_scale.data_ptr(), v_scale.data_ptr(),
+        k_dscale.data_ptr(), v_dscale.data_ptr(), side_k.data_ptr(), side_v.data_ptr(),
+        out_idx2d.data_ptr(), head_n_out.data_ptr(), n_out_max,
+        pages, page_size, num_kv_heads, head_dim,
+        block_tables.data_ptr(), block_tables.stride(0), max_blocks,
+        context_lens.data_ptr(), batch, num_heads, float(scale),
+        output.data_ptr(), output.stride(0), output.stride(1),
+        nat.ptr(ws), ws_bytes, nat.stream_of(q),
+    )
+    return output
+
+
 def paged_decode_append_static(q, key, value, k_cache, v_cache, slot_mapping, block_tables,
                                context_lens, scale, out):
     """paged_decode_append for callers that cannot allocate device memory:

@@ -450,3 +450,75 @@ def test_int8_tokhead_decode_append_equals_store_then_decode(case, decode_path):
         assert np.array_equal(codes.view(-1, kvh, 128)[sl].cpu().numpy(), want_c)
         assert np.array_equal(sc.view(-1, kvh)[sl].cpu().numpy().view(np.uint32),
                               want_s.view(np.uint32))
+
+
+@pytest.mark.parametrize("n_out_max", [8, 4, 1])
+def test_int8_chan_decode_append_equals_store_then_decode(n_out_max, decode_path):
+    """paged_decode_append_int8_chan (the engine's per-channel int8 step in one
+    call) against store_kvcache_int8 then paged_decode_attention: the same
+    codes and side values in the pools and the same output bits, with heads
+    holding 0 .. n_out_max outlier dims, ragged contexts with an empty row,
+    and int64 slots given in Python's negative form."""
+    from nanovllm_amd.kernels.paged_attention import paged_decode_append_int8_chan
+    B, H, KVH, D, page, blocks = 7, 32, 4, 128, 256, 70
+    lens = [1, 0, 4097, 300, 2600, 33, 1800]
+    g = torch.Generator().manual_seed(70 + n_out_max)
+    bt = build_block_tables([max(1, n) for n in lens], blocks, page, g)
+    kc = torch.randint(-127, 128, (blocks, page, KVH, D), generator=g, dtype=torch.int8)
+    vc = torch.randint(-127, 128, (blocks, page, KVH, D), generator=g, dtype=torch.int8)
+    counts = [n_out_max, 0, max(n_out_max - 1, 1), n_out_max // 2]
+    head_n_out = torch.tensor(counts, dtype=torch.int32)
+    out_idx2d = torch.zeros(KVH, n_out_max, dtype=torch.int32)
+    s_k = torch.rand(KVH, D, generator=g) * 0.02 + 0.01
+    s_v = torch.rand(KVH, D, generator=g) * 0.02 + 0.01
+    ds_k, ds_v = s_k.clone(), s_v.clone()
+    for h in range(KVH):
+        dims = torch.randperm(D, generator=g)[:n_out_max].to(torch.int32)
+        out_idx2d[h] = dims
+        ds_k[h, dims[:counts[h]].long()] = 0.0
+        ds_v[h, dims[:counts[h]].long()] = 0.0
+    sk = (torch.randn(blocks, page, KVH, n_out_max, generator=g) * 4).to(torch.bfloat16)
+    sv = (torch.randn(blocks, page, KVH, n_out_max, generator=g) * 4).to(torch.bfloat16)
+    q = torch.randn(B, H, D, generator=g).to(torch.bfloat16)
+    key = (torch.randn(B, KVH, D, generator=g) * 0.5).to(torch.bfloat16)
+    value = (torch.randn(B, KVH, D, generator=g) * 0.5).to(torch.bfloat16)
+    slots = torch.tensor([int(bt[i, (max(1, n) - 1) // page]) * page + (max(1, n) - 1) % page
+                          for i, n in enumerate(lens)], dtype=torch.int64)
+    slots[::2] -= blocks * page
+    dev = {k: v.to(DEV) for k, v in dict(kc=kc, vc=vc, sk=sk, sv=sv, s_k=s_k, s_v=s_v,
+                                         ds_k=ds_k, ds_v=ds_v, oi=out_idx2d, hn=head_n_out,
+                                         q=q, key=key, value=value, slots=slots,
+                                         bt=bt).items()}
+    lens_t = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    print(f"[int8-chan] step in one call: n_out_max={n_out_max} counts={counts}", flush=True)
+    kc0, vc0, sk0, sv0 = dev["kc"].clone(), dev["vc"].clone(), dev["sk"].clone(), dev["sv"].clone()
+    store_kvcache_int8(dev["key"], dev["value"], kc0, vc0, dev["s_k"], dev["s_v"], sk0, sv0,
+                       dev["oi"], dev["hn"], dev["slots"])
+    ref = paged_decode_attention(dev["q"], kc0, vc0, dev["bt"], lens_t, D ** -0.5, 0,
+                                 k_scale=dev["ds_k"], v_scale=dev["ds_v"], side_k=sk0,
+                                 side_v=sv0, out_idx2d=dev["oi"], head_n_out=dev["hn"])
+    kc1, vc1, sk1, sv1 = dev["kc"].clone(), dev["vc"].clone(), dev["sk"].clone(), dev["sv"].clone()
+    out = paged_decode_append_int8_chan(dev["q"], dev["key"], dev["value"], kc1, vc1, dev["s_k"],
+                                        dev["s_v"], dev["ds_k"], dev["ds_v"], sk1, sv1,
+                                        dev["oi"], dev["hn"], dev["slots"], dev["bt"], lens_t,
+                                        D ** -0.5)
+    torch.cuda.synchronize()
+    assert torch.equal(kc1, kc0) and torch.equal(vc1, vc0), "codes differ"
+    assert torch.equal(sk1.view(torch.int16), sk0.view(torch.int16)), "K side values differ"
+    assert torch.equal(sv1.view(torch.int16), sv0.view(torch.int16)), "V side values differ"
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), "outputs differ"
+    # and the stored token itself is the oracle's per-channel quantisation
+    rk, rv = np.zeros((B, KVH, D), np.int8), np.zeros((B, KVH, D), np.int8)
+    rsk, rsv = np.zeros((B, KVH, n_out_max), np.uint16), np.zeros((B, KVH, n_out_max), np.uint16)
+    for i in range(B):
+        ko.store_int8_chan(bits(key[i:i + 1]), bits(value[i:i + 1]), rk[i:i + 1], rv[i:i + 1],
+                           s_k.numpy(), s_v.numpy(), rsk[i:i + 1], rsv[i:i + 1],
+                           out_idx2d.numpy(), head_n_out.numpy(), np.zeros(1, np.int64))
+    flat = lambda t: t.reshape(-1, KVH, t.shape[-1])
+    sl = (slots % (blocks * page)).numpy()
+    assert np.array_equal(flat(kc1.cpu()).numpy()[sl], rk)
+    assert np.array_equal(flat(vc1.cpu()).numpy()[sl], rv)
+    for h in range(KVH):
+        n = counts[h]
+        assert np.array_equal(bits(flat(sk1.cpu())[sl])[:, h, :n], rsk[:, h, :n])
+        assert np.array_equal(bits(flat(sv1.cpu())[sl])[:, h, :n], rsv[:, h, :n])
