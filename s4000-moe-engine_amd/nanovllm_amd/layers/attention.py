@@ -24,7 +24,8 @@ from torch import nn
 
 from .. import _native as nat
 from ..kernels.kv_int8 import store_kvcache_int8
-from ..kernels.paged_attention import (paged_decode_append, paged_decode_append_int8_tokhead,
+from ..kernels.paged_attention import (paged_decode_append, paged_decode_append_int8_chan,
+                                       paged_decode_append_int8_tokhead,
                                        paged_decode_attention)
 from ..kernels.varlen import varlen_attention, varlen_attention_append
 from ..utils.context import get_context
@@ -100,6 +101,13 @@ class Attention(nn.Module):
     def _int8_tokhead(self) -> bool:
         return self.kv_cache_is_int8 and self.k_scale is not None and self.k_scale.dim() == 3
 
+    def _int8_chan_step(self) -> bool:
+        """A per-channel pool with its side pools and read scales bound: the
+        decode step is one call (store, then decode)."""
+        return (self.kv_cache_is_int8 and not self._int8_tokhead() and self.k_scale is not None
+                and self.k_dscale is not None and self.side_k is not None
+                and self.out_idx2d is not None and self.head_n_out is not None)
+
     def _read_scales(self):
         """Scales the read path needs: per-slot scales (per-token-head) or the
         per-channel read scales (0 at outlier dims)."""
@@ -148,11 +156,13 @@ class Attention(nn.Module):
         k_cache, v_cache = self.k_cache, self.v_cache
         if k_cache.numel() and self.block_size is None:
             self.block_size = k_cache.size(1)
-        # A decode step on a bf16 or per-token-head int8 pool appends inside
-        # the decode call.
+        # A decode step appends inside the decode call (bf16 and per-token-head
+        # int8 pools inside the decode launch; per-channel int8 in the same
+        # call, as a store launch ahead of the decode).
         fuse_append = (not kv_stored and not (context.is_mixed or context.is_prefill)
                        and bool(k_cache.numel() and v_cache.numel())
-                       and (not self.kv_cache_is_int8 or self._int8_tokhead()))
+                       and (not self.kv_cache_is_int8 or self._int8_tokhead()
+                            or self._int8_chan_step()))
         # A mixed (or prefix-cached prefill) step on a bf16 pool stores and
         # attends in one call: the decode rows append inside the decode launch.
         varlen_append = (not kv_stored and (context.is_mixed or context.is_prefill)
@@ -204,6 +214,15 @@ class Attention(nn.Module):
                     decode_context_lens_list=(context.decode_context_lens_list
                                               if context.is_mixed else None),
                 )
+        if fuse_append and self.kv_cache_is_int8 and not self._int8_tokhead():
+            with self._profile("attention.paged_decode"):
+                return paged_decode_append_int8_chan(
+                    q.view(-1, self.num_heads, self.head_dim),
+                    k.view(-1, self.num_kv_heads, self.head_dim),
+                    v.view(-1, self.num_kv_heads, self.head_dim), k_cache, v_cache,
+                    self.k_scale, self.v_scale, self.k_dscale, self.v_dscale, self.side_k,
+                    self.side_v, self.out_idx2d, self.head_n_out, context.slot_mapping,
+                    context.block_tables, context.context_lens, self.scale)
         if fuse_append and self.kv_cache_is_int8:
             with self._profile("attention.paged_decode"):
                 return paged_decode_append_int8_tokhead(

@@ -522,3 +522,61 @@ def test_int8_chan_decode_append_equals_store_then_decode(n_out_max, decode_path
         n = counts[h]
         assert np.array_equal(bits(flat(sk1.cpu())[sl])[:, h, :n], rsk[:, h, :n])
         assert np.array_equal(bits(flat(sv1.cpu())[sl])[:, h, :n], rsv[:, h, :n])
+
+
+def test_chan_layer_decode_step_is_store_then_decode():
+    """Attention.forward's decode step over a bound per-channel pool (after a
+    calibration freeze) runs the one-call step, and its output, codes and
+    side values equal the engine's two calls, store_kvcache_int8 then
+    paged_decode_attention with the read scales (attention.py:130-177)."""
+    from nanovllm_amd.engine.kv_runner import KVCacheRunner
+    from nanovllm_amd.layers.attention import Attention
+    from nanovllm_amd.utils.context import reset_context, set_context
+    key, value, s_k, s_v, ds_k, ds_v, out_idx2d, head_n_out = p17_unit_inputs()
+    N, KVH, D = key.shape
+    n_out = out_idx2d.shape[1]
+    H, B = 16, 3
+    runner = KVCacheRunner(1, 12, 256, KVH, D, kv_int8="chan", n_out_max=n_out)
+    mod = Attention(H, D, D ** -0.5, KVH)
+    assert runner.bind([mod]) == 1
+    runner.kv_calibrate_begin()
+    mod.kv_observe(0, key.to(DEV), value.to(DEV))
+    runner.kv_calibrate_freeze()
+    assert mod._int8_chan_step()
+    runner.kv_cache.zero_()
+    runner.kv_side.zero_()
+    # three sequences of 512 / 300 / 700 tokens already in the pool, then one step
+    lens = [512, 300, 700]
+    g = torch.Generator().manual_seed(31)
+    bt = build_block_tables([n + 1 for n in lens], 12, 256, g)
+    prior = torch.randn(sum(lens), KVH, D, generator=g).to(torch.bfloat16).to(DEV)
+    pslots = torch.tensor([int(bt[i, t // 256]) * 256 + t % 256
+                           for i, n in enumerate(lens) for t in range(n)],
+                          dtype=torch.int32, device=DEV)
+    store_kvcache_int8(prior, prior.flip(0).contiguous(), mod.k_cache, mod.v_cache, mod.k_scale,
+                       mod.v_scale, mod.side_k, mod.side_v, mod.out_idx2d, mod.head_n_out, pslots)
+    slots = torch.tensor([int(bt[i, n // 256]) * 256 + n % 256 for i, n in enumerate(lens)],
+                         dtype=torch.int32, device=DEV)
+    ctx = torch.tensor([n + 1 for n in lens], dtype=torch.int32, device=DEV)
+    q = torch.randn(B, H * D, generator=g).to(torch.bfloat16).to(DEV)
+    k = torch.randn(B, KVH * D, generator=g).to(torch.bfloat16).to(DEV)
+    v = torch.randn(B, KVH * D, generator=g).to(torch.bfloat16).to(DEV)
+    kc0, vc0 = mod.k_cache.clone(), mod.v_cache.clone()
+    sk0, sv0 = mod.side_k.clone(), mod.side_v.clone()
+    store_kvcache_int8(k.view(B, KVH, D), v.view(B, KVH, D), kc0, vc0, mod.k_scale, mod.v_scale,
+                       sk0, sv0, mod.out_idx2d, mod.head_n_out, slots)
+    ref = paged_decode_attention(q.view(B, H, D), kc0, vc0, bt.to(DEV), ctx, D ** -0.5, 0,
+                                 k_scale=mod.k_dscale, v_scale=mod.v_dscale, side_k=sk0,
+                                 side_v=sv0, out_idx2d=mod.out_idx2d, head_n_out=mod.head_n_out)
+    print("[int8-chan] layer decode step", flush=True)
+    try:
+        set_context(False, slot_mapping=slots, context_lens=ctx, block_tables=bt.to(DEV),
+                    max_context_len=max(lens) + 1)
+        out = mod.forward(q, k, v)
+    finally:
+        reset_context()
+    torch.cuda.synchronize()
+    assert torch.equal(mod.k_cache, kc0) and torch.equal(mod.v_cache, vc0)
+    assert torch.equal(mod.side_k.view(torch.int16), sk0.view(torch.int16))
+    assert torch.equal(mod.side_v.view(torch.int16), sv0.view(torch.int16))
+    assert torch.equal(out.view(B, H, D).view(torch.int16), ref.view(torch.int16))
