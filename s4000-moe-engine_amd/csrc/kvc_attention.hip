@@ -522,15 +522,17 @@ __device__ __forceinline__ void build_q(QOps<kEnc, NCB, kSideN>& Q, const AttnPa
 //   slot0      pool slot of the tile's first key (side pool rows)
 // kMasked = false is the fast path for tiles whose 32 keys are all visible to
 // every valid column (all but the last tile of a decode row).
-// kSideRegs (per-channel int8): the side-pool rows came with the tile (t.sk,
-// t.sv) instead of being read from HBM here.
+// Per-channel int8 side-pool rows: kSideRegs, they came with the tile (t.sk,
+// t.sv); otherwise they are in LDS at side_lds, 16 bytes per key (up to 8
+// slots, padded), K rows of the tile's 32 keys then V rows.
 // ---------------------------------------------------------------------------
 template <int kEnc, int NCB, bool kMasked, bool kSideRegs = false, int kSideN = kSideMax>
 __device__ __forceinline__ void attend_tile(ColState<NCB, kSideN>& st, const Tile<kEnc>& t,
                                             const QOps<kEnc, NCB, kSideN>& Q,
                                             const ColInfo (&ci)[NCB],
                                             int key0, int valid_end, int64_t slot0,
-                                            const AttnParams& p, int g, const LaneId& L) {
+                                            const AttnParams& p, int g, const LaneId& L,
+                                            const char* side_lds = nullptr) {
   bool kvalid[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) kvalid[i] = !kMasked || (key0 + key_of_slot(L.lg, i) < valid_end);
@@ -621,11 +623,12 @@ __device__ __forceinline__ void attend_tile(ColState<NCB, kSideN>& st, const Til
             for (int j = 0; j < kSideN; ++j)
               if (j < n_out) acc += Q.qout[cb][j] * side_value(w, j);
           } else {
-            const uint16_t* srow =
-                p.side_k + ((slot0 + key_of_slot(L.lg, i)) * p.kvh + g) * p.n_out_max;
+            const u32x4_t r =
+                *reinterpret_cast<const u32x4_t*>(side_lds + key_of_slot(L.lg, i) * 16);
+            const uint32_t w[4] = {r[0], r[1], r[2], r[3]};
 #pragma unroll
             for (int j = 0; j < kSideN; ++j)
-              if (j < n_out) acc += Q.qout[cb][j] * bf16_bits_to_f32(srow[j]);
+              if (j < n_out) acc += Q.qout[cb][j] * side_value(w, j);
           }
           x[i] += acc;
         }
@@ -708,11 +711,12 @@ __device__ __forceinline__ void attend_tile(ColState<NCB, kSideN>& st, const Til
               if (j < n_out) st.sd[cb][j] += pr[i] * side_value(w, j);
           } else {
             if (!kvalid[i]) continue;
-            const uint16_t* srow =
-                p.side_v + ((slot0 + key_of_slot(L.lg, i)) * p.kvh + g) * p.n_out_max;
+            const u32x4_t r =
+                *reinterpret_cast<const u32x4_t*>(side_lds + 32 * 16 + key_of_slot(L.lg, i) * 16);
+            const uint32_t w[4] = {r[0], r[1], r[2], r[3]};
 #pragma unroll
             for (int j = 0; j < kSideN; ++j)
-              if (j < n_out) st.sd[cb][j] += pr[i] * bf16_bits_to_f32(srow[j]);
+              if (j < n_out) st.sd[cb][j] += pr[i] * side_value(w, j);
           }
         }
       }
@@ -738,11 +742,14 @@ template <int kEnc, int NCB, bool kSideRegs = false, int kSideN = kSideMax>
 __device__ __forceinline__ void attend(ColState<NCB, kSideN>& st, const Tile<kEnc>& t,
                                        const QOps<kEnc, NCB, kSideN>& Q, const ColInfo (&ci)[NCB],
                                        int key0, int valid_end, int min_klim, int64_t slot0,
-                                       const AttnParams& p, int g, const LaneId& L) {
+                                       const AttnParams& p, int g, const LaneId& L,
+                                       const char* side_lds = nullptr) {
   if (key0 + kTile <= valid_end && key0 + kTile - 1 <= min_klim) {
-    attend_tile<kEnc, NCB, false, kSideRegs>(st, t, Q, ci, key0, valid_end, slot0, p, g, L);
+    attend_tile<kEnc, NCB, false, kSideRegs>(st, t, Q, ci, key0, valid_end, slot0, p, g, L,
+                                             side_lds);
   } else {
-    attend_tile<kEnc, NCB, true, kSideRegs>(st, t, Q, ci, key0, valid_end, slot0, p, g, L);
+    attend_tile<kEnc, NCB, true, kSideRegs>(st, t, Q, ci, key0, valid_end, slot0, p, g, L,
+                                            side_lds);
   }
 }
 
@@ -832,8 +839,9 @@ constexpr int kDecodeSmem = kWaves * int(sizeof(WaveOut));
 constexpr int kPitchBF16 = kD * 2 + 16;
 constexpr int kPitchI8 = kD + 16;
 constexpr int kTileBytesBF16 = kTile * kPitchBF16;
-// Two buffers of (K tile, V tile, K scales, V scales).
-constexpr int kPrefillStage = 2 * kTileBytesBF16 + 2 * kTile * 4;
+// Two buffers of (K tile, V tile, then the per-token-head K and V scales
+// (256 B) or the per-channel side rows (K then V, 16 B per key: 1 KiB)).
+constexpr int kPrefillStage = 2 * kTileBytesBF16 + 2 * kTile * 16;
 constexpr int kPrefillSmem = 2 * kPrefillStage;
 constexpr int kSmemBytes = kDecodeSmem > kPrefillSmem ? kDecodeSmem : kPrefillSmem;
 
@@ -2749,6 +2757,7 @@ __device__ void prefill_segment(const AttnParams& p, char* smem, const int32_t* 
   // register set `set`; two sets keep two tiles in flight.
   u32x4_t pre[2][kLoadsPerThread];
   float pre_s[2] = {0.f, 0.f};
+  u32x4_t pre_side[2] = {u32x4_t{0u, 0u, 0u, 0u}, u32x4_t{0u, 0u, 0u, 0u}};
   auto fetch = [&](int set, int64_t slot0, int key0) {
 #pragma unroll
     for (int e = 0; e < kLoadsPerThread; ++e) {
@@ -2779,6 +2788,38 @@ __device__ void prefill_segment(const AttnParams& p, char* smem, const int32_t* 
         pre_s[set] = (key0 + key < sk) ? sp[(slot0 + key) * p.kvh + g] : 0.f;
       }
     }
+    if constexpr (kEnc == kI8Chan) {
+      // The side rows of the tile's keys for kv head g (n_out_max bf16 each,
+      // a power of two up to 8): wave 0's lane k brings key k's K row, lane
+      // 32 + k its V row, dword by dword through buffer resources (past the
+      // row or the context: 0, no traffic).
+      if (threadIdx.x < 2 * kTile) {
+        const int nom = p.n_out_max;
+        const int key = threadIdx.x & (kTile - 1);
+        const bool vside = threadIdx.x >= kTile;
+        const bool has = p.head_n_out != nullptr && key0 + key < sk;
+        const int row = p.kvh * nom * 2;  // bytes between consecutive slots
+        const int bytes = ((kTile - 1) * p.kvh + 1) * nom * 2;
+        const int64_t first = (slot0 * p.kvh + g) * nom;
+        const __amdgpu_buffer_rsrc_t kr = wave_rsrc(p.side_k + first, bytes);
+        const __amdgpu_buffer_rsrc_t vr = wave_rsrc(p.side_v + first, bytes);
+        const int base = key * row;
+        const int big = 0x40000000;
+        u32x4_t w;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const bool ok = has && 4 * d + 4 <= 2 * nom;
+          const uint32_t a = __builtin_amdgcn_raw_buffer_load_b32(kr, ok && !vside ? base + 4 * d : big, 0, 0);
+          const uint32_t b = __builtin_amdgcn_raw_buffer_load_b32(vr, ok && vside ? base + 4 * d : big, 0, 0);
+          w[d] = a | b;
+        }
+        // a 2-byte row (n_out_max 1)
+        const bool one = has && nom == 1;
+        w[0] |= uint32_t(__builtin_amdgcn_raw_buffer_load_b16(kr, one && !vside ? base : big, 0, 0)) |
+                uint32_t(__builtin_amdgcn_raw_buffer_load_b16(vr, one && vside ? base : big, 0, 0));
+        pre_side[set] = w;
+      }
+    }
   };
   auto commit = [&](int set, int buf) {
     char* st_base = stage_ptr(buf);
@@ -2797,6 +2838,10 @@ __device__ void prefill_segment(const AttnParams& p, char* smem, const int32_t* 
     if constexpr (kEnc == kI8Tok) {
       if (threadIdx.x < 2 * kTile)
         reinterpret_cast<float*>(st_base + 2 * kTileBytesBF16)[threadIdx.x] = pre_s[set];
+    }
+    if constexpr (kEnc == kI8Chan) {
+      if (threadIdx.x < 2 * kTile)
+        reinterpret_cast<u32x4_t*>(st_base + 2 * kTileBytesBF16)[threadIdx.x] = pre_side[set];
     }
   };
   // LDS -> operand registers, same lane mapping as the HBM loads.
@@ -2859,7 +2904,8 @@ __device__ void prefill_segment(const AttnParams& p, char* smem, const int32_t* 
           Tile<kEnc> t;
           read_tile(t, r);
           attend<kEnc, kPreNCB>(st, t, Q, ci, k_begin + tix * kTile, sk, min_klim,
-                                kFresh ? -1 : slots[0], p, g, L);
+                                kFresh ? -1 : slots[0], p, g, L,
+                                stage_ptr(r) + 2 * kTileBytesBF16);
           if (tix + 1 < ntiles) commit(1 - r, 1 - r);
           __syncthreads();
           slots[0] = slots[1];
