@@ -244,6 +244,24 @@ def kv_float(cache, fmt: str, scale=None, side=None, out_idx2d=None, head_n_out=
     raise ValueError(fmt)
 
 
+def kv_float_prefill(cache, fmt: str, scale=None, side=None, out_idx2d=None, head_n_out=None):
+    """Pool -> fp32 values as the reference's prefill reads them
+    (nanovllm/layers/attention.py:33-51, _gather_kv): an int8 pool is
+    dequantised to bf16 (bf16(fp32(code) * scale), the side pool's exact
+    values at the outlier dims) before the bf16 attention, i.e.
+    dequant_chan / dequant_tokhead over the whole pool."""
+    if fmt == "bf16":
+        return bf16_to_f32(cache)
+    if fmt == "int8_tokhead":
+        return bf16_to_f32(dequant_tokhead(cache, scale))
+    if fmt == "int8_chan":
+        kvh, d = cache.shape[-2:]
+        sb = None if side is None else side.reshape(-1, kvh, side.shape[-1])
+        bits = dequant_chan(cache.reshape(-1, kvh, d), scale, sb, out_idx2d, head_n_out)
+        return bf16_to_f32(bits.reshape(cache.shape))
+    raise ValueError(fmt)
+
+
 def attend_rows(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float,
                 allowed: np.ndarray | None = None) -> np.ndarray:
     """softmax(q k^T * scale) v per head in fp32.  q [Sq, H, D]; k, v [Sk, KVH, D]
@@ -310,12 +328,16 @@ def prefill_ref(q_bits, k_f32, v_f32, block_tables, cu_q, cu_k, scale, row_offse
 
 
 def mixed_ref(q_bits, k_f32, v_f32, block_tables, num_decode_rows, decode_context_lens, cu_q, cu_k,
-              scale) -> np.ndarray:
+              scale, k_pre=None, v_pre=None) -> np.ndarray:
     """Mixed batch (attention.py:146-166): decode rows through the decode
-    reference, then prefill rows with block table rows num_decode_rows + i."""
+    reference, then prefill rows with block table rows num_decode_rows + i.
+    k_pre / v_pre: the pool as the prefill reads it, when that differs from
+    the decode's read (an int8 pool: kv_float_prefill against kv_float)."""
     n = num_decode_rows
     dec = paged_decode_ref(q_bits[:n], k_f32, v_f32, block_tables[:n], decode_context_lens, scale)
-    pre = prefill_ref(q_bits[n:], k_f32, v_f32, block_tables, cu_q, cu_k, scale, row_offset=n)
+    pre = prefill_ref(q_bits[n:], k_f32 if k_pre is None else k_pre,
+                      v_f32 if v_pre is None else v_pre, block_tables, cu_q, cu_k, scale,
+                      row_offset=n)
     return np.concatenate([dec, pre], axis=0)
 
 

@@ -44,6 +44,7 @@ constexpr int kTile = 32;
 constexpr int kWaves = 8;  // two waves per SIMD
 constexpr int kThreads = 64 * kWaves;
 constexpr int kSideMax = 8;
+constexpr int kPitchBF16 = kD * 2 + 16;  // a bf16 key row in LDS (16 B pad)
 constexpr int kPreNCB = 2;  // column blocks per wave in prefill units
 constexpr float kRescaleLog2 = 8.f;  // lazy-rescale threshold (log2 units)
 // Virtual tiles per row of a ragged stream-K decode (see decode_sk_share):
@@ -522,17 +523,28 @@ __device__ __forceinline__ void build_q(QOps<kEnc, NCB, kSideN>& Q, const AttnPa
 //   slot0      pool slot of the tile's first key (side pool rows)
 // kMasked = false is the fast path for tiles whose 32 keys are all visible to
 // every valid column (all but the last tile of a decode row).
-// Per-channel int8 side-pool rows: kSideRegs, they came with the tile (t.sk,
-// t.sv); otherwise they are in LDS at side_lds, 16 bytes per key (up to 8
-// slots, padded), K rows of the tile's 32 keys then V rows.
+// Per-channel int8 (the register decode segment): the side-pool rows came
+// with the tile (t.sk, t.sv).
+// kPLo (bf16 tiles dequantised from a per-channel pool, whose outlier dims
+// hold the side pool's values): the PV product of the outlier dims also takes
+// the rounding residue of the bf16 P operand, P - bf16(P), so that the large
+// side values meet an fp32-accurate P.  plo_v is the tile's V rows in LDS
+// (pitch kPitchBF16), plo_dim the outlier dim of side slot lm (lanes
+// lm < n_plo); plo[cb] accumulates the residue product, C row j = slot j,
+// column = the lane's query column.
 // ---------------------------------------------------------------------------
-template <int kEnc, int NCB, bool kMasked, bool kSideRegs = false, int kSideN = kSideMax>
+template <int kEnc, int NCB, bool kMasked, bool kSideRegs = false, int kSideN = kSideMax,
+          bool kPLo = false>
 __device__ __forceinline__ void attend_tile(ColState<NCB, kSideN>& st, const Tile<kEnc>& t,
                                             const QOps<kEnc, NCB, kSideN>& Q,
                                             const ColInfo (&ci)[NCB],
                                             int key0, int valid_end, int64_t slot0,
                                             const AttnParams& p, int g, const LaneId& L,
-                                            const char* side_lds = nullptr) {
+                                            const char* plo_v = nullptr,
+                                            f32x4_t* plo = nullptr, int n_plo = 0,
+                                            int plo_dim = 0) {
+  static_assert(kEnc != kI8Chan || kSideRegs, "per-channel tiles carry their side rows");
+  static_assert(!kPLo || kEnc == kBF16, "the residue product is for bf16 tiles");
   bool kvalid[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) kvalid[i] = !kMasked || (key0 + key_of_slot(L.lg, i) < valid_end);
@@ -616,20 +628,11 @@ __device__ __forceinline__ void attend_tile(ColState<NCB, kSideN>& st, const Til
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           float acc = 0.f;
-          if constexpr (kSideRegs) {
-            uint32_t w[4];
-            side_row_of_slot<kSideN>(w, t.sk, i);
+          uint32_t w[4];
+          side_row_of_slot<kSideN>(w, t.sk, i);
 #pragma unroll
-            for (int j = 0; j < kSideN; ++j)
-              if (j < n_out) acc += Q.qout[cb][j] * side_value(w, j);
-          } else {
-            const u32x4_t r =
-                *reinterpret_cast<const u32x4_t*>(side_lds + key_of_slot(L.lg, i) * 16);
-            const uint32_t w[4] = {r[0], r[1], r[2], r[3]};
-#pragma unroll
-            for (int j = 0; j < kSideN; ++j)
-              if (j < n_out) acc += Q.qout[cb][j] * side_value(w, j);
-          }
+          for (int j = 0; j < kSideN; ++j)
+            if (j < n_out) acc += Q.qout[cb][j] * side_value(w, j);
           x[i] += acc;
         }
       }
@@ -665,6 +668,10 @@ __device__ __forceinline__ void attend_tile(ColState<NCB, kSideN>& st, const Til
         st.o[cb][jj][2] *= alpha;
         st.o[cb][jj][3] *= alpha;
       }
+      if constexpr (kPLo) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) plo[cb][r] *= alpha;
+      }
     }
     const float m_use = (st.m[cb] == -INFINITY) ? 0.f : st.m[cb];
     float pr[8], psum = 0.f;
@@ -688,6 +695,26 @@ __device__ __forceinline__ void attend_tile(ColState<NCB, kSideN>& st, const Til
     u32x4_t pb;
 #pragma unroll
     for (int w = 0; w < 4; ++w) pb[w] = pack_bf16x2_fast(pv[2 * w], pv[2 * w + 1]);
+    if constexpr (kPLo) {
+      if (n_plo > 0) {
+        // Residue A operand: row j = lm (side slot j, whose value the V tile
+        // holds at dim plo_dim), the lane's 8 key slots; rows past n_plo 0.
+        uint32_t e[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          e[i] = L.lm < n_plo ? *reinterpret_cast<const uint16_t*>(
+                                    plo_v + key_of_slot(L.lg, i) * kPitchBF16 + 2 * plo_dim)
+                              : 0u;
+        const u32x4_t plo_op = u32x4_t{e[0] | (e[1] << 16), e[2] | (e[3] << 16),
+                                       e[4] | (e[5] << 16), e[6] | (e[7] << 16)};
+        u32x4_t pl;
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+          pl[w] = pack_bf16x2_fast(pv[2 * w] - bf16_bits_to_f32(pb[w] & 0xffffu),
+                                   pv[2 * w + 1] - bf16_bits_to_f32(pb[w] >> 16));
+        plo[cb] = mfma_bf16(plo_op, pl, plo[cb]);
+      }
+    }
     if constexpr (kEnc != kBF16) {
       float vsum = 0.f;
 #pragma unroll
@@ -700,24 +727,14 @@ __device__ __forceinline__ void attend_tile(ColState<NCB, kSideN>& st, const Til
         for (int j = 0; j < kSideN; ++j) st.sd[cb][j] *= alpha;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          if constexpr (kSideRegs) {
-            // Every lane of a 16-lane row shares kvalid[i]: the row read
-            // stays outside the branch all the same.
-            uint32_t w[4];
-            side_row_of_slot<kSideN>(w, t.sv, i);
-            if (!kvalid[i]) continue;
+          // Every lane of a 16-lane row shares kvalid[i]: the row read stays
+          // outside the branch all the same.
+          uint32_t w[4];
+          side_row_of_slot<kSideN>(w, t.sv, i);
+          if (!kvalid[i]) continue;
 #pragma unroll
-            for (int j = 0; j < kSideN; ++j)
-              if (j < n_out) st.sd[cb][j] += pr[i] * side_value(w, j);
-          } else {
-            if (!kvalid[i]) continue;
-            const u32x4_t r =
-                *reinterpret_cast<const u32x4_t*>(side_lds + 32 * 16 + key_of_slot(L.lg, i) * 16);
-            const uint32_t w[4] = {r[0], r[1], r[2], r[3]};
-#pragma unroll
-            for (int j = 0; j < kSideN; ++j)
-              if (j < n_out) st.sd[cb][j] += pr[i] * side_value(w, j);
-          }
+          for (int j = 0; j < kSideN; ++j)
+            if (j < n_out) st.sd[cb][j] += pr[i] * side_value(w, j);
         }
       }
     }
@@ -738,18 +755,19 @@ __device__ __forceinline__ void attend_tile(ColState<NCB, kSideN>& st, const Til
 
 // Full tiles take the unmasked path; a tile with a key at or past valid_end,
 // or past some valid column's limit, takes the masked one.
-template <int kEnc, int NCB, bool kSideRegs = false, int kSideN = kSideMax>
+template <int kEnc, int NCB, bool kSideRegs = false, int kSideN = kSideMax, bool kPLo = false>
 __device__ __forceinline__ void attend(ColState<NCB, kSideN>& st, const Tile<kEnc>& t,
                                        const QOps<kEnc, NCB, kSideN>& Q, const ColInfo (&ci)[NCB],
                                        int key0, int valid_end, int min_klim, int64_t slot0,
                                        const AttnParams& p, int g, const LaneId& L,
-                                       const char* side_lds = nullptr) {
+                                       const char* plo_v = nullptr, f32x4_t* plo = nullptr,
+                                       int n_plo = 0, int plo_dim = 0) {
   if (key0 + kTile <= valid_end && key0 + kTile - 1 <= min_klim) {
-    attend_tile<kEnc, NCB, false, kSideRegs>(st, t, Q, ci, key0, valid_end, slot0, p, g, L,
-                                             side_lds);
+    attend_tile<kEnc, NCB, false, kSideRegs, kSideN, kPLo>(st, t, Q, ci, key0, valid_end, slot0,
+                                                           p, g, L, plo_v, plo, n_plo, plo_dim);
   } else {
-    attend_tile<kEnc, NCB, true, kSideRegs>(st, t, Q, ci, key0, valid_end, slot0, p, g, L,
-                                            side_lds);
+    attend_tile<kEnc, NCB, true, kSideRegs, kSideN, kPLo>(st, t, Q, ci, key0, valid_end, slot0,
+                                                          p, g, L, plo_v, plo, n_plo, plo_dim);
   }
 }
 
@@ -836,13 +854,11 @@ __device__ __forceinline__ void store_partial(const AttnParams& p, int64_t row, 
 }
 
 constexpr int kDecodeSmem = kWaves * int(sizeof(WaveOut));
-constexpr int kPitchBF16 = kD * 2 + 16;
-constexpr int kPitchI8 = kD + 16;
 constexpr int kTileBytesBF16 = kTile * kPitchBF16;
-// Two buffers of (K tile, V tile, then the per-token-head K and V scales
-// (256 B) or the per-channel side rows (K then V, 16 B per key: 1 KiB)).
-constexpr int kPrefillStage = 2 * kTileBytesBF16 + 2 * kTile * 16;
-constexpr int kPrefillSmem = 2 * kPrefillStage;
+// Two buffers of (K tile, V tile) in bf16 (an int8 pool's tiles are
+// dequantised on their way in), then the per-channel read scales (1 KiB).
+constexpr int kPrefillStage = 2 * kTileBytesBF16;
+constexpr int kPrefillSmem = 2 * kPrefillStage + 2 * kD * 4;
 constexpr int kSmemBytes = kDecodeSmem > kPrefillSmem ? kDecodeSmem : kPrefillSmem;
 
 // ---------------------------------------------------------------------------
@@ -2692,6 +2708,11 @@ __device__ __forceinline__ void store_prefill_block(const AttnParams& p, const C
 template <int kEnc, bool kFresh>
 __device__ void prefill_segment(const AttnParams& p, char* smem, const int32_t* bt_base, int i,
                                 int qt, int kvs, int t0, int t1, int split) {
+  // An int8 pool's tiles are dequantised to bf16 as they are committed to
+  // LDS (the reference's prefill reads the pool through dequant_gathered,
+  // nanovllm/kernels/kv_int8.py:96-107, then attends in bf16), so the
+  // attention itself is the bf16 path (kCmp) whatever the pool encoding.
+  constexpr int kCmp = kBF16;
   const LaneId L = lane_id();
   const int wave = uniform(int(threadIdx.x >> 6));  // wave-uniform (scalar) index
   const int g = kvs / p.nslices;
@@ -2716,8 +2737,8 @@ __device__ void prefill_segment(const AttnParams& p, char* smem, const int32_t* 
     ci[cb].valid = ok;
     ci[cb].klim = ok ? prefix + tq : -1;
   }
-  QOps<kEnc, kPreNCB> Q;
-  build_q<kEnc, kPreNCB>(Q, p, ci, g, L);
+  QOps<kCmp, kPreNCB> Q;
+  build_q<kCmp, kPreNCB>(Q, p, ci, g, L);
   ColState<kPreNCB> st;
   init_state(st);
   // Smallest key limit over the wave's valid columns: tiles entirely below it
@@ -2736,9 +2757,10 @@ __device__ void prefill_segment(const AttnParams& p, char* smem, const int32_t* 
   const int ntiles = k_end > k_begin ? (k_end - k_begin + kTile - 1) / kTile : 0;
 
   const int32_t* bt = kFresh ? nullptr : bt_base + int64_t(p.n_dec + i) * p.bt_stride;
-  constexpr int kPitch = (kEnc == kBF16) ? kPitchBF16 : kPitchI8;
-  constexpr int kRowBytes = (kEnc == kBF16) ? kD * 2 : kD;
+  constexpr int kPitch = kPitchBF16;  // the stage holds bf16 rows
+  constexpr int kRowBytes = (kEnc == kBF16) ? kD * 2 : kD;  // a pool row
   constexpr int kVecPerRow = kRowBytes / 16;
+  static_assert(kEnc != kI8Chan || kVecPerRow >= kSideMax, "a key's chunk lanes hold its side row");
   constexpr int kVecPerTile = kTile * kVecPerRow;  // per tensor
   constexpr int kLoadsPerThread = (2 * kVecPerTile + kThreads - 1) / kThreads;
   const int64_t head_off = int64_t(g) * kRowBytes;
@@ -2756,14 +2778,46 @@ __device__ void prefill_segment(const AttnParams& p, char* smem, const int32_t* 
   // Cooperative global -> register fetch of one tile (16 B per element) into
   // register set `set`; two sets keep two tiles in flight.
   u32x4_t pre[2][kLoadsPerThread];
-  float pre_s[2] = {0.f, 0.f};
-  u32x4_t pre_side[2] = {u32x4_t{0u, 0u, 0u, 0u}, u32x4_t{0u, 0u, 0u, 0u}};
-  auto fetch = [&](int set, int64_t slot0, int key0) {
+  // int8 pools: the element's dequantisation scale (per-token-head) or one
+  // side value of its key (per-channel)
+  float pre_sc[2][kLoadsPerThread];
+  uint32_t pre_sd[2][kLoadsPerThread];
+  // live = false (int8 pools): issue the loads all the same, out of range
+  // (no traffic, 0), so that every iteration has the same loads in flight
+  // and the commit's waits count only the loads it needs.
+  auto fetch = [&](int set, int64_t slot0, int key0, bool live) {
 #pragma unroll
     for (int e = 0; e < kLoadsPerThread; ++e) {
       const int idx = e * kThreads + threadIdx.x;
       pre[set][e] = u32x4_t{0u, 0u, 0u, 0u};
-      if (idx < 2 * kVecPerTile) {
+      if constexpr (kEnc == kI8Tok) pre_sc[set][e] = 0.f;
+      if constexpr (kEnc != kBF16) {
+        // int8 pools: one buffer load and no branch (a key past the chunk
+        // reads 0).  Under a branch the code unpacking of the commit would
+        // be folded into the branch, and the load's wait with it.
+        const int tensor = idx / kVecPerTile;  // wave-uniform
+        const int rem = idx - tensor * kVecPerTile;
+        const int key = rem / kVecPerRow;
+        const int vec = rem - key * kVecPerRow;
+        const uintptr_t kc = reinterpret_cast<uintptr_t>(p.k_cache);
+        const uintptr_t vc = reinterpret_cast<uintptr_t>(p.v_cache);
+        const char* base = reinterpret_cast<const char*>(kc + (vc - kc) * uintptr_t(tensor != 0)) +
+                           slot0 * p.tok_bytes + head_off;
+        const __amdgpu_buffer_rsrc_t rs = wave_rsrc(base, int((kTile - 1) * p.tok_bytes) + kRowBytes);
+        const bool ok = live && idx < 2 * kVecPerTile && key0 + key < sk;
+        pre[set][e] = __builtin_bit_cast(
+            u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                         rs, ok ? int(key * p.tok_bytes) + vec * 16 : 0x40000000, 0, 0));
+        if constexpr (kEnc == kI8Tok) {
+          const uintptr_t ksc = reinterpret_cast<uintptr_t>(p.k_scale);
+          const uintptr_t vsc = reinterpret_cast<uintptr_t>(p.v_scale);
+          const float* sbase = reinterpret_cast<const float*>(ksc + (vsc - ksc) * uintptr_t(tensor != 0)) +
+                               slot0 * p.kvh + g;
+          const __amdgpu_buffer_rsrc_t ss = wave_rsrc(sbase, ((kTile - 1) * p.kvh + 1) * 4);
+          pre_sc[set][e] = __builtin_bit_cast(
+              float, __builtin_amdgcn_raw_buffer_load_b32(ss, ok ? key * p.kvh * 4 : 0x40000000, 0, 0));
+        }
+      } else if (idx < 2 * kVecPerTile) {
         const int tensor = idx / kVecPerTile;
         const int rem = idx - tensor * kVecPerTile;
         const int key = rem / kVecPerRow;
@@ -2780,47 +2834,45 @@ __device__ void prefill_segment(const AttnParams& p, char* smem, const int32_t* 
           }
         }
       }
-    }
-    if constexpr (kEnc == kI8Tok) {
-      if (threadIdx.x < 2 * kTile) {
-        const int key = threadIdx.x & (kTile - 1);
-        const float* sp = (threadIdx.x < kTile) ? p.k_scale : p.v_scale;
-        pre_s[set] = (key0 + key < sk) ? sp[(slot0 + key) * p.kvh + g] : 0.f;
-      }
-    }
-    if constexpr (kEnc == kI8Chan) {
-      // The side rows of the tile's keys for kv head g (n_out_max bf16 each,
-      // a power of two up to 8): wave 0's lane k brings key k's K row, lane
-      // 32 + k its V row, dword by dword through buffer resources (past the
-      // row or the context: 0, no traffic).
-      if (threadIdx.x < 2 * kTile) {
+      if constexpr (kEnc == kI8Chan) {
+        // The dword holding one side value of the element's key (K rows for
+        // tensor 0, V rows for tensor 1, the tensor being wave-uniform): the
+        // lane of chunk v holds slot v's, so the 8 lanes of a key hold its
+        // row (n_out_max <= 8 slots).  Whole aligned dwords (a 16-bit load
+        // result would be widened by a copy that waits for it); slots past
+        // n_out_max and keys past the chunk read 0 (no traffic).
+        const int tensor = idx / kVecPerTile;
+        const int key = (idx - tensor * kVecPerTile) / kVecPerRow;
+        const int slot = idx & (kVecPerRow - 1);
         const int nom = p.n_out_max;
-        const int key = threadIdx.x & (kTile - 1);
-        const bool vside = threadIdx.x >= kTile;
-        const bool has = p.head_n_out != nullptr && key0 + key < sk;
-        const int row = p.kvh * nom * 2;  // bytes between consecutive slots
-        const int bytes = ((kTile - 1) * p.kvh + 1) * nom * 2;
-        const int64_t first = (slot0 * p.kvh + g) * nom;
-        const __amdgpu_buffer_rsrc_t kr = wave_rsrc(p.side_k + first, bytes);
-        const __amdgpu_buffer_rsrc_t vr = wave_rsrc(p.side_v + first, bytes);
-        const int base = key * row;
-        const int big = 0x40000000;
-        u32x4_t w;
-#pragma unroll
-        for (int d = 0; d < 4; ++d) {
-          const bool ok = has && 4 * d + 4 <= 2 * nom;
-          const uint32_t a = __builtin_amdgcn_raw_buffer_load_b32(kr, ok && !vside ? base + 4 * d : big, 0, 0);
-          const uint32_t b = __builtin_amdgcn_raw_buffer_load_b32(vr, ok && vside ? base + 4 * d : big, 0, 0);
-          w[d] = a | b;
-        }
-        // a 2-byte row (n_out_max 1)
-        const bool one = has && nom == 1;
-        w[0] |= uint32_t(__builtin_amdgcn_raw_buffer_load_b16(kr, one && !vside ? base : big, 0, 0)) |
-                uint32_t(__builtin_amdgcn_raw_buffer_load_b16(vr, one && vside ? base : big, 0, 0));
-        pre_side[set] = w;
+        const bool has = live && p.head_n_out != nullptr && idx < 2 * kVecPerTile && key0 + key < sk;
+        const uintptr_t ks = reinterpret_cast<uintptr_t>(p.side_k);
+        const uintptr_t vs = reinterpret_cast<uintptr_t>(p.side_v);
+        const uint16_t* sbase = reinterpret_cast<const uint16_t*>(ks + (vs - ks) * uintptr_t(tensor != 0));
+        // all heads of the tile's 32 slots (a tile lies in one block)
+        const __amdgpu_buffer_rsrc_t rs = wave_rsrc(sbase + slot0 * p.kvh * nom, kTile * p.kvh * nom * 2);
+        const int el = (key * p.kvh + g) * nom + slot;
+        pre_sd[set][e] = __builtin_amdgcn_raw_buffer_load_b32(rs, has && slot < nom ? (2 * el) & ~3 : 0x40000000, 0, 0);
       }
     }
   };
+  // (per-channel) the read scales of kv head g, K then V, in LDS after the
+  // two stages: filled once per segment, read at every commit.
+  float* const sc_lds = reinterpret_cast<float*>(smem + 2 * kPrefillStage);
+  if constexpr (kEnc == kI8Chan) {
+    if (threadIdx.x < 2 * kD)
+      sc_lds[threadIdx.x] = (threadIdx.x < kD ? p.k_scale : p.v_scale)[g * kD + (threadIdx.x & (kD - 1))];
+    __syncthreads();
+  }
+  const int n_out = (kEnc == kI8Chan && p.head_n_out != nullptr)
+                        ? min(table_entry(p.head_n_out, g), int(p.n_out_max))
+                        : 0;
+  // (per-channel) the outlier dim of side slot lm, for the residue product
+  const int plo_dim =
+      (kEnc == kI8Chan && L.lm < n_out) ? (p.out_idx[int64_t(g) * p.n_out_max + L.lm] & (kD - 1)) : 0;
+  f32x4_t plo[kPreNCB];
+#pragma unroll
+  for (int cb = 0; cb < kPreNCB; ++cb) plo[cb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   auto commit = [&](int set, int buf) {
     char* st_base = stage_ptr(buf);
 #pragma unroll
@@ -2831,49 +2883,67 @@ __device__ void prefill_segment(const AttnParams& p, char* smem, const int32_t* 
         const int rem = idx - tensor * kVecPerTile;
         const int key = rem / kVecPerRow;
         const int vec = rem - key * kVecPerRow;
-        char* dst = st_base + tensor * kTileBytesBF16 + key * kPitch + vec * 16;
-        *reinterpret_cast<u32x4_t*>(dst) = pre[set][e];
+        if constexpr (kEnc == kBF16) {
+          char* dst = st_base + tensor * kTileBytesBF16 + key * kPitch + vec * 16;
+          *reinterpret_cast<u32x4_t*>(dst) = pre[set][e];
+        } else {
+          // 16 codes, dims 16 vec .. + 15, to bf16 exactly as the dequant
+          // kernels round them: bf16(float(code) * scale), nearest-even.
+          const u32x4_t c = pre[set][e];
+          uint32_t o[8];
+          if constexpr (kEnc == kI8Tok) {
+            const float sc = pre_sc[set][e];
+#pragma unroll
+            for (int w2 = 0; w2 < 8; ++w2) {
+              const uint32_t word = c[w2 >> 1];
+              const int sh = (w2 & 1) * 16;
+              o[w2] = pack_bf16x2_fast(float(int8_t((word >> sh) & 0xffu)) * sc,
+                                       float(int8_t((word >> (sh + 8)) & 0xffu)) * sc);
+            }
+          } else {
+            const float* ds = sc_lds + tensor * kD + vec * 16;
+#pragma unroll
+            for (int w2 = 0; w2 < 8; ++w2) {
+              const uint32_t word = c[w2 >> 1];
+              const int sh = (w2 & 1) * 16;
+              o[w2] = pack_bf16x2_fast(float(int8_t((word >> sh) & 0xffu)) * ds[2 * w2],
+                                       float(int8_t((word >> (sh + 8)) & 0xffu)) * ds[2 * w2 + 1]);
+            }
+          }
+          char* dst = st_base + tensor * kTileBytesBF16 + key * kPitch + vec * 32;
+          *reinterpret_cast<u32x4_t*>(dst) = u32x4_t{o[0], o[1], o[2], o[3]};
+          *reinterpret_cast<u32x4_t*>(dst + 16) = u32x4_t{o[4], o[5], o[6], o[7]};
+          if constexpr (kEnc == kI8Chan) {
+            // The head's outlier dims take the side row's exact values: the
+            // lane that wrote the chunk rewrites them (one lane's LDS writes
+            // land in order), slot by slot, so that a later slot wins on a
+            // duplicate dim, like dequant_chan.
+            const int kl = L.lane & ~7;  // lane of the key's chunk 0 (slot 0)
+            for (int j = 0; j < n_out; ++j) {
+              const uint32_t w = __shfl(pre_sd[set][e], kl + j, 64);
+              const int el = (key * p.kvh + g) * p.n_out_max + j;
+              const uint16_t sv = uint16_t((el & 1) ? (w >> 16) : (w & 0xffffu));
+              const int d = table_entry(p.out_idx, int64_t(g) * p.n_out_max + j);
+              if ((d >> 4) == vec) *reinterpret_cast<uint16_t*>(dst + 2 * (d & 15)) = sv;
+            }
+          }
+        }
       }
-    }
-    if constexpr (kEnc == kI8Tok) {
-      if (threadIdx.x < 2 * kTile)
-        reinterpret_cast<float*>(st_base + 2 * kTileBytesBF16)[threadIdx.x] = pre_s[set];
-    }
-    if constexpr (kEnc == kI8Chan) {
-      if (threadIdx.x < 2 * kTile)
-        reinterpret_cast<u32x4_t*>(st_base + 2 * kTileBytesBF16)[threadIdx.x] = pre_side[set];
     }
   };
   // LDS -> operand registers, same lane mapping as the HBM loads.
-  auto read_tile = [&](Tile<kEnc>& t, int buf) {
+  auto read_tile = [&](Tile<kCmp>& t, int buf) {
     const char* kb = stage_ptr(buf);
     const char* vb = kb + kTileBytesBF16;
-    if constexpr (kEnc == kBF16) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const char* row = kb + (h * 16 + L.lm) * kPitch + L.lg * 16;
+    for (int h = 0; h < 2; ++h) {
+      const char* row = kb + (h * 16 + L.lm) * kPitch + L.lg * 16;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) t.k[h][c] = *reinterpret_cast<const u32x4_t*>(row + c * 64);
-      }
-#pragma unroll
-      for (int ii = 0; ii < 8; ++ii)
-        t.v[ii] = *reinterpret_cast<const u32x4_t*>(vb + key_of_slot(L.lg, ii) * kPitch + L.lm * 16);
-    } else {
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const char* row = kb + (h * 16 + L.lm) * kPitch + L.lg * 32;
-        t.k[h][0] = *reinterpret_cast<const u32x4_t*>(row);
-        t.k[h][1] = *reinterpret_cast<const u32x4_t*>(row + 16);
-      }
-#pragma unroll
-      for (int ii = 0; ii < 8; ++ii)
-        t.v[ii] = *reinterpret_cast<const u32x2_t*>(vb + key_of_slot(L.lg, ii) * kPitch + L.lm * 8);
-      if constexpr (kEnc == kI8Tok) {
-        // Same lane order as load_scales_buf: K scales then V scales.
-        t.sck = reinterpret_cast<const float*>(kb + 2 * kTileBytesBF16)[L.lane];
-        t.scv = 0.f;
-      }
+      for (int c = 0; c < 4; ++c) t.k[h][c] = *reinterpret_cast<const u32x4_t*>(row + c * 64);
     }
+#pragma unroll
+    for (int ii = 0; ii < 8; ++ii)
+      t.v[ii] = *reinterpret_cast<const u32x4_t*>(vb + key_of_slot(L.lg, ii) * kPitch + L.lm * 16);
   };
 
   if (ntiles > 0) {
@@ -2883,12 +2953,12 @@ __device__ void prefill_segment(const AttnParams& p, char* smem, const int32_t* 
     // compute cover each tile's global latency.
     int64_t slots[3];
     slots[0] = tile_slot0(0);
-    fetch(0, slots[0], k_begin);
+    fetch(0, slots[0], k_begin, true);
     commit(0, 0);
     slots[1] = 0;
     if (ntiles > 1) {
       slots[1] = tile_slot0(1);
-      fetch(1, slots[1], k_begin + kTile);
+      fetch(1, slots[1], k_begin + kTile, true);
     }
     __syncthreads();
     for (int j0 = 0; j0 < ntiles; j0 += 2) {
@@ -2897,15 +2967,18 @@ __device__ void prefill_segment(const AttnParams& p, char* smem, const int32_t* 
         const int tix = j0 + r;
         if (tix < ntiles) {
           slots[2] = 0;
-          if (tix + 2 < ntiles) {
-            slots[2] = tile_slot0(tix + 2);
-            fetch(r, slots[2], k_begin + (tix + 2) * kTile);
+          const bool more = tix + 2 < ntiles;
+          if (more) slots[2] = tile_slot0(tix + 2);
+          if constexpr (kEnc != kBF16) {
+            fetch(r, slots[2], k_begin + (tix + 2) * kTile, more);
+          } else if (more) {
+            fetch(r, slots[2], k_begin + (tix + 2) * kTile, true);
           }
-          Tile<kEnc> t;
+          Tile<kCmp> t;
           read_tile(t, r);
-          attend<kEnc, kPreNCB>(st, t, Q, ci, k_begin + tix * kTile, sk, min_klim,
-                                kFresh ? -1 : slots[0], p, g, L,
-                                stage_ptr(r) + 2 * kTileBytesBF16);
+          attend<kCmp, kPreNCB, false, kSideMax, kEnc == kI8Chan>(
+              st, t, Q, ci, k_begin + tix * kTile, sk, min_klim, kFresh ? -1 : slots[0], p, g, L,
+              stage_ptr(r) + kTileBytesBF16, plo, n_out, plo_dim);
           if (tix + 1 < ntiles) commit(1 - r, 1 - r);
           __syncthreads();
           slots[0] = slots[1];
@@ -2916,45 +2989,37 @@ __device__ void prefill_segment(const AttnParams& p, char* smem, const int32_t* 
   }
 
   // Epilogue: each wave finalises its own columns (no cross-wave merge).
-  if constexpr (kEnc == kI8Chan) {
-    // The outlier dims come from the side pool: the block goes through LDS so
-    // that their exact values can replace the main path's zeros.
-    WaveOut* wo = reinterpret_cast<WaveOut*>(smem);
+  {
 #pragma unroll
     for (int cb = 0; cb < kPreNCB; ++cb) {
-      dump_block<kEnc, kPreNCB>(wo[wave], st, cb, p, g, L);
-      __syncthreads();
-      // Lane -> (column lm, 32 dims of group lg) of this wave's block.
       const int col = L.lm;
       const int tq = q0 + (wave * kPreNCB + cb) * p.tpb + col / p.hs;
       const int hh = col % p.hs;
-      if (col < p.tpb * p.hs && hh < hs && tq < sq) {
-        const int64_t row = int64_t(p.n_dec) + cq0 + tq;
-        const int head = g * p.group + s * p.hs + hh;
-        const float m = wo[wave].m[col];
-        const float l = wo[wave].l[col];
+      if constexpr (kEnc == kI8Chan) {
+        // The residue product of side slot j (C row j: lane lm + 16 (j >> 2),
+        // element j & 3) joins O at the slot's dim d (lane group d >> 5,
+        // chunk d & 7, row (d >> 3) & 3).  A dim listed twice took the later
+        // slot's value, so only that slot's residue counts.
+        for (int j = 0; j < n_out; ++j) {
+          const int d = table_entry(p.out_idx, int64_t(g) * p.n_out_max + j);
+          bool later = false;
+          for (int j2 = j + 1; j2 < n_out; ++j2)
+            later |= table_entry(p.out_idx, int64_t(g) * p.n_out_max + j2) == d;
+          if (later) continue;
+          const int e = j & 3;
+          const f32x4_t c = plo[cb];
+          const float mine = e == 0 ? c[0] : e == 1 ? c[1] : e == 2 ? c[2] : c[3];
+          const float val = __shfl(mine, L.lm + 16 * (j >> 2), 64);
+          if (L.lg == (d >> 5)) {
 #pragma unroll
-        for (int part = 0; part < 4; ++part) {
-          const int d0 = 32 * L.lg + 8 * part;
-          float v[8];
+            for (int jj = 0; jj < 8; ++jj)
 #pragma unroll
-          for (int e = 0; e < 8; ++e) v[e] = wo[wave].o[col][d0 + e];
-          if (split < 0) {
-            store_final(p, row, head, d0, v, 1.f / l);
-          } else {
-            store_partial(p, row, head, split, d0, v, m, l);
+              for (int r = 0; r < 4; ++r)
+                if (jj == (d & 7) && r == ((d >> 3) & 3)) st.o[cb][jj][r] += val;
           }
         }
       }
-      __syncthreads();
-    }
-  } else {
-#pragma unroll
-    for (int cb = 0; cb < kPreNCB; ++cb) {
-      const int col = L.lm;
-      const int tq = q0 + (wave * kPreNCB + cb) * p.tpb + col / p.hs;
-      const int hh = col % p.hs;
-      store_prefill_block<kEnc, kPreNCB>(p, st, cb, int64_t(p.n_dec) + cq0 + tq,
+      store_prefill_block<kCmp, kPreNCB>(p, st, cb, int64_t(p.n_dec) + cq0 + tq,
                                          g * p.group + s * p.hs + hh,
                                          col < p.tpb * p.hs && hh < hs && tq < sq, split, L);
     }

@@ -180,8 +180,10 @@ def test_fresh_kv_prefill_without_block_tables(partition):
 
 def test_mixed_int8_tokhead_pool(partition):
     # Decode rows and prefix-cached prefill chunks over a per-token-head int8
-    # pool (codes + fp32 scale per slot and kv head): the oracle reads the
-    # pool as codes x scale in fp32 (paged_attention.py:138-145).
+    # pool (codes + fp32 scale per slot and kv head): the decode rows read the
+    # pool as codes x scale in fp32 (paged_attention.py:138-145), the prefill
+    # rows through the bf16 dequantisation the reference's prefill gathers
+    # with (attention.py:33-51).
     H, KVH, D = 32, 4, 128
     dec_lens = [900, 1, 2500]
     chunks = [(0, 40), (700, 90), (3000, 33)]
@@ -210,8 +212,10 @@ def test_mixed_int8_tokhead_pool(partition):
     torch.cuda.synchronize()
     kf = ko.kv_float(kc.numpy(), "int8_tokhead", ks.numpy())
     vf = ko.kv_float(vc.numpy(), "int8_tokhead", vs.numpy())
+    kp = ko.kv_float_prefill(kc.numpy(), "int8_tokhead", ks.numpy())
+    vp = ko.kv_float_prefill(vc.numpy(), "int8_tokhead", vs.numpy())
     ref = ko.mixed_ref(bits(q), kf, vf, bt.numpy(), len(dec_lens), np.asarray(dec_lens), cu_q,
-                       cu_k, D ** -0.5)
+                       cu_k, D ** -0.5, k_pre=kp, v_pre=vp)
     assert_attention_close(out, ref, "mixed-int8-tokhead")
 
 
@@ -252,7 +256,12 @@ def test_mixed_int8_channel_pool_with_side(partition):
                      head_n_out.numpy())
     vf = ko.kv_float(vc.cpu().numpy(), "int8_chan", ds_v.numpy(), bits(sv), out_idx2d.numpy(),
                      head_n_out.numpy())
-    ref = ko.mixed_ref(bits(q), kf, vf, bt.numpy(), 1, np.asarray([512]), cu_q, cu_k, D ** -0.5)
+    kp = ko.kv_float_prefill(kc.cpu().numpy(), "int8_chan", ds_k.numpy(), bits(sk),
+                             out_idx2d.numpy(), head_n_out.numpy())
+    vp = ko.kv_float_prefill(vc.cpu().numpy(), "int8_chan", ds_v.numpy(), bits(sv),
+                             out_idx2d.numpy(), head_n_out.numpy())
+    ref = ko.mixed_ref(bits(q), kf, vf, bt.numpy(), 1, np.asarray([512]), cu_q, cu_k, D ** -0.5,
+                       k_pre=kp, v_pre=vp)
     assert_attention_close(out, ref, "mixed-int8-chan-side")
 
 

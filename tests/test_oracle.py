@@ -159,6 +159,32 @@ def test_chan_dequant_against_torch():
     assert np.array_equal(got, ko.torch_bf16_bits(ref))
 
 
+def test_prefill_read_of_an_int8_pool_is_the_gather_dequantisation():
+    # attention.py:33-51 (_gather_kv) restated in torch over a paged pool: the
+    # blocks of a table row, (code.float() * dscale).to(bf16), then each
+    # head's outlier dims from the side pool; and the per-token-head form
+    # bf16(code * scale).  kv_float_prefill must read every slot the same way.
+    g = torch.Generator().manual_seed(8)
+    blocks, page, kvh, d, nout = 3, 32, 2, 16, 4
+    codes = torch.randint(-127, 128, (blocks, page, kvh, d), generator=g, dtype=torch.int8)
+    ds = torch.rand(kvh, d, generator=g) * 0.05
+    side = torch.randn(blocks, page, kvh, nout, generator=g).to(torch.bfloat16)
+    idx = torch.tensor([[3, 9, 1, 0], [14, 0, 0, 0]], dtype=torch.int32)
+    nh = torch.tensor([3, 1], dtype=torch.int32)
+    table = torch.tensor([2, 0, 1])
+    kv = (codes[table].float() * ds).to(torch.bfloat16).view(-1, kvh, d)
+    s = side[table].view(-1, kvh, nout)
+    for h in range(kvh):
+        kv[:, h, idx[h, :nh[h]].long()] = s[:, h, :nh[h]]
+    got = ko.kv_float_prefill(codes.numpy(), "int8_chan", ds.numpy(), ko.torch_bf16_bits(side),
+                              idx.numpy(), nh.numpy())
+    assert np.array_equal(got[table.numpy()].reshape(-1, kvh, d), kv.float().numpy())
+    sc = torch.rand(blocks, page, kvh, generator=g) * 0.05
+    want = (codes.float() * sc.unsqueeze(-1)).to(torch.bfloat16).float()
+    got = ko.kv_float_prefill(codes.numpy(), "int8_tokhead", sc.numpy())
+    assert np.array_equal(got, want.numpy())
+
+
 # ---------------------------------------------------------------------------
 # attention references
 # ---------------------------------------------------------------------------
