@@ -610,6 +610,21 @@ __device__ __forceinline__ void attend_tile(ColState<NCB, kSideN>& st, const Til
     }
   }
 
+  // Residue A operand (kPLo): row j = lm (side slot j, whose value the V
+  // tile holds at dim plo_dim), the lane's 8 key slots; rows past n_plo 0.
+  u32x4_t plo_op = u32x4_t{0u, 0u, 0u, 0u};
+  if constexpr (kPLo) {
+    if (n_plo > 0) {
+      uint32_t e[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        e[i] = L.lm < n_plo ? *reinterpret_cast<const uint16_t*>(
+                                  plo_v + key_of_slot(L.lg, i) * kPitchBF16 + 2 * plo_dim)
+                            : 0u;
+      plo_op = u32x4_t{e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16),
+                       e[6] | (e[7] << 16)};
+    }
+  }
 #pragma unroll
   for (int cb = 0; cb < NCB; ++cb) {
     const f32x4_t s0 = sacc[cb][0], s1 = sacc[cb][1];
@@ -697,16 +712,6 @@ __device__ __forceinline__ void attend_tile(ColState<NCB, kSideN>& st, const Til
     for (int w = 0; w < 4; ++w) pb[w] = pack_bf16x2_fast(pv[2 * w], pv[2 * w + 1]);
     if constexpr (kPLo) {
       if (n_plo > 0) {
-        // Residue A operand: row j = lm (side slot j, whose value the V tile
-        // holds at dim plo_dim), the lane's 8 key slots; rows past n_plo 0.
-        uint32_t e[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-          e[i] = L.lm < n_plo ? *reinterpret_cast<const uint16_t*>(
-                                    plo_v + key_of_slot(L.lg, i) * kPitchBF16 + 2 * plo_dim)
-                              : 0u;
-        const u32x4_t plo_op = u32x4_t{e[0] | (e[1] << 16), e[2] | (e[3] << 16),
-                                       e[4] | (e[5] << 16), e[6] | (e[7] << 16)};
         u32x4_t pl;
 #pragma unroll
         for (int w = 0; w < 4; ++w)
@@ -2867,6 +2872,21 @@ __device__ void prefill_segment(const AttnParams& p, char* smem, const int32_t* 
   const int n_out = (kEnc == kI8Chan && p.head_n_out != nullptr)
                         ? min(table_entry(p.head_n_out, g), int(p.n_out_max))
                         : 0;
+  // (per-channel) the slots whose outlier dims fall in this lane's 16-dim
+  // chunk of a key row (the chunk is the same in every tile): bit j of
+  // hit_mask, the dim within the chunk in bits 4j .. 4j + 3 of hit_pos.
+  uint32_t hit_mask = 0, hit_pos = 0;
+  if constexpr (kEnc == kI8Chan) {
+    static_assert(kLoadsPerThread == 1, "one 16-code chunk per lane");
+    const int vec = (threadIdx.x % kVecPerTile) % kVecPerRow;
+    for (int j = 0; j < n_out; ++j) {
+      const int d = table_entry(p.out_idx, int64_t(g) * p.n_out_max + j);
+      if ((d >> 4) == vec) {
+        hit_mask |= 1u << j;
+        hit_pos |= uint32_t(d & 15) << (4 * j);
+      }
+    }
+  }
   // (per-channel) the outlier dim of side slot lm, for the residue product
   const int plo_dim =
       (kEnc == kI8Chan && L.lm < n_out) ? (p.out_idx[int64_t(g) * p.n_out_max + L.lm] & (kD - 1)) : 0;
@@ -2918,13 +2938,19 @@ __device__ void prefill_segment(const AttnParams& p, char* smem, const int32_t* 
             // lane that wrote the chunk rewrites them (one lane's LDS writes
             // land in order), slot by slot, so that a later slot wins on a
             // duplicate dim, like dequant_chan.
-            const int kl = L.lane & ~7;  // lane of the key's chunk 0 (slot 0)
-            for (int j = 0; j < n_out; ++j) {
-              const uint32_t w = __shfl(pre_sd[set][e], kl + j, 64);
-              const int el = (key * p.kvh + g) * p.n_out_max + j;
-              const uint16_t sv = uint16_t((el & 1) ? (w >> 16) : (w & 0xffffu));
-              const int d = table_entry(p.out_idx, int64_t(g) * p.n_out_max + j);
-              if ((d >> 4) == vec) *reinterpret_cast<uint16_t*>(dst + 2 * (d & 15)) = sv;
+            if (n_out > 0) {
+              const int kl = L.lane & ~7;  // lane of the key's chunk 0 (slot 0)
+              const int hsel = ((key * p.kvh + g) * p.n_out_max) & 1;  // slot 0's half
+              uint32_t w[kSideMax];
+#pragma unroll
+              for (int j = 0; j < kSideMax; ++j) w[j] = __shfl(pre_sd[set][e], kl + j, 64);
+#pragma unroll
+              for (int j = 0; j < kSideMax; ++j) {
+                if ((hit_mask >> j) & 1u) {
+                  const uint16_t sv = uint16_t(((hsel + j) & 1) ? (w[j] >> 16) : (w[j] & 0xffffu));
+                  *reinterpret_cast<uint16_t*>(dst + 2 * ((hit_pos >> (4 * j)) & 15u)) = sv;
+                }
+              }
             }
           }
         }
