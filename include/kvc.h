@@ -429,6 +429,28 @@ int kvc_dequant_chan(const int8_t* kv, const float* dscale, const void* side,
 int kvc_dequant_tokhead(const int8_t* kv, const float* scale, int64_t num_tokens,
                         int64_t num_kv_heads, int64_t head_dim, void* out, kvc_stream_t stream);
 
+/* Replaces _gather_kv (nanovllm/layers/attention.py:33-51), called there per
+ * prefill chunk for K and for V, with one launch over every chunk of a step:
+ * chunk i's keys 0 .. sk_i - 1 (sk_i = cu_seqlens_k[i+1] - cu_seqlens_k[i]),
+ * read through block table row block_table_row0 + i, land at rows
+ * cu_seqlens_k[i] .. of out_k / out_v (bf16 [total_keys, KVH, D],
+ * contiguous; total_keys = cu_seqlens_k[num_prefill], the host's value).
+ * Per-channel int8: bf16(fp32(code) * k_scale[h][d]) (the [KVH, D] read
+ * scales), then the head's outlier dims out_idx2d[h][j], j < head_n_out[h],
+ * take the side pool's values (a later j wins on a duplicate dim), exactly as
+ * _gather_kv; per-token-head int8 (the p14 probe's encoding):
+ * bf16(fp32(code) * k_scale[slot][h]); bf16 pools are copied.  A table entry
+ * outside the pool reads zeros.  cu_seqlens_k: int32 device array of
+ * num_prefill + 1 entries, non-decreasing from 0; n_out_max at most 8. */
+int kvc_gather_kv(const void* k_cache, const void* v_cache, int64_t num_cache_blocks,
+                  int64_t page_size, int64_t num_kv_heads, int64_t head_dim, int kv_dtype,
+                  const float* k_scale, const float* v_scale, const void* side_k,
+                  const void* side_v, const int32_t* out_idx2d, const int32_t* head_n_out,
+                  int64_t n_out_max, const int32_t* block_tables, int64_t bt_stride,
+                  int64_t max_blocks_per_seq, int64_t block_table_row0, int64_t num_prefill,
+                  const int32_t* cu_seqlens_k, int64_t total_keys, void* out_k, void* out_v,
+                  kvc_stream_t stream);
+
 /* ---------------------------------------------------------------------------
  * Whole-block movement (LRU eviction, host offload, compaction).
  * ------------------------------------------------------------------------- */

@@ -2710,7 +2710,7 @@ __device__ __forceinline__ void store_prefill_block(const AttnParams& p, const C
 // LDS.  split < 0: the segment is the whole item and writes final rows;
 // otherwise it writes split-K partials at slot `split`.
 // ---------------------------------------------------------------------------
-template <int kEnc, bool kFresh>
+template <int kEnc, bool kFresh, bool kPLo = (kEnc == kI8Chan)>
 __device__ void prefill_segment(const AttnParams& p, char* smem, const int32_t* bt_base, int i,
                                 int qt, int kvs, int t0, int t1, int split) {
   // An int8 pool's tiles are dequantised to bf16 as they are committed to
@@ -2869,7 +2869,7 @@ __device__ void prefill_segment(const AttnParams& p, char* smem, const int32_t* 
       sc_lds[threadIdx.x] = (threadIdx.x < kD ? p.k_scale : p.v_scale)[g * kD + (threadIdx.x & (kD - 1))];
     __syncthreads();
   }
-  const int n_out = (kEnc == kI8Chan && p.head_n_out != nullptr)
+  const int n_out = (kPLo && p.head_n_out != nullptr)
                         ? min(table_entry(p.head_n_out, g), int(p.n_out_max))
                         : 0;
   // (per-channel) the slots whose outlier dims fall in this lane's 16-dim
@@ -2889,7 +2889,7 @@ __device__ void prefill_segment(const AttnParams& p, char* smem, const int32_t* 
   }
   // (per-channel) the outlier dim of side slot lm, for the residue product
   const int plo_dim =
-      (kEnc == kI8Chan && L.lm < n_out) ? (p.out_idx[int64_t(g) * p.n_out_max + L.lm] & (kD - 1)) : 0;
+      (kPLo && L.lm < n_out) ? (p.out_idx[int64_t(g) * p.n_out_max + L.lm] & (kD - 1)) : 0;
   f32x4_t plo[kPreNCB];
 #pragma unroll
   for (int cb = 0; cb < kPreNCB; ++cb) plo[cb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -3002,7 +3002,7 @@ __device__ void prefill_segment(const AttnParams& p, char* smem, const int32_t* 
           }
           Tile<kCmp> t;
           read_tile(t, r);
-          attend<kCmp, kPreNCB, false, kSideMax, kEnc == kI8Chan>(
+          attend<kCmp, kPreNCB, false, kSideMax, kPLo>(
               st, t, Q, ci, k_begin + tix * kTile, sk, min_klim, kFresh ? -1 : slots[0], p, g, L,
               stage_ptr(r) + kTileBytesBF16, plo, n_out, plo_dim);
           if (tix + 1 < ntiles) commit(1 - r, 1 - r);
@@ -3021,7 +3021,7 @@ __device__ void prefill_segment(const AttnParams& p, char* smem, const int32_t* 
       const int col = L.lm;
       const int tq = q0 + (wave * kPreNCB + cb) * p.tpb + col / p.hs;
       const int hh = col % p.hs;
-      if constexpr (kEnc == kI8Chan) {
+      if constexpr (kPLo) {
         // The residue product of side slot j (C row j: lane lm + 16 (j >> 2),
         // element j & 3) joins O at the slot's dim d (lane group d >> 5,
         // chunk d & 7, row (d >> 3) & 3).  A dim listed twice took the later
@@ -3567,7 +3567,7 @@ __device__ __forceinline__ bool find_prefill_unit(const AttnParams& p, int u, in
 
 // One workgroup per prefill unit (chunk, query tile, kv slice, key split):
 // the launch for int8 pools and for KVC_PREFILL_SK=0.
-template <int kEnc, bool kFresh>
+template <int kEnc, bool kFresh, bool kPLo = (kEnc == kI8Chan)>
 __global__ void __launch_bounds__(kThreads)
 varlen_kernel(AttnParams p, const int32_t* __restrict__ block_tables) {
   __shared__ __align__(16) char smem[kSmemBytes];
@@ -3578,8 +3578,8 @@ varlen_kernel(AttnParams p, const int32_t* __restrict__ block_tables) {
   const int sk = p.cu_k[i + 1] - p.cu_k[i];
   const int nsplit = max(1, (sk + p.split_tokens - 1) / p.split_tokens);
   const int per = p.split_tokens / kTile;
-  prefill_segment<kEnc, kFresh>(p, smem, block_tables, i, qt, kvs, split * per,
-                                (split + 1) * per, nsplit == 1 ? -1 : split);
+  prefill_segment<kEnc, kFresh, kPLo>(p, smem, block_tables, i, qt, kvs, split * per,
+                                      (split + 1) * per, nsplit == 1 ? -1 : split);
 }
 
 // ---------------------------------------------------------------------------
@@ -3670,12 +3670,15 @@ __device__ __forceinline__ u32x2_t lds_read_tr16(const char* p) {
 // S^T, the online softmax and P of one tile.  k: K operands as in
 // Tile<kBF16>; klim[cb]: the lane's column key limit (-1 for an invalid
 // column); pb[cb]: P^T of column block cb (bf16), the PV operand.
-template <bool kMasked>
+// kPLo: also pl[cb] = bf16(P - pb), the rounding residue of the operand, and
+// the residue accumulators plo[cb] follow a move of the reference max.
+template <bool kMasked, bool kPLo = false>
 __device__ __forceinline__ void pf_score(PfState& st, const u32x4_t (&k)[2][4],
                                          const QOps<kBF16, kPreNCB>& Q,
                                          const int (&klim)[kPreNCB], int key0, int valid_end,
                                          float scale_log2, const LaneId& L,
-                                         u32x4_t (&pb)[kPreNCB]) {
+                                         u32x4_t (&pb)[kPreNCB], f32x4_t* plo = nullptr,
+                                         u32x4_t* pl = nullptr) {
   static_assert(kPreNCB == 2, "the schedule below pairs two column blocks");
   // S^T of column block 0, then of block 1 (block 0's max runs under block
   // 1's MFMAs).
@@ -3730,6 +3733,10 @@ __device__ __forceinline__ void pf_score(PfState& st, const u32x4_t (&k)[2][4],
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) st.l[cb][r] *= alpha;
+      if constexpr (kPLo) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) plo[cb][r] *= alpha;
+      }
     }
   }
 #pragma unroll
@@ -3741,6 +3748,12 @@ __device__ __forceinline__ void pf_score(PfState& st, const u32x4_t (&k)[2][4],
       pr[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[cb][i], scale_log2, neg_m));
 #pragma unroll
     for (int w = 0; w < 4; ++w) pb[cb][w] = pack_bf16x2_fast(pr[2 * w], pr[2 * w + 1]);
+    if constexpr (kPLo) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+        pl[cb][w] = pack_bf16x2_fast(pr[2 * w] - bf16_bits_to_f32(pb[cb][w] & 0xffffu),
+                                     pr[2 * w + 1] - bf16_bits_to_f32(pb[cb][w] >> 16));
+    }
   }
 }
 
@@ -3751,9 +3764,11 @@ __device__ __forceinline__ void pf_score(PfState& st, const u32x4_t (&k)[2][4],
 // arithmetic results need no canonicalising max (MFMA results do).  The rare
 // branch recomputes S^T (the logits are not kept live across the test),
 // moves the reference and redoes P exactly as pf_score does.
+template <bool kPLo = false>
 __device__ __forceinline__ void pf_score_fast(PfState& st, const u32x4_t (&k)[2][4],
                                               const QOps<kBF16, kPreNCB>& Q, float scale_log2,
-                                              u32x4_t (&pb)[kPreNCB]) {
+                                              u32x4_t (&pb)[kPreNCB], f32x4_t* plo = nullptr,
+                                              u32x4_t* pl = nullptr) {
   auto qk = [&](f32x4_t (&sacc)[kPreNCB][2]) {
 #pragma unroll
     for (int cb = 0; cb < kPreNCB; ++cb) {
@@ -3813,6 +3828,10 @@ __device__ __forceinline__ void pf_score_fast(PfState& st, const u32x4_t (&k)[2]
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) st.l[cb][r] *= alpha;
+      if constexpr (kPLo) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) plo[cb][r] *= alpha;
+      }
     }
     exp_all(sacc, pr);
   }
@@ -3820,6 +3839,12 @@ __device__ __forceinline__ void pf_score_fast(PfState& st, const u32x4_t (&k)[2]
   for (int cb = 0; cb < kPreNCB; ++cb) {
 #pragma unroll
     for (int w = 0; w < 4; ++w) pb[cb][w] = pack_bf16x2_fast(pr[cb][2 * w], pr[cb][2 * w + 1]);
+    if constexpr (kPLo) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+        pl[cb][w] = pack_bf16x2_fast(pr[cb][2 * w] - bf16_bits_to_f32(pb[cb][w] & 0xffffu),
+                                     pr[cb][2 * w + 1] - bf16_bits_to_f32(pb[cb][w] >> 16));
+    }
   }
 }
 
@@ -3947,7 +3972,11 @@ __device__ __forceinline__ void p2_next_item(PfItem& it, const int4* ctab, const
 // One workgroup's share (workgroup v of G) of a stream-K prefill launch;
 // lds holds the ring, the query regions and the dummy block (kP2Smem bytes),
 // ctab the first 64 chunks' geometry.
-template <bool kFresh>
+// kPLo (fresh rows gathered from a per-channel int8 pool, p.head_n_out set):
+// the outlier dims' PV and the column sums also take the rounding residue of
+// the bf16 P operand (one MFMA per column block and tile: rows j < n_plo read
+// the V stage at slot j's dim, row 15 is ones), added in at the segment end.
+template <bool kFresh, bool kPLo = false>
 __device__ __forceinline__ void prefill_sk2_share(const AttnParams& p,
                                                   const int32_t* __restrict__ cu_q,
                                                   const int32_t* __restrict__ cu_k,
@@ -4209,6 +4238,13 @@ __device__ __forceinline__ void prefill_sk2_share(const AttnParams& p,
   issue_next_q();
 
   PfState st;
+  f32x4_t plo[kPreNCB];
+  u32x4_t pl[kPreNCB];
+  int n_plo = 0, plo_dim = 0;  // (kPLo) the item's slots, the dim of slot lm
+  // (kPLo) residue operand rows: lanes lm < n_plo keep the V values, lane
+  // row 15 is ones, the rest 0
+  const uint32_t plo_one = L.lm == 15 ? kOnesBf16x2 : 0u;
+  uint32_t plo_keep = 0u;
   int klim[kPreNCB];
   int min_klim = 0, split = -1, nrows = 0;
   int stage = 0;  // stage of the tile the next step attends
@@ -4236,6 +4272,23 @@ __device__ __forceinline__ void prefill_sk2_share(const AttnParams& p,
       const u32x2_t lo = lds_read_tr16(vb + jj * 32);
       const u32x2_t hi = lds_read_tr16(vb + 16 * kPfPitchV + jj * 32);
       va[jj] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
+    }
+  };
+
+  // (kPLo) the residue product of the tile in stage stg (branch-free, so
+  // that its LDS reads schedule with the tile's own).
+  auto residue = [&](int stg) {
+    if constexpr (kPLo) {
+      const char* vb = lds + stg * kPfStage + kPfTensor + 2 * plo_dim;
+      uint32_t e[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        e[i] = *reinterpret_cast<const uint16_t*>(vb + key_of_slot(L.lg, i) * kPfPitchV);
+      u32x4_t op;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) op[w] = ((e[2 * w] | (e[2 * w + 1] << 16)) & plo_keep) | plo_one;
+#pragma unroll
+      for (int cb = 0; cb < kPreNCB; ++cb) plo[cb] = mfma_bf16(op, pl[cb], plo[cb]);
     }
   };
 
@@ -4328,11 +4381,12 @@ __device__ __forceinline__ void prefill_sk2_share(const AttnParams& p,
           {
             u32x4_t kop[2][4];
             read_k(stage, kop);
-            pf_score_fast(st, kop, Q, p.scale_log2, pb);
+            pf_score_fast<kPLo>(st, kop, Q, p.scale_log2, pb, plo, pl);
           }
           u32x4_t va[8];
           read_v(stage, va);
           pf_pv(st, va, pb);
+          residue(stage);
           ++ct;
           stage = stage == kP2Stages - 1 ? 0 : stage + 1;
         }
@@ -4361,6 +4415,21 @@ __device__ __forceinline__ void prefill_sk2_share(const AttnParams& p,
         min_klim = k0 >= 0 ? k0 : 0x7fffffff;
       }
       pf_init(st);
+      if constexpr (kPLo) {
+#pragma unroll
+        for (int cb = 0; cb < kPreNCB; ++cb) plo[cb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        n_plo = p.head_n_out != nullptr ? min(table_entry(p.head_n_out, it.g), p.n_out_max) : 0;
+        int dsel = 0;
+#pragma unroll
+        for (int j = 0; j < kSideMax; ++j) {
+          if (j < n_plo) {
+            const int d = table_entry(p.out_idx, int64_t(it.g) * p.n_out_max + j) & (kD - 1);
+            dsel = L.lm == j ? d : dsel;
+          }
+        }
+        plo_dim = dsel;
+        plo_keep = L.lm < n_plo ? 0xffffffffu : 0u;
+      }
       const int f = (it.P + kP2ItemCost) / S;
       const int nseg = (it.P + kP2ItemCost + it.T - 1) / S - f + 1;
       split = nseg == 1 ? -1 : w - f;
@@ -4389,15 +4458,16 @@ __device__ __forceinline__ void prefill_sk2_share(const AttnParams& p,
       u32x4_t kop[2][4];
       read_k(stage, kop);
       if (key0 + kTile <= it.geo.sk && key0 + kTile - 1 <= min_klim) {
-        pf_score<false>(st, kop, Q, klim, key0, it.geo.sk, p.scale_log2, L, pb);
+        pf_score<false, kPLo>(st, kop, Q, klim, key0, it.geo.sk, p.scale_log2, L, pb, plo, pl);
       } else {
-        pf_score<true>(st, kop, Q, klim, key0, it.geo.sk, p.scale_log2, L, pb);
+        pf_score<true, kPLo>(st, kop, Q, klim, key0, it.geo.sk, p.scale_log2, L, pb, plo, pl);
       }
     }
     {
       u32x4_t va[8];
       read_v(stage, va);
       pf_pv(st, va, pb);
+      residue(stage);
     }
     stage = stage == kP2Stages - 1 ? 0 : stage + 1;
     // Segment end: every lane's dims (16 jj + 4 lg .. + 3 of its column), as
@@ -4424,12 +4494,43 @@ __device__ __forceinline__ void prefill_sk2_share(const AttnParams& p,
     if (seg_end) {
       const int hs = min(p.hs, p.group - it.s * p.hs);
       const int hbase = it.g * p.group + it.s * p.hs;
+      float lres[kPreNCB] = {};
+      if constexpr (kPLo) {
+        {
+          // Residue row j (lane lm + 16 (j >> 2), element j & 3) joins O at
+          // slot j's dim d (lane group (d >> 2) & 3, chunk d >> 4, row d & 3;
+          // a dim listed twice took the later slot's value, so only that
+          // slot's residue counts); row 15 joins the column sum.
+#pragma unroll
+          for (int cb = 0; cb < kPreNCB; ++cb) {
+            lres[cb] = __shfl(plo[cb][3], L.lm + 48, 64);
+            for (int j = 0; j < n_plo; ++j) {
+              const int d = table_entry(p.out_idx, int64_t(it.g) * p.n_out_max + j) & (kD - 1);
+              bool later = false;
+              for (int j2 = j + 1; j2 < n_plo; ++j2)
+                later |= (table_entry(p.out_idx, int64_t(it.g) * p.n_out_max + j2) & (kD - 1)) == d;
+              if (later) continue;
+              const int e = j & 3;
+              const f32x4_t c = plo[cb];
+              const float mine = e == 0 ? c[0] : e == 1 ? c[1] : e == 2 ? c[2] : c[3];
+              const float val = __shfl(mine, L.lm + 16 * (j >> 2), 64);
+              if (L.lg == ((d >> 2) & 3)) {
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj)
+#pragma unroll
+                  for (int r = 0; r < 4; ++r)
+                    if (jj == (d >> 4) && r == (d & 3)) st.o[cb][jj][r] += val;
+              }
+            }
+          }
+        }
+      }
 #pragma unroll
       for (int cb = 0; cb < kPreNCB; ++cb) {
         const int tr = (wave * kPreNCB + cb) * p.tpb + L.lm / p.hs;  // row in the query tile
         const int hh = L.lm % p.hs;
         const bool ok = (L.lm < p.tpb * p.hs) && hh < hs && tr < nrows;
-        const float l = st.l[cb][0];
+        const float l = st.l[cb][0] + lres[cb];
         if (split < 0) {
           const float inv = 1.f / l;
           // Even rows of lanes (lg even) keep jj = 2t, odd rows jj = 2t + 1.
@@ -4480,14 +4581,14 @@ __device__ __forceinline__ void prefill_sk2_share(const AttnParams& p,
   __builtin_amdgcn_s_waitcnt(0);
 }
 
-template <bool kFresh>
+template <bool kFresh, bool kPLo = false>
 __global__ void __launch_bounds__(kThreads)
 prefill_sk2_kernel(AttnParams p, const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k,
                    const int32_t* __restrict__ block_tables) {
   __shared__ __align__(16) char lds[kP2Smem];
   __shared__ int4 ctab[64];
   touch_kernel_args(int(sizeof(AttnParams) + 3 * sizeof(void*)));
-  prefill_sk2_share<kFresh>(p, cu_q, cu_k, block_tables, int(blockIdx.x), int(gridDim.x), lds,
+  prefill_sk2_share<kFresh, kPLo>(p, cu_q, cu_k, block_tables, int(blockIdx.x), int(gridDim.x), lds,
                             ctab);
 }
 
@@ -5155,7 +5256,11 @@ SkPlan plan_prefill_sk(int64_t num_q_tokens, int64_t num_heads, int64_t max_seql
 
 void launch_prefill_sk(const AttnParams& p, int grid, bool fresh, hipStream_t st) {
   if (fresh) {
-    prefill_sk2_kernel<true><<<grid, kThreads, 0, st>>>(p, p.cu_q, p.cu_k, p.block_tables);
+    if (p.head_n_out != nullptr) {
+      prefill_sk2_kernel<true, true><<<grid, kThreads, 0, st>>>(p, p.cu_q, p.cu_k, p.block_tables);
+    } else {
+      prefill_sk2_kernel<true><<<grid, kThreads, 0, st>>>(p, p.cu_q, p.cu_k, p.block_tables);
+    }
   } else {
     prefill_sk2_kernel<false><<<grid, kThreads, 0, st>>>(p, p.cu_q, p.cu_k, p.block_tables);
   }
@@ -5164,8 +5269,14 @@ void launch_prefill_sk(const AttnParams& p, int grid, bool fresh, hipStream_t st
 template <int kEnc>
 void launch_varlen_enc(const AttnParams& p, int grid, bool fresh, hipStream_t st) {
   if (fresh) {
-    if constexpr (kEnc == kBF16)
-      varlen_kernel<kBF16, true><<<grid, kThreads, 0, st>>>(p, p.block_tables);
+    // Fresh rows gathered from a per-channel pool carry its outlier dims.
+    if constexpr (kEnc == kBF16) {
+      if (p.head_n_out != nullptr) {
+        varlen_kernel<kBF16, true, true><<<grid, kThreads, 0, st>>>(p, p.block_tables);
+      } else {
+        varlen_kernel<kBF16, true><<<grid, kThreads, 0, st>>>(p, p.block_tables);
+      }
+    }
   } else {
     varlen_kernel<kEnc, false><<<grid, kThreads, 0, st>>>(p, p.block_tables);
   }
@@ -5717,6 +5828,16 @@ int varlen_impl(
   int rc = check_kv_args(fresh ? KVC_KV_BF16 : kv_dtype, k_scale, v_scale, side_k, side_v,
                          out_idx2d, head_n_out, n_out_max, "varlen_attention");
   if (rc != KVC_OK) return rc;
+  // Fresh rows gathered from a per-channel pool (kvc_gather_kv) name its
+  // outlier dims through out_idx2d / head_n_out (side pools unused).
+  const bool fresh_outliers = fresh && head_n_out != nullptr;
+  if (fresh_outliers) {
+    KVC_REQUIRE(out_idx2d != nullptr, KVC_ERR_VALUE,
+                "varlen_attention: head_n_out needs out_idx2d");
+    KVC_REQUIRE(n_out_max >= 1 && n_out_max <= kSideMax && (n_out_max & (n_out_max - 1)) == 0,
+                KVC_ERR_VALUE, "varlen_attention: n_out_max must be 1, 2, 4 or 8 (got %lld)",
+                (long long)n_out_max);
+  }
   KVC_REQUIRE((q_stride_t % 8) == 0 && (q_stride_h % 8) == 0 && (out_stride_t % 8) == 0 &&
                   (out_stride_h % 8) == 0 && (reinterpret_cast<uintptr_t>(q) % 16) == 0 &&
                   (reinterpret_cast<uintptr_t>(out) % 16) == 0,
@@ -5842,6 +5963,11 @@ int varlen_impl(
   p.scale_log2 = scale * kLog2e;
   fill_kv(p, k_cache, v_cache, page_size, num_kv_heads, fresh ? KVC_KV_BF16 : kv_dtype, k_scale,
           v_scale, side_k, side_v, out_idx2d, head_n_out, n_out_max);
+  if (fresh_outliers) {
+    p.out_idx = out_idx2d;
+    p.head_n_out = head_n_out;
+    p.n_out_max = int(n_out_max);
+  }
   p.block_tables = block_tables;
   p.bt_stride = bt_stride;
   p.n_dec = 0;

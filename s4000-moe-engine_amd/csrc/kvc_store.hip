@@ -231,6 +231,140 @@ dequant_tokhead_kernel(const int8_t* __restrict__ kv, const float* __restrict__ 
   *reinterpret_cast<u32x4_t*>(out + row * kD + lane16 * 8) = u32x4_t{o[0], o[1], o[2], o[3]};
 }
 
+// ---------------------------------------------------------------------------
+// Gather of every prefill chunk's keys out of the paged pool, dequantised to
+// bf16 (the prefill's read of an int8 pool).  Block = 32 tokens of one kv
+// head (blockIdx.y), so the head's scales and outlier dims are uniform;
+// thread = 16 dims of one token's row of K and of V (8 threads a row).  The
+// token's chunk is found by a binary search over cu_k (num_prefill + 1
+// entries).
+// ---------------------------------------------------------------------------
+constexpr int kSideMaxStore = 8;  // side slots a gathered row takes (the attention's bound)
+constexpr int kGatherLanes = 8;
+constexpr int kGatherRows = kThreads / kGatherLanes;
+constexpr int kGatherIters = 2;  // token groups a block runs (per-head constants loaded once)
+
+// One side-pool row (n_out_max bf16, a power of two up to 8, row-aligned)
+// as 16-bit values.
+__device__ __forceinline__ void load_side_row16(const uint16_t* row, int nom,
+                                                uint32_t (&v)[kSideMaxStore]) {
+  uint32_t w[4] = {0u, 0u, 0u, 0u};
+  if (nom == 8) {
+    const u32x4_t x = *reinterpret_cast<const u32x4_t*>(row);
+    w[0] = x[0], w[1] = x[1], w[2] = x[2], w[3] = x[3];
+  } else if (nom == 4) {
+    const u32x2_t x = *reinterpret_cast<const u32x2_t*>(row);
+    w[0] = x[0], w[1] = x[1];
+  } else if (nom == 2) {
+    w[0] = *reinterpret_cast<const uint32_t*>(row);
+  } else {
+    w[0] = *row;
+  }
+#pragma unroll
+  for (int j = 0; j < kSideMaxStore; ++j) v[j] = (w[j >> 1] >> ((j & 1) * 16)) & 0xffffu;
+}
+
+template <int kEnc>
+__global__ void __launch_bounds__(kThreads)
+gather_kv_kernel(const char* __restrict__ k_cache, const char* __restrict__ v_cache,
+                 int64_t num_slots, int page, int kvh, const float* __restrict__ k_scale,
+                 const float* __restrict__ v_scale, const uint16_t* __restrict__ side_k,
+                 const uint16_t* __restrict__ side_v, const int32_t* __restrict__ out_idx2d,
+                 const int32_t* __restrict__ head_n_out, int n_out_max,
+                 const int32_t* __restrict__ block_tables, int64_t bt_stride, int max_blocks,
+                 int64_t bt_row0, int num_prefill, const int32_t* __restrict__ cu_k,
+                 int64_t tokens, uint16_t* __restrict__ out_k, uint16_t* __restrict__ out_v) {
+  const int lane8 = threadIdx.x & (kGatherLanes - 1);
+  const int h = int(blockIdx.y);
+  // Per-block constants of head h: this thread's 16 read scales of K and V
+  // (per-channel), the head's outlier dims relative to this thread's 16.
+  float dsk[16], dsv[16];
+  int n_out = 0;
+  int dims[kSideMaxStore];
+  if constexpr (kEnc == KVC_KV_INT8_CHAN) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      dsk[i] = k_scale[h * kD + lane8 * 16 + i];
+      dsv[i] = v_scale[h * kD + lane8 * 16 + i];
+    }
+    if (head_n_out != nullptr) n_out = min(head_n_out[h], n_out_max);
+#pragma unroll
+    for (int j = 0; j < kSideMaxStore; ++j)
+      dims[j] = j < n_out ? out_idx2d[h * n_out_max + j] - lane8 * 16 : -1;
+  }
+#pragma unroll
+  for (int it = 0; it < kGatherIters; ++it) {
+    const int64_t t =
+        (int64_t(blockIdx.x) * kGatherIters + it) * kGatherRows + (threadIdx.x / kGatherLanes);
+    if (t >= tokens) break;
+    const int64_t row = t * kvh + h;
+    // chunk i: the last with cu_k[i] <= t
+    int lo = 0, hi = num_prefill - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (cu_k[mid] <= t) lo = mid; else hi = mid - 1;
+    }
+    const int64_t key = t - cu_k[lo];
+    const int64_t bi = key / page;
+    const int64_t blk = bi < max_blocks ? block_tables[(bt_row0 + lo) * bt_stride + bi] : -1;
+    const int64_t slot = blk * page + (key - bi * page);
+    const bool ok = blk >= 0 && slot < num_slots;  // a bad table entry reads nothing
+    const int64_t src = (slot * kvh + h) * kD + lane8 * 16;  // element index
+    const int64_t dst = row * kD + lane8 * 16;
+    uint32_t sk[kSideMaxStore], sv[kSideMaxStore];
+    if constexpr (kEnc == KVC_KV_INT8_CHAN) {
+      if (ok && n_out > 0) {
+        load_side_row16(side_k + (slot * kvh + h) * n_out_max, n_out_max, sk);
+        load_side_row16(side_v + (slot * kvh + h) * n_out_max, n_out_max, sv);
+      }
+    }
+#pragma unroll
+    for (int tensor = 0; tensor < 2; ++tensor) {
+      const char* cache = tensor == 0 ? k_cache : v_cache;
+      uint16_t* out = tensor == 0 ? out_k : out_v;
+      u32x4_t o0 = u32x4_t{0u, 0u, 0u, 0u}, o1 = o0;
+      if (ok) {
+        if constexpr (kEnc == KVC_KV_BF16) {
+          o0 = *reinterpret_cast<const u32x4_t*>(cache + src * 2);
+          o1 = *reinterpret_cast<const u32x4_t*>(cache + src * 2 + 16);
+        } else {
+          const u32x4_t c = *reinterpret_cast<const u32x4_t*>(cache + src);
+          float sc[16];
+          if constexpr (kEnc == KVC_KV_INT8_TOKHEAD) {
+            const float s1 = (tensor == 0 ? k_scale : v_scale)[slot * kvh + h];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) sc[i] = s1;
+          } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) sc[i] = tensor == 0 ? dsk[i] : dsv[i];
+          }
+          uint32_t e[16];
+#pragma unroll
+          for (int i = 0; i < 16; ++i)
+            e[i] = f32_to_bf16_bits(float(int8_t((c[i >> 2] >> ((i & 3) * 8)) & 0xffu)) * sc[i]);
+          o0 = u32x4_t{e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16),
+                       e[6] | (e[7] << 16)};
+          o1 = u32x4_t{e[8] | (e[9] << 16), e[10] | (e[11] << 16), e[12] | (e[13] << 16),
+                       e[14] | (e[15] << 16)};
+        }
+      }
+      *reinterpret_cast<u32x4_t*>(out + dst) = o0;
+      *reinterpret_cast<u32x4_t*>(out + dst + 8) = o1;
+      if constexpr (kEnc == KVC_KV_INT8_CHAN) {
+        // The head's outlier dims in this thread's 16 take the side values,
+        // written over the row just stored (one thread's stores to an address
+        // land in order), slot by slot: a later slot wins on a duplicate dim,
+        // as the sequential assignment does.
+#pragma unroll
+        for (int j = 0; j < kSideMaxStore; ++j) {
+          if (j < n_out && ok && dims[j] >= 0 && dims[j] < 16)
+            out[dst + dims[j]] = uint16_t(tensor == 0 ? sk[j] : sv[j]);
+        }
+      }
+    }
+  }
+}
+
 int check_int8_args(const void* key, int64_t k_sn, int64_t k_sh, const void* value, int64_t v_sn,
                     int64_t v_sh, int64_t num_tokens, int64_t kvh, int64_t head_dim,
                     int slot_bytes, const char* what) {
@@ -387,4 +521,58 @@ extern "C" int kvc_dequant_tokhead(const int8_t* kv, const float* scale, int64_t
   dequant_tokhead_kernel<<<grid, kThreads, 0, as_stream(stream)>>>(kv, scale, rows,
                                                                    static_cast<uint16_t*>(out));
   return check_launch("dequant_tokhead");
+}
+
+extern "C" int kvc_gather_kv(const void* k_cache, const void* v_cache, int64_t num_cache_blocks,
+                             int64_t page_size, int64_t num_kv_heads, int64_t head_dim,
+                             int kv_dtype, const float* k_scale, const float* v_scale,
+                             const void* side_k, const void* side_v, const int32_t* out_idx2d,
+                             const int32_t* head_n_out, int64_t n_out_max,
+                             const int32_t* block_tables, int64_t bt_stride,
+                             int64_t max_blocks_per_seq, int64_t block_table_row0,
+                             int64_t num_prefill, const int32_t* cu_seqlens_k,
+                             int64_t total_keys, void* out_k, void* out_v, kvc_stream_t stream) {
+  clear_error();
+  KVC_REQUIRE(head_dim == kD, KVC_ERR_VALUE, "gather_kv: head_dim must be 128 (got %lld)",
+              (long long)head_dim);
+  KVC_REQUIRE(num_kv_heads > 0 && num_kv_heads < 65536 && page_size > 0 && num_cache_blocks >= 0,
+              KVC_ERR_VALUE,
+              "gather_kv: bad pool geometry");
+  KVC_REQUIRE(num_prefill >= 0 && total_keys >= 0 && block_table_row0 >= 0, KVC_ERR_VALUE,
+              "gather_kv: bad chunk count / key total / table row");
+  KVC_REQUIRE(kv_dtype == KVC_KV_BF16 || kv_dtype == KVC_KV_INT8_TOKHEAD ||
+                  kv_dtype == KVC_KV_INT8_CHAN,
+              KVC_ERR_VALUE, "gather_kv: unknown kv_dtype %d", kv_dtype);
+  if (num_prefill == 0 || total_keys == 0) return KVC_OK;
+  KVC_REQUIRE(k_cache && v_cache && block_tables && cu_seqlens_k && out_k && out_v,
+              KVC_ERR_VALUE, "gather_kv: null pointer");
+  KVC_REQUIRE(kv_dtype == KVC_KV_BF16 || (k_scale && v_scale), KVC_ERR_VALUE,
+              "gather_kv: int8 pools need their scales");
+  if (kv_dtype == KVC_KV_INT8_CHAN && head_n_out != nullptr) {
+    KVC_REQUIRE(side_k && side_v && out_idx2d && n_out_max >= 1 && n_out_max <= kSideMaxStore,
+                KVC_ERR_VALUE,
+                "gather_kv: head_n_out needs side_k, side_v, out_idx2d and n_out_max in [1, %d]",
+                kSideMaxStore);
+  }
+  KVC_REQUIRE(max_blocks_per_seq > 0 && max_blocks_per_seq <= bt_stride, KVC_ERR_VALUE,
+              "gather_kv: max_blocks_per_seq must be in [1, bt_stride]");
+  const int64_t per_block = int64_t(kGatherRows) * kGatherIters;
+  const dim3 grid(unsigned((total_keys + per_block - 1) / per_block), unsigned(num_kv_heads));
+  auto launch = [&](auto kern) {
+    kern<<<grid, kThreads, 0, as_stream(stream)>>>(
+        static_cast<const char*>(k_cache), static_cast<const char*>(v_cache),
+        num_cache_blocks * page_size, int(page_size), int(num_kv_heads), k_scale, v_scale,
+        static_cast<const uint16_t*>(side_k), static_cast<const uint16_t*>(side_v), out_idx2d,
+        kv_dtype == KVC_KV_INT8_CHAN ? head_n_out : nullptr, int(n_out_max), block_tables,
+        bt_stride, int(max_blocks_per_seq), block_table_row0, int(num_prefill), cu_seqlens_k,
+        total_keys, static_cast<uint16_t*>(out_k), static_cast<uint16_t*>(out_v));
+  };
+  if (kv_dtype == KVC_KV_BF16) {
+    launch(gather_kv_kernel<KVC_KV_BF16>);
+  } else if (kv_dtype == KVC_KV_INT8_TOKHEAD) {
+    launch(gather_kv_kernel<KVC_KV_INT8_TOKHEAD>);
+  } else {
+    launch(gather_kv_kernel<KVC_KV_INT8_CHAN>);
+  }
+  return check_launch("gather_kv");
 }

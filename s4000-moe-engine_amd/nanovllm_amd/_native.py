@@ -87,6 +87,8 @@ SIGNATURES = {
     "kvc_varlen_decode_cus": (_INT, [_I64, _I64, _I64, _I64, _INT, _I64, _I64]),
     "kvc_dequant_chan": (_INT, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P]),
     "kvc_dequant_tokhead": (_INT, [_P, _P, _I64, _I64, _I64, _P, _P]),
+    "kvc_gather_kv": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _INT, _P, _P, _P, _P, _P, _P,
+                             _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P, _P, _P]),
     "kvc_block_gather": (_INT, [_P, _I64, _I64, _I64, _P, _I64, _P, _I64, _I64, _P]),
     "kvc_block_scatter": (_INT, [_P, _I64, _I64, _I64, _I64, _P, _I64, _P, _I64, _P]),
     "kvc_block_copy": (_INT, [_P, _I64, _I64, _I64, _P, _P, _I64, _P]),

@@ -11,6 +11,8 @@ j <= its position (attention.py:210-212).
 """
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import torch
 
@@ -88,6 +90,8 @@ def _prepare(q, k_cache, v_cache, block_tables, num_decode_rows, decode_context_
         if a > 0 and b < a:
             raise ValueError("a prefill chunk has fewer keys than queries")
     c.max_seqlen_k = max(sk) if sk else 0
+    c.total_keys = cu_k[-1]
+    c.cu_k_list = cu_k
     cu_q_np = np.asarray(cu_q, dtype=np.int32)
     cu_k_np = np.asarray(cu_k, dtype=np.int32)
     c.pre_units = nat.query("kvc_varlen_prefill_units", cu_q_np.ctypes.data, cu_k_np.ctypes.data,
@@ -122,6 +126,71 @@ def _prepare(q, k_cache, v_cache, block_tables, num_decode_rows, decode_context_
     return c
 
 
+def gather_kv(k_cache, v_cache, block_tables, cu_seqlens_k, cu_seqlens_k_list, *,
+              block_table_row0=0, k_scale=None, v_scale=None, side_k=None, side_v=None,
+              out_idx2d=None, head_n_out=None):
+    """_gather_kv (nanovllm/layers/attention.py:33-51) for every prefill chunk
+    of a step in one launch (kvc_gather_kv): chunk i's keys, read through
+    block table row block_table_row0 + i and dequantised as the reference
+    does for an int8 pool, at rows cu_seqlens_k[i] .. of the returned bf16
+    (K, V), each [cu_seqlens_k[-1], KVH, D]."""
+    enc = _kv_encoding(k_cache, k_scale)
+    cu_k = list(cu_seqlens_k_list)
+    total = cu_k[-1]
+    kvh, page = k_cache.size(2), k_cache.size(1)
+    out_k = torch.empty((total, kvh, k_cache.size(3)), dtype=torch.bfloat16, device=k_cache.device)
+    out_v = torch.empty_like(out_k)
+    if total == 0:
+        return out_k, out_v
+    nat.require_device(k_cache, v_cache, block_tables, cu_seqlens_k)
+    assert k_cache.is_contiguous() and v_cache.is_contiguous()
+    bt = block_tables.to(torch.int32)
+    if bt.stride(1) != 1:
+        bt = bt.contiguous()
+    cu = cu_seqlens_k.to(torch.int32).contiguous()
+    has_side = enc == nat.KVC_KV_INT8_CHAN and side_k is not None and head_n_out is not None
+    if enc == nat.KVC_KV_INT8_TOKHEAD:
+        k_scale, v_scale = k_scale.contiguous(), v_scale.contiguous()
+    elif enc == nat.KVC_KV_INT8_CHAN:
+        k_scale = k_scale.to(torch.float32).contiguous()
+        v_scale = v_scale.to(torch.float32).contiguous()
+    nat.call(
+        "kvc_gather_kv", nat.ptr(k_cache), nat.ptr(v_cache), k_cache.size(0), page, kvh,
+        k_cache.size(3), enc, nat.ptr(k_scale), nat.ptr(v_scale),
+        nat.ptr(side_k) if has_side else None, nat.ptr(side_v) if has_side else None,
+        nat.ptr(out_idx2d) if has_side else None, nat.ptr(head_n_out) if has_side else None,
+        side_k.size(-1) if has_side else 0, nat.ptr(bt), bt.stride(0), bt.size(1),
+        block_table_row0, len(cu_k) - 1, nat.ptr(cu), total, nat.ptr(out_k), nat.ptr(out_v),
+        nat.stream_of(out_k),
+    )
+    return out_k, out_v
+
+
+def _gathered_prefill(c, q, k_cache, v_cache, scale, k_scale, v_scale, side_k, side_v,
+                      out_idx2d, head_n_out):
+    """Prefill rows over an int8 pool as the reference reads them: the chunks'
+    keys gathered and dequantised to bf16 (gather_kv), then the bf16
+    stream-K prefill over those rows, whose outlier dims (a per-channel pool)
+    take the residue product."""
+    kg, vg = gather_kv(k_cache, v_cache, c.block_tables, c.cu_seqlens_k, c.cu_k_list,
+                       k_scale=k_scale, v_scale=v_scale, side_k=side_k, side_v=side_v,
+                       out_idx2d=out_idx2d, head_n_out=head_n_out)
+    has_side = c.enc == nat.KVC_KV_INT8_CHAN and side_k is not None and head_n_out is not None
+    nat.call(
+        "kvc_varlen_attention",
+        q.data_ptr(), q.stride(0), q.stride(1), c.T, c.num_heads, None, None, 0, 0,
+        c.num_kv_heads, c.head_dim, nat.KVC_KV_BF16, None, None, None, None,
+        nat.ptr(out_idx2d) if has_side else None, nat.ptr(head_n_out) if has_side else None,
+        side_k.size(-1) if has_side else 0,
+        nat.ptr(kg), kg.stride(0), kg.stride(1), nat.ptr(vg), vg.stride(0), vg.stride(1),
+        None, 0, 0, 0, None, c.num_prefill, nat.ptr(c.cu_seqlens_q), nat.ptr(c.cu_seqlens_k),
+        c.pre_units, c.max_seqlen_k, 0, 0,
+        float(scale), c.out.data_ptr(), c.out.stride(0), c.out.stride(1),
+        nat.ptr(c.ws), c.ws_bytes, nat.stream_of(q),
+    )
+    return c.out
+
+
 def varlen_attention(q, k_cache, v_cache, *, scale, block_tables=None,
                      num_decode_rows=0, decode_context_lens=None,
                      cu_seqlens_q=None, cu_seqlens_k=None,
@@ -142,6 +211,10 @@ def varlen_attention(q, k_cache, v_cache, *, scale, block_tables=None,
     if c.T == 0:
         return c.out
     enc, fresh, q = c.enc, c.fresh, c.q
+    if (enc != nat.KVC_KV_BF16 and not fresh and num_decode_rows == 0 and c.num_prefill
+            and os.environ.get("KVC_PREFILL_SK", "1") != "0"):
+        return _gathered_prefill(c, q, k_cache, v_cache, scale, k_scale, v_scale, side_k, side_v,
+                                 out_idx2d, head_n_out)
     has_side = enc == nat.KVC_KV_INT8_CHAN and side_k is not None and head_n_out is not None
     if enc == nat.KVC_KV_INT8_TOKHEAD:
         k_scale, v_scale = k_scale.contiguous(), v_scale.contiguous()

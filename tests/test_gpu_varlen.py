@@ -178,14 +178,16 @@ def test_fresh_kv_prefill_without_block_tables(partition):
     assert_attention_close(out, ref, "fresh-kv")
 
 
-def test_mixed_int8_tokhead_pool(partition):
+@pytest.mark.parametrize("rows", ["mixed", "prefill-only"])
+def test_mixed_int8_tokhead_pool(rows, partition):
     # Decode rows and prefix-cached prefill chunks over a per-token-head int8
     # pool (codes + fp32 scale per slot and kv head): the decode rows read the
     # pool as codes x scale in fp32 (paged_attention.py:138-145), the prefill
     # rows through the bf16 dequantisation the reference's prefill gathers
-    # with (attention.py:33-51).
+    # with (attention.py:33-51).  Prefill rows alone take the gathered form
+    # (gather_kv, then the bf16 stream-K prefill) unless KVC_PREFILL_SK=0.
     H, KVH, D = 32, 4, 128
-    dec_lens = [900, 1, 2500]
+    dec_lens = [900, 1, 2500] if rows == "mixed" else []
     chunks = [(0, 40), (700, 90), (3000, 33)]
     g = torch.Generator().manual_seed(21)
     all_lens = dec_lens + [p + c for p, c in chunks]
@@ -201,11 +203,12 @@ def test_mixed_int8_tokhead_pool(partition):
     for p, c in chunks:
         cu_q.append(cu_q[-1] + c)
         cu_k.append(cu_k[-1] + p + c)
-    print(f"[varlen] int8 tokhead mixed: rows={T} ({partition})", flush=True)
+    print(f"[varlen] int8 tokhead {rows}: rows={T} ({partition})", flush=True)
     out = varlen_attention(
         q.to(DEV), kc.to(DEV), vc.to(DEV), scale=D ** -0.5, block_tables=bt.to(DEV),
         num_decode_rows=len(dec_lens),
-        decode_context_lens=torch.tensor(dec_lens, dtype=torch.int32, device=DEV),
+        decode_context_lens=torch.tensor(dec_lens, dtype=torch.int32, device=DEV)
+        if dec_lens else None,
         cu_seqlens_q=torch.tensor(cu_q, dtype=torch.int32, device=DEV),
         cu_seqlens_k=torch.tensor(cu_k, dtype=torch.int32, device=DEV),
         cu_seqlens_q_list=cu_q, cu_seqlens_k_list=cu_k, k_scale=ks.to(DEV), v_scale=vs.to(DEV))
@@ -219,11 +222,14 @@ def test_mixed_int8_tokhead_pool(partition):
     assert_attention_close(out, ref, "mixed-int8-tokhead")
 
 
-def test_mixed_int8_channel_pool_with_side(partition):
+@pytest.mark.parametrize("rows", ["mixed", "prefill-only"])
+def test_mixed_int8_channel_pool_with_side(rows, partition):
     # The engine's per-channel int8 pool with the bf16 outlier side pool
     # (tests/p17_kv_int8.py:64-136 geometry, 16 q / 8 kv heads): one decode
     # row over 512 stored tokens plus a 100-token chunk after a 200-token
-    # prefix; the outlier dims come from the side pool exactly.
+    # prefix; the outlier dims come from the side pool exactly.  Head 2's
+    # value outliers (x60) hold the prefill rows to the fp32 reference only
+    # with the residue product on the bf16 P operand.
     key, value, s_k, s_v, ds_k, ds_v, out_idx2d, head_n_out = p17_unit_inputs()
     KVH, D, H = key.shape[1], key.shape[2], 16
     nout = out_idx2d.shape[1]
@@ -243,10 +249,12 @@ def test_mixed_int8_channel_pool_with_side(partition):
                        torch.tensor(slots_b, dtype=torch.int32, device=DEV))
     q = torch.randn(101, H, D, generator=torch.Generator().manual_seed(22)).to(torch.bfloat16)
     cu_q, cu_k = [0, 100], [0, 300]
-    print(f"[varlen] int8 channel mixed + side pool ({partition})", flush=True)
+    nd = 1 if rows == "mixed" else 0
+    q, bt = q[1 - nd:], bt[1 - nd:]
+    print(f"[varlen] int8 channel {rows} + side pool ({partition})", flush=True)
     out = varlen_attention(
-        q.to(DEV), kc, vc, scale=D ** -0.5, block_tables=bt.to(DEV), num_decode_rows=1,
-        decode_context_lens=torch.tensor([512], dtype=torch.int32, device=DEV),
+        q.to(DEV), kc, vc, scale=D ** -0.5, block_tables=bt.to(DEV), num_decode_rows=nd,
+        decode_context_lens=torch.tensor([512], dtype=torch.int32, device=DEV) if nd else None,
         cu_seqlens_q=torch.tensor(cu_q, dtype=torch.int32, device=DEV),
         cu_seqlens_k=torch.tensor(cu_k, dtype=torch.int32, device=DEV),
         cu_seqlens_q_list=cu_q, cu_seqlens_k_list=cu_k, k_scale=ds_k.to(DEV),
@@ -260,8 +268,8 @@ def test_mixed_int8_channel_pool_with_side(partition):
                              out_idx2d.numpy(), head_n_out.numpy())
     vp = ko.kv_float_prefill(vc.cpu().numpy(), "int8_chan", ds_v.numpy(), bits(sv),
                              out_idx2d.numpy(), head_n_out.numpy())
-    ref = ko.mixed_ref(bits(q), kf, vf, bt.numpy(), 1, np.asarray([512]), cu_q, cu_k, D ** -0.5,
-                       k_pre=kp, v_pre=vp)
+    ref = ko.mixed_ref(bits(q), kf, vf, bt.numpy(), nd, np.asarray([512][:nd]), cu_q, cu_k,
+                       D ** -0.5, k_pre=kp, v_pre=vp)
     assert_attention_close(out, ref, "mixed-int8-chan-side")
 
 
