@@ -166,29 +166,48 @@ def gather_kv(k_cache, v_cache, block_tables, cu_seqlens_k, cu_seqlens_k_list, *
     return out_k, out_v
 
 
-def _gathered_prefill(c, q, k_cache, v_cache, scale, k_scale, v_scale, side_k, side_v,
+def _gathered_prefill(c, q, nd, k_cache, v_cache, scale, k_scale, v_scale, side_k, side_v,
                       out_idx2d, head_n_out):
-    """Prefill rows over an int8 pool as the reference reads them: the chunks'
-    keys gathered and dequantised to bf16 (gather_kv), then the bf16
-    stream-K prefill over those rows, whose outlier dims (a per-channel pool)
-    take the residue product."""
+    """Prefill rows (query rows nd ..) over an int8 pool as the reference reads
+    them: the chunks' keys gathered and dequantised to bf16 (gather_kv,
+    block table rows nd + i), then the bf16 stream-K prefill over those rows,
+    whose outlier dims (a per-channel pool) take the residue product."""
     kg, vg = gather_kv(k_cache, v_cache, c.block_tables, c.cu_seqlens_k, c.cu_k_list,
-                       k_scale=k_scale, v_scale=v_scale, side_k=side_k, side_v=side_v,
-                       out_idx2d=out_idx2d, head_n_out=head_n_out)
+                       block_table_row0=nd, k_scale=k_scale, v_scale=v_scale, side_k=side_k,
+                       side_v=side_v, out_idx2d=out_idx2d, head_n_out=head_n_out)
     has_side = c.enc == nat.KVC_KV_INT8_CHAN and side_k is not None and head_n_out is not None
+    qp, op = q[nd:], c.out[nd:]
     nat.call(
         "kvc_varlen_attention",
-        q.data_ptr(), q.stride(0), q.stride(1), c.T, c.num_heads, None, None, 0, 0,
+        qp.data_ptr(), q.stride(0), q.stride(1), c.T - nd, c.num_heads, None, None, 0, 0,
         c.num_kv_heads, c.head_dim, nat.KVC_KV_BF16, None, None, None, None,
         nat.ptr(out_idx2d) if has_side else None, nat.ptr(head_n_out) if has_side else None,
         side_k.size(-1) if has_side else 0,
         nat.ptr(kg), kg.stride(0), kg.stride(1), nat.ptr(vg), vg.stride(0), vg.stride(1),
         None, 0, 0, 0, None, c.num_prefill, nat.ptr(c.cu_seqlens_q), nat.ptr(c.cu_seqlens_k),
         c.pre_units, c.max_seqlen_k, 0, 0,
-        float(scale), c.out.data_ptr(), c.out.stride(0), c.out.stride(1),
+        float(scale), op.data_ptr(), c.out.stride(0), c.out.stride(1),
         nat.ptr(c.ws), c.ws_bytes, nat.stream_of(q),
     )
     return c.out
+
+
+def _paged_rows(c, q, nd, k_cache, v_cache, scale, k_scale, v_scale, side_k, side_v, out_idx2d,
+                head_n_out, has_side):
+    """The decode rows 0 .. nd - 1 of a mixed call alone (no prefill chunks)."""
+    nat.call(
+        "kvc_varlen_attention",
+        q.data_ptr(), q.stride(0), q.stride(1), nd, c.num_heads,
+        nat.ptr(k_cache), nat.ptr(v_cache), k_cache.size(0), c.page_size, c.num_kv_heads,
+        c.head_dim, c.enc, nat.ptr(k_scale), nat.ptr(v_scale),
+        nat.ptr(side_k) if has_side else None, nat.ptr(side_v) if has_side else None,
+        nat.ptr(out_idx2d) if has_side else None, nat.ptr(head_n_out) if has_side else None,
+        side_k.size(-1) if has_side else 0, None, 0, 0, None, 0, 0,
+        nat.ptr(c.block_tables), c.block_tables.stride(0), c.max_blocks,
+        nd, nat.ptr(c.decode_context_lens), 0, None, None, 0, 0, 0, 0,
+        float(scale), c.out.data_ptr(), c.out.stride(0), c.out.stride(1),
+        nat.ptr(c.ws), c.ws_bytes, nat.stream_of(q),
+    )
 
 
 def varlen_attention(q, k_cache, v_cache, *, scale, block_tables=None,
@@ -211,16 +230,22 @@ def varlen_attention(q, k_cache, v_cache, *, scale, block_tables=None,
     if c.T == 0:
         return c.out
     enc, fresh, q = c.enc, c.fresh, c.q
-    if (enc != nat.KVC_KV_BF16 and not fresh and num_decode_rows == 0 and c.num_prefill
-            and os.environ.get("KVC_PREFILL_SK", "1") != "0"):
-        return _gathered_prefill(c, q, k_cache, v_cache, scale, k_scale, v_scale, side_k, side_v,
-                                 out_idx2d, head_n_out)
+    gathered = (enc != nat.KVC_KV_BF16 and not fresh and c.num_prefill
+                and os.environ.get("KVC_PREFILL_SK", "1") != "0")
     has_side = enc == nat.KVC_KV_INT8_CHAN and side_k is not None and head_n_out is not None
     if enc == nat.KVC_KV_INT8_TOKHEAD:
         k_scale, v_scale = k_scale.contiguous(), v_scale.contiguous()
     elif enc == nat.KVC_KV_INT8_CHAN:
         k_scale = k_scale.to(torch.float32).contiguous()
         v_scale = v_scale.to(torch.float32).contiguous()
+    if gathered:
+        # Int8 pool: the decode rows (if any) through the paged decode alone,
+        # then the prefill rows over their gathered, dequantised keys.
+        if num_decode_rows:
+            _paged_rows(c, q, num_decode_rows, k_cache, v_cache, scale, k_scale, v_scale,
+                        side_k, side_v, out_idx2d, head_n_out, has_side)
+        return _gathered_prefill(c, q, num_decode_rows, k_cache, v_cache, scale, k_scale, v_scale,
+                                 side_k, side_v, out_idx2d, head_n_out)
     nat.call(
         "kvc_varlen_attention",
         q.data_ptr(), q.stride(0), q.stride(1), c.T, c.num_heads,
