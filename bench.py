@@ -11,7 +11,7 @@ torch CPU decode path (gather + GQA expand + masked SDPA) timed on a bounded
 sample of the same workload on this host (cpu_baseline).
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 10]
-    python bench.py --workload mixed|mixed16|int8|decode-dist|append|swap|copy|rope|
+    python bench.py --workload mixed|mixed16|int8|prefill-int8|decode-dist|append|swap|copy|rope|
                      decode-graph|offload-overlap|pd-wire      (extra lines)
 """
 from __future__ import annotations
@@ -43,7 +43,7 @@ def parse_args():
                     choices=["decode", "decode-dist", "decode-tp2", "decode-cold", "cfg1",
                              "p15-grid", "int8", "mixed", "mixed16", "append", "swap", "copy",
                              "rope", "decode-graph", "offload-overlap", "pd-wire",
-                             "block-manager", "int8-chan"])
+                             "block-manager", "int8-chan", "prefill-int8"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--stamps", action="store_true",
                     help="decode workloads: also report the per-workgroup end times of the "
@@ -759,6 +759,82 @@ def run_mixed(args, torch, mix="mixed"):
     return res
 
 
+def run_prefill_int8(args, torch):
+    """The prefill rows of the mixed workload (4 chunks of 256 tokens after
+    prefixes 0 / 512 / 2048 / 8192, 32 q / 4 kv heads) over a bf16 pool, a
+    per-token-head int8 pool and a per-channel int8 pool (read scales, a side
+    pool of 8 slots per kv head with 4 outlier dims in use): one varlen call
+    each, timed in turn within every step.  The int8 calls read the pool as
+    the reference's prefill does (nanovllm/layers/attention.py:33-51): keys
+    gathered and dequantised to bf16, then the bf16 prefill."""
+    from nanovllm_amd.kernels.varlen import varlen_attention
+    from nanovllm_amd.workloads import build_block_tables
+
+    dev = torch.device("cuda:0")
+    heads, kvh = 32, 4
+    chunks = MIXES["mixed"][2]
+    lens = [p + c for p, c in chunks]
+    g = torch.Generator().manual_seed(4)
+    blocks = sum((n + 255) // 256 for n in lens) + 8
+    bt = build_block_tables(lens, blocks, 256, g).to(dev)
+    dg = torch.Generator(device=dev).manual_seed(5)
+    T = sum(c for _, c in chunks)
+    q = torch.randn(T, heads, 128, generator=dg, device=dev, dtype=torch.bfloat16)
+    cu_q, cu_k = [0], [0]
+    for p, c in chunks:
+        cu_q.append(cu_q[-1] + c)
+        cu_k.append(cu_k[-1] + p + c)
+    kw = dict(scale=128 ** -0.5, block_tables=bt, num_decode_rows=0,
+              cu_seqlens_q=torch.tensor(cu_q, dtype=torch.int32, device=dev),
+              cu_seqlens_k=torch.tensor(cu_k, dtype=torch.int32, device=dev),
+              cu_seqlens_q_list=cu_q, cu_seqlens_k_list=cu_k)
+    kcb = torch.randn(blocks, 256, kvh, 128, generator=dg, device=dev, dtype=torch.bfloat16)
+    vcb = torch.randn(blocks, 256, kvh, 128, generator=dg, device=dev, dtype=torch.bfloat16)
+    kc8 = torch.randint(-127, 128, (blocks, 256, kvh, 128), generator=dg, device=dev,
+                        dtype=torch.int8)
+    vc8 = torch.randint(-127, 128, (blocks, 256, kvh, 128), generator=dg, device=dev,
+                        dtype=torch.int8)
+    ksc = torch.rand(blocks, 256, kvh, generator=dg, device=dev) * 0.02
+    vsc = torch.rand(blocks, 256, kvh, generator=dg, device=dev) * 0.02
+    nom = 8
+    oi = torch.tensor([[3, 77, 20, 101, 45, 64, 9, 120]] * kvh, dtype=torch.int32, device=dev)
+    hn = torch.full((kvh,), 4, dtype=torch.int32, device=dev)
+    ds = torch.rand(kvh, 128, generator=dg, device=dev) * 0.02 + 0.01
+    ds[:, oi[0, :4].long()] = 0.0
+    side = torch.randn(blocks, 256, kvh, nom, generator=dg, device=dev).to(torch.bfloat16)
+    forms = {
+        "bf16": lambda: varlen_attention(q, kcb, vcb, **kw),
+        "int8_tokhead": lambda: varlen_attention(q, kc8, vc8, k_scale=ksc, v_scale=vsc, **kw),
+        "int8_chan": lambda: varlen_attention(q, kc8, vc8, k_scale=ds, v_scale=ds, side_k=side,
+                                              side_v=side, out_idx2d=oi, head_n_out=hn, **kw),
+    }
+    for _ in range(args.warmup):
+        for fn in forms.values():
+            fn()
+    torch.cuda.synchronize()
+    timers = {k: EventTimer(torch) for k in forms}
+    for _ in range(args.steps):
+        for k, fn in forms.items():
+            s = timers[k].start()
+            fn()
+            timers[k].stop(s)
+    torch.cuda.synchronize()
+    flops = 0
+    for p, c in chunks:
+        for r in range(c):
+            flops += 4 * 128 * heads * (p + r + 1)
+    out = {"workload": "prefill rows of the mixed workload (4x256-token chunks after prefixes "
+                       "0/512/2048/8192, 32q/4kv/128) over bf16 / int8 per-token-head / int8 "
+                       "per-channel (8 side slots, 4 in use) pools, one varlen call each",
+           "prefill_gflop": round(flops / 1e9, 2)}
+    for k, t in timers.items():
+        ms = t.mean_ms()
+        out[f"{k}_us"] = round(ms * 1e3, 1)
+        out[f"{k}_TFLOPs"] = round(flops / (ms * 1e-3) / 1e12, 1)
+        out[f"{k}_mfma_frac"] = round(flops / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)
+    return out
+
+
 def run_append(args, torch):
     from nanovllm_amd.layers.attention import store_kvcache
     dev = torch.device("cuda:0")
@@ -1263,6 +1339,8 @@ def main():
         res = run_p15_grid(args, torch)
     elif args.workload == "int8-chan":
         res = run_int8_chan(args, torch)
+    elif args.workload == "prefill-int8":
+        res = run_prefill_int8(args, torch)
     elif args.workload in MIXES:
         res = run_mixed(args, torch, args.workload)
     elif args.workload == "append":
