@@ -348,6 +348,10 @@ int64_t kvc_varlen_prefill_units(const int32_t* cu_q_host, const int32_t* cu_k_h
  *     block table row num_decode_rows + i, or, when block_tables is NULL (no
  *     prefix cache, attention.py:195-199), from the bf16 k_fresh/v_fresh
  *     [tokens, KVH, D] rows cu_seqlens_k[i] .. (then num_decode_rows == 0).
+ *     Fresh rows gathered from a per-channel int8 pool (kvc_gather_kv) may
+ *     come with that pool's out_idx2d / head_n_out / n_out_max (side pools
+ *     unused): the outlier dims' P V and the softmax sums then also take the
+ *     rounding residue of the bf16 P operand.
  * cu_seqlens_q/k are int32 device arrays of num_prefill + 1 entries;
  * num_prefill_units comes from kvc_varlen_prefill_units.
  * decode_ctx_tokens and prefill_kq_pairs are host-side hints (0: none) that
