@@ -99,8 +99,11 @@ struct AttnParams {
   const uint16_t* vf;
   int64_t vf_st, vf_sh;
   // split-K partials: [rows, heads, max_splits, D] fp32 and [rows, heads, max_splits]
+  // (the stream-K prefill: fp16 rows in part_o's first half, (lse, scale
+  // exponent) pairs in part_ml, in its second half)
   float* part_o;
   float* part_lse;
+  float2* part_ml;
   int max_splits;
   int merge_first;  // splits the merge loads before it reads a row's split count
   float xcd_skew;   // stream-K decode: even workgroups take (1 + skew) shares, odd (1 - skew)
@@ -3883,7 +3886,7 @@ constexpr int kP2QOff = kP2Stages * kPfStage;
 constexpr int kP2DummyOff = kP2QOff + kWaves * kP2QRegion;
 constexpr int kP2Smem = kP2DummyOff + 1024;
 constexpr int kP2StoresFinal = kPreNCB * 4;   // bf16 rows: 4 x 16 B a lane per column block
-constexpr int kP2StoresPart = kPreNCB * 9;    // fp32 partials: 8 x 16 B + the lse
+constexpr int kP2StoresPart = kPreNCB * 5;    // fp16 partials: 4 x 16 B + (lse, exponent)
 constexpr int kP2Steady = kPfTileLoads * (kP2Stages - 2);   // loads after the next tile's
 static_assert(kP2Smem <= 160 * 1024, "one workgroup per CU");
 static_assert(kPfTileLoads * (kP2Stages - 1) + kP2QLoads + kP2StoresPart + 1 <= 47,
@@ -4439,8 +4442,9 @@ __device__ __forceinline__ void prefill_sk2_share(const AttnParams& p,
         ro = tile_rsrc(p.out + row0 * p.o_st, int(int64_t(nrows) * p.o_st * 2));
       } else {
         const int64_t per_row = int64_t(p.num_heads) * p.max_splits;
-        ro = tile_rsrc(p.part_o + row0 * per_row * kD, int(nrows * per_row * kD * 4));
-        rl = tile_rsrc(p.part_lse + row0 * per_row, int(nrows * per_row * 4));
+        ro = tile_rsrc(reinterpret_cast<const uint16_t*>(p.part_o) + row0 * per_row * kD,
+                       int(nrows * per_row * kD * 2));
+        rl = tile_rsrc(p.part_ml + row0 * per_row, int(nrows * per_row * 8));
       }
       if (f == w && p.sk_nseg != nullptr && 64 * wave < nrows) {
         // Split counts of the item's rows (one per row and kv slice).
@@ -4553,20 +4557,37 @@ __device__ __forceinline__ void prefill_sk2_share(const AttnParams& p,
             __builtin_amdgcn_raw_buffer_store_b128(val, ro, base + 64 * t, 0, 0);
           }
         } else {
+          // Normalised partial row in fp16 (half the bytes of fp32 both
+          // ways), scaled by 2^-ex: ex = 0 unless the row's largest |value|
+          // reaches 2^15, then the smallest that keeps it below; the merge
+          // takes ex from the (lse, ex) pair.  Same lane swap and 16-byte
+          // pieces as the bf16 rows.
           const int idx = (tr * p.num_heads + hbase + hh) * p.max_splits + split;
           const float il = l > 0.f ? 1.f / l : 0.f;
-          const int base = ok ? idx * (kD * 4) + 16 * L.lg : kOob;
+          float amax = 0.f;
 #pragma unroll
-          for (int jj = 0; jj < 8; ++jj) {
-            const u32x4_t val = u32x4_t{__float_as_uint(st.o[cb][jj][0] * il),
-                                        __float_as_uint(st.o[cb][jj][1] * il),
-                                        __float_as_uint(st.o[cb][jj][2] * il),
-                                        __float_as_uint(st.o[cb][jj][3] * il)};
-            __builtin_amdgcn_raw_buffer_store_b128(val, ro, base + 64 * jj, 0, 0);
+          for (int jj = 0; jj < 8; ++jj)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) amax = fmaxf(amax, fabsf(st.o[cb][jj][r]));
+          amax = rows4_max(amax) * il;
+          const int ex = amax >= 32768.f ? ((__float_as_int(amax) >> 23) & 0xff) - 127 - 14 : 0;
+          const float sc = ldexpf(il, -ex);
+          const int base = ok ? idx * (kD * 2) + 32 * (L.lg & 1) + 16 * (L.lg >> 1) : kOob;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const uint32_t a0 = pack_f16x2(st.o[cb][2 * t][0] * sc, st.o[cb][2 * t][1] * sc);
+            const uint32_t a1 = pack_f16x2(st.o[cb][2 * t][2] * sc, st.o[cb][2 * t][3] * sc);
+            const uint32_t b0 = pack_f16x2(st.o[cb][2 * t + 1][0] * sc, st.o[cb][2 * t + 1][1] * sc);
+            const uint32_t b1 = pack_f16x2(st.o[cb][2 * t + 1][2] * sc, st.o[cb][2 * t + 1][3] * sc);
+            const auto x0 = __builtin_amdgcn_permlane16_swap(a0, b0, false, false);
+            const auto x1 = __builtin_amdgcn_permlane16_swap(a1, b1, false, false);
+            const u32x4_t val = u32x4_t{x0[0], x1[0], x0[1], x1[1]};
+            __builtin_amdgcn_raw_buffer_store_b128(val, ro, base + 64 * t, 0, 0);
           }
           const float lse = l > 0.f ? st.m[cb] + __log2f(l) : -INFINITY;
-          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(lse), rl,
-                                                (ok && L.lg == 0) ? idx * 4 : kOob, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b64(
+              u32x2_t{__float_as_uint(lse), __float_as_uint(float(ex))}, rl,
+              (ok && L.lg == 0) ? idx * 8 : kOob, 0, 0);
         }
       }
       issued += split < 0 ? kP2StoresFinal : kP2StoresPart;
@@ -4800,8 +4821,8 @@ constexpr int kSliceBatch = 4;  // splits per load batch (124 VGPRs: every wave 
 // Block `block` of the split merge of a stream-K prefill launch
 // (merge_slices_kernel).
 __device__ __forceinline__ void merge_slice_rows(const AttnParams& p, int num_rows,
-                                                 const float* __restrict__ part_o,
-                                                 const float* __restrict__ part_lse,
+                                                 const uint16_t* __restrict__ part_h,
+                                                 const float2* __restrict__ part_ml,
                                                  const int* __restrict__ nseg_arr,
                                                  int64_t block) {
   const int lane = threadIdx.x & 63;
@@ -4827,17 +4848,22 @@ __device__ __forceinline__ void merge_slice_rows(const AttnParams& p, int num_ro
     for (int d = 0; d < 16; ++d) acc[d] = 0.f;
     for (int s0 = 0; s0 < nsplit; s0 += kSliceBatch) {
       const int cnt = min(kSliceBatch, nsplit - s0);
-      float lse[kSliceBatch];
+      float lse[kSliceBatch], esc[kSliceBatch];
       float4 o[kSliceBatch][4];
 #pragma unroll
       for (int k = 0; k < kSliceBatch; ++k) {
         if (k < cnt) {
-          lse[k] = part_lse[base + s0 + k];
-          // lane sub: dims 32 q + 4 sub .. + 3, so each load of a wave reads
-          // 128 contiguous bytes per head
-          const float4* src = reinterpret_cast<const float4*>(part_o + (base + s0 + k) * kD) + sub;
+          const float2 ml = part_ml[base + s0 + k];
+          lse[k] = ml.x;
+          esc[k] = ml.y;
+          // lane sub: dims 32 q + 4 sub .. + 3 (fp16), so each load of a
+          // wave reads 64 contiguous bytes per head
+          const u32x2_t* src = reinterpret_cast<const u32x2_t*>(part_h + (base + s0 + k) * kD) + sub;
 #pragma unroll
-          for (int q = 0; q < 4; ++q) o[k][q] = src[8 * q];
+          for (int q = 0; q < 4; ++q) {
+            const u32x2_t h = src[8 * q];
+            o[k][q] = float4{f16_lo(h[0]), f16_hi(h[0]), f16_lo(h[1]), f16_hi(h[1])};
+          }
         }
       }
       float bm = -INFINITY;
@@ -4855,12 +4881,13 @@ __device__ __forceinline__ void merge_slice_rows(const AttnParams& p, int num_ro
           if (k < cnt) {
             const float wgt = __builtin_amdgcn_exp2f(lse[k] - m_new);
             l += wgt;
+            const float wo = ldexpf(wgt, int(esc[k]));  // the row's fp16 scale
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-              acc[4 * q + 0] += wgt * o[k][q].x;
-              acc[4 * q + 1] += wgt * o[k][q].y;
-              acc[4 * q + 2] += wgt * o[k][q].z;
-              acc[4 * q + 3] += wgt * o[k][q].w;
+              acc[4 * q + 0] += wo * o[k][q].x;
+              acc[4 * q + 1] += wo * o[k][q].y;
+              acc[4 * q + 2] += wo * o[k][q].z;
+              acc[4 * q + 3] += wo * o[k][q].w;
             }
           }
         }
@@ -4881,10 +4908,10 @@ __device__ __forceinline__ void merge_slice_rows(const AttnParams& p, int num_ro
 }
 
 __global__ void __launch_bounds__(64 * kMergeWaves)
-merge_slices_kernel(AttnParams p, int num_rows, const float* __restrict__ part_o,
-                    const float* __restrict__ part_lse, const int* __restrict__ nseg_arr) {
+merge_slices_kernel(AttnParams p, int num_rows, const uint16_t* __restrict__ part_h,
+                    const float2* __restrict__ part_ml, const int* __restrict__ nseg_arr) {
   touch_kernel_args(int(sizeof(AttnParams) + 4 * sizeof(void*)));
-  merge_slice_rows(p, num_rows, part_o, part_lse, nseg_arr, blockIdx.x);
+  merge_slice_rows(p, num_rows, part_h, part_ml, nseg_arr, blockIdx.x);
 }
 
 // Both merges of a mixed call's split launch in one launch: blocks
@@ -4897,14 +4924,16 @@ merge_mixed_kernel(AttnParams pd, AttnParams pp, int dec_rows, int dec_blocks, i
   if (b < dec_blocks) {
     merge_rows(pd, dec_rows, b);
   } else {
-    merge_slice_rows(pp, pre_rows, pp.part_o, pp.part_lse, pp.sk_nseg, b - dec_blocks);
+    merge_slice_rows(pp, pre_rows, reinterpret_cast<const uint16_t*>(pp.part_o), pp.part_ml,
+                     pp.sk_nseg, b - dec_blocks);
   }
 }
 
 void launch_merge_slices(const AttnParams& p, int64_t rows, hipStream_t st) {
   const int64_t waves = rows * p.kvh * p.nslices;
   merge_slices_kernel<<<unsigned((waves + kMergeWaves - 1) / kMergeWaves), 64 * kMergeWaves, 0,
-                        st>>>(p, int(rows), p.part_o, p.part_lse, p.sk_nseg);
+                        st>>>(p, int(rows), reinterpret_cast<const uint16_t*>(p.part_o),
+                              p.part_ml, p.sk_nseg);
 }
 
 // ---------------------------------------------------------------------------
@@ -5114,10 +5143,14 @@ void set_partials(AttnParams& p, void* ws, int64_t rows) {
   if (p.max_splits <= 1 || ws == nullptr) {
     p.part_o = nullptr;
     p.part_lse = nullptr;
+    p.part_ml = nullptr;
     return;
   }
   p.part_o = static_cast<float*>(ws);
   p.part_lse = p.part_o + size_t(rows) * p.num_heads * p.max_splits * kD;
+  // (stream-K prefill) pairs after the fp16 rows, inside part_o's span
+  p.part_ml = reinterpret_cast<float2*>(reinterpret_cast<char*>(ws) +
+                                        size_t(rows) * p.num_heads * p.max_splits * kD * 2);
 }
 
 int check_kv_args(int kv_dtype, const float* k_scale, const float* v_scale, const void* side_k,

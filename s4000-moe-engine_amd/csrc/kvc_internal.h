@@ -94,6 +94,18 @@ __device__ __forceinline__ uint32_t pack_bf16x2_fast(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// fp16 pair, round to nearest even (v_cvt_f16_f32), and back.
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  const _Float16 a = static_cast<_Float16>(lo), b = static_cast<_Float16>(hi);
+  return uint32_t(__builtin_bit_cast(uint16_t, a)) | (uint32_t(__builtin_bit_cast(uint16_t, b)) << 16);
+}
+__device__ __forceinline__ float f16_lo(uint32_t w) {
+  return float(__builtin_bit_cast(_Float16, uint16_t(w & 0xffffu)));
+}
+__device__ __forceinline__ float f16_hi(uint32_t w) {
+  return float(__builtin_bit_cast(_Float16, uint16_t(w >> 16)));
+}
+
 // max / sum over the lanes l, l ^ 16, l ^ 32, l ^ 48 (the four 16-lane rows),
 // with the row-swap permutes instead of LDS-routed shuffles.
 __device__ __forceinline__ float rows4_max(float x) {
