@@ -181,8 +181,10 @@ int kvc_paged_decode_layout(int64_t batch, int64_t num_heads, int64_t num_kv_hea
  * (side pointers may be NULL when no head has outliers; with head_n_out
  * given, n_out_max must be 1, 2, 4 or 8, the powers of two the reference
  * kernel's tl.arange(0, N_OUT_MAX) admits, and the side pools 4-byte
- * aligned, 2-byte for n_out_max 1).  context_lens[b] == 0 yields 0/0 = NaN
- * rows, as the reference kernel does. */
+ * aligned, 2-byte for n_out_max 1; a head's outlier dims are distinct, as
+ * the calibration makes them: the reference kernel sums the side logits of
+ * a repeated dim and stores its output once, in no defined order).
+ * context_lens[b] == 0 yields 0/0 = NaN rows, as the reference kernel does. */
 int kvc_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                      const void* k_cache, const void* v_cache, int64_t num_cache_blocks,
                      int64_t page_size, int64_t num_kv_heads, int64_t head_dim, int kv_dtype,

@@ -149,6 +149,72 @@ def test_many_chunks_empty_chunks_and_empty_context(partition):
     _check_mixed(c, "many-chunks")
 
 
+@pytest.mark.parametrize("enc", ["int8_tokhead", "int8_chan"])
+def test_int8_many_chunks_empty_chunks_and_empty_context(enc, partition):
+    # The many-chunks case over int8 pools: 70 chunks (every ninth empty),
+    # decode rows with an empty context, prefixes of any length; the prefill
+    # rows' keys are gathered with empty chunks in between.
+    rng = np.random.default_rng(13)
+    chunks = [(int(rng.integers(0, 300)), 0 if i % 9 == 4 else int(rng.integers(1, 24)))
+              for i in range(70)]
+    H, KVH, D = 32, 4, 128
+    dec_lens = [40, 0, 700]
+    g = torch.Generator().manual_seed(13)
+    all_lens = dec_lens + [p + c for p, c in chunks]
+    blocks = sum(max(1, (n + 255) // 256) for n in all_lens) + 3
+    bt = build_block_tables(all_lens, blocks, 256, g)
+    kc = torch.randint(-127, 128, (blocks, 256, KVH, D), generator=g, dtype=torch.int8)
+    vc = torch.randint(-127, 128, (blocks, 256, KVH, D), generator=g, dtype=torch.int8)
+    kw, side = {}, (None, None, None, None)
+    if enc == "int8_tokhead":
+        ks = torch.rand(blocks, 256, KVH, generator=g) * 0.03 + 0.005
+        vs = torch.rand(blocks, 256, KVH, generator=g) * 0.03 + 0.005
+        kw = dict(k_scale=ks.to(DEV), v_scale=vs.to(DEV))
+    else:
+        ks = torch.rand(KVH, D, generator=g) * 0.03 + 0.005
+        vs = torch.rand(KVH, D, generator=g) * 0.03 + 0.005
+        oi = torch.tensor([[7, 64, 0, 0], [1, 2, 3, 127], [50, 0, 0, 0], [9, 33, 100, 0]],
+                          dtype=torch.int32)
+        hn = torch.tensor([2, 4, 0, 3], dtype=torch.int32)
+        for h in range(KVH):
+            ks[h, oi[h, :int(hn[h])].long()] = 0.0
+            vs[h, oi[h, :int(hn[h])].long()] = 0.0
+        sk_ = (torch.randn(blocks, 256, KVH, 4, generator=g) * 3).to(torch.bfloat16)
+        sv_ = (torch.randn(blocks, 256, KVH, 4, generator=g) * 3).to(torch.bfloat16)
+        kw = dict(k_scale=ks.to(DEV), v_scale=vs.to(DEV), side_k=sk_.to(DEV), side_v=sv_.to(DEV),
+                  out_idx2d=oi.to(DEV), head_n_out=hn.to(DEV))
+        side = (bits(sk_), bits(sv_), oi.numpy(), hn.numpy())
+    T = len(dec_lens) + sum(c for _, c in chunks)
+    q = torch.randn(T, H, D, generator=g).to(torch.bfloat16)
+    cu_q, cu_k = [0], [0]
+    for p, c in chunks:
+        cu_q.append(cu_q[-1] + c)
+        cu_k.append(cu_k[-1] + p + c)
+    print(f"[varlen] {enc} many chunks ({partition})", flush=True)
+    out = varlen_attention(
+        q.to(DEV), kc.to(DEV), vc.to(DEV), scale=D ** -0.5, block_tables=bt.to(DEV),
+        num_decode_rows=len(dec_lens),
+        decode_context_lens=torch.tensor(dec_lens, dtype=torch.int32, device=DEV),
+        cu_seqlens_q=torch.tensor(cu_q, dtype=torch.int32, device=DEV),
+        cu_seqlens_k=torch.tensor(cu_k, dtype=torch.int32, device=DEV),
+        cu_seqlens_q_list=cu_q, cu_seqlens_k_list=cu_k, **kw)
+    torch.cuda.synchronize()
+    if enc == "int8_tokhead":
+        kf = ko.kv_float(kc.numpy(), enc, ks.numpy())
+        vf = ko.kv_float(vc.numpy(), enc, vs.numpy())
+        kp = ko.kv_float_prefill(kc.numpy(), enc, ks.numpy())
+        vp = ko.kv_float_prefill(vc.numpy(), enc, vs.numpy())
+    else:
+        sk_b, sv_b, oi_n, hn_n = side
+        kf = ko.kv_float(kc.numpy(), enc, ks.numpy(), sk_b, oi_n, hn_n)
+        vf = ko.kv_float(vc.numpy(), enc, vs.numpy(), sv_b, oi_n, hn_n)
+        kp = ko.kv_float_prefill(kc.numpy(), enc, ks.numpy(), sk_b, oi_n, hn_n)
+        vp = ko.kv_float_prefill(vc.numpy(), enc, vs.numpy(), sv_b, oi_n, hn_n)
+    ref = ko.mixed_ref(bits(q), kf, vf, bt.numpy(), len(dec_lens), np.asarray(dec_lens), cu_q,
+                       cu_k, D ** -0.5, k_pre=kp, v_pre=vp)
+    assert_attention_close(out, ref, f"{enc}-many-chunks")
+
+
 def test_long_chunk_many_query_tiles(partition):
     # 64 q / 2 kv heads: 16-head slices and 16-token query tiles, so a
     # 1100-token chunk spans 69 query tiles (the item search crosses a
