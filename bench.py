@@ -43,7 +43,7 @@ def parse_args():
                     choices=["decode", "decode-dist", "decode-tp2", "decode-cold", "cfg1",
                              "p15-grid", "int8", "mixed", "mixed16", "append", "swap", "copy",
                              "rope", "decode-graph", "offload-overlap", "pd-wire",
-                             "block-manager", "int8-chan", "prefill-int8"])
+                             "block-manager", "int8-chan", "prefill-int8", "prefill-scale"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--stamps", action="store_true",
                     help="decode workloads: also report the per-workgroup end times of the "
@@ -835,6 +835,85 @@ def run_prefill_int8(args, torch):
     return out
 
 
+def run_prefill_scale(args, torch):
+    """The stream-K prefill (prefill rows only, bf16 pool) over four chunks
+    after prefixes 0 / 512 / 2048 / 8192 whose length runs 64 .. 1024 tokens
+    (256 is the mixed workload's): the call time against the FLOPs, fitted
+    as fixed + FLOPs / rate, and the per-workgroup start and end stamps of
+    the prefill launch (KVC_PREFILL_STAMPS) at each length."""
+    import ctypes
+    from nanovllm_amd import _native as nat
+    from nanovllm_amd.kernels.varlen import varlen_attention
+    from nanovllm_amd.workloads import build_block_tables
+
+    dev = torch.device("cuda:0")
+    heads, kvh = 32, 4
+    points = []
+    for c in (64, 128, 256, 512, 1024):
+        chunks = [(0, c), (512, c), (2048, c), (8192, c)]
+        lens = [p + n for p, n in chunks]
+        g = torch.Generator().manual_seed(4)
+        blocks = sum((n + 255) // 256 for n in lens) + 8
+        bt = build_block_tables(lens, blocks, 256, g).to(dev)
+        dg = torch.Generator(device=dev).manual_seed(5)
+        T = sum(n for _, n in chunks)
+        q = torch.randn(T, heads, 128, generator=dg, device=dev, dtype=torch.bfloat16)
+        kc = torch.randn(blocks, 256, kvh, 128, generator=dg, device=dev, dtype=torch.bfloat16)
+        vc = torch.randn(blocks, 256, kvh, 128, generator=dg, device=dev, dtype=torch.bfloat16)
+        cu_q, cu_k = [0], [0]
+        for p, n in chunks:
+            cu_q.append(cu_q[-1] + n)
+            cu_k.append(cu_k[-1] + p + n)
+        kw = dict(scale=128 ** -0.5, block_tables=bt, num_decode_rows=0,
+                  cu_seqlens_q=torch.tensor(cu_q, dtype=torch.int32, device=dev),
+                  cu_seqlens_k=torch.tensor(cu_k, dtype=torch.int32, device=dev),
+                  cu_seqlens_q_list=cu_q, cu_seqlens_k_list=cu_k)
+        for _ in range(args.warmup):
+            varlen_attention(q, kc, vc, **kw)
+        torch.cuda.synchronize()
+        timer = EventTimer(torch)
+        for _ in range(args.steps):
+            st = timer.start()
+            varlen_attention(q, kc, vc, **kw)
+            timer.stop(st)
+        torch.cuda.synchronize()
+        us = timer.mean_ms() * 1e3
+        flops = sum(4 * 128 * heads * (p + r + 1) for p, n in chunks for r in range(n))
+        # Stamps of the prefill launch (the slice merge is a launch of its own).
+        buf = (ctypes.c_ulonglong * 8192)()
+        nwg, khz = ctypes.c_int(), ctypes.c_int()
+        os.environ["KVC_PREFILL_STAMPS"] = "1"
+        rows = []
+        try:
+            for _ in range(5):
+                varlen_attention(q, kc, vc, **kw)
+                torch.cuda.synchronize()
+                nat.call("kvc_decode_stamps", ctypes.addressof(buf), 4096,
+                         ctypes.addressof(nwg), ctypes.addressof(khz))
+                n_wg, tick = nwg.value, 1e3 / khz.value
+                t0 = min(buf[2 * v] for v in range(n_wg))
+                ends = sorted((buf[2 * v + 1] - t0) * tick for v in range(n_wg))
+                busy = [e for e in ends if e > 5.0] or ends
+                rows.append((busy[len(busy) // 10], ends[n_wg // 2], ends[-1]))
+        finally:
+            del os.environ["KVC_PREFILL_STAMPS"]
+        med = [round(statistics.median(r[i] for r in rows), 2) for i in range(3)]
+        points.append({"chunk": c, "gflop": round(flops / 1e9, 2), "call_us": round(us, 1),
+                       "TFLOPs": round(flops / (us * 1e-6) / 1e12, 1),
+                       "end_p10_us": med[0], "end_median_us": med[1], "end_last_us": med[2]})
+    # Least-squares fit of call_us = fixed + gflop / rate over the five points.
+    xs = [pt["gflop"] for pt in points]
+    ys = [pt["call_us"] for pt in points]
+    mx, my = sum(xs) / len(xs), sum(ys) / len(ys)
+    slope = sum((x - mx) * (y - my) for x, y in zip(xs, ys)) / sum((x - mx) ** 2 for x in xs)
+    return {"workload": "stream-K prefill rows only (bf16 pool, 32q/4kv/128, page 256), four "
+                        "chunks after prefixes 0/512/2048/8192, chunk length 64..1024 tokens",
+            "points": points,
+            "fit_fixed_us": round(my - slope * mx, 1),
+            "fit_marginal_TFLOPs": round(1e3 / slope, 1),
+            "fit_marginal_mfma_frac": round(1e3 / slope / MFMA_BF16_PEAK_TFLOPS, 4)}
+
+
 def run_append(args, torch):
     from nanovllm_amd.layers.attention import store_kvcache
     dev = torch.device("cuda:0")
@@ -1341,6 +1420,8 @@ def main():
         res = run_int8_chan(args, torch)
     elif args.workload == "prefill-int8":
         res = run_prefill_int8(args, torch)
+    elif args.workload == "prefill-scale":
+        res = run_prefill_scale(args, torch)
     elif args.workload in MIXES:
         res = run_mixed(args, torch, args.workload)
     elif args.workload == "append":

@@ -310,8 +310,9 @@ int kvc_paged_decode_append_static(
 
 /* Diagnostics, no reference counterpart: with KVC_DECODE_STAMPS=1 in the
  * environment, every stream-K decode launch (up to 4096 workgroups) has each
- * workgroup w record its start and end wall-clock stamps; this copies the
- * last recording launch's stamps on the current device to host_out
+ * workgroup w record its start and end wall-clock stamps (with
+ * KVC_PREFILL_STAMPS=1, every prefill-only stream-K prefill launch); this
+ * copies the last recording launch's stamps on the current device to host_out
  * ([2 w] start, [2 w + 1] end, up to max_workgroups workgroups; a blocking
  * copy, so synchronise the launch's stream first) and reports the number of
  * workgroups and the stamp clock's rate in kHz.  KVC_ERR_VALUE when no launch

@@ -3986,6 +3986,14 @@ __device__ __forceinline__ void prefill_sk2_share(const AttnParams& p,
                                                   const int32_t* __restrict__ block_tables,
                                                   const int v, const int G, char* lds,
                                                   int4* ctab) {
+  const unsigned long long t_start =
+      p.wg_stamps != nullptr ? __builtin_amdgcn_s_memrealtime() : 0ull;
+  auto stamp = [&]() {  // diagnostics: this workgroup's start and end
+    if (p.wg_stamps != nullptr && threadIdx.x == 0) {
+      p.wg_stamps[2 * v] = t_start;
+      p.wg_stamps[2 * v + 1] = __builtin_amdgcn_s_memrealtime();
+    }
+  };
   const LaneId L = lane_id();
   const int wave = uniform(int(threadIdx.x >> 6));
   const int kvs_total = p.kvh * p.nslices;
@@ -4023,7 +4031,10 @@ __device__ __forceinline__ void prefill_sk2_share(const AttnParams& p,
   int S = max(p.sk_min_share, (W + G - 1) / G);
   if (p.max_splits > 1) S = max(S, (Tmax + kP2ItemCost + p.max_splits - 2) / (p.max_splits - 1));
   S = uniform(S);
-  if (int64_t(w) * S >= W) return;
+  if (int64_t(w) * S >= W) {
+    stamp();
+    return;
+  }
   const int start = w * S;
   const int end = min(W, start + S);
 
@@ -4600,6 +4611,11 @@ __device__ __forceinline__ void prefill_sk2_share(const AttnParams& p,
     }
   }
   __builtin_amdgcn_s_waitcnt(0);
+  if (p.wg_stamps != nullptr) {
+    __syncthreads();  // every wave has issued its last stores
+    stamp();
+  }
+
 }
 
 template <bool kFresh, bool kPLo = false>
@@ -6050,6 +6066,10 @@ int varlen_impl(
       return KVC_OK;
     }
     if (num_prefill > 0) {
+      // Per-workgroup stamps for diagnostics (KVC_PREFILL_STAMPS=1), read
+      // back through kvc_decode_stamps.
+      if (env_int("KVC_PREFILL_STAMPS", 0) != 0 && sp.grid <= stamp_slots())
+        p.wg_stamps = stamp_buffer(sp.grid);
       launch_prefill_sk(p, sp.grid, fresh, st);
       rc = check_launch("varlen_attention");
       if (rc != KVC_OK) return rc;
