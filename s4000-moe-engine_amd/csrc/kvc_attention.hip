@@ -5249,8 +5249,9 @@ constexpr double kMixPrefillFlopsPerCuUs = 4.3e6;
 // With the host's hints (the decode rows' total context in tokens, and the
 // prefill's query-key pairs per head: sum over chunks of
 // sq (sk - sq) + sq (sq + 1) / 2), the CUs split in proportion to the two
-// sides' CU-time at the rates above, so that both end together (rounded to
-// a multiple of 8, at least 8 on each side).  Without hints the decode side
+// sides' CU-time at the rates above, so that both end together (at a
+// multiple of 8, at least 8 on each side: of the two around the balance
+// point, the one whose slower side ends sooner).  Without hints the decode side
 // gets 3/8 of the CUs, the balance of 60 decode rows of U[256,4096] and four
 // 256-token chunks.  KVC_MIXED_DECODE_CUS overrides both (rounded down to a
 // multiple of 8; 0: the two launches one after the other).
@@ -5272,8 +5273,14 @@ int mixed_decode_cus(int64_t num_decode_rows, int64_t num_prefill_tokens, int kv
                          kMixDecodeBytesPerCuUs;
       const double pre =
           4.0 * kD * double(num_heads) * double(prefill_kq_pairs) / kMixPrefillFlopsPerCuUs;
-      n = int(std::lround(double(total) * dec / (dec + pre) / 8.0)) * 8;
-      n = std::min(std::max(n, 8), total - 8);
+      // The two multiples of 8 around the balance point; of them, the one
+      // whose slower side ends sooner (a side's time falls as 1 / its CUs,
+      // so the nearer multiple is not always the better one).
+      const double nf = double(total) * dec / (dec + pre);
+      const int lo = std::min(std::max(int(nf / 8.0) * 8, 8), total - 8);
+      const int hi = std::min(lo + 8, total - 8);
+      auto slower = [&](int m) { return std::max(dec / m, pre / (total - m)); };
+      n = slower(hi) < slower(lo) ? hi : lo;
     } else {
       n = total * 3 / 8;
     }
