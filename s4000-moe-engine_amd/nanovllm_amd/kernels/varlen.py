@@ -219,7 +219,9 @@ def varlen_attention(q, k_cache, v_cache, *, scale, block_tables=None,
                      out_idx2d=None, head_n_out=None, decode_context_lens_list=None):
     """q: [T, H, D] bf16 with T = num_decode_rows + prefill tokens.
     k/v: the step's fresh [T_k, KVH, D] bf16 keys/values, used only when
-    block_tables is None (pure prefill without a prefix cache).
+    block_tables is None (pure prefill without a prefix cache); rows that
+    gather_kv read from a per-channel int8 pool may come with that pool's
+    out_idx2d / head_n_out, which give its outlier dims the residue product.
     decode_context_lens_list: the decode rows' context lengths as host ints
     (optional; with them a mixed call over a bf16 pool sizes its CU split to
     the work of both sides).
@@ -233,6 +235,8 @@ def varlen_attention(q, k_cache, v_cache, *, scale, block_tables=None,
     gathered = (enc != nat.KVC_KV_BF16 and not fresh and c.num_prefill
                 and os.environ.get("KVC_PREFILL_SK", "1") != "0")
     has_side = enc == nat.KVC_KV_INT8_CHAN and side_k is not None and head_n_out is not None
+    # fresh rows gathered from a per-channel pool name its outlier dims
+    fresh_out = fresh and out_idx2d is not None and head_n_out is not None
     if enc == nat.KVC_KV_INT8_TOKHEAD:
         k_scale, v_scale = k_scale.contiguous(), v_scale.contiguous()
     elif enc == nat.KVC_KV_INT8_CHAN:
@@ -253,8 +257,9 @@ def varlen_attention(q, k_cache, v_cache, *, scale, block_tables=None,
         k_cache.size(0) if not fresh else 0, c.page_size, c.num_kv_heads, c.head_dim, enc,
         nat.ptr(k_scale), nat.ptr(v_scale),
         nat.ptr(side_k) if has_side else None, nat.ptr(side_v) if has_side else None,
-        nat.ptr(out_idx2d) if has_side else None, nat.ptr(head_n_out) if has_side else None,
-        side_k.size(-1) if has_side else 0,
+        nat.ptr(out_idx2d) if has_side or fresh_out else None,
+        nat.ptr(head_n_out) if has_side or fresh_out else None,
+        side_k.size(-1) if has_side else (out_idx2d.size(1) if fresh_out else 0),
         nat.ptr(k) if fresh else None, k.stride(0) if fresh else 0, k.stride(1) if fresh else 0,
         nat.ptr(v) if fresh else None, v.stride(0) if fresh else 0, v.stride(1) if fresh else 0,
         nat.ptr(c.block_tables) if not fresh else None,

@@ -10,7 +10,7 @@ import torch
 
 from helpers import assert_attention_close, bits, gathered_pool, p17_unit_inputs
 from nanovllm_amd.kernels.kv_int8 import store_kvcache_int8
-from nanovllm_amd.kernels.varlen import (varlen_attention, varlen_attention_append,
+from nanovllm_amd.kernels.varlen import (gather_kv, varlen_attention, varlen_attention_append,
                                          varlen_decode_cus)
 from nanovllm_amd.layers.attention import Attention, store_kvcache
 from nanovllm_amd.utils.context import reset_context, set_context
@@ -337,6 +337,41 @@ def test_mixed_int8_channel_pool_with_side(rows, partition):
     ref = ko.mixed_ref(bits(q), kf, vf, bt.numpy(), nd, np.asarray([512][:nd]), cu_q, cu_k,
                        D ** -0.5, k_pre=kp, v_pre=vp)
     assert_attention_close(out, ref, "mixed-int8-chan-side")
+
+
+def test_fresh_rows_gathered_from_a_channel_pool(partition):
+    # The two calls an int8 prefill makes, by hand: gather_kv of the p17
+    # per-channel pool, then a no-prefix-cache call over the gathered rows
+    # naming the pool's outlier dims (the residue product on both prefill
+    # launch forms).  Same result as the paged call against the oracle.
+    key, value, s_k, s_v, ds_k, ds_v, out_idx2d, head_n_out = p17_unit_inputs()
+    KVH, D, H = key.shape[1], key.shape[2], 16
+    nout = out_idx2d.shape[1]
+    kc = torch.zeros(2, 256, KVH, D, dtype=torch.int8, device=DEV)
+    vc = torch.zeros_like(kc)
+    sk = torch.zeros(2, 256, KVH, nout, dtype=torch.bfloat16, device=DEV)
+    sv = torch.zeros_like(sk)
+    oi, hn = out_idx2d.to(DEV), head_n_out.to(DEV)
+    slots = torch.tensor([256 + t if t < 256 else t - 256 for t in range(512)], dtype=torch.int32,
+                         device=DEV)
+    store_kvcache_int8(key.to(DEV), value.to(DEV), kc, vc, s_k.to(DEV), s_v.to(DEV), sk, sv, oi,
+                       hn, slots)
+    bt = torch.tensor([[1, 0], [1, 0]], dtype=torch.int32)
+    cu_q, cu_k = [0, 60, 160], [0, 300, 812]   # chunk 0: 60 queries after 240 keys; chunk 1: 100 after 412
+    cuk = torch.tensor(cu_k, dtype=torch.int32, device=DEV)
+    kg, vg = gather_kv(kc, vc, bt.to(DEV), cuk, cu_k, k_scale=ds_k.to(DEV), v_scale=ds_v.to(DEV),
+                       side_k=sk, side_v=sv, out_idx2d=oi, head_n_out=hn)
+    q = torch.randn(160, H, D, generator=torch.Generator().manual_seed(23)).to(torch.bfloat16)
+    print(f"[varlen] fresh rows from a channel pool ({partition})", flush=True)
+    out = varlen_attention(q.to(DEV), None, None, scale=D ** -0.5, block_tables=None, k=kg, v=vg,
+                           cu_seqlens_q=torch.tensor(cu_q, dtype=torch.int32, device=DEV),
+                           cu_seqlens_k=cuk, cu_seqlens_q_list=cu_q, cu_seqlens_k_list=cu_k,
+                           out_idx2d=oi, head_n_out=hn)
+    torch.cuda.synchronize()
+    ref = ko.prefill_ref(bits(q), None, None, None, cu_q, cu_k, D ** -0.5,
+                         fresh_k=ko.bf16_to_f32(bits(kg.cpu())),
+                         fresh_v=ko.bf16_to_f32(bits(vg.cpu())))
+    assert_attention_close(out, ref, "fresh-from-channel-pool")
 
 
 def test_attention_forward_mixed_matches_decode_and_prefill_paths():
