@@ -3569,7 +3569,10 @@ __device__ __forceinline__ bool find_prefill_unit(const AttnParams& p, int u, in
 }
 
 // One workgroup per prefill unit (chunk, query tile, kv slice, key split):
-// the launch for int8 pools and for KVC_PREFILL_SK=0.
+// the launch under KVC_PREFILL_SK=0, and for a paged int8 pool passed to
+// kvc_varlen_attention directly (its stage dequantises the tiles; the faster
+// route gathers the keys first, kvc_gather_kv, and runs the stream-K
+// prefill over them).
 template <int kEnc, bool kFresh, bool kPLo = (kEnc == kI8Chan)>
 __global__ void __launch_bounds__(kThreads)
 varlen_kernel(AttnParams p, const int32_t* __restrict__ block_tables) {
@@ -3586,8 +3589,9 @@ varlen_kernel(AttnParams p, const int32_t* __restrict__ block_tables) {
 }
 
 // ---------------------------------------------------------------------------
-// Stream-K prefill launch over bf16 keys (a paged bf16 pool, or the step's
-// fresh k/v when there is no prefix cache).  Items are (chunk i, kv slice,
+// Stream-K prefill launch over bf16 keys (a paged bf16 pool, or fresh rows:
+// the step's k/v when there is no prefix cache, or an int8 pool's keys
+// gathered by kvc_gather_kv).  Items are (chunk i, kv slice,
 // query tile), query tile fastest; each is a run of 32-key tiles that stops
 // at the last key its queries see.  The concatenated tiles (plus a fixed cost
 // per item) are cut into one equal share per workgroup, so chunks of any
