@@ -244,8 +244,9 @@ constexpr int kGatherLanes = 8;
 constexpr int kGatherRows = kThreads / kGatherLanes;
 constexpr int kGatherIters = 2;  // token groups a block runs (per-head constants loaded once)
 
-// One side-pool row (n_out_max bf16, a power of two up to 8, row-aligned)
-// as 16-bit values.
+// One side-pool row (n_out_max bf16, up to 8) as 16-bit values: one aligned
+// load for the power-of-two widths (a row then starts at a multiple of its
+// size), else element by element.
 __device__ __forceinline__ void load_side_row16(const uint16_t* row, int nom,
                                                 uint32_t (&v)[kSideMaxStore]) {
   uint32_t w[4] = {0u, 0u, 0u, 0u};
@@ -258,7 +259,9 @@ __device__ __forceinline__ void load_side_row16(const uint16_t* row, int nom,
   } else if (nom == 2) {
     w[0] = *reinterpret_cast<const uint32_t*>(row);
   } else {
-    w[0] = *row;
+#pragma unroll
+    for (int j = 0; j < kSideMaxStore; ++j)
+      if (j < nom) w[j >> 1] |= uint32_t(row[j]) << ((j & 1) * 16);
   }
 #pragma unroll
   for (int j = 0; j < kSideMaxStore; ++j) v[j] = (w[j >> 1] >> ((j & 1) * 16)) & 0xffffu;

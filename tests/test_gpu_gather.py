@@ -28,9 +28,10 @@ def _expected(pool_bits, bt, cu_k, row0):
     return np.concatenate(parts, axis=0)
 
 
-@pytest.mark.parametrize("kv", ["bf16", "int8_tokhead", "int8_chan"])
+@pytest.mark.parametrize("kv,nom", [("bf16", 8), ("int8_tokhead", 8), ("int8_chan", 8),
+                                    ("int8_chan", 3), ("int8_chan", 1)])
 @pytest.mark.parametrize("page", [32, 256])
-def test_gather_kv_is_the_reference_gather(kv, page):
+def test_gather_kv_is_the_reference_gather(kv, nom, page):
     # Ragged chunks (an empty one, one key, a page edge, several pages), a
     # table row offset (rows of decode sequences ahead of the chunks).
     KVH, D = 4, 128
@@ -59,12 +60,14 @@ def test_gather_kv_is_the_reference_gather(kv, page):
         else:
             ks = torch.rand(KVH, D, generator=g) * 0.03 + 0.005
             vs = torch.rand(KVH, D, generator=g) * 0.03 + 0.005
-            nom = 8
+            # any side width up to 8 (the attention takes powers of two)
             oi = torch.zeros(KVH, nom, dtype=torch.int32)
-            oi[0, :3] = torch.tensor([5, 77, 127])
-            oi[1, :2] = torch.tensor([9, 9])           # a duplicate dim: the later slot wins
-            oi[3, :8] = torch.arange(0, 128, 16)[:8]
-            hn = torch.tensor([3, 2, 0, 8], dtype=torch.int32)
+            full = {0: [5, 77, 127], 1: [9, 9], 3: list(range(0, 128, 16))}  # 9, 9: the later slot wins
+            hn = torch.zeros(KVH, dtype=torch.int32)
+            for h, dims in full.items():
+                n_h = min(len(dims), nom)
+                oi[h, :n_h] = torch.tensor(dims[:n_h])
+                hn[h] = n_h
             for h in range(KVH):
                 ks[h, oi[h, :int(hn[h])].long()] = 0.0
                 vs[h, oi[h, :int(hn[h])].long()] = 0.0
@@ -77,7 +80,7 @@ def test_gather_kv_is_the_reference_gather(kv, page):
                                  hn.numpy()).reshape(blocks, page, KVH, D)
             kw = dict(k_scale=ks.to(DEV), v_scale=vs.to(DEV), side_k=sk_.to(DEV),
                       side_v=sv_.to(DEV), out_idx2d=oi.to(DEV), head_n_out=hn.to(DEV))
-    print(f"[gather] {kv} page={page} keys={cu_k[-1]}", flush=True)
+    print(f"[gather] {kv} side slots={nom} page={page} keys={cu_k[-1]}", flush=True)
     gk, gv = gather_kv(kc.to(DEV), vc.to(DEV), bt.to(DEV),
                        torch.tensor(cu_k, dtype=torch.int32, device=DEV), cu_k,
                        block_table_row0=1, **kw)
