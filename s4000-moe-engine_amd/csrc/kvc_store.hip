@@ -242,7 +242,11 @@ dequant_tokhead_kernel(const int8_t* __restrict__ kv, const float* __restrict__ 
 constexpr int kSideMaxStore = 8;  // side slots a gathered row takes (the attention's bound)
 constexpr int kGatherLanes = 8;
 constexpr int kGatherRows = kThreads / kGatherLanes;
-constexpr int kGatherIters = 2;  // token groups a block runs (per-head constants loaded once)
+// Token groups a block runs: two for the per-channel pool (its per-head read
+// scales and outlier dims are loaded once for both; 14.8 against 19 us on the
+// config-3 chunks), one otherwise (10.3 against 11.7 us per-token-head).
+template <int kEnc>
+constexpr int gather_iters() { return kEnc == KVC_KV_INT8_CHAN ? 2 : 1; }
 
 // One side-pool row (n_out_max bf16, up to 8) as 16-bit values: one aligned
 // load for the power-of-two widths (a row then starts at a multiple of its
@@ -296,9 +300,10 @@ gather_kv_kernel(const char* __restrict__ k_cache, const char* __restrict__ v_ca
       dims[j] = j < n_out ? out_idx2d[h * n_out_max + j] - lane8 * 16 : -1;
   }
 #pragma unroll
-  for (int it = 0; it < kGatherIters; ++it) {
+  for (int it = 0; it < gather_iters<kEnc>(); ++it) {
     const int64_t t =
-        (int64_t(blockIdx.x) * kGatherIters + it) * kGatherRows + (threadIdx.x / kGatherLanes);
+        (int64_t(blockIdx.x) * gather_iters<kEnc>() + it) * kGatherRows +
+        (threadIdx.x / kGatherLanes);
     if (t >= tokens) break;
     const int64_t row = t * kvh + h;
     // chunk i: the last with cu_k[i] <= t
@@ -559,9 +564,9 @@ extern "C" int kvc_gather_kv(const void* k_cache, const void* v_cache, int64_t n
   }
   KVC_REQUIRE(max_blocks_per_seq > 0 && max_blocks_per_seq <= bt_stride, KVC_ERR_VALUE,
               "gather_kv: max_blocks_per_seq must be in [1, bt_stride]");
-  const int64_t per_block = int64_t(kGatherRows) * kGatherIters;
-  const dim3 grid(unsigned((total_keys + per_block - 1) / per_block), unsigned(num_kv_heads));
-  auto launch = [&](auto kern) {
+  auto launch = [&](auto kern, int iters) {
+    const int64_t per_block = int64_t(kGatherRows) * iters;
+    const dim3 grid(unsigned((total_keys + per_block - 1) / per_block), unsigned(num_kv_heads));
     kern<<<grid, kThreads, 0, as_stream(stream)>>>(
         static_cast<const char*>(k_cache), static_cast<const char*>(v_cache),
         num_cache_blocks * page_size, int(page_size), int(num_kv_heads), k_scale, v_scale,
@@ -571,11 +576,11 @@ extern "C" int kvc_gather_kv(const void* k_cache, const void* v_cache, int64_t n
         total_keys, static_cast<uint16_t*>(out_k), static_cast<uint16_t*>(out_v));
   };
   if (kv_dtype == KVC_KV_BF16) {
-    launch(gather_kv_kernel<KVC_KV_BF16>);
+    launch(gather_kv_kernel<KVC_KV_BF16>, gather_iters<KVC_KV_BF16>());
   } else if (kv_dtype == KVC_KV_INT8_TOKHEAD) {
-    launch(gather_kv_kernel<KVC_KV_INT8_TOKHEAD>);
+    launch(gather_kv_kernel<KVC_KV_INT8_TOKHEAD>, gather_iters<KVC_KV_INT8_TOKHEAD>());
   } else {
-    launch(gather_kv_kernel<KVC_KV_INT8_CHAN>);
+    launch(gather_kv_kernel<KVC_KV_INT8_CHAN>, gather_iters<KVC_KV_INT8_CHAN>());
   }
   return check_launch("gather_kv");
 }
