@@ -215,6 +215,67 @@ def test_int8_many_chunks_empty_chunks_and_empty_context(enc, partition):
     assert_attention_close(out, ref, f"{enc}-many-chunks")
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_int8_chan_random_mixes(seed):
+    # Seeded random mixes over a per-channel pool: head groupings, pages,
+    # side widths, outlier counts per head (distinct dims), decode rows and
+    # chunks with and without prefixes; decode rows read the pool in fp32,
+    # prefill rows through the bf16 gather (both against the oracle).
+    rng = np.random.default_rng(100 + seed)
+    H, KVH = [(32, 4), (16, 8), (64, 2), (32, 8), (12, 4), (32, 32)][seed]
+    D = 128
+    page = int(rng.choice([64, 128, 256]))
+    nom = int(rng.choice([1, 2, 4, 8]))
+    n_dec = int(rng.integers(0, 5))
+    dec_lens = [int(rng.integers(1, 1500)) for _ in range(n_dec)]
+    chunks = [(int(rng.integers(0, 900)), int(rng.integers(1, 200)))
+              for _ in range(int(rng.integers(1, 6)))]
+    g = torch.Generator().manual_seed(200 + seed)
+    all_lens = dec_lens + [p + c for p, c in chunks]
+    blocks = sum(max(1, (n + page - 1) // page) for n in all_lens) + 2
+    bt = build_block_tables(all_lens, blocks, page, g)
+    kc = torch.randint(-127, 128, (blocks, page, KVH, D), generator=g, dtype=torch.int8)
+    vc = torch.randint(-127, 128, (blocks, page, KVH, D), generator=g, dtype=torch.int8)
+    ks = torch.rand(KVH, D, generator=g) * 0.02 + 0.004
+    vs = torch.rand(KVH, D, generator=g) * 0.02 + 0.004
+    oi = torch.zeros(KVH, nom, dtype=torch.int32)
+    hn = torch.zeros(KVH, dtype=torch.int32)
+    for h in range(KVH):
+        n_h = int(rng.integers(0, nom + 1))
+        oi[h, :n_h] = torch.from_numpy(rng.choice(D, n_h, replace=False).astype(np.int32))
+        hn[h] = n_h
+        ks[h, oi[h, :n_h].long()] = 0.0
+        vs[h, oi[h, :n_h].long()] = 0.0
+    sk_ = (torch.randn(blocks, page, KVH, nom, generator=g) * 4).to(torch.bfloat16)
+    sv_ = (torch.randn(blocks, page, KVH, nom, generator=g) * 4).to(torch.bfloat16)
+    T = n_dec + sum(c for _, c in chunks)
+    q = torch.randn(T, H, D, generator=g).to(torch.bfloat16)
+    cu_q, cu_k = [0], [0]
+    for p, c in chunks:
+        cu_q.append(cu_q[-1] + c)
+        cu_k.append(cu_k[-1] + p + c)
+    print(f"[varlen] int8 chan random mix {seed}: H={H} KVH={KVH} page={page} slots={nom} "
+          f"dec={dec_lens} chunks={chunks}", flush=True)
+    out = varlen_attention(
+        q.to(DEV), kc.to(DEV), vc.to(DEV), scale=D ** -0.5, block_tables=bt.to(DEV),
+        num_decode_rows=n_dec,
+        decode_context_lens=torch.tensor(dec_lens, dtype=torch.int32, device=DEV) if n_dec else None,
+        cu_seqlens_q=torch.tensor(cu_q, dtype=torch.int32, device=DEV),
+        cu_seqlens_k=torch.tensor(cu_k, dtype=torch.int32, device=DEV),
+        cu_seqlens_q_list=cu_q, cu_seqlens_k_list=cu_k, k_scale=ks.to(DEV), v_scale=vs.to(DEV),
+        side_k=sk_.to(DEV), side_v=sv_.to(DEV), out_idx2d=oi.to(DEV), head_n_out=hn.to(DEV))
+    torch.cuda.synchronize()
+    args = (bits(sk_), oi.numpy(), hn.numpy())
+    kf = ko.kv_float(kc.numpy(), "int8_chan", ks.numpy(), *args)
+    vf = ko.kv_float(vc.numpy(), "int8_chan", vs.numpy(), bits(sv_), oi.numpy(), hn.numpy())
+    kp = ko.kv_float_prefill(kc.numpy(), "int8_chan", ks.numpy(), *args)
+    vp = ko.kv_float_prefill(vc.numpy(), "int8_chan", vs.numpy(), bits(sv_), oi.numpy(),
+                             hn.numpy())
+    ref = ko.mixed_ref(bits(q), kf, vf, bt.numpy(), n_dec, np.asarray(dec_lens), cu_q, cu_k,
+                       D ** -0.5, k_pre=kp, v_pre=vp)
+    assert_attention_close(out, ref, f"int8-chan-random-{seed}")
+
+
 def test_long_chunk_many_query_tiles(partition):
     # 64 q / 2 kv heads: 16-head slices and 16-token query tiles, so a
     # 1100-token chunk spans 69 query tiles (the item search crosses a
