@@ -276,6 +276,50 @@ def test_int8_chan_random_mixes(seed):
     assert_attention_close(out, ref, f"int8-chan-random-{seed}")
 
 
+@pytest.mark.parametrize("seed", range(4))
+def test_int8_tokhead_random_mixes(seed):
+    # The same kind of seeded random mixes over a per-token-head int8 pool.
+    rng = np.random.default_rng(300 + seed)
+    H, KVH = [(32, 4), (16, 2), (64, 8), (8, 8)][seed]
+    D = 128
+    page = int(rng.choice([32, 128, 256]))
+    n_dec = int(rng.integers(0, 5))
+    dec_lens = [int(rng.integers(1, 1500)) for _ in range(n_dec)]
+    chunks = [(int(rng.integers(0, 900)), int(rng.integers(1, 200)))
+              for _ in range(int(rng.integers(1, 6)))]
+    g = torch.Generator().manual_seed(400 + seed)
+    all_lens = dec_lens + [p + c for p, c in chunks]
+    blocks = sum(max(1, (n + page - 1) // page) for n in all_lens) + 2
+    bt = build_block_tables(all_lens, blocks, page, g)
+    kc = torch.randint(-127, 128, (blocks, page, KVH, D), generator=g, dtype=torch.int8)
+    vc = torch.randint(-127, 128, (blocks, page, KVH, D), generator=g, dtype=torch.int8)
+    ks = torch.rand(blocks, page, KVH, generator=g) * 0.03 + 0.005
+    vs = torch.rand(blocks, page, KVH, generator=g) * 0.03 + 0.005
+    T = n_dec + sum(c for _, c in chunks)
+    q = torch.randn(T, H, D, generator=g).to(torch.bfloat16)
+    cu_q, cu_k = [0], [0]
+    for p, c in chunks:
+        cu_q.append(cu_q[-1] + c)
+        cu_k.append(cu_k[-1] + p + c)
+    print(f"[varlen] int8 tokhead random mix {seed}: H={H} KVH={KVH} page={page} "
+          f"dec={dec_lens} chunks={chunks}", flush=True)
+    out = varlen_attention(
+        q.to(DEV), kc.to(DEV), vc.to(DEV), scale=D ** -0.5, block_tables=bt.to(DEV),
+        num_decode_rows=n_dec,
+        decode_context_lens=torch.tensor(dec_lens, dtype=torch.int32, device=DEV) if n_dec else None,
+        cu_seqlens_q=torch.tensor(cu_q, dtype=torch.int32, device=DEV),
+        cu_seqlens_k=torch.tensor(cu_k, dtype=torch.int32, device=DEV),
+        cu_seqlens_q_list=cu_q, cu_seqlens_k_list=cu_k, k_scale=ks.to(DEV), v_scale=vs.to(DEV))
+    torch.cuda.synchronize()
+    kf = ko.kv_float(kc.numpy(), "int8_tokhead", ks.numpy())
+    vf = ko.kv_float(vc.numpy(), "int8_tokhead", vs.numpy())
+    kp = ko.kv_float_prefill(kc.numpy(), "int8_tokhead", ks.numpy())
+    vp = ko.kv_float_prefill(vc.numpy(), "int8_tokhead", vs.numpy())
+    ref = ko.mixed_ref(bits(q), kf, vf, bt.numpy(), n_dec, np.asarray(dec_lens), cu_q, cu_k,
+                       D ** -0.5, k_pre=kp, v_pre=vp)
+    assert_attention_close(out, ref, f"int8-tokhead-random-{seed}")
+
+
 def test_long_chunk_many_query_tiles(partition):
     # 64 q / 2 kv heads: 16-head slices and 16-token query tiles, so a
     # 1100-token chunk spans 69 query tiles (the item search crosses a
