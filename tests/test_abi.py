@@ -108,6 +108,35 @@ def test_bad_arguments_map_to_python_exceptions():
         _native.call("kvc_block_gather", None, 1, 16, 15, None, 1, None, 16, 16, None)
 
 
+def test_gather_kv_checks_its_arguments_on_the_host():
+    import pytest
+    # kvc_gather_kv validates shapes, encodings and pointers before any device
+    # work; fake pointers are never dereferenced because a check fails first.
+
+    def gather(head_dim=128, kv_dtype=2, scales=64, side=64, head_n_out=64, n_out_max=4,
+               num_prefill=1, total_keys=1, pool=64, max_blocks=1, bt_stride=1):
+        _native.call("kvc_gather_kv", pool, pool, 2, 256, 4, head_dim, kv_dtype, scales, scales,
+                     side, side, 64, head_n_out, n_out_max, 64, bt_stride, max_blocks, 0,
+                     num_prefill, 64, total_keys, None if pool is None else 64, 64, None)
+
+    gather(num_prefill=0)   # nothing to gather: validated, then nothing to do
+    gather(total_keys=0)
+    with pytest.raises(ValueError, match="head_dim"):
+        gather(head_dim=64)
+    with pytest.raises(ValueError, match="kv_dtype"):
+        gather(kv_dtype=7)
+    with pytest.raises(ValueError, match="null pointer"):
+        gather(pool=None)
+    with pytest.raises(ValueError, match="scales"):
+        gather(scales=None)
+    with pytest.raises(ValueError, match="n_out_max"):
+        gather(n_out_max=9)
+    with pytest.raises(ValueError, match="n_out_max"):
+        gather(side=None)
+    with pytest.raises(ValueError, match="max_blocks_per_seq"):
+        gather(max_blocks=2, bt_stride=1)
+
+
 def test_side_pool_widths_and_alignment():
     import pytest
     # Per-channel side pools (kv_dtype 2): n_out_max must be 1, 2, 4 or 8 and
