@@ -137,6 +137,28 @@ def test_gather_kv_checks_its_arguments_on_the_host():
         gather(max_blocks=2, bt_stride=1)
 
 
+def test_fresh_rows_with_outlier_dims_are_checked_on_the_host():
+    import pytest
+    # Fresh rows gathered from a per-channel pool may name its outlier dims;
+    # their side width follows the attention's rule (1, 2, 4 or 8), checked
+    # before any device work (num_q_tokens 0: nothing runs after the checks).
+
+    def call(out_idx2d=64, n_out_max=4):
+        _native.call("kvc_varlen_attention", 64, 4096, 128, 0, 32, None, None, 0, 0, 4, 128,
+                     _native.KVC_KV_BF16, None, None, None, None, out_idx2d, 64, n_out_max,
+                     64, 512, 128, 64, 512, 128, None, 0, 0, 0, None, 0, None, None, 0, 0,
+                     0, 0, 1.0, 64, 4096, 128, None, 0, None)
+
+    call()
+    for n in (1, 2, 8):
+        call(n_out_max=n)
+    for n in (0, 3, 16):
+        with pytest.raises(ValueError, match="n_out_max"):
+            call(n_out_max=n)
+    with pytest.raises(ValueError, match="out_idx2d"):
+        call(out_idx2d=None)
+
+
 def test_side_pool_widths_and_alignment():
     import pytest
     # Per-channel side pools (kv_dtype 2): n_out_max must be 1, 2, 4 or 8 and
