@@ -1247,7 +1247,7 @@ def run_pd_wire(args, torch):
 
 
 def run_swap(args, torch):
-    """Block eviction / offload step at the config-5 shape: a pool of 8192
+    """Block eviction / offload step at the 48-layer 30B-A3B pool shape: a pool of 8192
     blocks of [2 (K, V), 48 layers, 256, 4 kv heads, 128] bf16 (24 MiB each,
     192 GiB; the 16384-block pool of the workload does not fit one 288 GB GPU,
     and bytes/s do not depend on the pool size), 512 active blocks chosen by a

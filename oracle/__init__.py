@@ -6,8 +6,8 @@ reference algorithms this repository's HIP kernels replace.  Each function
 cites the reference file:line it follows.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
-import it, and only as the checker or as the timed CPU baseline — never as a
-product code path.  The product (s4000-moe-engine_amd/nanovllm_amd) has no
+import it, and only as the results the tests compare against or as the timed
+CPU baseline — never as a product code path.  The product (s4000-moe-engine_amd/nanovllm_amd) has no
 CPU fallback and raises if libkvc.so is missing.
 
 How each function is pinned (checked in tests/test_oracle.py):

@@ -4832,11 +4832,12 @@ void launch_merge_steal(const AttnParams& p, int64_t rows, const StealArgs& sa, 
 // Split-K merge of a stream-K prefill launch: one wave per (query row, kv
 // slice).  The wave reads the slice's split count once; lane l then owns
 // head l / 8 of the slice (eight heads per pass) and dims 32 q + 4 (l % 8)
-// .. + 3 (q < 4: each load instruction reads 128 contiguous bytes of a head's
-// partial row, 0.8 us faster on config 3's merge than 16 contiguous dims per
-// lane), so a whole slice's partials are in flight together and a row costs
-// two memory round trips (the count, then the partials) whatever its head
-// count.
+// .. + 3 (q < 4: each load instruction reads 64 contiguous bytes of a head's
+// fp16 partial row; with fp32 rows, 128 bytes were 0.8 us faster than 16
+// contiguous dims per lane on the merge of 60 decode rows + four 256-token
+// chunks after prefixes 0 / 512 / 2048 / 8192), so a whole slice's partials
+// are in flight together and a row costs two memory round trips (the count,
+// then the partials) whatever its head count.
 constexpr int kSliceBatch = 4;  // splits per load batch (124 VGPRs: every wave resident)
 // Block `block` of the split merge of a stream-K prefill launch
 // (merge_slices_kernel).

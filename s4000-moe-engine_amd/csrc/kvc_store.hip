@@ -243,8 +243,9 @@ constexpr int kSideMaxStore = 8;  // side slots a gathered row takes (the attent
 constexpr int kGatherLanes = 8;
 constexpr int kGatherRows = kThreads / kGatherLanes;
 // Token groups a block runs: two for the per-channel pool (its per-head read
-// scales and outlier dims are loaded once for both; 14.8 against 19 us on the
-// config-3 chunks), one otherwise (10.3 against 11.7 us per-token-head).
+// scales and outlier dims are loaded once for both; 14.8 against 19 us on four
+// 256-token chunks after prefixes 0 / 512 / 2048 / 8192, 4 kv heads), one
+// otherwise (10.3 against 11.7 us per-token-head).
 template <int kEnc>
 constexpr int gather_iters() { return kEnc == KVC_KV_INT8_CHAN ? 2 : 1; }
 
